@@ -1,0 +1,133 @@
+"""ctypes binding of the C ABI (include/goi_b2.h) and the loader of the in-tree libgoi_b2.so.
+
+The library is built by __graft_entry__.build() (or getting-over-it-rl_amd/build.py) into
+getting-over-it-rl_amd/lib/libgoi_b2.so. There is no fallback: `lib()` raises when the library is missing.
+"""
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent.parent
+LIB_PATH = PKG / "lib" / "libgoi_b2.so"
+NUM_LEAVES = 71
+ABI_VERSION = 1
+
+GOI_OK, GOI_E_ARG, GOI_E_SHAPE, GOI_E_HIP, GOI_E_UNSUPPORTED = 0, -1, -2, -3, -4
+
+
+class GoiError(RuntimeError):
+    """A non-zero return code of the C ABI, with goi_last_error()'s message."""
+
+    def __init__(self, code, msg):
+        super().__init__(f"goi_b2 error {code}: {msg}")
+        self.code = code
+
+
+class GoiSettings(ctypes.Structure):
+    _fields_ = [("velocity_iterations", ctypes.c_int32), ("position_iterations", ctypes.c_int32),
+                ("linear_slop", ctypes.c_float), ("angular_slop", ctypes.c_float),
+                ("polygon_radius", ctypes.c_float), ("velocity_threshold", ctypes.c_float),
+                ("max_linear_correction", ctypes.c_float), ("max_angular_correction", ctypes.c_float),
+                ("max_translation", ctypes.c_float), ("max_rotation", ctypes.c_float),
+                ("baumgarte", ctypes.c_float), ("toi_baumgarte", ctypes.c_float),
+                ("time_to_sleep", ctypes.c_float), ("linear_sleep_tolerance", ctypes.c_float),
+                ("angular_sleep_tolerance", ctypes.c_float), ("clamps_per_second", ctypes.c_int32),
+                ("allow_sleep", ctypes.c_int32), ("warm_starting", ctypes.c_int32),
+                ("continuous_physics", ctypes.c_int32), ("unity_toi", ctypes.c_int32),
+                ("toi_tie_oldest", ctypes.c_int32), ("auto_clear_forces", ctypes.c_int32),
+                ("revolute_v24", ctypes.c_int32), ("max_events", ctypes.c_int32)]
+
+
+_P = ctypes.c_void_p
+
+
+class GoiModelDesc(ctypes.Structure):
+    _fields_ = [("F", ctypes.c_int32), ("J", ctypes.c_int32), ("P", ctypes.c_int32), ("B", ctypes.c_int32)] + [
+        (n, _P) for n in ("fixture_body", "shape_type", "radius", "count", "verts", "normals", "joint_type", "joint_a",
+                          "joint_b", "local_anchor_a", "local_anchor_b", "local_axis_a", "local_yaxis_a",
+                          "reference_angle", "pair_a", "pair_b", "fixture_slot", "static_fat", "static_friction",
+                          "static_restitution", "body_type", "toi_bodies")]
+
+
+class GoiStateView(ctypes.Structure):
+    _fields_ = [("n_worlds", ctypes.c_int32), ("pitch", ctypes.c_int32), ("B", ctypes.c_int32),
+                ("C", ctypes.c_int32), ("R", ctypes.c_int32), ("J", ctypes.c_int32), ("leaf", _P * NUM_LEAVES)]
+
+
+class GoiDebug(ctypes.Structure):
+    _fields_ = [("body_island", _P), ("contact_island", _P), ("contact_order", _P), ("n_islands", _P)]
+
+
+EXPORTS = ("goi_abi_version", "goi_model_create", "goi_model_destroy", "goi_step", "goi_collide", "goi_sincos",
+           "goi_last_error")
+
+_LIB = None
+
+
+def lib(path=None):
+    """The loaded libgoi_b2.so with argtypes set. Raises FileNotFoundError if it was not built."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = Path(path or os.environ.get("GOI_B2_LIB", LIB_PATH))
+    if not p.exists():
+        raise FileNotFoundError(f"{p} not built: run __graft_entry__.build() (hipcc for gfx950)")
+    L = ctypes.CDLL(str(p))
+    L.goi_abi_version.restype = ctypes.c_int32
+    L.goi_last_error.restype = ctypes.c_char_p
+    L.goi_model_create.argtypes = [ctypes.POINTER(GoiModelDesc), ctypes.c_int32, _P, ctypes.POINTER(_P)]
+    L.goi_model_create.restype = ctypes.c_int32
+    L.goi_model_destroy.argtypes = [_P]
+    L.goi_model_destroy.restype = ctypes.c_int32
+    L.goi_step.argtypes = [_P, ctypes.POINTER(GoiStateView), ctypes.POINTER(GoiSettings), ctypes.c_float, _P,
+                           ctypes.POINTER(GoiDebug)]
+    L.goi_step.restype = ctypes.c_int32
+    L.goi_collide.argtypes = [_P, ctypes.POINTER(GoiStateView), ctypes.POINTER(GoiSettings), _P]
+    L.goi_collide.restype = ctypes.c_int32
+    L.goi_sincos.argtypes = [_P, _P, _P, ctypes.c_int32, _P]
+    L.goi_sincos.restype = ctypes.c_int32
+    if L.goi_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{p}: ABI version {L.goi_abi_version()} != {ABI_VERSION}")
+    if path is None:
+        _LIB = L
+    return L
+
+
+def check(code, L=None):
+    if code != GOI_OK:
+        L = L or lib()
+        raise GoiError(code, L.goi_last_error().decode())
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def model_desc(model):
+    """GoiModelDesc over a compact Model's numpy arrays; returns (desc, keepalive)."""
+    if model.fixture_slot is None or model.body_type is None:
+        raise ValueError("the device step needs a compact Model (world.compact_model)")
+    keep = []
+
+    def arr(a, dt):
+        if a is None:
+            return None
+        x = np.ascontiguousarray(np.asarray(a), dtype=dt)
+        keep.append(x)
+        return x
+    I, F, U = np.int32, np.float32, np.uint8
+    d = GoiModelDesc()
+    d.F = int(model.fixture_body.shape[0])
+    d.J = int(model.joint_type.shape[0])
+    d.P = int(model.pair_a.shape[0])
+    d.B = int(model.body_type.shape[0])
+    fields = dict(fixture_body=I, shape_type=I, radius=F, count=I, verts=F, normals=F, joint_type=I, joint_a=I,
+                  joint_b=I, local_anchor_a=F, local_anchor_b=F, local_axis_a=F, local_yaxis_a=F, reference_angle=F,
+                  pair_a=I, pair_b=I, fixture_slot=I, static_fat=F, static_friction=F, static_restitution=F,
+                  body_type=I)
+    for name, dt in fields.items():
+        setattr(d, name, _ptr(arr(getattr(model, name), dt)))
+    d.toi_bodies = _ptr(arr(model.toi_bodies, U)) if model.toi_bodies is not None else None
+    return d, keep

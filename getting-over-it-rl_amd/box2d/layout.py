@@ -1,0 +1,83 @@
+"""Batches of States on the GPU in the kernels' worlds-minor layout, and back.
+
+A device State has the reference's field names and logical shapes (N, *inner) (goi_jax/box2d/world.py:70-174), as
+torch tensors whose storage is worlds-minor: leaf L with inner shape S is one contiguous (prod(S), pitch) buffer
+viewed as (N, *S) with stride 1 on the world axis. `state_view` hands those buffers to the C ABI without copies.
+"""
+import numpy as np
+import torch
+
+from . import world as wd
+from ._abi import GoiStateView
+
+_TORCH = {np.dtype(np.float32): torch.float32, np.dtype(np.int32): torch.int32, np.dtype(bool): torch.bool}
+
+
+def _dtype(dt):
+    return _TORCH[np.dtype(dt)]
+
+
+def empty_device_state(n, dims, device="cuda", pitch=None):
+    """An uninitialised device State of n worlds with capacities dims = (B, R, J, C)."""
+    pitch = n if pitch is None else pitch
+    vals = []
+    for _, _, dt, inner in wd.LEAVES:
+        shape = wd.leaf_shape(inner, dims)
+        buf = torch.empty(tuple(shape) + (pitch,), dtype=_dtype(dt), device=device)
+        vals.append(buf[..., :n].movedim(-1, 0))
+    return wd.from_leaves(vals)
+
+
+def to_device(state, device="cuda", pitch=None):
+    """A batched numpy State (leading world axis) to a device State."""
+    leaves = wd.leaves(state)
+    n = np.asarray(leaves[0]).shape[0]
+    dims = wd.dims(state)
+    out = empty_device_state(n, dims, device, pitch)
+    for dst, src in zip(wd.leaves(out), leaves):
+        src = np.asarray(src)
+        dst.copy_(torch.from_numpy(np.ascontiguousarray(src)).to(device))
+    return out
+
+
+def to_host(state):
+    """A device State to a batched numpy State (contiguous, batch-major)."""
+    return wd.from_leaves([np.ascontiguousarray(t.detach().cpu().numpy()) for t in wd.leaves(state)])
+
+
+def clone(state):
+    """A deep copy of a device State in the same layout."""
+    leaves = wd.leaves(state)
+    n = leaves[0].shape[0]
+    dims = wd.dims(state)
+    out = empty_device_state(n, dims, leaves[0].device)
+    for dst, src in zip(wd.leaves(out), leaves):
+        dst.copy_(src)
+    return out
+
+
+def state_view(state):
+    """GoiStateView over a device State; checks the worlds-minor layout."""
+    leaves = wd.leaves(state)
+    n = leaves[0].shape[0]
+    B, R, J, C = wd.dims(state)
+    v = GoiStateView()
+    v.n_worlds = n
+    pitch = None
+    for t, (_, name, dt, inner) in zip(leaves, wd.LEAVES):
+        if t.dtype != _dtype(dt):
+            raise TypeError(f"leaf {name}: dtype {t.dtype}, expected {_dtype(dt)}")
+        if not t.is_cuda:
+            raise ValueError(f"leaf {name}: not on a GPU")
+        if t.dim() > 1:
+            p = t.stride(-1)
+            if t.stride(0) != 1 or (pitch is not None and p != pitch):
+                raise ValueError(f"leaf {name}: not in the worlds-minor layout (strides {t.stride()})")
+            pitch = p
+        elif t.stride(0) != 1:
+            raise ValueError(f"leaf {name}: world stride must be 1")
+    v.pitch = n if pitch is None else pitch
+    v.B, v.C, v.R, v.J = B, C, R, J
+    for i, t in enumerate(leaves):
+        v.leaf[i] = t.data_ptr()
+    return v

@@ -1,0 +1,122 @@
+"""b2World::Step over a batch of worlds on the MI355X: the drop-in for goi_jax/box2d/step.py:28-47.
+
+    model, state = WorldDef(settings) ... .build(contact_capacity=32)
+    model = compact_model(model, state)                  # shared static terrain, as the reference GPU path needs
+    dev = layout.to_device(world.batch(compact_state(model, state), 16384))
+    dev = step(model, dev, settings, dt)                 # a new State (step_ steps in place)
+
+`step(model, state, settings, dt, axis_name=None)` keeps the reference signature; axis_name is accepted and ignored
+(the device kernels need no shared trip count, cf. goi_jax/box2d/gpu/solve.py:28). Settings.solver must be "hip":
+there is no CPU fallback, a missing or unloadable libgoi_b2.so raises.
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _abi
+from . import layout
+from . import world as wd
+
+_MODELS = {}
+
+
+class DeviceModel:
+    """The library's model handle (goi_model_create) for one compact Model, contact capacity and device."""
+
+    def __init__(self, model, contact_capacity, device=None):
+        self.L = _abi.lib()
+        desc, self._keep = _abi.model_desc(model)
+        handle = ctypes.c_void_p()
+        dev = torch.device("cuda") if device is None else torch.device(device)
+        with torch.cuda.device(dev):
+            stream = torch.cuda.current_stream().cuda_stream
+            _abi.check(self.L.goi_model_create(ctypes.byref(desc), int(contact_capacity), ctypes.c_void_p(stream),
+                                               ctypes.byref(handle)), self.L)
+        self.handle = handle
+        self.device = dev
+        self.capacity = int(contact_capacity)
+
+    def __del__(self):
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            try:
+                self.L.goi_model_destroy(self.handle)
+            except Exception:  # interpreter shutdown
+                pass
+            self.handle = None
+
+
+def device_model(model, contact_capacity, device=None):
+    """Cached DeviceModel for (model object, capacity, device)."""
+    key = (id(model), int(contact_capacity), str(device))
+    hit = _MODELS.get(key)
+    if hit is not None and hit[0] is model:
+        return hit[1]
+    dm = DeviceModel(model, contact_capacity, device)
+    _MODELS[key] = (model, dm)
+    return dm
+
+
+def step_(model, state, settings, dt, debug=None, stream=None):
+    """One step of every world of a device State, in place. Returns the same State."""
+    if getattr(settings, "solver", "hip") != "hip":
+        raise ValueError(f"Settings.solver={settings.solver!r}: this package steps on the GPU only ('hip')")
+    C = state.contacts.pair.shape[-1]
+    dev = state.contacts.pair.device
+    dm = device_model(model, C, dev)
+    view = layout.state_view(state)
+    cs = settings.to_c()
+    st = torch.cuda.current_stream(dev).cuda_stream if stream is None else stream
+    dbg = None if debug is None else ctypes.byref(debug)
+    _abi.check(dm.L.goi_step(dm.handle, ctypes.byref(view), ctypes.byref(cs), ctypes.c_float(np.float32(dt)),
+                             ctypes.c_void_p(st), dbg), dm.L)
+    return state
+
+
+def step(model, state, settings, dt, axis_name=None):
+    """b2World::Step (step.py:28-47) of a batched device State; returns a new State (the input is unchanged)."""
+    del axis_name
+    out = layout.clone(state)
+    return step_(model, out, settings, dt)
+
+
+def collide_(model, state, settings, stream=None):
+    """Broadphase + narrowphase only, in place: start-of-step FindNewContacts where new_fixture, then Collide."""
+    C = state.contacts.pair.shape[-1]
+    dev = state.contacts.pair.device
+    dm = device_model(model, C, dev)
+    view = layout.state_view(state)
+    cs = settings.to_c()
+    st = torch.cuda.current_stream(dev).cuda_stream if stream is None else stream
+    _abi.check(dm.L.goi_collide(dm.handle, ctypes.byref(view), ctypes.byref(cs), ctypes.c_void_p(st)), dm.L)
+    return state
+
+
+def sincos(x):
+    """(float)sin((double)x), (float)cos((double)x) of a float32 CUDA tensor, as the kernels compute them."""
+    L = _abi.lib()
+    x = x.contiguous()
+    s, c = torch.empty_like(x), torch.empty_like(x)
+    st = torch.cuda.current_stream(x.device).cuda_stream
+    _abi.check(L.goi_sincos(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(s.data_ptr()),
+                            ctypes.c_void_p(c.data_ptr()), ctypes.c_int32(x.numel()), ctypes.c_void_p(st)), L)
+    return s, c
+
+
+def make_debug(n, dims, device="cuda"):
+    """GoiDebug buffers (island ids, solve order) for a device State of n worlds; returns (struct, tensors)."""
+    B, _, _, C = dims
+    t = dict(body_island=torch.full((B, n), -1, dtype=torch.int32, device=device),
+             contact_island=torch.full((C, n), -1, dtype=torch.int32, device=device),
+             contact_order=torch.full((C, n), -1, dtype=torch.int32, device=device),
+             n_islands=torch.zeros((n,), dtype=torch.int32, device=device))
+    d = _abi.GoiDebug()
+    for k, v in t.items():
+        setattr(d, k, ctypes.c_void_p(v.data_ptr()))
+    return d, t
+
+
+def prepare(model, state):
+    """(compact Model, compact State) from a WorldDef build, as the device step expects."""
+    cm = wd.compact_model(model, state)
+    return cm, wd.compact_state(cm, state)

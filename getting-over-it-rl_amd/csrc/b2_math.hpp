@@ -1,0 +1,97 @@
+// b2_math.hpp - float32 b2Math for gfx950 device code, one rounding per C operation in C order.
+//
+// The whole library is compiled with -ffp-contract=off (no FMA contraction), IEEE-correct division and square root,
+// and f32 denormals kept, so every expression below rounds exactly as Box2D 2.3.1 built with -ffp-contract=off does
+// (goi_jax/box2d/math2d.py:1-13, scripts/build_box2d.sh:11). C's `a + b + c` is `(a + b) + c`; products are written
+// in the source order of b2Math.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define GOI_D __device__ __forceinline__
+
+namespace goi {
+
+constexpr float kEps = 1.1920928955078125e-7f;       // b2_epsilon
+constexpr float kMaxFloat = 3.40282346638528859812e+38f;  // b2_maxFloat
+constexpr float kPi = 3.14159265359f;                // b2_pi
+constexpr int kMaxSubSteps = 8;
+constexpr int kMaxToiContacts = 32;
+constexpr int kPoly = 8;
+
+struct V2 { float x, y; };
+struct Rot { float c, s; };
+struct Xf { V2 p; Rot q; };
+struct V3 { float x, y, z; };
+
+GOI_D V2 mk(float x, float y) { V2 r; r.x = x; r.y = y; return r; }
+GOI_D V3 mk3(float x, float y, float z) { V3 r; r.x = x; r.y = y; r.z = z; return r; }
+GOI_D V2 operator+(V2 a, V2 b) { return mk(a.x + b.x, a.y + b.y); }
+GOI_D V2 operator-(V2 a, V2 b) { return mk(a.x - b.x, a.y - b.y); }
+GOI_D V2 operator-(V2 a) { return mk(-a.x, -a.y); }
+GOI_D V2 operator*(float s, V2 a) { return mk(s * a.x, s * a.y); }
+GOI_D float dot(V2 a, V2 b) { return a.x * b.x + a.y * b.y; }
+GOI_D float cross(V2 a, V2 b) { return a.x * b.y - a.y * b.x; }
+GOI_D V2 cross(V2 a, float s) { return mk(s * a.y, -s * a.x); }
+GOI_D V2 cross(float s, V2 a) { return mk(-s * a.y, s * a.x); }
+GOI_D V2 mul(Rot q, V2 v) { return mk(q.c * v.x - q.s * v.y, q.s * v.x + q.c * v.y); }
+GOI_D V2 mulT(Rot q, V2 v) { return mk(q.c * v.x + q.s * v.y, -q.s * v.x + q.c * v.y); }
+GOI_D V2 mul(const Xf& t, V2 v) { return mk((t.q.c * v.x - t.q.s * v.y) + t.p.x, (t.q.s * v.x + t.q.c * v.y) + t.p.y); }
+GOI_D V2 mulT(const Xf& t, V2 v) {
+    float px = v.x - t.p.x, py = v.y - t.p.y;
+    return mk(t.q.c * px + t.q.s * py, -t.q.s * px + t.q.c * py);
+}
+GOI_D Xf mulT(const Xf& A, const Xf& B) {
+    Xf C;
+    C.q.s = A.q.c * B.q.s - A.q.s * B.q.c;
+    C.q.c = A.q.c * B.q.c + A.q.s * B.q.s;
+    C.p = mulT(A.q, B.p - A.p);
+    return C;
+}
+GOI_D float length(V2 a) { return __fsqrt_rn(a.x * a.x + a.y * a.y); }
+// b2Vec2::Normalize: unchanged below b2_epsilon
+GOI_D float normalize(V2& a) {
+    float n = length(a);
+    if (n < kEps) return 0.0f;
+    float inv = __fdiv_rn(1.0f, n);
+    a.x *= inv;
+    a.y *= inv;
+    return n;
+}
+GOI_D float bmin(float a, float b) { return a < b ? a : b; }   // b2Min keeps b on ties and NaN
+GOI_D float bmax(float a, float b) { return a > b ? a : b; }
+GOI_D float bclamp(float a, float lo, float hi) { return bmax(lo, bmin(a, hi)); }
+GOI_D float babs(float a) { return a > 0.0f ? a : -a; }
+GOI_D float fdiv(float a, float b) { return __fdiv_rn(a, b); }
+GOI_D float fsqrt(float a) { return __fsqrt_rn(a); }
+
+// Correctly rounded float32 sin/cos: (float)sin((double)x), the value the reference computes with a float-float
+// series (math2d.py:291-310) and its oracle with the C library (scripts/patches/box2d-2.3.1-trig.patch:17-23).
+// Evaluated on the FP64 units: the double result is within an ulp of the exact value, so rounding it to float gives
+// the correctly rounded float except when sin x lies within ~2^-53 relative of a float rounding boundary.
+GOI_D Rot rot_of(float a) {
+    double s, c;
+    sincos((double)a, &s, &c);
+    Rot q;
+    q.s = (float)s;
+    q.c = (float)c;
+    return q;
+}
+
+// b2Mat22::Solve / b2Mat33::Solve22
+GOI_D V2 solve22(float a11, float a12, float a21, float a22, V2 b) {
+    float det = a11 * a22 - a12 * a21;
+    if (det != 0.0f) det = fdiv(1.0f, det);
+    return mk(det * (a22 * b.x - a12 * b.y), det * (a11 * b.y - a21 * b.x));
+}
+GOI_D float dot(V3 a, V3 b) { return (a.x * b.x + a.y * b.y) + a.z * b.z; }
+GOI_D V3 cross(V3 a, V3 b) { return mk3(a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x); }
+// b2Mat33::Solve33 with columns ex, ey, ez
+GOI_D V3 solve33(V3 ex, V3 ey, V3 ez, V3 b) {
+    float det = dot(ex, cross(ey, ez));
+    if (det != 0.0f) det = fdiv(1.0f, det);
+    return mk3(det * dot(b, cross(ey, ez)), det * dot(ex, cross(b, ez)), det * dot(ex, cross(ey, b)));
+}
+
+}  // namespace goi

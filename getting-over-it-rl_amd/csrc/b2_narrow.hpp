@@ -1,0 +1,216 @@
+// b2_narrow.hpp - Box2D 2.3.1 narrowphase on the device: b2CollidePolygons, b2CollidePolygonAndCircle,
+// b2CollideCircles (goi_jax/box2d/collide.py:22-207). Only the collider of the slot's shape pair runs (the reference
+// evaluates all three and selects, collide.py:197-207). Vertex loops run over the real count (<= 8) instead of
+// masked (8 x 8) tiles; Box2D's strict `<` / `>` running extremes give the reference's first-index argmin/argmax.
+//
+// Manifold fields that the reference leaves as don't-care (collide.py:5-7) follow its values: on an early out only
+// count = 0 matters (the caller keeps the old geometry, pairs.py:73-81); with one kept clip point, point slot 1 holds
+// the second clip point (collide.py:122-127); polygon-circle and circle-circle write the circle centre and key 0 into
+// both point slots (collide.py:168-170, 184-186).
+#pragma once
+
+#include "b2_view.hpp"
+
+namespace goi {
+
+enum { kCircles = 0, kFaceA = 1, kFaceB = 2 };
+
+struct Manifold {
+    int mtype, count;
+    V2 ln, lp, pl0, pl1;
+    int id0, id1;
+};
+
+GOI_D int feature_key(int ia, int ib, int ta, int tb) { return ia | (ib << 8) | (ta << 16) | (tb << 24); }
+
+GOI_D V2 mvert(const DModel& m, int f, int i) { return m.verts[f * kPoly + i]; }
+GOI_D V2 mnorm(const DModel& m, int f, int i) { return m.normals[f * kPoly + i]; }
+
+// b2FindMaxSeparation: (edge of poly1, separation) over poly1's normals against poly2's vertices
+GOI_D float max_separation(const DModel& m, int f1, const Xf& xf1, int f2, const Xf& xf2, int& edge) {
+    const int c1 = m.count[f1], c2 = m.count[f2];
+    const Xf xf = mulT(xf2, xf1);
+    V2 v2s[kPoly];
+#pragma unroll
+    for (int j = 0; j < kPoly; ++j) v2s[j] = j < c2 ? mvert(m, f2, j) : mk(0.0f, 0.0f);
+    int best = 0;
+    float maxsep = -kMaxFloat;
+    for (int i = 0; i < c1; ++i) {
+        const V2 n = mul(xf.q, mnorm(m, f1, i));
+        const V2 v1 = mul(xf, mvert(m, f1, i));
+        float si = kMaxFloat;
+#pragma unroll
+        for (int j = 0; j < kPoly; ++j) {
+            if (j < c2) {
+                const float sij = dot(n, v2s[j] - v1);
+                if (sij < si) si = sij;
+            }
+        }
+        if (si > maxsep) {
+            maxsep = si;
+            best = i;
+        }
+    }
+    edge = best;
+    return maxsep;
+}
+
+struct ClipV {
+    V2 v;
+    int ia, ib, ta, tb;
+};
+
+// b2ClipSegmentToLine for two input vertices; returns numOut
+GOI_D int clip_line(ClipV& o0, ClipV& o1, const ClipV& i0, const ClipV& i1, V2 n, float offset, int vidx) {
+    const float d0 = dot(n, i0.v) - offset;
+    const float d1 = dot(n, i1.v) - offset;
+    const bool in0 = d0 <= 0.0f, in1 = d1 <= 0.0f;
+    int num = (int)in0 + (int)in1;
+    ClipV x;
+    x.v = mk(0.0f, 0.0f);
+    x.ia = vidx; x.ib = i0.ib; x.ta = 0; x.tb = 1;  // vertex A hits edge B
+    if (d0 * d1 < 0.0f) {
+        const float interp = d0 / (d0 - d1);
+        x.v = i0.v + interp * (i1.v - i0.v);
+        ++num;
+    }
+    o0 = in0 ? i0 : i1;
+    o1 = (in0 && in1) ? i1 : x;
+    return num;
+}
+
+GOI_D void collide_polygons(const DModel& m, int fa, const Xf& xfa, int fb, const Xf& xfb, float linear_slop,
+                            Manifold& out) {
+    out.count = 0;
+    const float total_radius = m.radius[fa] + m.radius[fb];
+    int edge_a, edge_b;
+    const float sep_a = max_separation(m, fa, xfa, fb, xfb, edge_a);
+    if (sep_a > total_radius) return;
+    const float sep_b = max_separation(m, fb, xfb, fa, xfa, edge_b);
+    if (sep_b > total_radius) return;
+    const float k_tol = 0.1f * linear_slop;
+    const bool flip = sep_b > sep_a + k_tol;
+    const int f1 = flip ? fb : fa, f2 = flip ? fa : fb;
+    const Xf xf1 = flip ? xfb : xfa, xf2 = flip ? xfa : xfb;
+    const int edge1 = flip ? edge_b : edge_a;
+    out.mtype = flip ? kFaceB : kFaceA;
+
+    // b2FindIncidentEdge
+    const int c2 = m.count[f2];
+    const V2 n1 = mulT(xf2.q, mul(xf1.q, mnorm(m, f1, edge1)));
+    int idx = 0;
+    float mind = kMaxFloat;
+    for (int i = 0; i < c2; ++i) {
+        const float d = dot(n1, mnorm(m, f2, i));
+        if (d < mind) {
+            mind = d;
+            idx = i;
+        }
+    }
+    const int i2 = idx + 1 < c2 ? idx + 1 : 0;
+    ClipV inc0, inc1;
+    inc0.v = mul(xf2, mvert(m, f2, idx)); inc0.ia = edge1; inc0.ib = idx; inc0.ta = 1; inc0.tb = 0;
+    inc1.v = mul(xf2, mvert(m, f2, i2));  inc1.ia = edge1; inc1.ib = i2;  inc1.ta = 1; inc1.tb = 0;
+
+    const int c1 = m.count[f1];
+    const int iv1 = edge1, iv2 = edge1 + 1 < c1 ? edge1 + 1 : 0;
+    V2 v11 = mvert(m, f1, iv1), v12 = mvert(m, f1, iv2);
+    V2 lt = v12 - v11;
+    normalize(lt);
+    const V2 ln = cross(lt, 1.0f);
+    const V2 plane = 0.5f * (v11 + v12);
+    const V2 tangent = mul(xf1.q, lt);
+    const V2 normal = cross(tangent, 1.0f);
+    v11 = mul(xf1, v11);
+    v12 = mul(xf1, v12);
+    const float front = dot(normal, v11);
+    const float side1 = -dot(tangent, v11) + total_radius;
+    const float side2 = dot(tangent, v12) + total_radius;
+
+    ClipV a0, a1, b0, b1;
+    if (clip_line(a0, a1, inc0, inc1, -tangent, side1, iv1) < 2) return;
+    if (clip_line(b0, b1, a0, a1, tangent, side2, iv2) < 2) return;
+
+    out.ln = ln;
+    out.lp = plane;
+    const bool k0 = dot(normal, b0.v) - front <= total_radius;
+    const bool k1 = dot(normal, b1.v) - front <= total_radius;
+    const V2 p0 = mulT(xf2, b0.v), p1 = mulT(xf2, b1.v);
+    const int id0 = flip ? feature_key(b0.ib, b0.ia, b0.tb, b0.ta) : feature_key(b0.ia, b0.ib, b0.ta, b0.tb);
+    const int id1 = flip ? feature_key(b1.ib, b1.ia, b1.tb, b1.ta) : feature_key(b1.ia, b1.ib, b1.ta, b1.tb);
+    out.count = (int)k0 + (int)k1;
+    out.pl0 = k0 ? p0 : p1;
+    out.id0 = k0 ? id0 : id1;
+    out.pl1 = p1;
+    out.id1 = id1;
+}
+
+GOI_D void collide_polygon_circle(const DModel& m, int fa, const Xf& xfa, int fb, const Xf& xfb, Manifold& out) {
+    out.count = 0;
+    const V2 cl = mulT(xfa, mul(xfb, mvert(m, fb, 0)));
+    const float radius = m.radius[fa] + m.radius[fb];
+    const int n = m.count[fa];
+    int ni = 0;
+    float sep = -kMaxFloat;
+    for (int i = 0; i < n; ++i) {
+        const float s = dot(mnorm(m, fa, i), cl - mvert(m, fa, i));
+        if (s > radius) return;
+        if (s > sep) {
+            sep = s;
+            ni = i;
+        }
+    }
+    const int i2 = ni + 1 < n ? ni + 1 : 0;
+    const V2 v1 = mvert(m, fa, ni), v2 = mvert(m, fa, i2);
+    const V2 centre = mvert(m, fb, 0);
+    out.mtype = kFaceA;
+    out.pl0 = centre; out.pl1 = centre;
+    out.id0 = 0; out.id1 = 0;
+    if (sep < kEps) {
+        out.count = 1;
+        out.ln = mnorm(m, fa, ni);
+        out.lp = 0.5f * (v1 + v2);
+        return;
+    }
+    const float u1 = dot(cl - v1, v2 - v1);
+    const float u2 = dot(cl - v2, v1 - v2);
+    const float rr = radius * radius;
+    if (u1 <= 0.0f) {
+        V2 d = cl - v1;
+        if (dot(d, d) > rr) return;
+        normalize(d);
+        out.count = 1; out.ln = d; out.lp = v1;
+    } else if (u2 <= 0.0f) {
+        V2 d = cl - v2;
+        if (dot(d, d) > rr) return;
+        normalize(d);
+        out.count = 1; out.ln = d; out.lp = v2;
+    } else {
+        const V2 fc = 0.5f * (v1 + v2);
+        if (dot(cl - fc, mnorm(m, fa, ni)) > radius) return;
+        out.count = 1; out.ln = mnorm(m, fa, ni); out.lp = fc;
+    }
+}
+
+GOI_D void collide_circles(const DModel& m, int fa, const Xf& xfa, int fb, const Xf& xfb, Manifold& out) {
+    out.count = 0;
+    const V2 d = mul(xfb, mvert(m, fb, 0)) - mul(xfa, mvert(m, fa, 0));
+    const float r = m.radius[fa] + m.radius[fb];
+    if (dot(d, d) > r * r) return;
+    out.mtype = kCircles;
+    out.count = 1;
+    out.ln = mk(0.0f, 0.0f);
+    out.lp = mvert(m, fa, 0);
+    out.pl0 = mvert(m, fb, 0); out.pl1 = out.pl0;
+    out.id0 = 0; out.id1 = 0;
+}
+
+// b2Contact::Evaluate by shape types (b2Contact::Create puts the polygon first)
+GOI_D void evaluate(const DModel& m, int fa, int fb, const Xf& xfa, const Xf& xfb, float linear_slop, Manifold& out) {
+    const int ta = m.shape_type[fa], tb = m.shape_type[fb];
+    if (ta == GOI_POLYGON && tb == GOI_POLYGON) collide_polygons(m, fa, xfa, fb, xfb, linear_slop, out);
+    else if (ta == GOI_POLYGON) collide_polygon_circle(m, fa, xfa, fb, xfb, out);
+    else collide_circles(m, fa, xfa, fb, xfb, out);
+}
+
+}  // namespace goi

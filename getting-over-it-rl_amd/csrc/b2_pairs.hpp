@@ -1,0 +1,252 @@
+// b2_pairs.hpp - contact management on the device: the contact list order, b2Contact::Update, Collide,
+// FindNewContacts through the static-terrain BVH, SynchronizeFixtures (goi_jax/box2d/pairs.py:38-207).
+#pragma once
+
+#include "b2_narrow.hpp"
+
+namespace goi {
+
+// Upper bound on contact slots per world the kernels handle (State capacity C <= kMaxC).
+constexpr int kMaxC = 64;
+
+// Live slots in contact-list order: newest first = descending key (pairs.py:12-13). Insertion into a per-lane
+// array; returns the count.
+GOI_D int list_order(const World& W, int* order) {
+    int n = 0;
+    for (int k = 0; k < W.C; ++k) {
+        if (W.i32(GOI_C_PAIR, k) < 0) continue;
+        const int key = W.i32(GOI_C_KEY, k);
+        int j = n++;
+        while (j > 0 && W.i32(GOI_C_KEY, order[j - 1]) < key) {
+            order[j] = order[j - 1];
+            --j;
+        }
+        order[j] = k;
+    }
+    return n;
+}
+
+// b2Contact::Update's manifold part: new manifold, impulses carried over from the first old point with the same
+// feature key, touching flag (pairs.py:56-83). Returns whether touching flipped.
+GOI_D bool contact_update(const World& W, int k, const Manifold& mf) {
+    const int oldn = W.i32(GOI_C_COUNT, k);
+    const int o0 = W.i32(GOI_C_POINT_ID, 2 * k), o1 = W.i32(GOI_C_POINT_ID, 2 * k + 1);
+    const float n0 = W.f(GOI_C_NORMAL_IMPULSE, 2 * k), n1 = W.f(GOI_C_NORMAL_IMPULSE, 2 * k + 1);
+    const float t0 = W.f(GOI_C_TANGENT_IMPULSE, 2 * k), t1 = W.f(GOI_C_TANGENT_IMPULSE, 2 * k + 1);
+    const int n = mf.count;
+    float ni0 = 0.0f, ti0 = 0.0f, ni1 = 0.0f, ti1 = 0.0f;
+    if (n > 0) {
+        if (oldn > 0 && o0 == mf.id0) { ni0 = n0; ti0 = t0; }
+        else if (oldn > 1 && o1 == mf.id0) { ni0 = n1; ti0 = t1; }
+    }
+    if (n > 1) {
+        if (oldn > 0 && o0 == mf.id1) { ni1 = n0; ti1 = t0; }
+        else if (oldn > 1 && o1 == mf.id1) { ni1 = n1; ti1 = t1; }
+    }
+    const bool touching = n > 0;
+    const bool flip = touching != (W.u8(GOI_C_TOUCHING, k) != 0);
+    W.u8(GOI_C_TOUCHING, k) = touching;
+    W.i32(GOI_C_COUNT, k) = n;
+    if (n > 0) {
+        W.i32(GOI_C_MTYPE, k) = mf.mtype;
+        W.set2(GOI_C_LOCAL_NORMAL, k, mf.ln);
+        W.set2(GOI_C_LOCAL_POINT, k, mf.lp);
+        W.set2(GOI_C_POINT_LOCAL, 2 * k, mf.pl0);
+        W.set2(GOI_C_POINT_LOCAL, 2 * k + 1, mf.pl1);
+        W.i32(GOI_C_POINT_ID, 2 * k) = mf.id0;
+        W.i32(GOI_C_POINT_ID, 2 * k + 1) = mf.id1;
+    }
+    W.f(GOI_C_NORMAL_IMPULSE, 2 * k) = ni0;
+    W.f(GOI_C_NORMAL_IMPULSE, 2 * k + 1) = ni1;
+    W.f(GOI_C_TANGENT_IMPULSE, 2 * k) = ti0;
+    W.f(GOI_C_TANGENT_IMPULSE, 2 * k + 1) = ti1;
+    return flip;
+}
+
+// b2ContactManager::Collide (pairs.py:38-87): the list newest first, a contact with both bodies inactive skipped,
+// separated fat AABBs destroy it (waking both bodies if it still had points), the rest updated (waking both bodies
+// when touching flips). Wakes change which later contacts are visited, as in Box2D's walk.
+GOI_D void collide_walk(const DModel& m, const World& W, float linear_slop) {
+    int order[kMaxC];
+    const int n = list_order(W, order);
+    for (int i = 0; i < n; ++i) {
+        const int k = order[i];
+        const int fa = W.i32(GOI_C_FA, k), fb = W.i32(GOI_C_FB, k);
+        const int ba = m.fixture_body[fa], bb = m.fixture_body[fb];
+        const bool act_a = W.u8(GOI_B_AWAKE, ba) && m.body_type[ba] != GOI_STATIC;
+        const bool act_b = W.u8(GOI_B_AWAKE, bb) && m.body_type[bb] != GOI_STATIC;
+        if (!act_a && !act_b) continue;
+        if (!overlap(fat_of(m, W, fa), fat_of(m, W, fb))) {
+            if (W.i32(GOI_C_COUNT, k) > 0) { W.wake(ba); W.wake(bb); }
+            W.i32(GOI_C_PAIR, k) = -1;
+            W.u8(GOI_C_TOUCHING, k) = 0;
+            W.i32(GOI_C_COUNT, k) = 0;
+            continue;
+        }
+        Manifold mf;
+        evaluate(m, fa, fb, W.xf(ba), W.xf(bb), linear_slop, mf);
+        if (contact_update(W, k, mf)) { W.wake(ba); W.wake(bb); }
+    }
+}
+
+// Sorted buffer of the smallest new candidate indices of one FindNewContacts call, plus the count of all of them.
+struct NewPairs {
+    int cand[kMaxC];
+    int kept, total, cap;
+    GOI_D void add(int p) {
+        ++total;
+        if (kept == cap && (cap == 0 || cand[kept - 1] < p)) return;
+        int j = kept < cap ? kept++ : kept - 1;
+        while (j > 0 && cand[j - 1] > p) {
+            cand[j] = cand[j - 1];
+            --j;
+        }
+        cand[j] = p;
+    }
+};
+
+GOI_D bool slot_has_pair(const World& W, int p) {
+    for (int k = 0; k < W.C; ++k)
+        if (W.i32(GOI_C_PAIR, k) == p) return true;
+    return false;
+}
+
+// b2ContactManager::FindNewContacts (pairs.py:134-178) without scanning the candidate list: each non-static fixture
+// queries the static BVH with its fat AABB, a hit maps to its candidate index through cand_static, and the few
+// non-static/non-static candidates are tested directly. New pairs (overlapping, a dynamic body, both active, no
+// contact yet) take the lowest free slots in ascending candidate order with keys in that order; a full table counts
+// the rest in overflow.
+GOI_D void find_new_contacts(const DModel& m, const World& W) {
+    if (m.P == 0) return;
+    int n_free = 0;
+    for (int k = 0; k < W.C; ++k) n_free += W.i32(GOI_C_PAIR, k) < 0;
+    NewPairs np;
+    np.kept = 0;
+    np.total = 0;
+    np.cap = n_free;
+    // static x non-static candidates via the BVH
+    for (int r = 0; r < m.R; ++r) {
+        const int fd = m.slot_fixture[r];
+        const int bd = m.fixture_body[fd];
+        if (!W.u8(GOI_B_ACTIVE, bd)) continue;
+        const float4 q = make_float4(W.f(GOI_F_FAT, 4 * r), W.f(GOI_F_FAT, 4 * r + 1), W.f(GOI_F_FAT, 4 * r + 2),
+                                     W.f(GOI_F_FAT, 4 * r + 3));
+        const bool dyn_d = m.body_type[bd] == GOI_DYNAMIC;
+        int stack[32];
+        int sp = 0;
+        if (m.n_nodes > 0) stack[sp++] = 0;
+        while (sp > 0) {
+            const int nd = stack[--sp];
+            if (!overlap(q, m.node_box[nd])) continue;
+            const int2 ch = m.node_child[nd];
+            if (ch.x >= 0) {
+                stack[sp++] = ch.y;
+                stack[sp++] = ch.x;
+                continue;
+            }
+            for (int i = ~ch.x, e = ~ch.x + ch.y; i < e; ++i) {
+                const int fs = m.leaf_fixture[i];
+                const int p = m.cand_static[(size_t)fs * m.R + r];
+                if (p < 0) continue;
+                if (!overlap(m.static_fat[fs], q)) continue;
+                const int bs = m.fixture_body[fs];
+                if (!(dyn_d || m.body_type[bs] == GOI_DYNAMIC)) continue;
+                if (!W.u8(GOI_B_ACTIVE, bs)) continue;
+                if (slot_has_pair(W, p)) continue;
+                np.add(p);
+            }
+        }
+    }
+    // non-static x non-static candidates
+    for (int i = 0; i < m.n_dd; ++i) {
+        const int p = m.dd_cand[i];
+        const int a = m.pair_a[p], b = m.pair_b[p];
+        const int ba = m.fixture_body[a], bb = m.fixture_body[b];
+        if (!overlap(fat_of(m, W, a), fat_of(m, W, b))) continue;
+        if (!(m.body_type[ba] == GOI_DYNAMIC || m.body_type[bb] == GOI_DYNAMIC)) continue;
+        if (!(W.u8(GOI_B_ACTIVE, ba) && W.u8(GOI_B_ACTIVE, bb))) continue;
+        if (slot_has_pair(W, p)) continue;
+        np.add(p);
+    }
+    if (np.total == 0) return;
+    const int base_key = W.i32(GOI_S_NEXT_KEY, 0);
+    int k = 0;
+    for (int i = 0; i < np.kept; ++i) {
+        while (W.i32(GOI_C_PAIR, k) >= 0) ++k;
+        const int p = np.cand[i];
+        const int a = m.pair_a[p], b = m.pair_b[p];
+        W.i32(GOI_C_PAIR, k) = p;
+        W.i32(GOI_C_FA, k) = a;
+        W.i32(GOI_C_FB, k) = b;
+        W.i32(GOI_C_KEY, k) = base_key + i;
+        W.u8(GOI_C_TOUCHING, k) = 0;
+        W.i32(GOI_C_COUNT, k) = 0;
+        W.f(GOI_C_NORMAL_IMPULSE, 2 * k) = 0.0f;
+        W.f(GOI_C_NORMAL_IMPULSE, 2 * k + 1) = 0.0f;
+        W.f(GOI_C_TANGENT_IMPULSE, 2 * k) = 0.0f;
+        W.f(GOI_C_TANGENT_IMPULSE, 2 * k + 1) = 0.0f;
+        W.i32(GOI_C_POINT_ID, 2 * k) = 0;
+        W.i32(GOI_C_POINT_ID, 2 * k + 1) = 0;
+        W.f(GOI_C_FRICTION, k) = fsqrt(friction_of(m, W, a) * friction_of(m, W, b));  // b2MixFriction
+        const float ra = restitution_of(m, W, a), rb = restitution_of(m, W, b);
+        W.f(GOI_C_RESTITUTION, k) = ra > rb ? ra : rb;                                // b2MixRestitution
+        W.f(GOI_C_TANGENT_SPEED, k) = 0.0f;
+        W.wake(m.fixture_body[a]);
+        W.wake(m.fixture_body[b]);
+        ++k;
+    }
+    W.i32(GOI_S_NEXT_KEY, 0) = base_key + np.total;
+    W.i32(GOI_S_OVERFLOW, 0) += np.total - np.kept;
+}
+
+// b2Fixture::ComputeAABB for fixture f at transform t
+GOI_D float4 shape_aabb(const DModel& m, int f, const Xf& t) {
+    const float r = m.radius[f];
+    if (m.shape_type[f] == GOI_CIRCLE) {
+        const V2 p = t.p + mul(t.q, mvert(m, f, 0));
+        return make_float4(p.x - r, p.y - r, p.x + r, p.y + r);
+    }
+    V2 lo = mul(t, mvert(m, f, 0)), hi = lo;
+    const int n = m.count[f];
+    for (int i = 1; i < n; ++i) {
+        const V2 v = mul(t, mvert(m, f, i));
+        lo.x = bmin(lo.x, v.x); lo.y = bmin(lo.y, v.y);
+        hi.x = bmax(hi.x, v.x); hi.y = bmax(hi.y, v.y);
+    }
+    return make_float4(lo.x - r, lo.y - r, hi.x + r, hi.y + r);
+}
+
+// b2Body::SynchronizeFixtures for body b (pairs.py:181-207): swept AABB over the sweep start and the current
+// transform; b2DynamicTree::MoveProxy re-fattens only if the fat box no longer contains it.
+GOI_D void sync_body_fixtures(const DModel& m, const World& W, int b, const Xf& x1) {
+    const Xf x2 = W.xf(b);
+    for (int r = 0; r < m.R; ++r) {
+        const int f = m.slot_fixture[r];
+        if (m.fixture_body[f] != b) continue;
+        const float4 a1 = shape_aabb(m, f, x1), a2 = shape_aabb(m, f, x2);
+        float lx = bmin(a1.x, a2.x), ly = bmin(a1.y, a2.y);
+        float ux = bmax(a1.z, a2.z), uy = bmax(a1.w, a2.w);
+        const float fx0 = W.f(GOI_F_FAT, 4 * r), fy0 = W.f(GOI_F_FAT, 4 * r + 1);
+        const float fx1 = W.f(GOI_F_FAT, 4 * r + 2), fy1 = W.f(GOI_F_FAT, 4 * r + 3);
+        if (fx0 <= lx && fy0 <= ly && ux <= fx1 && uy <= fy1) continue;
+        const V2 d = x2.p - x1.p;
+        lx = lx - 0.1f; ly = ly - 0.1f; ux = ux + 0.1f; uy = uy + 0.1f;  // b2_aabbExtension
+        const float ddx = 2.0f * d.x, ddy = 2.0f * d.y;                  // b2_aabbMultiplier
+        if (ddx < 0.0f) lx = lx + ddx; else ux = ux + ddx;
+        if (ddy < 0.0f) ly = ly + ddy; else uy = uy + ddy;
+        W.f(GOI_F_FAT, 4 * r) = lx;
+        W.f(GOI_F_FAT, 4 * r + 1) = ly;
+        W.f(GOI_F_FAT, 4 * r + 2) = ux;
+        W.f(GOI_F_FAT, 4 * r + 3) = uy;
+    }
+}
+
+// the sweep-start transform of body b: q(a0), c0 - q * localCenter
+GOI_D Xf sweep_start_xf(const World& W, int b) {
+    Xf t;
+    t.q = rot_of(W.f(GOI_B_A0, b));
+    t.p = W.v2(GOI_B_C0, b) - mul(t.q, W.v2(GOI_B_LOCAL_CENTER, b));
+    return t;
+}
+
+}  // namespace goi

@@ -1,0 +1,402 @@
+// b2_solver.hpp - b2World::Solve on the device (goi_jax/box2d/step.py:73-251, island.py, contact_solver.py,
+// joints.py): the island search, velocity integration, contact and joint constraint set-up, warm start, the
+// Gauss-Seidel velocity sweeps, position integration with the per-step clamps, position sweeps with per-island
+// early exit, transform sync, sleeping, fixture sync and FindNewContacts.
+//
+// Storage: the solver's body arrays (v, w, c, a per body) live in LDS as [field][body][lane] so each lane's random
+// body index hits its own bank; the prepared constraint rows live in a per-world HBM scratch laid out
+// [row][field][pitch] (one coalesced 256-byte segment per field per wavefront).
+#pragma once
+
+#include "b2_pairs.hpp"
+
+namespace goi {
+
+constexpr int kMaxB = 64;  // bodies per world the kernels handle
+constexpr int kMaxJ = 64;  // joints per world
+
+// Per-lane view of the solver body arrays in LDS.
+struct Bodies {
+    float* s;  // LDS base + lane
+    int B;
+    GOI_D float& at(int field, int b) const { return s[(field * B + b) * 64]; }
+    GOI_D float& vx(int b) const { return at(0, b); }
+    GOI_D float& vy(int b) const { return at(1, b); }
+    GOI_D float& w(int b) const { return at(2, b); }
+    GOI_D float& cx(int b) const { return at(3, b); }
+    GOI_D float& cy(int b) const { return at(4, b); }
+    GOI_D float& a(int b) const { return at(5, b); }
+    GOI_D V2 v(int b) const { return mk(vx(b), vy(b)); }
+    GOI_D V2 c(int b) const { return mk(cx(b), cy(b)); }
+    GOI_D void set_v(int b, V2 x, float ww) const { vx(b) = x.x; vy(b) = x.y; w(b) = ww; }
+    GOI_D void set_c(int b, V2 x, float aa) const { cx(b) = x.x; cy(b) = x.y; a(b) = aa; }
+};
+
+// Per-world HBM scratch rows: element (row, field) at base[((row * nf) + field) * pitch + w].
+struct Rows {
+    uint32_t* base;
+    int pitch, w, nf;
+    GOI_D uint32_t& u(int row, int field) const { return base[((size_t)row * nf + field) * pitch + w]; }
+    GOI_D float getf(int row, int field) const { return __uint_as_float(u(row, field)); }
+    GOI_D void setf(int row, int field, float v) const { u(row, field) = __float_as_uint(v); }
+    GOI_D int geti(int row, int field) const { return (int)u(row, field); }
+    GOI_D void seti(int row, int field, int v) const { u(row, field) = (uint32_t)v; }
+    GOI_D V2 get2(int row, int field) const { return mk(getf(row, field), getf(row, field + 1)); }
+    GOI_D void set2(int row, int field, V2 v) const { setf(row, field, v.x); setf(row, field + 1, v.y); }
+};
+
+// contact constraint row fields
+enum {
+    CF_SLOT, CF_IA, CF_IB, CF_COUNT, CF_PC_COUNT, CF_MTYPE,
+    CF_MA, CF_MB, CF_IIA, CF_IIB, CF_NX, CF_NY, CF_FRICTION, CF_TSPEED,
+    CF_RA0, CF_RA0Y, CF_RA1, CF_RA1Y, CF_RB0, CF_RB0Y, CF_RB1, CF_RB1Y,
+    CF_NMASS0, CF_NMASS1, CF_TMASS0, CF_TMASS1, CF_BIAS0, CF_BIAS1,
+    CF_NI0, CF_NI1, CF_TI0, CF_TI1, CF_K0, CF_K1, CF_K2, CF_K3, CF_NM0, CF_NM1, CF_NM2, CF_NM3,
+    CF_LN, CF_LNY, CF_LP, CF_LPY, CF_PL0, CF_PL0Y, CF_PL1, CF_PL1Y, CF_LCA, CF_LCAY, CF_LCB, CF_LCBY,
+    CF_RADA, CF_RADB,
+    CF_N
+};
+
+// joint row fields
+enum {
+    JF_JID, JF_TYPE, JF_IA, JF_IB, JF_STATE, JF_EMOTOR, JF_ELIMIT, JF_SOFT,
+    JF_MA, JF_MB, JF_IIA, JF_IIB, JF_RA, JF_RAY, JF_RB, JF_RBY,
+    JF_EXX, JF_EXY, JF_EXZ, JF_EYX, JF_EYY, JF_EYZ, JF_EZX, JF_EZY, JF_EZZ,
+    JF_MMASS, JF_MSPEED, JF_MAXIMP, JF_AX, JF_AXY, JF_PX, JF_PXY, JF_A1, JF_A2, JF_S1, JF_S2,
+    JF_GAMMA, JF_BIAS, JF_ANGLE, JF_INVDT, JF_LA, JF_LAY, JF_LB, JF_LBY, JF_LX, JF_LXY, JF_LY, JF_LYY,
+    JF_REF, JF_LOWER, JF_UPPER, JF_IMP0, JF_IMP1, JF_IMP2, JF_IMP3, JF_IMP4, JF_MIMP,
+    JF_N
+};
+
+struct Cfg {
+    GoiSettings s;
+    float dt, inv_dt, dt_ratio_unused;
+};
+
+GOI_D V2 rel_vel(V2 vB, float wB, V2 rB, V2 vA, float wA, V2 rA) {
+    return ((vB + cross(wB, rB)) - vA) - cross(wA, rA);
+}
+
+// ---------------------------------------------------------------- islands (island.py:41-140)
+
+struct Islands {
+    int corder[kMaxC];
+    int jorder[kMaxJ];
+    int body_island[kMaxB];
+    int contact_island[kMaxC];
+    int joint_island[kMaxJ];
+    int nc, nj, n;
+};
+
+// b2World::Solve's depth-first search: seeds newest body first; popping b wakes it, walks b's touching contacts
+// newest first (each joins the island and pushes its unvisited non-static other body), then b's joints newest
+// first (joints to inactive bodies skipped). Contacts and joints append to one solve order across islands.
+GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
+    int order[kMaxC];
+    const int n = list_order(W, order);
+    unsigned long long bflag = 0ull, cflag = 0ull, jflag = 0ull;
+    for (int b = 0; b < W.B; ++b) I.body_island[b] = -1;
+    for (int c = 0; c < W.C; ++c) I.contact_island[c] = -1;
+    for (int j = 0; j < W.J; ++j) I.joint_island[j] = -1;
+    int nisl = 0, nc = 0, nj = 0;
+    int stack[kMaxB];
+    for (int seed = W.B - 1; seed >= 0; --seed) {
+        if ((bflag >> seed) & 1ull) continue;
+        if (!W.u8(GOI_B_AWAKE, seed) || !W.u8(GOI_B_ACTIVE, seed) || m.body_type[seed] == GOI_STATIC) continue;
+        const int isl = nisl++;
+        int sp = 0;
+        stack[sp++] = seed;
+        bflag |= 1ull << seed;
+        while (sp > 0) {
+            const int b = stack[--sp];
+            I.body_island[b] = isl;
+            W.wake(b);
+            for (int i = 0; i < n; ++i) {
+                const int c = order[i];
+                const int ba = m.fixture_body[W.i32(GOI_C_FA, c)], bb = m.fixture_body[W.i32(GOI_C_FB, c)];
+                if (ba != b && bb != b) continue;
+                if (((cflag >> c) & 1ull) || !W.u8(GOI_C_TOUCHING, c)) continue;
+                I.corder[nc++] = c;
+                cflag |= 1ull << c;
+                I.contact_island[c] = isl;
+                const int other = ba == b ? bb : ba;
+                if (((bflag >> other) & 1ull) || m.body_type[other] == GOI_STATIC) continue;
+                stack[sp++] = other;
+                bflag |= 1ull << other;
+            }
+            for (int j = W.J - 1; j >= 0; --j) {
+                const int ja = m.joint_a[j], jb = m.joint_b[j];
+                if (ja != b && jb != b) continue;
+                if ((jflag >> j) & 1ull) continue;
+                const int other = ja == b ? jb : ja;
+                if (!W.u8(GOI_B_ACTIVE, other)) continue;
+                I.jorder[nj++] = j;
+                jflag |= 1ull << j;
+                I.joint_island[j] = isl;
+                if (((bflag >> other) & 1ull) || m.body_type[other] == GOI_STATIC) continue;
+                stack[sp++] = other;
+                bflag |= 1ull << other;
+            }
+        }
+    }
+    I.nc = nc;
+    I.nj = nj;
+    I.n = nisl;
+}
+
+// ---------------------------------------------------------------- contact solver (contact_solver.py)
+
+// b2ContactSolver constructor + InitializeVelocityConstraints for contact slot `slot` into row i
+// (contact_solver.py:32-147). Body positions/velocities from the LDS arrays; qA/qB the bodies' rotations.
+GOI_D void cs_prepare(const DModel& m, const World& W, const Bodies& bd, const Rows& R, int i, int slot, bool warm,
+                      float dt_ratio, Rot qA, Rot qB, float velocity_threshold) {
+    const int fa = W.i32(GOI_C_FA, slot), fb = W.i32(GOI_C_FB, slot);
+    const int ia = m.fixture_body[fa], ib = m.fixture_body[fb];
+    const float mA = W.f(GOI_B_INV_MASS, ia), mB = W.f(GOI_B_INV_MASS, ib);
+    const float iA = W.f(GOI_B_INV_INERTIA, ia), iB = W.f(GOI_B_INV_INERTIA, ib);
+    const V2 lcA = W.v2(GOI_B_LOCAL_CENTER, ia), lcB = W.v2(GOI_B_LOCAL_CENTER, ib);
+    const float radA = m.radius[fa], radB = m.radius[fb];
+    const int mtype = W.i32(GOI_C_MTYPE, slot);
+    const int cnt = W.i32(GOI_C_COUNT, slot);
+    const V2 ln = W.v2(GOI_C_LOCAL_NORMAL, slot), lp = W.v2(GOI_C_LOCAL_POINT, slot);
+    const V2 pl0 = W.v2(GOI_C_POINT_LOCAL, 2 * slot), pl1 = W.v2(GOI_C_POINT_LOCAL, 2 * slot + 1);
+    R.seti(i, CF_SLOT, slot); R.seti(i, CF_IA, ia); R.seti(i, CF_IB, ib);
+    R.seti(i, CF_PC_COUNT, cnt); R.seti(i, CF_MTYPE, mtype);
+    R.setf(i, CF_MA, mA); R.setf(i, CF_MB, mB); R.setf(i, CF_IIA, iA); R.setf(i, CF_IIB, iB);
+    R.set2(i, CF_LN, ln); R.set2(i, CF_LP, lp); R.set2(i, CF_PL0, pl0); R.set2(i, CF_PL1, pl1);
+    R.set2(i, CF_LCA, lcA); R.set2(i, CF_LCB, lcB); R.setf(i, CF_RADA, radA); R.setf(i, CF_RADB, radB);
+    R.setf(i, CF_NI0, warm ? dt_ratio * W.f(GOI_C_NORMAL_IMPULSE, 2 * slot) : 0.0f);
+    R.setf(i, CF_NI1, warm ? dt_ratio * W.f(GOI_C_NORMAL_IMPULSE, 2 * slot + 1) : 0.0f);
+    R.setf(i, CF_TI0, warm ? dt_ratio * W.f(GOI_C_TANGENT_IMPULSE, 2 * slot) : 0.0f);
+    R.setf(i, CF_TI1, warm ? dt_ratio * W.f(GOI_C_TANGENT_IMPULSE, 2 * slot + 1) : 0.0f);
+    R.setf(i, CF_FRICTION, W.f(GOI_C_FRICTION, slot));
+    R.setf(i, CF_TSPEED, W.f(GOI_C_TANGENT_SPEED, slot));
+    const float restitution = W.f(GOI_C_RESTITUTION, slot);
+    const V2 cA = bd.c(ia), cB = bd.c(ib);
+    const V2 vA = bd.v(ia), vB = bd.v(ib);
+    const float wA = bd.w(ia), wB = bd.w(ib);
+    Xf xfA, xfB;
+    xfA.q = qA; xfB.q = qB;
+    xfA.p = cA - mul(qA, lcA);
+    xfB.p = cB - mul(qB, lcB);
+    // b2WorldManifold::Initialize
+    V2 n = mk(1.0f, 0.0f), p0, p1;
+    if (mtype == kCircles) {
+        const V2 pA = mul(xfA, lp), pB = mul(xfB, pl0);
+        const V2 d = pB - pA;
+        if (dot(d, d) > kEps * kEps) {
+            n = d;
+            normalize(n);
+        }
+        const V2 ccA = pA + radA * n, ccB = pB - radB * n;
+        p0 = 0.5f * (ccA + ccB);
+        p1 = p0;
+    } else if (mtype == kFaceA) {
+        n = mul(qA, ln);
+        const V2 pp = mul(xfA, lp);
+        const V2 q0 = mul(xfB, pl0), q1 = mul(xfB, pl1);
+        p0 = 0.5f * ((q0 + (radA - dot(q0 - pp, n)) * n) + (q0 - radB * n));
+        p1 = 0.5f * ((q1 + (radA - dot(q1 - pp, n)) * n) + (q1 - radB * n));
+    } else {
+        n = mul(qB, ln);
+        const V2 pp = mul(xfB, lp);
+        const V2 q0 = mul(xfA, pl0), q1 = mul(xfA, pl1);
+        p0 = 0.5f * ((q0 - radA * n) + (q0 + (radB - dot(q0 - pp, n)) * n));
+        p1 = 0.5f * ((q1 - radA * n) + (q1 + (radB - dot(q1 - pp, n)) * n));
+        n = -n;
+    }
+    R.set2(i, CF_NX, n);
+    const V2 t = cross(n, 1.0f);
+    const V2 pts[2] = {p0, p1};
+    float rnA2[2], rnB2[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const V2 rA = pts[j] - cA, rB = pts[j] - cB;
+        R.set2(i, CF_RA0 + 2 * j, rA);
+        R.set2(i, CF_RB0 + 2 * j, rB);
+        const float rnA = cross(rA, n), rnB = cross(rB, n);
+        rnA2[j] = rnA;
+        rnB2[j] = rnB;
+        const float kn = ((mA + mB) + iA * rnA * rnA) + iB * rnB * rnB;
+        const float rtA = cross(rA, t), rtB = cross(rB, t);
+        const float kt = ((mA + mB) + iA * rtA * rtA) + iB * rtB * rtB;
+        R.setf(i, CF_NMASS0 + j, kn > 0.0f ? 1.0f / kn : 0.0f);
+        R.setf(i, CF_TMASS0 + j, kt > 0.0f ? 1.0f / kt : 0.0f);
+        const float vrel = dot(n, rel_vel(vB, wB, rB, vA, wA, rA));
+        R.setf(i, CF_BIAS0 + j, vrel < -velocity_threshold ? -restitution * vrel : 0.0f);
+    }
+    int vcount = cnt;
+    float K0 = 0.0f, K1 = 0.0f, K2 = 0.0f, K3 = 0.0f, N0 = 0.0f, N1 = 0.0f, N2 = 0.0f, N3 = 0.0f;
+    if (cnt == 2) {
+        const float k11 = ((mA + mB) + iA * rnA2[0] * rnA2[0]) + iB * rnB2[0] * rnB2[0];
+        const float k22 = ((mA + mB) + iA * rnA2[1] * rnA2[1]) + iB * rnB2[1] * rnB2[1];
+        const float k12 = ((mA + mB) + iA * rnA2[0] * rnA2[1]) + iB * rnB2[0] * rnB2[1];
+        if (k11 * k11 < 1000.0f * (k11 * k22 - k12 * k12)) {
+            float det = k11 * k22 - k12 * k12;
+            if (det != 0.0f) det = 1.0f / det;
+            K0 = k11; K1 = k12; K2 = k12; K3 = k22;
+            N0 = det * k22; N1 = -det * k12; N2 = -det * k12; N3 = det * k11;
+        } else {
+            vcount = 1;
+        }
+    }
+    R.seti(i, CF_COUNT, vcount);
+    R.setf(i, CF_K0, K0); R.setf(i, CF_K1, K1); R.setf(i, CF_K2, K2); R.setf(i, CF_K3, K3);
+    R.setf(i, CF_NM0, N0); R.setf(i, CF_NM1, N1); R.setf(i, CF_NM2, N2); R.setf(i, CF_NM3, N3);
+}
+
+GOI_D void cs_warm_start(const Bodies& bd, const Rows& R, int i) {
+    const int ia = R.geti(i, CF_IA), ib = R.geti(i, CF_IB), cnt = R.geti(i, CF_COUNT);
+    const float mA = R.getf(i, CF_MA), mB = R.getf(i, CF_MB), iA = R.getf(i, CF_IIA), iB = R.getf(i, CF_IIB);
+    const V2 n = R.get2(i, CF_NX), t = cross(n, 1.0f);
+    V2 vA = bd.v(ia), vB = bd.v(ib);
+    float wA = bd.w(ia), wB = bd.w(ib);
+    for (int j = 0; j < cnt; ++j) {
+        const V2 P = R.getf(i, CF_NI0 + j) * n + R.getf(i, CF_TI0 + j) * t;
+        wA = wA - iA * cross(R.get2(i, CF_RA0 + 2 * j), P);
+        vA = vA - mA * P;
+        wB = wB + iB * cross(R.get2(i, CF_RB0 + 2 * j), P);
+        vB = vB + mB * P;
+    }
+    bd.set_v(ia, vA, wA);
+    bd.set_v(ib, vB, wB);
+}
+
+// b2ContactSolver::SolveVelocityConstraints for row i (contact_solver.py:194-279)
+GOI_D void cs_solve_velocity(const Bodies& bd, const Rows& R, int i) {
+    const int ia = R.geti(i, CF_IA), ib = R.geti(i, CF_IB), cnt = R.geti(i, CF_COUNT);
+    const float mA = R.getf(i, CF_MA), mB = R.getf(i, CF_MB), iA = R.getf(i, CF_IIA), iB = R.getf(i, CF_IIB);
+    const V2 n = R.get2(i, CF_NX), t = cross(n, 1.0f);
+    const float friction = R.getf(i, CF_FRICTION), tspeed = R.getf(i, CF_TSPEED);
+    const V2 rA0 = R.get2(i, CF_RA0), rA1 = R.get2(i, CF_RA1), rB0 = R.get2(i, CF_RB0), rB1 = R.get2(i, CF_RB1);
+    float ni0 = R.getf(i, CF_NI0), ni1 = R.getf(i, CF_NI1), ti0 = R.getf(i, CF_TI0), ti1 = R.getf(i, CF_TI1);
+    V2 vA = bd.v(ia), vB = bd.v(ib);
+    float wA = bd.w(ia), wB = bd.w(ib);
+    // tangent constraints first
+    if (cnt > 0) {
+        const float vt = dot(rel_vel(vB, wB, rB0, vA, wA, rA0), t) - tspeed;
+        float lam = R.getf(i, CF_TMASS0) * (-vt);
+        const float maxf = friction * ni0;
+        const float nw = bclamp(ti0 + lam, -maxf, maxf);
+        lam = nw - ti0;
+        ti0 = nw;
+        const V2 P = lam * t;
+        vA = vA - mA * P; wA = wA - iA * cross(rA0, P);
+        vB = vB + mB * P; wB = wB + iB * cross(rB0, P);
+    }
+    if (cnt > 1) {
+        const float vt = dot(rel_vel(vB, wB, rB1, vA, wA, rA1), t) - tspeed;
+        float lam = R.getf(i, CF_TMASS1) * (-vt);
+        const float maxf = friction * ni1;
+        const float nw = bclamp(ti1 + lam, -maxf, maxf);
+        lam = nw - ti1;
+        ti1 = nw;
+        const V2 P = lam * t;
+        vA = vA - mA * P; wA = wA - iA * cross(rA1, P);
+        vB = vB + mB * P; wB = wB + iB * cross(rB1, P);
+    }
+    if (cnt == 1) {
+        const float vn = dot(rel_vel(vB, wB, rB0, vA, wA, rA0), n);
+        float lam = -R.getf(i, CF_NMASS0) * (vn - R.getf(i, CF_BIAS0));
+        const float nw = bmax(ni0 + lam, 0.0f);
+        lam = nw - ni0;
+        ni0 = nw;
+        const V2 P = lam * n;
+        vA = vA - mA * P; wA = wA - iA * cross(rA0, P);
+        vB = vB + mB * P; wB = wB + iB * cross(rB0, P);
+    } else if (cnt == 2) {
+        const float K0 = R.getf(i, CF_K0), K1 = R.getf(i, CF_K1), K2 = R.getf(i, CF_K2), K3 = R.getf(i, CF_K3);
+        const float ax = ni0, ay = ni1;
+        const float vn1 = dot(rel_vel(vB, wB, rB0, vA, wA, rA0), n);
+        const float vn2 = dot(rel_vel(vB, wB, rB1, vA, wA, rA1), n);
+        float bx = vn1 - R.getf(i, CF_BIAS0), by = vn2 - R.getf(i, CF_BIAS1);
+        bx = bx - (K0 * ax + K2 * ay);
+        by = by - (K1 * ax + K3 * ay);
+        float xx = -(R.getf(i, CF_NM0) * bx + R.getf(i, CF_NM2) * by);
+        float xy = -(R.getf(i, CF_NM1) * bx + R.getf(i, CF_NM3) * by);
+        bool ok = xx >= 0.0f && xy >= 0.0f;
+        if (!ok) {
+            xx = -R.getf(i, CF_NMASS0) * bx;
+            xy = 0.0f;
+            ok = xx >= 0.0f && K1 * xx + by >= 0.0f;
+        }
+        if (!ok) {
+            xx = 0.0f;
+            xy = -R.getf(i, CF_NMASS1) * by;
+            ok = xy >= 0.0f && K2 * xy + bx >= 0.0f;
+        }
+        if (!ok) {
+            xx = 0.0f;
+            xy = 0.0f;
+            ok = bx >= 0.0f && by >= 0.0f;
+        }
+        if (ok) {
+            const float dx = xx - ax, dy = xy - ay;
+            const V2 P1 = dx * n, P2 = dy * n;
+            vA = vA - mA * (P1 + P2);
+            wA = wA - iA * (cross(rA0, P1) + cross(rA1, P2));
+            vB = vB + mB * (P1 + P2);
+            wB = wB + iB * (cross(rB0, P1) + cross(rB1, P2));
+            ni0 = xx;
+            ni1 = xy;
+        }
+    }
+    R.setf(i, CF_NI0, ni0); R.setf(i, CF_NI1, ni1); R.setf(i, CF_TI0, ti0); R.setf(i, CF_TI1, ti1);
+    bd.set_v(ia, vA, wA);
+    bd.set_v(ib, vB, wB);
+}
+
+// b2ContactSolver::SolvePositionConstraints for row i (contact_solver.py:307-354); masses given (the TOI solve
+// passes zero for bodies other than the TOI pair). Returns the row's min separation, starting at 0.
+GOI_D float cs_solve_position(const Bodies& bd, const Rows& R, int i, float baumgarte, float mA, float mB, float iA,
+                              float iB, float linear_slop, float max_linear_correction) {
+    const int ia = R.geti(i, CF_IA), ib = R.geti(i, CF_IB), cnt = R.geti(i, CF_PC_COUNT);
+    const int mtype = R.geti(i, CF_MTYPE);
+    const V2 lcA = R.get2(i, CF_LCA), lcB = R.get2(i, CF_LCB), ln = R.get2(i, CF_LN), lp = R.get2(i, CF_LP);
+    const float radA = R.getf(i, CF_RADA), radB = R.getf(i, CF_RADB);
+    V2 cA = bd.c(ia), cB = bd.c(ib);
+    float aA = bd.a(ia), aB = bd.a(ib);
+    float min_sep = 0.0f;
+    for (int j = 0; j < cnt; ++j) {
+        Xf xfA, xfB;
+        xfA.q = rot_of(aA);
+        xfB.q = rot_of(aB);
+        xfA.p = cA - mul(xfA.q, lcA);
+        xfB.p = cB - mul(xfB.q, lcB);
+        const V2 plj = R.get2(i, CF_PL0 + 2 * j);
+        V2 n, p;
+        float sep;
+        if (mtype == kCircles) {
+            const V2 pA = mul(xfA, lp), pB = mul(xfB, R.get2(i, CF_PL0));
+            n = pB - pA;
+            normalize(n);
+            p = 0.5f * (pA + pB);
+            sep = (dot(pB - pA, n) - radA) - radB;
+        } else if (mtype == kFaceA) {
+            n = mul(xfA.q, ln);
+            const V2 cp = mul(xfB, plj);
+            sep = (dot(cp - mul(xfA, lp), n) - radA) - radB;
+            p = cp;
+        } else {
+            n = mul(xfB.q, ln);
+            const V2 cp = mul(xfA, plj);
+            sep = (dot(cp - mul(xfB, lp), n) - radA) - radB;
+            p = cp;
+            n = -n;
+        }
+        const V2 rA = p - cA, rB = p - cB;
+        min_sep = bmin(min_sep, sep);
+        const float C = bclamp(baumgarte * (sep + linear_slop), -max_linear_correction, 0.0f);
+        const float rnA = cross(rA, n), rnB = cross(rB, n);
+        const float K = ((mA + mB) + iA * rnA * rnA) + iB * rnB * rnB;
+        const float imp = K > 0.0f ? -C / K : 0.0f;
+        const V2 P = imp * n;
+        cA = cA - mA * P; aA = aA - iA * cross(rA, P);
+        cB = cB + mB * P; aB = aB + iB * cross(rB, P);
+    }
+    bd.set_c(ia, cA, aA);
+    bd.set_c(ib, cB, aB);
+    return min_sep;
+}
+
+}  // namespace goi

@@ -1,0 +1,355 @@
+// b2_toi.hpp - continuous collision on the device: b2World::SolveTOI with b2TimeOfImpact, b2Distance (GJK),
+// b2SeparationFunction, b2Sweep::Advance and b2Island::SolveTOI (goi_jax/box2d/toi.py:73-865). Each lane runs its
+// own world's event loop; the sweeps live in the State leaves (c0, c, a0, a, toi.alpha0).
+#pragma once
+
+#include "b2_joints.hpp"
+
+namespace goi {
+
+struct Sweep {
+    V2 lc, c0, c;
+    float a0, a;
+};
+
+// b2Sweep::GetTransform (toi.py:73-81)
+GOI_D Xf sweep_xf(const Sweep& sw, float beta) {
+    Xf t;
+    const float omb = 1.0f - beta;
+    t.q = rot_of(omb * sw.a0 + beta * sw.a);
+    t.p = mk(omb * sw.c0.x + beta * sw.c.x, omb * sw.c0.y + beta * sw.c.y) - mul(t.q, sw.lc);
+    return t;
+}
+
+GOI_D Sweep body_sweep(const World& W, int b) {
+    Sweep s;
+    s.lc = W.v2(GOI_B_LOCAL_CENTER, b);
+    s.c0 = W.v2(GOI_B_C0, b);
+    s.c = W.v2(GOI_B_C, b);
+    s.a0 = W.f(GOI_B_A0, b);
+    s.a = W.f(GOI_B_A, b);
+    return s;
+}
+
+// b2Sweep::Advance on body b's sweep (toi.py:100-104)
+GOI_D void sweep_advance(const World& W, int b, float alpha) {
+    const float al0 = W.f(GOI_T_ALPHA0, b);
+    const float den = 1.0f - al0;
+    const float beta = (alpha - al0) / (den != 0.0f ? den : 1.0f);
+    const V2 c0 = W.v2(GOI_B_C0, b), c = W.v2(GOI_B_C, b);
+    W.set2(GOI_B_C0, b, c0 + beta * (c - c0));
+    const float a0 = W.f(GOI_B_A0, b);
+    W.f(GOI_B_A0, b) = a0 + beta * (W.f(GOI_B_A, b) - a0);
+    W.f(GOI_T_ALPHA0, b) = alpha;
+}
+
+// b2Body::SynchronizeTransform
+GOI_D void sync_transform(const World& W, int b) {
+    const Rot q = rot_of(W.f(GOI_B_A, b));
+    W.set2(GOI_B_XF_P, b, W.v2(GOI_B_C, b) - mul(q, W.v2(GOI_B_LOCAL_CENTER, b)));
+    W.f(GOI_B_XF_Q, 2 * b) = q.c;
+    W.f(GOI_B_XF_Q, 2 * b + 1) = q.s;
+}
+
+// b2Body::Advance
+GOI_D void body_advance(const World& W, int b, float alpha) {
+    sweep_advance(W, b, alpha);
+    W.set2(GOI_B_C, b, W.v2(GOI_B_C0, b));
+    W.f(GOI_B_A, b) = W.f(GOI_B_A0, b);
+    sync_transform(W, b);
+}
+
+struct SweepBackup {
+    V2 c0, c;
+    float a0, a, alpha0;
+};
+GOI_D SweepBackup backup(const World& W, int b) {
+    SweepBackup k;
+    k.c0 = W.v2(GOI_B_C0, b); k.c = W.v2(GOI_B_C, b);
+    k.a0 = W.f(GOI_B_A0, b); k.a = W.f(GOI_B_A, b); k.alpha0 = W.f(GOI_T_ALPHA0, b);
+    return k;
+}
+GOI_D void restore(const World& W, int b, const SweepBackup& k) {
+    W.set2(GOI_B_C0, b, k.c0); W.set2(GOI_B_C, b, k.c);
+    W.f(GOI_B_A0, b) = k.a0; W.f(GOI_B_A, b) = k.a; W.f(GOI_T_ALPHA0, b) = k.alpha0;
+    sync_transform(W, b);
+}
+
+// ---------------------------------------------------------------- distance proxies and GJK (toi.py:116-294)
+
+struct Proxy {
+    const V2* v;
+    int count;
+    float radius;
+};
+GOI_D Proxy proxy_of(const DModel& m, int f) {
+    Proxy p;
+    p.v = m.verts + f * kPoly;
+    p.count = m.count[f];
+    p.radius = m.radius[f];
+    return p;
+}
+// b2DistanceProxy::GetSupport: first index of the largest dot
+GOI_D int support(const Proxy& p, V2 d) {
+    int best = 0;
+    float bv = dot(p.v[0], d);
+    for (int i = 1; i < p.count; ++i) {
+        const float v = dot(p.v[i], d);
+        if (v > bv) {
+            best = i;
+            bv = v;
+        }
+    }
+    return best;
+}
+
+struct SVert {
+    V2 wA, wB, w;
+    float a;
+    int iA, iB;
+};
+struct SimplexCache {
+    float metric;
+    int count;
+    int iA[3], iB[3];
+};
+
+GOI_D float metric(const SVert* v, int count) {
+    if (count == 2) return length(v[0].w - v[1].w);
+    if (count == 3) return cross(v[1].w - v[0].w, v[2].w - v[0].w);
+    return 0.0f;
+}
+
+GOI_D void set_vertex(SVert& v, const Proxy& pA, const Xf& xA, int iA, const Proxy& pB, const Xf& xB, int iB) {
+    v.iA = iA;
+    v.iB = iB;
+    v.wA = mul(xA, pA.v[iA]);
+    v.wB = mul(xB, pB.v[iB]);
+    v.w = v.wB - v.wA;
+}
+
+GOI_D void simplex_solve2(SVert* v, int& count) {
+    const V2 w1 = v[0].w, w2 = v[1].w, e12 = w2 - w1;
+    const float d12_2 = -dot(w1, e12);
+    if (d12_2 <= 0.0f) { v[0].a = 1.0f; count = 1; return; }
+    const float d12_1 = dot(w2, e12);
+    if (d12_1 <= 0.0f) { v[1].a = 1.0f; count = 1; v[0] = v[1]; return; }
+    const float inv = 1.0f / (d12_1 + d12_2);
+    v[0].a = d12_1 * inv;
+    v[1].a = d12_2 * inv;
+    count = 2;
+}
+
+GOI_D void simplex_solve3(SVert* v, int& count) {
+    const V2 w1 = v[0].w, w2 = v[1].w, w3 = v[2].w;
+    const V2 e12 = w2 - w1, e13 = w3 - w1, e23 = w3 - w2;
+    const float d12_1 = dot(w2, e12), d12_2 = -dot(w1, e12);
+    const float d13_1 = dot(w3, e13), d13_2 = -dot(w1, e13);
+    const float d23_1 = dot(w3, e23), d23_2 = -dot(w2, e23);
+    const float n123 = cross(e12, e13);
+    const float d123_1 = n123 * cross(w2, w3), d123_2 = n123 * cross(w3, w1), d123_3 = n123 * cross(w1, w2);
+    if (d12_2 <= 0.0f && d13_2 <= 0.0f) { v[0].a = 1.0f; count = 1; return; }
+    if (d12_1 > 0.0f && d12_2 > 0.0f && d123_3 <= 0.0f) {
+        const float inv = 1.0f / (d12_1 + d12_2);
+        v[0].a = d12_1 * inv; v[1].a = d12_2 * inv; count = 2; return;
+    }
+    if (d13_1 > 0.0f && d13_2 > 0.0f && d123_2 <= 0.0f) {
+        const float inv = 1.0f / (d13_1 + d13_2);
+        v[0].a = d13_1 * inv; v[2].a = d13_2 * inv; count = 2; v[1] = v[2]; return;
+    }
+    if (d12_1 <= 0.0f && d23_2 <= 0.0f) { v[1].a = 1.0f; count = 1; v[0] = v[1]; return; }
+    if (d13_1 <= 0.0f && d23_1 <= 0.0f) { v[2].a = 1.0f; count = 1; v[0] = v[2]; return; }
+    if (d23_1 > 0.0f && d23_2 > 0.0f && d123_1 <= 0.0f) {
+        const float inv = 1.0f / (d23_1 + d23_2);
+        v[1].a = d23_1 * inv; v[2].a = d23_2 * inv; count = 2; v[0] = v[2]; return;
+    }
+    const float inv = 1.0f / ((d123_1 + d123_2) + d123_3);
+    v[0].a = d123_1 * inv; v[1].a = d123_2 * inv; v[2].a = d123_3 * inv;
+    count = 3;
+}
+
+// b2Distance (useRadii = false): the distance and the updated simplex cache
+GOI_D float gjk_distance(SimplexCache& cache, const Proxy& pA, const Xf& xA, const Proxy& pB, const Xf& xB) {
+    SVert v[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        v[i].a = 0.0f;
+        v[i].iA = 0; v[i].iB = 0;
+        v[i].wA = mk(0.0f, 0.0f); v[i].wB = v[i].wA; v[i].w = v[i].wA;
+    }
+    int count = cache.count;
+    for (int i = 0; i < count; ++i) set_vertex(v[i], pA, xA, cache.iA[i], pB, xB, cache.iB[i]);
+    if (count > 1) {
+        const float m1 = cache.metric, m2 = metric(v, count);
+        if (m2 < 0.5f * m1 || 2.0f * m1 < m2 || m2 < kEps) count = 0;
+    }
+    if (count == 0) {
+        set_vertex(v[0], pA, xA, 0, pB, xB, 0);
+        v[0].a = 1.0f;
+        count = 1;
+    }
+    int saveA[3], saveB[3];
+    for (int iter = 0; iter < 20;) {
+        const int save = count;
+        for (int i = 0; i < save; ++i) { saveA[i] = v[i].iA; saveB[i] = v[i].iB; }
+        if (count == 2) simplex_solve2(v, count);
+        else if (count == 3) simplex_solve3(v, count);
+        if (count == 3) break;
+        V2 d;
+        if (count == 1) {
+            d = -v[0].w;
+        } else {
+            const V2 e12 = v[1].w - v[0].w;
+            d = cross(e12, -v[0].w) > 0.0f ? cross(1.0f, e12) : cross(e12, 1.0f);
+        }
+        if (dot(d, d) < kEps * kEps) break;
+        SVert& nv = v[count];
+        const float keep_a = nv.a;  // the new vertex's barycentric coordinate is left as it was
+        set_vertex(nv, pA, xA, support(pA, mulT(xA.q, -d)), pB, xB, support(pB, mulT(xB.q, d)));
+        nv.a = keep_a;
+        ++iter;
+        bool dup = false;
+        for (int i = 0; i < save; ++i) dup |= (nv.iA == saveA[i] && nv.iB == saveB[i]);
+        if (dup) break;
+        ++count;
+    }
+    V2 pa, pb;
+    if (count == 1) {
+        pa = v[0].wA;
+        pb = v[0].wB;
+    } else if (count == 2) {
+        pa = v[0].a * v[0].wA + v[1].a * v[1].wA;
+        pb = v[0].a * v[0].wB + v[1].a * v[1].wB;
+    } else {
+        pa = (v[0].a * v[0].wA + v[1].a * v[1].wA) + v[2].a * v[2].wA;
+        pb = pa;
+    }
+    cache.metric = metric(v, count);
+    cache.count = count;
+    for (int i = 0; i < count; ++i) { cache.iA[i] = v[i].iA; cache.iB[i] = v[i].iB; }
+    return length(pa - pb);
+}
+
+// ---------------------------------------------------------------- b2SeparationFunction and b2TimeOfImpact
+
+enum { kSepPoints = 0, kSepFaceA = 1, kSepFaceB = 2 };
+struct SepFn {
+    int type;
+    V2 axis, lp;
+};
+
+GOI_D SepFn sep_init(const SimplexCache& cache, const Proxy& pA, const Sweep& sA, const Proxy& pB, const Sweep& sB,
+                     float t1) {
+    const Xf xA = sweep_xf(sA, t1), xB = sweep_xf(sB, t1);
+    SepFn f;
+    f.lp = mk(0.0f, 0.0f);
+    if (cache.count == 1) {
+        f.type = kSepPoints;
+        f.axis = mul(xB, pB.v[cache.iB[0]]) - mul(xA, pA.v[cache.iA[0]]);
+        normalize(f.axis);
+    } else if (cache.iA[0] == cache.iA[1]) {
+        f.type = kSepFaceB;
+        const V2 b1 = pB.v[cache.iB[0]], b2 = pB.v[cache.iB[1]];
+        f.axis = cross(b2 - b1, 1.0f);
+        normalize(f.axis);
+        const V2 n = mul(xB.q, f.axis);
+        f.lp = 0.5f * (b1 + b2);
+        if (dot(mul(xA, pA.v[cache.iA[0]]) - mul(xB, f.lp), n) < 0.0f) f.axis = -f.axis;
+    } else {
+        f.type = kSepFaceA;
+        const V2 a1 = pA.v[cache.iA[0]], a2 = pA.v[cache.iA[1]];
+        f.axis = cross(a2 - a1, 1.0f);
+        normalize(f.axis);
+        const V2 n = mul(xA.q, f.axis);
+        f.lp = 0.5f * (a1 + a2);
+        if (dot(mul(xB, pB.v[cache.iB[0]]) - mul(xA, f.lp), n) < 0.0f) f.axis = -f.axis;
+    }
+    return f;
+}
+
+GOI_D float sep_eval(const SepFn& f, const Proxy& pA, const Sweep& sA, const Proxy& pB, const Sweep& sB, int iA,
+                     int iB, float t) {
+    const Xf xA = sweep_xf(sA, t), xB = sweep_xf(sB, t);
+    if (f.type == kSepPoints) return dot(mul(xB, pB.v[iB]) - mul(xA, pA.v[iA]), f.axis);
+    if (f.type == kSepFaceA) return dot(mul(xB, pB.v[iB]) - mul(xA, f.lp), mul(xA.q, f.axis));
+    return dot(mul(xA, pA.v[iA]) - mul(xB, f.lp), mul(xB.q, f.axis));
+}
+
+GOI_D float sep_find_min(const SepFn& f, const Proxy& pA, const Sweep& sA, const Proxy& pB, const Sweep& sB, int& iA,
+                         int& iB, float t) {
+    const Xf xA = sweep_xf(sA, t), xB = sweep_xf(sB, t);
+    if (f.type == kSepPoints) {
+        iA = support(pA, mulT(xA.q, f.axis));
+        iB = support(pB, mulT(xB.q, -f.axis));
+        return dot(mul(xB, pB.v[iB]) - mul(xA, pA.v[iA]), f.axis);
+    }
+    if (f.type == kSepFaceA) {
+        const V2 n = mul(xA.q, f.axis);
+        iA = -1;
+        iB = support(pB, mulT(xB.q, -n));
+        return dot(mul(xB, pB.v[iB]) - mul(xA, f.lp), n);
+    }
+    const V2 n = mul(xB.q, f.axis);
+    iB = -1;
+    iA = support(pA, mulT(xA.q, -n));
+    return dot(mul(xA, pA.v[iA]) - mul(xB, f.lp), n);
+}
+
+enum { kToiUnknown = 0, kToiFailed = 1, kToiOverlapped = 2, kToiTouching = 3, kToiSeparated = 4 };
+
+// b2TimeOfImpact with tMax = 1 (toi.py:364-457): separating axes (20), push-backs (8), root finder (50 steps of
+// alternating bisection and secant)
+GOI_D int time_of_impact(const Proxy& pA, Sweep sA, const Proxy& pB, Sweep sB, float linear_slop, float& t_out) {
+    const float two_pi = 2.0f * kPi;
+    {
+        const float d = two_pi * floorf(sA.a0 / two_pi);
+        sA.a0 = sA.a0 - d; sA.a = sA.a - d;
+    }
+    {
+        const float d = two_pi * floorf(sB.a0 / two_pi);
+        sB.a0 = sB.a0 - d; sB.a = sB.a - d;
+    }
+    const float total_radius = pA.radius + pB.radius;
+    const float target = bmax(linear_slop, total_radius - 3.0f * linear_slop);
+    const float tol = 0.25f * linear_slop;
+    float t1 = 0.0f;
+    SimplexCache cache;
+    cache.count = 0;
+    cache.metric = 0.0f;
+    int state = kToiUnknown;
+    t_out = 1.0f;
+    for (int iter = 0;;) {
+        const float dist = gjk_distance(cache, pA, sweep_xf(sA, t1), pB, sweep_xf(sB, t1));
+        if (dist <= 0.0f) { state = kToiOverlapped; t_out = 0.0f; break; }
+        if (dist < target + tol) { state = kToiTouching; t_out = t1; break; }
+        const SepFn f = sep_init(cache, pA, sA, pB, sB, t1);
+        bool done = false;
+        float t2 = 1.0f;
+        for (int push = 0;;) {
+            int iA, iB;
+            float s2 = sep_find_min(f, pA, sA, pB, sB, iA, iB, t2);
+            if (s2 > target + tol) { state = kToiSeparated; t_out = 1.0f; done = true; break; }
+            if (s2 > target - tol) { t1 = t2; break; }
+            float s1 = sep_eval(f, pA, sA, pB, sB, iA, iB, t1);
+            if (s1 < target - tol) { state = kToiFailed; t_out = t1; done = true; break; }
+            if (s1 <= target + tol) { state = kToiTouching; t_out = t1; done = true; break; }
+            float a1 = t1, a2 = t2;
+            for (int rc = 0;;) {
+                const float t = (rc & 1) ? a1 + (target - s1) * (a2 - a1) / (s2 - s1) : 0.5f * (a1 + a2);
+                ++rc;
+                const float s = sep_eval(f, pA, sA, pB, sB, iA, iB, t);
+                if (babs(s - target) < tol) { t2 = t; break; }
+                if (s > target) { a1 = t; s1 = s; }
+                else { a2 = t; s2 = s; }
+                if (rc == 50) break;
+            }
+            if (++push == kPoly) break;
+        }
+        ++iter;
+        if (done) break;
+        if (iter == 20) { state = kToiFailed; t_out = t1; break; }
+    }
+    return state;
+}
+
+}  // namespace goi

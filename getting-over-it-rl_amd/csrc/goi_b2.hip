@@ -1,0 +1,406 @@
+// goi_b2.hip - the MI355X batched Box2D 2.3.1 world step (libgoi_b2.so) and its C ABI (include/goi_b2.h).
+//
+// Execution model: one lane per world. A step is three launches over ceil(N / 64) wavefronts of 64 lanes:
+//   k_collide  start-of-step FindNewContacts where new_fixture, then Collide     (step.py:30-35, pairs.py:38-178)
+//   k_solve    b2World::Solve: islands, solver, sleep, fixture sync, FindNewContacts (step.py:73-182)
+//   k_toi      b2World::SolveTOI event loop, then inv_dt0 and ClearForces         (toi.py:827-865, step.py:41-46)
+// Box2D's sequential orders inside a world (contact list newest first, island DFS, Gauss-Seidel sweeps, TOI events)
+// are kept exactly; the parallelism is across worlds. State leaves are read and written in place in the
+// worlds-minor layout; the solver's body arrays sit in LDS ([field][body][lane]), its constraint rows in a
+// per-world HBM scratch ([row][field][pitch]); the static terrain is a BVH over the static fixtures' fat AABBs,
+// shared by every world and read through L2.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/goi_b2.h"
+#include "b2_step.hpp"
+
+using namespace goi;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+    g_error = msg;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                      \
+    do {                                                                                   \
+        hipError_t e_ = (expr);                                                            \
+        if (e_ != hipSuccess) return fail(GOI_E_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+constexpr int kBlock = 64;
+constexpr int kBodyFields = 8;  // vx vy w cx cy a qc qs
+
+struct Launch {
+    void* leaf[GOI_NUM_LEAVES];
+    int n, pitch, B, C, R, J;
+    uint32_t* scratch;  // contact rows then joint rows
+    GoiSettings s;
+    float dt;
+    GoiDebug dbg;
+};
+
+__device__ __forceinline__ World make_world(const Launch& L, int w) {
+    World W;
+    W.pitch = L.pitch;
+    W.B = L.B;
+    W.C = L.C;
+    W.R = L.R;
+    W.J = L.J;
+    W.lv = L.leaf;
+    W.w = w;
+    return W;
+}
+
+__device__ __forceinline__ Rows contact_rows(const Launch& L, int w) {
+    Rows R;
+    R.base = L.scratch;
+    R.pitch = L.pitch;
+    R.w = w;
+    R.nf = CF_N;
+    return R;
+}
+__device__ __forceinline__ Rows joint_rows(const Launch& L, int w) {
+    Rows R;
+    R.base = L.scratch + (size_t)L.C * CF_N * L.pitch;
+    R.pitch = L.pitch;
+    R.w = w;
+    R.nf = JF_N;
+    return R;
+}
+
+// ---------------------------------------------------------------- kernels
+
+__global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int start_only) {
+    const int w = blockIdx.x * kBlock + threadIdx.x;
+    if (w >= L.n) return;
+    const World W = make_world(L, w);
+    if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
+    W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
+    if (!start_only) collide_walk(m, W, L.s.linear_slop);
+}
+
+__global__ void __launch_bounds__(kBlock) k_solve(DModel m, Launch L) {
+    extern __shared__ float lds[];
+    const int w = blockIdx.x * kBlock + threadIdx.x;
+    if (w >= L.n) return;
+    const World W = make_world(L, w);
+    Bodies bd;
+    bd.s = lds + threadIdx.x;
+    bd.B = L.B;
+    solve_world(m, W, bd, contact_rows(L, w), joint_rows(L, w), L.s, L.dt, L.dbg);
+}
+
+__global__ void __launch_bounds__(kBlock) k_toi(DModel m, Launch L) {
+    extern __shared__ float lds[];
+    const int w = blockIdx.x * kBlock + threadIdx.x;
+    if (w >= L.n) return;
+    const World W = make_world(L, w);
+    Bodies bd;
+    bd.s = lds + threadIdx.x;
+    bd.B = L.B;
+    if (L.s.continuous_physics) solve_toi_world(m, W, bd, contact_rows(L, w), L.s, L.dt);
+    const float dt = L.dt;
+    if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
+    if (L.s.auto_clear_forces)
+        for (int b = 0; b < W.B; ++b) {
+            W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
+            W.f(GOI_B_TORQUE, b) = 0.0f;
+        }
+}
+
+__global__ void k_sincos(const float* x, float* s, float* c, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const Rot q = rot_of(x[i]);
+    s[i] = q.s;
+    c[i] = q.c;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- model upload and the static BVH
+
+struct GoiModel {
+    DModel d;
+    std::vector<void*> allocs;
+    int C;
+    uint32_t* scratch = nullptr;
+    size_t scratch_words = 0;
+    int device = 0;
+};
+
+namespace {
+
+template <typename T>
+int upload(GoiModel* M, const T* host, size_t n, const T*& dev, hipStream_t st) {
+    if (n == 0 || host == nullptr) {
+        dev = nullptr;
+        return GOI_OK;
+    }
+    void* p = nullptr;
+    HIP_TRY(hipMalloc(&p, n * sizeof(T)));
+    M->allocs.push_back(p);
+    HIP_TRY(hipMemcpyAsync(p, host, n * sizeof(T), hipMemcpyHostToDevice, st));
+    dev = static_cast<const T*>(p);
+    return GOI_OK;
+}
+
+struct BvhBuild {
+    const float* fat;  // [F, 4]
+    std::vector<int> leaf;
+    std::vector<float4> box;
+    std::vector<int2> child;
+    int max_depth = 0;
+
+    float4 bounds(int lo, int hi) const {
+        float4 b = make_float4(3.4e38f, 3.4e38f, -3.4e38f, -3.4e38f);
+        for (int i = lo; i < hi; ++i) {
+            const float* f = fat + 4 * leaf[i];
+            b.x = std::min(b.x, f[0]); b.y = std::min(b.y, f[1]);
+            b.z = std::max(b.z, f[2]); b.w = std::max(b.w, f[3]);
+        }
+        return b;
+    }
+    // median split on the longer axis of the centroid bounds; leaves of up to 4 fixtures
+    int build(int lo, int hi, int depth) {
+        max_depth = std::max(max_depth, depth);
+        const int node = (int)box.size();
+        box.push_back(bounds(lo, hi));
+        child.push_back(make_int2(0, 0));
+        if (hi - lo <= 4) {
+            child[node] = make_int2(~lo, hi - lo);
+            return node;
+        }
+        float cx0 = 3.4e38f, cy0 = 3.4e38f, cx1 = -3.4e38f, cy1 = -3.4e38f;
+        for (int i = lo; i < hi; ++i) {
+            const float* f = fat + 4 * leaf[i];
+            const float cx = 0.5f * (f[0] + f[2]), cy = 0.5f * (f[1] + f[3]);
+            cx0 = std::min(cx0, cx); cx1 = std::max(cx1, cx);
+            cy0 = std::min(cy0, cy); cy1 = std::max(cy1, cy);
+        }
+        const int axis = (cx1 - cx0) >= (cy1 - cy0) ? 0 : 1;
+        const int mid = (lo + hi) / 2;
+        std::nth_element(leaf.begin() + lo, leaf.begin() + mid, leaf.begin() + hi, [&](int a, int b) {
+            const float* fa = fat + 4 * a;
+            const float* fb = fat + 4 * b;
+            const float ca = fa[axis] + fa[axis + 2], cb = fb[axis] + fb[axis + 2];
+            return ca < cb || (ca == cb && a < b);
+        });
+        const int l = build(lo, mid, depth + 1);
+        const int r = build(mid, hi, depth + 1);
+        child[node] = make_int2(l, r);
+        return node;
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int32_t goi_abi_version(void) { return GOI_ABI_VERSION; }
+
+const char* goi_last_error(void) { return g_error.c_str(); }
+
+int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, void* hip_stream, GoiModel** out) {
+    if (!desc || !out) return fail(GOI_E_ARG, "goi_model_create: null argument");
+    *out = nullptr;
+    const int F = desc->F, J = desc->J, P = desc->P, B = desc->B;
+    if (F < 0 || J < 0 || P < 0 || B <= 0) return fail(GOI_E_ARG, "goi_model_create: negative or zero sizes");
+    if (!desc->fixture_slot || !desc->static_fat || !desc->body_type)
+        return fail(GOI_E_UNSUPPORTED, "goi_model_create: the device step needs the compact fixture layout and body types");
+    if (B > kMaxB) return fail(GOI_E_UNSUPPORTED, "goi_model_create: more than 64 bodies per world");
+    if (J > kMaxJ) return fail(GOI_E_UNSUPPORTED, "goi_model_create: more than 64 joints per world");
+    if (contact_capacity < 0 || contact_capacity > kMaxC)
+        return fail(GOI_E_UNSUPPORTED, "goi_model_create: contact capacity above 64");
+    for (int j = 0; j < J; ++j) {
+        const int t = desc->joint_type[j];
+        if (t != GOI_REVOLUTE && t != GOI_PRISMATIC && t != GOI_WELD)
+            return fail(GOI_E_UNSUPPORTED, "goi_model_create: unknown joint type");
+    }
+    for (int f = 0; f < F; ++f) {
+        const int t = desc->shape_type[f], c = desc->count[f];
+        if ((t != GOI_CIRCLE && t != GOI_POLYGON) || c < 1 || c > GOI_MAX_POLY)
+            return fail(GOI_E_UNSUPPORTED, "goi_model_create: bad shape");
+        if (desc->fixture_body[f] < 0 || desc->fixture_body[f] >= B) return fail(GOI_E_ARG, "goi_model_create: bad fixture body");
+    }
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    GoiModel* M = new GoiModel();
+    M->C = contact_capacity;
+    HIP_TRY(hipGetDevice(&M->device));
+    DModel& d = M->d;
+    d.F = F; d.J = J; d.P = P; d.B = B;
+    // non-static rows
+    std::vector<int> slot_fixture;
+    for (int f = 0; f < F; ++f)
+        if (desc->fixture_slot[f] >= 0) slot_fixture.push_back(f);
+    for (size_t r = 0; r < slot_fixture.size(); ++r)
+        if (desc->fixture_slot[slot_fixture[r]] != (int)r) {
+            delete M;
+            return fail(GOI_E_ARG, "goi_model_create: fixture_slot rows must ascend with the fixture index");
+        }
+    const int R = (int)slot_fixture.size();
+    d.R = R;
+    // candidate tables
+    std::vector<int> cand((size_t)F * std::max(R, 1), -1), dd;
+    for (int p = 0; p < P; ++p) {
+        const int a = desc->pair_a[p], b = desc->pair_b[p];
+        if (a < 0 || a >= F || b < 0 || b >= F) { delete M; return fail(GOI_E_ARG, "goi_model_create: bad candidate pair"); }
+        const int ra = desc->fixture_slot[a], rb = desc->fixture_slot[b];
+        if (ra >= 0 && rb >= 0) dd.push_back(p);
+        else if (ra < 0 && rb >= 0) cand[(size_t)a * R + rb] = p;
+        else if (rb < 0 && ra >= 0) cand[(size_t)b * R + ra] = p;
+        else { delete M; return fail(GOI_E_UNSUPPORTED, "goi_model_create: candidate between two static fixtures"); }
+    }
+    // static BVH
+    BvhBuild bvh;
+    bvh.fat = desc->static_fat;
+    for (int f = 0; f < F; ++f)
+        if (desc->fixture_slot[f] < 0) bvh.leaf.push_back(f);
+    if (!bvh.leaf.empty()) bvh.build(0, (int)bvh.leaf.size(), 1);
+    if (bvh.max_depth > 30) { delete M; return fail(GOI_E_UNSUPPORTED, "goi_model_create: BVH too deep"); }
+    d.n_nodes = (int)bvh.box.size();
+    d.n_dd = (int)dd.size();
+    int any = desc->toi_bodies ? 0 : 1;
+    if (desc->toi_bodies)
+        for (int b = 0; b < B; ++b) any |= desc->toi_bodies[b] ? 1 : 0;
+    d.any_toi_body = any;
+    int rc = GOI_OK;
+#define UP(field, host, n) \
+    if (rc == GOI_OK) rc = upload(M, host, (size_t)(n), d.field, st)
+    UP(fixture_body, desc->fixture_body, F);
+    UP(shape_type, desc->shape_type, F);
+    UP(radius, desc->radius, F);
+    UP(count, desc->count, F);
+    UP(verts, reinterpret_cast<const V2*>(desc->verts), (size_t)F * kPoly);
+    UP(normals, reinterpret_cast<const V2*>(desc->normals), (size_t)F * kPoly);
+    UP(joint_type, desc->joint_type, J);
+    UP(joint_a, desc->joint_a, J);
+    UP(joint_b, desc->joint_b, J);
+    UP(local_anchor_a, reinterpret_cast<const V2*>(desc->local_anchor_a), J);
+    UP(local_anchor_b, reinterpret_cast<const V2*>(desc->local_anchor_b), J);
+    UP(local_axis_a, reinterpret_cast<const V2*>(desc->local_axis_a), J);
+    UP(local_yaxis_a, reinterpret_cast<const V2*>(desc->local_yaxis_a), J);
+    UP(reference_angle, desc->reference_angle, J);
+    UP(pair_a, desc->pair_a, P);
+    UP(pair_b, desc->pair_b, P);
+    UP(fixture_slot, desc->fixture_slot, F);
+    UP(slot_fixture, slot_fixture.data(), R);
+    UP(static_fat, reinterpret_cast<const float4*>(desc->static_fat), F);
+    UP(static_friction, desc->static_friction, F);
+    UP(static_restitution, desc->static_restitution, F);
+    UP(body_type, desc->body_type, B);
+    UP(node_box, bvh.box.data(), bvh.box.size());
+    UP(node_child, bvh.child.data(), bvh.child.size());
+    UP(leaf_fixture, bvh.leaf.data(), bvh.leaf.size());
+    UP(cand_static, cand.data(), (size_t)F * R);
+    UP(dd_cand, dd.data(), dd.size());
+#undef UP
+    if (rc == GOI_OK) {
+        hipError_t e = hipStreamSynchronize(st);
+        if (e != hipSuccess) rc = fail(GOI_E_HIP, std::string("goi_model_create: ") + hipGetErrorString(e));
+    }
+    if (rc != GOI_OK) {
+        goi_model_destroy(M);
+        return rc;
+    }
+    *out = M;
+    return GOI_OK;
+}
+
+int32_t goi_model_destroy(GoiModel* M) {
+    if (!M) return GOI_OK;
+    for (void* p : M->allocs) (void)hipFree(p);
+    if (M->scratch) (void)hipFree(M->scratch);
+    delete M;
+    return GOI_OK;
+}
+
+static int check_view(const GoiModel* M, const GoiStateView* v, const char* who) {
+    if (!M || !v) return fail(GOI_E_ARG, std::string(who) + ": null argument");
+    if (v->n_worlds < 0 || v->pitch < v->n_worlds) return fail(GOI_E_ARG, std::string(who) + ": bad n_worlds/pitch");
+    if (v->B != M->d.B || v->R != M->d.R || v->J != M->d.J || v->C != M->C)
+        return fail(GOI_E_SHAPE, std::string(who) + ": state capacities differ from the model's (B, R, J, C)");
+    for (int i = 0; i < GOI_NUM_LEAVES; ++i)
+        if (!v->leaf[i] && v->n_worlds > 0) return fail(GOI_E_ARG, std::string(who) + ": null leaf pointer");
+    return GOI_OK;
+}
+
+static void fill_launch(Launch& L, const GoiStateView* v, const GoiSettings* s, float dt) {
+    std::memcpy(L.leaf, v->leaf, sizeof(L.leaf));
+    L.n = v->n_worlds;
+    L.pitch = v->pitch;
+    L.B = v->B;
+    L.C = v->C;
+    L.R = v->R;
+    L.J = v->J;
+    L.s = *s;
+    L.dt = dt;
+    std::memset(&L.dbg, 0, sizeof(L.dbg));
+    L.scratch = nullptr;
+}
+
+int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
+                 void* hip_stream, const GoiDebug* debug) {
+    int rc = check_view(model, state, "goi_step");
+    if (rc != GOI_OK) return rc;
+    if (!settings) return fail(GOI_E_ARG, "goi_step: null settings");
+    if (settings->velocity_iterations < 0 || settings->position_iterations < 0)
+        return fail(GOI_E_ARG, "goi_step: negative iteration counts");
+    if (state->n_worlds == 0) return GOI_OK;
+    GoiModel* M = const_cast<GoiModel*>(model);
+    const size_t words = ((size_t)state->C * CF_N + (size_t)state->J * JF_N) * state->pitch;
+    if (words > M->scratch_words) {
+        if (M->scratch) HIP_TRY(hipFree(M->scratch));
+        M->scratch = nullptr;
+        M->scratch_words = 0;
+        HIP_TRY(hipMalloc(&M->scratch, std::max<size_t>(words, 1) * sizeof(uint32_t)));
+        M->scratch_words = words;
+    }
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    Launch L;
+    fill_launch(L, state, settings, dt);
+    L.scratch = M->scratch;
+    if (debug) L.dbg = *debug;
+    const int grid = (state->n_worlds + kBlock - 1) / kBlock;
+    const size_t lds = (size_t)kBodyFields * state->B * kBlock * sizeof(float);
+    hipLaunchKernelGGL(k_collide, dim3(grid), dim3(kBlock), 0, st, M->d, L, 0);
+    HIP_TRY(hipGetLastError());
+    hipLaunchKernelGGL(k_solve, dim3(grid), dim3(kBlock), lds, st, M->d, L);
+    HIP_TRY(hipGetLastError());
+    hipLaunchKernelGGL(k_toi, dim3(grid), dim3(kBlock), lds, st, M->d, L);
+    HIP_TRY(hipGetLastError());
+    return GOI_OK;
+}
+
+int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, void* hip_stream) {
+    int rc = check_view(model, state, "goi_collide");
+    if (rc != GOI_OK) return rc;
+    if (!settings) return fail(GOI_E_ARG, "goi_collide: null settings");
+    if (state->n_worlds == 0) return GOI_OK;
+    Launch L;
+    fill_launch(L, state, settings, 0.0f);
+    const int grid = (state->n_worlds + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL(k_collide, dim3(grid), dim3(kBlock), 0, static_cast<hipStream_t>(hip_stream), model->d, L, 0);
+    HIP_TRY(hipGetLastError());
+    return GOI_OK;
+}
+
+int32_t goi_sincos(const float* x, float* s, float* c, int32_t n, void* hip_stream) {
+    if (n < 0 || (n > 0 && (!x || !s || !c))) return fail(GOI_E_ARG, "goi_sincos: bad arguments");
+    if (n == 0) return GOI_OK;
+    hipLaunchKernelGGL(k_sincos, dim3((n + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(hip_stream), x, s, c, n);
+    HIP_TRY(hipGetLastError());
+    return GOI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,244 @@
+/* goi_b2.h - C ABI of the MI355X batched Box2D 2.3.1 world step (libgoi_b2.so).
+ *
+ * The library steps N independent worlds that share one Model, on the GPU, in place, on caller-owned device
+ * buffers. It replaces the reference's operator boundary for this path:
+ *   - goi_jax/box2d/step.py:28          step(model, state, settings, dt, axis_name=None)
+ *   - goi_jax/box2d/step.py:36-40       Settings.solver dispatch to the batched kernels
+ *   - goi_jax/box2d/gpu/kernel.py:573-598, gpu/pairs.py:242-263, gpu/toi_loop.py:66-130
+ *                                      the custom_vmap rules that receive the whole batch and run one kernel
+ *   - goi_jax/reference/capi.cpp:184-189 goi_b2_world_step (int return codes, ids in creation order)
+ *
+ * Data layout. A State is the reference pytree (goi_jax/box2d/world.py:70-174) flattened in field order into
+ * GOI_NUM_LEAVES leaves (enum GoiLeaf below). Each leaf of per-world inner shape S (e.g. contacts.point_local has
+ * S = [C, 2, 2]) is one device array stored worlds-minor: element (inner index i, world w) lives at
+ * leaf[i * pitch + w]. Bools are uint8 (0/1), ints int32, floats IEEE binary32.
+ *
+ * Return codes (capi.cpp style): 0 ok, GOI_E_ARG bad argument, GOI_E_SHAPE capacity/shape mismatch, GOI_E_HIP a HIP
+ * runtime error, GOI_E_UNSUPPORTED settings or model the kernels do not cover. goi_last_error() returns a
+ * thread-local message for the last failure. Contact-table overflow is not an error: it is counted in the overflow
+ * leaf (world.py:173), as the reference does.
+ *
+ * Threading: calls are stream-ordered and asynchronous on the given hipStream_t (NULL = default stream). A model
+ * handle is read-only after creation and may be shared by calls on different streams; a state must not be stepped
+ * by two calls at once.
+ */
+#ifndef GOI_B2_H
+#define GOI_B2_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GOI_ABI_VERSION 1
+
+#define GOI_OK 0
+#define GOI_E_ARG (-1)
+#define GOI_E_SHAPE (-2)
+#define GOI_E_HIP (-3)
+#define GOI_E_UNSUPPORTED (-4)
+
+/* Box2D enums as the reference numbers them (world.py:24-27, shapes.py:13, collide.py:18). */
+#define GOI_STATIC 0
+#define GOI_KINEMATIC 1
+#define GOI_DYNAMIC 2
+#define GOI_REVOLUTE 1
+#define GOI_PRISMATIC 2
+#define GOI_WELD 8
+#define GOI_CIRCLE 0
+#define GOI_POLYGON 2
+#define GOI_MAX_POLY 8
+
+/* The State leaves in pytree order (world.py:70-174). Per-world inner shapes in brackets: B bodies, R fixture rows
+ * (F in the full layout, the non-static fixtures in the compact layout, world.py:400-434), J joints, C slots. */
+enum GoiLeaf {
+    /* Bodies (world.py:70-95) */
+    GOI_B_TYPE = 0,       /* i32[B]   */
+    GOI_B_ACTIVE,         /* u8[B]    */
+    GOI_B_AWAKE,          /* u8[B]    */
+    GOI_B_ALLOW_SLEEP,    /* u8[B]    */
+    GOI_B_BULLET,         /* u8[B]    */
+    GOI_B_CONTINUOUS,     /* u8[B]    */
+    GOI_B_SLEEP_TIME,     /* f32[B]   */
+    GOI_B_XF_P,           /* f32[B,2] */
+    GOI_B_XF_Q,           /* f32[B,2] (cos, sin) */
+    GOI_B_LOCAL_CENTER,   /* f32[B,2] */
+    GOI_B_C0,             /* f32[B,2] */
+    GOI_B_C,              /* f32[B,2] */
+    GOI_B_A0,             /* f32[B]   */
+    GOI_B_A,              /* f32[B]   */
+    GOI_B_V,              /* f32[B,2] */
+    GOI_B_W,              /* f32[B]   */
+    GOI_B_FORCE,          /* f32[B,2] */
+    GOI_B_TORQUE,         /* f32[B]   */
+    GOI_B_MASS,           /* f32[B]   */
+    GOI_B_INV_MASS,       /* f32[B]   */
+    GOI_B_INERTIA,        /* f32[B]   */
+    GOI_B_INV_INERTIA,    /* f32[B]   */
+    GOI_B_LINEAR_DAMPING, /* f32[B]   */
+    GOI_B_ANGULAR_DAMPING,/* f32[B]   */
+    GOI_B_GRAVITY_SCALE,  /* f32[B]   */
+    /* Fixtures (world.py:98-101) */
+    GOI_F_FRICTION,       /* f32[R]   */
+    GOI_F_RESTITUTION,    /* f32[R]   */
+    GOI_F_FAT,            /* f32[R,4] lower x, lower y, upper x, upper y */
+    /* Joints (world.py:104-118) */
+    GOI_J_ENABLE_MOTOR,   /* u8[J]    */
+    GOI_J_MOTOR_SPEED,    /* f32[J]   (the action-driven motor target) */
+    GOI_J_MAX_MOTOR,      /* f32[J]   */
+    GOI_J_ENABLE_LIMIT,   /* u8[J]    */
+    GOI_J_LOWER,          /* f32[J]   */
+    GOI_J_UPPER,          /* f32[J]   */
+    GOI_J_FREQUENCY,      /* f32[J]   */
+    GOI_J_DAMPING,        /* f32[J]   */
+    GOI_J_IMPULSE,        /* f32[J,3] */
+    GOI_J_MOTOR_IMPULSE,  /* f32[J]   */
+    GOI_J_LIMIT_STATE,    /* i32[J]   */
+    GOI_J_LOWER_IMPULSE,  /* f32[J]   */
+    GOI_J_UPPER_IMPULSE,  /* f32[J]   */
+    /* Contacts (world.py:121-139) */
+    GOI_C_PAIR,           /* i32[C]   candidate index, -1 empty slot */
+    GOI_C_FA,             /* i32[C]   */
+    GOI_C_FB,             /* i32[C]   */
+    GOI_C_KEY,            /* i32[C]   */
+    GOI_C_TOUCHING,       /* u8[C]    */
+    GOI_C_MTYPE,          /* i32[C]   */
+    GOI_C_COUNT,          /* i32[C]   */
+    GOI_C_LOCAL_NORMAL,   /* f32[C,2] */
+    GOI_C_LOCAL_POINT,    /* f32[C,2] */
+    GOI_C_POINT_LOCAL,    /* f32[C,2,2] */
+    GOI_C_POINT_ID,       /* i32[C,2] */
+    GOI_C_NORMAL_IMPULSE, /* f32[C,2] */
+    GOI_C_TANGENT_IMPULSE,/* f32[C,2] */
+    GOI_C_FRICTION,       /* f32[C]   */
+    GOI_C_RESTITUTION,    /* f32[C]   */
+    GOI_C_TANGENT_SPEED,  /* f32[C]   */
+    /* World scalars (world.py:169-173) */
+    GOI_S_GRAVITY,        /* f32[2]   */
+    GOI_S_INV_DT0,        /* f32[]    */
+    GOI_S_NEXT_KEY,       /* i32[]    */
+    GOI_S_NEW_FIXTURE,    /* u8[]     */
+    GOI_S_OVERFLOW,       /* i32[]    */
+    /* ContactTOI (world.py:142-154) */
+    GOI_T_ALPHA0,         /* f32[B]   */
+    GOI_T_COUNT,          /* i32[C]   */
+    GOI_T_TOI,            /* f32[C]   */
+    GOI_T_FLAG,           /* u8[C]    */
+    GOI_T_ENABLED,        /* u8[C]    */
+    GOI_T_SOLVED,         /* u8[C]    */
+    GOI_T_NORMAL_IMPULSE, /* f32[C,2] */
+    GOI_T_TANGENT_IMPULSE,/* f32[C,2] */
+    GOI_T_EVENTS,         /* i32[]    */
+    GOI_NUM_LEAVES
+};
+
+/* Settings (settings.py:42-107) as a POD. The step reads gravity from the State (world.py:169), as the reference
+ * does. max_events < 0 selects the reference default C * (b2_maxSubSteps + 1) + 8 (toi.py:838-840). */
+typedef struct GoiSettings {
+    int32_t velocity_iterations;
+    int32_t position_iterations;
+    float linear_slop;
+    float angular_slop;
+    float polygon_radius;
+    float velocity_threshold;
+    float max_linear_correction;
+    float max_angular_correction;
+    float max_translation;
+    float max_rotation;
+    float baumgarte;
+    float toi_baumgarte;
+    float time_to_sleep;
+    float linear_sleep_tolerance;
+    float angular_sleep_tolerance;
+    int32_t clamps_per_second;
+    int32_t allow_sleep;
+    int32_t warm_starting;
+    int32_t continuous_physics;
+    int32_t unity_toi;
+    int32_t toi_tie_oldest;
+    int32_t auto_clear_forces;
+    int32_t revolute_v24;
+    int32_t max_events;
+} GoiSettings;
+
+/* The shared Model (world.py:30-67), host pointers. fixture_slot == NULL is the full fixture layout; otherwise the
+ * compact layout (world.py:437-472): fixture_slot[f] is the State row of fixture f or -1 for a static body's
+ * fixture, whose fat AABB, friction and restitution are static_fat/static_friction/static_restitution[f].
+ * body_type[B] are the body types every world shares (the compact layout requires it, world.py:447-450).
+ * toi_bodies[B] (nullable) is Model.toi_bodies (world.py:48-50). */
+typedef struct GoiModelDesc {
+    int32_t F, J, P, B;
+    const int32_t* fixture_body;   /* [F] */
+    const int32_t* shape_type;     /* [F] */
+    const float* radius;           /* [F] */
+    const int32_t* count;          /* [F] */
+    const float* verts;            /* [F,8,2] */
+    const float* normals;          /* [F,8,2] */
+    const int32_t* joint_type;     /* [J] */
+    const int32_t* joint_a;        /* [J] */
+    const int32_t* joint_b;        /* [J] */
+    const float* local_anchor_a;   /* [J,2] */
+    const float* local_anchor_b;   /* [J,2] */
+    const float* local_axis_a;     /* [J,2] */
+    const float* local_yaxis_a;    /* [J,2] */
+    const float* reference_angle;  /* [J] */
+    const int32_t* pair_a;         /* [P] */
+    const int32_t* pair_b;         /* [P] */
+    const int32_t* fixture_slot;   /* [F] or NULL */
+    const float* static_fat;       /* [F,4] or NULL */
+    const float* static_friction;  /* [F] or NULL */
+    const float* static_restitution; /* [F] or NULL */
+    const int32_t* body_type;      /* [B] */
+    const uint8_t* toi_bodies;     /* [B] or NULL */
+} GoiModelDesc;
+
+/* A batch of States on the device: GOI_NUM_LEAVES device pointers, worlds-minor with the given pitch (>= n). */
+typedef struct GoiStateView {
+    int32_t n_worlds;
+    int32_t pitch;
+    int32_t B, C, R, J;
+    void* leaf[GOI_NUM_LEAVES];
+} GoiStateView;
+
+/* Optional per-world integer outputs that are not State leaves (island ids, solve order, TOI event counts),
+ * written worlds-minor with the view's pitch when non-NULL. */
+typedef struct GoiDebug {
+    int32_t* body_island;      /* [B] island of each body after Solve's search, -1 none (island.py:33) */
+    int32_t* contact_island;   /* [C] (island.py:34) */
+    int32_t* contact_order;    /* [C] slots in solve order, -1 padded (island.py:29) */
+    int32_t* n_islands;        /* [] */
+} GoiDebug;
+
+typedef struct GoiModel GoiModel;
+
+/* ABI version of the loaded library (GOI_ABI_VERSION). */
+int32_t goi_abi_version(void);
+
+/* Upload the shared Model to the current device and build the static-terrain acceleration structures: the
+ * bounding-volume hierarchy over static fixtures' fat AABBs and the candidate-index table. The library owns *out.
+ * Replaces the host build of world.py:331-386 + compact_model (world.py:437-472) for the device. */
+int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, void* hip_stream, GoiModel** out);
+int32_t goi_model_destroy(GoiModel* model);
+
+/* One b2World::Step (step.py:28-47) of every world in place. dt in seconds. debug may be NULL. */
+int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
+                 void* hip_stream, const GoiDebug* debug);
+
+/* Broadphase and narrowphase only: start-of-step FindNewContacts where new_fixture
+ * (step.py:50-70), then Collide (pairs.py:38-87). */
+int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings,
+                    void* hip_stream);
+
+/* Correctly rounded float32 sin/cos of n values on the device, as the step computes them (math2d.py:291-310):
+ * s[i] = (float)sin((double)x[i]), c[i] = (float)cos((double)x[i]). Device pointers. */
+int32_t goi_sincos(const float* x, float* s, float* c, int32_t n, void* hip_stream);
+
+/* Thread-local message of the last failed call ("" if none). */
+const char* goi_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GOI_B2_H */
