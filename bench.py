@@ -1,0 +1,159 @@
+"""World-steps/s of the batched Box2D 2.3.1 step on one MI355X, and its fraction of the HBM roofline.
+
+    python bench.py [--gpus 1] [--steps 100] [--warmup 5] [--config 4]
+
+Workload (default, the headline): 16,384 worlds of the 4-body character rig over a seed-2 terrain (1,024 edge quads
++ 256 rocks), linear velocities N(0, 25) m/s, hammer-head spin U[-60, 60] rad/s, dt 0.02 s, g -9.81, 8 / 3
+iterations, continuous physics on with Box2D's stock TOI pair rule, random unit-disk actions written into the motor
+joint before every step. Inputs are resident in HBM before timing. One step = one k_step launch plus the two
+elementwise action writes; `value` counts every world of the timed steps.
+
+Roofline: k_step is HBM-bound work in the roofline sense (no dense contraction). Its algorithmic bytes per world-step
+follow the reference State's field set in the compact layout, each leaf read once and each mutable leaf written once:
+R = 113 B + 24 F_d + 54 J + 93 C + 21 and W = 81 B + 16 F_d + 28 J + 120 C + 17 (B bodies, F_d non-static fixtures,
+J joints, C contact slots); achieved = N x (R + W) / mean k_step duration (HIP events on its stream).
+
+cpu_baseline: the CPU restatement of the same step (oracle/, C, sequential per world, OpenMP over worlds) on the host
+cores, on the same configuration.
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+
+
+def bytes_per_world_step(B, Fd, J, C):
+    r = 113 * B + 24 * Fd + 54 * J + 93 * C + 21
+    w = 81 * B + 16 * Fd + 28 * J + 120 * C + 17
+    return r + w
+
+
+def traffic_from_profiles(kernel, workload):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, calibrated against a copy
+    kernel), read from the committed summary profiles/<kernel>_<workload>_traffic.txt ('bytes_per_launch: X')."""
+    p = ROOT / "profiles" / f"{kernel}_{workload}_traffic.txt"
+    if not p.exists():
+        return None
+    m = re.search(r"^bytes_per_launch:\s*([0-9.eE+]+)", p.read_text(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(model, state, settings, cfg, steps):
+    from oracle import oracle as O
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS"):
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    x = O.copy(state)
+    n = int(np.asarray(x.bodies.type).shape[0])
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        O.step_(model, x, settings, cfg.dt, threads)
+    dt = time.perf_counter() - t0
+    return {"value": n * steps / dt, "unit": "world-steps/s", "cores": threads, "kind": "port",
+            "sample": f"{cfg.name}: {n} worlds x {steps} steps ({n * steps} world-steps, {dt:.1f} s) of the oracle "
+                      f"(oracle/b2_oracle.c, -O2, OpenMP over worlds)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=4)
+    ap.add_argument("--worlds", type=int, default=None)
+    ap.add_argument("--cpu-steps", type=int, default=None, help="oracle steps for cpu_baseline (0: skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (worlds shard trivially "
+              "across GPUs with no per-step exchange, but only the 1-GPU figure is measured)", file=sys.stderr)
+        sys.exit(2)
+
+    import importlib
+
+    import torch
+
+    b2 = importlib.import_module("getting-over-it-rl_amd.box2d")
+    scenes = b2.scenes
+    settings, model, state, cfg = scenes.make_config(args.config, args.worlds)
+    n = int(np.asarray(state.bodies.type).shape[0])
+    B, R, J, C = b2.world.dims(state)
+    dev = b2.layout.to_device(state, "cuda")
+    rng = np.random.default_rng(12345)
+    acts = torch.from_numpy(np.stack([scenes.actions(rng, n) for _ in range(args.warmup + args.steps)])).to("cuda")
+    speed, torque = dev.joints.motor_speed, dev.joints.max_motor
+
+    def one(i):
+        scenes.apply_actions(speed, torque, acts[i])
+        b2.step_(model, dev, settings, cfg.dt)
+
+    for i in range(args.warmup):
+        one(i)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for k in range(args.steps):
+        scenes.apply_actions(speed, torque, acts[args.warmup + k])
+        evs[k][0].record()
+        b2.step_(model, dev, settings, cfg.dt)
+        evs[k][1].record()
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    kern_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    ms_per_step = total_ms / args.steps
+    value = n * args.steps / (total_ms / 1e3)
+    bpw = bytes_per_world_step(B, R, J, C)
+    achieved = n * bpw / (kern_ms / 1e3) / 1e9
+    host = b2.layout.to_host(dev)
+    finite = bool(np.isfinite(np.asarray(host.bodies.c)).all())
+    workload = f"config{args.config}"
+    traffic = traffic_from_profiles("k_step", workload)
+
+    cpu = None
+    cpu_steps = args.cpu_steps if args.cpu_steps is not None else (cfg.steps if n <= 16384 else 10)
+    if cpu_steps > 0:
+        s2, m2, st2, _ = scenes.make_config(args.config, args.worlds)
+        cpu = cpu_baseline(m2, st2, s2, cfg, cpu_steps)
+
+    out = {
+        "metric": "world-steps/sec at 16384 worlds (full step incl. TOI); % of HBM roofline",
+        "value": value,
+        "unit": "world-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded terrain + rig generators, random unit-disk actions)",
+        "config": {"workload": f"{cfg.name}: {n} worlds, 4-body rig, terrain {cfg.n_edges} edges + {cfg.n_rocks} "
+                               f"rocks (seed {cfg.seed}), v~N(0,{cfg.v_sigma}), head w~U[-{cfg.head_w},{cfg.head_w}], "
+                               f"dt {cfg.dt}, 8/3 iterations, TOI on (stock rule)",
+                   "worlds": n, "bodies": B, "dynamic_fixtures": R, "joints": J, "contact_slots": C},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": "k_step",
+                     "kernel_ms": kern_ms, "bytes_per_world_step": bpw},
+        "cpu_baseline": cpu,
+        "toi_events_last_step": int(np.asarray(host.toi.events).sum()),
+        "overflow": int(np.asarray(host.overflow).sum()),
+        "finite": finite,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -49,12 +49,12 @@ GOI_D Xf mulT(const Xf& A, const Xf& B) {
     C.p = mulT(A.q, B.p - A.p);
     return C;
 }
-GOI_D float length(V2 a) { return __fsqrt_rn(a.x * a.x + a.y * a.y); }
+GOI_D float length(V2 a) { return sqrtf(a.x * a.x + a.y * a.y); }
 // b2Vec2::Normalize: unchanged below b2_epsilon
 GOI_D float normalize(V2& a) {
     float n = length(a);
     if (n < kEps) return 0.0f;
-    float inv = __fdiv_rn(1.0f, n);
+    float inv = 1.0f / n;
     a.x *= inv;
     a.y *= inv;
     return n;
@@ -63,8 +63,8 @@ GOI_D float bmin(float a, float b) { return a < b ? a : b; }   // b2Min keeps b 
 GOI_D float bmax(float a, float b) { return a > b ? a : b; }
 GOI_D float bclamp(float a, float lo, float hi) { return bmax(lo, bmin(a, hi)); }
 GOI_D float babs(float a) { return a > 0.0f ? a : -a; }
-GOI_D float fdiv(float a, float b) { return __fdiv_rn(a, b); }
-GOI_D float fsqrt(float a) { return __fsqrt_rn(a); }
+GOI_D float fdiv(float a, float b) { return a / b; }
+GOI_D float fsqrt(float a) { return sqrtf(a); }  // IEEE sqrt under -fhip-fp32-correctly-rounded-divide-sqrt
 
 // Correctly rounded float32 sin/cos: (float)sin((double)x), the value the reference computes with a float-float
 // series (math2d.py:291-310) and its oracle with the C library (scripts/patches/box2d-2.3.1-trig.patch:17-23).

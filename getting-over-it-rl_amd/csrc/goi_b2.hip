@@ -1,10 +1,10 @@
 // goi_b2.hip - the MI355X batched Box2D 2.3.1 world step (libgoi_b2.so) and its C ABI (include/goi_b2.h).
 //
-// Execution model: one lane per world. A step is three launches over ceil(N / 64) wavefronts of 64 lanes:
-//   k_collide  start-of-step FindNewContacts where new_fixture, then Collide     (step.py:30-35, pairs.py:38-178)
-//   k_solve    b2World::Solve: islands, solver, sleep, fixture sync, FindNewContacts (step.py:73-182)
-//   k_toi      b2World::SolveTOI event loop, then inv_dt0 and ClearForces         (toi.py:827-865, step.py:41-46)
-// Box2D's sequential orders inside a world (contact list newest first, island DFS, Gauss-Seidel sweeps, TOI events)
+// Execution model: one lane per world; a step is one launch (k_step) over ceil(N / 64) wavefronts of 64 lanes:
+//   start-of-step FindNewContacts where new_fixture, then Collide           (step.py:30-35, pairs.py:38-178)
+//   b2World::Solve: islands, solver, sleep, fixture sync, FindNewContacts   (step.py:73-182)
+//   b2World::SolveTOI's event loop, then inv_dt0 and ClearForces             (toi.py:827-865, step.py:41-46)
+// goi_collide launches k_collide (the first part only). Box2D's sequential orders inside a world (contact list newest first, island DFS, Gauss-Seidel sweeps, TOI events)
 // are kept exactly; the parallelism is across worlds. State leaves are read and written in place in the
 // worlds-minor layout; the solver's body arrays sit in LDS ([field][body][lane]), its constraint rows in a
 // per-world HBM scratch ([row][field][pitch]); the static terrain is a BVH over the static fixtures' fat AABBs,
@@ -89,26 +89,22 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
     if (!start_only) collide_walk(m, W, L.s.linear_slop);
 }
 
-__global__ void __launch_bounds__(kBlock) k_solve(DModel m, Launch L) {
+// The whole b2World::Step (step.py:28-47) of one world per lane: FindNewContacts where new_fixture, Collide,
+// Solve, SolveTOI, inv_dt0, ClearForces.
+__global__ void __launch_bounds__(kBlock) k_step(DModel m, Launch L) {
     extern __shared__ float lds[];
     const int w = blockIdx.x * kBlock + threadIdx.x;
     if (w >= L.n) return;
     const World W = make_world(L, w);
+    if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
+    W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
+    collide_walk(m, W, L.s.linear_slop);
     Bodies bd;
     bd.s = lds + threadIdx.x;
     bd.B = L.B;
-    solve_world(m, W, bd, contact_rows(L, w), joint_rows(L, w), L.s, L.dt, L.dbg);
-}
-
-__global__ void __launch_bounds__(kBlock) k_toi(DModel m, Launch L) {
-    extern __shared__ float lds[];
-    const int w = blockIdx.x * kBlock + threadIdx.x;
-    if (w >= L.n) return;
-    const World W = make_world(L, w);
-    Bodies bd;
-    bd.s = lds + threadIdx.x;
-    bd.B = L.B;
-    if (L.s.continuous_physics) solve_toi_world(m, W, bd, contact_rows(L, w), L.s, L.dt);
+    const Rows CR = contact_rows(L, w);
+    solve_world(m, W, bd, CR, joint_rows(L, w), L.s, L.dt, L.dbg);
+    if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt);
     const float dt = L.dt;
     if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
     if (L.s.auto_clear_forces)
@@ -330,8 +326,16 @@ static int check_view(const GoiModel* M, const GoiStateView* v, const char* who)
     if (v->n_worlds < 0 || v->pitch < v->n_worlds) return fail(GOI_E_ARG, std::string(who) + ": bad n_worlds/pitch");
     if (v->B != M->d.B || v->R != M->d.R || v->J != M->d.J || v->C != M->C)
         return fail(GOI_E_SHAPE, std::string(who) + ": state capacities differ from the model's (B, R, J, C)");
-    for (int i = 0; i < GOI_NUM_LEAVES; ++i)
-        if (!v->leaf[i] && v->n_worlds > 0) return fail(GOI_E_ARG, std::string(who) + ": null leaf pointer");
+    for (int i = 0; i < GOI_NUM_LEAVES; ++i) {
+        // leaves over an empty axis (no joints, no non-static fixtures, no slots) may be null
+        const bool by_j = i >= GOI_J_ENABLE_MOTOR && i <= GOI_J_UPPER_IMPULSE;
+        const bool by_r = i >= GOI_F_FRICTION && i <= GOI_F_FAT;
+        const bool by_c = (i >= GOI_C_PAIR && i <= GOI_C_TANGENT_SPEED) ||
+                          (i >= GOI_T_COUNT && i <= GOI_T_TANGENT_IMPULSE);
+        const bool empty = (by_j && v->J == 0) || (by_r && v->R == 0) || (by_c && v->C == 0);
+        if (!v->leaf[i] && v->n_worlds > 0 && !empty)
+            return fail(GOI_E_ARG, std::string(who) + ": null leaf pointer");
+    }
     return GOI_OK;
 }
 
@@ -373,11 +377,7 @@ int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSett
     if (debug) L.dbg = *debug;
     const int grid = (state->n_worlds + kBlock - 1) / kBlock;
     const size_t lds = (size_t)kBodyFields * state->B * kBlock * sizeof(float);
-    hipLaunchKernelGGL(k_collide, dim3(grid), dim3(kBlock), 0, st, M->d, L, 0);
-    HIP_TRY(hipGetLastError());
-    hipLaunchKernelGGL(k_solve, dim3(grid), dim3(kBlock), lds, st, M->d, L);
-    HIP_TRY(hipGetLastError());
-    hipLaunchKernelGGL(k_toi, dim3(grid), dim3(kBlock), lds, st, M->d, L);
+    hipLaunchKernelGGL(k_step, dim3(grid), dim3(kBlock), lds, st, M->d, L);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
 }

@@ -1,0 +1,122 @@
+"""HIP step vs the CPU oracle, bit for bit, through the C ABI on the GPU.
+
+Integer/index leaves (contact slots, candidate indices, keys, manifold point counts and feature ids, TOI counts and
+flags) and float leaves (positions, angles, velocities, impulses, manifold geometry) must be identical at every step:
+both sides perform the reference's float32 operations in the same order, so the tolerance of the north star
+(1e-4 abs / 1e-3 rel) is not needed; any difference is a bug. Island ids and solve order (not State leaves) are
+compared through the debug outputs.
+"""
+import numpy as np
+import pytest
+
+from util import b2, leaf_mismatches, perturbed, wd
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def _run(model, state, settings, dt, steps, oracle, actions=None):
+    dev = b2.layout.to_device(state, "cuda")
+    ref = oracle.copy(state)
+    for k in range(steps):
+        if actions is not None:
+            a = actions[k]
+            b2.scenes.apply_actions(ref.joints.motor_speed, ref.joints.max_motor, a)
+            b2.scenes.apply_actions(dev.joints.motor_speed, dev.joints.max_motor, torch.from_numpy(a).cuda())
+        b2.step_(model, dev, settings, dt)
+        oracle.step_(model, ref, settings, dt)
+        got = b2.layout.to_host(dev)
+        bad = leaf_mismatches(ref, got)
+        assert bad == [], f"step {k + 1}: {bad[:4]}"
+    return ref
+
+
+@pytest.mark.parametrize("name", list(b2.scenes.TEST_SCENES))
+def test_scene_parity(name, oracle):
+    """Every test scene, 64 perturbed copies, 90 steps, stock iteration counts."""
+    s, m, st = b2.scenes.build_test_scene(name, iterations=(8, 3))
+    _run(m, perturbed(st, 64), s, 1.0 / 60.0, 90, oracle)
+
+
+@pytest.mark.parametrize("name", ["pile", "hammer_chain", "island_walk", "joints"])
+def test_scene_parity_game_iterations(name, oracle):
+    """The game's 300 / 30 iterations on the heavier scenes."""
+    s, m, st = b2.scenes.build_test_scene(name)
+    _run(m, perturbed(st, 16, seed=3), s, b2.GAME_DT, 60, oracle)
+
+
+@pytest.mark.parametrize("k,n,steps", [(1, 1, 200), (3, 512, 30), (4, 512, 30)])
+def test_config_parity(k, n, steps, oracle):
+    s, m, st, cfg = b2.scenes.make_config(k, n)
+    rng = np.random.default_rng(5)
+    acts = [b2.scenes.actions(rng, n) for _ in range(steps)]
+    ref = _run(m, st, s, cfg.dt, steps, oracle, acts)
+    assert np.isfinite(np.asarray(ref.bodies.c)).all()
+
+
+def test_collide_config2(oracle):
+    """Broadphase + narrowphase only over 4096 worlds: candidate pairs, slots, keys, point
+    counts and manifolds bit for bit."""
+    s, m, st, cfg = b2.scenes.make_config(2)
+    dev = b2.layout.to_device(st, "cuda")
+    ref = oracle.copy(st)
+    b2.collide_(m, dev, s)
+    oracle.collide_(m, ref, s)
+    got = b2.layout.to_host(dev)
+    assert leaf_mismatches(ref, got) == []
+    live = np.asarray(got.contacts.pair) >= 0
+    assert live.sum() > 1000 and (np.asarray(got.contacts.count)[live] > 0).any()
+
+
+def test_island_debug_outputs(oracle):
+    """Island ids and solve order of the device Solve equal the oracle's."""
+    s, m, st = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+    st = perturbed(st, 64, seed=9)
+    dev = b2.layout.to_device(st, "cuda")
+    ref = oracle.copy(st)
+    B, R, J, C = wd.dims(st)
+    for _ in range(40):
+        dbg, t = b2.make_debug(64, (B, R, J, C))
+        b2.step_(m, dev, s, 1.0 / 60.0, debug=dbg)
+        d = {k: np.zeros(v.shape, np.int32) for k, v in t.items()}
+        oracle.step_(m, ref, s, 1.0 / 60.0, debug=d)
+        torch.cuda.synchronize()
+        for k in d:
+            assert np.array_equal(d[k], t[k].cpu().numpy()), k
+
+
+def test_sincos_correctly_rounded(oracle):
+    """The kernels' sin/cos equal (float)sin((double)x) on the reference's sample design (20k U[-8, 8], 5k
+    U[-300, 300], +-0, pi; tests/box2d/test_box2d_parity.py:44-50) plus 4M uniform samples in [-100, 100]."""
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.uniform(-8, 8, 20000), rng.uniform(-300, 300, 5000), [0.0, -0.0, np.pi],
+                        rng.uniform(-100, 100, 4_000_000)]).astype(np.float32)
+    s, c = b2.sincos(torch.from_numpy(x).cuda())
+    rs, rc = oracle.sincos(x)
+    gs, gc = s.cpu().numpy(), c.cpu().numpy()
+    assert np.signbit(gs[20001])
+    assert np.array_equal(gs[:25003], rs[:25003]) and np.array_equal(gc[:25003], rc[:25003])
+    bad = int((gs != rs).sum() + (gc != rc).sum())
+    assert bad <= 4, f"{bad} of {2 * x.size} values differ from (float)sin((double)x)"
+
+
+def test_full_size_config4_properties():
+    """16384 worlds (the headline workload), 20 steps: finite state, no contact-table overflow, TOI events happen,
+    every live slot's keys unique per world, feature ids only on touching slots."""
+    s, m, st, cfg = b2.scenes.make_config(4)
+    dev = b2.layout.to_device(st, "cuda")
+    rng = np.random.default_rng(11)
+    events = 0
+    for k in range(20):
+        b2.scenes.apply_actions(dev.joints.motor_speed, dev.joints.max_motor,
+                                torch.from_numpy(b2.scenes.actions(rng, st.bodies.type.shape[0])).cuda())
+        b2.step_(m, dev, s, cfg.dt)
+        events += int(dev.toi.events.sum())
+    h = b2.layout.to_host(dev)
+    assert np.isfinite(h.bodies.c).all() and np.isfinite(h.bodies.v).all()
+    assert int(h.overflow.sum()) == 0
+    assert events > 0
+    live = h.contacts.pair >= 0
+    keys = np.where(live, h.contacts.key, -1 - np.arange(live.shape[1])[None, :])
+    assert all(len(set(r)) == len(r) for r in keys[:512])
+    assert (h.contacts.count[~live] == 0).all()
