@@ -72,7 +72,20 @@ def main():
     ap.add_argument("--config", type=int, default=4)
     ap.add_argument("--worlds", type=int, default=None)
     ap.add_argument("--cpu-steps", type=int, default=None, help="oracle steps for cpu_baseline (0: skip)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="run only a plain device copy of MIB MiB 10 times (the rocprofv3 FETCH_SIZE/WRITE_SIZE "
+                         "calibration) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": 4 * n, "launches": 10}))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (worlds shard trivially "
               "across GPUs with no per-step exchange, but only the 1-GPU figure is measured)", file=sys.stderr)
