@@ -64,14 +64,25 @@ def state_view(state):
     v = GoiStateView()
     v.n_worlds = n
     pitch = None
+    device = None
     for t, (_, name, dt, inner) in zip(leaves, wd.LEAVES):
+        if not isinstance(t, torch.Tensor) or not t.is_cuda:
+            raise ValueError(f"leaf {name}: not a GPU tensor (move the State with layout.to_device)")
+        if device is not None and t.device != device:
+            raise ValueError(f"leaf {name}: on {t.device}, other leaves on {device}")
+        device = t.device
         if t.dtype != _dtype(dt):
             raise TypeError(f"leaf {name}: dtype {t.dtype}, expected {_dtype(dt)}")
-        if not t.is_cuda:
-            raise ValueError(f"leaf {name}: not on a GPU")
+        shape = (n,) + wd.leaf_shape(inner, (B, R, J, C))
+        if tuple(t.shape) != shape:
+            raise ValueError(f"leaf {name}: shape {tuple(t.shape)}, expected {shape}")
         if t.dim() > 1:
             p = t.stride(-1)
-            if t.stride(0) != 1 or (pitch is not None and p != pitch):
+            want, acc = [1], p
+            for d in reversed(shape[1:]):
+                want.insert(1, acc)
+                acc *= d
+            if tuple(t.stride()) != tuple(want) or p < n or (pitch is not None and p != pitch):
                 raise ValueError(f"leaf {name}: not in the worlds-minor layout (strides {t.stride()})")
             pitch = p
         elif t.stride(0) != 1:

@@ -67,13 +67,16 @@ def settings_for(cfg=None):
 
 # ---------------------------------------------------------------- terrain
 
-def _convex_polygon(rng, radius):
+def _convex_polygon(rng, radius, centre):
+    """A strictly convex CCW polygon at `centre`, convex after the float32 translation too (far from the origin the
+    rounding can merge close vertices; such draws are redrawn)."""
     while True:
         n = int(rng.integers(3, 9))
         ang = np.sort(rng.uniform(0.0, 2.0 * np.pi, n))
         v = np.stack([radius * np.cos(ang), radius * np.sin(ang)], 1).astype(F32)
         try:
-            return shapes.polygon_raw(v)
+            shapes.polygon_raw(v)
+            return shapes.polygon_raw((v + np.asarray(centre, F32)).astype(F32))
         except ValueError:
             continue
 
@@ -95,9 +98,7 @@ def terrain(seed, n_edges, n_rocks):
         radius = rng.uniform(0.3, 2.0)
         x = rng.uniform(pts[0, 0], pts[-1, 0])
         y = float(np.interp(x, pts[:, 0], pts[:, 1]))
-        v, _ = _convex_polygon(rng, radius)
-        v = (v + np.array([x, y], F32)).astype(F32)
-        rocks.append(shapes.polygon_raw(v))
+        rocks.append(_convex_polygon(rng, radius, (x, y)))
     return pts, rocks
 
 

@@ -61,10 +61,10 @@ def step_(model, state, settings, dt, debug=None, stream=None):
     """One step of every world of a device State, in place. Returns the same State."""
     if getattr(settings, "solver", "hip") != "hip":
         raise ValueError(f"Settings.solver={settings.solver!r}: this package steps on the GPU only ('hip')")
+    view = layout.state_view(state)
     C = state.contacts.pair.shape[-1]
     dev = state.contacts.pair.device
     dm = device_model(model, C, dev)
-    view = layout.state_view(state)
     cs = settings.to_c()
     st = torch.cuda.current_stream(dev).cuda_stream if stream is None else stream
     dbg = None if debug is None else ctypes.byref(debug)
@@ -82,10 +82,10 @@ def step(model, state, settings, dt, axis_name=None):
 
 def collide_(model, state, settings, stream=None):
     """Broadphase + narrowphase only, in place: start-of-step FindNewContacts where new_fixture, then Collide."""
+    view = layout.state_view(state)
     C = state.contacts.pair.shape[-1]
     dev = state.contacts.pair.device
     dm = device_model(model, C, dev)
-    view = layout.state_view(state)
     cs = settings.to_c()
     st = torch.cuda.current_stream(dev).cuda_stream if stream is None else stream
     _abi.check(dm.L.goi_collide(dm.handle, ctypes.byref(view), ctypes.byref(cs), ctypes.c_void_p(st)), dm.L)

@@ -33,21 +33,27 @@ def lib():
     if _L is None:
         if not LIB.exists():
             build()
-        L = ctypes.CDLL(str(LIB))
-        P = ctypes.c_void_p
-        L.oracle_step.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), P] + [ctypes.c_int32] * 5 + [
-            ctypes.POINTER(_abi.GoiSettings), ctypes.c_float, ctypes.c_int32, ctypes.POINTER(_abi.GoiDebug)]
-        L.oracle_collide.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), P] + [ctypes.c_int32] * 5 + [
-            ctypes.POINTER(_abi.GoiSettings), ctypes.c_int32]
-        L.oracle_evaluate.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), ctypes.c_int, ctypes.c_int, P, P,
-                                      ctypes.c_float, P, P, P]
-        L.oracle_distance.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), ctypes.c_int, ctypes.c_int, P, P]
-        L.oracle_distance.restype = ctypes.c_float
-        L.oracle_toi.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), ctypes.c_int, ctypes.c_int, P, P,
-                                 ctypes.c_float, P]
-        L.oracle_sincos.argtypes = [P, P, P, ctypes.c_int32]
-        _L = L
+        _L = load(LIB)
     return _L
+
+
+def load(path):
+    """A ctypes handle on an oracle library at `path` with the argument types set (the tests also load variants of
+    the restatement built with a planted mistake, to show that the pins catch it)."""
+    L = ctypes.CDLL(str(path))
+    P = ctypes.c_void_p
+    L.oracle_step.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), P] + [ctypes.c_int32] * 5 + [
+        ctypes.POINTER(_abi.GoiSettings), ctypes.c_float, ctypes.c_int32, ctypes.POINTER(_abi.GoiDebug)]
+    L.oracle_collide.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), P] + [ctypes.c_int32] * 5 + [
+        ctypes.POINTER(_abi.GoiSettings), ctypes.c_int32]
+    L.oracle_evaluate.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), ctypes.c_int, ctypes.c_int, P, P,
+                                  ctypes.c_float, P, P, P]
+    L.oracle_distance.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), ctypes.c_int, ctypes.c_int, P, P]
+    L.oracle_distance.restype = ctypes.c_float
+    L.oracle_toi.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), ctypes.c_int, ctypes.c_int, P, P,
+                             ctypes.c_float, P]
+    L.oracle_sincos.argtypes = [P, P, P, ctypes.c_int32]
+    return L
 
 
 def model_desc(model):

@@ -1,0 +1,270 @@
+"""Host logic without a GPU: engine constants, the State leaf table against the C header, the compact fixture layout,
+the scene generators, and the C-ABI library (loads, exports every declared symbol, rejects bad arguments before
+touching the device). No kernel is launched here."""
+import ctypes
+import dataclasses
+import os
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from util import b2, leaf_mismatches
+
+F32 = np.float32
+wd = b2.world
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "goi_b2.h"
+
+
+def abi():
+    import importlib
+    return importlib.import_module(b2.__name__ + "._abi")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# constants
+
+def test_stock_settings_are_b2settings_2_3_1():
+    """b2Settings.h v2.3.1 values, computed as C computes them in float32 (settings.py:17-80)."""
+    s = b2.Settings.stock()
+    pi = F32(3.14159265359)
+    assert s.linear_slop == F32(0.005) and s.polygon_radius == F32(0.01)
+    assert s.angular_slop == F32(F32(F32(2.0) / F32(180.0)) * pi)
+    assert s.max_angular_correction == F32(F32(F32(8.0) / F32(180.0)) * pi)
+    assert s.max_rotation == F32(F32(0.5) * pi)
+    assert (s.velocity_threshold, s.max_linear_correction, s.max_translation) == (F32(1), F32(0.2), F32(2))
+    assert (s.baumgarte, s.toi_baumgarte, s.time_to_sleep) == (F32(0.2), F32(0.75), F32(0.5))
+    assert s.linear_sleep_tolerance == F32(0.01) and s.angular_sleep_tolerance == s.angular_slop
+    assert (s.velocity_iterations, s.position_iterations) == (8, 3)
+    assert not s.unity_toi and not s.continuous_physics and s.revolute_v24 and s.warm_starting
+
+
+def test_game_settings():
+    """Getting Over It's Physics2D settings (settings.py:87-95): Unity's degree conversion in float32."""
+    g = b2.Settings.game()
+    assert g.gravity == (F32(0), F32(-30)) and (g.velocity_iterations, g.position_iterations) == (300, 30)
+    assert g.max_rotation == F32(F32(360) * F32(0.0174532924)) and g.baumgarte == F32(0.4)
+    assert g.unity_toi and g.toi_tie_oldest and g.continuous_physics and g.max_translation == F32(100)
+    assert b2.GAME_DT == F32(1 / 120)
+
+
+def test_settings_to_c_round_trip():
+    s = b2.Settings.game(gravity=(1, 2), velocity_iterations=7, max_events=5)
+    c = s.to_c()
+    for f in dataclasses.fields(s):
+        if f.name in ("gravity", "solver"):
+            continue
+        want = getattr(s, f.name)
+        got = getattr(c, f.name)
+        if f.name == "max_events":
+            assert got == 5
+        elif isinstance(want, (bool, np.bool_)):
+            assert got == int(want), f.name
+        else:
+            assert F32(got) == F32(want), f.name
+    assert b2.Settings.stock().to_c().max_events == -1
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the leaf table and the header
+
+def _header_leaves():
+    text = HEADER.read_text()
+    a = text.index("enum GoiLeaf {")
+    body = text[a:text.index("GOI_NUM_LEAVES", a)]
+    return re.findall(r"\b(GOI_[BFJCST]_[A-Z0-9_]+)\b", body)
+
+
+def test_leaf_table_matches_header():
+    """The Python leaf order (the reference pytree order, world.py:70-174) is the header's GoiLeaf enum."""
+    groups = {"bodies": "B", "fixtures": "F", "joints": "J", "contacts": "C", None: "S", "toi": "T"}
+    names = [f"GOI_{groups[g]}_{n.upper()}" for g, n, _, _ in wd.LEAVES]
+    assert names == _header_leaves()
+    assert len(names) == 71 == abi().NUM_LEAVES
+
+
+def test_state_fields_follow_reference_pytree():
+    """Field names of every State group in the reference's order (world.py:70-174)."""
+    assert wd.State._fields == ("bodies", "fixtures", "joints", "contacts", "gravity", "inv_dt0", "next_key",
+                                "new_fixture", "overflow", "toi")
+    assert wd.Contacts._fields[:4] == ("pair", "fa", "fb", "key")
+    assert wd.ContactTOI._fields[-1] == "events"
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# compact fixture layout and scene generators
+
+@pytest.mark.parametrize("k", [1, 3, 5])
+def test_compact_expand_round_trip(k):
+    s, m, st, cfg = b2.scenes.make_config(k, 8)
+    full = wd.expand_state(m, st)
+    assert full.fixtures.fat.shape[-2] == m.fixture_body.shape[0]
+    assert leaf_mismatches(st, wd.compact_state(m, full)) == []
+    rows = np.asarray(m.slot_fixture)
+    assert (np.asarray(m.body_type)[np.asarray(m.fixture_body)[rows]] != wd.STATIC).all()
+    static = np.asarray(m.fixture_slot) < 0
+    assert np.array_equal(full.fixtures.fat[0][static], np.asarray(m.static_fat)[static])
+
+
+def test_compact_step_equals_full_step(oracle):
+    """The compact layout is an exact re-encoding: the oracle steps a full-layout State and its compact form to the
+    same bits (world.py:437-563)."""
+    s, m, st, cfg = b2.scenes.make_config(1, 16)
+    full_model, _ = b2.scenes.build_world(cfg, s)[:2]
+    full = wd.expand_state(m, st)
+    a, c = oracle.copy(full), oracle.copy(st)
+    for _ in range(20):
+        oracle.step_(full_model, a, s, cfg.dt)
+        oracle.step_(m, c, s, cfg.dt)
+    assert leaf_mismatches(wd.compact_state(m, a), c) == []
+
+
+def test_candidate_pairs_rules():
+    """UpdatePairs candidate list: no same-body, no static-static, no jointed pair without collide_connected, polygon
+    first in mixed pairs (world.py:308-329)."""
+    d = wd.WorldDef(b2.Settings.stock())
+    g = d.add_body(wd.STATIC)
+    d.add_box(g, (5, 0.5))
+    d.add_box(g, (0.5, 5))
+    a = d.add_body(wd.DYNAMIC, (0, 2), mass=1, inertia=0.1)
+    d.add_circle(a, 0.2)
+    d.add_box(a, (0.1, 0.1))
+    b = d.add_body(wd.DYNAMIC, (1, 2), mass=1, inertia=0.1)
+    d.add_circle(b, 0.2)
+    c = d.add_body(wd.DYNAMIC, (2, 2), mass=1, inertia=0.1)
+    d.add_box(c, (0.2, 0.2))
+    d.add_revolute(a, b)
+    pairs = d.candidate_pairs()
+    fb = [f["body"] for f in d.fixtures]
+    st = [f["shape_type"] for f in d.fixtures]
+    for i, k in pairs:
+        assert fb[i] != fb[k]
+        assert not (fb[i] == g and fb[k] == g)
+        assert {fb[i], fb[k]} != {a, b}
+        if {st[i], st[k]} == {b2.shapes.CIRCLE, b2.shapes.POLYGON}:
+            assert st[i] == b2.shapes.POLYGON
+    want = {frozenset((i, k)) for i in range(6) for k in range(i + 1, 6)
+            if fb[i] != fb[k] and not (fb[i] == g and fb[k] == g) and {fb[i], fb[k]} != {a, b}}
+    assert {frozenset(p) for p in pairs} == want
+
+
+def test_polygon_set_hull_and_normals():
+    """b2PolygonShape::Set: convex hull in CCW order from the lowest-x point, unit outward normals (capi.cpp:378-416)."""
+    v, n = b2.shapes.polygon_set([(0, 0), (1, 0), (1, 1), (0, 1), (0.5, 0.5), (0.2, 0.9)], F32(0.005))
+    assert len(v) == 4
+    area = 0.5 * sum(v[i][0] * v[(i + 1) % 4][1] - v[(i + 1) % 4][0] * v[i][1] for i in range(4))
+    assert area == pytest.approx(1.0)  # CCW
+    for i in range(len(v)):
+        e = v[(i + 1) % len(v)] - v[i]
+        assert e[0] * n[i][1] - e[1] * n[i][0] < 0  # outward normal = right of a CCW edge: e x n = -|e|^2
+        assert abs(float(np.hypot(*n[i])) - 1) < 1e-6
+        assert abs(float(np.dot(n[i], e))) < 1e-6
+
+
+def test_edge_quad_encoding():
+    """Terrain segment p0 -> p1 as the thin CCW quad {p0, p1, p1 - t n, p0 - t n} with n the left normal."""
+    v, n = b2.shapes.edge_quad((0, 0), (2, 0), 0.1)
+    got = {tuple(np.round(x, 6)) for x in np.asarray(v, np.float64)}
+    assert got == {(0.0, 0.0), (2.0, 0.0), (2.0, -0.1), (0.0, -0.1)}
+    area = 0.5 * sum(v[i][0] * v[(i + 1) % 4][1] - v[(i + 1) % 4][0] * v[i][1] for i in range(4))
+    assert area > 0
+
+
+@pytest.mark.parametrize("k", [1, 2, 3, 4, 5])
+def test_config_shapes(k):
+    """Benchmark configurations: bodies, joints, terrain size and candidate count as specified."""
+    s, m, st, cfg = b2.scenes.make_config(k, 4)
+    B, R, J, C = wd.dims(st)
+    F = m.fixture_body.shape[0]
+    assert J == 3 and (B, R) == ((5, 4) if k < 5 else (17, 16))
+    assert F - R == cfg.n_edges + cfg.n_rocks
+    assert C == (32 if k < 5 else 64)
+    assert s.continuous_physics and not s.unity_toi and s.gravity == (F32(0), F32(-9.81))
+
+
+def test_actions_map_to_motor():
+    """The action -> motor mapping: motor speed = gain * a_x on the torso-handle joint, max torque scaled by |a|."""
+    rng = np.random.default_rng(0)
+    a = b2.scenes.actions(rng, 1000)
+    assert a.shape == (1000, 2) and (np.hypot(a[:, 0], a[:, 1]) <= 1 + 1e-6).all()
+    speed = np.zeros((1000, 3), F32)
+    torque = np.zeros((1000, 3), F32)
+    b2.scenes.apply_actions(speed, torque, a)
+    j = b2.scenes.MOTOR_JOINT
+    assert np.allclose(speed[:, j], b2.scenes.MOTOR_GAIN * a[:, 0])
+    assert np.allclose(torque[:, j], b2.scenes.MOTOR_TORQUE * np.hypot(a[:, 0], a[:, 1]))
+    others = [i for i in range(3) if i != j]
+    assert (speed[:, others] == 0).all() and (torque[:, others] == 0).all()
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the C-ABI library, without launching anything
+
+def _declared_symbols():
+    return re.findall(r"^\S.*?\b(goi_[a-z_]+)\s*\(", HEADER.read_text(), re.M)
+
+
+def test_library_exports_every_declared_symbol():
+    L = abi().lib()
+    names = _declared_symbols()
+    assert set(names) >= {"goi_abi_version", "goi_model_create", "goi_model_destroy", "goi_step", "goi_collide",
+                          "goi_sincos", "goi_last_error"}
+    for n in names:
+        assert hasattr(L, n), n
+    out = subprocess.run(["nm", "-D", "--defined-only", str(abi().LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (goi_[a-z_]+)", out))
+    assert set(names) <= exported
+
+
+def test_library_is_built_for_gfx950():
+    data = Path(abi().LIB_PATH).read_bytes()
+    assert b"gfx950" in data
+
+
+def test_bad_arguments_fail_before_the_device():
+    """Argument errors return the header's codes with a message and allocate nothing (no GPU needed)."""
+    A = abi()
+    L = A.lib()
+    out = ctypes.c_void_p()
+    assert L.goi_model_create(None, 32, None, ctypes.byref(out)) == A.GOI_E_ARG
+    assert b"null" in L.goi_last_error()
+    s, m, st, cfg = b2.scenes.make_config(1, 2)
+    full_model = b2.scenes.build_world(cfg, s)[0]
+    desc, keep = A.model_desc(m)
+    assert L.goi_model_create(ctypes.byref(desc), 65, None, ctypes.byref(out)) == A.GOI_E_UNSUPPORTED
+    assert b"capacity" in L.goi_last_error()
+    with pytest.raises(ValueError):
+        A.model_desc(full_model)  # the device step needs the compact layout
+    view = A.GoiStateView()
+    cs = s.to_c()
+    assert L.goi_step(None, ctypes.byref(view), ctypes.byref(cs), ctypes.c_float(0.01), None, None) == A.GOI_E_ARG
+    assert L.goi_collide(None, ctypes.byref(view), ctypes.byref(cs), None) == A.GOI_E_ARG
+    assert L.goi_sincos(None, None, None, -1, None) == A.GOI_E_ARG
+    assert L.goi_sincos(None, None, None, 0, None) == A.GOI_OK
+    assert L.goi_model_destroy(None) == A.GOI_OK
+
+
+def test_host_state_is_rejected():
+    """The step runs on device States only: numpy or CPU tensors raise before anything reaches the library."""
+    s, m, st, cfg = b2.scenes.make_config(1, 2)
+    with pytest.raises(ValueError):
+        b2.layout.state_view(st)
+    with pytest.raises(ValueError):
+        b2.step_(m, st, s, cfg.dt)
+    with pytest.raises(ValueError):
+        b2.step_(m, st, dataclasses.replace(s, solver="xla"), cfg.dt)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    """No fallback: with the HIP library absent, loading the step raises instead of computing anything else."""
+    code = ("import importlib, sys; sys.path.insert(0, %r); b2 = importlib.import_module('getting-over-it-rl_amd.box2d');"
+            "from importlib import import_module as im; A = im('getting-over-it-rl_amd.box2d._abi');"
+            "\ntry:\n    A.lib()\nexcept FileNotFoundError as e:\n    print('raised', e)\n" % str(ROOT))
+    env = dict(os.environ, GOI_B2_LIB=str(tmp_path / "absent.so"))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
+    assert r.returncode == 0 and "raised" in r.stdout, r.stderr

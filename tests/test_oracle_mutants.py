@@ -1,0 +1,52 @@
+"""The pins have teeth: each case plants one plausible slip in a copy of the CPU restatement (oracle/b2_oracle.c,
+rebuilt into a temporary directory), loads it in place of the real oracle and shows that the named pin of
+test_oracle_pins now fails. CPU only; the real oracle is untouched.
+"""
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import test_oracle_pins as P
+from oracle import oracle as O
+
+SRC = Path(O.__file__).resolve().parent / "b2_oracle.c"
+INC = SRC.parent.parent / "include"
+
+# (name, text in b2_oracle.c, replacement, the pin that must fail)
+MUTANTS = [
+    ("damping_as_1_minus_hc", "float ld = 1.0f / (1.0f + h * w->b_ld[b]);", "float ld = 1.0f - h * w->b_ld[b];",
+     lambda o: P.test_free_fall_is_semi_implicit_euler_bit_exact(o, 0.2)),
+    ("friction_mix_max", "sqrtf(friction_of(x, w, a) * friction_of(x, w, b))",
+     "fmaxf(friction_of(x, w, a), friction_of(x, w, b))",
+     lambda o: P.test_contact_impulses_carry_the_weight(o)),
+    ("restitution_mix_min", "w->c_restitution[k] = ra > rb ? ra : rb;", "w->c_restitution[k] = ra < rb ? ra : rb;",
+     lambda o: P.test_restitution_mix_is_max(o)),
+    ("toi_target_one_slop", "float target = bmax(linear_slop, total_radius - 3.0f * linear_slop);",
+     "float target = bmax(linear_slop, total_radius - 1.0f * linear_slop);",
+     lambda o: P.test_time_of_impact_contract(o)),
+    ("contact_list_oldest_first", "while (j > 0 && w->c_key[order[j - 1]] < w->c_key[k])",
+     "while (j > 0 && w->c_key[order[j - 1]] > w->c_key[k])",
+     lambda o: P.test_islands_vs_sequential_dfs(o, "pile")),
+    ("circle_radius_dropped", "float r = m->radius[fa] + m->radius[fb];", "float r = m->radius[fa];",
+     lambda o: P.test_narrowphase_vs_brute_force(o, P.shape_model.__wrapped__())),
+]
+
+
+def _build(tmp, name, old, new):
+    text = SRC.read_text()
+    assert text.count(old) == 1, f"{name}: the planted text must occur exactly once"
+    src = tmp / f"{name}.c"
+    src.write_text(text.replace(old, new))
+    lib = tmp / f"lib{name}.so"
+    subprocess.run(["gcc", "-O1", "-std=c11", "-ffp-contract=off", "-fno-fast-math", "-fopenmp", "-fPIC",
+                    "-shared", f"-I{INC}", f"-I{SRC.parent}", str(src), "-o", str(lib), "-lm"], check=True)
+    return lib
+
+
+@pytest.mark.parametrize("name,old,new,pin", MUTANTS, ids=[m[0] for m in MUTANTS])
+def test_pin_catches_planted_mistake(tmp_path, monkeypatch, oracle, name, old, new, pin):
+    pin(oracle)  # passes on the real restatement
+    monkeypatch.setattr(O, "_L", O.load(_build(tmp_path, name, old, new)))
+    with pytest.raises(AssertionError):
+        pin(O)

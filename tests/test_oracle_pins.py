@@ -1,0 +1,648 @@
+"""Pins of the CPU oracle (oracle/b2_oracle.c) that need no reference import: closed forms, known answers, brute
+force and physical invariants, each chosen so that a plausible slip (a dropped term, a swapped operand, a wrong
+index, a wrong tie rule) fails it. The checks follow the reference's own oracle tests where it has them
+(tests/reference/test_box2d_reference.py:23-155, tests/box2d/test_toi.py:23-35, test_box2d_parity.py:44-50) and
+the b2Distance / b2TimeOfImpact / b2Collide contracts otherwise. CPU only.
+"""
+import numpy as np
+import pytest
+
+from util import b2
+
+F32 = np.float32
+H = b2.GAME_DT
+wd = b2.world
+S = b2.Settings
+CIRCLE, POLYGON = b2.shapes.CIRCLE, b2.shapes.POLYGON
+
+
+def run(d, steps, capacity=16, settings=None, dt=H, n=1, oracle=None, each=None):
+    model, state = d.build(capacity)
+    st = wd.batch(state, n)
+    for k in range(steps):
+        oracle.step_(model, st, settings or d.settings, dt)
+        if each is not None:
+            each(k, st)
+    return model, st
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# sin / cos: correctly rounded float32, (float)sin((double)x)   (math2d.py:291-310, test_box2d_parity.py:44-50)
+
+def test_sincos_known_answers(oracle):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.uniform(-8, 8, 20000), rng.uniform(-300, 300, 5000), [0.0, -0.0, np.pi],
+                        rng.uniform(-1e4, 1e4, 20000)]).astype(F32)
+    s, c = oracle.sincos(x)
+    xs = x.astype(np.float64)
+    assert np.array_equal(s, np.sin(xs).astype(F32)) and np.array_equal(c, np.cos(xs).astype(F32))
+    assert np.signbit(s[25001]) and not np.signbit(s[25000])  # sin(-0) = -0
+    assert s[25002] == F32(np.sin(np.float64(F32(np.pi))))
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# integration: semi-implicit Euler with 2.3.1 damping, bit exact   (test_box2d_reference.py:23-35, step.py:86-93)
+
+@pytest.mark.parametrize("drag", [0.0, 0.2])
+def test_free_fall_is_semi_implicit_euler_bit_exact(oracle, drag):
+    d = wd.WorldDef(S.game())
+    d.add_body(wd.DYNAMIC, (1.25, 7.5), velocity=(3, 2), mass=4, inertia=1, linear_damping=drag)
+    g = F32(-30)
+    x, y, vx, vy = F32(1.25), F32(7.5), F32(3), F32(2)
+    damp = F32(1) / (F32(1) + H * F32(drag))
+    model, st = d.build(4)
+    st = wd.batch(st, 1)
+    for _ in range(300):
+        oracle.step_(model, st, d.settings, H)
+        vx = (vx + H * (F32(1) * F32(0) + F32(0))) * damp
+        vy = (vy + H * (F32(1) * g + F32(0))) * damp
+        x, y = x + H * vx, y + H * vy
+        got = (st.bodies.c[0, 0, 0], st.bodies.c[0, 0, 1], st.bodies.v[0, 0, 0], st.bodies.v[0, 0, 1])
+        assert got == (x, y, vx, vy)
+        assert tuple(st.bodies.xf_p[0, 0]) == (x, y)  # local centre 0: xf.p = c
+
+
+def test_max_translation_clamp(oracle):
+    """b2Island::Solve: a step that would move further than max_translation is scaled to exactly that length."""
+    d = wd.WorldDef(S.stock(gravity=(0, 0)))
+    d.add_body(wd.DYNAMIC, (0, 0), velocity=(300, 400), mass=1, inertia=1)
+    model, st = run(d, 1, dt=F32(1 / 60), oracle=oracle, settings=d.settings)
+    moved = float(np.hypot(*st.bodies.c[0, 0]))
+    assert moved == pytest.approx(2.0, rel=1e-6)  # stock max_translation 2 m
+    assert float(np.hypot(*st.bodies.v[0, 0])) == pytest.approx(120.0, rel=1e-6)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# resting contact   (test_box2d_reference.py:14-63)
+
+def resting_box(settings=None, y=1.015):
+    d = wd.WorldDef(settings or S.game())
+    ground = d.add_body(wd.STATIC)
+    d.add_box(ground, (10, 0.5), friction=1.0)
+    box = d.add_body(wd.DYNAMIC, (0, y), mass=2, inertia=F32(2) / F32(6))
+    d.add_box(box, (0.5, 0.5), friction=0.5)
+    return d, box
+
+
+def world_points(model, st, w, slot):
+    """b2WorldManifold::Initialize for one slot: (points [count, 2], separations [count]) in float64."""
+    ct, bd = st.contacts, st.bodies
+    fa, fb = int(ct.fa[w, slot]), int(ct.fb[w, slot])
+    ba, bb = int(model.fixture_body[fa]), int(model.fixture_body[fb])
+    ra, rb = float(model.radius[fa]), float(model.radius[fb])
+
+    def xf(b):
+        return np.array(bd.xf_p[w, b], np.float64), np.array(bd.xf_q[w, b], np.float64)
+
+    def mul(t, v):
+        (p, (c, s)) = t
+        return np.array([c * v[0] - s * v[1] + p[0], s * v[0] + c * v[1] + p[1]])
+
+    def rot(t, v):
+        c, s = t[1]
+        return np.array([c * v[0] - s * v[1], s * v[0] + c * v[1]])
+    xa, xb = xf(ba), xf(bb)
+    mt, n = int(ct.mtype[w, slot]), int(ct.count[w, slot])
+    pts, seps = [], []
+    for i in range(n):
+        lp = ct.point_local[w, slot, i].astype(np.float64)
+        if mt == 0:
+            pa, pb = mul(xa, ct.local_point[w, slot]), mul(xb, lp)
+            nrm = pb - pa
+            nrm = nrm / np.linalg.norm(nrm) if np.linalg.norm(nrm) > 1e-12 else np.array([1.0, 0.0])
+            ca, cb = pa + ra * nrm, pb - rb * nrm
+        elif mt == 1:
+            nrm = rot(xa, ct.local_normal[w, slot])
+            plane = mul(xa, ct.local_point[w, slot])
+            clip = mul(xb, lp)
+            ca = clip + (ra - np.dot(clip - plane, nrm)) * nrm
+            cb = clip - rb * nrm
+        else:
+            nrm = rot(xb, ct.local_normal[w, slot])
+            plane = mul(xb, ct.local_point[w, slot])
+            clip = mul(xa, lp)
+            cb = clip + (rb - np.dot(clip - plane, nrm)) * nrm
+            ca = clip - ra * nrm
+            nrm = -nrm
+        pts.append(0.5 * (ca + cb))
+        seps.append(float(np.dot(cb - ca, nrm)))
+    return np.array(pts).reshape(-1, 2), np.array(seps)
+
+
+def test_box_rests_and_sleeps(oracle):
+    d, box = resting_box()
+    model, state = d.build(8)
+    x0, y0 = state.bodies.c[box]
+    _, st = run(d, 240, capacity=8, oracle=oracle)
+    assert abs(st.bodies.c[0, box, 0] - x0) < 1e-5 and abs(st.bodies.a[0, box]) < 1e-5
+    assert abs(st.bodies.c[0, box, 1] - y0) < 1e-3  # settles only into the linear-slop skin
+    assert not st.bodies.awake[0, box]  # time_to_sleep 0.5 s at rest
+    assert np.all(st.bodies.v[0, box] == 0) and st.bodies.w[0, box] == 0  # sleeping zeroes velocity
+
+
+def test_contact_impulses_carry_the_weight(oracle):
+    d, box = resting_box()
+    model, st = run(d, 30, capacity=8, oracle=oracle)
+    ct = st.contacts
+    live = np.nonzero((ct.pair[0] >= 0) & ct.touching[0])[0]
+    assert len(live) == 1
+    k = int(live[0])
+    assert int(ct.mtype[0, k]) in (1, 2) and int(ct.count[0, k]) == 2
+    assert len(set(ct.point_id[0, k].tolist())) == 2  # distinct feature ids
+    total = float(ct.normal_impulse[0, k].sum())
+    assert total == pytest.approx(2 * 30 * float(H), rel=1e-3)  # m g dt per step at rest
+    assert ct.friction[0, k] == pytest.approx(np.sqrt(F32(0.5) * F32(1.0)), rel=1e-6)
+    assert ct.friction[0, k] == F32(np.sqrt(np.float64(F32(F32(0.5) * F32(1.0)))))  # b2MixFriction in float32
+    _, seps = world_points(model, st, 0, k)
+    assert -0.02 < seps.min() < 0  # rests inside the 2 x 0.01 skin
+
+
+def test_restitution_mix_is_max(oracle):
+    """b2MixRestitution = max(a, b); friction mix = sqrt(a * b) (pairs.py:134-178)."""
+    d = wd.WorldDef(S.stock())
+    g = d.add_body(wd.STATIC)
+    d.add_box(g, (10, 0.5), friction=0.9, restitution=0.1)
+    b = d.add_body(wd.DYNAMIC, (0, 1.0), mass=1, inertia=0.1)
+    d.add_box(b, (0.5, 0.5), friction=0.4, restitution=0.6)
+    _, st = run(d, 2, capacity=4, oracle=oracle, dt=F32(1 / 60))
+    k = int(np.nonzero(st.contacts.pair[0] >= 0)[0][0])
+    assert st.contacts.restitution[0, k] == F32(0.6)
+    assert st.contacts.friction[0, k] == F32(np.sqrt(np.float64(F32(F32(0.9) * F32(0.4)))))
+
+
+def test_bounce_with_restitution_one(oracle):
+    """A ball dropped on a restitutive floor comes back up: restitution bias applies when the approach speed exceeds
+    velocity_threshold (contact_solver.py:32-147)."""
+    d = wd.WorldDef(S.stock(gravity=(0, -10)))
+    g = d.add_body(wd.STATIC)
+    d.add_box(g, (10, 0.5), restitution=1.0)
+    ball = d.add_body(wd.DYNAMIC, (0, 3.0), mass=1, inertia=0.01)
+    d.add_circle(ball, 0.25, restitution=1.0)
+    vmax = []
+    _, st = run(d, 120, capacity=4, oracle=oracle, dt=F32(1 / 60),
+                each=lambda k, s: vmax.append(float(s.bodies.v[0, ball, 1])))
+    v = np.array(vmax)
+    hit = int(np.argmax(v > 0))
+    assert hit > 0 and v[hit] == pytest.approx(-v[hit - 1], rel=0.05)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# solver invariants
+
+def test_normal_impulses_non_negative(oracle):
+    """Accumulated normal impulses are clamped at 0 (contact_solver.py:194-290), over a pile of boxes."""
+    s, m, st = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+    st = wd.batch(st, 4)
+    for _ in range(60):
+        oracle.step_(m, st, s, F32(1 / 60))
+        ct = st.contacts
+        npts = (np.arange(2)[None, None, :] < ct.count[..., None]) & (ct.pair >= 0)[..., None]
+        assert (ct.normal_impulse[npts] >= 0).all()
+
+
+@pytest.mark.parametrize("mu,slides", [(0.5, False), (0.1, True)])
+def test_box_on_incline(oracle, mu, slides):
+    """Coulomb friction: on a slope of angle th a box sticks when tan th < mu, else slides with acceleration
+    g (sin th - mu cos th); both fixtures carry mu so the mixed friction sqrt(mu mu) is mu."""
+    th, g = 0.3, 10.0
+    d = wd.WorldDef(S.stock(gravity=(0, -g)))
+    ground = d.add_body(wd.STATIC, (0, 0), th)
+    d.add_box(ground, (20, 0.5), friction=mu)
+    n = np.array([-np.sin(th), np.cos(th)])
+    box = d.add_body(wd.DYNAMIC, tuple(n * (0.5 + 0.25)), th, mass=1, inertia=1 / 24)
+    d.add_box(box, (0.25, 0.25), friction=mu)
+    t_hat = np.array([np.cos(th), np.sin(th)])
+    pos = []
+    run(d, 120, capacity=4, oracle=oracle, dt=F32(1 / 60),
+        each=lambda k, s: pos.append(float(np.dot(s.bodies.c[0, box].astype(np.float64), t_hat))))
+    x = np.array(pos[30:])
+    if not slides:
+        assert abs(x[-1] - x[0]) < 1e-3
+    else:
+        acc = np.polyfit(np.arange(len(x)) / 60.0, x, 2)[0] * 2
+        assert acc == pytest.approx(-g * (np.sin(th) - mu * np.cos(th)), rel=0.03)
+
+
+def test_momentum_conserved_in_free_collision(oracle):
+    """Two free boxes collide in zero gravity: total linear momentum is unchanged by the contact impulses (equal and
+    opposite, applied to both bodies) to float32 accuracy; so is angular momentum about the origin, since both
+    impulses act at the same world point. Position iterations are off: their projection moves the centres (not the
+    centre of mass) without a matching velocity change, which is Box2D's behaviour but not a conserved quantity."""
+    d = wd.WorldDef(S.stock(gravity=(0, 0), position_iterations=0))
+    a = d.add_body(wd.DYNAMIC, (-1.0, 0.05), velocity=(4, 0), angular_velocity=0.5, mass=2, inertia=0.3)
+    d.add_box(a, (0.3, 0.2), friction=0.6)
+    b = d.add_body(wd.DYNAMIC, (1.0, -0.05), velocity=(-3, 0.5), angular_velocity=-1.0, mass=1, inertia=0.1)
+    d.add_box(b, (0.25, 0.25), friction=0.6)
+    m = np.array([2.0, 1.0])
+    inertia = np.array([0.3, 0.1])
+
+    def momenta(st):
+        v = st.bodies.v[0].astype(np.float64)
+        c = st.bodies.c[0].astype(np.float64)
+        w = st.bodies.w[0].astype(np.float64)
+        p = (m[:, None] * v).sum(0)
+        L = float((inertia * w + m * (c[:, 0] * v[:, 1] - c[:, 1] * v[:, 0])).sum())
+        return p, L
+    model, state = d.build(4)
+    p0, L0 = momenta(wd.batch(state, 1))
+    touched = []
+    _, st = run(d, 60, capacity=4, oracle=oracle, dt=F32(1 / 60),
+                each=lambda k, s: touched.append(bool(s.contacts.touching[0].any())))
+    p1, L1 = momenta(st)
+    assert any(touched)
+    assert np.allclose(p1, p0, atol=1e-4 * np.abs(p0).sum())
+    assert L1 == pytest.approx(L0, abs=1e-5)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# joints   (test_box2d_reference.py:90-127)
+
+def test_pendulum_conserves_energy_and_joint(oracle):
+    d = wd.WorldDef(S.game())
+    pivot = d.add_body(wd.STATIC)
+    L, m, inertia = 2.0, 1.0, 0.01
+    bob = d.add_body(wd.DYNAMIC, (L, 0), mass=m, inertia=inertia)
+    d.add_revolute(pivot, bob, (0, 0), (-L, 0))
+    trace = []
+    run(d, 240, capacity=2, oracle=oracle,
+        each=lambda k, s: trace.append((s.bodies.c[0, bob].astype(np.float64), s.bodies.v[0, bob].astype(np.float64))))
+    lowest = None
+    for c, v in trace:
+        assert abs(np.hypot(*c) - L) < 1e-3
+        if lowest is None and c[0] <= 0:
+            lowest = v
+    assert lowest is not None
+    assert np.hypot(*lowest) == pytest.approx(np.sqrt(2 * 30 * L / (1 + inertia / (m * L * L))), rel=0.03)
+
+
+@pytest.mark.parametrize("v24", [True, False])
+def test_revolute_limit_and_motor(oracle, v24):
+    d = wd.WorldDef(S.game(gravity=(0, 0), revolute_v24=v24))
+    pivot = d.add_body(wd.STATIC)
+    arm = d.add_body(wd.DYNAMIC, (1, 0), mass=1, inertia=0.1)
+    d.add_revolute(pivot, arm, (0, 0), (-1, 0), limits=(-0.5, 0.5), motor_speed=2.0, max_motor_torque=1000,
+                   enable_motor=True)
+    model, st = run(d, 12, capacity=2, oracle=oracle)
+    assert st.bodies.w[0, arm] == pytest.approx(2.0, rel=1e-4)
+    for _ in range(120):
+        oracle.step_(model, st, d.settings, H)
+    assert st.joints.limit_state[0, 0] == 2  # AT_UPPER
+    assert st.bodies.a[0, arm] == pytest.approx(0.5, abs=float(b2.settings.deg2rad(2)))
+
+
+def test_prismatic_limit_holds(oracle):
+    """A prismatic joint along x with limits keeps the body on the axis and within [lower, upper] (+ slop)."""
+    d = wd.WorldDef(S.stock(gravity=(0, -10)))
+    g = d.add_body(wd.STATIC)
+    box = d.add_body(wd.DYNAMIC, (0, 0), velocity=(5, 0), mass=1, inertia=0.1)
+    d.add_prismatic(g, box, (0, 0), (0, 0), axis=(1, 0), limits=(-1.0, 1.0))
+    ys, xs = [], []
+    run(d, 120, capacity=2, oracle=oracle, dt=F32(1 / 60),
+        each=lambda k, s: (ys.append(float(s.bodies.c[0, box, 1])), xs.append(float(s.bodies.c[0, box, 0]))))
+    assert max(abs(y) for y in ys) < 0.01
+    assert max(xs) < 1.0 + 0.05 and max(xs) > 0.9
+
+
+def test_weld_keeps_relative_pose(oracle):
+    """A rigid weld joint holds two boxes' relative pose while the pair falls and spins."""
+    d = wd.WorldDef(S.stock(gravity=(0, -10)))
+    a = d.add_body(wd.DYNAMIC, (0, 0), angular_velocity=2.0, mass=1, inertia=0.1)
+    b = d.add_body(wd.DYNAMIC, (1, 0), mass=1, inertia=0.1)
+    d.add_weld(a, b, (0.5, 0), (-0.5, 0))
+    _, st = run(d, 90, capacity=2, oracle=oracle, dt=F32(1 / 60))
+    c = st.bodies.c[0].astype(np.float64)
+    ang = st.bodies.a[0].astype(np.float64)
+    assert np.hypot(*(c[1] - c[0])) == pytest.approx(1.0, abs=5e-3)
+    assert ang[1] - ang[0] == pytest.approx(0.0, abs=1e-2)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# continuous collision   (test_box2d_reference.py:130-155, test_toi.py:23-35)
+
+def _bullet_through_wall(oracle, continuous=False, unity=True):
+    d = wd.WorldDef(S.game(gravity=(0, 0), unity_toi=unity))
+    wall = d.add_body(wd.STATIC, (0, 0))
+    d.add_box(wall, (0.05, 2))
+    ball = d.add_body(wd.DYNAMIC, (-1, 0), velocity=(240, 0), mass=1, inertia=0.01, continuous=continuous)
+    d.add_circle(ball, 0.05)
+    _, st = run(d, 3, capacity=4, oracle=oracle)
+    return float(st.bodies.c[0, ball, 0])
+
+
+def test_toi_pair_rules(oracle):
+    assert _bullet_through_wall(oracle) > 0  # Unity rule: a discrete body tunnels
+    assert _bullet_through_wall(oracle, continuous=True) < 0  # a Continuous body is stopped
+    assert _bullet_through_wall(oracle, unity=False) < 0  # stock rule: every dynamic-vs-static pair gets TOI
+
+
+def test_toi_off_tunnels(oracle):
+    d = wd.WorldDef(S.game(gravity=(0, 0), continuous_physics=False))
+    wall = d.add_body(wd.STATIC)
+    d.add_box(wall, (0.05, 2))
+    ball = d.add_body(wd.DYNAMIC, (-1, 0), velocity=(240, 0), mass=1, inertia=0.01, continuous=True)
+    d.add_circle(ball, 0.05)
+    _, st = run(d, 3, capacity=4, oracle=oracle)
+    assert st.bodies.c[0, ball, 0] > 0 and int(st.toi.events[0]) == 0
+
+
+def _sweep_xf(sw, t):
+    lc, c0, c, a0, a = sw[0:2], sw[2:4], sw[4:6], sw[6], sw[7]
+    cc = (1 - t) * c0 + t * c
+    aa = (1 - t) * a0 + t * a
+    q = np.array([np.cos(aa), np.sin(aa)])
+    p = cc - np.array([q[0] * lc[0] - q[1] * lc[1], q[1] * lc[0] + q[0] * lc[1]])
+    return np.array([p[0], p[1], q[0], q[1]], np.float32)
+
+
+def test_time_of_impact_contract(oracle):
+    """b2TimeOfImpact: when it reports TOUCHING at t, the core shapes' distance at t is within target +- tol, target
+    = max(slop, r_A + r_B - 3 slop), tol = slop / 4 (toi.py:372-375); when it reports SEPARATED at t = 1 they never
+    came within target."""
+    d = wd.WorldDef(S.stock())
+    g = d.add_body(wd.STATIC)
+    d.add_box(g, (0.5, 0.1))
+    d.add_polygon(g, [(0, 0), (1, 0.2), (0.3, 0.8)])
+    p = d.add_body(wd.DYNAMIC, (0, 3), mass=1, inertia=0.1)
+    d.add_box(p, (0.2, 0.05))
+    d.add_circle(p, 0.1, center=(0.3, 0))
+    model, _ = d.build(4)
+    slop = float(S.stock().linear_slop)
+    rng = np.random.default_rng(7)
+    touching = separated = 0
+    for trial in range(300):
+        fa = int(rng.integers(0, 2))
+        fb = 2 + int(rng.integers(0, 2))
+        ra, rb = float(model.radius[fa]), float(model.radius[fb])
+        target = max(slop, ra + rb - 3 * slop)
+        c0 = rng.uniform([-2, 1.5], [2, 3])
+        c1 = rng.uniform([-1, -1.5], [1, 0.5])
+        a0, a1 = rng.uniform(-3, 3), rng.uniform(-6, 6)
+        sa = np.array([0, 0, 0, 0, 0, 0, 0, 0], np.float32)
+        sb = np.array([0, 0, c0[0], c0[1], c1[0], c1[1], a0, a1], np.float32)
+        state, t = oracle.time_of_impact(model, fa, fb, sa, sb, F32(slop))
+        tol = 0.25 * slop
+        dist = oracle.distance(model, fa, fb, _sweep_xf(sa, t), _sweep_xf(sb.astype(np.float64), t))
+        if state == 3 and t > 0:  # reached by the root finder: the separation function is within target +- tol
+            assert target - tol - 1e-4 <= dist < target + tol + 1e-4, (trial, t, dist, target)
+            touching += 1
+        elif state == 3:  # already closer than target + tol at t = 0 (but not overlapping)
+            assert 0 < dist < target + tol + 1e-4
+        elif state == 4:  # separated at the end of the sweep along the final axis, so the distance there exceeds it
+            assert t == 1.0 and dist > target + tol - 1e-4
+            separated += 1
+    assert touching > 50 and separated > 20
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# distance (GJK) and narrowphase vs brute force
+
+def _poly_world(model, f, xf):
+    n = int(model.count[f])
+    v = model.verts[f, :n].astype(np.float64)
+    c, s = float(xf[2]), float(xf[3])
+    return np.stack([c * v[:, 0] - s * v[:, 1] + xf[0], s * v[:, 0] + c * v[:, 1] + xf[1]], 1)
+
+
+def _seg_dist(p, a, b):
+    ab = b - a
+    t = np.clip(np.dot(p - a, ab) / max(np.dot(ab, ab), 1e-300), 0, 1)
+    return float(np.linalg.norm(p - (a + t * ab)))
+
+
+def _inside(p, poly):
+    n = len(poly)
+    return n >= 3 and all(_cross(poly[(i + 1) % n] - poly[i], p - poly[i]) >= 0 for i in range(n))
+
+
+def _cross(a, b):
+    return a[0] * b[1] - a[1] * b[0]
+
+
+def _poly_dist(A, B):
+    """Exact distance between convex polygons (vertex lists, CCW; 1 vertex = point): 0 if they overlap (no
+    separating edge normal, or a point inside the polygon), else the minimum vertex-to-edge distance both ways."""
+    if len(A) >= 3 and len(B) >= 3 and max(_sat(A, B), _sat(B, A)) <= 0:
+        return 0.0
+    if (len(B) == 1 and _inside(B[0], A)) or (len(A) == 1 and _inside(A[0], B)):
+        return 0.0
+
+    def edges(P):
+        return [(P[i], P[(i + 1) % len(P)]) for i in range(len(P))] if len(P) > 1 else [(P[0], P[0])]
+    dmin = min(_seg_dist(p, a, b) for p in A for (a, b) in edges(B))
+    return min(dmin, min(_seg_dist(p, a, b) for p in B for (a, b) in edges(A)))
+
+
+def _sat(A, B):
+    """max over A's faces of min over B's vertices of the face separation (b2FindMaxSeparation, exhaustive)."""
+    best = -np.inf
+    for i in range(len(A)):
+        e = A[(i + 1) % len(A)] - A[i]
+        nrm = np.array([e[1], -e[0]]) / np.linalg.norm(e)
+        best = max(best, min(np.dot(nrm, v - A[i]) for v in B))
+    return best
+
+
+@pytest.fixture(scope="module")
+def shape_model():
+    d = wd.WorldDef(S.stock())
+    g = d.add_body(wd.STATIC)
+    d.add_box(g, (0.6, 0.3))
+    d.add_polygon(g, [(0, 0), (1, 0.2), (0.3, 0.8)])
+    d.add_polygon(g, [(0, 0), (0.5, -0.1), (0.9, 0.3), (0.6, 0.7), (0.1, 0.6)])
+    d.add_circle(g, 0.3)
+    d.add_circle(g, 0.15, center=(0.2, -0.1))
+    model, _ = d.build(2)
+    return model
+
+
+def _rand_xf(rng, spread=1.5):
+    a = rng.uniform(-np.pi, np.pi)
+    p = rng.uniform(-spread, spread, 2)
+    return np.array([p[0], p[1], np.cos(a), np.sin(a)], np.float32)
+
+
+def test_gjk_distance_vs_exhaustive(oracle, shape_model):
+    m = shape_model
+    rng = np.random.default_rng(11)
+    for trial in range(400):
+        fa, fb = (int(x) for x in rng.integers(0, 5, 2))
+        xa, xb = _rand_xf(rng), _rand_xf(rng)
+        got = oracle.distance(m, fa, fb, xa, xb)
+        want = _poly_dist(_poly_world(m, fa, xa), _poly_world(m, fb, xb))
+        if want == 0.0:
+            assert got <= 1e-3, (trial, got)
+        else:
+            assert got == pytest.approx(want, abs=5e-5 + 5e-5 * want), (trial, fa, fb, got, want)
+
+
+def test_narrowphase_vs_brute_force(oracle, shape_model):
+    """Manifold point count against exhaustive geometry: circles touch iff |c1 - c2| <= r1 + r2; polygon-circle iff
+    the centre is within r_p + r_c of the polygon; polygon pairs: no points when the exhaustive face separation
+    exceeds r_A + r_B, some point when the true distance is below it; every manifold point's separation is at
+    most r_A + r_B and no deeper than the exhaustive overlap allows."""
+    m = shape_model
+    rng = np.random.default_rng(12)
+    slop = F32(0.005)
+    seen = {"cc": [0, 0], "pc": [0, 0], "pp": [0, 0]}
+    for trial in range(3000):
+        fa, fb = (int(x) for x in rng.integers(0, 5, 2))
+        ta, tb = int(m.shape_type[fa]), int(m.shape_type[fb])
+        if ta == CIRCLE and tb == POLYGON:  # the contact always puts the polygon first
+            fa, fb, ta, tb = fb, fa, tb, ta
+        xa, xb = _rand_xf(rng, 0.8), _rand_xf(rng, 0.8)
+        man = oracle.evaluate(m, fa, fb, xa, xb, slop)
+        A, B = _poly_world(m, fa, xa), _poly_world(m, fb, xb)
+        r = float(m.radius[fa]) + float(m.radius[fb])
+        dist = _poly_dist(A, B)
+        if abs(dist - r) < 1e-3:
+            continue
+        if ta == CIRCLE and tb == CIRCLE:
+            kind = "cc"
+            assert man["count"] == (1 if dist <= r else 0)
+        elif tb == CIRCLE:
+            kind = "pc"
+            assert man["count"] == (1 if dist <= r else 0), (trial, dist, r, man)
+        else:
+            kind = "pp"
+            sep = max(_sat(A, B), _sat(B, A))
+            if sep > r + 1e-4:
+                assert man["count"] == 0
+            if dist < r - 1e-4:
+                assert man["count"] >= 1
+        seen[kind][man["count"] > 0] += 1
+    assert all(a > 30 and b > 30 for a, b in seen.values()), seen
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# broadphase: FindNewContacts vs a brute-force scan of the candidate list   (world.py:308-329, pairs.py:134-178)
+
+def _overlap(a, b):
+    return not (b[0] - a[2] > 0 or b[1] - a[3] > 0 or a[0] - b[2] > 0 or a[1] - b[3] > 0)
+
+
+@pytest.mark.parametrize("cfg", [1, 3])
+def test_find_new_contacts_vs_brute_force(oracle, cfg):
+    """From an empty contact table, FindNewContacts creates exactly the candidates whose fat AABBs overlap (one body
+    dynamic and awake-or-not, both active), in candidate order: the r-th overlapping candidate takes slot r and key
+    next_key + r. Integer equality with a plain scan of Model.pair_a/pair_b."""
+    s, model, state, c = b2.scenes.make_config(cfg, 64)
+    st = oracle.copy(state)
+    fat = wd.expand_state(model, st).fixtures.fat  # [N, F, 4] lower x, lower y, upper x, upper y
+    oracle.collide_(model, st, s)
+    pa, pb = np.asarray(model.pair_a), np.asarray(model.pair_b)
+    fb_ = np.asarray(model.fixture_body)
+    btype = np.asarray(state.bodies.type)
+    for w in range(state.bodies.type.shape[0]):
+        f = fat[w]
+        want = []
+        for p in range(pa.shape[0]):
+            a, b = int(pa[p]), int(pb[p])
+            if btype[w, fb_[a]] != wd.DYNAMIC and btype[w, fb_[b]] != wd.DYNAMIC:
+                continue
+            if _overlap(f[a], f[b]):
+                want.append(p)
+        C = st.contacts.pair.shape[1]
+        got_pairs = st.contacts.pair[w]
+        keep = want[:C]
+        # Collide may destroy a fresh contact only if its fat AABBs stopped overlapping, which they cannot here.
+        assert got_pairs[:len(keep)].tolist() == keep, w
+        assert (got_pairs[len(keep):] == -1).all()
+        assert st.contacts.key[w, :len(keep)].tolist() == list(range(len(keep)))
+        assert int(st.next_key[w]) == len(keep)
+        assert int(st.overflow[w]) == max(0, len(want) - C)
+
+
+def test_find_new_contacts_keys_follow_candidate_order(oracle):
+    """Later FindNewContacts calls (one per step with TOI off): surviving contacts keep their slot and key, and the
+    contacts created in one call take keys next_key, next_key + 1, ... in candidate (pair index) order."""
+    import dataclasses
+    s, m, st0 = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+    s = dataclasses.replace(s, continuous_physics=False)
+    st = wd.batch(st0, 1)
+    oracle.step_(m, st, s, F32(1 / 60))
+    created = 0
+    for _ in range(60):
+        bp, bk, nk = st.contacts.pair[0].copy(), st.contacts.key[0].copy(), int(st.next_key[0])
+        oracle.step_(m, st, s, F32(1 / 60))
+        ap, ak = st.contacts.pair[0], st.contacts.key[0]
+        kept = (bp >= 0) & (ap >= 0) & (ak < nk)
+        assert (ap[kept] == bp[kept]).all() and (ak[kept] == bk[kept]).all()
+        new = np.nonzero((ap >= 0) & (ak >= nk))[0]
+        by_key = new[np.argsort(ak[new])]
+        assert ak[by_key].tolist() == list(range(nk, nk + len(new)))
+        assert ap[by_key].tolist() == sorted(ap[by_key].tolist())
+        assert int(st.next_key[0]) == nk + len(new)
+        created += len(new)
+    assert created > 5
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# islands: a plain sequential DFS from the rules of b2World::Solve   (island.py:1-19)
+
+def _dfs_islands(model, st, w):
+    """body_island, contact_order from the rules: seeds in descending body index (awake, active, not static,
+    unvisited); pop LIFO; each popped body walks its touching contacts newest first (descending key), then its
+    joints newest first (descending index); static bodies are never expanded."""
+    bd, ct = st.bodies, st.contacts
+    B, C = bd.type.shape[1], ct.pair.shape[1]
+    fbody = np.asarray(model.fixture_body)
+    isl = [-1] * B
+    c_in = [False] * C
+    order = []
+    n = 0
+    for seed in range(B - 1, -1, -1):
+        if isl[seed] >= 0 or not bd.awake[w, seed] or not bd.active[w, seed] or bd.type[w, seed] == wd.STATIC:
+            continue
+        stack = [seed]
+        isl[seed] = n
+        while stack:
+            b = stack.pop()
+            if bd.type[w, b] == wd.STATIC:
+                continue
+            edges = [k for k in range(C) if ct.pair[w, k] >= 0 and ct.touching[w, k]
+                     and b in (fbody[ct.fa[w, k]], fbody[ct.fb[w, k]])]
+            for k in sorted(edges, key=lambda k: -int(ct.key[w, k])):
+                if c_in[k]:
+                    continue
+                c_in[k] = True
+                order.append(k)
+                ba, bb = fbody[ct.fa[w, k]], fbody[ct.fb[w, k]]
+                other = bb if ba == b else ba
+                if isl[other] < 0 and bd.type[w, other] != wd.STATIC:
+                    isl[other] = n
+                    stack.append(other)
+            for j in range(model.joint_type.shape[0] - 1, -1, -1):
+                ja, jb = int(model.joint_a[j]), int(model.joint_b[j])
+                if b not in (ja, jb):
+                    continue
+                other = jb if ja == b else ja
+                if not bd.active[w, other]:
+                    continue
+                if isl[other] < 0 and bd.type[w, other] != wd.STATIC:
+                    isl[other] = n
+                    stack.append(other)
+        n += 1
+    return isl, order, n
+
+
+@pytest.mark.parametrize("scene", ["pile", "joints", "island_walk"])
+def test_islands_vs_sequential_dfs(oracle, scene):
+    s, m, st0 = b2.scenes.build_test_scene(scene, iterations=(8, 3))
+    st = wd.batch(st0, 1)
+    B, R, J, C = wd.dims(st)
+    checked = 0
+    for k in range(60):
+        pre = oracle.copy(st)
+        dbg = dict(body_island=np.zeros((B, 1), np.int32), contact_island=np.zeros((C, 1), np.int32),
+                   contact_order=np.zeros((C, 1), np.int32), n_islands=np.zeros(1, np.int32))
+        oracle.collide_(m, pre, s)  # the contact table Solve sees: after FindNewContacts and Collide
+        oracle.step_(m, st, s, F32(1 / 60), debug=dbg)
+        isl, order, n = _dfs_islands(m, pre, 0)
+        if n == 0:
+            continue
+        assert dbg["n_islands"][0] == n
+        assert dbg["body_island"][:, 0].tolist() == [i if pre.bodies.type[0, b] != wd.STATIC else -1
+                                                     for b, i in enumerate(isl)]
+        assert dbg["contact_order"][:len(order), 0].tolist() == order
+        checked += 1
+    assert checked > 10
