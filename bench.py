@@ -14,7 +14,7 @@ R = 113 B + 24 F_d + 54 J + 93 C + 21 and W = 81 B + 16 F_d + 28 J + 120 C + 17 
 J joints, C contact slots); achieved = N x (R + W) / mean k_step duration (HIP events on its stream).
 
 cpu_baseline: the CPU restatement of the same step (oracle/, C, sequential per world, OpenMP over worlds) on the host
-cores, on the same configuration.
+cores, over the same initial State and actions (warmup + timed steps), repeated to at least --cpu-seconds.
 """
 import argparse
 import json
@@ -48,20 +48,28 @@ def traffic_from_profiles(kernel, workload):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(model, state, settings, cfg, steps):
+def cpu_baseline(model, state, settings, cfg, acts, apply, min_seconds=10.0, max_passes=20):
+    """The oracle on the host cores over the same workload: passes of the same action-driven steps from the same
+    initial State, repeated until at least min_seconds of CPU work (a bounded sample, a few tens of seconds)."""
     from oracle import oracle as O
     threads = len(os.sched_getaffinity(0))
     if os.environ.get("OMP_NUM_THREADS"):
         threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
-    x = O.copy(state)
-    n = int(np.asarray(x.bodies.type).shape[0])
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        O.step_(model, x, settings, cfg.dt, threads)
-    dt = time.perf_counter() - t0
-    return {"value": n * steps / dt, "unit": "world-steps/s", "cores": threads, "kind": "port",
-            "sample": f"{cfg.name}: {n} worlds x {steps} steps ({n * steps} world-steps, {dt:.1f} s) of the oracle "
-                      f"(oracle/b2_oracle.c, -O2, OpenMP over worlds)"}
+    n = int(np.asarray(state.bodies.type).shape[0])
+    done, elapsed, passes = 0, 0.0, 0
+    while elapsed < min_seconds and passes < max_passes:
+        x = O.copy(state)
+        t0 = time.perf_counter()
+        for a in acts:
+            apply(x.joints.motor_speed, x.joints.max_motor, a)
+            O.step_(model, x, settings, cfg.dt, threads)
+        elapsed += time.perf_counter() - t0
+        done += n * len(acts)
+        passes += 1
+    return {"value": done / elapsed, "unit": "world-steps/s", "cores": threads, "kind": "port",
+            "sample": f"{cfg.name}: {passes} passes x {len(acts)} steps x {n} worlds ({done} world-steps, "
+                      f"{elapsed:.1f} s) of the oracle (oracle/b2_oracle.c, -O2, OpenMP over worlds), same initial "
+                      "State and actions as the timed GPU steps"}
 
 
 def main():
@@ -71,7 +79,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=4)
     ap.add_argument("--worlds", type=int, default=None)
-    ap.add_argument("--cpu-steps", type=int, default=None, help="oracle steps for cpu_baseline (0: skip)")
+    ap.add_argument("--cpu-steps", type=int, default=None,
+                    help="steps per oracle pass for cpu_baseline (default: warmup + steps; 0: skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum CPU time of the cpu_baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run only a plain device copy of MIB MiB 10 times (the rocprofv3 FETCH_SIZE/WRITE_SIZE "
                          "calibration) and exit")
@@ -135,10 +145,11 @@ def main():
     traffic = traffic_from_profiles("k_step", workload)
 
     cpu = None
-    cpu_steps = args.cpu_steps if args.cpu_steps is not None else (cfg.steps if n <= 16384 else 10)
+    cpu_steps = args.warmup + args.steps if args.cpu_steps is None else args.cpu_steps
     if cpu_steps > 0:
         s2, m2, st2, _ = scenes.make_config(args.config, args.worlds)
-        cpu = cpu_baseline(m2, st2, s2, cfg, cpu_steps)
+        host_acts = acts[:cpu_steps].cpu().numpy()
+        cpu = cpu_baseline(m2, st2, s2, cfg, host_acts, scenes.apply_actions, args.cpu_seconds)
 
     out = {
         "metric": "world-steps/sec at 16384 worlds (full step incl. TOI); % of HBM roofline",

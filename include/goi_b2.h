@@ -225,7 +225,7 @@ int32_t goi_model_destroy(GoiModel* model);
 int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
                  void* hip_stream, const GoiDebug* debug);
 
-/* Broadphase and narrowphase only: start-of-step FindNewContacts where new_fixture
+/* Broadphase and narrowphase only (the collide-only workload): start-of-step FindNewContacts where new_fixture
  * (step.py:50-70), then Collide (pairs.py:38-87). */
 int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings,
                     void* hip_stream);

@@ -24,6 +24,17 @@
  * (:90-110), revolute limit and motor (:112-127), TOI ball stopped / discrete ball tunnels (test_toi.py:181-185,
  * test_box2d_reference.py:130-155), narrowphase against brute-force distances, GJK against exhaustive distances,
  * broadphase candidate scan against a brute-force scan, and the b2TimeOfImpact target contract (toi.py:372-375).
+ *
+ * Parity unpinned: the reference commits no golden vectors for this path and can be run neither here (jax absent)
+ * nor from source (Box2D 2.3.1 is fetched over the network), so these parts are right only by faithful reading of
+ * the cited reference text; no closed form fixes their exact bits:
+ *   - collide_polygons' feature ids and clip order under ties (collide.py:65-127);
+ *   - the wake cascade of collide() in list order (pairs.py:90-117);
+ *   - cs_solve_velocity's block-solver case selection path (contact_solver.py:236-279);
+ *   - the revolute v2.4.1 velocity/position rows, prismatic and weld rows (joints.py:302-343, 482-498);
+ *   - time_of_impact / distance iteration paths (toi.py:230-459);
+ *   - toi_event's island walk membership and break (toi.py:604-716);
+ *   - the min-TOI tie rule in toi_search (toi.py:552-556).
  */
 #include <math.h>
 #include <stdint.h>

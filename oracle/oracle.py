@@ -1,5 +1,6 @@
 """ctypes wrapper of the CPU restatement (liboracle_b2.so). TEST INFRASTRUCTURE ONLY: tests/, smoke() and bench.py's
-cpu_baseline leg use it as the checker; the product path never imports it.
+cpu_baseline leg use it, to check the device step and to time the CPU baseline; the product path never imports
+it.
 
 States are batched numpy States (leading world axis, contiguous), in either fixture layout; the oracle steps them in
 place. `step` copies first and returns the stepped copy.

@@ -2,8 +2,8 @@
 
 Integer/index leaves (contact slots, candidate indices, keys, manifold point counts and feature ids, TOI counts and
 flags) and float leaves (positions, angles, velocities, impulses, manifold geometry) must be identical at every step:
-both sides perform the reference's float32 operations in the same order, so the tolerance of the north star
-(1e-4 abs / 1e-3 rel) is not needed; any difference is a bug. Island ids and solve order (not State leaves) are
+both sides perform the reference's float32 operations in the same order, so a float tolerance (1e-4 abs /
+1e-3 rel per step would be allowed) is not needed; any difference is a bug. Island ids and solve order (not State leaves) are
 compared through the debug outputs.
 """
 import numpy as np
@@ -45,7 +45,7 @@ def test_scene_parity_game_iterations(name, oracle):
     _run(m, perturbed(st, 16, seed=3), s, b2.GAME_DT, 60, oracle)
 
 
-@pytest.mark.parametrize("k,n,steps", [(1, 1, 200), (3, 512, 30), (4, 512, 30)])
+@pytest.mark.parametrize("k,n,steps", [(1, 1, 200), (3, 512, 30), (4, 512, 30), (5, 128, 20)])
 def test_config_parity(k, n, steps, oracle):
     s, m, st, cfg = b2.scenes.make_config(k, n)
     rng = np.random.default_rng(5)
@@ -55,7 +55,7 @@ def test_config_parity(k, n, steps, oracle):
 
 
 def test_collide_config2(oracle):
-    """Broadphase + narrowphase only over 4096 worlds: candidate pairs, slots, keys, point
+    """Broadphase + narrowphase only over 4096 worlds (the collide-only workload, seed-1 terrain): candidate pairs, slots, keys, point
     counts and manifolds bit for bit."""
     s, m, st, cfg = b2.scenes.make_config(2)
     dev = b2.layout.to_device(st, "cuda")
@@ -121,3 +121,30 @@ def test_full_size_config4_properties():
     keys = np.where(live, h.contacts.key, -1 - np.arange(live.shape[1])[None, :])
     assert all(len(set(r)) == len(r) for r in keys[:512])
     assert (h.contacts.count[~live] == 0).all()
+
+
+def test_step_returns_new_state(oracle):
+    """step() (the reference signature, step.py:28) leaves its input untouched and returns the stepped copy."""
+    s, m, st, cfg = b2.scenes.make_config(4, 64)
+    dev = b2.layout.to_device(st, "cuda")
+    out = b2.step(m, dev, s, cfg.dt, axis_name="worlds")
+    assert leaf_mismatches(st, b2.layout.to_host(dev)) == []
+    assert leaf_mismatches(oracle.step(m, st, s, cfg.dt), b2.layout.to_host(out)) == []
+
+
+def test_malformed_device_state_is_rejected():
+    """A leaf with the wrong shape, dtype, layout or device never reaches the kernels."""
+    s, m, st, cfg = b2.scenes.make_config(1, 8)
+    dev = b2.layout.to_device(st, "cuda")
+    bad = dev._replace(contacts=dev.contacts._replace(key=dev.contacts.key[:, :16]))
+    with pytest.raises(ValueError):
+        b2.step_(m, bad, s, cfg.dt)
+    bad = dev._replace(bodies=dev.bodies._replace(v=dev.bodies.v.contiguous()))
+    with pytest.raises(ValueError):
+        b2.step_(m, bad, s, cfg.dt)
+    bad = dev._replace(bodies=dev.bodies._replace(w=dev.bodies.w.double()))
+    with pytest.raises(TypeError):
+        b2.step_(m, bad, s, cfg.dt)
+    bad = dev._replace(bodies=dev.bodies._replace(w=dev.bodies.w.cpu()))
+    with pytest.raises(ValueError):
+        b2.step_(m, bad, s, cfg.dt)
