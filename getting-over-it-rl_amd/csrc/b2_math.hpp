@@ -10,6 +10,7 @@
 #include <stdint.h>
 
 #define GOI_D __device__ __forceinline__
+#define GOI_HD __host__ __device__ __forceinline__
 
 namespace goi {
 

@@ -9,19 +9,21 @@ namespace goi {
 // Upper bound on contact slots per world the kernels handle (State capacity C <= kMaxC).
 constexpr int kMaxC = 64;
 
-// Live slots in contact-list order: newest first = descending key (pairs.py:12-13). Insertion into a per-lane
-// array; returns the count.
-GOI_D int list_order(const World& W, int* order) {
+// Live slots in contact-list order: newest first = descending key (pairs.py:12-13), by insertion into the
+// workspace's order array (W.order(0..n-1)); returns the count n.
+GOI_D int list_order(const World& W) {
     int n = 0;
     for (int k = 0; k < W.C; ++k) {
-        if (W.i32(GOI_C_PAIR, k) < 0) continue;
-        const int key = W.i32(GOI_C_KEY, k);
+        if (W.pair(k) < 0) continue;
+        const int key = W.key(k);
         int j = n++;
-        while (j > 0 && W.i32(GOI_C_KEY, order[j - 1]) < key) {
-            order[j] = order[j - 1];
+        while (j > 0) {
+            const int prev = W.order(j - 1);
+            if (!(W.key(prev) < key)) break;
+            W.order(j) = prev;
             --j;
         }
-        order[j] = k;
+        W.order(j) = k;
     }
     return n;
 }
@@ -67,18 +69,17 @@ GOI_D bool contact_update(const World& W, int k, const Manifold& mf) {
 // separated fat AABBs destroy it (waking both bodies if it still had points), the rest updated (waking both bodies
 // when touching flips). Wakes change which later contacts are visited, as in Box2D's walk.
 GOI_D void collide_walk(const DModel& m, const World& W, float linear_slop) {
-    int order[kMaxC];
-    const int n = list_order(W, order);
+    const int n = list_order(W);
     for (int i = 0; i < n; ++i) {
-        const int k = order[i];
-        const int fa = W.i32(GOI_C_FA, k), fb = W.i32(GOI_C_FB, k);
+        const int k = W.order(i);
+        const int fa = W.fa(k), fb = W.fb(k);
         const int ba = m.fixture_body[fa], bb = m.fixture_body[fb];
-        const bool act_a = W.u8(GOI_B_AWAKE, ba) && m.body_type[ba] != GOI_STATIC;
-        const bool act_b = W.u8(GOI_B_AWAKE, bb) && m.body_type[bb] != GOI_STATIC;
+        const bool act_a = W.awake(ba) && m.body_type[ba] != GOI_STATIC;
+        const bool act_b = W.awake(bb) && m.body_type[bb] != GOI_STATIC;
         if (!act_a && !act_b) continue;
         if (!overlap(fat_of(m, W, fa), fat_of(m, W, fb))) {
             if (W.i32(GOI_C_COUNT, k) > 0) { W.wake(ba); W.wake(bb); }
-            W.i32(GOI_C_PAIR, k) = -1;
+            W.pair(k) = -1;
             W.u8(GOI_C_TOUCHING, k) = 0;
             W.i32(GOI_C_COUNT, k) = 0;
             continue;
@@ -89,26 +90,29 @@ GOI_D void collide_walk(const DModel& m, const World& W, float linear_slop) {
     }
 }
 
-// Sorted buffer of the smallest new candidate indices of one FindNewContacts call, plus the count of all of them.
+// Sorted buffer (the workspace's newp array) of the smallest new candidate indices of one FindNewContacts call,
+// plus the count of all of them.
 struct NewPairs {
-    int cand[kMaxC];
+    const World& W;
     int kept, total, cap;
     GOI_D void add(int p) {
         ++total;
-        if (kept == cap && (cap == 0 || cand[kept - 1] < p)) return;
+        if (kept == cap && (cap == 0 || W.newp(kept - 1) < p)) return;
         int j = kept < cap ? kept++ : kept - 1;
-        while (j > 0 && cand[j - 1] > p) {
-            cand[j] = cand[j - 1];
+        while (j > 0) {
+            const int prev = W.newp(j - 1);
+            if (!(prev > p)) break;
+            W.newp(j) = prev;
             --j;
         }
-        cand[j] = p;
+        W.newp(j) = p;
     }
 };
 
 GOI_D bool slot_has_pair(const World& W, int p) {
-    for (int k = 0; k < W.C; ++k)
-        if (W.i32(GOI_C_PAIR, k) == p) return true;
-    return false;
+    bool has = false;
+    for (int k = 0; k < W.C; ++k) has |= W.pair(k) == p;
+    return has;
 }
 
 // b2ContactManager::FindNewContacts (pairs.py:134-178) without scanning the candidate list: each non-static fixture
@@ -119,11 +123,8 @@ GOI_D bool slot_has_pair(const World& W, int p) {
 GOI_D void find_new_contacts(const DModel& m, const World& W) {
     if (m.P == 0) return;
     int n_free = 0;
-    for (int k = 0; k < W.C; ++k) n_free += W.i32(GOI_C_PAIR, k) < 0;
-    NewPairs np;
-    np.kept = 0;
-    np.total = 0;
-    np.cap = n_free;
+    for (int k = 0; k < W.C; ++k) n_free += W.pair(k) < 0;
+    NewPairs np{W, 0, 0, n_free};
     // static x non-static candidates via the BVH
     for (int r = 0; r < m.R; ++r) {
         const int fd = m.slot_fixture[r];
@@ -132,19 +133,20 @@ GOI_D void find_new_contacts(const DModel& m, const World& W) {
         const float4 q = make_float4(W.f(GOI_F_FAT, 4 * r), W.f(GOI_F_FAT, 4 * r + 1), W.f(GOI_F_FAT, 4 * r + 2),
                                      W.f(GOI_F_FAT, 4 * r + 3));
         const bool dyn_d = m.body_type[bd] == GOI_DYNAMIC;
-        int stack[32];
-        int sp = 0;
-        if (m.n_nodes > 0) stack[sp++] = 0;
-        while (sp > 0) {
-            const int nd = stack[--sp];
-            if (!overlap(q, m.node_box[nd])) continue;
-            const int2 ch = m.node_child[nd];
-            if (ch.x >= 0) {
-                stack[sp++] = ch.y;
-                stack[sp++] = ch.x;
+        // stackless preorder walk: descend into an overlapping internal node, else jump past its subtree
+        int nd = 0;
+        while (nd < m.n_nodes) {
+            const int2 ln = m.node_link[nd];
+            if (!overlap(q, m.node_box[nd])) {
+                nd = ln.x;
                 continue;
             }
-            for (int i = ~ch.x, e = ~ch.x + ch.y; i < e; ++i) {
+            if (ln.y < 0) {
+                ++nd;
+                continue;
+            }
+            nd = ln.x;
+            for (int i = ln.y >> 3, e = (ln.y >> 3) + (ln.y & 7); i < e; ++i) {
                 const int fs = m.leaf_fixture[i];
                 const int p = m.cand_static[(size_t)fs * m.R + r];
                 if (p < 0) continue;
@@ -172,13 +174,13 @@ GOI_D void find_new_contacts(const DModel& m, const World& W) {
     const int base_key = W.i32(GOI_S_NEXT_KEY, 0);
     int k = 0;
     for (int i = 0; i < np.kept; ++i) {
-        while (W.i32(GOI_C_PAIR, k) >= 0) ++k;
-        const int p = np.cand[i];
+        while (W.pair(k) >= 0) ++k;
+        const int p = W.newp(i);
         const int a = m.pair_a[p], b = m.pair_b[p];
-        W.i32(GOI_C_PAIR, k) = p;
-        W.i32(GOI_C_FA, k) = a;
-        W.i32(GOI_C_FB, k) = b;
-        W.i32(GOI_C_KEY, k) = base_key + i;
+        W.pair(k) = p;
+        W.fa(k) = a;
+        W.fb(k) = b;
+        W.key(k) = base_key + i;
         W.u8(GOI_C_TOUCHING, k) = 0;
         W.i32(GOI_C_COUNT, k) = 0;
         W.f(GOI_C_NORMAL_IMPULSE, 2 * k) = 0.0f;

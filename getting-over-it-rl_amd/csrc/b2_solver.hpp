@@ -19,7 +19,8 @@ constexpr int kMaxJ = 64;  // joints per world
 struct Bodies {
     float* s;  // LDS base + lane
     int B;
-    GOI_D float& at(int field, int b) const { return s[(field * B + b) * 64]; }
+    int st;    // lanes per block
+    GOI_D float& at(int field, int b) const { return s[(field * B + b) * st]; }
     GOI_D float& vx(int b) const { return at(0, b); }
     GOI_D float& vy(int b) const { return at(1, b); }
     GOI_D float& w(int b) const { return at(2, b); }
@@ -79,49 +80,49 @@ GOI_D V2 rel_vel(V2 vB, float wB, V2 rB, V2 vA, float wA, V2 rA) {
 
 // ---------------------------------------------------------------- islands (island.py:41-140)
 
+// Solve order and island ids, stored in the world's LDS workspace.
 struct Islands {
-    int corder[kMaxC];
-    int jorder[kMaxJ];
-    int body_island[kMaxB];
-    int contact_island[kMaxC];
-    int joint_island[kMaxJ];
+    const World& W;
     int nc, nj, n;
+    GOI_D int& corder(int i) const { return W.corder(i); }
+    GOI_D int& jorder(int i) const { return W.jorder(i); }
+    GOI_D int& body_island(int b) const { return W.bisl(b); }
+    GOI_D int& contact_island(int c) const { return W.cisl(c); }
+    GOI_D int& joint_island(int j) const { return W.jisl(j); }
 };
 
 // b2World::Solve's depth-first search: seeds newest body first; popping b wakes it, walks b's touching contacts
 // newest first (each joins the island and pushes its unvisited non-static other body), then b's joints newest
 // first (joints to inactive bodies skipped). Contacts and joints append to one solve order across islands.
 GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
-    int order[kMaxC];
-    const int n = list_order(W, order);
+    const int n = list_order(W);
     unsigned long long bflag = 0ull, cflag = 0ull, jflag = 0ull;
-    for (int b = 0; b < W.B; ++b) I.body_island[b] = -1;
-    for (int c = 0; c < W.C; ++c) I.contact_island[c] = -1;
-    for (int j = 0; j < W.J; ++j) I.joint_island[j] = -1;
+    for (int b = 0; b < W.B; ++b) I.body_island(b) = -1;
+    for (int c = 0; c < W.C; ++c) I.contact_island(c) = -1;
+    for (int j = 0; j < W.J; ++j) I.joint_island(j) = -1;
     int nisl = 0, nc = 0, nj = 0;
-    int stack[kMaxB];
     for (int seed = W.B - 1; seed >= 0; --seed) {
         if ((bflag >> seed) & 1ull) continue;
-        if (!W.u8(GOI_B_AWAKE, seed) || !W.u8(GOI_B_ACTIVE, seed) || m.body_type[seed] == GOI_STATIC) continue;
+        if (!W.awake(seed) || !W.u8(GOI_B_ACTIVE, seed) || m.body_type[seed] == GOI_STATIC) continue;
         const int isl = nisl++;
         int sp = 0;
-        stack[sp++] = seed;
+        W.stack(sp++) = seed;
         bflag |= 1ull << seed;
         while (sp > 0) {
-            const int b = stack[--sp];
-            I.body_island[b] = isl;
+            const int b = W.stack(--sp);
+            I.body_island(b) = isl;
             W.wake(b);
             for (int i = 0; i < n; ++i) {
-                const int c = order[i];
-                const int ba = m.fixture_body[W.i32(GOI_C_FA, c)], bb = m.fixture_body[W.i32(GOI_C_FB, c)];
+                const int c = W.order(i);
+                const int ba = m.fixture_body[W.fa(c)], bb = m.fixture_body[W.fb(c)];
                 if (ba != b && bb != b) continue;
                 if (((cflag >> c) & 1ull) || !W.u8(GOI_C_TOUCHING, c)) continue;
-                I.corder[nc++] = c;
+                I.corder(nc++) = c;
                 cflag |= 1ull << c;
-                I.contact_island[c] = isl;
+                I.contact_island(c) = isl;
                 const int other = ba == b ? bb : ba;
                 if (((bflag >> other) & 1ull) || m.body_type[other] == GOI_STATIC) continue;
-                stack[sp++] = other;
+                W.stack(sp++) = other;
                 bflag |= 1ull << other;
             }
             for (int j = W.J - 1; j >= 0; --j) {
@@ -130,11 +131,11 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
                 if ((jflag >> j) & 1ull) continue;
                 const int other = ja == b ? jb : ja;
                 if (!W.u8(GOI_B_ACTIVE, other)) continue;
-                I.jorder[nj++] = j;
+                I.jorder(nj++) = j;
                 jflag |= 1ull << j;
-                I.joint_island[j] = isl;
+                I.joint_island(j) = isl;
                 if (((bflag >> other) & 1ull) || m.body_type[other] == GOI_STATIC) continue;
-                stack[sp++] = other;
+                W.stack(sp++) = other;
                 bflag |= 1ull << other;
             }
         }
@@ -150,7 +151,7 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
 // (contact_solver.py:32-147). Body positions/velocities from the LDS arrays; qA/qB the bodies' rotations.
 GOI_D void cs_prepare(const DModel& m, const World& W, const Bodies& bd, const Rows& R, int i, int slot, bool warm,
                       float dt_ratio, Rot qA, Rot qB, float velocity_threshold) {
-    const int fa = W.i32(GOI_C_FA, slot), fb = W.i32(GOI_C_FB, slot);
+    const int fa = W.fa(slot), fb = W.fb(slot);
     const int ia = m.fixture_body[fa], ib = m.fixture_body[fb];
     const float mA = W.f(GOI_B_INV_MASS, ia), mB = W.f(GOI_B_INV_MASS, ib);
     const float iA = W.f(GOI_B_INV_INERTIA, ia), iB = W.f(GOI_B_INV_INERTIA, ib);

@@ -11,7 +11,7 @@ namespace goi {
 GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const Rows& JRw,
                             const GoiSettings& s, float dt, const GoiDebug& dbg) {
     const float dt_ratio = W.f(GOI_S_INV_DT0, 0) * dt;
-    Islands I;
+    Islands I{W, 0, 0, 0};
     find_islands(m, W, I);
     const float h = dt;
     const float gx = W.f(GOI_S_GRAVITY, 0), gy = W.f(GOI_S_GRAVITY, 1);
@@ -21,7 +21,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         float w = W.f(GOI_B_W, b);
         const V2 c = W.v2(GOI_B_C, b);
         const float a = W.f(GOI_B_A, b);
-        if (I.body_island[b] >= 0) {
+        if (I.body_island(b) >= 0) {
             if (m.body_type[b] == GOI_DYNAMIC) {
                 const float gs = W.f(GOI_B_GRAVITY_SCALE, b), im = W.f(GOI_B_INV_MASS, b);
                 const float ax = gs * gx + im * W.f(GOI_B_FORCE, 2 * b);
@@ -45,8 +45,8 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     const bool warm = s.warm_starting != 0;
     const bool v24 = s.revolute_v24 != 0;
     for (int i = 0; i < I.nc; ++i) {
-        const int slot = I.corder[i];
-        const int ia = m.fixture_body[W.i32(GOI_C_FA, slot)], ib = m.fixture_body[W.i32(GOI_C_FB, slot)];
+        const int slot = I.corder(i);
+        const int ia = m.fixture_body[W.fa(slot)], ib = m.fixture_body[W.fb(slot)];
         Rot qA, qB;
         qA.c = bd.at(6, ia); qA.s = bd.at(7, ia);
         qB.c = bd.at(6, ib); qB.s = bd.at(7, ib);
@@ -55,7 +55,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     if (warm)
         for (int i = 0; i < I.nc; ++i) cs_warm_start(bd, CR, i);
     for (int i = 0; i < I.nj; ++i) {
-        const int jid = I.jorder[i];
+        const int jid = I.jorder(i);
         const int ia = m.joint_a[jid], ib = m.joint_b[jid];
         Rot qA, qB;
         qA.c = bd.at(6, ia); qA.s = bd.at(7, ia);
@@ -84,7 +84,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     const float max_t = s.clamps_per_second ? s.max_translation * h : s.max_translation;
     const float max_r = s.clamps_per_second ? s.max_rotation * h : s.max_rotation;
     for (int b = 0; b < W.B; ++b) {
-        if (I.body_island[b] < 0) continue;
+        if (I.body_island(b) < 0) continue;
         V2 v = bd.v(b);
         float w = bd.w(b);
         const V2 t = h * v;
@@ -100,29 +100,28 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     // position iterations with per-island early exit (step.py:197-251)
     unsigned long long done = 0ull, all = I.n >= 64 ? ~0ull : ((1ull << I.n) - 1ull);
     for (int it = 0; it < s.position_iterations && done != all; ++it) {
-        float min_sep[kMaxB];
         unsigned long long jbad = 0ull;
-        for (int i = 0; i < I.n; ++i) min_sep[i] = 0.0f;
+        for (int i = 0; i < I.n; ++i) W.fwork(i) = 0.0f;  // min separation per island
         for (int i = 0; i < I.nc; ++i) {
-            const int isl = I.contact_island[CR.geti(i, CF_SLOT)];
+            const int isl = I.contact_island(CR.geti(i, CF_SLOT));
             if ((done >> isl) & 1ull) continue;
             const float ms = cs_solve_position(bd, CR, i, s.baumgarte, CR.getf(i, CF_MA), CR.getf(i, CF_MB),
                                                CR.getf(i, CF_IIA), CR.getf(i, CF_IIB), s.linear_slop,
                                                s.max_linear_correction);
-            min_sep[isl] = bmin(min_sep[isl], ms);
+            W.fwork(isl) = bmin(W.fwork(isl), ms);
         }
         for (int i = 0; i < I.nj; ++i) {
-            const int isl = I.joint_island[JRw.geti(i, JF_JID)];
+            const int isl = I.joint_island(JRw.geti(i, JF_JID));
             if ((done >> isl) & 1ull) continue;
             if (!jn_solve_position(bd, JRw, i, s)) jbad |= 1ull << isl;
         }
         const float okay_sep = -3.0f * s.linear_slop;
         for (int i = 0; i < I.n; ++i)
-            if (!((done >> i) & 1ull) && min_sep[i] >= okay_sep && !((jbad >> i) & 1ull)) done |= 1ull << i;
+            if (!((done >> i) & 1ull) && W.fwork(i) >= okay_sep && !((jbad >> i) & 1ull)) done |= 1ull << i;
     }
     // write back + SynchronizeTransform
     for (int b = 0; b < W.B; ++b) {
-        if (I.body_island[b] < 0) continue;
+        if (I.body_island(b) < 0) continue;
         const V2 c = bd.c(b);
         const float a = bd.a(b);
         W.set2(GOI_B_C, b, c);
@@ -139,30 +138,29 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     if (s.allow_sleep) {
         const float lin_tol = s.linear_sleep_tolerance * s.linear_sleep_tolerance;
         const float ang_tol = s.angular_sleep_tolerance * s.angular_sleep_tolerance;
-        float min_st[kMaxB];
-        for (int i = 0; i < I.n; ++i) min_st[i] = kMaxFloat;
+        for (int i = 0; i < I.n; ++i) W.fwork(i) = kMaxFloat;  // min sleep time per island
         for (int b = 0; b < W.B; ++b) {
-            const int isl = I.body_island[b];
+            const int isl = I.body_island(b);
             if (isl < 0 || m.body_type[b] == GOI_STATIC) continue;
             const V2 v = W.v2(GOI_B_V, b);
             const float w = W.f(GOI_B_W, b);
             const bool moving = !W.u8(GOI_B_ALLOW_SLEEP, b) || w * w > ang_tol || dot(v, v) > lin_tol;
             if (moving) {
                 W.f(GOI_B_SLEEP_TIME, b) = 0.0f;
-                min_st[isl] = 0.0f;
+                W.fwork(isl) = 0.0f;
             } else {
                 const float st = W.f(GOI_B_SLEEP_TIME, b) + h;
                 W.f(GOI_B_SLEEP_TIME, b) = st;
-                min_st[isl] = bmin(min_st[isl], st);
+                W.fwork(isl) = bmin(W.fwork(isl), st);
             }
         }
         for (int i = 0; i < I.n; ++i)
-            if (min_st[i] >= s.time_to_sleep && ((done >> i) & 1ull)) isl_sleep |= 1ull << i;
+            if (W.fwork(i) >= s.time_to_sleep && ((done >> i) & 1ull)) isl_sleep |= 1ull << i;
         for (int b = 0; b < W.B; ++b) {
-            const int isl = I.body_island[b];
+            const int isl = I.body_island(b);
             if (isl < 0 || m.body_type[b] == GOI_STATIC || !((isl_sleep >> isl) & 1ull)) continue;
             W.f(GOI_B_SLEEP_TIME, b) = 0.0f;
-            W.u8(GOI_B_AWAKE, b) = 0;
+            W.awake(b) = 0;
             W.set2(GOI_B_V, b, mk(0.0f, 0.0f));
             W.f(GOI_B_W, b) = 0.0f;
             W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
@@ -174,28 +172,28 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         if (m.body_type[b] != GOI_STATIC) continue;
         int last = -1;
         for (int c = 0; c < W.C; ++c) {
-            const int isl = I.contact_island[c];
+            const int isl = I.contact_island(c);
             if (isl < 0) continue;
-            if (m.fixture_body[W.i32(GOI_C_FA, c)] == b || m.fixture_body[W.i32(GOI_C_FB, c)] == b) last = max(last, isl);
+            if (m.fixture_body[W.fa(c)] == b || m.fixture_body[W.fb(c)] == b) last = max(last, isl);
         }
         for (int j = 0; j < W.J; ++j) {
-            const int isl = I.joint_island[j];
+            const int isl = I.joint_island(j);
             if (isl >= 0 && (m.joint_a[j] == b || m.joint_b[j] == b)) last = max(last, isl);
         }
         if (last < 0) continue;
-        W.u8(GOI_B_AWAKE, b) = !((isl_sleep >> last) & 1ull);
+        W.awake(b) = !((isl_sleep >> last) & 1ull);
         W.f(GOI_B_SLEEP_TIME, b) = 0.0f;
     }
     if (dbg.body_island)
-        for (int b = 0; b < W.B; ++b) dbg.body_island[(size_t)b * W.pitch + W.w] = I.body_island[b];
+        for (int b = 0; b < W.B; ++b) dbg.body_island[(size_t)b * W.pitch + W.w] = I.body_island(b);
     if (dbg.contact_island)
-        for (int c = 0; c < W.C; ++c) dbg.contact_island[(size_t)c * W.pitch + W.w] = I.contact_island[c];
+        for (int c = 0; c < W.C; ++c) dbg.contact_island[(size_t)c * W.pitch + W.w] = I.contact_island(c);
     if (dbg.contact_order)
-        for (int c = 0; c < W.C; ++c) dbg.contact_order[(size_t)c * W.pitch + W.w] = c < I.nc ? I.corder[c] : -1;
+        for (int c = 0; c < W.C; ++c) dbg.contact_order[(size_t)c * W.pitch + W.w] = c < I.nc ? I.corder(c) : -1;
     if (dbg.n_islands) dbg.n_islands[W.w] = I.n;
     // SynchronizeFixtures of the non-static island bodies, then FindNewContacts
     for (int b = 0; b < W.B; ++b) {
-        if (I.body_island[b] < 0 || m.body_type[b] == GOI_STATIC) continue;
+        if (I.body_island(b) < 0 || m.body_type[b] == GOI_STATIC) continue;
         sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
     }
     find_new_contacts(m, W);
@@ -215,21 +213,20 @@ GOI_D bool pair_rule(const DModel& m, const World& W, const GoiSettings& s, int 
 
 // the min-TOI search (toi.py:488-558); returns whether an event was found
 GOI_D bool toi_search(const DModel& m, const World& W, const GoiSettings& s, int& min_slot, float& min_alpha) {
-    int order[kMaxC];
-    const int n = list_order(W, order);
+    const int n = list_order(W);
     int best = -1;
     float best_alpha = 1.0f;
     for (int i = 0; i < n; ++i) {
-        const int c = order[i];
-        if (!W.u8(GOI_T_ENABLED, c) || W.i32(GOI_T_COUNT, c) > kMaxSubSteps) continue;
+        const int c = W.order(i);
+        if (!W.ten(c) || W.tcount(c) > kMaxSubSteps) continue;
         float alpha;
-        if (W.u8(GOI_T_FLAG, c)) {
-            alpha = W.f(GOI_T_TOI, c);
+        if (W.tflag(c)) {
+            alpha = W.ttoi(c);
         } else {
-            const int fa = W.i32(GOI_C_FA, c), fb = W.i32(GOI_C_FB, c);
+            const int fa = W.fa(c), fb = W.fb(c);
             const int A = m.fixture_body[fa], Bb = m.fixture_body[fb];
-            const bool act_a = W.u8(GOI_B_AWAKE, A) && m.body_type[A] != GOI_STATIC;
-            const bool act_b = W.u8(GOI_B_AWAKE, Bb) && m.body_type[Bb] != GOI_STATIC;
+            const bool act_a = W.awake(A) && m.body_type[A] != GOI_STATIC;
+            const bool act_b = W.awake(Bb) && m.body_type[Bb] != GOI_STATIC;
             if (!act_a && !act_b) continue;
             if (!pair_rule(m, W, s, A, Bb)) continue;
             const float alA = W.f(GOI_T_ALPHA0, A), alB = W.f(GOI_T_ALPHA0, Bb);
@@ -240,8 +237,8 @@ GOI_D bool toi_search(const DModel& m, const World& W, const GoiSettings& s, int
             const int st = time_of_impact(proxy_of(m, fa), body_sweep(W, A), proxy_of(m, fb), body_sweep(W, Bb),
                                           s.linear_slop, beta);
             alpha = st == kToiTouching ? bmin(alpha0 + (1.0f - alpha0) * beta, 1.0f) : 1.0f;
-            W.f(GOI_T_TOI, c) = alpha;
-            W.u8(GOI_T_FLAG, c) = 1;
+            W.ttoi(c) = alpha;
+            W.tflag(c) = 1;
         }
         if (alpha < 1.0f && (s.toi_tie_oldest ? alpha <= best_alpha : alpha < best_alpha)) {
             best = c;
@@ -256,7 +253,7 @@ GOI_D bool toi_search(const DModel& m, const World& W, const GoiSettings& s, int
 
 // position-constraint fields of contact slot `slot` into row i (the TOI island's b2ContactPositionConstraint)
 GOI_D void cs_position_row(const DModel& m, const World& W, const Rows& R, int i, int slot) {
-    const int fa = W.i32(GOI_C_FA, slot), fb = W.i32(GOI_C_FB, slot);
+    const int fa = W.fa(slot), fb = W.fb(slot);
     const int ia = m.fixture_body[fa], ib = m.fixture_body[fb];
     R.seti(i, CF_SLOT, slot); R.seti(i, CF_IA, ia); R.seti(i, CF_IB, ib);
     R.seti(i, CF_PC_COUNT, W.i32(GOI_C_COUNT, slot)); R.seti(i, CF_MTYPE, W.i32(GOI_C_MTYPE, slot));
@@ -269,7 +266,7 @@ GOI_D void cs_position_row(const DModel& m, const World& W, const Rows& R, int i
 // one TOI event (toi.py:604-716) on min_slot at min_alpha
 GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
                           float dt, int min_slot, float min_alpha) {
-    const int fa = W.i32(GOI_C_FA, min_slot), fb = W.i32(GOI_C_FB, min_slot);
+    const int fa = W.fa(min_slot), fb = W.fb(min_slot);
     const int A = m.fixture_body[fa], Bb = m.fixture_body[fb];
     const SweepBackup bkA = backup(W, A), bkB = backup(W, Bb);
     body_advance(W, A, min_alpha);
@@ -279,32 +276,31 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         evaluate(m, fa, fb, W.xf(A), W.xf(Bb), s.linear_slop, mf);
         if (contact_update(W, min_slot, mf)) { W.wake(A); W.wake(Bb); }
     }
-    W.u8(GOI_T_FLAG, min_slot) = 0;
-    W.i32(GOI_T_COUNT, min_slot) += 1;
+    W.tflag(min_slot) = 0;
+    W.tcount(min_slot) += 1;
     if (!W.u8(GOI_C_TOUCHING, min_slot)) {
-        W.u8(GOI_T_ENABLED, min_slot) = 0;
+        W.ten(min_slot) = 0;
         restore(W, A, bkA);
         restore(W, Bb, bkB);
         return;
     }
-    W.u8(GOI_T_ENABLED, min_slot) = 1;
+    W.ten(min_slot) = 1;
     W.wake(A);
     W.wake(Bb);
-    // the island walk: bodyA's then bodyB's contact lists, newest first, at most 32 contacts / 64 bodies
-    int isl_b[2 * kMaxToiContacts];
+    // the island walk: bodyA's then bodyB's contact lists, newest first, at most 32 contacts / 64 bodies; island
+    // bodies (distinct, so at most B) in the workspace's ibuf
     int nb = 0, nc = 0;
     unsigned long long bflag = (1ull << A) | (1ull << Bb), cflag = 1ull << min_slot;
-    isl_b[nb++] = A;
-    isl_b[nb++] = Bb;
+    W.ibuf(nb++) = A;
+    W.ibuf(nb++) = Bb;
     cs_position_row(m, W, CR, nc++, min_slot);
-    int order[kMaxC];
-    const int n = list_order(W, order);
+    const int n = list_order(W);
     for (int pi = 0; pi < 2; ++pi) {
         const int body = pi == 0 ? A : Bb;
         if (m.body_type[body] != GOI_DYNAMIC) continue;
         for (int i = 0; i < n; ++i) {
-            const int c = order[i];
-            const int ca = m.fixture_body[W.i32(GOI_C_FA, c)], cb = m.fixture_body[W.i32(GOI_C_FB, c)];
+            const int c = W.order(i);
+            const int ca = m.fixture_body[W.fa(c)], cb = m.fixture_body[W.fb(c)];
             if (ca != body && cb != body) continue;
             if (nb == 2 * kMaxToiContacts || nc == kMaxToiContacts) break;
             if ((cflag >> c) & 1ull) continue;
@@ -314,9 +310,9 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
             const SweepBackup bk = backup(W, other);
             if (!((bflag >> other) & 1ull)) body_advance(W, other, min_alpha);
             Manifold mf;
-            evaluate(m, W.i32(GOI_C_FA, c), W.i32(GOI_C_FB, c), W.xf(ca), W.xf(cb), s.linear_slop, mf);
+            evaluate(m, W.fa(c), W.fb(c), W.xf(ca), W.xf(cb), s.linear_slop, mf);
             if (contact_update(W, c, mf)) { W.wake(ca); W.wake(cb); }
-            W.u8(GOI_T_ENABLED, c) = 1;
+            W.ten(c) = 1;
             if (!W.u8(GOI_C_TOUCHING, c)) {
                 restore(W, other, bk);
                 continue;
@@ -326,12 +322,12 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
             if ((bflag >> other) & 1ull) continue;
             bflag |= 1ull << other;
             if (m.body_type[other] != GOI_STATIC) W.wake(other);
-            isl_b[nb++] = other;
+            W.ibuf(nb++) = other;
         }
     }
     // b2Island::SolveTOI (toi.py:719-799)
     for (int i = 0; i < nb; ++i) {
-        const int b = isl_b[i];
+        const int b = W.ibuf(i);
         bd.set_c(b, W.v2(GOI_B_C, b), W.f(GOI_B_A, b));
         bd.set_v(b, W.v2(GOI_B_V, b), W.f(GOI_B_W, b));
     }
@@ -363,7 +359,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     const float max_t = s.clamps_per_second ? s.max_translation * dt : s.max_translation;
     const float max_r = s.clamps_per_second ? s.max_rotation * dt : s.max_rotation;
     for (int i = 0; i < nb; ++i) {
-        const int b = isl_b[i];
+        const int b = W.ibuf(i);
         V2 v = bd.v(b);
         float w = bd.w(b);
         const V2 t = h * v;
@@ -391,29 +387,29 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     // fixture sync of the island's dynamic bodies and TOI invalidation of their contacts
     unsigned long long moved = 0ull;
     for (int i = 0; i < nb; ++i) {
-        const int b = isl_b[i];
+        const int b = W.ibuf(i);
         if (m.body_type[b] != GOI_DYNAMIC) continue;
         moved |= 1ull << b;
         sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
     }
     for (int c = 0; c < W.C; ++c) {
-        if (W.i32(GOI_C_PAIR, c) < 0) continue;
-        const int ca = m.fixture_body[W.i32(GOI_C_FA, c)], cb = m.fixture_body[W.i32(GOI_C_FB, c)];
-        if (((moved >> ca) & 1ull) || ((moved >> cb) & 1ull)) W.u8(GOI_T_FLAG, c) = 0;
+        if (W.pair(c) < 0) continue;
+        const int ca = m.fixture_body[W.fa(c)], cb = m.fixture_body[W.fb(c)];
+        if (((moved >> ca) & 1ull) || ((moved >> cb) & 1ull)) W.tflag(c) = 0;
     }
-    // FindNewContacts; a slot that received a new contact starts with fresh TOI state
+    // FindNewContacts; a slot that received a new contact starts with fresh TOI state. The keys before it go to
+    // the workspace's corder array, which Solve's island order no longer needs.
     unsigned long long was_free = 0ull;
-    int old_key[kMaxC];
     for (int c = 0; c < W.C; ++c) {
-        if (W.i32(GOI_C_PAIR, c) < 0) was_free |= 1ull << c;
-        old_key[c] = W.i32(GOI_C_KEY, c);
+        if (W.pair(c) < 0) was_free |= 1ull << c;
+        W.corder(c) = W.key(c);
     }
     find_new_contacts(m, W);
     for (int c = 0; c < W.C; ++c) {
-        if (W.i32(GOI_C_PAIR, c) >= 0 && (((was_free >> c) & 1ull) || old_key[c] != W.i32(GOI_C_KEY, c))) {
-            W.i32(GOI_T_COUNT, c) = 0;
-            W.u8(GOI_T_FLAG, c) = 0;
-            W.u8(GOI_T_ENABLED, c) = 1;
+        if (W.pair(c) >= 0 && (((was_free >> c) & 1ull) || W.corder(c) != W.key(c))) {
+            W.tcount(c) = 0;
+            W.tflag(c) = 0;
+            W.ten(c) = 1;
         }
     }
 }
@@ -424,10 +420,10 @@ GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, co
     if (s.unity_toi && !m.any_toi_body) return;
     for (int b = 0; b < W.B; ++b) W.f(GOI_T_ALPHA0, b) = 0.0f;
     for (int c = 0; c < W.C; ++c) {
-        W.i32(GOI_T_COUNT, c) = 0;
-        W.f(GOI_T_TOI, c) = 1.0f;
-        W.u8(GOI_T_FLAG, c) = 0;
-        W.u8(GOI_T_ENABLED, c) = 1;
+        W.tcount(c) = 0;
+        W.ttoi(c) = 1.0f;
+        W.tflag(c) = 0;
+        W.ten(c) = 1;
         W.u8(GOI_T_SOLVED, c) = 0;
         W.f(GOI_T_NORMAL_IMPULSE, 2 * c) = 0.0f;
         W.f(GOI_T_NORMAL_IMPULSE, 2 * c + 1) = 0.0f;
@@ -435,18 +431,20 @@ GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, co
         W.f(GOI_T_TANGENT_IMPULSE, 2 * c + 1) = 0.0f;
     }
     W.i32(GOI_T_EVENTS, 0) = 0;
-    if (!(dt > 0.0f)) return;
-    const int max_events = s.max_events >= 0 ? s.max_events : W.C * (kMaxSubSteps + 1) + 8;
-    int slot;
-    float alpha;
-    int events = 0;
-    bool found = toi_search(m, W, s, slot, alpha);
-    while (found && events < max_events) {
-        toi_event(m, W, bd, CR, s, dt, slot, alpha);
-        ++events;
+    if (dt > 0.0f) {
+        const int max_events = s.max_events >= 0 ? s.max_events : W.C * (kMaxSubSteps + 1) + 8;
+        int slot;
+        float alpha;
+        int events = 0;
+        bool found = toi_search(m, W, s, slot, alpha);
+        while (found && events < max_events) {
+            toi_event(m, W, bd, CR, s, dt, slot, alpha);
+            ++events;
+            found = toi_search(m, W, s, slot, alpha);
+        }
         W.i32(GOI_T_EVENTS, 0) = events;
-        found = toi_search(m, W, s, slot, alpha);
     }
+    W.store_toi();
 }
 
 }  // namespace goi

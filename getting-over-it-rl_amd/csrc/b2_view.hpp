@@ -36,23 +36,76 @@ struct DModel {
     const float* static_restitution;
     const int* body_type;       // [B]
     int any_toi_body;           // Model.toi_bodies has a set entry (or is absent)
-    // Static BVH over the static fixtures' fat AABBs (node 0 = root). Internal node: child[0], child[1] >= 0.
-    // Leaf: child[0] = ~first (index into leaf_fixture), child[1] = count.
+    // Static BVH over the static fixtures' fat AABBs, nodes in preorder (node 0 = root, a node's first child is the
+    // next node). node_link.x = escape: the node after this node's subtree; node_link.y = -1 for an internal node,
+    // (first << 3) | count for a leaf of `count` (<= 4) entries of leaf_fixture starting at `first`.
     int n_nodes;
     const float4* node_box;     // [n_nodes] lx ly ux uy
-    const int2* node_child;     // [n_nodes]
+    const int2* node_link;      // [n_nodes]
     const int* leaf_fixture;    // static fixture ids in leaf order
     const int* cand_static;     // [F * R]: candidate index of (static fixture f, row r), -1 if none
     int n_dd;                   // candidates whose fixtures are both non-static
     const int* dd_cand;         // [n_dd] candidate indices (ascending)
 };
 
-// One world's State: leaf pointers already offset by the lane's world index.
+// Per-lane workspace in LDS. Every array is [index][lane] with the block's lane count as stride: lane l's element
+// i of an array at offset o sits at base[(o + i) * S + l], so one index across a wavefront is consecutive words.
+// It mirrors the per-world contact metadata (pair, key, fixtures), the awake flags and the TOI bookkeeping for the
+// whole step (loaded once, written back once) and holds the per-world work arrays (contact list order, island
+// lists and stacks, new-pair buffer), which would otherwise live in private scratch memory.
+struct Workspace {
+    int o_pair, o_key, o_fa, o_fb, o_tflag, o_ten, o_tcount, o_ttoi, o_order, o_newp, o_corder, o_cisl;  // [C]
+    int o_awake, o_bisl, o_stack, o_fwork, o_ibuf;                                                      // [B]
+    int o_jorder, o_jisl;                                                                               // [J]
+    int o_body;  // 8 solver body fields x B
+    int words;   // per lane
+    GOI_HD static Workspace layout(int B, int C, int J) {
+        Workspace k;
+        int o = 0;
+        k.o_body = o; o += 8 * B;
+        k.o_pair = o; o += C; k.o_key = o; o += C; k.o_fa = o; o += C; k.o_fb = o; o += C;
+        k.o_tflag = o; o += C; k.o_ten = o; o += C; k.o_tcount = o; o += C; k.o_ttoi = o; o += C;
+        k.o_order = o; o += C; k.o_newp = o; o += C; k.o_corder = o; o += C; k.o_cisl = o; o += C;
+        k.o_awake = o; o += B; k.o_bisl = o; o += B; k.o_stack = o; o += B; k.o_fwork = o; o += B; k.o_ibuf = o; o += B;
+        k.o_jorder = o; o += J; k.o_jisl = o; o += J;
+        k.words = o;
+        return k;
+    }
+};
+
+// One world's State: leaf pointers already offset by the lane's world index, plus the lane's LDS workspace.
 struct World {
     int pitch;
     int B, C, R, J;
     void* const* lv;  // leaf base pointers (kernel argument block)
     int w;
+    int* ws;          // LDS workspace base + lane
+    int S;            // workspace stride (lanes per block)
+    Workspace k;
+
+    GOI_D int& wi(int off, int i) const { return ws[(off + i) * S]; }
+    GOI_D float& wf(int off, int i) const { return reinterpret_cast<float*>(ws)[(off + i) * S]; }
+    // mirrored State leaves
+    GOI_D int& pair(int c) const { return wi(k.o_pair, c); }      // contacts.pair
+    GOI_D int& key(int c) const { return wi(k.o_key, c); }        // contacts.key
+    GOI_D int& fa(int c) const { return wi(k.o_fa, c); }          // contacts.fa
+    GOI_D int& fb(int c) const { return wi(k.o_fb, c); }          // contacts.fb
+    GOI_D int& awake(int b) const { return wi(k.o_awake, b); }    // bodies.awake
+    GOI_D int& tflag(int c) const { return wi(k.o_tflag, c); }    // toi.flag
+    GOI_D int& ten(int c) const { return wi(k.o_ten, c); }        // toi.enabled
+    GOI_D int& tcount(int c) const { return wi(k.o_tcount, c); }  // toi.count
+    GOI_D float& ttoi(int c) const { return wf(k.o_ttoi, c); }    // toi.toi
+    // work arrays
+    GOI_D int& order(int i) const { return wi(k.o_order, i); }
+    GOI_D int& newp(int i) const { return wi(k.o_newp, i); }
+    GOI_D int& corder(int i) const { return wi(k.o_corder, i); }
+    GOI_D int& cisl(int c) const { return wi(k.o_cisl, c); }
+    GOI_D int& bisl(int b) const { return wi(k.o_bisl, b); }
+    GOI_D int& stack(int i) const { return wi(k.o_stack, i); }
+    GOI_D float& fwork(int i) const { return wf(k.o_fwork, i); }
+    GOI_D int& ibuf(int i) const { return wi(k.o_ibuf, i); }
+    GOI_D int& jorder(int i) const { return wi(k.o_jorder, i); }
+    GOI_D int& jisl(int j) const { return wi(k.o_jisl, j); }
 
     template <typename T>
     GOI_D T& at(int leaf, int i) const {
@@ -75,9 +128,37 @@ struct World {
     }
     // b2Body::SetAwake(true): the sleep timer restarts only if the body was asleep
     GOI_D void wake(int b) const {
-        if (!u8(GOI_B_AWAKE, b)) {
-            u8(GOI_B_AWAKE, b) = 1;
+        if (!awake(b)) {
+            awake(b) = 1;
             f(GOI_B_SLEEP_TIME, b) = 0.0f;
+        }
+    }
+    // the mirrored leaves from the State into the workspace (contact metadata, awake flags)
+    GOI_D void load_mirror() const {
+        for (int c = 0; c < C; ++c) {
+            pair(c) = i32(GOI_C_PAIR, c);
+            key(c) = i32(GOI_C_KEY, c);
+            fa(c) = i32(GOI_C_FA, c);
+            fb(c) = i32(GOI_C_FB, c);
+        }
+        for (int b = 0; b < B; ++b) awake(b) = u8(GOI_B_AWAKE, b);
+    }
+    GOI_D void store_mirror() const {
+        for (int c = 0; c < C; ++c) {
+            i32(GOI_C_PAIR, c) = pair(c);
+            i32(GOI_C_KEY, c) = key(c);
+            i32(GOI_C_FA, c) = fa(c);
+            i32(GOI_C_FB, c) = fb(c);
+        }
+        for (int b = 0; b < B; ++b) u8(GOI_B_AWAKE, b) = (uint8_t)awake(b);
+    }
+    // the TOI bookkeeping (written by SolveTOI only)
+    GOI_D void store_toi() const {
+        for (int c = 0; c < C; ++c) {
+            u8(GOI_T_FLAG, c) = (uint8_t)tflag(c);
+            u8(GOI_T_ENABLED, c) = (uint8_t)ten(c);
+            i32(GOI_T_COUNT, c) = tcount(c);
+            f(GOI_T_TOI, c) = ttoi(c);
         }
     }
     GOI_D int body_of(const DModel& m, int fixture) const { return m.fixture_body[fixture]; }

@@ -39,7 +39,6 @@ int fail(int code, const std::string& msg) {
     } while (0)
 
 constexpr int kBlock = 64;
-constexpr int kBodyFields = 8;  // vx vy w cx cy a qc qs
 
 struct Launch {
     void* leaf[GOI_NUM_LEAVES];
@@ -51,7 +50,8 @@ struct Launch {
     GoiDebug dbg;
 };
 
-__device__ __forceinline__ World make_world(const Launch& L, int w) {
+// World w on lane `lane` of its block; the block's LDS workspace holds L.wpw lanes.
+__device__ __forceinline__ World make_world(const Launch& L, int w, int* lds, int lane) {
     World W;
     W.pitch = L.pitch;
     W.B = L.B;
@@ -60,6 +60,9 @@ __device__ __forceinline__ World make_world(const Launch& L, int w) {
     W.J = L.J;
     W.lv = L.leaf;
     W.w = w;
+    W.k = Workspace::layout(L.B, L.C, L.J);
+    W.ws = lds + lane;
+    W.S = L.wpw;
     return W;
 }
 
@@ -83,27 +86,32 @@ __device__ __forceinline__ Rows joint_rows(const Launch& L, int w) {
 // ---------------------------------------------------------------- kernels
 
 __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int start_only) {
+    extern __shared__ int lds[];
     const int w = blockIdx.x * L.wpw + threadIdx.x;
     if ((int)threadIdx.x >= L.wpw || w >= L.n) return;
-    const World W = make_world(L, w);
+    const World W = make_world(L, w, lds, threadIdx.x);
+    W.load_mirror();
     if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
     W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     if (!start_only) collide_walk(m, W, L.s.linear_slop);
+    W.store_mirror();
 }
 
 // The whole b2World::Step (step.py:28-47) of one world per lane: FindNewContacts where new_fixture, Collide,
 // Solve, SolveTOI, inv_dt0, ClearForces.
 __global__ void __launch_bounds__(kBlock) k_step(DModel m, Launch L) {
-    extern __shared__ float lds[];
+    extern __shared__ int lds[];
     const int w = blockIdx.x * L.wpw + threadIdx.x;
     if ((int)threadIdx.x >= L.wpw || w >= L.n) return;
-    const World W = make_world(L, w);
+    const World W = make_world(L, w, lds, threadIdx.x);
+    W.load_mirror();
     if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
     W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     collide_walk(m, W, L.s.linear_slop);
     Bodies bd;
-    bd.s = lds + threadIdx.x;
+    bd.s = reinterpret_cast<float*>(lds) + W.k.o_body * W.S + threadIdx.x;
     bd.B = L.B;
+    bd.st = W.S;
     const Rows CR = contact_rows(L, w);
     solve_world(m, W, bd, CR, joint_rows(L, w), L.s, L.dt, L.dbg);
     if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt);
@@ -114,6 +122,7 @@ __global__ void __launch_bounds__(kBlock) k_step(DModel m, Launch L) {
             W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
             W.f(GOI_B_TORQUE, b) = 0.0f;
         }
+    W.store_mirror();
 }
 
 __global__ void k_sincos(const float* x, float* s, float* c, int n) {
@@ -157,7 +166,7 @@ struct BvhBuild {
     const float* fat;  // [F, 4]
     std::vector<int> leaf;
     std::vector<float4> box;
-    std::vector<int2> child;
+    std::vector<int2> link;  // (escape, -1) internal; (escape, first << 3 | count) leaf
     int max_depth = 0;
 
     float4 bounds(int lo, int hi) const {
@@ -169,15 +178,15 @@ struct BvhBuild {
         }
         return b;
     }
-    // median split on the longer axis of the centroid bounds; leaves of up to 4 fixtures
-    int build(int lo, int hi, int depth) {
+    // median split on the longer axis of the centroid bounds; leaves of up to 4 fixtures; nodes in preorder
+    void build(int lo, int hi, int depth) {
         max_depth = std::max(max_depth, depth);
         const int node = (int)box.size();
         box.push_back(bounds(lo, hi));
-        child.push_back(make_int2(0, 0));
+        link.push_back(make_int2(0, -1));
         if (hi - lo <= 4) {
-            child[node] = make_int2(~lo, hi - lo);
-            return node;
+            link[node] = make_int2(node + 1, (lo << 3) | (hi - lo));
+            return;
         }
         float cx0 = 3.4e38f, cy0 = 3.4e38f, cx1 = -3.4e38f, cy1 = -3.4e38f;
         for (int i = lo; i < hi; ++i) {
@@ -194,10 +203,9 @@ struct BvhBuild {
             const float ca = fa[axis] + fa[axis + 2], cb = fb[axis] + fb[axis + 2];
             return ca < cb || (ca == cb && a < b);
         });
-        const int l = build(lo, mid, depth + 1);
-        const int r = build(mid, hi, depth + 1);
-        child[node] = make_int2(l, r);
-        return node;
+        build(lo, mid, depth + 1);
+        build(mid, hi, depth + 1);
+        link[node] = make_int2((int)box.size(), -1);
     }
 };
 
@@ -265,7 +273,10 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     for (int f = 0; f < F; ++f)
         if (desc->fixture_slot[f] < 0) bvh.leaf.push_back(f);
     if (!bvh.leaf.empty()) bvh.build(0, (int)bvh.leaf.size(), 1);
-    if (bvh.max_depth > 30) { delete M; return fail(GOI_E_UNSUPPORTED, "goi_model_create: BVH too deep"); }
+    if (bvh.max_depth > 30 || bvh.leaf.size() >= (1u << 27)) {
+        delete M;
+        return fail(GOI_E_UNSUPPORTED, "goi_model_create: static terrain too large for the BVH");
+    }
     d.n_nodes = (int)bvh.box.size();
     d.n_dd = (int)dd.size();
     int any = desc->toi_bodies ? 0 : 1;
@@ -298,7 +309,7 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     UP(static_restitution, desc->static_restitution, F);
     UP(body_type, desc->body_type, B);
     UP(node_box, bvh.box.data(), bvh.box.size());
-    UP(node_child, bvh.child.data(), bvh.child.size());
+    UP(node_link, bvh.link.data(), bvh.link.size());
     UP(leaf_fixture, bvh.leaf.data(), bvh.leaf.size());
     UP(cand_static, cand.data(), (size_t)F * R);
     UP(dd_cand, dd.data(), dd.size());
@@ -341,22 +352,27 @@ static int check_view(const GoiModel* M, const GoiStateView* v, const char* who)
     return GOI_OK;
 }
 
+// LDS workspace bytes per world (Workspace::layout) and the block budget it is held to.
+constexpr size_t kMaxLdsBytes = 64 * 1024;
+static size_t workspace_bytes(int B, int C, int J) { return (size_t)Workspace::layout(B, C, J).words * sizeof(int); }
+
 // Worlds per 64-lane wavefront. One lane runs one world's whole step (a long serial chain of dependent work), so
 // a launch wants at least a few wavefronts per SIMD (256 CUs x 4 SIMDs) even when that leaves lanes idle.
 // GOI_WORLDS_PER_WAVE overrides (1..64).
-static int worlds_per_wave(int n) {
+static int worlds_per_wave(int n, size_t ws_bytes_per_world) {
     static int forced = -1;
     if (forced < 0) {
         const char* e = getenv("GOI_WORLDS_PER_WAVE");
         forced = e ? atoi(e) : 0;
         if (forced < 0 || forced > kBlock) forced = 0;
     }
-    if (forced > 0) return forced;
+    if (forced > 0) return std::min<long>(forced, std::max<long>(1, kMaxLdsBytes / ws_bytes_per_world));
     // Fewer worlds per wave raise the wave count (latency hiding) but spend a full wave instruction on fewer lanes.
     // Measured at 16384 worlds of the 4-body rig: 64 -> 3.81 ms, 32 -> 3.51, 16 -> 3.51, 8 -> 4.54, 4 -> 5.70;
     // keep at least 512 waves (two per CU) and otherwise pack as many worlds per wave as possible.
     int wpw = kBlock;
     while (wpw > 1 && (long)n / wpw < 512) wpw /= 2;
+    while (wpw > 1 && ws_bytes_per_world * wpw > kMaxLdsBytes) wpw /= 2;
     return wpw;
 }
 
@@ -372,7 +388,7 @@ static void fill_launch(Launch& L, const GoiStateView* v, const GoiSettings* s, 
     L.dt = dt;
     std::memset(&L.dbg, 0, sizeof(L.dbg));
     L.scratch = nullptr;
-    L.wpw = worlds_per_wave(v->n_worlds);
+    L.wpw = worlds_per_wave(v->n_worlds, workspace_bytes(v->B, v->C, v->J));
 }
 
 int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
@@ -398,7 +414,7 @@ int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSett
     L.scratch = M->scratch;
     if (debug) L.dbg = *debug;
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
-    const size_t lds = (size_t)kBodyFields * state->B * kBlock * sizeof(float);
+    const size_t lds = workspace_bytes(state->B, state->C, state->J) * L.wpw;
     hipLaunchKernelGGL(k_step, dim3(grid), dim3(kBlock), lds, st, M->d, L);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
@@ -412,7 +428,8 @@ int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiS
     Launch L;
     fill_launch(L, state, settings, 0.0f);
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
-    hipLaunchKernelGGL(k_collide, dim3(grid), dim3(kBlock), 0, static_cast<hipStream_t>(hip_stream), model->d, L, 0);
+    const size_t lds = workspace_bytes(state->B, state->C, state->J) * L.wpw;
+    hipLaunchKernelGGL(k_collide, dim3(grid), dim3(kBlock), lds, static_cast<hipStream_t>(hip_stream), model->d, L, 0);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
 }
