@@ -9,24 +9,24 @@ namespace goi {
 // Upper bound on contact slots per world the kernels handle (State capacity C <= kMaxC).
 constexpr int kMaxC = 64;
 
-// Live slots in contact-list order: newest first = descending key (pairs.py:12-13), by insertion into the
-// workspace's order array (W.order(0..n-1)); returns the count n.
-GOI_D int list_order(const World& W) {
+// The contact list (Box2D's m_contactList: newest first = descending key, pairs.py:12-13) is kept in the
+// workspace as W.order(0 .. nlive-1). build_order ranks the live slots once per step; Collide's destructions and
+// FindNewContacts' creations then update it in place (see collide_walk, find_new_contacts).
+GOI_D void build_order(const World& W) {
     int n = 0;
     for (int k = 0; k < W.C; ++k) {
         if (W.pair(k) < 0) continue;
         const int key = W.key(k);
-        int j = n++;
-        while (j > 0) {
-            const int prev = W.order(j - 1);
-            if (!(W.key(prev) < key)) break;
-            W.order(j) = prev;
-            --j;
-        }
-        W.order(j) = k;
+        int rank = 0;
+        for (int j = 0; j < W.C; ++j) rank += (W.pair(j) >= 0 && W.key(j) > key) ? 1 : 0;
+        W.order(rank) = k;
+        ++n;
     }
-    return n;
+    W.nlive() = n;
 }
+
+// Live slots in contact-list order: W.order(0 .. n-1); returns n.
+GOI_D int list_order(const World& W) { return W.nlive(); }
 
 // b2Contact::Update's manifold part: new manifold, impulses carried over from the first old point with the same
 // feature key, touching flag (pairs.py:56-83). Returns whether touching flipped.
@@ -88,6 +88,13 @@ GOI_D void collide_walk(const DModel& m, const World& W, float linear_slop) {
         evaluate(m, fa, fb, W.xf(ba), W.xf(bb), linear_slop, mf);
         if (contact_update(W, k, mf)) { W.wake(ba); W.wake(bb); }
     }
+    // drop the destroyed contacts from the list, keeping the order of the rest
+    int j = 0;
+    for (int i = 0; i < n; ++i) {
+        const int k = W.order(i);
+        if (W.pair(k) >= 0) W.order(j++) = k;
+    }
+    W.nlive() = j;
 }
 
 // Sorted buffer (the workspace's newp array) of the smallest new candidate indices of one FindNewContacts call,
@@ -115,45 +122,51 @@ GOI_D bool slot_has_pair(const World& W, int p) {
     return has;
 }
 
-// b2ContactManager::FindNewContacts (pairs.py:134-178) without scanning the candidate list: each non-static fixture
-// queries the static BVH with its fat AABB, a hit maps to its candidate index through cand_static, and the few
-// non-static/non-static candidates are tested directly. New pairs (overlapping, a dynamic body, both active, no
-// contact yet) take the lowest free slots in ascending candidate order with keys in that order; a full table counts
-// the rest in overflow.
+// b2ContactManager::FindNewContacts (pairs.py:134-178) without scanning the candidate list: one walk of the static
+// BVH with the union of the world's non-static fat AABBs; at a leaf, each entry is tested against each row's box and
+// a hit maps to its candidate index through leaf_cand; the few non-static/non-static candidates are tested directly.
+// New pairs (overlapping, a dynamic body, both active, no contact yet) take the lowest free slots in ascending
+// candidate order with keys in that order, and enter the contact list at its head (newest first); a full table
+// counts the rest in overflow. Every (leaf entry, row) is met once, so no candidate is found twice.
 GOI_D void find_new_contacts(const DModel& m, const World& W) {
     if (m.P == 0) return;
     int n_free = 0;
     for (int k = 0; k < W.C; ++k) n_free += W.pair(k) < 0;
     NewPairs np{W, 0, 0, n_free};
-    // static x non-static candidates via the BVH
+    // the query boxes of the rows on active bodies, and their union
+    unsigned long long rows = 0ull;
+    float4 U = make_float4(kMaxFloat, kMaxFloat, -kMaxFloat, -kMaxFloat);
     for (int r = 0; r < m.R; ++r) {
-        const int fd = m.slot_fixture[r];
-        const int bd = m.fixture_body[fd];
-        if (!W.u8(GOI_B_ACTIVE, bd)) continue;
+        if (!W.active(m.fixture_body[m.slot_fixture[r]])) continue;
         const float4 q = make_float4(W.f(GOI_F_FAT, 4 * r), W.f(GOI_F_FAT, 4 * r + 1), W.f(GOI_F_FAT, 4 * r + 2),
                                      W.f(GOI_F_FAT, 4 * r + 3));
-        const bool dyn_d = m.body_type[bd] == GOI_DYNAMIC;
-        // stackless preorder walk: descend into an overlapping internal node, else jump past its subtree
-        int nd = 0;
-        while (nd < m.n_nodes) {
-            const int2 ln = m.node_link[nd];
-            if (!overlap(q, m.node_box[nd])) {
-                nd = ln.x;
-                continue;
-            }
-            if (ln.y < 0) {
-                ++nd;
-                continue;
-            }
+        W.set_qbox(r, q);
+        rows |= 1ull << r;
+        U.x = fminf(U.x, q.x); U.y = fminf(U.y, q.y); U.z = fmaxf(U.z, q.z); U.w = fmaxf(U.w, q.w);
+    }
+    // stackless preorder walk: descend into a node the union overlaps, else jump past its subtree
+    int nd = rows ? 0 : m.n_nodes;
+    while (nd < m.n_nodes) {
+        const int2 ln = m.node_link[nd];
+        if (!overlap(U, m.node_box[nd])) {
             nd = ln.x;
-            for (int i = ln.y >> 3, e = (ln.y >> 3) + (ln.y & 7); i < e; ++i) {
-                const int fs = m.leaf_fixture[i];
-                const int p = m.cand_static[(size_t)fs * m.R + r];
+            continue;
+        }
+        if (ln.y < 0) {
+            ++nd;
+            continue;
+        }
+        nd = ln.x;
+        for (int i = ln.y >> 3, e = (ln.y >> 3) + (ln.y & 7); i < e; ++i) {
+            const float4 sf = m.leaf_fat[i];
+            const int info = m.leaf_info[i];  // static body | dynamic << 16
+            if (!W.active(info & 0xffff)) continue;
+            for (unsigned long long left = rows; left; left &= left - 1) {
+                const int r = __builtin_ctzll(left);
+                const int p = m.leaf_cand[(size_t)i * m.R + r];
                 if (p < 0) continue;
-                if (!overlap(m.static_fat[fs], q)) continue;
-                const int bs = m.fixture_body[fs];
-                if (!(dyn_d || m.body_type[bs] == GOI_DYNAMIC)) continue;
-                if (!W.u8(GOI_B_ACTIVE, bs)) continue;
+                if (!overlap(sf, W.get_qbox(r))) continue;
+                if (!(m.row_dynamic[r] || (info >> 16))) continue;
                 if (slot_has_pair(W, p)) continue;
                 np.add(p);
             }
@@ -166,15 +179,20 @@ GOI_D void find_new_contacts(const DModel& m, const World& W) {
         const int ba = m.fixture_body[a], bb = m.fixture_body[b];
         if (!overlap(fat_of(m, W, a), fat_of(m, W, b))) continue;
         if (!(m.body_type[ba] == GOI_DYNAMIC || m.body_type[bb] == GOI_DYNAMIC)) continue;
-        if (!(W.u8(GOI_B_ACTIVE, ba) && W.u8(GOI_B_ACTIVE, bb))) continue;
+        if (!(W.active(ba) && W.active(bb))) continue;
         if (slot_has_pair(W, p)) continue;
         np.add(p);
     }
     if (np.total == 0) return;
     const int base_key = W.i32(GOI_S_NEXT_KEY, 0);
+    // the new contacts (keys base_key .. base_key + kept - 1) go to the head of the list, newest first
+    const int nl = W.nlive();
+    for (int i = nl - 1; i >= 0; --i) W.order(i + np.kept) = W.order(i);
+    W.nlive() = nl + np.kept;
     int k = 0;
     for (int i = 0; i < np.kept; ++i) {
         while (W.pair(k) >= 0) ++k;
+        W.order(np.kept - 1 - i) = k;
         const int p = W.newp(i);
         const int a = m.pair_a[p], b = m.pair_b[p];
         W.pair(k) = p;

@@ -103,7 +103,7 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
     int nisl = 0, nc = 0, nj = 0;
     for (int seed = W.B - 1; seed >= 0; --seed) {
         if ((bflag >> seed) & 1ull) continue;
-        if (!W.awake(seed) || !W.u8(GOI_B_ACTIVE, seed) || m.body_type[seed] == GOI_STATIC) continue;
+        if (!W.awake(seed) || !W.active(seed) || m.body_type[seed] == GOI_STATIC) continue;
         const int isl = nisl++;
         int sp = 0;
         W.stack(sp++) = seed;
@@ -130,7 +130,7 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
                 if (ja != b && jb != b) continue;
                 if ((jflag >> j) & 1ull) continue;
                 const int other = ja == b ? jb : ja;
-                if (!W.u8(GOI_B_ACTIVE, other)) continue;
+                if (!W.active(other)) continue;
                 I.jorder(nj++) = j;
                 jflag |= 1ull << j;
                 I.joint_island(j) = isl;

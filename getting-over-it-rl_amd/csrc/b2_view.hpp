@@ -42,8 +42,10 @@ struct DModel {
     int n_nodes;
     const float4* node_box;     // [n_nodes] lx ly ux uy
     const int2* node_link;      // [n_nodes]
-    const int* leaf_fixture;    // static fixture ids in leaf order
-    const int* cand_static;     // [F * R]: candidate index of (static fixture f, row r), -1 if none
+    const float4* leaf_fat;     // [n_leaf] fat AABB of each leaf entry (a static fixture)
+    const int* leaf_info;       // [n_leaf] the entry's body | (body is dynamic) << 16
+    const int* leaf_cand;       // [n_leaf * R]: candidate index of (leaf entry i, row r), -1 if none
+    const int* row_dynamic;     // [R] the row's body is dynamic
     int n_dd;                   // candidates whose fixtures are both non-static
     const int* dd_cand;         // [n_dd] candidate indices (ascending)
 };
@@ -55,19 +57,23 @@ struct DModel {
 // lists and stacks, new-pair buffer), which would otherwise live in private scratch memory.
 struct Workspace {
     int o_pair, o_key, o_fa, o_fb, o_tflag, o_ten, o_tcount, o_ttoi, o_order, o_newp, o_corder, o_cisl;  // [C]
-    int o_awake, o_bisl, o_stack, o_fwork, o_ibuf;                                                      // [B]
+    int o_awake, o_active, o_bisl, o_stack, o_fwork, o_ibuf;                                            // [B]
+    int o_qbox;                                                                                         // [4 R]
+    int o_nlive;                                                                                        // [1]
     int o_jorder, o_jisl;                                                                               // [J]
     int o_body;  // 8 solver body fields x B
     int words;   // per lane
-    GOI_HD static Workspace layout(int B, int C, int J) {
+    GOI_HD static Workspace layout(int B, int C, int J, int R) {
         Workspace k;
         int o = 0;
         k.o_body = o; o += 8 * B;
         k.o_pair = o; o += C; k.o_key = o; o += C; k.o_fa = o; o += C; k.o_fb = o; o += C;
         k.o_tflag = o; o += C; k.o_ten = o; o += C; k.o_tcount = o; o += C; k.o_ttoi = o; o += C;
         k.o_order = o; o += C; k.o_newp = o; o += C; k.o_corder = o; o += C; k.o_cisl = o; o += C;
-        k.o_awake = o; o += B; k.o_bisl = o; o += B; k.o_stack = o; o += B; k.o_fwork = o; o += B; k.o_ibuf = o; o += B;
+        k.o_awake = o; o += B; k.o_active = o; o += B; k.o_bisl = o; o += B; k.o_stack = o; o += B; k.o_fwork = o; o += B; k.o_ibuf = o; o += B;
         k.o_jorder = o; o += J; k.o_jisl = o; o += J;
+        k.o_qbox = o; o += 4 * R;
+        k.o_nlive = o; o += 1;
         k.words = o;
         return k;
     }
@@ -91,6 +97,7 @@ struct World {
     GOI_D int& fa(int c) const { return wi(k.o_fa, c); }          // contacts.fa
     GOI_D int& fb(int c) const { return wi(k.o_fb, c); }          // contacts.fb
     GOI_D int& awake(int b) const { return wi(k.o_awake, b); }    // bodies.awake
+    GOI_D int& active(int b) const { return wi(k.o_active, b); }  // bodies.active (read-only in a step)
     GOI_D int& tflag(int c) const { return wi(k.o_tflag, c); }    // toi.flag
     GOI_D int& ten(int c) const { return wi(k.o_ten, c); }        // toi.enabled
     GOI_D int& tcount(int c) const { return wi(k.o_tcount, c); }  // toi.count
@@ -106,6 +113,13 @@ struct World {
     GOI_D int& ibuf(int i) const { return wi(k.o_ibuf, i); }
     GOI_D int& jorder(int i) const { return wi(k.o_jorder, i); }
     GOI_D int& jisl(int j) const { return wi(k.o_jisl, j); }
+    GOI_D int& nlive() const { return wi(k.o_nlive, 0); }   // length of the contact list in order()
+    GOI_D void set_qbox(int r, float4 q) const {
+        wf(k.o_qbox, 4 * r) = q.x; wf(k.o_qbox, 4 * r + 1) = q.y; wf(k.o_qbox, 4 * r + 2) = q.z; wf(k.o_qbox, 4 * r + 3) = q.w;
+    }
+    GOI_D float4 get_qbox(int r) const {
+        return make_float4(wf(k.o_qbox, 4 * r), wf(k.o_qbox, 4 * r + 1), wf(k.o_qbox, 4 * r + 2), wf(k.o_qbox, 4 * r + 3));
+    }
 
     template <typename T>
     GOI_D T& at(int leaf, int i) const {
@@ -141,7 +155,10 @@ struct World {
             fa(c) = i32(GOI_C_FA, c);
             fb(c) = i32(GOI_C_FB, c);
         }
-        for (int b = 0; b < B; ++b) awake(b) = u8(GOI_B_AWAKE, b);
+        for (int b = 0; b < B; ++b) {
+            awake(b) = u8(GOI_B_AWAKE, b);
+            active(b) = u8(GOI_B_ACTIVE, b);
+        }
     }
     GOI_D void store_mirror() const {
         for (int c = 0; c < C; ++c) {

@@ -60,7 +60,7 @@ __device__ __forceinline__ World make_world(const Launch& L, int w, int* lds, in
     W.J = L.J;
     W.lv = L.leaf;
     W.w = w;
-    W.k = Workspace::layout(L.B, L.C, L.J);
+    W.k = Workspace::layout(L.B, L.C, L.J, L.R);
     W.ws = lds + lane;
     W.S = L.wpw;
     return W;
@@ -91,6 +91,7 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
     if ((int)threadIdx.x >= L.wpw || w >= L.n) return;
     const World W = make_world(L, w, lds, threadIdx.x);
     W.load_mirror();
+    build_order(W);
     if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
     W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     if (!start_only) collide_walk(m, W, L.s.linear_slop);
@@ -105,6 +106,7 @@ __global__ void __launch_bounds__(kBlock) k_step(DModel m, Launch L) {
     if ((int)threadIdx.x >= L.wpw || w >= L.n) return;
     const World W = make_world(L, w, lds, threadIdx.x);
     W.load_mirror();
+    build_order(W);
     if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
     W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     collide_walk(m, W, L.s.linear_slop);
@@ -255,6 +257,7 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
             return fail(GOI_E_ARG, "goi_model_create: fixture_slot rows must ascend with the fixture index");
         }
     const int R = (int)slot_fixture.size();
+    if (R > 64) { delete M; return fail(GOI_E_UNSUPPORTED, "goi_model_create: more than 64 non-static fixtures"); }
     d.R = R;
     // candidate tables
     std::vector<int> cand((size_t)F * std::max(R, 1), -1), dd;
@@ -278,6 +281,18 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
         return fail(GOI_E_UNSUPPORTED, "goi_model_create: static terrain too large for the BVH");
     }
     d.n_nodes = (int)bvh.box.size();
+    // per leaf entry: fat box, body, candidate row; per row: dynamic body
+    const size_t n_leaf = bvh.leaf.size();
+    std::vector<float4> leaf_fat(n_leaf);
+    std::vector<int> leaf_info(n_leaf), leaf_cand(std::max<size_t>(n_leaf * R, 1), -1), row_dyn(std::max(R, 1), 0);
+    for (size_t i = 0; i < n_leaf; ++i) {
+        const int f = bvh.leaf[i], b = desc->fixture_body[f];
+        leaf_fat[i] = make_float4(desc->static_fat[4 * f], desc->static_fat[4 * f + 1], desc->static_fat[4 * f + 2],
+                                  desc->static_fat[4 * f + 3]);
+        leaf_info[i] = b | ((desc->body_type[b] == GOI_DYNAMIC ? 1 : 0) << 16);
+        for (int r = 0; r < R; ++r) leaf_cand[i * R + r] = cand[(size_t)f * R + r];
+    }
+    for (int r = 0; r < R; ++r) row_dyn[r] = desc->body_type[desc->fixture_body[slot_fixture[r]]] == GOI_DYNAMIC;
     d.n_dd = (int)dd.size();
     int any = desc->toi_bodies ? 0 : 1;
     if (desc->toi_bodies)
@@ -310,8 +325,10 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     UP(body_type, desc->body_type, B);
     UP(node_box, bvh.box.data(), bvh.box.size());
     UP(node_link, bvh.link.data(), bvh.link.size());
-    UP(leaf_fixture, bvh.leaf.data(), bvh.leaf.size());
-    UP(cand_static, cand.data(), (size_t)F * R);
+    UP(leaf_fat, leaf_fat.data(), n_leaf);
+    UP(leaf_info, leaf_info.data(), n_leaf);
+    UP(leaf_cand, leaf_cand.data(), n_leaf * R);
+    UP(row_dynamic, row_dyn.data(), R);
     UP(dd_cand, dd.data(), dd.size());
 #undef UP
     if (rc == GOI_OK) {
@@ -354,7 +371,9 @@ static int check_view(const GoiModel* M, const GoiStateView* v, const char* who)
 
 // LDS workspace bytes per world (Workspace::layout) and the block budget it is held to.
 constexpr size_t kMaxLdsBytes = 64 * 1024;
-static size_t workspace_bytes(int B, int C, int J) { return (size_t)Workspace::layout(B, C, J).words * sizeof(int); }
+static size_t workspace_bytes(int B, int C, int J, int R) {
+    return (size_t)Workspace::layout(B, C, J, R).words * sizeof(int);
+}
 
 // Worlds per 64-lane wavefront. One lane runs one world's whole step (a long serial chain of dependent work), so
 // a launch wants at least a few wavefronts per SIMD (256 CUs x 4 SIMDs) even when that leaves lanes idle.
@@ -388,7 +407,7 @@ static void fill_launch(Launch& L, const GoiStateView* v, const GoiSettings* s, 
     L.dt = dt;
     std::memset(&L.dbg, 0, sizeof(L.dbg));
     L.scratch = nullptr;
-    L.wpw = worlds_per_wave(v->n_worlds, workspace_bytes(v->B, v->C, v->J));
+    L.wpw = worlds_per_wave(v->n_worlds, workspace_bytes(v->B, v->C, v->J, v->R));
 }
 
 int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
@@ -414,7 +433,7 @@ int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSett
     L.scratch = M->scratch;
     if (debug) L.dbg = *debug;
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
-    const size_t lds = workspace_bytes(state->B, state->C, state->J) * L.wpw;
+    const size_t lds = workspace_bytes(state->B, state->C, state->J, state->R) * L.wpw;
     hipLaunchKernelGGL(k_step, dim3(grid), dim3(kBlock), lds, st, M->d, L);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
@@ -428,7 +447,7 @@ int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiS
     Launch L;
     fill_launch(L, state, settings, 0.0f);
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
-    const size_t lds = workspace_bytes(state->B, state->C, state->J) * L.wpw;
+    const size_t lds = workspace_bytes(state->B, state->C, state->J, state->R) * L.wpw;
     hipLaunchKernelGGL(k_collide, dim3(grid), dim3(kBlock), lds, static_cast<hipStream_t>(hip_stream), model->d, L, 0);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
