@@ -128,8 +128,13 @@ GOI_D bool slot_has_pair(const World& W, int p) {
 // New pairs (overlapping, a dynamic body, both active, no contact yet) take the lowest free slots in ascending
 // candidate order with keys in that order, and enter the contact list at its head (newest first); a full table
 // counts the rest in overflow. Every (leaf entry, row) is met once, so no candidate is found twice.
-GOI_D void find_new_contacts(const DModel& m, const World& W) {
-    if (m.P == 0) return;
+//
+// query_rows restricts the search to candidates with at least one of the given non-static rows. The result is the
+// full scan's as long as every candidate without such a row was decided by an earlier call of the same step whose
+// boxes it still has and whose contacts still exist, and no earlier call dropped a candidate (overflow still 0):
+// true after a TOI event, which moves only the rows it re-fattens and destroys no contact.
+GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long query_rows = ~0ull) {
+    if (m.P == 0 || query_rows == 0ull) return;
     int n_free = 0;
     for (int k = 0; k < W.C; ++k) n_free += W.pair(k) < 0;
     NewPairs np{W, 0, 0, n_free};
@@ -137,7 +142,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W) {
     unsigned long long rows = 0ull;
     float4 U = make_float4(kMaxFloat, kMaxFloat, -kMaxFloat, -kMaxFloat);
     for (int r = 0; r < m.R; ++r) {
-        if (!W.active(m.fixture_body[m.slot_fixture[r]])) continue;
+        if (!((query_rows >> r) & 1ull) || !W.active(m.fixture_body[m.slot_fixture[r]])) continue;
         const float4 q = make_float4(W.f(GOI_F_FAT, 4 * r), W.f(GOI_F_FAT, 4 * r + 1), W.f(GOI_F_FAT, 4 * r + 2),
                                      W.f(GOI_F_FAT, 4 * r + 3));
         W.set_qbox(r, q);
@@ -157,17 +162,25 @@ GOI_D void find_new_contacts(const DModel& m, const World& W) {
             continue;
         }
         nd = ln.x;
-        for (int i = ln.y >> 3, e = (ln.y >> 3) + (ln.y & 7); i < e; ++i) {
-            const float4 sf = m.leaf_fat[i];
-            const int info = m.leaf_info[i];  // static body | dynamic << 16
-            if (!W.active(info & 0xffff)) continue;
+        // a leaf's entries (at most 4; the arrays are padded by 4) load together, then the cheap box tests run
+        // first and only a hit reads its candidate index
+        const int first = ln.y >> 3, cnt = ln.y & 7;
+        float4 sf[4];
+        int info[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            sf[j] = m.leaf_fat[first + j];
+            info[j] = m.leaf_info[first + j];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (j >= cnt || !overlap(sf[j], U) || !W.active(info[j] & 0xffff)) continue;
             for (unsigned long long left = rows; left; left &= left - 1) {
                 const int r = __builtin_ctzll(left);
-                const int p = m.leaf_cand[(size_t)i * m.R + r];
-                if (p < 0) continue;
-                if (!overlap(sf, W.get_qbox(r))) continue;
-                if (!(m.row_dynamic[r] || (info >> 16))) continue;
-                if (slot_has_pair(W, p)) continue;
+                if (!overlap(sf[j], W.get_qbox(r))) continue;
+                if (!(m.row_dynamic[r] || (info[j] >> 16))) continue;
+                const int p = m.leaf_cand[(size_t)(first + j) * m.R + r];
+                if (p < 0 || slot_has_pair(W, p)) continue;
                 np.add(p);
             }
         }
@@ -176,6 +189,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W) {
     for (int i = 0; i < m.n_dd; ++i) {
         const int p = m.dd_cand[i];
         const int a = m.pair_a[p], b = m.pair_b[p];
+        if (!(((query_rows >> m.fixture_slot[a]) | (query_rows >> m.fixture_slot[b])) & 1ull)) continue;
         const int ba = m.fixture_body[a], bb = m.fixture_body[b];
         if (!overlap(fat_of(m, W, a), fat_of(m, W, b))) continue;
         if (!(m.body_type[ba] == GOI_DYNAMIC || m.body_type[bb] == GOI_DYNAMIC)) continue;
@@ -237,8 +251,10 @@ GOI_D float4 shape_aabb(const DModel& m, int f, const Xf& t) {
 }
 
 // b2Body::SynchronizeFixtures for body b (pairs.py:181-207): swept AABB over the sweep start and the current
-// transform; b2DynamicTree::MoveProxy re-fattens only if the fat box no longer contains it.
-GOI_D void sync_body_fixtures(const DModel& m, const World& W, int b, const Xf& x1) {
+// transform; b2DynamicTree::MoveProxy re-fattens only if the fat box no longer contains it. Returns the rows it
+// re-fattened.
+GOI_D unsigned long long sync_body_fixtures(const DModel& m, const World& W, int b, const Xf& x1) {
+    unsigned long long moved = 0ull;
     const Xf x2 = W.xf(b);
     for (int r = 0; r < m.R; ++r) {
         const int f = m.slot_fixture[r];
@@ -258,7 +274,9 @@ GOI_D void sync_body_fixtures(const DModel& m, const World& W, int b, const Xf& 
         W.f(GOI_F_FAT, 4 * r + 1) = ly;
         W.f(GOI_F_FAT, 4 * r + 2) = ux;
         W.f(GOI_F_FAT, 4 * r + 3) = uy;
+        moved |= 1ull << r;
     }
+    return moved;
 }
 
 // the sweep-start transform of body b: q(a0), c0 - q * localCenter

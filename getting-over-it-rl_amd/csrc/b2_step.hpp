@@ -385,12 +385,12 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         W.u8(GOI_T_SOLVED, slot) = 1;
     }
     // fixture sync of the island's dynamic bodies and TOI invalidation of their contacts
-    unsigned long long moved = 0ull;
+    unsigned long long moved = 0ull, refat = 0ull;
     for (int i = 0; i < nb; ++i) {
         const int b = W.ibuf(i);
         if (m.body_type[b] != GOI_DYNAMIC) continue;
         moved |= 1ull << b;
-        sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
+        refat |= sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
     }
     for (int c = 0; c < W.C; ++c) {
         if (W.pair(c) < 0) continue;
@@ -404,7 +404,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         if (W.pair(c) < 0) was_free |= 1ull << c;
         W.corder(c) = W.key(c);
     }
-    find_new_contacts(m, W);
+    find_new_contacts(m, W, W.i32(GOI_S_OVERFLOW, 0) == 0 ? refat : ~0ull);
     for (int c = 0; c < W.C; ++c) {
         if (W.pair(c) >= 0 && (((was_free >> c) & 1ull) || W.corder(c) != W.key(c))) {
             W.tcount(c) = 0;

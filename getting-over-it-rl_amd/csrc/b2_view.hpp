@@ -42,8 +42,8 @@ struct DModel {
     int n_nodes;
     const float4* node_box;     // [n_nodes] lx ly ux uy
     const int2* node_link;      // [n_nodes]
-    const float4* leaf_fat;     // [n_leaf] fat AABB of each leaf entry (a static fixture)
-    const int* leaf_info;       // [n_leaf] the entry's body | (body is dynamic) << 16
+    const float4* leaf_fat;     // [n_leaf + 4] fat AABB of each leaf entry (a static fixture); 4 padding records
+    const int* leaf_info;       // [n_leaf + 4] the entry's body | (body is dynamic) << 16
     const int* leaf_cand;       // [n_leaf * R]: candidate index of (leaf entry i, row r), -1 if none
     const int* row_dynamic;     // [R] the row's body is dynamic
     int n_dd;                   // candidates whose fixtures are both non-static

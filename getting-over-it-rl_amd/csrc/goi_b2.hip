@@ -283,8 +283,9 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     d.n_nodes = (int)bvh.box.size();
     // per leaf entry: fat box, body, candidate row; per row: dynamic body
     const size_t n_leaf = bvh.leaf.size();
-    std::vector<float4> leaf_fat(n_leaf);
-    std::vector<int> leaf_info(n_leaf), leaf_cand(std::max<size_t>(n_leaf * R, 1), -1), row_dyn(std::max(R, 1), 0);
+    // entry records padded by 4 so that a leaf's 4 records always load in bounds
+    std::vector<float4> leaf_fat(n_leaf + 4, make_float4(0.f, 0.f, 0.f, 0.f));
+    std::vector<int> leaf_info(n_leaf + 4, 0), leaf_cand(std::max<size_t>(n_leaf * R, 1), -1), row_dyn(std::max(R, 1), 0);
     for (size_t i = 0; i < n_leaf; ++i) {
         const int f = bvh.leaf[i], b = desc->fixture_body[f];
         leaf_fat[i] = make_float4(desc->static_fat[4 * f], desc->static_fat[4 * f + 1], desc->static_fat[4 * f + 2],
@@ -325,8 +326,8 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     UP(body_type, desc->body_type, B);
     UP(node_box, bvh.box.data(), bvh.box.size());
     UP(node_link, bvh.link.data(), bvh.link.size());
-    UP(leaf_fat, leaf_fat.data(), n_leaf);
-    UP(leaf_info, leaf_info.data(), n_leaf);
+    UP(leaf_fat, leaf_fat.data(), leaf_fat.size());
+    UP(leaf_info, leaf_info.data(), leaf_info.size());
     UP(leaf_cand, leaf_cand.data(), n_leaf * R);
     UP(row_dynamic, row_dyn.data(), R);
     UP(dd_cand, dd.data(), dd.size());
