@@ -211,35 +211,111 @@ GOI_D bool pair_rule(const DModel& m, const World& W, const GoiSettings& s, int 
     return stock && rule;
 }
 
-// the min-TOI search (toi.py:488-558); returns whether an event was found
-GOI_D bool toi_search(const DModel& m, const World& W, const GoiSettings& s, int& min_slot, float& min_alpha) {
+// ---------------------------------------------------------------- the min-TOI search (toi.py:488-558)
+//
+// Box2D's search walks the contact list once: for each contact without a cached TOI it aligns the two sweeps
+// (b2Sweep::Advance of the body with the smaller alpha0) and computes the TOI, then keeps the minimum. Alignments
+// depend only on alpha0 values, never on TOI results, so the walk splits into three passes with the same results:
+//   1. toi_search_prepare (each world, list order): the alignments, with each TOI's inputs (fixtures, both sweeps
+//      as aligned at that contact, alpha0) snapshotted into the world's contact row `task`;
+//   2. toi_tasks_run (the whole wavefront): the TOIs of all worlds of the block, spread over all 64 lanes;
+//   3. toi_search_pick (each world, list order): the minimum with the reference's tie rule.
+
+// task snapshot fields in a contact row
+enum { TT_FA = 0, TT_FB, TT_ALPHA0, TT_SA, TT_SB = TT_SA + 8, TT_N = TT_SB + 8 };
+static_assert(TT_N <= CF_N, "TOI task snapshot must fit a contact row");
+
+GOI_D void put_sweep(const Rows& R, int row, int f, const Sweep& sw) {
+    R.set2(row, f, sw.lc); R.set2(row, f + 2, sw.c0); R.set2(row, f + 4, sw.c);
+    R.setf(row, f + 6, sw.a0); R.setf(row, f + 7, sw.a);
+}
+
+// pass 1; returns the number of TOI tasks, whose slots are W.newp(0 .. n-1)
+GOI_D int toi_search_prepare(const DModel& m, const World& W, const Rows& CR, const GoiSettings& s) {
+    const int n = list_order(W);
+    int nt = 0;
+    for (int i = 0; i < n; ++i) {
+        const int c = W.order(i);
+        if (!W.ten(c) || W.tcount(c) > kMaxSubSteps || W.tflag(c)) continue;
+        const int fa = W.fa(c), fb = W.fb(c);
+        const int A = m.fixture_body[fa], Bb = m.fixture_body[fb];
+        const bool act_a = W.awake(A) && m.body_type[A] != GOI_STATIC;
+        const bool act_b = W.awake(Bb) && m.body_type[Bb] != GOI_STATIC;
+        if (!act_a && !act_b) continue;
+        if (!pair_rule(m, W, s, A, Bb)) continue;
+        const float alA = W.f(GOI_T_ALPHA0, A), alB = W.f(GOI_T_ALPHA0, Bb);
+        float alpha0 = alA;
+        if (alA < alB) { alpha0 = alB; sweep_advance(W, A, alpha0); }
+        else if (alB < alA) { alpha0 = alA; sweep_advance(W, Bb, alpha0); }
+        CR.seti(nt, TT_FA, fa);
+        CR.seti(nt, TT_FB, fb);
+        CR.setf(nt, TT_ALPHA0, alpha0);
+        put_sweep(CR, nt, TT_SA, body_sweep(W, A));
+        put_sweep(CR, nt, TT_SB, body_sweep(W, Bb));
+        W.newp(nt++) = c;
+        W.tflag(c) = 1;  // the toi itself arrives in pass 2
+    }
+    return nt;
+}
+
+// The block's view for pass 2: every lane of the wavefront computes TOI tasks of any world of the block.
+struct ToiCoop {
+    int* lds;        // the block's LDS workspace (lane 0's base)
+    int* scan;       // 64 ints after the workspaces
+    int S;           // worlds (lanes with a world) per block
+    Workspace k;
+    uint32_t* rows;  // contact rows (Launch.scratch)
+    int pitch, w0;   // row pitch, the block's first world
+    int lanes;       // lanes sharing the tasks (the block size)
+};
+
+// pass 2: called by all 64 lanes of the block together; `my` = this lane's task count (0 for lanes without one)
+GOI_D void toi_tasks_run(const DModel& m, const ToiCoop& co, int my, float linear_slop) {
+    const int lane = threadIdx.x;
+    int incl = my;
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += v;
+    }
+    const int total = __shfl(incl, 63, 64);
+    if (total == 0) return;
+    co.scan[lane] = incl;
+    __syncthreads();  // scan entries and the owners' task rows visible to the whole block
+    for (int t = lane; t < total; t += co.lanes) {
+        int lo = 0, hi = 63;  // owner: the first lane whose inclusive count exceeds t
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (co.scan[mid] > t) hi = mid; else lo = mid + 1;
+        }
+        const int o = lo;
+        const int i = t - (o ? co.scan[o - 1] : 0);
+        Rows R;
+        R.base = co.rows; R.pitch = co.pitch; R.w = co.w0 + o; R.nf = CF_N;
+        Sweep sa, sb;
+        sa.lc = R.get2(i, TT_SA); sa.c0 = R.get2(i, TT_SA + 2); sa.c = R.get2(i, TT_SA + 4);
+        sa.a0 = R.getf(i, TT_SA + 6); sa.a = R.getf(i, TT_SA + 7);
+        sb.lc = R.get2(i, TT_SB); sb.c0 = R.get2(i, TT_SB + 2); sb.c = R.get2(i, TT_SB + 4);
+        sb.a0 = R.getf(i, TT_SB + 6); sb.a = R.getf(i, TT_SB + 7);
+        const float alpha0 = R.getf(i, TT_ALPHA0);
+        float beta;
+        const int st = time_of_impact(proxy_of(m, R.geti(i, TT_FA)), sa, proxy_of(m, R.geti(i, TT_FB)), sb,
+                                      linear_slop, beta);
+        const float alpha = st == kToiTouching ? bmin(alpha0 + (1.0f - alpha0) * beta, 1.0f) : 1.0f;
+        const int c = co.lds[(co.k.o_newp + i) * co.S + o];
+        reinterpret_cast<float*>(co.lds)[(co.k.o_ttoi + c) * co.S + o] = alpha;
+    }
+    __syncthreads();  // the tois visible to their owners
+}
+
+// pass 3; returns whether an event was found
+GOI_D bool toi_search_pick(const World& W, const GoiSettings& s, int& min_slot, float& min_alpha) {
     const int n = list_order(W);
     int best = -1;
     float best_alpha = 1.0f;
     for (int i = 0; i < n; ++i) {
         const int c = W.order(i);
-        if (!W.ten(c) || W.tcount(c) > kMaxSubSteps) continue;
-        float alpha;
-        if (W.tflag(c)) {
-            alpha = W.ttoi(c);
-        } else {
-            const int fa = W.fa(c), fb = W.fb(c);
-            const int A = m.fixture_body[fa], Bb = m.fixture_body[fb];
-            const bool act_a = W.awake(A) && m.body_type[A] != GOI_STATIC;
-            const bool act_b = W.awake(Bb) && m.body_type[Bb] != GOI_STATIC;
-            if (!act_a && !act_b) continue;
-            if (!pair_rule(m, W, s, A, Bb)) continue;
-            const float alA = W.f(GOI_T_ALPHA0, A), alB = W.f(GOI_T_ALPHA0, Bb);
-            float alpha0 = alA;
-            if (alA < alB) { alpha0 = alB; sweep_advance(W, A, alpha0); }
-            else if (alB < alA) { alpha0 = alA; sweep_advance(W, Bb, alpha0); }
-            float beta;
-            const int st = time_of_impact(proxy_of(m, fa), body_sweep(W, A), proxy_of(m, fb), body_sweep(W, Bb),
-                                          s.linear_slop, beta);
-            alpha = st == kToiTouching ? bmin(alpha0 + (1.0f - alpha0) * beta, 1.0f) : 1.0f;
-            W.ttoi(c) = alpha;
-            W.tflag(c) = 1;
-        }
+        if (!W.ten(c) || W.tcount(c) > kMaxSubSteps || !W.tflag(c)) continue;
+        const float alpha = W.ttoi(c);
         if (alpha < 1.0f && (s.toi_tie_oldest ? alpha <= best_alpha : alpha < best_alpha)) {
             best = c;
             best_alpha = alpha;
@@ -414,37 +490,48 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     }
 }
 
-GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR,
-                                const GoiSettings& s, float dt) {
+// b2World::SolveTOI (toi.py:827-865). Called by every lane of the block (the TOI searches are cooperative);
+// `valid` marks the lanes that own a world.
+GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
+                           float dt, bool valid, const ToiCoop& co) {
     if (W.C == 0 || m.P == 0) return;
     if (s.unity_toi && !m.any_toi_body) return;
-    for (int b = 0; b < W.B; ++b) W.f(GOI_T_ALPHA0, b) = 0.0f;
-    for (int c = 0; c < W.C; ++c) {
-        W.tcount(c) = 0;
-        W.ttoi(c) = 1.0f;
-        W.tflag(c) = 0;
-        W.ten(c) = 1;
-        W.u8(GOI_T_SOLVED, c) = 0;
-        W.f(GOI_T_NORMAL_IMPULSE, 2 * c) = 0.0f;
-        W.f(GOI_T_NORMAL_IMPULSE, 2 * c + 1) = 0.0f;
-        W.f(GOI_T_TANGENT_IMPULSE, 2 * c) = 0.0f;
-        W.f(GOI_T_TANGENT_IMPULSE, 2 * c + 1) = 0.0f;
+    if (valid) {
+        for (int b = 0; b < W.B; ++b) W.f(GOI_T_ALPHA0, b) = 0.0f;
+        for (int c = 0; c < W.C; ++c) {
+            W.tcount(c) = 0;
+            W.ttoi(c) = 1.0f;
+            W.tflag(c) = 0;
+            W.ten(c) = 1;
+            W.u8(GOI_T_SOLVED, c) = 0;
+            W.f(GOI_T_NORMAL_IMPULSE, 2 * c) = 0.0f;
+            W.f(GOI_T_NORMAL_IMPULSE, 2 * c + 1) = 0.0f;
+            W.f(GOI_T_TANGENT_IMPULSE, 2 * c) = 0.0f;
+            W.f(GOI_T_TANGENT_IMPULSE, 2 * c + 1) = 0.0f;
+        }
     }
-    W.i32(GOI_T_EVENTS, 0) = 0;
+    int events = 0;
     if (dt > 0.0f) {
         const int max_events = s.max_events >= 0 ? s.max_events : W.C * (kMaxSubSteps + 1) + 8;
-        int slot;
-        float alpha;
-        int events = 0;
-        bool found = toi_search(m, W, s, slot, alpha);
-        while (found && events < max_events) {
-            toi_event(m, W, bd, CR, s, dt, slot, alpha);
-            ++events;
-            found = toi_search(m, W, s, slot, alpha);
+        int slot = -1;
+        float alpha = 1.0f;
+        toi_tasks_run(m, co, valid ? toi_search_prepare(m, W, CR, s) : 0, s.linear_slop);
+        bool found = valid && toi_search_pick(W, s, slot, alpha);
+        // the block iterates while any world has an event to process; the others take part in the searches only
+        while (__any(found && events < max_events)) {
+            const bool act = found && events < max_events;
+            if (act) {
+                toi_event(m, W, bd, CR, s, dt, slot, alpha);
+                ++events;
+            }
+            toi_tasks_run(m, co, act ? toi_search_prepare(m, W, CR, s) : 0, s.linear_slop);
+            found = act && toi_search_pick(W, s, slot, alpha);
         }
-        W.i32(GOI_T_EVENTS, 0) = events;
     }
-    W.store_toi();
+    if (valid) {
+        W.i32(GOI_T_EVENTS, 0) = events;
+        W.store_toi();
+    }
 }
 
 }  // namespace goi

@@ -99,24 +99,39 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
 }
 
 // The whole b2World::Step (step.py:28-47) of one world per lane: FindNewContacts where new_fixture, Collide,
-// Solve, SolveTOI, inv_dt0, ClearForces.
+// Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to help with the block's TOI searches.
 __global__ void __launch_bounds__(kBlock) k_step(DModel m, Launch L) {
     extern __shared__ int lds[];
-    const int w = blockIdx.x * L.wpw + threadIdx.x;
-    if ((int)threadIdx.x >= L.wpw || w >= L.n) return;
-    const World W = make_world(L, w, lds, threadIdx.x);
-    W.load_mirror();
-    build_order(W);
-    if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
-    W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
-    collide_walk(m, W, L.s.linear_slop);
+    const int lane = threadIdx.x;
+    const int w0 = blockIdx.x * L.wpw;
+    const bool valid = lane < L.wpw && w0 + lane < L.n;
+    const World W = make_world(L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
     Bodies bd;
-    bd.s = reinterpret_cast<float*>(lds) + W.k.o_body * W.S + threadIdx.x;
+    bd.s = reinterpret_cast<float*>(lds) + W.k.o_body * W.S + (valid ? lane : 0);
     bd.B = L.B;
     bd.st = W.S;
-    const Rows CR = contact_rows(L, w);
-    solve_world(m, W, bd, CR, joint_rows(L, w), L.s, L.dt, L.dbg);
-    if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt);
+    const Rows CR = contact_rows(L, W.w);
+    if (valid) {
+        W.load_mirror();
+        build_order(W);
+        if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
+        W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
+        collide_walk(m, W, L.s.linear_slop);
+        solve_world(m, W, bd, CR, joint_rows(L, W.w), L.s, L.dt, L.dbg);
+    }
+    if (L.s.continuous_physics) {
+        ToiCoop co;
+        co.lds = lds;
+        co.scan = lds + W.k.words * L.wpw;
+        co.S = L.wpw;
+        co.k = W.k;
+        co.rows = L.scratch;
+        co.pitch = L.pitch;
+        co.w0 = w0;
+        co.lanes = kBlock;
+        solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, co);
+    }
+    if (!valid) return;
     const float dt = L.dt;
     if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
     if (L.s.auto_clear_forces)
@@ -386,13 +401,14 @@ static int worlds_per_wave(int n, size_t ws_bytes_per_world) {
         forced = e ? atoi(e) : 0;
         if (forced < 0 || forced > kBlock) forced = 0;
     }
-    if (forced > 0) return std::min<long>(forced, std::max<long>(1, kMaxLdsBytes / ws_bytes_per_world));
+    if (forced > 0)
+        return std::min<long>(forced, std::max<long>(1, (kMaxLdsBytes - kBlock * sizeof(int)) / ws_bytes_per_world));
     // Fewer worlds per wave raise the wave count (latency hiding) but spend a full wave instruction on fewer lanes.
     // Measured at 16384 worlds of the 4-body rig: 64 -> 3.81 ms, 32 -> 3.51, 16 -> 3.51, 8 -> 4.54, 4 -> 5.70;
     // keep at least 512 waves (two per CU) and otherwise pack as many worlds per wave as possible.
     int wpw = kBlock;
     while (wpw > 1 && (long)n / wpw < 512) wpw /= 2;
-    while (wpw > 1 && ws_bytes_per_world * wpw > kMaxLdsBytes) wpw /= 2;
+    while (wpw > 1 && ws_bytes_per_world * wpw + kBlock * sizeof(int) > kMaxLdsBytes) wpw /= 2;
     return wpw;
 }
 
@@ -434,7 +450,7 @@ int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSett
     L.scratch = M->scratch;
     if (debug) L.dbg = *debug;
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
-    const size_t lds = workspace_bytes(state->B, state->C, state->J, state->R) * L.wpw;
+    const size_t lds = workspace_bytes(state->B, state->C, state->J, state->R) * L.wpw + kBlock * sizeof(int);
     hipLaunchKernelGGL(k_step, dim3(grid), dim3(kBlock), lds, st, M->d, L);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
