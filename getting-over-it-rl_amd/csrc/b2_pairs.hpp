@@ -65,19 +65,109 @@ GOI_D bool contact_update(const World& W, int k, const Manifold& mf) {
     return flip;
 }
 
+// ---------------------------------------------------------------- block-cooperative task runs
+//
+// A block is one wavefront: its first S lanes own worlds, and all 64 lanes share the work of task lists the worlds
+// build (TOIs to compute, manifolds to evaluate). Each world numbers its tasks 0..n-1 and keeps their inputs in its
+// workspace or its contact rows; coop_run hands task i of the world on lane o to some lane of the block.
+struct Coop {
+    World base;      // lane 0's world (the fields common to the block)
+    int* lds;        // the block's LDS workspace (lane 0's base)
+    int* scan;       // 64 ints after the workspaces
+    uint32_t* rows;  // contact rows (Launch.scratch)
+    int w0;          // the block's first world
+    int lanes;       // lanes sharing the tasks (the block size)
+    GOI_D World world(int o) const {
+        World W = base;
+        W.ws = lds + o;
+        W.w = w0 + o;
+        return W;
+    }
+    GOI_D Rows task_rows(int o) const {
+        Rows R;
+        R.base = rows; R.pitch = base.pitch; R.w = w0 + o; R.nf = CF_N;
+        return R;
+    }
+};
+
+// Called by all lanes of the block together; `my` = this lane's task count (0 for lanes without a world).
+template <typename F>
+GOI_D void coop_run(const Coop& co, int my, F&& task) {
+    const int lane = threadIdx.x;
+    int incl = my;
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += v;
+    }
+    const int total = __shfl(incl, 63, 64);
+    if (total == 0) return;
+    co.scan[lane] = incl;
+    __syncthreads();  // scan entries and the owners' task inputs visible to the whole block
+    for (int t = lane; t < total; t += co.lanes) {
+        int lo = 0, hi = 63;  // owner: the first lane whose inclusive count exceeds t
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (co.scan[mid] > t) hi = mid; else lo = mid + 1;
+        }
+        task(lo, t - (lo ? co.scan[lo - 1] : 0));
+    }
+    __syncthreads();  // the results visible to their owners
+}
+
+// manifold fields of a Collide task in a contact row
+enum { MT_MTYPE = 0, MT_COUNT, MT_LN, MT_LP = MT_LN + 2, MT_PL0 = MT_LP + 2, MT_PL1 = MT_PL0 + 2, MT_ID0 = MT_PL1 + 2,
+       MT_ID1, MT_N };
+static_assert(MT_N <= CF_N, "a manifold must fit a contact row");
+
 // b2ContactManager::Collide (pairs.py:38-87): the list newest first, a contact with both bodies inactive skipped,
 // separated fat AABBs destroy it (waking both bodies if it still had points), the rest updated (waking both bodies
 // when touching flips). Wakes change which later contacts are visited, as in Box2D's walk.
-GOI_D void collide_walk(const DModel& m, const World& W, float linear_slop) {
+//
+// The manifolds are pure functions of the fixtures and the body transforms, which Collide does not change, so the
+// walk runs in three passes with the same results: each world marks the live contacts with overlapping fat AABBs
+// (W.cisl(k) = task index, or -1), the block evaluates all their manifolds (coop_run), and each world walks its list
+// with the wake cascade, taking the precomputed manifold of each contact it updates. A contact the walk skips (both
+// bodies asleep) had its manifold evaluated for nothing, which changes no result.
+GOI_D int collide_mark(const DModel& m, const World& W) {
+    const int n = list_order(W);
+    int nt = 0;
+    for (int i = 0; i < n; ++i) {
+        const int k = W.order(i);
+        W.cisl(k) = -1;
+        if (!overlap(fat_of(m, W, W.fa(k)), fat_of(m, W, W.fb(k)))) continue;
+        W.newp(nt) = k;
+        W.cisl(k) = nt++;
+    }
+    return nt;
+}
+
+GOI_D void collide_task(const DModel& m, const Coop& co, int o, int i, float linear_slop) {
+    const World W = co.world(o);
+    const Rows R = co.task_rows(o);
+    const int k = W.newp(i);
+    const int fa = W.fa(k), fb = W.fb(k);
+    Manifold mf;
+    evaluate(m, fa, fb, W.xf(m.fixture_body[fa]), W.xf(m.fixture_body[fb]), linear_slop, mf);
+    R.seti(i, MT_MTYPE, mf.mtype);
+    R.seti(i, MT_COUNT, mf.count);
+    R.set2(i, MT_LN, mf.ln);
+    R.set2(i, MT_LP, mf.lp);
+    R.set2(i, MT_PL0, mf.pl0);
+    R.set2(i, MT_PL1, mf.pl1);
+    R.seti(i, MT_ID0, mf.id0);
+    R.seti(i, MT_ID1, mf.id1);
+}
+
+GOI_D void collide_apply(const DModel& m, const World& W, const Rows& R) {
     const int n = list_order(W);
     for (int i = 0; i < n; ++i) {
         const int k = W.order(i);
-        const int fa = W.fa(k), fb = W.fb(k);
-        const int ba = m.fixture_body[fa], bb = m.fixture_body[fb];
+        const int ba = m.fixture_body[W.fa(k)], bb = m.fixture_body[W.fb(k)];
         const bool act_a = W.awake(ba) && m.body_type[ba] != GOI_STATIC;
         const bool act_b = W.awake(bb) && m.body_type[bb] != GOI_STATIC;
         if (!act_a && !act_b) continue;
-        if (!overlap(fat_of(m, W, fa), fat_of(m, W, fb))) {
+        const int t = W.cisl(k);
+        if (t < 0) {
             if (W.i32(GOI_C_COUNT, k) > 0) { W.wake(ba); W.wake(bb); }
             W.pair(k) = -1;
             W.u8(GOI_C_TOUCHING, k) = 0;
@@ -85,7 +175,14 @@ GOI_D void collide_walk(const DModel& m, const World& W, float linear_slop) {
             continue;
         }
         Manifold mf;
-        evaluate(m, fa, fb, W.xf(ba), W.xf(bb), linear_slop, mf);
+        mf.mtype = R.geti(t, MT_MTYPE);
+        mf.count = R.geti(t, MT_COUNT);
+        mf.ln = R.get2(t, MT_LN);
+        mf.lp = R.get2(t, MT_LP);
+        mf.pl0 = R.get2(t, MT_PL0);
+        mf.pl1 = R.get2(t, MT_PL1);
+        mf.id0 = R.geti(t, MT_ID0);
+        mf.id1 = R.geti(t, MT_ID1);
         if (contact_update(W, k, mf)) { W.wake(ba); W.wake(bb); }
     }
     // drop the destroyed contacts from the list, keeping the order of the rest
@@ -95,6 +192,13 @@ GOI_D void collide_walk(const DModel& m, const World& W, float linear_slop) {
         if (W.pair(k) >= 0) W.order(j++) = k;
     }
     W.nlive() = j;
+}
+
+// Collide for the block: called by all lanes together; `valid` marks the lanes that own a world.
+GOI_D void collide_block(const DModel& m, const Coop& co, const World& W, bool valid, float linear_slop) {
+    const int nt = valid ? collide_mark(m, W) : 0;
+    coop_run(co, nt, [&](int o, int i) { collide_task(m, co, o, i, linear_slop); });
+    if (valid) collide_apply(m, W, co.task_rows(threadIdx.x));
 }
 
 // Sorted buffer (the workspace's newp array) of the smallest new candidate indices of one FindNewContacts call,
@@ -152,8 +256,10 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
     // stackless preorder walk: descend into a node the union overlaps, else jump past its subtree
     int nd = rows ? 0 : m.n_nodes;
     while (nd < m.n_nodes) {
-        const int2 ln = m.node_link[nd];
-        if (!overlap(U, m.node_box[nd])) {
+        const bool staged = nd < W.nk;  // the first nodes come from LDS, the rest from global memory
+        const int2 ln = staged ? W.nlink[nd] : m.node_link[nd];
+        const float4 nb = staged ? W.nbox[nd] : m.node_box[nd];
+        if (!overlap(U, nb)) {
             nd = ln.x;
             continue;
         }

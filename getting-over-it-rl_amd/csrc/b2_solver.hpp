@@ -33,47 +33,6 @@ struct Bodies {
     GOI_D void set_c(int b, V2 x, float aa) const { cx(b) = x.x; cy(b) = x.y; a(b) = aa; }
 };
 
-// Per-world HBM scratch rows: element (row, field) at base[((row * nf) + field) * pitch + w].
-struct Rows {
-    uint32_t* base;
-    int pitch, w, nf;
-    GOI_D uint32_t& u(int row, int field) const { return base[((size_t)row * nf + field) * pitch + w]; }
-    GOI_D float getf(int row, int field) const { return __uint_as_float(u(row, field)); }
-    GOI_D void setf(int row, int field, float v) const { u(row, field) = __float_as_uint(v); }
-    GOI_D int geti(int row, int field) const { return (int)u(row, field); }
-    GOI_D void seti(int row, int field, int v) const { u(row, field) = (uint32_t)v; }
-    GOI_D V2 get2(int row, int field) const { return mk(getf(row, field), getf(row, field + 1)); }
-    GOI_D void set2(int row, int field, V2 v) const { setf(row, field, v.x); setf(row, field + 1, v.y); }
-};
-
-// contact constraint row fields
-enum {
-    CF_SLOT, CF_IA, CF_IB, CF_COUNT, CF_PC_COUNT, CF_MTYPE,
-    CF_MA, CF_MB, CF_IIA, CF_IIB, CF_NX, CF_NY, CF_FRICTION, CF_TSPEED,
-    CF_RA0, CF_RA0Y, CF_RA1, CF_RA1Y, CF_RB0, CF_RB0Y, CF_RB1, CF_RB1Y,
-    CF_NMASS0, CF_NMASS1, CF_TMASS0, CF_TMASS1, CF_BIAS0, CF_BIAS1,
-    CF_NI0, CF_NI1, CF_TI0, CF_TI1, CF_K0, CF_K1, CF_K2, CF_K3, CF_NM0, CF_NM1, CF_NM2, CF_NM3,
-    CF_LN, CF_LNY, CF_LP, CF_LPY, CF_PL0, CF_PL0Y, CF_PL1, CF_PL1Y, CF_LCA, CF_LCAY, CF_LCB, CF_LCBY,
-    CF_RADA, CF_RADB,
-    CF_N
-};
-
-// joint row fields
-enum {
-    JF_JID, JF_TYPE, JF_IA, JF_IB, JF_STATE, JF_EMOTOR, JF_ELIMIT, JF_SOFT,
-    JF_MA, JF_MB, JF_IIA, JF_IIB, JF_RA, JF_RAY, JF_RB, JF_RBY,
-    JF_EXX, JF_EXY, JF_EXZ, JF_EYX, JF_EYY, JF_EYZ, JF_EZX, JF_EZY, JF_EZZ,
-    JF_MMASS, JF_MSPEED, JF_MAXIMP, JF_AX, JF_AXY, JF_PX, JF_PXY, JF_A1, JF_A2, JF_S1, JF_S2,
-    JF_GAMMA, JF_BIAS, JF_ANGLE, JF_INVDT, JF_LA, JF_LAY, JF_LB, JF_LBY, JF_LX, JF_LXY, JF_LY, JF_LYY,
-    JF_REF, JF_LOWER, JF_UPPER, JF_IMP0, JF_IMP1, JF_IMP2, JF_IMP3, JF_IMP4, JF_MIMP,
-    JF_N
-};
-
-struct Cfg {
-    GoiSettings s;
-    float dt, inv_dt, dt_ratio_unused;
-};
-
 GOI_D V2 rel_vel(V2 vB, float wB, V2 rB, V2 vA, float wA, V2 rA) {
     return ((vB + cross(wB, rB)) - vA) - cross(wA, rA);
 }

@@ -218,7 +218,7 @@ GOI_D bool pair_rule(const DModel& m, const World& W, const GoiSettings& s, int 
 // depend only on alpha0 values, never on TOI results, so the walk splits into three passes with the same results:
 //   1. toi_search_prepare (each world, list order): the alignments, with each TOI's inputs (fixtures, both sweeps
 //      as aligned at that contact, alpha0) snapshotted into the world's contact row `task`;
-//   2. toi_tasks_run (the whole wavefront): the TOIs of all worlds of the block, spread over all 64 lanes;
+//   2. toi_task under coop_run (the whole wavefront): the TOIs of all worlds of the block, over all 64 lanes;
 //   3. toi_search_pick (each world, list order): the minimum with the reference's tie rule.
 
 // task snapshot fields in a contact row
@@ -253,58 +253,25 @@ GOI_D int toi_search_prepare(const DModel& m, const World& W, const Rows& CR, co
         put_sweep(CR, nt, TT_SA, body_sweep(W, A));
         put_sweep(CR, nt, TT_SB, body_sweep(W, Bb));
         W.newp(nt++) = c;
-        W.tflag(c) = 1;  // the toi itself arrives in pass 2
+        W.set_tflag(c, 1);  // the toi itself arrives in pass 2
     }
     return nt;
 }
 
-// The block's view for pass 2: every lane of the wavefront computes TOI tasks of any world of the block.
-struct ToiCoop {
-    int* lds;        // the block's LDS workspace (lane 0's base)
-    int* scan;       // 64 ints after the workspaces
-    int S;           // worlds (lanes with a world) per block
-    Workspace k;
-    uint32_t* rows;  // contact rows (Launch.scratch)
-    int pitch, w0;   // row pitch, the block's first world
-    int lanes;       // lanes sharing the tasks (the block size)
-};
-
-// pass 2: called by all 64 lanes of the block together; `my` = this lane's task count (0 for lanes without one)
-GOI_D void toi_tasks_run(const DModel& m, const ToiCoop& co, int my, float linear_slop) {
-    const int lane = threadIdx.x;
-    int incl = my;
-    for (int d = 1; d < 64; d <<= 1) {
-        const int v = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += v;
-    }
-    const int total = __shfl(incl, 63, 64);
-    if (total == 0) return;
-    co.scan[lane] = incl;
-    __syncthreads();  // scan entries and the owners' task rows visible to the whole block
-    for (int t = lane; t < total; t += co.lanes) {
-        int lo = 0, hi = 63;  // owner: the first lane whose inclusive count exceeds t
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (co.scan[mid] > t) hi = mid; else lo = mid + 1;
-        }
-        const int o = lo;
-        const int i = t - (o ? co.scan[o - 1] : 0);
-        Rows R;
-        R.base = co.rows; R.pitch = co.pitch; R.w = co.w0 + o; R.nf = CF_N;
-        Sweep sa, sb;
-        sa.lc = R.get2(i, TT_SA); sa.c0 = R.get2(i, TT_SA + 2); sa.c = R.get2(i, TT_SA + 4);
-        sa.a0 = R.getf(i, TT_SA + 6); sa.a = R.getf(i, TT_SA + 7);
-        sb.lc = R.get2(i, TT_SB); sb.c0 = R.get2(i, TT_SB + 2); sb.c = R.get2(i, TT_SB + 4);
-        sb.a0 = R.getf(i, TT_SB + 6); sb.a = R.getf(i, TT_SB + 7);
-        const float alpha0 = R.getf(i, TT_ALPHA0);
-        float beta;
-        const int st = time_of_impact(proxy_of(m, R.geti(i, TT_FA)), sa, proxy_of(m, R.geti(i, TT_FB)), sb,
-                                      linear_slop, beta);
-        const float alpha = st == kToiTouching ? bmin(alpha0 + (1.0f - alpha0) * beta, 1.0f) : 1.0f;
-        const int c = co.lds[(co.k.o_newp + i) * co.S + o];
-        reinterpret_cast<float*>(co.lds)[(co.k.o_ttoi + c) * co.S + o] = alpha;
-    }
-    __syncthreads();  // the tois visible to their owners
+// pass 2: the TOI of task i of the world on lane o
+GOI_D void toi_task(const DModel& m, const Coop& co, int o, int i, float linear_slop) {
+    const Rows R = co.task_rows(o);
+    Sweep sa, sb;
+    sa.lc = R.get2(i, TT_SA); sa.c0 = R.get2(i, TT_SA + 2); sa.c = R.get2(i, TT_SA + 4);
+    sa.a0 = R.getf(i, TT_SA + 6); sa.a = R.getf(i, TT_SA + 7);
+    sb.lc = R.get2(i, TT_SB); sb.c0 = R.get2(i, TT_SB + 2); sb.c = R.get2(i, TT_SB + 4);
+    sb.a0 = R.getf(i, TT_SB + 6); sb.a = R.getf(i, TT_SB + 7);
+    const float alpha0 = R.getf(i, TT_ALPHA0);
+    float beta;
+    const int st = time_of_impact(proxy_of(m, R.geti(i, TT_FA)), sa, proxy_of(m, R.geti(i, TT_FB)), sb, linear_slop,
+                                  beta);
+    const World W = co.world(o);
+    W.ttoi(W.newp(i)) = st == kToiTouching ? bmin(alpha0 + (1.0f - alpha0) * beta, 1.0f) : 1.0f;
 }
 
 // pass 3; returns whether an event was found
@@ -352,15 +319,15 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         evaluate(m, fa, fb, W.xf(A), W.xf(Bb), s.linear_slop, mf);
         if (contact_update(W, min_slot, mf)) { W.wake(A); W.wake(Bb); }
     }
-    W.tflag(min_slot) = 0;
-    W.tcount(min_slot) += 1;
+    W.set_tflag(min_slot, 0);
+    W.set_tcount(min_slot, W.tcount(min_slot) + 1);
     if (!W.u8(GOI_C_TOUCHING, min_slot)) {
-        W.ten(min_slot) = 0;
+        W.set_ten(min_slot, 0);
         restore(W, A, bkA);
         restore(W, Bb, bkB);
         return;
     }
-    W.ten(min_slot) = 1;
+    W.set_ten(min_slot, 1);
     W.wake(A);
     W.wake(Bb);
     // the island walk: bodyA's then bodyB's contact lists, newest first, at most 32 contacts / 64 bodies; island
@@ -388,7 +355,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
             Manifold mf;
             evaluate(m, W.fa(c), W.fb(c), W.xf(ca), W.xf(cb), s.linear_slop, mf);
             if (contact_update(W, c, mf)) { W.wake(ca); W.wake(cb); }
-            W.ten(c) = 1;
+            W.set_ten(c, 1);
             if (!W.u8(GOI_C_TOUCHING, c)) {
                 restore(W, other, bk);
                 continue;
@@ -471,7 +438,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     for (int c = 0; c < W.C; ++c) {
         if (W.pair(c) < 0) continue;
         const int ca = m.fixture_body[W.fa(c)], cb = m.fixture_body[W.fb(c)];
-        if (((moved >> ca) & 1ull) || ((moved >> cb) & 1ull)) W.tflag(c) = 0;
+        if (((moved >> ca) & 1ull) || ((moved >> cb) & 1ull)) W.set_tflag(c, 0);
     }
     // FindNewContacts; a slot that received a new contact starts with fresh TOI state. The keys before it go to
     // the workspace's corder array, which Solve's island order no longer needs.
@@ -483,9 +450,9 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     find_new_contacts(m, W, W.i32(GOI_S_OVERFLOW, 0) == 0 ? refat : ~0ull);
     for (int c = 0; c < W.C; ++c) {
         if (W.pair(c) >= 0 && (((was_free >> c) & 1ull) || W.corder(c) != W.key(c))) {
-            W.tcount(c) = 0;
-            W.tflag(c) = 0;
-            W.ten(c) = 1;
+            W.set_tcount(c, 0);
+            W.set_tflag(c, 0);
+            W.set_ten(c, 1);
         }
     }
 }
@@ -493,16 +460,16 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
 // b2World::SolveTOI (toi.py:827-865). Called by every lane of the block (the TOI searches are cooperative);
 // `valid` marks the lanes that own a world.
 GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
-                           float dt, bool valid, const ToiCoop& co) {
+                           float dt, bool valid, const Coop& co) {
     if (W.C == 0 || m.P == 0) return;
     if (s.unity_toi && !m.any_toi_body) return;
     if (valid) {
         for (int b = 0; b < W.B; ++b) W.f(GOI_T_ALPHA0, b) = 0.0f;
         for (int c = 0; c < W.C; ++c) {
-            W.tcount(c) = 0;
+            W.set_tcount(c, 0);
             W.ttoi(c) = 1.0f;
-            W.tflag(c) = 0;
-            W.ten(c) = 1;
+            W.set_tflag(c, 0);
+            W.set_ten(c, 1);
             W.u8(GOI_T_SOLVED, c) = 0;
             W.f(GOI_T_NORMAL_IMPULSE, 2 * c) = 0.0f;
             W.f(GOI_T_NORMAL_IMPULSE, 2 * c + 1) = 0.0f;
@@ -515,7 +482,8 @@ GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, co
         const int max_events = s.max_events >= 0 ? s.max_events : W.C * (kMaxSubSteps + 1) + 8;
         int slot = -1;
         float alpha = 1.0f;
-        toi_tasks_run(m, co, valid ? toi_search_prepare(m, W, CR, s) : 0, s.linear_slop);
+        const auto toi = [&](int o, int i) { toi_task(m, co, o, i, s.linear_slop); };
+        coop_run(co, valid ? toi_search_prepare(m, W, CR, s) : 0, toi);
         bool found = valid && toi_search_pick(W, s, slot, alpha);
         // the block iterates while any world has an event to process; the others take part in the searches only
         while (__any(found && events < max_events)) {
@@ -524,7 +492,7 @@ GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, co
                 toi_event(m, W, bd, CR, s, dt, slot, alpha);
                 ++events;
             }
-            toi_tasks_run(m, co, act ? toi_search_prepare(m, W, CR, s) : 0, s.linear_slop);
+            coop_run(co, act ? toi_search_prepare(m, W, CR, s) : 0, toi);
             found = act && toi_search_pick(W, s, slot, alpha);
         }
     }

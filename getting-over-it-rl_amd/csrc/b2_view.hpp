@@ -56,7 +56,7 @@ struct DModel {
 // whole step (loaded once, written back once) and holds the per-world work arrays (contact list order, island
 // lists and stacks, new-pair buffer), which would otherwise live in private scratch memory.
 struct Workspace {
-    int o_pair, o_key, o_fa, o_fb, o_tflag, o_ten, o_tcount, o_ttoi, o_order, o_newp, o_corder, o_cisl;  // [C]
+    int o_pair, o_key, o_fa, o_fb, o_tmeta, o_ttoi, o_order, o_newp, o_corder, o_cisl;  // [C]
     int o_awake, o_active, o_bisl, o_stack, o_fwork, o_ibuf;                                            // [B]
     int o_qbox;                                                                                         // [4 R]
     int o_nlive;                                                                                        // [1]
@@ -68,7 +68,7 @@ struct Workspace {
         int o = 0;
         k.o_body = o; o += 8 * B;
         k.o_pair = o; o += C; k.o_key = o; o += C; k.o_fa = o; o += C; k.o_fb = o; o += C;
-        k.o_tflag = o; o += C; k.o_ten = o; o += C; k.o_tcount = o; o += C; k.o_ttoi = o; o += C;
+        k.o_tmeta = o; o += C; k.o_ttoi = o; o += C;
         k.o_order = o; o += C; k.o_newp = o; o += C; k.o_corder = o; o += C; k.o_cisl = o; o += C;
         k.o_awake = o; o += B; k.o_active = o; o += B; k.o_bisl = o; o += B; k.o_stack = o; o += B; k.o_fwork = o; o += B; k.o_ibuf = o; o += B;
         k.o_jorder = o; o += J; k.o_jisl = o; o += J;
@@ -88,6 +88,9 @@ struct World {
     int* ws;          // LDS workspace base + lane
     int S;            // workspace stride (lanes per block)
     Workspace k;
+    const float4* nbox;  // the static BVH's first nk nodes, staged in LDS by the block
+    const int2* nlink;
+    int nk;
 
     GOI_D int& wi(int off, int i) const { return ws[(off + i) * S]; }
     GOI_D float& wf(int off, int i) const { return reinterpret_cast<float*>(ws)[(off + i) * S]; }
@@ -98,9 +101,13 @@ struct World {
     GOI_D int& fb(int c) const { return wi(k.o_fb, c); }          // contacts.fb
     GOI_D int& awake(int b) const { return wi(k.o_awake, b); }    // bodies.awake
     GOI_D int& active(int b) const { return wi(k.o_active, b); }  // bodies.active (read-only in a step)
-    GOI_D int& tflag(int c) const { return wi(k.o_tflag, c); }    // toi.flag
-    GOI_D int& ten(int c) const { return wi(k.o_ten, c); }        // toi.enabled
-    GOI_D int& tcount(int c) const { return wi(k.o_tcount, c); }  // toi.count
+    // toi.flag (bit 0), toi.enabled (bit 1) and toi.count (bits 8-15) of a slot, packed in one word
+    GOI_D int tflag(int c) const { return wi(k.o_tmeta, c) & 1; }
+    GOI_D int ten(int c) const { return (wi(k.o_tmeta, c) >> 1) & 1; }
+    GOI_D int tcount(int c) const { return (wi(k.o_tmeta, c) >> 8) & 0xff; }
+    GOI_D void set_tflag(int c, int v) const { int& t = wi(k.o_tmeta, c); t = (t & ~1) | (v ? 1 : 0); }
+    GOI_D void set_ten(int c, int v) const { int& t = wi(k.o_tmeta, c); t = (t & ~2) | (v ? 2 : 0); }
+    GOI_D void set_tcount(int c, int v) const { int& t = wi(k.o_tmeta, c); t = (t & 0xff) | (v << 8); }
     GOI_D float& ttoi(int c) const { return wf(k.o_ttoi, c); }    // toi.toi
     // work arrays
     GOI_D int& order(int i) const { return wi(k.o_order, i); }
@@ -203,5 +210,42 @@ GOI_D bool overlap(float4 a, float4 b) {
     float d2x = a.x - b.z, d2y = a.y - b.w;
     return !(d1x > 0.0f || d1y > 0.0f || d2x > 0.0f || d2y > 0.0f);
 }
+
+// Per-world HBM scratch rows: element (row, field) at base[((row * nf) + field) * pitch + w].
+struct Rows {
+    uint32_t* base;
+    int pitch, w, nf;
+    GOI_D uint32_t& u(int row, int field) const { return base[((size_t)row * nf + field) * pitch + w]; }
+    GOI_D float getf(int row, int field) const { return __uint_as_float(u(row, field)); }
+    GOI_D void setf(int row, int field, float v) const { u(row, field) = __float_as_uint(v); }
+    GOI_D int geti(int row, int field) const { return (int)u(row, field); }
+    GOI_D void seti(int row, int field, int v) const { u(row, field) = (uint32_t)v; }
+    GOI_D V2 get2(int row, int field) const { return mk(getf(row, field), getf(row, field + 1)); }
+    GOI_D void set2(int row, int field, V2 v) const { setf(row, field, v.x); setf(row, field + 1, v.y); }
+};
+
+// contact constraint row fields
+enum {
+    CF_SLOT, CF_IA, CF_IB, CF_COUNT, CF_PC_COUNT, CF_MTYPE,
+    CF_MA, CF_MB, CF_IIA, CF_IIB, CF_NX, CF_NY, CF_FRICTION, CF_TSPEED,
+    CF_RA0, CF_RA0Y, CF_RA1, CF_RA1Y, CF_RB0, CF_RB0Y, CF_RB1, CF_RB1Y,
+    CF_NMASS0, CF_NMASS1, CF_TMASS0, CF_TMASS1, CF_BIAS0, CF_BIAS1,
+    CF_NI0, CF_NI1, CF_TI0, CF_TI1, CF_K0, CF_K1, CF_K2, CF_K3, CF_NM0, CF_NM1, CF_NM2, CF_NM3,
+    CF_LN, CF_LNY, CF_LP, CF_LPY, CF_PL0, CF_PL0Y, CF_PL1, CF_PL1Y, CF_LCA, CF_LCAY, CF_LCB, CF_LCBY,
+    CF_RADA, CF_RADB,
+    CF_N
+};
+
+// joint row fields
+enum {
+    JF_JID, JF_TYPE, JF_IA, JF_IB, JF_STATE, JF_EMOTOR, JF_ELIMIT, JF_SOFT,
+    JF_MA, JF_MB, JF_IIA, JF_IIB, JF_RA, JF_RAY, JF_RB, JF_RBY,
+    JF_EXX, JF_EXY, JF_EXZ, JF_EYX, JF_EYY, JF_EYZ, JF_EZX, JF_EZY, JF_EZZ,
+    JF_MMASS, JF_MSPEED, JF_MAXIMP, JF_AX, JF_AXY, JF_PX, JF_PXY, JF_A1, JF_A2, JF_S1, JF_S2,
+    JF_GAMMA, JF_BIAS, JF_ANGLE, JF_INVDT, JF_LA, JF_LAY, JF_LB, JF_LBY, JF_LX, JF_LXY, JF_LY, JF_LYY,
+    JF_REF, JF_LOWER, JF_UPPER, JF_IMP0, JF_IMP1, JF_IMP2, JF_IMP3, JF_IMP4, JF_MIMP,
+    JF_N
+};
+
 
 }  // namespace goi

@@ -44,11 +44,16 @@ struct Launch {
     void* leaf[GOI_NUM_LEAVES];
     int n, pitch, B, C, R, J;
     int wpw;  // worlds per wavefront: lanes >= wpw idle, so small batches still spread over every SIMD
+    int lds_nodes;  // BVH nodes staged in LDS per block
     uint32_t* scratch;  // contact rows then joint rows
     GoiSettings s;
     float dt;
     GoiDebug dbg;
 };
+
+// The block's LDS: the worlds' workspaces (words x wpw ints), 64 ints of scan space, then the staged BVH nodes
+// (float4 boxes, then int2 links) at a 16-byte aligned offset.
+__host__ __device__ inline int node_offset(int words, int wpw) { return ((words * wpw + kBlock) + 3) & ~3; }
 
 // World w on lane `lane` of its block; the block's LDS workspace holds L.wpw lanes.
 __device__ __forceinline__ World make_world(const Launch& L, int w, int* lds, int lane) {
@@ -63,7 +68,22 @@ __device__ __forceinline__ World make_world(const Launch& L, int w, int* lds, in
     W.k = Workspace::layout(L.B, L.C, L.J, L.R);
     W.ws = lds + lane;
     W.S = L.wpw;
+    W.nk = L.lds_nodes;
+    W.nbox = reinterpret_cast<const float4*>(lds + node_offset(W.k.words, L.wpw));
+    W.nlink = reinterpret_cast<const int2*>(W.nbox + L.lds_nodes);
     return W;
+}
+
+// All lanes of the block copy the first L.lds_nodes BVH nodes into LDS.
+__device__ __forceinline__ void stage_nodes(const DModel& m, const Launch& L, int* lds) {
+    const int words = Workspace::layout(L.B, L.C, L.J, L.R).words;
+    float4* box = reinterpret_cast<float4*>(lds + node_offset(words, L.wpw));
+    int2* link = reinterpret_cast<int2*>(box + L.lds_nodes);
+    for (int i = threadIdx.x; i < L.lds_nodes; i += kBlock) {
+        box[i] = m.node_box[i];
+        link[i] = m.node_link[i];
+    }
+    __syncthreads();
 }
 
 __device__ __forceinline__ Rows contact_rows(const Launch& L, int w) {
@@ -85,27 +105,47 @@ __device__ __forceinline__ Rows joint_rows(const Launch& L, int w) {
 
 // ---------------------------------------------------------------- kernels
 
-__global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int start_only) {
-    extern __shared__ int lds[];
-    const int w = blockIdx.x * L.wpw + threadIdx.x;
-    if ((int)threadIdx.x >= L.wpw || w >= L.n) return;
-    const World W = make_world(L, w, lds, threadIdx.x);
-    W.load_mirror();
-    build_order(W);
-    if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
-    W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
-    if (!start_only) collide_walk(m, W, L.s.linear_slop);
-    W.store_mirror();
+// The block's cooperative view (Coop) for lanes whose world is W (or lane 0's, for lanes without one).
+__device__ __forceinline__ Coop block_coop(const Launch& L, const World& W, int* lds, int w0) {
+    Coop co;
+    co.base = W;
+    co.lds = lds;
+    co.scan = lds + W.k.words * L.wpw;
+    co.rows = L.scratch;
+    co.w0 = w0;
+    co.lanes = kBlock;
+    return co;
 }
 
-// The whole b2World::Step (step.py:28-47) of one world per lane: FindNewContacts where new_fixture, Collide,
-// Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to help with the block's TOI searches.
-__global__ void __launch_bounds__(kBlock) k_step(DModel m, Launch L) {
+// Start-of-step FindNewContacts where new_fixture, then Collide (unless start_only). All lanes of the block take
+// part in Collide's manifold evaluations.
+__global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int start_only) {
     extern __shared__ int lds[];
+    stage_nodes(m, L, lds);
     const int lane = threadIdx.x;
     const int w0 = blockIdx.x * L.wpw;
     const bool valid = lane < L.wpw && w0 + lane < L.n;
     const World W = make_world(L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
+    if (valid) {
+        W.load_mirror();
+        build_order(W);
+        if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
+        W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
+    }
+    if (!start_only) collide_block(m, block_coop(L, W, lds, w0), W, valid, L.s.linear_slop);
+    if (valid) W.store_mirror();
+}
+
+// The whole b2World::Step (step.py:28-47) of one world per lane: FindNewContacts where new_fixture, Collide,
+// Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to share the block's manifold and TOI work.
+__global__ void __launch_bounds__(kBlock) k_step(DModel m, Launch L) {
+    extern __shared__ int lds[];
+    stage_nodes(m, L, lds);
+    const int lane = threadIdx.x;
+    const int w0 = blockIdx.x * L.wpw;
+    const bool valid = lane < L.wpw && w0 + lane < L.n;
+    const World W = make_world(L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
+    const Coop co = block_coop(L, W, lds, w0);
     Bodies bd;
     bd.s = reinterpret_cast<float*>(lds) + W.k.o_body * W.S + (valid ? lane : 0);
     bd.B = L.B;
@@ -116,21 +156,10 @@ __global__ void __launch_bounds__(kBlock) k_step(DModel m, Launch L) {
         build_order(W);
         if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
         W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
-        collide_walk(m, W, L.s.linear_slop);
-        solve_world(m, W, bd, CR, joint_rows(L, W.w), L.s, L.dt, L.dbg);
     }
-    if (L.s.continuous_physics) {
-        ToiCoop co;
-        co.lds = lds;
-        co.scan = lds + W.k.words * L.wpw;
-        co.S = L.wpw;
-        co.k = W.k;
-        co.rows = L.scratch;
-        co.pitch = L.pitch;
-        co.w0 = w0;
-        co.lanes = kBlock;
-        solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, co);
-    }
+    collide_block(m, co, W, valid, L.s.linear_slop);
+    if (valid) solve_world(m, W, bd, CR, joint_rows(L, W.w), L.s, L.dt, L.dbg);
+    if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, co);
     if (!valid) return;
     const float dt = L.dt;
     if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
@@ -385,8 +414,23 @@ static int check_view(const GoiModel* M, const GoiStateView* v, const char* who)
     return GOI_OK;
 }
 
+// Compute units of the current device (cached per process; one device per process is the common case).
+static int cu_count() {
+    static int n = 0;
+    if (n <= 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) ==
+                                                    hipSuccess && v > 0)
+            n = v;
+        else
+            n = 256;
+    }
+    return n;
+}
+
 // LDS workspace bytes per world (Workspace::layout) and the block budget it is held to.
-constexpr size_t kMaxLdsBytes = 64 * 1024;
+constexpr size_t kMaxLdsBytes = 64 * 1024;   // workspaces + scan space of one block
+constexpr size_t kCuLdsBytes = 160 * 1024;    // LDS of one CU, shared by the blocks resident on it
 static size_t workspace_bytes(int B, int C, int J, int R) {
     return (size_t)Workspace::layout(B, C, J, R).words * sizeof(int);
 }
@@ -403,16 +447,23 @@ static int worlds_per_wave(int n, size_t ws_bytes_per_world) {
     }
     if (forced > 0)
         return std::min<long>(forced, std::max<long>(1, (kMaxLdsBytes - kBlock * sizeof(int)) / ws_bytes_per_world));
-    // Fewer worlds per wave raise the wave count (latency hiding) but spend a full wave instruction on fewer lanes.
-    // Measured at 16384 worlds of the 4-body rig: 64 -> 3.81 ms, 32 -> 3.51, 16 -> 3.51, 8 -> 4.54, 4 -> 5.70;
-    // keep at least 512 waves (two per CU) and otherwise pack as many worlds per wave as possible.
+    // Fewer worlds per wave fill more SIMDs, shrink the slowest lane a wave waits for and give each world more lanes
+    // in the block-cooperative passes, but past one wave per SIMD (the register budget of k_step allows one) the
+    // launch needs a second round. Measured at 16384 worlds of the 4-body rig: 32 -> 1.56 ms, 16 -> 1.48, 8 -> 2.08.
+    // Aim for one wave per SIMD (4 per CU).
     int wpw = kBlock;
-    while (wpw > 1 && (long)n / wpw < 512) wpw /= 2;
+    while (wpw > 1 && (long)n / wpw < 4L * cu_count()) wpw /= 2;
     while (wpw > 1 && ws_bytes_per_world * wpw + kBlock * sizeof(int) > kMaxLdsBytes) wpw /= 2;
     return wpw;
 }
 
-static void fill_launch(Launch& L, const GoiStateView* v, const GoiSettings* s, float dt) {
+// LDS bytes of one block of launch L
+static size_t block_lds_bytes(const Launch& L) {
+    const int words = Workspace::layout(L.B, L.C, L.J, L.R).words;
+    return (size_t)node_offset(words, L.wpw) * sizeof(int) + (size_t)L.lds_nodes * (sizeof(float4) + sizeof(int2));
+}
+
+static void fill_launch(Launch& L, const GoiModel* M, const GoiStateView* v, const GoiSettings* s, float dt) {
     std::memcpy(L.leaf, v->leaf, sizeof(L.leaf));
     L.n = v->n_worlds;
     L.pitch = v->pitch;
@@ -425,6 +476,27 @@ static void fill_launch(Launch& L, const GoiStateView* v, const GoiSettings* s, 
     std::memset(&L.dbg, 0, sizeof(L.dbg));
     L.scratch = nullptr;
     L.wpw = worlds_per_wave(v->n_worlds, workspace_bytes(v->B, v->C, v->J, v->R));
+    // Stage as many BVH nodes (preorder: the root and the tree's upper-left part first) as the LDS left over allows
+    // when every block of the launch is resident at once (ceil(blocks / CUs) per CU).
+    const long blocks = (v->n_worlds + L.wpw - 1) / L.wpw;
+    const long per_cu = std::max<long>(1, (blocks + cu_count() - 1) / cu_count());
+    const size_t budget = kCuLdsBytes / per_cu;
+    const size_t base = (size_t)node_offset(Workspace::layout(v->B, v->C, v->J, v->R).words, L.wpw) * sizeof(int);
+    const size_t room = base < budget ? (budget - base) / (sizeof(float4) + sizeof(int2)) : 0;
+    L.lds_nodes = (int)std::min<size_t>((size_t)M->d.n_nodes, room);
+}
+
+// The model's scratch rows (per world: C contact rows, J joint rows), grown to the batch's pitch on demand.
+static int ensure_scratch(GoiModel* M, const GoiStateView* state) {
+    const size_t words = ((size_t)state->C * CF_N + (size_t)state->J * JF_N) * state->pitch;
+    if (words > M->scratch_words) {
+        if (M->scratch) HIP_TRY(hipFree(M->scratch));
+        M->scratch = nullptr;
+        M->scratch_words = 0;
+        HIP_TRY(hipMalloc(&M->scratch, std::max<size_t>(words, 1) * sizeof(uint32_t)));
+        M->scratch_words = words;
+    }
+    return GOI_OK;
 }
 
 int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
@@ -436,21 +508,15 @@ int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSett
         return fail(GOI_E_ARG, "goi_step: negative iteration counts");
     if (state->n_worlds == 0) return GOI_OK;
     GoiModel* M = const_cast<GoiModel*>(model);
-    const size_t words = ((size_t)state->C * CF_N + (size_t)state->J * JF_N) * state->pitch;
-    if (words > M->scratch_words) {
-        if (M->scratch) HIP_TRY(hipFree(M->scratch));
-        M->scratch = nullptr;
-        M->scratch_words = 0;
-        HIP_TRY(hipMalloc(&M->scratch, std::max<size_t>(words, 1) * sizeof(uint32_t)));
-        M->scratch_words = words;
-    }
+    rc = ensure_scratch(M, state);
+    if (rc != GOI_OK) return rc;
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
     Launch L;
-    fill_launch(L, state, settings, dt);
+    fill_launch(L, M, state, settings, dt);
     L.scratch = M->scratch;
     if (debug) L.dbg = *debug;
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
-    const size_t lds = workspace_bytes(state->B, state->C, state->J, state->R) * L.wpw + kBlock * sizeof(int);
+    const size_t lds = block_lds_bytes(L);
     hipLaunchKernelGGL(k_step, dim3(grid), dim3(kBlock), lds, st, M->d, L);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
@@ -462,9 +528,12 @@ int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiS
     if (!settings) return fail(GOI_E_ARG, "goi_collide: null settings");
     if (state->n_worlds == 0) return GOI_OK;
     Launch L;
-    fill_launch(L, state, settings, 0.0f);
+    fill_launch(L, model, state, settings, 0.0f);
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
-    const size_t lds = workspace_bytes(state->B, state->C, state->J, state->R) * L.wpw;
+    rc = ensure_scratch(const_cast<GoiModel*>(model), state);
+    if (rc != GOI_OK) return rc;
+    L.scratch = model->scratch;
+    const size_t lds = block_lds_bytes(L);
     hipLaunchKernelGGL(k_collide, dim3(grid), dim3(kBlock), lds, static_cast<hipStream_t>(hip_stream), model->d, L, 0);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
