@@ -147,7 +147,7 @@ GOI_D void collide_task(const DModel& m, const Coop& co, int o, int i, float lin
     const int k = W.newp(i);
     const int fa = W.fa(k), fb = W.fb(k);
     Manifold mf;
-    evaluate(m, fa, fb, W.xf(m.fixture_body[fa]), W.xf(m.fixture_body[fb]), linear_slop, mf);
+    evaluate(m, fa, fb, W.xf(W.ba(k)), W.xf(W.bb(k)), linear_slop, mf);
     R.seti(i, MT_MTYPE, mf.mtype);
     R.seti(i, MT_COUNT, mf.count);
     R.set2(i, MT_LN, mf.ln);
@@ -162,9 +162,9 @@ GOI_D void collide_apply(const DModel& m, const World& W, const Rows& R) {
     const int n = list_order(W);
     for (int i = 0; i < n; ++i) {
         const int k = W.order(i);
-        const int ba = m.fixture_body[W.fa(k)], bb = m.fixture_body[W.fb(k)];
-        const bool act_a = W.awake(ba) && m.body_type[ba] != GOI_STATIC;
-        const bool act_b = W.awake(bb) && m.body_type[bb] != GOI_STATIC;
+        const int ba = W.ba(k), bb = W.bb(k);
+        const bool act_a = W.awake(ba) && !W.is_static(ba);
+        const bool act_b = W.awake(bb) && !W.is_static(bb);
         if (!act_a && !act_b) continue;
         const int t = W.cisl(k);
         if (t < 0) {
@@ -246,7 +246,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
     unsigned long long rows = 0ull;
     float4 U = make_float4(kMaxFloat, kMaxFloat, -kMaxFloat, -kMaxFloat);
     for (int r = 0; r < m.R; ++r) {
-        if (!((query_rows >> r) & 1ull) || !W.active(m.fixture_body[m.slot_fixture[r]])) continue;
+        if (!((query_rows >> r) & 1ull) || !W.active(m.row_body[r])) continue;
         const float4 q = make_float4(W.f(GOI_F_FAT, 4 * r), W.f(GOI_F_FAT, 4 * r + 1), W.f(GOI_F_FAT, 4 * r + 2),
                                      W.f(GOI_F_FAT, 4 * r + 3));
         W.set_qbox(r, q);
@@ -298,7 +298,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         if (!(((query_rows >> m.fixture_slot[a]) | (query_rows >> m.fixture_slot[b])) & 1ull)) continue;
         const int ba = m.fixture_body[a], bb = m.fixture_body[b];
         if (!overlap(fat_of(m, W, a), fat_of(m, W, b))) continue;
-        if (!(m.body_type[ba] == GOI_DYNAMIC || m.body_type[bb] == GOI_DYNAMIC)) continue;
+        if (!(W.is_dynamic(ba) || W.is_dynamic(bb))) continue;
         if (!(W.active(ba) && W.active(bb))) continue;
         if (slot_has_pair(W, p)) continue;
         np.add(p);
@@ -331,8 +331,10 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         const float ra = restitution_of(m, W, a), rb = restitution_of(m, W, b);
         W.f(GOI_C_RESTITUTION, k) = ra > rb ? ra : rb;                                // b2MixRestitution
         W.f(GOI_C_TANGENT_SPEED, k) = 0.0f;
-        W.wake(m.fixture_body[a]);
-        W.wake(m.fixture_body[b]);
+        const int ba = m.fixture_body[a], bb = m.fixture_body[b];
+        W.set_bodies(k, ba, bb);
+        W.wake(ba);
+        W.wake(bb);
         ++k;
     }
     W.i32(GOI_S_NEXT_KEY, 0) = base_key + np.total;
@@ -363,8 +365,8 @@ GOI_D unsigned long long sync_body_fixtures(const DModel& m, const World& W, int
     unsigned long long moved = 0ull;
     const Xf x2 = W.xf(b);
     for (int r = 0; r < m.R; ++r) {
+        if (m.row_body[r] != b) continue;
         const int f = m.slot_fixture[r];
-        if (m.fixture_body[f] != b) continue;
         const float4 a1 = shape_aabb(m, f, x1), a2 = shape_aabb(m, f, x2);
         float lx = bmin(a1.x, a2.x), ly = bmin(a1.y, a2.y);
         float ux = bmax(a1.z, a2.z), uy = bmax(a1.w, a2.w);

@@ -62,7 +62,7 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
     int nisl = 0, nc = 0, nj = 0;
     for (int seed = W.B - 1; seed >= 0; --seed) {
         if ((bflag >> seed) & 1ull) continue;
-        if (!W.awake(seed) || !W.active(seed) || m.body_type[seed] == GOI_STATIC) continue;
+        if (!W.awake(seed) || !W.active(seed) || W.is_static(seed)) continue;
         const int isl = nisl++;
         int sp = 0;
         W.stack(sp++) = seed;
@@ -73,14 +73,14 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
             W.wake(b);
             for (int i = 0; i < n; ++i) {
                 const int c = W.order(i);
-                const int ba = m.fixture_body[W.fa(c)], bb = m.fixture_body[W.fb(c)];
+                const int ba = W.ba(c), bb = W.bb(c);
                 if (ba != b && bb != b) continue;
                 if (((cflag >> c) & 1ull) || !W.u8(GOI_C_TOUCHING, c)) continue;
                 I.corder(nc++) = c;
                 cflag |= 1ull << c;
                 I.contact_island(c) = isl;
                 const int other = ba == b ? bb : ba;
-                if (((bflag >> other) & 1ull) || m.body_type[other] == GOI_STATIC) continue;
+                if (((bflag >> other) & 1ull) || W.is_static(other)) continue;
                 W.stack(sp++) = other;
                 bflag |= 1ull << other;
             }
@@ -93,7 +93,7 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
                 I.jorder(nj++) = j;
                 jflag |= 1ull << j;
                 I.joint_island(j) = isl;
-                if (((bflag >> other) & 1ull) || m.body_type[other] == GOI_STATIC) continue;
+                if (((bflag >> other) & 1ull) || W.is_static(other)) continue;
                 W.stack(sp++) = other;
                 bflag |= 1ull << other;
             }
@@ -111,7 +111,7 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
 GOI_D void cs_prepare(const DModel& m, const World& W, const Bodies& bd, const Rows& R, int i, int slot, bool warm,
                       float dt_ratio, Rot qA, Rot qB, float velocity_threshold) {
     const int fa = W.fa(slot), fb = W.fb(slot);
-    const int ia = m.fixture_body[fa], ib = m.fixture_body[fb];
+    const int ia = W.ba(slot), ib = W.bb(slot);
     const float mA = W.f(GOI_B_INV_MASS, ia), mB = W.f(GOI_B_INV_MASS, ib);
     const float iA = W.f(GOI_B_INV_INERTIA, ia), iB = W.f(GOI_B_INV_INERTIA, ib);
     const V2 lcA = W.v2(GOI_B_LOCAL_CENTER, ia), lcB = W.v2(GOI_B_LOCAL_CENTER, ib);

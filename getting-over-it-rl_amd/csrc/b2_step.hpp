@@ -22,7 +22,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         const V2 c = W.v2(GOI_B_C, b);
         const float a = W.f(GOI_B_A, b);
         if (I.body_island(b) >= 0) {
-            if (m.body_type[b] == GOI_DYNAMIC) {
+            if (W.is_dynamic(b)) {
                 const float gs = W.f(GOI_B_GRAVITY_SCALE, b), im = W.f(GOI_B_INV_MASS, b);
                 const float ax = gs * gx + im * W.f(GOI_B_FORCE, 2 * b);
                 const float ay = gs * gy + im * W.f(GOI_B_FORCE, 2 * b + 1);
@@ -46,7 +46,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     const bool v24 = s.revolute_v24 != 0;
     for (int i = 0; i < I.nc; ++i) {
         const int slot = I.corder(i);
-        const int ia = m.fixture_body[W.fa(slot)], ib = m.fixture_body[W.fb(slot)];
+        const int ia = W.ba(slot), ib = W.bb(slot);
         Rot qA, qB;
         qA.c = bd.at(6, ia); qA.s = bd.at(7, ia);
         qB.c = bd.at(6, ib); qB.s = bd.at(7, ib);
@@ -141,7 +141,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         for (int i = 0; i < I.n; ++i) W.fwork(i) = kMaxFloat;  // min sleep time per island
         for (int b = 0; b < W.B; ++b) {
             const int isl = I.body_island(b);
-            if (isl < 0 || m.body_type[b] == GOI_STATIC) continue;
+            if (isl < 0 || W.is_static(b)) continue;
             const V2 v = W.v2(GOI_B_V, b);
             const float w = W.f(GOI_B_W, b);
             const bool moving = !W.u8(GOI_B_ALLOW_SLEEP, b) || w * w > ang_tol || dot(v, v) > lin_tol;
@@ -158,7 +158,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
             if (W.fwork(i) >= s.time_to_sleep && ((done >> i) & 1ull)) isl_sleep |= 1ull << i;
         for (int b = 0; b < W.B; ++b) {
             const int isl = I.body_island(b);
-            if (isl < 0 || m.body_type[b] == GOI_STATIC || !((isl_sleep >> isl) & 1ull)) continue;
+            if (isl < 0 || W.is_static(b) || !((isl_sleep >> isl) & 1ull)) continue;
             W.f(GOI_B_SLEEP_TIME, b) = 0.0f;
             W.awake(b) = 0;
             W.set2(GOI_B_V, b, mk(0.0f, 0.0f));
@@ -169,12 +169,12 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     }
     // static bodies end with the awake flag of the last island that included them (step.py:173-194)
     for (int b = 0; b < W.B; ++b) {
-        if (m.body_type[b] != GOI_STATIC) continue;
+        if (!W.is_static(b)) continue;
         int last = -1;
         for (int c = 0; c < W.C; ++c) {
             const int isl = I.contact_island(c);
             if (isl < 0) continue;
-            if (m.fixture_body[W.fa(c)] == b || m.fixture_body[W.fb(c)] == b) last = max(last, isl);
+            if (W.ba(c) == b || W.bb(c) == b) last = max(last, isl);
         }
         for (int j = 0; j < W.J; ++j) {
             const int isl = I.joint_island(j);
@@ -193,7 +193,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     if (dbg.n_islands) dbg.n_islands[W.w] = I.n;
     // SynchronizeFixtures of the non-static island bodies, then FindNewContacts
     for (int b = 0; b < W.B; ++b) {
-        if (I.body_island(b) < 0 || m.body_type[b] == GOI_STATIC) continue;
+        if (I.body_island(b) < 0 || W.is_static(b)) continue;
         sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
     }
     find_new_contacts(m, W);
@@ -202,7 +202,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
 // ---------------------------------------------------------------- b2World::SolveTOI for one world
 
 GOI_D bool pair_rule(const DModel& m, const World& W, const GoiSettings& s, int a, int b) {
-    const bool dyn_a = m.body_type[a] == GOI_DYNAMIC, dyn_b = m.body_type[b] == GOI_DYNAMIC;
+    const bool dyn_a = W.is_dynamic(a), dyn_b = W.is_dynamic(b);
     const bool bul_a = W.u8(GOI_B_BULLET, a) != 0, bul_b = W.u8(GOI_B_BULLET, b) != 0;
     const bool stock = bul_a || !dyn_a || bul_b || !dyn_b;
     if (!s.unity_toi) return stock;
@@ -238,9 +238,9 @@ GOI_D int toi_search_prepare(const DModel& m, const World& W, const Rows& CR, co
         const int c = W.order(i);
         if (!W.ten(c) || W.tcount(c) > kMaxSubSteps || W.tflag(c)) continue;
         const int fa = W.fa(c), fb = W.fb(c);
-        const int A = m.fixture_body[fa], Bb = m.fixture_body[fb];
-        const bool act_a = W.awake(A) && m.body_type[A] != GOI_STATIC;
-        const bool act_b = W.awake(Bb) && m.body_type[Bb] != GOI_STATIC;
+        const int A = W.ba(c), Bb = W.bb(c);
+        const bool act_a = W.awake(A) && !W.is_static(A);
+        const bool act_b = W.awake(Bb) && !W.is_static(Bb);
         if (!act_a && !act_b) continue;
         if (!pair_rule(m, W, s, A, Bb)) continue;
         const float alA = W.f(GOI_T_ALPHA0, A), alB = W.f(GOI_T_ALPHA0, Bb);
@@ -297,7 +297,7 @@ GOI_D bool toi_search_pick(const World& W, const GoiSettings& s, int& min_slot, 
 // position-constraint fields of contact slot `slot` into row i (the TOI island's b2ContactPositionConstraint)
 GOI_D void cs_position_row(const DModel& m, const World& W, const Rows& R, int i, int slot) {
     const int fa = W.fa(slot), fb = W.fb(slot);
-    const int ia = m.fixture_body[fa], ib = m.fixture_body[fb];
+    const int ia = W.ba(slot), ib = W.bb(slot);
     R.seti(i, CF_SLOT, slot); R.seti(i, CF_IA, ia); R.seti(i, CF_IB, ib);
     R.seti(i, CF_PC_COUNT, W.i32(GOI_C_COUNT, slot)); R.seti(i, CF_MTYPE, W.i32(GOI_C_MTYPE, slot));
     R.set2(i, CF_LN, W.v2(GOI_C_LOCAL_NORMAL, slot)); R.set2(i, CF_LP, W.v2(GOI_C_LOCAL_POINT, slot));
@@ -310,7 +310,7 @@ GOI_D void cs_position_row(const DModel& m, const World& W, const Rows& R, int i
 GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
                           float dt, int min_slot, float min_alpha) {
     const int fa = W.fa(min_slot), fb = W.fb(min_slot);
-    const int A = m.fixture_body[fa], Bb = m.fixture_body[fb];
+    const int A = W.ba(min_slot), Bb = W.bb(min_slot);
     const SweepBackup bkA = backup(W, A), bkB = backup(W, Bb);
     body_advance(W, A, min_alpha);
     body_advance(W, Bb, min_alpha);
@@ -340,15 +340,15 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     const int n = list_order(W);
     for (int pi = 0; pi < 2; ++pi) {
         const int body = pi == 0 ? A : Bb;
-        if (m.body_type[body] != GOI_DYNAMIC) continue;
+        if (!W.is_dynamic(body)) continue;
         for (int i = 0; i < n; ++i) {
             const int c = W.order(i);
-            const int ca = m.fixture_body[W.fa(c)], cb = m.fixture_body[W.fb(c)];
+            const int ca = W.ba(c), cb = W.bb(c);
             if (ca != body && cb != body) continue;
             if (nb == 2 * kMaxToiContacts || nc == kMaxToiContacts) break;
             if ((cflag >> c) & 1ull) continue;
             const int other = ca == body ? cb : ca;
-            if (m.body_type[other] == GOI_DYNAMIC && !W.u8(GOI_B_BULLET, body) && !W.u8(GOI_B_BULLET, other)) continue;
+            if (W.is_dynamic(other) && !W.u8(GOI_B_BULLET, body) && !W.u8(GOI_B_BULLET, other)) continue;
             if (s.unity_toi && !pair_rule(m, W, s, body, other)) continue;
             const SweepBackup bk = backup(W, other);
             if (!((bflag >> other) & 1ull)) body_advance(W, other, min_alpha);
@@ -364,7 +364,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
             cs_position_row(m, W, CR, nc++, c);
             if ((bflag >> other) & 1ull) continue;
             bflag |= 1ull << other;
-            if (m.body_type[other] != GOI_STATIC) W.wake(other);
+            if (!W.is_static(other)) W.wake(other);
             W.ibuf(nb++) = other;
         }
     }
@@ -431,13 +431,13 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     unsigned long long moved = 0ull, refat = 0ull;
     for (int i = 0; i < nb; ++i) {
         const int b = W.ibuf(i);
-        if (m.body_type[b] != GOI_DYNAMIC) continue;
+        if (!W.is_dynamic(b)) continue;
         moved |= 1ull << b;
         refat |= sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
     }
     for (int c = 0; c < W.C; ++c) {
         if (W.pair(c) < 0) continue;
-        const int ca = m.fixture_body[W.fa(c)], cb = m.fixture_body[W.fb(c)];
+        const int ca = W.ba(c), cb = W.bb(c);
         if (((moved >> ca) & 1ull) || ((moved >> cb) & 1ull)) W.set_tflag(c, 0);
     }
     // FindNewContacts; a slot that received a new contact starts with fresh TOI state. The keys before it go to

@@ -46,6 +46,7 @@ struct DModel {
     const int* leaf_info;       // [n_leaf + 4] the entry's body | (body is dynamic) << 16
     const int* leaf_cand;       // [n_leaf * R]: candidate index of (leaf entry i, row r), -1 if none
     const int* row_dynamic;     // [R] the row's body is dynamic
+    const int* row_body;        // [R] the row's body
     int n_dd;                   // candidates whose fixtures are both non-static
     const int* dd_cand;         // [n_dd] candidate indices (ascending)
 };
@@ -56,7 +57,7 @@ struct DModel {
 // whole step (loaded once, written back once) and holds the per-world work arrays (contact list order, island
 // lists and stacks, new-pair buffer), which would otherwise live in private scratch memory.
 struct Workspace {
-    int o_pair, o_key, o_fa, o_fb, o_tmeta, o_ttoi, o_order, o_newp, o_corder, o_cisl;  // [C]
+    int o_pair, o_key, o_fa, o_fb, o_bab, o_tmeta, o_ttoi, o_order, o_newp, o_corder, o_cisl;  // [C]
     int o_awake, o_active, o_bisl, o_stack, o_fwork, o_ibuf;                                            // [B]
     int o_qbox;                                                                                         // [4 R]
     int o_nlive;                                                                                        // [1]
@@ -67,7 +68,7 @@ struct Workspace {
         Workspace k;
         int o = 0;
         k.o_body = o; o += 8 * B;
-        k.o_pair = o; o += C; k.o_key = o; o += C; k.o_fa = o; o += C; k.o_fb = o; o += C;
+        k.o_pair = o; o += C; k.o_key = o; o += C; k.o_fa = o; o += C; k.o_fb = o; o += C; k.o_bab = o; o += C;
         k.o_tmeta = o; o += C; k.o_ttoi = o; o += C;
         k.o_order = o; o += C; k.o_newp = o; o += C; k.o_corder = o; o += C; k.o_cisl = o; o += C;
         k.o_awake = o; o += B; k.o_active = o; o += B; k.o_bisl = o; o += B; k.o_stack = o; o += B; k.o_fwork = o; o += B; k.o_ibuf = o; o += B;
@@ -91,6 +92,10 @@ struct World {
     const float4* nbox;  // the static BVH's first nk nodes, staged in LDS by the block
     const int2* nlink;
     int nk;
+    unsigned long long smask, dmask;  // static and dynamic bodies (Model.body_type, the same in every world)
+
+    GOI_D bool is_static(int b) const { return (smask >> b) & 1ull; }
+    GOI_D bool is_dynamic(int b) const { return (dmask >> b) & 1ull; }
 
     GOI_D int& wi(int off, int i) const { return ws[(off + i) * S]; }
     GOI_D float& wf(int off, int i) const { return reinterpret_cast<float*>(ws)[(off + i) * S]; }
@@ -99,6 +104,10 @@ struct World {
     GOI_D int& key(int c) const { return wi(k.o_key, c); }        // contacts.key
     GOI_D int& fa(int c) const { return wi(k.o_fa, c); }          // contacts.fa
     GOI_D int& fb(int c) const { return wi(k.o_fb, c); }          // contacts.fb
+    // the bodies of a live slot's fixtures (fixture_body[fa] | fixture_body[fb] << 8)
+    GOI_D int ba(int c) const { return wi(k.o_bab, c) & 0xff; }
+    GOI_D int bb(int c) const { return (wi(k.o_bab, c) >> 8) & 0xff; }
+    GOI_D void set_bodies(int c, int a, int b) const { wi(k.o_bab, c) = a | (b << 8); }
     GOI_D int& awake(int b) const { return wi(k.o_awake, b); }    // bodies.awake
     GOI_D int& active(int b) const { return wi(k.o_active, b); }  // bodies.active (read-only in a step)
     // toi.flag (bit 0), toi.enabled (bit 1) and toi.count (bits 8-15) of a slot, packed in one word
@@ -154,13 +163,23 @@ struct World {
             f(GOI_B_SLEEP_TIME, b) = 0.0f;
         }
     }
+    GOI_D void init_masks(const DModel& m) {
+        smask = dmask = 0ull;
+        for (int b = 0; b < B; ++b) {
+            const int t = m.body_type[b];
+            if (t == GOI_STATIC) smask |= 1ull << b;
+            if (t == GOI_DYNAMIC) dmask |= 1ull << b;
+        }
+    }
     // the mirrored leaves from the State into the workspace (contact metadata, awake flags)
-    GOI_D void load_mirror() const {
+    GOI_D void load_mirror(const DModel& m) const {
         for (int c = 0; c < C; ++c) {
             pair(c) = i32(GOI_C_PAIR, c);
             key(c) = i32(GOI_C_KEY, c);
-            fa(c) = i32(GOI_C_FA, c);
-            fb(c) = i32(GOI_C_FB, c);
+            const int a = i32(GOI_C_FA, c), b = i32(GOI_C_FB, c);
+            fa(c) = a;
+            fb(c) = b;
+            if (pair(c) >= 0) set_bodies(c, m.fixture_body[a], m.fixture_body[b]);
         }
         for (int b = 0; b < B; ++b) {
             awake(b) = u8(GOI_B_AWAKE, b);
@@ -185,7 +204,6 @@ struct World {
             f(GOI_T_TOI, c) = ttoi(c);
         }
     }
-    GOI_D int body_of(const DModel& m, int fixture) const { return m.fixture_body[fixture]; }
 };
 
 // Fat AABB of a fixture in the compact layout: the world's own row, or the Model's shared static box.

@@ -56,7 +56,7 @@ struct Launch {
 __host__ __device__ inline int node_offset(int words, int wpw) { return ((words * wpw + kBlock) + 3) & ~3; }
 
 // World w on lane `lane` of its block; the block's LDS workspace holds L.wpw lanes.
-__device__ __forceinline__ World make_world(const Launch& L, int w, int* lds, int lane) {
+__device__ __forceinline__ World make_world(const DModel& m, const Launch& L, int w, int* lds, int lane) {
     World W;
     W.pitch = L.pitch;
     W.B = L.B;
@@ -71,6 +71,7 @@ __device__ __forceinline__ World make_world(const Launch& L, int w, int* lds, in
     W.nk = L.lds_nodes;
     W.nbox = reinterpret_cast<const float4*>(lds + node_offset(W.k.words, L.wpw));
     W.nlink = reinterpret_cast<const int2*>(W.nbox + L.lds_nodes);
+    W.init_masks(m);
     return W;
 }
 
@@ -125,9 +126,9 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
     const int lane = threadIdx.x;
     const int w0 = blockIdx.x * L.wpw;
     const bool valid = lane < L.wpw && w0 + lane < L.n;
-    const World W = make_world(L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
+    const World W = make_world(m, L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
     if (valid) {
-        W.load_mirror();
+        W.load_mirror(m);
         build_order(W);
         if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
         W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
@@ -144,7 +145,7 @@ __global__ void __launch_bounds__(kBlock) k_step(DModel m, Launch L) {
     const int lane = threadIdx.x;
     const int w0 = blockIdx.x * L.wpw;
     const bool valid = lane < L.wpw && w0 + lane < L.n;
-    const World W = make_world(L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
+    const World W = make_world(m, L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
     const Coop co = block_coop(L, W, lds, w0);
     Bodies bd;
     bd.s = reinterpret_cast<float*>(lds) + W.k.o_body * W.S + (valid ? lane : 0);
@@ -152,7 +153,7 @@ __global__ void __launch_bounds__(kBlock) k_step(DModel m, Launch L) {
     bd.st = W.S;
     const Rows CR = contact_rows(L, W.w);
     if (valid) {
-        W.load_mirror();
+        W.load_mirror(m);
         build_order(W);
         if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
         W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
@@ -337,7 +338,11 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
         leaf_info[i] = b | ((desc->body_type[b] == GOI_DYNAMIC ? 1 : 0) << 16);
         for (int r = 0; r < R; ++r) leaf_cand[i * R + r] = cand[(size_t)f * R + r];
     }
-    for (int r = 0; r < R; ++r) row_dyn[r] = desc->body_type[desc->fixture_body[slot_fixture[r]]] == GOI_DYNAMIC;
+    std::vector<int> row_body(std::max(R, 1), 0);
+    for (int r = 0; r < R; ++r) {
+        row_body[r] = desc->fixture_body[slot_fixture[r]];
+        row_dyn[r] = desc->body_type[row_body[r]] == GOI_DYNAMIC;
+    }
     d.n_dd = (int)dd.size();
     int any = desc->toi_bodies ? 0 : 1;
     if (desc->toi_bodies)
@@ -374,6 +379,7 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     UP(leaf_info, leaf_info.data(), leaf_info.size());
     UP(leaf_cand, leaf_cand.data(), n_leaf * R);
     UP(row_dynamic, row_dyn.data(), R);
+    UP(row_body, row_body.data(), R);
     UP(dd_cand, dd.data(), dd.size());
 #undef UP
     if (rc == GOI_OK) {
