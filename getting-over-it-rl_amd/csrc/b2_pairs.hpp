@@ -242,14 +242,14 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
     int n_free = 0;
     for (int k = 0; k < W.C; ++k) n_free += W.pair(k) < 0;
     NewPairs np{W, 0, 0, n_free};
-    // the query boxes of the rows on active bodies, and their union
+    // the fat boxes of all rows into the workspace; the queried rows on active bodies and their union box
     unsigned long long rows = 0ull;
     float4 U = make_float4(kMaxFloat, kMaxFloat, -kMaxFloat, -kMaxFloat);
     for (int r = 0; r < m.R; ++r) {
-        if (!((query_rows >> r) & 1ull) || !W.active(m.row_body[r])) continue;
         const float4 q = make_float4(W.f(GOI_F_FAT, 4 * r), W.f(GOI_F_FAT, 4 * r + 1), W.f(GOI_F_FAT, 4 * r + 2),
                                      W.f(GOI_F_FAT, 4 * r + 3));
         W.set_qbox(r, q);
+        if (!((query_rows >> r) & 1ull) || !W.active(m.row_body[r])) continue;
         rows |= 1ull << r;
         U.x = fminf(U.x, q.x); U.y = fminf(U.y, q.y); U.z = fmaxf(U.z, q.z); U.w = fmaxf(U.w, q.w);
     }
@@ -293,11 +293,10 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
     }
     // non-static x non-static candidates
     for (int i = 0; i < m.n_dd; ++i) {
-        const int p = m.dd_cand[i];
-        const int a = m.pair_a[p], b = m.pair_b[p];
-        if (!(((query_rows >> m.fixture_slot[a]) | (query_rows >> m.fixture_slot[b])) & 1ull)) continue;
-        const int ba = m.fixture_body[a], bb = m.fixture_body[b];
-        if (!overlap(fat_of(m, W, a), fat_of(m, W, b))) continue;
+        const int4 d = m.dd_info[i];  // candidate, rows, bodies
+        const int p = d.x, ra = d.y & 0xff, rb = d.y >> 8, ba = d.z & 0xff, bb = d.z >> 8;
+        if (!(((query_rows >> ra) | (query_rows >> rb)) & 1ull)) continue;
+        if (!overlap(W.get_qbox(ra), W.get_qbox(rb))) continue;
         if (!(W.is_dynamic(ba) || W.is_dynamic(bb))) continue;
         if (!(W.active(ba) && W.active(bb))) continue;
         if (slot_has_pair(W, p)) continue;

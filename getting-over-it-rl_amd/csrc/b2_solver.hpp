@@ -223,20 +223,44 @@ GOI_D void cs_warm_start(const Bodies& bd, const Rows& R, int i) {
 }
 
 // b2ContactSolver::SolveVelocityConstraints for row i (contact_solver.py:194-279)
-GOI_D void cs_solve_velocity(const Bodies& bd, const Rows& R, int i) {
-    const int ia = R.geti(i, CF_IA), ib = R.geti(i, CF_IB), cnt = R.geti(i, CF_COUNT);
-    const float mA = R.getf(i, CF_MA), mB = R.getf(i, CF_MB), iA = R.getf(i, CF_IIA), iB = R.getf(i, CF_IIB);
-    const V2 n = R.get2(i, CF_NX), t = cross(n, 1.0f);
-    const float friction = R.getf(i, CF_FRICTION), tspeed = R.getf(i, CF_TSPEED);
-    const V2 rA0 = R.get2(i, CF_RA0), rA1 = R.get2(i, CF_RA1), rB0 = R.get2(i, CF_RB0), rB1 = R.get2(i, CF_RB1);
-    float ni0 = R.getf(i, CF_NI0), ni1 = R.getf(i, CF_NI1), ti0 = R.getf(i, CF_TI0), ti1 = R.getf(i, CF_TI1);
-    V2 vA = bd.v(ia), vB = bd.v(ib);
-    float wA = bd.w(ia), wB = bd.w(ib);
+// A contact row's velocity-solver fields, loaded in one batch (every field, whether or not the row's point count
+// uses it) so that the next row can be fetched while the current one is solved.
+struct VRow {
+    int ia, ib, cnt;
+    float mA, mB, iA, iB, friction, tspeed, tm0, tm1, nm0, nm1, b0, b1, K0, K1, K2, K3, N0, N1, N2, N3;
+    V2 n, rA0, rA1, rB0, rB1;
+    float ni0, ni1, ti0, ti1;
+};
+
+GOI_D VRow load_vrow(const Rows& R, int i) {
+    VRow r;
+    r.ia = R.geti(i, CF_IA); r.ib = R.geti(i, CF_IB); r.cnt = R.geti(i, CF_COUNT);
+    r.mA = R.getf(i, CF_MA); r.mB = R.getf(i, CF_MB); r.iA = R.getf(i, CF_IIA); r.iB = R.getf(i, CF_IIB);
+    r.n = R.get2(i, CF_NX); r.friction = R.getf(i, CF_FRICTION); r.tspeed = R.getf(i, CF_TSPEED);
+    r.rA0 = R.get2(i, CF_RA0); r.rA1 = R.get2(i, CF_RA1); r.rB0 = R.get2(i, CF_RB0); r.rB1 = R.get2(i, CF_RB1);
+    r.tm0 = R.getf(i, CF_TMASS0); r.tm1 = R.getf(i, CF_TMASS1);
+    r.nm0 = R.getf(i, CF_NMASS0); r.nm1 = R.getf(i, CF_NMASS1);
+    r.b0 = R.getf(i, CF_BIAS0); r.b1 = R.getf(i, CF_BIAS1);
+    r.K0 = R.getf(i, CF_K0); r.K1 = R.getf(i, CF_K1); r.K2 = R.getf(i, CF_K2); r.K3 = R.getf(i, CF_K3);
+    r.N0 = R.getf(i, CF_NM0); r.N1 = R.getf(i, CF_NM1); r.N2 = R.getf(i, CF_NM2); r.N3 = R.getf(i, CF_NM3);
+    r.ni0 = R.getf(i, CF_NI0); r.ni1 = R.getf(i, CF_NI1); r.ti0 = R.getf(i, CF_TI0); r.ti1 = R.getf(i, CF_TI1);
+    return r;
+}
+
+// b2ContactSolver::SolveVelocityConstraints for one row (contact_solver.py:194-290): tangent rows first, then the
+// normal row or the 2-point block solver's four cases. Updates the row's impulses in r and the bodies in LDS.
+GOI_D void solve_vrow(const Bodies& bd, VRow& r) {
+    const V2 n = r.n, t = cross(n, 1.0f);
+    const float mA = r.mA, mB = r.mB, iA = r.iA, iB = r.iB;
+    const V2 rA0 = r.rA0, rA1 = r.rA1, rB0 = r.rB0, rB1 = r.rB1;
+    float ni0 = r.ni0, ni1 = r.ni1, ti0 = r.ti0, ti1 = r.ti1;
+    V2 vA = bd.v(r.ia), vB = bd.v(r.ib);
+    float wA = bd.w(r.ia), wB = bd.w(r.ib);
     // tangent constraints first
-    if (cnt > 0) {
-        const float vt = dot(rel_vel(vB, wB, rB0, vA, wA, rA0), t) - tspeed;
-        float lam = R.getf(i, CF_TMASS0) * (-vt);
-        const float maxf = friction * ni0;
+    if (r.cnt > 0) {
+        const float vt = dot(rel_vel(vB, wB, rB0, vA, wA, rA0), t) - r.tspeed;
+        float lam = r.tm0 * (-vt);
+        const float maxf = r.friction * ni0;
         const float nw = bclamp(ti0 + lam, -maxf, maxf);
         lam = nw - ti0;
         ti0 = nw;
@@ -244,10 +268,10 @@ GOI_D void cs_solve_velocity(const Bodies& bd, const Rows& R, int i) {
         vA = vA - mA * P; wA = wA - iA * cross(rA0, P);
         vB = vB + mB * P; wB = wB + iB * cross(rB0, P);
     }
-    if (cnt > 1) {
-        const float vt = dot(rel_vel(vB, wB, rB1, vA, wA, rA1), t) - tspeed;
-        float lam = R.getf(i, CF_TMASS1) * (-vt);
-        const float maxf = friction * ni1;
+    if (r.cnt > 1) {
+        const float vt = dot(rel_vel(vB, wB, rB1, vA, wA, rA1), t) - r.tspeed;
+        float lam = r.tm1 * (-vt);
+        const float maxf = r.friction * ni1;
         const float nw = bclamp(ti1 + lam, -maxf, maxf);
         lam = nw - ti1;
         ti1 = nw;
@@ -255,34 +279,34 @@ GOI_D void cs_solve_velocity(const Bodies& bd, const Rows& R, int i) {
         vA = vA - mA * P; wA = wA - iA * cross(rA1, P);
         vB = vB + mB * P; wB = wB + iB * cross(rB1, P);
     }
-    if (cnt == 1) {
+    if (r.cnt == 1) {
         const float vn = dot(rel_vel(vB, wB, rB0, vA, wA, rA0), n);
-        float lam = -R.getf(i, CF_NMASS0) * (vn - R.getf(i, CF_BIAS0));
+        float lam = -r.nm0 * (vn - r.b0);
         const float nw = bmax(ni0 + lam, 0.0f);
         lam = nw - ni0;
         ni0 = nw;
         const V2 P = lam * n;
         vA = vA - mA * P; wA = wA - iA * cross(rA0, P);
         vB = vB + mB * P; wB = wB + iB * cross(rB0, P);
-    } else if (cnt == 2) {
-        const float K0 = R.getf(i, CF_K0), K1 = R.getf(i, CF_K1), K2 = R.getf(i, CF_K2), K3 = R.getf(i, CF_K3);
+    } else if (r.cnt == 2) {
+        const float K0 = r.K0, K1 = r.K1, K2 = r.K2, K3 = r.K3;
         const float ax = ni0, ay = ni1;
         const float vn1 = dot(rel_vel(vB, wB, rB0, vA, wA, rA0), n);
         const float vn2 = dot(rel_vel(vB, wB, rB1, vA, wA, rA1), n);
-        float bx = vn1 - R.getf(i, CF_BIAS0), by = vn2 - R.getf(i, CF_BIAS1);
+        float bx = vn1 - r.b0, by = vn2 - r.b1;
         bx = bx - (K0 * ax + K2 * ay);
         by = by - (K1 * ax + K3 * ay);
-        float xx = -(R.getf(i, CF_NM0) * bx + R.getf(i, CF_NM2) * by);
-        float xy = -(R.getf(i, CF_NM1) * bx + R.getf(i, CF_NM3) * by);
+        float xx = -(r.N0 * bx + r.N2 * by);
+        float xy = -(r.N1 * bx + r.N3 * by);
         bool ok = xx >= 0.0f && xy >= 0.0f;
         if (!ok) {
-            xx = -R.getf(i, CF_NMASS0) * bx;
+            xx = -r.nm0 * bx;
             xy = 0.0f;
             ok = xx >= 0.0f && K1 * xx + by >= 0.0f;
         }
         if (!ok) {
             xx = 0.0f;
-            xy = -R.getf(i, CF_NMASS1) * by;
+            xy = -r.nm1 * by;
             ok = xy >= 0.0f && K2 * xy + bx >= 0.0f;
         }
         if (!ok) {
@@ -301,38 +325,66 @@ GOI_D void cs_solve_velocity(const Bodies& bd, const Rows& R, int i) {
             ni1 = xy;
         }
     }
-    R.setf(i, CF_NI0, ni0); R.setf(i, CF_NI1, ni1); R.setf(i, CF_TI0, ti0); R.setf(i, CF_TI1, ti1);
-    bd.set_v(ia, vA, wA);
-    bd.set_v(ib, vB, wB);
+    r.ni0 = ni0; r.ni1 = ni1; r.ti0 = ti0; r.ti1 = ti1;
+    bd.set_v(r.ia, vA, wA);
+    bd.set_v(r.ib, vB, wB);
 }
 
-// b2ContactSolver::SolvePositionConstraints for row i (contact_solver.py:307-354); masses given (the TOI solve
+GOI_D void store_vimpulses(const Rows& R, int i, const VRow& r) {
+    R.setf(i, CF_NI0, r.ni0); R.setf(i, CF_NI1, r.ni1); R.setf(i, CF_TI0, r.ti0); R.setf(i, CF_TI1, r.ti1);
+}
+
+// rows 0..n-1 once each, in order, each loaded in one batch
+GOI_D void cs_solve_velocity_sweep(const Bodies& bd, const Rows& R, int n) {
+    for (int i = 0; i < n; ++i) {
+        VRow r = load_vrow(R, i);
+        solve_vrow(bd, r);
+        store_vimpulses(R, i, r);
+    }
+}
+
+// A contact row's position-solver fields (b2ContactPositionConstraint), loaded in one batch.
+struct PRow {
+    int ia, ib, cnt, mtype;
+    V2 lcA, lcB, ln, lp, pl0, pl1;
+    float radA, radB, mA, mB, iA, iB;
+};
+
+GOI_D PRow load_prow(const Rows& R, int i) {
+    PRow r;
+    r.ia = R.geti(i, CF_IA); r.ib = R.geti(i, CF_IB); r.cnt = R.geti(i, CF_PC_COUNT); r.mtype = R.geti(i, CF_MTYPE);
+    r.lcA = R.get2(i, CF_LCA); r.lcB = R.get2(i, CF_LCB); r.ln = R.get2(i, CF_LN); r.lp = R.get2(i, CF_LP);
+    r.pl0 = R.get2(i, CF_PL0); r.pl1 = R.get2(i, CF_PL1);
+    r.radA = R.getf(i, CF_RADA); r.radB = R.getf(i, CF_RADB);
+    r.mA = R.getf(i, CF_MA); r.mB = R.getf(i, CF_MB); r.iA = R.getf(i, CF_IIA); r.iB = R.getf(i, CF_IIB);
+    return r;
+}
+
+// b2ContactSolver::SolvePositionConstraints for one row (contact_solver.py:307-354); masses given (the TOI solve
 // passes zero for bodies other than the TOI pair). Returns the row's min separation, starting at 0.
-GOI_D float cs_solve_position(const Bodies& bd, const Rows& R, int i, float baumgarte, float mA, float mB, float iA,
-                              float iB, float linear_slop, float max_linear_correction) {
-    const int ia = R.geti(i, CF_IA), ib = R.geti(i, CF_IB), cnt = R.geti(i, CF_PC_COUNT);
-    const int mtype = R.geti(i, CF_MTYPE);
-    const V2 lcA = R.get2(i, CF_LCA), lcB = R.get2(i, CF_LCB), ln = R.get2(i, CF_LN), lp = R.get2(i, CF_LP);
-    const float radA = R.getf(i, CF_RADA), radB = R.getf(i, CF_RADB);
-    V2 cA = bd.c(ia), cB = bd.c(ib);
-    float aA = bd.a(ia), aB = bd.a(ib);
+GOI_D float solve_prow(const Bodies& bd, const PRow& r, float baumgarte, float mA, float mB, float iA, float iB,
+                       float linear_slop, float max_linear_correction) {
+    const V2 lcA = r.lcA, lcB = r.lcB, ln = r.ln, lp = r.lp;
+    const float radA = r.radA, radB = r.radB;
+    V2 cA = bd.c(r.ia), cB = bd.c(r.ib);
+    float aA = bd.a(r.ia), aB = bd.a(r.ib);
     float min_sep = 0.0f;
-    for (int j = 0; j < cnt; ++j) {
+    for (int j = 0; j < r.cnt; ++j) {
         Xf xfA, xfB;
         xfA.q = rot_of(aA);
         xfB.q = rot_of(aB);
         xfA.p = cA - mul(xfA.q, lcA);
         xfB.p = cB - mul(xfB.q, lcB);
-        const V2 plj = R.get2(i, CF_PL0 + 2 * j);
+        const V2 plj = j == 0 ? r.pl0 : r.pl1;
         V2 n, p;
         float sep;
-        if (mtype == kCircles) {
-            const V2 pA = mul(xfA, lp), pB = mul(xfB, R.get2(i, CF_PL0));
+        if (r.mtype == kCircles) {
+            const V2 pA = mul(xfA, lp), pB = mul(xfB, r.pl0);
             n = pB - pA;
             normalize(n);
             p = 0.5f * (pA + pB);
             sep = (dot(pB - pA, n) - radA) - radB;
-        } else if (mtype == kFaceA) {
+        } else if (r.mtype == kFaceA) {
             n = mul(xfA.q, ln);
             const V2 cp = mul(xfB, plj);
             sep = (dot(cp - mul(xfA, lp), n) - radA) - radB;
@@ -354,8 +406,8 @@ GOI_D float cs_solve_position(const Bodies& bd, const Rows& R, int i, float baum
         cA = cA - mA * P; aA = aA - iA * cross(rA, P);
         cB = cB + mB * P; aB = aB + iB * cross(rB, P);
     }
-    bd.set_c(ia, cA, aA);
-    bd.set_c(ib, cB, aB);
+    bd.set_c(r.ia, cA, aA);
+    bd.set_c(r.ib, cB, aB);
     return min_sep;
 }
 

@@ -65,7 +65,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     for (int i = 0; i < I.nj; ++i) jn_warm_start(bd, JRw, i, v24);
     for (int it = 0; it < s.velocity_iterations; ++it) {
         for (int i = 0; i < I.nj; ++i) jn_solve_velocity(bd, JRw, i, v24);
-        for (int i = 0; i < I.nc; ++i) cs_solve_velocity(bd, CR, i);
+        cs_solve_velocity_sweep(bd, CR, I.nc);
     }
     // StoreImpulses (contact_solver.py:293-304)
     for (int i = 0; i < I.nc; ++i) {
@@ -103,12 +103,11 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         unsigned long long jbad = 0ull;
         for (int i = 0; i < I.n; ++i) W.fwork(i) = 0.0f;  // min separation per island
         for (int i = 0; i < I.nc; ++i) {
-            const int isl = I.contact_island(CR.geti(i, CF_SLOT));
+            const int isl = I.contact_island(I.corder(i));
             if ((done >> isl) & 1ull) continue;
-            const float ms = cs_solve_position(bd, CR, i, s.baumgarte, CR.getf(i, CF_MA), CR.getf(i, CF_MB),
-                                               CR.getf(i, CF_IIA), CR.getf(i, CF_IIB), s.linear_slop,
-                                               s.max_linear_correction);
-            W.fwork(isl) = bmin(W.fwork(isl), ms);
+            const PRow r = load_prow(CR, i);
+            W.fwork(isl) = bmin(W.fwork(isl), solve_prow(bd, r, s.baumgarte, r.mA, r.mB, r.iA, r.iB, s.linear_slop,
+                                                         s.max_linear_correction));
         }
         for (int i = 0; i < I.nj; ++i) {
             const int isl = I.joint_island(JRw.geti(i, JF_JID));
@@ -379,12 +378,13 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     for (int it = 0; it < 20; ++it) {
         float min_sep = 0.0f;
         for (int i = 0; i < nc; ++i) {
-            const int ia = CR.geti(i, CF_IA), ib = CR.geti(i, CF_IB);
+            const PRow cur = load_prow(CR, i);
+            const int ia = cur.ia, ib = cur.ib;
             const bool ta = ia == A || ia == Bb, tb = ib == A || ib == Bb;
             const float mA = ta ? (ia == A ? mA_ : mB_) : 0.0f, iA = ta ? (ia == A ? iA_ : iB_) : 0.0f;
             const float mB = tb ? (ib == A ? mA_ : mB_) : 0.0f, iB = tb ? (ib == A ? iA_ : iB_) : 0.0f;
-            min_sep = bmin(min_sep, cs_solve_position(bd, CR, i, s.toi_baumgarte, mA, mB, iA, iB, s.linear_slop,
-                                                      s.max_linear_correction));
+            min_sep = bmin(min_sep, solve_prow(bd, cur, s.toi_baumgarte, mA, mB, iA, iB, s.linear_slop,
+                                               s.max_linear_correction));
         }
         if (min_sep >= -1.5f * s.linear_slop) break;
     }
@@ -396,8 +396,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         const int ia = CR.geti(i, CF_IA), ib = CR.geti(i, CF_IB);
         cs_prepare(m, W, bd, CR, i, slot, false, 1.0f, rot_of(bd.a(ia)), rot_of(bd.a(ib)), s.velocity_threshold);
     }
-    for (int it = 0; it < s.velocity_iterations; ++it)
-        for (int i = 0; i < nc; ++i) cs_solve_velocity(bd, CR, i);
+    for (int it = 0; it < s.velocity_iterations; ++it) cs_solve_velocity_sweep(bd, CR, nc);
     const float h = (1.0f - min_alpha) * dt;
     const float max_t = s.clamps_per_second ? s.max_translation * dt : s.max_translation;
     const float max_r = s.clamps_per_second ? s.max_rotation * dt : s.max_rotation;

@@ -48,7 +48,7 @@ struct DModel {
     const int* row_dynamic;     // [R] the row's body is dynamic
     const int* row_body;        // [R] the row's body
     int n_dd;                   // candidates whose fixtures are both non-static
-    const int* dd_cand;         // [n_dd] candidate indices (ascending)
+    const int4* dd_info;        // [n_dd] ascending: candidate, row_a | row_b << 8, body_a | body_b << 8, 0
 };
 
 // Per-lane workspace in LDS. Every array is [index][lane] with the block's lane count as stride: lane l's element

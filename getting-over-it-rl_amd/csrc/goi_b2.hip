@@ -380,7 +380,13 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     UP(leaf_cand, leaf_cand.data(), n_leaf * R);
     UP(row_dynamic, row_dyn.data(), R);
     UP(row_body, row_body.data(), R);
-    UP(dd_cand, dd.data(), dd.size());
+    std::vector<int4> dd_info(std::max<size_t>(dd.size(), 1));
+    for (size_t i = 0; i < dd.size(); ++i) {
+        const int p = dd[i], a = desc->pair_a[p], b = desc->pair_b[p];
+        dd_info[i] = make_int4(p, desc->fixture_slot[a] | (desc->fixture_slot[b] << 8),
+                               desc->fixture_body[a] | (desc->fixture_body[b] << 8), 0);
+    }
+    UP(dd_info, dd_info.data(), dd.size());
 #undef UP
     if (rc == GOI_OK) {
         hipError_t e = hipStreamSynchronize(st);
