@@ -106,6 +106,14 @@ __device__ __forceinline__ Rows joint_rows(const Launch& L, int w) {
 
 // ---------------------------------------------------------------- kernels
 
+// World group of this block. Blocks are dealt to the 8 XCDs round robin (block b on XCD b % 8), and each XCD has its
+// own L2; numbering the groups so that every XCD holds one contiguous range keeps neighbouring worlds, which share
+// 128-byte lines of every State leaf, behind the same L2. A bijection on [0, gridDim.x) for any grid.
+__device__ __forceinline__ int xcd_group() {
+    const int nb = gridDim.x, b = blockIdx.x, x = b & 7, q = nb >> 3, r = nb & 7;
+    return x * q + min(x, r) + (b >> 3);
+}
+
 // The block's cooperative view (Coop) for lanes whose world is W (or lane 0's, for lanes without one).
 __device__ __forceinline__ Coop block_coop(const Launch& L, const World& W, int* lds, int w0) {
     Coop co;
@@ -124,7 +132,7 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
     extern __shared__ int lds[];
     stage_nodes(m, L, lds);
     const int lane = threadIdx.x;
-    const int w0 = blockIdx.x * L.wpw;
+    const int w0 = xcd_group() * L.wpw;
     const bool valid = lane < L.wpw && w0 + lane < L.n;
     const World W = make_world(m, L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
     if (valid) {
@@ -143,7 +151,7 @@ __global__ void __launch_bounds__(kBlock) k_step(DModel m, Launch L) {
     extern __shared__ int lds[];
     stage_nodes(m, L, lds);
     const int lane = threadIdx.x;
-    const int w0 = blockIdx.x * L.wpw;
+    const int w0 = xcd_group() * L.wpw;
     const bool valid = lane < L.wpw && w0 + lane < L.n;
     const World W = make_world(m, L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
     const Coop co = block_coop(L, W, lds, w0);
