@@ -51,6 +51,22 @@ struct DModel {
     const int4* dd_info;        // [n_dd] ascending: candidate, row_a | row_b << 8, body_a | body_b << 8, 0
 };
 
+// Float body leaves mirrored in the workspace for the whole step: the leaf's per-body element count and the
+// multiple of B at which its elements start (-1 for leaves that stay in the State only).
+GOI_HD constexpr int body_mirror_coef(int leaf) {
+    return leaf == GOI_B_C0 ? 0 : leaf == GOI_B_C ? 2 : leaf == GOI_B_A0 ? 4 : leaf == GOI_B_A ? 5 : leaf == GOI_B_V ? 6
+         : leaf == GOI_B_W ? 8 : leaf == GOI_B_XF_P ? 9 : leaf == GOI_B_XF_Q ? 11 : leaf == GOI_T_ALPHA0 ? 13
+         : leaf == GOI_B_LOCAL_CENTER ? 14 : leaf == GOI_B_INV_MASS ? 16 : leaf == GOI_B_INV_INERTIA ? 17
+         : leaf == GOI_B_SLEEP_TIME ? 18 : -1;
+}
+constexpr int kBodyMirrorWords = 19;  // per body
+// the mirrored leaves with their per-body widths; the first `kBodyMirrorMutable` change during a step
+constexpr int kBodyMirrorLeaves[13] = {GOI_B_C0, GOI_B_C, GOI_B_A0, GOI_B_A, GOI_B_V, GOI_B_W, GOI_B_XF_P, GOI_B_XF_Q,
+                                       GOI_T_ALPHA0, GOI_B_SLEEP_TIME, GOI_B_LOCAL_CENTER, GOI_B_INV_MASS,
+                                       GOI_B_INV_INERTIA};
+constexpr int kBodyMirrorWidth[13] = {2, 2, 1, 1, 2, 1, 2, 2, 1, 1, 2, 1, 1};
+constexpr int kBodyMirrorMutable = 10;
+
 // Per-lane workspace in LDS. Every array is [index][lane] with the block's lane count as stride: lane l's element
 // i of an array at offset o sits at base[(o + i) * S + l], so one index across a wavefront is consecutive words.
 // It mirrors the per-world contact metadata (pair, key, fixtures), the awake flags and the TOI bookkeeping for the
@@ -63,11 +79,13 @@ struct Workspace {
     int o_nlive;                                                                                        // [1]
     int o_jorder, o_jisl;                                                                               // [J]
     int o_body;  // 8 solver body fields x B
+    int o_bm;    // mirrored body leaves, kBodyMirrorWords x B
     int words;   // per lane
     GOI_HD static Workspace layout(int B, int C, int J, int R) {
         Workspace k;
         int o = 0;
         k.o_body = o; o += 8 * B;
+        k.o_bm = o; o += kBodyMirrorWords * B;
         k.o_pair = o; o += C; k.o_key = o; o += C; k.o_fa = o; o += C; k.o_fb = o; o += C; k.o_bab = o; o += C;
         k.o_tmeta = o; o += C; k.o_ttoi = o; o += C;
         k.o_order = o; o += C; k.o_newp = o; o += C; k.o_corder = o; o += C; k.o_cisl = o; o += C;
@@ -141,7 +159,11 @@ struct World {
     GOI_D T& at(int leaf, int i) const {
         return reinterpret_cast<T*>(lv[leaf])[(size_t)i * pitch + w];
     }
-    GOI_D float& f(int leaf, int i) const { return at<float>(leaf, i); }
+    GOI_D float& f(int leaf, int i) const {
+        const int c = body_mirror_coef(leaf);  // a constant at every call site
+        if (c >= 0) return wf(k.o_bm + c * B, i);
+        return at<float>(leaf, i);
+    }
     GOI_D int& i32(int leaf, int i) const { return at<int>(leaf, i); }
     GOI_D uint8_t& u8(int leaf, int i) const { return at<uint8_t>(leaf, i); }
     GOI_D V2 v2(int leaf, int i) const { return mk(f(leaf, 2 * i), f(leaf, 2 * i + 1)); }
@@ -185,6 +207,11 @@ struct World {
             awake(b) = u8(GOI_B_AWAKE, b);
             active(b) = u8(GOI_B_ACTIVE, b);
         }
+        for (int l = 0; l < 13; ++l) {
+            const int leaf = kBodyMirrorLeaves[l], n = kBodyMirrorWidth[l] * B;
+            float* dst = &wf(k.o_bm + body_mirror_coef(leaf) * B, 0);
+            for (int i = 0; i < n; ++i) dst[i * S] = at<float>(leaf, i);
+        }
     }
     GOI_D void store_mirror() const {
         for (int c = 0; c < C; ++c) {
@@ -194,6 +221,11 @@ struct World {
             i32(GOI_C_FB, c) = fb(c);
         }
         for (int b = 0; b < B; ++b) u8(GOI_B_AWAKE, b) = (uint8_t)awake(b);
+        for (int l = 0; l < kBodyMirrorMutable; ++l) {
+            const int leaf = kBodyMirrorLeaves[l], n = kBodyMirrorWidth[l] * B;
+            const float* src = &wf(k.o_bm + body_mirror_coef(leaf) * B, 0);
+            for (int i = 0; i < n; ++i) at<float>(leaf, i) = src[i * S];
+        }
     }
     // the TOI bookkeeping (written by SolveTOI only)
     GOI_D void store_toi() const {
