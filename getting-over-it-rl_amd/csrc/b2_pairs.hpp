@@ -31,7 +31,7 @@ GOI_D int list_order(const World& W) { return W.nlive(); }
 // b2Contact::Update's manifold part: new manifold, impulses carried over from the first old point with the same
 // feature key, touching flag (pairs.py:56-83). Returns whether touching flipped.
 GOI_D bool contact_update(const World& W, int k, const Manifold& mf) {
-    const int oldn = W.i32(GOI_C_COUNT, k);
+    const int oldn = W.ccount(k);
     const int o0 = W.i32(GOI_C_POINT_ID, 2 * k), o1 = W.i32(GOI_C_POINT_ID, 2 * k + 1);
     const float n0 = W.f(GOI_C_NORMAL_IMPULSE, 2 * k), n1 = W.f(GOI_C_NORMAL_IMPULSE, 2 * k + 1);
     const float t0 = W.f(GOI_C_TANGENT_IMPULSE, 2 * k), t1 = W.f(GOI_C_TANGENT_IMPULSE, 2 * k + 1);
@@ -46,9 +46,8 @@ GOI_D bool contact_update(const World& W, int k, const Manifold& mf) {
         else if (oldn > 1 && o1 == mf.id1) { ni1 = n1; ti1 = t1; }
     }
     const bool touching = n > 0;
-    const bool flip = touching != (W.u8(GOI_C_TOUCHING, k) != 0);
-    W.u8(GOI_C_TOUCHING, k) = touching;
-    W.i32(GOI_C_COUNT, k) = n;
+    const bool flip = touching != W.touching(k);
+    W.set_touch_count(k, touching, n);
     if (n > 0) {
         W.i32(GOI_C_MTYPE, k) = mf.mtype;
         W.set2(GOI_C_LOCAL_NORMAL, k, mf.ln);
@@ -168,10 +167,9 @@ GOI_D void collide_apply(const DModel& m, const World& W, const Rows& R) {
         if (!act_a && !act_b) continue;
         const int t = W.cisl(k);
         if (t < 0) {
-            if (W.i32(GOI_C_COUNT, k) > 0) { W.wake(ba); W.wake(bb); }
+            if (W.ccount(k) > 0) { W.wake(ba); W.wake(bb); }
             W.pair(k) = -1;
-            W.u8(GOI_C_TOUCHING, k) = 0;
-            W.i32(GOI_C_COUNT, k) = 0;
+            W.set_touch_count(k, false, 0);
             continue;
         }
         Manifold mf;
@@ -318,8 +316,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         W.fa(k) = a;
         W.fb(k) = b;
         W.key(k) = base_key + i;
-        W.u8(GOI_C_TOUCHING, k) = 0;
-        W.i32(GOI_C_COUNT, k) = 0;
+        W.set_touch_count(k, false, 0);
         W.f(GOI_C_NORMAL_IMPULSE, 2 * k) = 0.0f;
         W.f(GOI_C_NORMAL_IMPULSE, 2 * k + 1) = 0.0f;
         W.f(GOI_C_TANGENT_IMPULSE, 2 * k) = 0.0f;

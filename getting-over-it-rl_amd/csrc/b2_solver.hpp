@@ -75,7 +75,7 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
                 const int c = W.order(i);
                 const int ba = W.ba(c), bb = W.bb(c);
                 if (ba != b && bb != b) continue;
-                if (((cflag >> c) & 1ull) || !W.u8(GOI_C_TOUCHING, c)) continue;
+                if (((cflag >> c) & 1ull) || !W.touching(c)) continue;
                 I.corder(nc++) = c;
                 cflag |= 1ull << c;
                 I.contact_island(c) = isl;
@@ -117,7 +117,7 @@ GOI_D void cs_prepare(const DModel& m, const World& W, const Bodies& bd, const R
     const V2 lcA = W.v2(GOI_B_LOCAL_CENTER, ia), lcB = W.v2(GOI_B_LOCAL_CENTER, ib);
     const float radA = m.radius[fa], radB = m.radius[fb];
     const int mtype = W.i32(GOI_C_MTYPE, slot);
-    const int cnt = W.i32(GOI_C_COUNT, slot);
+    const int cnt = W.ccount(slot);
     const V2 ln = W.v2(GOI_C_LOCAL_NORMAL, slot), lp = W.v2(GOI_C_LOCAL_POINT, slot);
     const V2 pl0 = W.v2(GOI_C_POINT_LOCAL, 2 * slot), pl1 = W.v2(GOI_C_POINT_LOCAL, 2 * slot + 1);
     R.seti(i, CF_SLOT, slot); R.seti(i, CF_IA, ia); R.seti(i, CF_IB, ib);

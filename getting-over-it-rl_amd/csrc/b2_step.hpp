@@ -298,7 +298,7 @@ GOI_D void cs_position_row(const DModel& m, const World& W, const Rows& R, int i
     const int fa = W.fa(slot), fb = W.fb(slot);
     const int ia = W.ba(slot), ib = W.bb(slot);
     R.seti(i, CF_SLOT, slot); R.seti(i, CF_IA, ia); R.seti(i, CF_IB, ib);
-    R.seti(i, CF_PC_COUNT, W.i32(GOI_C_COUNT, slot)); R.seti(i, CF_MTYPE, W.i32(GOI_C_MTYPE, slot));
+    R.seti(i, CF_PC_COUNT, W.ccount(slot)); R.seti(i, CF_MTYPE, W.i32(GOI_C_MTYPE, slot));
     R.set2(i, CF_LN, W.v2(GOI_C_LOCAL_NORMAL, slot)); R.set2(i, CF_LP, W.v2(GOI_C_LOCAL_POINT, slot));
     R.set2(i, CF_PL0, W.v2(GOI_C_POINT_LOCAL, 2 * slot)); R.set2(i, CF_PL1, W.v2(GOI_C_POINT_LOCAL, 2 * slot + 1));
     R.set2(i, CF_LCA, W.v2(GOI_B_LOCAL_CENTER, ia)); R.set2(i, CF_LCB, W.v2(GOI_B_LOCAL_CENTER, ib));
@@ -320,7 +320,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     }
     W.set_tflag(min_slot, 0);
     W.set_tcount(min_slot, W.tcount(min_slot) + 1);
-    if (!W.u8(GOI_C_TOUCHING, min_slot)) {
+    if (!W.touching(min_slot)) {
         W.set_ten(min_slot, 0);
         restore(W, A, bkA);
         restore(W, Bb, bkB);
@@ -355,7 +355,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
             evaluate(m, W.fa(c), W.fb(c), W.xf(ca), W.xf(cb), s.linear_slop, mf);
             if (contact_update(W, c, mf)) { W.wake(ca); W.wake(cb); }
             W.set_ten(c, 1);
-            if (!W.u8(GOI_C_TOUCHING, c)) {
+            if (!W.touching(c)) {
                 restore(W, other, bk);
                 continue;
             }

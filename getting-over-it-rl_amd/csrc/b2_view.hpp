@@ -73,7 +73,7 @@ constexpr int kBodyMirrorMutable = 10;
 // whole step (loaded once, written back once) and holds the per-world work arrays (contact list order, island
 // lists and stacks, new-pair buffer), which would otherwise live in private scratch memory.
 struct Workspace {
-    int o_pair, o_key, o_fa, o_fb, o_bab, o_tmeta, o_ttoi, o_order, o_newp, o_corder, o_cisl;  // [C]
+    int o_pair, o_key, o_fa, o_fb, o_bab, o_cmeta, o_tmeta, o_ttoi, o_order, o_newp, o_corder, o_cisl;  // [C]
     int o_awake, o_active, o_bisl, o_stack, o_fwork, o_ibuf;                                            // [B]
     int o_qbox;                                                                                         // [4 R]
     int o_nlive;                                                                                        // [1]
@@ -86,7 +86,7 @@ struct Workspace {
         int o = 0;
         k.o_body = o; o += 8 * B;
         k.o_bm = o; o += kBodyMirrorWords * B;
-        k.o_pair = o; o += C; k.o_key = o; o += C; k.o_fa = o; o += C; k.o_fb = o; o += C; k.o_bab = o; o += C;
+        k.o_pair = o; o += C; k.o_key = o; o += C; k.o_fa = o; o += C; k.o_fb = o; o += C; k.o_bab = o; o += C; k.o_cmeta = o; o += C;
         k.o_tmeta = o; o += C; k.o_ttoi = o; o += C;
         k.o_order = o; o += C; k.o_newp = o; o += C; k.o_corder = o; o += C; k.o_cisl = o; o += C;
         k.o_awake = o; o += B; k.o_active = o; o += B; k.o_bisl = o; o += B; k.o_stack = o; o += B; k.o_fwork = o; o += B; k.o_ibuf = o; o += B;
@@ -126,6 +126,14 @@ struct World {
     GOI_D int ba(int c) const { return wi(k.o_bab, c) & 0xff; }
     GOI_D int bb(int c) const { return (wi(k.o_bab, c) >> 8) & 0xff; }
     GOI_D void set_bodies(int c, int a, int b) const { wi(k.o_bab, c) = a | (b << 8); }
+    // contacts.touching (bit 0) and contacts.count (bits 8-15), read from the workspace and written through
+    GOI_D bool touching(int c) const { return wi(k.o_cmeta, c) & 1; }
+    GOI_D int ccount(int c) const { return (wi(k.o_cmeta, c) >> 8) & 0xff; }
+    GOI_D void set_touch_count(int c, bool t, int n) const {
+        wi(k.o_cmeta, c) = (t ? 1 : 0) | (n << 8);
+        u8(GOI_C_TOUCHING, c) = t ? 1 : 0;
+        i32(GOI_C_COUNT, c) = n;
+    }
     GOI_D int& awake(int b) const { return wi(k.o_awake, b); }    // bodies.awake
     GOI_D int& active(int b) const { return wi(k.o_active, b); }  // bodies.active (read-only in a step)
     // toi.flag (bit 0), toi.enabled (bit 1) and toi.count (bits 8-15) of a slot, packed in one word
@@ -201,6 +209,7 @@ struct World {
             const int a = i32(GOI_C_FA, c), b = i32(GOI_C_FB, c);
             fa(c) = a;
             fb(c) = b;
+            wi(k.o_cmeta, c) = (u8(GOI_C_TOUCHING, c) ? 1 : 0) | (i32(GOI_C_COUNT, c) << 8);
             if (pair(c) >= 0) set_bodies(c, m.fixture_body[a], m.fixture_body[b]);
         }
         for (int b = 0; b < B; ++b) {
