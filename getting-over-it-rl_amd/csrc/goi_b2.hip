@@ -147,7 +147,8 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
 
 // The whole b2World::Step (step.py:28-47) of one world per lane: FindNewContacts where new_fixture, Collide,
 // Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to share the block's manifold and TOI work.
-__global__ void __launch_bounds__(kBlock) k_step(DModel m, Launch L) {
+// At most 256 registers (two waves per SIMD): the second wave hides the latency chains of the first.
+__global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) {
     extern __shared__ int lds[];
     stage_nodes(m, L, lds);
     const int lane = threadIdx.x;
@@ -468,11 +469,11 @@ static int worlds_per_wave(int n, size_t ws_bytes_per_world) {
     if (forced > 0)
         return std::min<long>(forced, std::max<long>(1, (kMaxLdsBytes - kBlock * sizeof(int)) / ws_bytes_per_world));
     // Fewer worlds per wave fill more SIMDs, shrink the slowest lane a wave waits for and give each world more lanes
-    // in the block-cooperative passes, but past one wave per SIMD (the register budget of k_step allows one) the
-    // launch needs a second round. Measured at 16384 worlds of the 4-body rig: 32 -> 1.56 ms, 16 -> 1.48, 8 -> 2.08.
-    // Aim for one wave per SIMD (4 per CU).
+    // in the block-cooperative passes, but past the waves a SIMD can hold (k_step's register budget allows two) the
+    // launch needs a second round. Measured at 16384 worlds of the 4-body rig, two waves per SIMD: 16 -> 1.32 ms,
+    // 8 -> 1.25 (one wave per SIMD: 32 -> 1.56, 16 -> 1.48). Aim for two waves per SIMD (8 per CU).
     int wpw = kBlock;
-    while (wpw > 1 && (long)n / wpw < 4L * cu_count()) wpw /= 2;
+    while (wpw > 1 && (long)n / wpw < 8L * cu_count()) wpw /= 2;
     while (wpw > 1 && ws_bytes_per_world * wpw + kBlock * sizeof(int) > kMaxLdsBytes) wpw /= 2;
     return wpw;
 }
