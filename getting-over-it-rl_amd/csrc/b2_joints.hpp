@@ -186,10 +186,14 @@ GOI_D void jn_solve_velocity(const Bodies& bd, const Rows& R, int i, bool v24) {
     float i0 = R.getf(i, JF_IMP0), i1 = R.getf(i, JF_IMP1), i2 = R.getf(i, JF_IMP2);
     float i3 = R.getf(i, JF_IMP3), i4 = R.getf(i, JF_IMP4), mi = R.getf(i, JF_MIMP);
     const float maximp = R.getf(i, JF_MAXIMP), mspeed = R.getf(i, JF_MSPEED), mmass = R.getf(i, JF_MMASS);
+    // the revolute fields load with the rest, in one batch (a branch would serialize them behind it)
+    const V2 jrA = R.get2(i, JF_RA), jrB = R.get2(i, JF_RB);
+    const float jangle = R.getf(i, JF_ANGLE), jinv_dt = R.getf(i, JF_INVDT);
+    const float jlower = R.getf(i, JF_LOWER), jupper = R.getf(i, JF_UPPER);
     V2 vA = bd.v(ia), vB = bd.v(ib);
     float wA = bd.w(ia), wB = bd.w(ib);
     if (type == GOI_REVOLUTE) {
-        const V2 rA = R.get2(i, JF_RA), rB = R.get2(i, JF_RB);
+        const V2 rA = jrA, rB = jrB;
         const bool fixed = (iA + iB) == 0.0f;
         if (v24) {
             if (emotor && !fixed) {
@@ -201,15 +205,15 @@ GOI_D void jn_solve_velocity(const Bodies& bd, const Rows& R, int i, bool v24) {
                 wB = wB + iB * impulse;
             }
             if (elimit && !fixed) {
-                const float angle = R.getf(i, JF_ANGLE), inv_dt = R.getf(i, JF_INVDT);
-                float C = angle - R.getf(i, JF_LOWER);
+                const float angle = jangle, inv_dt = jinv_dt;
+                float C = angle - jlower;
                 float impulse = -mmass * ((wB - wA) + bmax(C, 0.0f) * inv_dt);
                 float old = i3;
                 i3 = bmax(i3 + impulse, 0.0f);
                 impulse = i3 - old;
                 wA = wA - iA * impulse;
                 wB = wB + iB * impulse;
-                C = R.getf(i, JF_UPPER) - angle;
+                C = jupper - angle;
                 impulse = -mmass * ((wA - wB) + bmax(C, 0.0f) * inv_dt);
                 old = i4;
                 i4 = bmax(i4 + impulse, 0.0f);
@@ -324,9 +328,9 @@ GOI_D void jn_solve_velocity(const Bodies& bd, const Rows& R, int i, bool v24) {
 }
 
 // the point part of the revolute position solve (joints.py:501-520)
-GOI_D bool rev_point(const Rows& R, int i, V2& cA, float& aA, V2& cB, float& aB, float ang_err, const GoiSettings& s) {
-    const float mA = R.getf(i, JF_MA), mB = R.getf(i, JF_MB), iA = R.getf(i, JF_IIA), iB = R.getf(i, JF_IIB);
-    const V2 rA = mul(rot_of(aA), R.get2(i, JF_LA)), rB = mul(rot_of(aB), R.get2(i, JF_LB));
+GOI_D bool rev_point(float mA, float mB, float iA, float iB, V2 la, V2 lb, V2& cA, float& aA, V2& cB, float& aB,
+                     float ang_err, const GoiSettings& s) {
+    const V2 rA = mul(rot_of(aA), la), rB = mul(rot_of(aB), lb);
     const V2 C = ((cB + rB) - cA) - rA;
     const float pos_err = length(C);
     const float kxx = ((mA + mB) + iA * rA.y * rA.y) + iB * rB.y * rB.y;
@@ -344,13 +348,17 @@ GOI_D bool jn_solve_position(const Bodies& bd, const Rows& R, int i, const GoiSe
     const float mA = R.getf(i, JF_MA), mB = R.getf(i, JF_MB), iA = R.getf(i, JF_IIA), iB = R.getf(i, JF_IIB);
     const bool elimit = R.geti(i, JF_ELIMIT) != 0;
     const float lower = R.getf(i, JF_LOWER), upper = R.getf(i, JF_UPPER), ref = R.getf(i, JF_REF);
+    // the revolute fields load with the rest, in one batch
+    const float jmmass = R.getf(i, JF_MMASS);
+    const int jst = R.geti(i, JF_STATE);
+    const V2 jla = R.get2(i, JF_LA), jlb = R.get2(i, JF_LB);
     const float mac = s.max_angular_correction;
     V2 cA = bd.c(ia), cB = bd.c(ib);
     float aA = bd.a(ia), aB = bd.a(ib);
     bool ok;
     if (type == GOI_REVOLUTE) {
         const bool fixed = (iA + iB) == 0.0f;
-        const float mmass = R.getf(i, JF_MMASS);
+        const float mmass = jmmass;
         float ang_err = 0.0f;
         if (s.revolute_v24) {
             if (elimit && !fixed) {
@@ -365,7 +373,7 @@ GOI_D bool jn_solve_position(const Bodies& bd, const Rows& R, int i, const GoiSe
                 ang_err = babs(C);
             }
         } else {
-            const int st = R.geti(i, JF_STATE);
+            const int st = jst;
             if (elimit && st != kInactive && !fixed) {
                 const float angle = (aB - aA) - ref;
                 float li;
@@ -388,7 +396,7 @@ GOI_D bool jn_solve_position(const Bodies& bd, const Rows& R, int i, const GoiSe
                 aB = aB + iB * li;
             }
         }
-        ok = rev_point(R, i, cA, aA, cB, aB, ang_err, s);
+        ok = rev_point(mA, mB, iA, iB, jla, jlb, cA, aA, cB, aB, ang_err, s);
     } else if (type == GOI_PRISMATIC) {
         const Rot qA = rot_of(aA), qB = rot_of(aB);
         const V2 rA = mul(qA, R.get2(i, JF_LA)), rB = mul(qB, R.get2(i, JF_LB));
