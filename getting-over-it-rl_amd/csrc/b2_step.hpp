@@ -190,12 +190,17 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     if (dbg.contact_order)
         for (int c = 0; c < W.C; ++c) dbg.contact_order[(size_t)c * W.pitch + W.w] = c < I.nc ? I.corder(c) : -1;
     if (dbg.n_islands) dbg.n_islands[W.w] = I.n;
-    // SynchronizeFixtures of the non-static island bodies, then FindNewContacts
+    // SynchronizeFixtures of the non-static island bodies, then FindNewContacts for the rows it re-fattened: Box2D's
+    // move buffer (b2BroadPhase::m_moveBuffer), empty at the end of every step. A candidate between rows whose fat
+    // AABBs did not change was decided by the last search of the previous step and its contact, if any, still exists
+    // (Collide destroys only contacts whose fat AABBs separated), so the result is the full scan's; a world that ever
+    // dropped a candidate (overflow) keeps scanning all rows, since its dropped pairs may now find a slot.
+    unsigned long long refat = 0ull;
     for (int b = 0; b < W.B; ++b) {
         if (I.body_island(b) < 0 || W.is_static(b)) continue;
-        sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
+        refat |= sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
     }
-    find_new_contacts(m, W);
+    find_new_contacts(m, W, W.i32(GOI_S_OVERFLOW, 0) == 0 ? refat : ~0ull);
 }
 
 // ---------------------------------------------------------------- b2World::SolveTOI for one world
