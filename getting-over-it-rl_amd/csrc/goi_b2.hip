@@ -460,12 +460,9 @@ static size_t workspace_bytes(int B, int C, int J, int R) {
 // a launch wants at least a few wavefronts per SIMD (256 CUs x 4 SIMDs) even when that leaves lanes idle.
 // GOI_WORLDS_PER_WAVE overrides (1..64).
 static int worlds_per_wave(int n, size_t ws_bytes_per_world) {
-    static int forced = -1;
-    if (forced < 0) {
-        const char* e = getenv("GOI_WORLDS_PER_WAVE");
-        forced = e ? atoi(e) : 0;
-        if (forced < 0 || forced > kBlock) forced = 0;
-    }
+    const char* e = getenv("GOI_WORLDS_PER_WAVE");  // read per call: tests vary it within one process
+    int forced = e ? atoi(e) : 0;
+    if (forced < 0 || forced > kBlock) forced = 0;
     if (forced > 0)
         return std::min<long>(forced, std::max<long>(1, (kMaxLdsBytes - kBlock * sizeof(int)) / ws_bytes_per_world));
     // Fewer worlds per wave fill more SIMDs, shrink the slowest lane a wave waits for and give each world more lanes

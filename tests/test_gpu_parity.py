@@ -148,3 +148,36 @@ def test_malformed_device_state_is_rejected():
     bad = dev._replace(bodies=dev.bodies._replace(w=dev.bodies.w.cpu()))
     with pytest.raises(ValueError):
         b2.step_(m, bad, s, cfg.dt)
+
+
+def test_new_fixture_forces_full_search(oracle):
+    """A State edited outside step (here: live contacts removed from the table) gets a full FindNewContacts when
+    new_fixture is set, as Box2D's e_newFixture asks: the device step then matches the oracle's full scan bit for
+    bit, and the removed contacts come back."""
+    s, m, st, cfg = b2.scenes.make_config(4, 256)
+    ref = oracle.copy(st)
+    for _ in range(5):
+        oracle.step_(m, ref, s, cfg.dt)
+    live = np.asarray(ref.contacts.pair) >= 0
+    drop = live & (np.arange(live.shape[1])[None, :] % 2 == 0)
+    assert drop.sum() > 100
+    ref.contacts.pair[drop] = -1
+    ref.contacts.touching[drop] = False
+    ref.contacts.count[drop] = 0
+    ref.new_fixture[...] = True
+    dev = b2.layout.to_device(ref, "cuda")
+    for k in range(3):
+        b2.step_(m, dev, s, cfg.dt)
+        oracle.step_(m, ref, s, cfg.dt)
+        assert leaf_mismatches(ref, b2.layout.to_host(dev)) == [], k
+    assert (np.asarray(ref.contacts.pair) >= 0).sum() > live.sum() - drop.sum()  # the search re-created contacts
+
+
+@pytest.mark.parametrize("wpw", [1, 2, 4, 32, 64])
+def test_worlds_per_wave_variants(oracle, monkeypatch, wpw):
+    """The block-cooperative passes (manifolds, TOIs) for other world counts per wavefront than the default (the
+    library reads GOI_WORLDS_PER_WAVE at every call): config 4, 256 worlds, 10 steps with actions, bit for bit."""
+    monkeypatch.setenv("GOI_WORLDS_PER_WAVE", str(wpw))
+    s, m, st, cfg = b2.scenes.make_config(4, 256)
+    rng = np.random.default_rng(21)
+    _run(m, st, s, cfg.dt, 10, oracle, [b2.scenes.actions(rng, 256) for _ in range(10)])
