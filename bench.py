@@ -79,6 +79,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=4)
     ap.add_argument("--worlds", type=int, default=None)
+    ap.add_argument("--edges", choices=("quad", "native"), default="quad",
+                    help="terrain edges as thin polygon quads (the default) or as a native b2ChainShape")
     ap.add_argument("--cpu-steps", type=int, default=None,
                     help="steps per oracle pass for cpu_baseline (default: warmup + steps; 0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum CPU time of the cpu_baseline sample")
@@ -107,7 +109,7 @@ def main():
 
     b2 = importlib.import_module("getting-over-it-rl_amd.box2d")
     scenes = b2.scenes
-    settings, model, state, cfg = scenes.make_config(args.config, args.worlds)
+    settings, model, state, cfg = scenes.make_config(args.config, args.worlds, edges=args.edges)
     n = int(np.asarray(state.bodies.type).shape[0])
     B, R, J, C = b2.world.dims(state)
     dev = b2.layout.to_device(state, "cuda")
@@ -141,13 +143,13 @@ def main():
     achieved = n * bpw / (kern_ms / 1e3) / 1e9
     host = b2.layout.to_host(dev)
     finite = bool(np.isfinite(np.asarray(host.bodies.c)).all())
-    workload = f"config{args.config}"
+    workload = f"config{args.config}" + ("" if args.edges == "quad" else "_native_edges")
     traffic = traffic_from_profiles("k_step", workload)
 
     cpu = None
     cpu_steps = args.warmup + args.steps if args.cpu_steps is None else args.cpu_steps
     if cpu_steps > 0:
-        s2, m2, st2, _ = scenes.make_config(args.config, args.worlds)
+        s2, m2, st2, _ = scenes.make_config(args.config, args.worlds, edges=args.edges)
         host_acts = acts[:cpu_steps].cpu().numpy()
         cpu = cpu_baseline(m2, st2, s2, cfg, host_acts, scenes.apply_actions, args.cpu_seconds)
 
@@ -164,7 +166,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded terrain + rig generators, random unit-disk actions)",
-        "config": {"workload": f"{cfg.name}: {n} worlds, 4-body rig, terrain {cfg.n_edges} edges + {cfg.n_rocks} "
+        "config": {"workload": f"{cfg.name}: {n} worlds, 4-body rig, terrain {cfg.n_edges} edges "
+                               f"({'thin quads' if args.edges == 'quad' else 'native chain'}) + {cfg.n_rocks} "
                                f"rocks (seed {cfg.seed}), v~N(0,{cfg.v_sigma}), head w~U[-{cfg.head_w},{cfg.head_w}], "
                                f"dt {cfg.dt}, 8/3 iterations, TOI on (stock rule)",
                    "worlds": n, "bodies": B, "dynamic_fixtures": R, "joints": J, "contact_slots": C},

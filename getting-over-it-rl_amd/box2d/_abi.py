@@ -12,7 +12,7 @@ import numpy as np
 PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = PKG / "lib" / "libgoi_b2.so"
 NUM_LEAVES = 71
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 GOI_OK, GOI_E_ARG, GOI_E_SHAPE, GOI_E_HIP, GOI_E_UNSUPPORTED = 0, -1, -2, -3, -4
 
@@ -48,7 +48,7 @@ class GoiModelDesc(ctypes.Structure):
         (n, _P) for n in ("fixture_body", "shape_type", "radius", "count", "verts", "normals", "joint_type", "joint_a",
                           "joint_b", "local_anchor_a", "local_anchor_b", "local_axis_a", "local_yaxis_a",
                           "reference_angle", "pair_a", "pair_b", "fixture_slot", "static_fat", "static_friction",
-                          "static_restitution", "body_type", "toi_bodies")]
+                          "static_restitution", "body_type", "toi_bodies", "centroid", "edge_flags")]
 
 
 class GoiStateView(ctypes.Structure):
@@ -130,4 +130,6 @@ def model_desc(model):
     for name, dt in fields.items():
         setattr(d, name, _ptr(arr(getattr(model, name), dt)))
     d.toi_bodies = _ptr(arr(model.toi_bodies, U)) if model.toi_bodies is not None else None
+    d.centroid = _ptr(arr(model.centroid, F))
+    d.edge_flags = _ptr(arr(model.edge_flags, I))
     return d, keep

@@ -1,8 +1,9 @@
 """Seeded synthetic worlds: the static terrain (edge chain + convex rocks), the 4-body character rig with its
 action-driven motor, the five benchmark configurations, and small deterministic test scenes.
 
-Terrain edges are thin polygon quads (shapes.edge_quad): the reference has no edge or chain shapes
-(goi_jax/box2d/shapes.py:13), so every contact stays on reference-defined polygon code.
+Terrain edges are thin polygon quads (shapes.edge_quad) by default: the reference has no edge or chain shapes
+(goi_jax/box2d/shapes.py:13), so every contact stays on reference-defined polygon code. `edges="native"` builds the
+same chain as a b2ChainShape (native edges with ghost vertices) instead.
 
 Fixture order (= broad-phase proxy order): the terrain body's fixtures first (edges, then rocks), then the rig bodies'
 (pot, torso, handle, head), then any extra boxes. Candidate index of (terrain fixture t, rig fixture d) is therefore
@@ -140,14 +141,20 @@ def add_rig(d, origin=(0.0, 10.0), friction=0.5):
     return ids
 
 
-def build_world(cfg, settings=None):
-    """(Model, single-world State, chain points) of a configuration: terrain body 0, rig bodies 1-4, boxes after."""
+def build_world(cfg, settings=None, edges="quad"):
+    """(Model, single-world State, chain points) of a configuration: terrain body 0, rig bodies 1-4, boxes after.
+    edges: "quad" (thin polygon quads) or "native" (one b2ChainShape)."""
     settings = settings or settings_for(cfg)
     pts, rocks = terrain(cfg.seed, cfg.n_edges, cfg.n_rocks)
     d = wd.WorldDef(settings)
     g = d.add_body(wd.STATIC)
-    for i in range(cfg.n_edges):
-        d.add_edge(g, pts[i], pts[i + 1], friction=0.8)
+    if edges == "native":
+        d.add_chain(g, pts, friction=0.8)
+    elif edges == "quad":
+        for i in range(cfg.n_edges):
+            d.add_edge(g, pts[i], pts[i + 1], friction=0.8)
+    else:
+        raise ValueError(f"edges must be 'quad' or 'native', not {edges!r}")
     for v, _ in rocks:
         d.add_polygon(g, v, raw=True, friction=0.8)
     x0 = 20.0
@@ -251,11 +258,11 @@ def apply_actions(joint_speed, joint_torque, a):
     joint_torque[:, MOTOR_JOINT] = MOTOR_TORQUE * mag
 
 
-def make_config(k, n=None):
+def make_config(k, n=None, edges="quad"):
     """(settings, compact Model, batched compact numpy State, Config) of benchmark configuration k (1-5)."""
     cfg = CONFIGS[k]
     settings = settings_for(cfg)
-    model, state, pts = build_world(cfg, settings)
+    model, state, pts = build_world(cfg, settings, edges)
     st = place_worlds(cfg, model, state, pts, n)
     cm = wd.compact_model(model, st)
     return settings, cm, wd.compact_state(cm, st), cfg
@@ -514,6 +521,34 @@ def scene_island_walk(s):
     return d
 
 
+def scene_edges(s):
+    """Native edge shapes: an open chain with convex and concave corners and a collinear run, a closed loop, an
+    isolated two-sided segment and a segment with ghost vertices but no neighbours; boxes slide across the chain's
+    junctions, polygons and circles land on corners, a fast circle reaches the loop by TOI."""
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC)
+    d.add_chain(g, [(-12, 4), (-8, 0.5), (-4, 0), (-2, 0), (0, 0), (2, 0), (4, 0.8), (6, 0.2), (9, 2.5), (12, 6)],
+                friction=0.6)
+    d.add_chain(g, [(-1, 3), (1, 3), (1, 3.5), (-1, 3.5)], loop=True, friction=0.6)
+    d.add_segment(g, (5, 4), (8, 4.5), friction=0.4)
+    d.add_segment(g, (-7, 5), (-5, 5), v0=(-8, 5.5), v3=(-4, 4.5), friction=0.4)
+    a = d.add_body(wd.DYNAMIC, (-3.5, 0.26), 0.0, (6.0, 0.0), 0.0, mass=1.0, inertia=F32(1) / F32(24))
+    d.add_box(a, (0.5, 0.25), friction=0.1)
+    b = d.add_body(wd.DYNAMIC, (-1.0, 0.4), 0.3, (-3.0, 0.0), 0.0, mass=0.8, inertia=0.02)
+    d.add_polygon(b, _ngon(5, 0.3), friction=0.3)
+    c = d.add_body(wd.DYNAMIC, (-9.0, 2.5), 0.0, (1.0, 0.0), 0.0, mass=0.5, inertia=0.01)
+    d.add_circle(c, 0.25, friction=0.5)
+    e = d.add_body(wd.DYNAMIC, (4.2, 2.0), 0.8, (0.0, -2.0), 1.0, mass=1.2, inertia=0.05)
+    d.add_polygon(e, [(-0.3, -0.2), (0.4, -0.1), (0.1, 0.35)], friction=0.5)
+    f = d.add_body(wd.DYNAMIC, (6.5, 5.0), 0.0, (0.0, 0.0), 0.0, mass=0.3, inertia=0.005)
+    d.add_circle(f, 0.15, friction=0.2)
+    h = d.add_body(wd.DYNAMIC, (-6.0, 6.0), 0.2, (0.0, 0.0), 0.0, mass=0.6, inertia=0.02)
+    d.add_box(h, (0.3, 0.2), friction=0.4)
+    k = d.add_body(wd.DYNAMIC, (0.0, 9.0), 0.0, (0.5, -120.0), 0.0, mass=0.2, inertia=0.002, bullet=True)
+    d.add_circle(k, 0.1, friction=0.3)
+    return d
+
+
 # (builder, settings, contact capacity); game settings as the reference scenes use them
 def _game(**kw):
     return Settings.game(**kw)
@@ -538,6 +573,7 @@ TEST_SCENES = {
     "multi_event": (scene_multi_event, lambda: _toi(gravity=(0.0, 0.0)), 16),
     "stock_bullets": (scene_stock_bullets, lambda: _toi(unity=False), 16),
     "island_walk": (scene_island_walk, _toi, 32),
+    "edges": (scene_edges, _toi, 32),
 }
 
 

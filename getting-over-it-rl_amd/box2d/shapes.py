@@ -1,8 +1,10 @@
 """Host-side shape construction in float32, b2PolygonShape / b2CircleShape v2.3.1 op for op (mirror of
-goi_jax/box2d/shapes.py:1-113), plus the thin-quad encoding of terrain edge segments.
+goi_jax/box2d/shapes.py:1-113), the thin-quad encoding of terrain edge segments, and native b2EdgeShape /
+b2ChainShape children (which the reference does not have, shapes.py:13).
 
 A fixture holds one shape. Polygons store up to 8 vertices and edge normals, padded by repeating vertex 0 (pads are
-masked by `count`); a circle stores its centre in vertex 0 and count 1.
+masked by `count`); a circle stores its centre in vertex 0 and count 1; an edge stores m_vertex1, m_vertex2,
+m_vertex0, m_vertex3 in vertices 0-3 with count 2, and its m_hasVertex0 / m_hasVertex3 in the fixture's edge flags.
 """
 import math
 
@@ -11,7 +13,8 @@ import numpy as np
 from .settings import EPSILON, MAX_POLYGON_VERTICES
 
 F32 = np.float32
-CIRCLE, POLYGON = 0, 2  # b2Shape::Type (shapes.py:13)
+CIRCLE, EDGE, POLYGON = 0, 1, 2  # b2Shape::Type (shapes.py:13; the reference leaves out edge 1)
+EDGE_HAS_V0, EDGE_HAS_V3, EDGE_CHAIN = 1, 2, 4  # edge flags; EDGE_CHAIN: a b2ChainShape child
 
 
 def host_sin_cos(a):
@@ -128,6 +131,72 @@ def edge_quad(p0, p1, thickness=0.1):
     n = np.array([-d[1], d[0]]) / np.hypot(d[0], d[1])
     q = np.array([p0 - thickness * n, p1 - thickness * n, p1, p0], np.float64)  # CCW: bottom edge first
     return polygon_raw(q.astype(F32))
+
+
+def centroid_raw(v):
+    """m_centroid of a raw polygon as the reference oracle's builder accumulates it: sum of (1/n) * v[i] in order
+    (goi_jax/reference/capi.cpp:386-401)."""
+    n = len(v)
+    inv = F32(F32(1.0) / F32(n))
+    cx, cy = F32(0), F32(0)
+    for x, y in np.asarray(v, F32):
+        cx, cy = F32(cx + F32(inv * x)), F32(cy + F32(inv * y))
+    return np.array([cx, cy], F32)
+
+
+def centroid_set(v):
+    """ComputeCentroid of b2PolygonShape::Set v2.3.1: area-weighted triangle fan from the origin."""
+    v = np.asarray(v, F32)
+    n = len(v)
+    cx, cy, area = F32(0), F32(0), F32(0)
+    inv3 = F32(F32(1.0) / F32(3.0))
+    for i in range(n):
+        p2, p3 = v[i], v[i + 1] if i + 1 < n else v[0]
+        e1x, e1y, e2x, e2y = p2[0], p2[1], p3[0], p3[1]  # p1 = (0, 0)
+        d = F32(F32(e1x * e2y) - F32(e1y * e2x))
+        tri = F32(F32(0.5) * d)
+        area = F32(area + tri)
+        w = F32(tri * inv3)
+        sx, sy = F32(F32(F32(0) + p2[0]) + p3[0]), F32(F32(F32(0) + p2[1]) + p3[1])
+        cx, cy = F32(cx + F32(w * sx)), F32(cy + F32(w * sy))
+    inv = F32(F32(1.0) / area)
+    return np.array([F32(inv * cx), F32(inv * cy)], F32)
+
+
+def edge_shape(v1, v2, v0=None, v3=None):
+    """b2EdgeShape::Set(v1, v2) with optional ghost vertices: ((4, 2) vertices v1, v2, v0, v3; flags)."""
+    v = np.zeros((4, 2), F32)
+    v[0], v[1] = v1, v2
+    flags = 0
+    if v0 is not None:
+        v[2], flags = v0, flags | EDGE_HAS_V0
+    if v3 is not None:
+        v[3], flags = v3, flags | EDGE_HAS_V3
+    if v[0][0] == v[1][0] and v[0][1] == v[1][1]:
+        raise ValueError("degenerate edge")
+    return v, flags
+
+
+def chain_edges(points, loop=False, prev_vertex=None, next_vertex=None):
+    """The child edges of b2ChainShape::CreateChain / CreateLoop (GetChildEdge): edge i runs from point i to i + 1,
+    with ghosts at points i - 1 and i + 2 where they exist (the loop wraps; an open chain takes prev_vertex /
+    next_vertex, b2ChainShape::SetPrevVertex / SetNextVertex, at its ends)."""
+    p = [np.asarray(x, F32) for x in np.asarray(points, F32).reshape(-1, 2)]
+    if loop:
+        if len(p) < 3:
+            raise ValueError("a loop needs 3 points")
+        prev_vertex, next_vertex = p[-1], p[1]
+        p = p + [p[0]]
+    if len(p) < 2:
+        raise ValueError("a chain needs 2 points")
+    n = len(p)
+    out = []
+    for i in range(n - 1):
+        v0 = p[i - 1] if i > 0 else prev_vertex
+        v3 = p[i + 2] if i < n - 2 else next_vertex
+        v, flags = edge_shape(p[i], p[i + 1], v0, v3)
+        out.append((v, flags | EDGE_CHAIN))
+    return out
 
 
 def pad(v, n):

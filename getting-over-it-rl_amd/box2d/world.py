@@ -47,6 +47,8 @@ class Model(NamedTuple):
     static_friction: np.ndarray = None  # f32[F]
     static_restitution: np.ndarray = None  # f32[F]
     body_type: np.ndarray = None  # i32[B] the body types every world shares (the compact layout requires it)
+    centroid: np.ndarray = None  # f32[F, 2] b2PolygonShape::m_centroid (read by edge contacts only)
+    edge_flags: np.ndarray = None  # i32[F] edge fixtures' ghost flags (shapes.EDGE_HAS_V0 | EDGE_HAS_V3 | EDGE_CHAIN)
 
 
 class Bodies(NamedTuple):
@@ -281,27 +283,29 @@ class WorldDef:
         b["v"] = np.array([F32(b["v"][0] + F32(-w * dy)), F32(b["v"][1] + F32(w * dx))], F32)
 
     def _add_fixture(self, body, shape_type, verts, normals, radius, friction, restitution, sensor, layer,
-                     category, mask, group):
+                     category, mask, group, centroid=(0.0, 0.0), edge_flags=0, count=None):
         vv, nn = shapes.pad(verts, normals)
-        self.fixtures.append(dict(body=body, shape_type=shape_type, verts=vv, normals=nn, count=len(verts),
-                                  radius=F32(radius), friction=F32(friction), restitution=F32(restitution),
-                                  sensor=bool(sensor), layer=int(layer) & 31, category=category, mask=mask,
-                                  group=group))
+        self.fixtures.append(dict(body=body, shape_type=shape_type, verts=vv, normals=nn,
+                                  count=len(verts) if count is None else count, radius=F32(radius),
+                                  friction=F32(friction), restitution=F32(restitution), sensor=bool(sensor),
+                                  layer=int(layer) & 31, category=category, mask=mask, group=group,
+                                  centroid=np.asarray(centroid, F32), edge_flags=int(edge_flags)))
         return len(self.fixtures) - 1
 
     def add_polygon(self, body, vertices, radius=None, raw=False, *, friction=0.2, restitution=0.0, density=0.0,
                     sensor=False, layer=0, category=1, mask=0xFFFF, group=0):
         v, n = shapes.polygon_raw(vertices) if raw else shapes.polygon_set(vertices, self.settings.linear_slop)
         r = self.settings.polygon_radius if radius is None else radius
+        c = shapes.centroid_raw(v) if raw else shapes.centroid_set(v)
         return self._add_fixture(body, shapes.POLYGON, v, n, r, friction, restitution, sensor, layer, category,
-                                 mask, group)
+                                 mask, group, centroid=c)
 
     def add_box(self, body, half_extents, center=(0, 0), angle=0.0, radius=None, *, friction=0.2, restitution=0.0,
                 density=0.0, sensor=False, layer=0, category=1, mask=0xFFFF, group=0):
         v, n = shapes.box(half_extents[0], half_extents[1], center, angle)
         r = self.settings.polygon_radius if radius is None else radius
         return self._add_fixture(body, shapes.POLYGON, v, n, r, friction, restitution, sensor, layer, category,
-                                 mask, group)
+                                 mask, group, centroid=center)
 
     def add_circle(self, body, radius, center=(0, 0), *, friction=0.2, restitution=0.0, density=0.0, sensor=False,
                    layer=0, category=1, mask=0xFFFF, group=0):
@@ -314,7 +318,27 @@ class WorldDef:
         """A terrain edge segment as a thin polygon quad (shapes.edge_quad)."""
         v, n = shapes.edge_quad(p0, p1, thickness)
         return self._add_fixture(body, shapes.POLYGON, v, n, self.settings.polygon_radius, friction, restitution,
-                                 False, layer, category, mask, group)
+                                 False, layer, category, mask, group, centroid=shapes.centroid_raw(v))
+
+    def _add_edge_shape(self, body, v, flags, friction, restitution, layer, category, mask, group):
+        if self.bodies[body]["type"] != STATIC:
+            raise ValueError("edge shapes belong to static bodies (the terrain)")
+        return self._add_fixture(body, shapes.EDGE, v, np.zeros((4, 2), F32), self.settings.polygon_radius,
+                                 friction, restitution, False, layer, category, mask, group, edge_flags=flags,
+                                 count=2)
+
+    def add_segment(self, body, v1, v2, v0=None, v3=None, *, friction=0.2, restitution=0.0, layer=0, category=1,
+                    mask=0xFFFF, group=0):
+        """A native b2EdgeShape from v1 to v2 with optional ghost vertices v0 (before v1) and v3 (after v2)."""
+        v, flags = shapes.edge_shape(v1, v2, v0, v3)
+        return self._add_edge_shape(body, v, flags, friction, restitution, layer, category, mask, group)
+
+    def add_chain(self, body, points, loop=False, prev_vertex=None, next_vertex=None, *, friction=0.2,
+                  restitution=0.0, layer=0, category=1, mask=0xFFFF, group=0):
+        """A native b2ChainShape as its child edges, one fixture each in child order (shapes.chain_edges).
+        Returns the fixture ids."""
+        return [self._add_edge_shape(body, v, flags, friction, restitution, layer, category, mask, group)
+                for v, flags in shapes.chain_edges(points, loop, prev_vertex, next_vertex)]
 
     def _add_joint(self, **j):
         self.joints.append(j)
@@ -344,7 +368,8 @@ class WorldDef:
                                collide=collide)
 
     def candidate_pairs(self):
-        """b2BroadPhase::UpdatePairs order with b2Contact::Create's polygon-first swap (world.py:308-329)."""
+        """b2BroadPhase::UpdatePairs order with b2Contact::Create's swap (world.py:308-329): a polygon before a
+        circle, an edge before either (b2Contact's registry); no contact between two edges."""
         no_collide = {frozenset((j["a"], j["b"])) for j in self.joints if not j["collide"]}
         out = []
         fs, bs = self.fixtures, self.bodies
@@ -358,7 +383,10 @@ class WorldDef:
                     continue
                 if frozenset((fi["body"], fk["body"])) in no_collide or not _filter_ok(fi, fk, self.layer_masks):
                     continue
-                if fi["shape_type"] == shapes.CIRCLE and fk["shape_type"] == shapes.POLYGON:
+                ti, tk = fi["shape_type"], fk["shape_type"]
+                if ti == shapes.EDGE and tk == shapes.EDGE:
+                    continue
+                if (ti == shapes.CIRCLE and tk == shapes.POLYGON) or (tk == shapes.EDGE and ti != shapes.EDGE):
                     out.append((k, i))
                 else:
                     out.append((i, k))
@@ -399,7 +427,8 @@ class WorldDef:
             reference_angle=jarr("ref"),
             pair_a=np.array([p[0] for p in pairs], I32).reshape(-1),
             pair_b=np.array([p[1] for p in pairs], I32).reshape(-1),
-            toi_bodies=bodies.bullet | bodies.continuous, body_type=bodies.type.copy())
+            toi_bodies=bodies.bullet | bodies.continuous, body_type=bodies.type.copy(),
+            centroid=farr("centroid", F32, (2,)), edge_flags=farr("edge_flags", I32))
         fb = model.fixture_body
         fat = fixture_fat_host(model, bodies.xf_p[fb, 0], bodies.xf_p[fb, 1], q[fb, 0], q[fb, 1])
         fixtures = Fixtures(friction=farr("friction"), restitution=farr("restitution"), fat=fat)
@@ -418,7 +447,7 @@ class WorldDef:
 
 def fixture_fat_host(model, px, py, c, s):
     """b2Shape::ComputeAABB at the given transforms, then the b2_aabbExtension margin (shapes.py:118-146), in
-    float32 with C's operation order."""
+    float32 with C's operation order. A chain child's box has no skin radius (b2ChainShape::ComputeAABB)."""
     F = model.fixture_body.shape[0]
     out = np.zeros((F, 4), F32)
     e = F32(0.1)
@@ -432,6 +461,8 @@ def fixture_fat_host(model, px, py, c, s):
             lx, ly, ux, uy = F32(x - r), F32(y - r), F32(x + r), F32(y + r)
         else:
             n = int(model.count[f])
+            if model.edge_flags is not None and model.edge_flags[f] & shapes.EDGE_CHAIN:
+                r = F32(0)
             vx, vy = model.verts[f, :n, 0], model.verts[f, :n, 1]
             wx = ((c[f] * vx).astype(F32) - (s[f] * vy).astype(F32)).astype(F32) + F32(px[f])
             wy = ((s[f] * vx).astype(F32) + (c[f] * vy).astype(F32)).astype(F32) + F32(py[f])

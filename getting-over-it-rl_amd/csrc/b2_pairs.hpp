@@ -140,13 +140,13 @@ GOI_D int collide_mark(const DModel& m, const World& W) {
     return nt;
 }
 
-GOI_D void collide_task(const DModel& m, const Coop& co, int o, int i, float linear_slop) {
+GOI_D void collide_task(const DModel& m, const Coop& co, int o, int i, const GoiSettings& s) {
     const World W = co.world(o);
     const Rows R = co.task_rows(o);
     const int k = W.newp(i);
     const int fa = W.fa(k), fb = W.fb(k);
     Manifold mf;
-    evaluate(m, fa, fb, W.xf(W.ba(k)), W.xf(W.bb(k)), linear_slop, mf);
+    evaluate(m, fa, fb, W.xf(W.ba(k)), W.xf(W.bb(k)), s, mf);
     R.seti(i, MT_MTYPE, mf.mtype);
     R.seti(i, MT_COUNT, mf.count);
     R.set2(i, MT_LN, mf.ln);
@@ -193,9 +193,9 @@ GOI_D void collide_apply(const DModel& m, const World& W, const Rows& R) {
 }
 
 // Collide for the block: called by all lanes together; `valid` marks the lanes that own a world.
-GOI_D void collide_block(const DModel& m, const Coop& co, const World& W, bool valid, float linear_slop) {
+GOI_D void collide_block(const DModel& m, const Coop& co, const World& W, bool valid, const GoiSettings& s) {
     const int nt = valid ? collide_mark(m, W) : 0;
-    coop_run(co, nt, [&](int o, int i) { collide_task(m, co, o, i, linear_slop); });
+    coop_run(co, nt, [&](int o, int i) { collide_task(m, co, o, i, s); });
     if (valid) collide_apply(m, W, co.task_rows(threadIdx.x));
 }
 

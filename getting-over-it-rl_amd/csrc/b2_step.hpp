@@ -320,7 +320,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     body_advance(W, Bb, min_alpha);
     {
         Manifold mf;
-        evaluate(m, fa, fb, W.xf(A), W.xf(Bb), s.linear_slop, mf);
+        evaluate(m, fa, fb, W.xf(A), W.xf(Bb), s, mf);
         if (contact_update(W, min_slot, mf)) { W.wake(A); W.wake(Bb); }
     }
     W.set_tflag(min_slot, 0);
@@ -357,7 +357,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
             const SweepBackup bk = backup(W, other);
             if (!((bflag >> other) & 1ull)) body_advance(W, other, min_alpha);
             Manifold mf;
-            evaluate(m, W.fa(c), W.fb(c), W.xf(ca), W.xf(cb), s.linear_slop, mf);
+            evaluate(m, W.fa(c), W.fb(c), W.xf(ca), W.xf(cb), s, mf);
             if (contact_update(W, c, mf)) { W.wake(ca); W.wake(cb); }
             W.set_ten(c, 1);
             if (!W.touching(c)) {

@@ -35,6 +35,8 @@ struct DModel {
     const float* static_friction;
     const float* static_restitution;
     const int* body_type;       // [B]
+    const V2* centroid;         // [F] polygon centroids (edge-polygon contacts); zeros when the Model has no edges
+    const int* edge_flags;      // [F] edge ghost flags; zeros when absent
     int any_toi_body;           // Model.toi_bodies has a set entry (or is absent)
     // Static BVH over the static fixtures' fat AABBs, nodes in preorder (node 0 = root, a node's first child is the
     // next node). node_link.x = escape: the node after this node's subtree; node_link.y = -1 for an internal node,

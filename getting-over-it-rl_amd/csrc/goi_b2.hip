@@ -141,7 +141,7 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
         if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
         W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     }
-    if (!start_only) collide_block(m, block_coop(L, W, lds, w0), W, valid, L.s.linear_slop);
+    if (!start_only) collide_block(m, block_coop(L, W, lds, w0), W, valid, L.s);
     if (valid) W.store_mirror();
 }
 
@@ -167,7 +167,7 @@ __global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) {
         if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
         W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     }
-    collide_block(m, co, W, valid, L.s.linear_slop);
+    collide_block(m, co, W, valid, L.s);
     if (valid) solve_world(m, W, bd, CR, joint_rows(L, W.w), L.s, L.dt, L.dbg);
     if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, co);
     if (!valid) return;
@@ -289,11 +289,25 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
         if (t != GOI_REVOLUTE && t != GOI_PRISMATIC && t != GOI_WELD)
             return fail(GOI_E_UNSUPPORTED, "goi_model_create: unknown joint type");
     }
+    bool any_edge = false;
     for (int f = 0; f < F; ++f) {
         const int t = desc->shape_type[f], c = desc->count[f];
-        if ((t != GOI_CIRCLE && t != GOI_POLYGON) || c < 1 || c > GOI_MAX_POLY)
+        if ((t != GOI_CIRCLE && t != GOI_POLYGON && t != GOI_EDGE) || c < 1 || c > GOI_MAX_POLY)
             return fail(GOI_E_UNSUPPORTED, "goi_model_create: bad shape");
         if (desc->fixture_body[f] < 0 || desc->fixture_body[f] >= B) return fail(GOI_E_ARG, "goi_model_create: bad fixture body");
+        if (t == GOI_EDGE) {
+            if (c != 2) return fail(GOI_E_ARG, "goi_model_create: an edge fixture has count 2");
+            if (desc->body_type[desc->fixture_body[f]] != GOI_STATIC)
+                return fail(GOI_E_UNSUPPORTED, "goi_model_create: edge fixtures belong to static bodies");
+            any_edge = true;
+        }
+    }
+    if (any_edge && !desc->centroid)
+        return fail(GOI_E_ARG, "goi_model_create: edge fixtures need the polygon centroids");
+    for (int p = 0; p < P; ++p) {
+        const int a = desc->pair_a[p], b = desc->pair_b[p];
+        if (a >= 0 && a < F && b >= 0 && b < F && desc->shape_type[b] == GOI_EDGE)
+            return fail(GOI_E_ARG, "goi_model_create: a candidate pair names its edge fixture first");
     }
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
     GoiModel* M = new GoiModel();
@@ -382,6 +396,15 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     UP(static_friction, desc->static_friction, F);
     UP(static_restitution, desc->static_restitution, F);
     UP(body_type, desc->body_type, B);
+    // host copies live until the stream synchronises below
+    std::vector<V2> cen(std::max(F, 1), V2{0.0f, 0.0f});
+    std::vector<int> eflags(std::max(F, 1), 0);
+    for (int f = 0; f < F; ++f) {
+        if (desc->centroid) cen[f] = V2{desc->centroid[2 * f], desc->centroid[2 * f + 1]};
+        if (desc->edge_flags) eflags[f] = desc->edge_flags[f];
+    }
+    UP(centroid, cen.data(), F);
+    UP(edge_flags, eflags.data(), F);
     UP(node_box, bvh.box.data(), bvh.box.size());
     UP(node_link, bvh.link.data(), bvh.link.size());
     UP(leaf_fat, leaf_fat.data(), leaf_fat.size());

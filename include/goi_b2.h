@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define GOI_ABI_VERSION 1
+#define GOI_ABI_VERSION 2
 
 #define GOI_OK 0
 #define GOI_E_ARG (-1)
@@ -49,6 +49,17 @@ extern "C" {
 #define GOI_CIRCLE 0
 #define GOI_POLYGON 2
 #define GOI_MAX_POLY 8
+/* b2Shape::e_edge, which the reference does not use (shapes.py:13: "edge 1 and chain 3 are not used by the game").
+ * An edge fixture holds b2EdgeShape: verts[f][0..1] = m_vertex1, m_vertex2 and count[f] = 2 (its distance proxy),
+ * verts[f][2] = m_vertex0 and verts[f][3] = m_vertex3 (the ghost vertices), edge_flags[f] = GOI_EDGE_HAS_V0 |
+ * GOI_EDGE_HAS_V3 as m_hasVertex0 / m_hasVertex3 are set. A b2ChainShape is its child edges (b2ChainShape::
+ * GetChildEdge), one edge fixture each, in child order, flagged GOI_EDGE_CHAIN (their fat AABBs, which the caller
+ * computes, have no skin radius: b2ChainShape::ComputeAABB). Edge fixtures belong to static bodies only, and a
+ * candidate pair names the edge first (b2Contact::Create). */
+#define GOI_EDGE 1
+#define GOI_EDGE_HAS_V0 1
+#define GOI_EDGE_HAS_V3 2
+#define GOI_EDGE_CHAIN 4
 
 /* The State leaves in pytree order (world.py:70-174). Per-world inner shapes in brackets: B bodies, R fixture rows
  * (F in the full layout, the non-static fixtures in the compact layout, world.py:400-434), J joints, C slots. */
@@ -166,7 +177,10 @@ typedef struct GoiSettings {
  * compact layout (world.py:437-472): fixture_slot[f] is the State row of fixture f or -1 for a static body's
  * fixture, whose fat AABB, friction and restitution are static_fat/static_friction/static_restitution[f].
  * body_type[B] are the body types every world shares (the compact layout requires it, world.py:447-450).
- * toi_bodies[B] (nullable) is Model.toi_bodies (world.py:48-50). */
+ * toi_bodies[B] (nullable) is Model.toi_bodies (world.py:48-50).
+ * centroid[F,2] and edge_flags[F] exist only for edge fixtures (GOI_EDGE): b2PolygonShape::m_centroid of each
+ * polygon, which edge-polygon contacts read, and each edge's ghost flags. Both may be NULL when no fixture is an
+ * edge. */
 typedef struct GoiModelDesc {
     int32_t F, J, P, B;
     const int32_t* fixture_body;   /* [F] */
@@ -191,6 +205,8 @@ typedef struct GoiModelDesc {
     const float* static_restitution; /* [F] or NULL */
     const int32_t* body_type;      /* [B] */
     const uint8_t* toi_bodies;     /* [B] or NULL */
+    const float* centroid;         /* [F,2] or NULL (required when an edge fixture exists) */
+    const int32_t* edge_flags;     /* [F] or NULL (no ghost vertices) */
 } GoiModelDesc;
 
 /* A batch of States on the device: GOI_NUM_LEAVES device pointers, worlds-minor with the given pitch (>= n). */

@@ -34,7 +34,10 @@
  *   - the revolute v2.4.1 velocity/position rows, prismatic and weld rows (joints.py:302-343, 482-498);
  *   - time_of_impact / distance iteration paths (toi.py:230-459);
  *   - toi_event's island walk membership and break (toi.py:604-716);
- *   - the min-TOI tie rule in toi_search (toi.py:552-556).
+ *   - the min-TOI tie rule in toi_search (toi.py:552-556);
+ *   - the native edge colliders collide_edge_circle / collide_edge_polygon, which have no reference function (the
+ *     reference has no edge shape, shapes.py:13): they restate Box2D 2.3.1's b2CollideEdge.cpp and are pinned by
+ *     closed forms, brute force and the thin-quad polygon path only (tests/test_edges.py).
  */
 #include <math.h>
 #include <stdint.h>
@@ -422,11 +425,244 @@ static void collide_circles(const GoiModelDesc* m, int fa, Xf xfa, int fb, Xf xf
     out->id[0] = 0; out->id[1] = 0;
 }
 
-/* b2Contact::Evaluate by shape types (collide.py:189-207) */
-static void evaluate(const GoiModelDesc* m, int fa, int fb, Xf xfa, Xf xfb, float linear_slop, Manifold* out) {
+/* ---- native edge shapes. The reference has no edge shape (shapes.py:13, __init__.py:53); these restate Box2D
+ * 2.3.1's b2CollideEdge.cpp (b2CollideEdgeAndCircle, b2EPCollider) from the published source of that release. An
+ * edge fixture holds m_vertex1, m_vertex2 in vertices 0-1 and the ghosts m_vertex0, m_vertex3 in vertices 2-3, with
+ * GOI_EDGE_HAS_V0 / GOI_EDGE_HAS_V3 in edge_flags. The manifold's unused point slot follows the polygon
+ * convention above: slot 1 holds the second clip point; the circle cases write the key into both slots. */
+
+static inline int edge_flags_of(const GoiModelDesc* m, int f) { return m->edge_flags ? m->edge_flags[f] : 0; }
+static inline V2 centroid_of(const GoiModelDesc* m, int f) {
+    return m->centroid ? v2(m->centroid[2 * f], m->centroid[2 * f + 1]) : v2(0.0f, 0.0f);
+}
+
+/* b2CollideEdgeAndCircle: regions A, B (vertex contacts, suppressed where the neighbouring edge owns the circle)
+ * and AB (face contact, two-sided normal). */
+static void collide_edge_circle(const GoiModelDesc* m, int fa, Xf xfa, int fb, Xf xfb, Manifold* out) {
+    out->count = 0;
+    V2 q = xmulT(xfa, xmul(xfb, vert(m, fb, 0)));
+    V2 a = vert(m, fa, 0), b = vert(m, fa, 1);
+    V2 e = sub(b, a);
+    float u = dot(e, sub(b, q)); /* barycentric coordinates */
+    float v = dot(e, sub(q, a));
+    float radius = m->radius[fa] + m->radius[fb];
+    int flags = edge_flags_of(m, fa);
+    V2 pl = vert(m, fb, 0);
+    out->pl[0] = pl; out->pl[1] = pl;
+    if (v <= 0.0f) { /* region A */
+        V2 d = sub(q, a);
+        if (dot(d, d) > radius * radius) return;
+        if (flags & GOI_EDGE_HAS_V0) {
+            V2 e1 = sub(a, vert(m, fa, 2));
+            if (dot(e1, sub(a, q)) > 0.0f) return; /* in region AB of the previous edge */
+        }
+        out->mtype = CIRCLES; out->count = 1;
+        out->ln = v2(0.0f, 0.0f); out->lp = a;
+        out->id[0] = out->id[1] = feature_key(0, 0, E_VERTEX, E_VERTEX);
+        return;
+    }
+    if (u <= 0.0f) { /* region B */
+        V2 d = sub(q, b);
+        if (dot(d, d) > radius * radius) return;
+        if (flags & GOI_EDGE_HAS_V3) {
+            V2 e2 = sub(vert(m, fa, 3), b);
+            if (dot(e2, sub(q, b)) > 0.0f) return; /* in region AB of the next edge */
+        }
+        out->mtype = CIRCLES; out->count = 1;
+        out->ln = v2(0.0f, 0.0f); out->lp = b;
+        out->id[0] = out->id[1] = feature_key(1, 0, E_VERTEX, E_VERTEX);
+        return;
+    }
+    float den = dot(e, e); /* region AB */
+    V2 p = scl(1.0f / den, add(scl(u, a), scl(v, b)));
+    V2 d = sub(q, p);
+    if (dot(d, d) > radius * radius) return;
+    V2 n = v2(-e.y, e.x);
+    if (dot(n, sub(q, a)) < 0.0f) n = v2(-n.x, -n.y);
+    normalize(&n);
+    out->mtype = FACE_A; out->count = 1;
+    out->ln = n; out->lp = a;
+    out->id[0] = out->id[1] = feature_key(0, 0, E_FACE, E_VERTEX);
+}
+
+/* b2EPCollider::Collide: edge A against polygon B in A's frame. Classify the centroid of B as in front of or behind
+ * the edge and bound the admissible normals by the neighbouring edges (ghost vertices), take the edge axis or the
+ * best admissible polygon axis (hysteresis 0.98 / 0.001), then clip the incident edge against the reference face's
+ * sides (no radius on the side planes). Skin radius 2 * b2_polygonRadius. */
+static void collide_edge_polygon(const GoiModelDesc* m, int fa, Xf xfa, int fb, Xf xfb, const GoiSettings* st,
+                                 Manifold* out) {
+    out->count = 0;
+    Xf xf = xmulT_xf(xfa, xfb);
+    V2 cb = xmul(xf, centroid_of(m, fb));
+    V2 v0 = vert(m, fa, 2), v1 = vert(m, fa, 0), v2_ = vert(m, fa, 1), v3 = vert(m, fa, 3);
+    int flags = edge_flags_of(m, fa);
+    int has0 = (flags & GOI_EDGE_HAS_V0) != 0, has3 = (flags & GOI_EDGE_HAS_V3) != 0;
+    V2 edge1 = sub(v2_, v1);
+    normalize(&edge1);
+    V2 n1 = v2(edge1.y, -edge1.x);
+    float offset1 = dot(n1, sub(cb, v1));
+    float offset0 = 0.0f, offset2 = 0.0f;
+    int convex1 = 0, convex2 = 0;
+    V2 n0 = v2(0.0f, 0.0f), n2 = v2(0.0f, 0.0f);
+    if (has0) {
+        V2 edge0 = sub(v1, v0);
+        normalize(&edge0);
+        n0 = v2(edge0.y, -edge0.x);
+        convex1 = crs(edge0, edge1) >= 0.0f;
+        offset0 = dot(n0, sub(cb, v0));
+    }
+    if (has3) {
+        V2 edge2 = sub(v3, v2_);
+        normalize(&edge2);
+        n2 = v2(edge2.y, -edge2.x);
+        convex2 = crs(edge1, edge2) > 0.0f;
+        offset2 = dot(n2, sub(cb, v2_));
+    }
+    int front;
+    V2 normal, lower, upper;
+    if (has0 && has3) {
+        if (convex1 && convex2) {
+            front = offset0 >= 0.0f || offset1 >= 0.0f || offset2 >= 0.0f;
+            if (front) { normal = n1; lower = n0; upper = n2; }
+            else { normal = neg(n1); lower = neg(n1); upper = neg(n1); }
+        } else if (convex1) {
+            front = offset0 >= 0.0f || (offset1 >= 0.0f && offset2 >= 0.0f);
+            if (front) { normal = n1; lower = n0; upper = n1; }
+            else { normal = neg(n1); lower = neg(n2); upper = neg(n1); }
+        } else if (convex2) {
+            front = offset2 >= 0.0f || (offset0 >= 0.0f && offset1 >= 0.0f);
+            if (front) { normal = n1; lower = n1; upper = n2; }
+            else { normal = neg(n1); lower = neg(n1); upper = neg(n0); }
+        } else {
+            front = offset0 >= 0.0f && offset1 >= 0.0f && offset2 >= 0.0f;
+            if (front) { normal = n1; lower = n1; upper = n1; }
+            else { normal = neg(n1); lower = neg(n2); upper = neg(n0); }
+        }
+    } else if (has0) {
+        if (convex1) {
+            front = offset0 >= 0.0f || offset1 >= 0.0f;
+            if (front) { normal = n1; lower = n0; upper = neg(n1); }
+            else { normal = neg(n1); lower = n1; upper = neg(n1); }
+        } else {
+            front = offset0 >= 0.0f && offset1 >= 0.0f;
+            if (front) { normal = n1; lower = n1; upper = neg(n1); }
+            else { normal = neg(n1); lower = n1; upper = neg(n0); }
+        }
+    } else if (has3) {
+        if (convex2) {
+            front = offset1 >= 0.0f || offset2 >= 0.0f;
+            if (front) { normal = n1; lower = neg(n1); upper = n2; }
+            else { normal = neg(n1); lower = neg(n1); upper = n1; }
+        } else {
+            front = offset1 >= 0.0f && offset2 >= 0.0f;
+            if (front) { normal = n1; lower = neg(n1); upper = n1; }
+            else { normal = neg(n1); lower = neg(n2); upper = n1; }
+        }
+    } else {
+        front = offset1 >= 0.0f;
+        if (front) { normal = n1; lower = neg(n1); upper = neg(n1); }
+        else { normal = neg(n1); lower = n1; upper = n1; }
+    }
+
+    /* polygon B in frame A */
+    int cnt = m->count[fb];
+    V2 pv[NPOLY], pn[NPOLY];
+    for (int i = 0; i < cnt; ++i) {
+        pv[i] = xmul(xf, vert(m, fb, i));
+        pn[i] = rmul(xf.q, nrm(m, fb, i));
+    }
+    float radius = 2.0f * st->polygon_radius;
+
+    /* ComputeEdgeSeparation: the edge axis is always known */
+    float edge_sep = MAXF;
+    for (int i = 0; i < cnt; ++i) {
+        float sv = dot(normal, sub(pv[i], v1));
+        if (sv < edge_sep) edge_sep = sv;
+    }
+    if (edge_sep > radius) return;
+
+    /* ComputePolygonSeparation: the first separating polygon axis, else the deepest admissible one */
+    int poly_known = 0, poly_index = -1;
+    float poly_sep = -MAXF;
+    V2 perp = v2(-normal.y, normal.x);
+    for (int i = 0; i < cnt; ++i) {
+        V2 n = neg(pn[i]);
+        float s1 = dot(n, sub(pv[i], v1));
+        float s2 = dot(n, sub(pv[i], v2_));
+        float sv = bmin(s1, s2);
+        if (sv > radius) { poly_known = 1; poly_index = i; poly_sep = sv; break; }
+        if (dot(n, perp) >= 0.0f) {
+            if (dot(sub(n, upper), normal) < -st->angular_slop) continue;
+        } else {
+            if (dot(sub(n, lower), normal) < -st->angular_slop) continue;
+        }
+        if (sv > poly_sep) { poly_known = 1; poly_index = i; poly_sep = sv; }
+    }
+    if (poly_known && poly_sep > radius) return;
+
+    int edge_primary = !poly_known || !(poly_sep > 0.98f * edge_sep + 0.001f);
+    ClipV ie[2];
+    int rf_i1, rf_i2;
+    V2 rf_v1, rf_v2, rf_n;
+    if (edge_primary) {
+        out->mtype = FACE_A;
+        int best = 0; /* the polygon normal most anti-parallel to the edge normal */
+        float bestv = dot(normal, pn[0]);
+        for (int i = 1; i < cnt; ++i) {
+            float val = dot(normal, pn[i]);
+            if (val < bestv) { bestv = val; best = i; }
+        }
+        int i1 = best, i2 = i1 + 1 < cnt ? i1 + 1 : 0;
+        ie[0].v = pv[i1]; ie[0].ia = 0; ie[0].ib = i1; ie[0].ta = E_FACE; ie[0].tb = E_VERTEX;
+        ie[1].v = pv[i2]; ie[1].ia = 0; ie[1].ib = i2; ie[1].ta = E_FACE; ie[1].tb = E_VERTEX;
+        if (front) { rf_i1 = 0; rf_i2 = 1; rf_v1 = v1; rf_v2 = v2_; rf_n = n1; }
+        else { rf_i1 = 1; rf_i2 = 0; rf_v1 = v2_; rf_v2 = v1; rf_n = neg(n1); }
+    } else {
+        out->mtype = FACE_B;
+        ie[0].v = v1; ie[0].ia = 0; ie[0].ib = poly_index; ie[0].ta = E_VERTEX; ie[0].tb = E_FACE;
+        ie[1].v = v2_; ie[1].ia = 0; ie[1].ib = poly_index; ie[1].ta = E_VERTEX; ie[1].tb = E_FACE;
+        rf_i1 = poly_index;
+        rf_i2 = rf_i1 + 1 < cnt ? rf_i1 + 1 : 0;
+        rf_v1 = pv[rf_i1]; rf_v2 = pv[rf_i2]; rf_n = pn[rf_i1];
+    }
+    V2 side1 = v2(rf_n.y, -rf_n.x);
+    V2 side2 = neg(side1);
+    float side_off1 = dot(side1, rf_v1);
+    float side_off2 = dot(side2, rf_v2);
+    ClipV cp1[2], cp2[2];
+    if (clip_segment(cp1, ie, side1, side_off1, rf_i1) < 2) return;
+    if (clip_segment(cp2, cp1, side2, side_off2, rf_i2) < 2) return;
+    if (edge_primary) { out->ln = rf_n; out->lp = rf_v1; }
+    else { out->ln = nrm(m, fb, rf_i1); out->lp = vert(m, fb, rf_i1); }
+    int keep[2];
+    V2 pts[2];
+    int32_t ids[2];
+    for (int i = 0; i < 2; ++i) {
+        float sep = dot(rf_n, sub(cp2[i].v, rf_v1));
+        keep[i] = sep <= radius;
+        if (edge_primary) {
+            pts[i] = xmulT(xf, cp2[i].v);
+            ids[i] = feature_key(cp2[i].ia, cp2[i].ib, cp2[i].ta, cp2[i].tb);
+        } else {
+            pts[i] = cp2[i].v;
+            ids[i] = feature_key(cp2[i].ib, cp2[i].ia, cp2[i].tb, cp2[i].ta);
+        }
+    }
+    out->count = keep[0] + keep[1];
+    out->pl[0] = keep[0] ? pts[0] : pts[1];
+    out->id[0] = keep[0] ? ids[0] : ids[1];
+    out->pl[1] = pts[1];
+    out->id[1] = ids[1];
+}
+
+/* b2Contact::Evaluate by shape types (collide.py:189-207); b2Contact::Create puts the polygon before a circle and
+ * an edge before either */
+static void evaluate(const GoiModelDesc* m, int fa, int fb, Xf xfa, Xf xfb, const GoiSettings* st, Manifold* out) {
     int ta = m->shape_type[fa], tb = m->shape_type[fb];
-    if (ta == GOI_POLYGON && tb == GOI_POLYGON) collide_polygons(m, fa, xfa, fb, xfb, linear_slop, out);
+    if (ta == GOI_POLYGON && tb == GOI_POLYGON) collide_polygons(m, fa, xfa, fb, xfb, st->linear_slop, out);
     else if (ta == GOI_POLYGON && tb == GOI_CIRCLE) collide_polygon_circle(m, fa, xfa, fb, xfb, out);
+    else if (ta == GOI_EDGE && tb == GOI_POLYGON) collide_edge_polygon(m, fa, xfa, fb, xfb, st, out);
+    else if (ta == GOI_EDGE && tb == GOI_CIRCLE) collide_edge_circle(m, fa, xfa, fb, xfb, out);
     else collide_circles(m, fa, xfa, fb, xfb, out);
 }
 
@@ -540,7 +776,7 @@ static void collide(const Ctx* x, W* w, int* order) {
             continue;
         }
         Manifold mf;
-        evaluate(m, fa, fb, body_xf(w, ba), body_xf(w, bb), x->s->linear_slop, &mf);
+        evaluate(m, fa, fb, body_xf(w, ba), body_xf(w, bb), x->s, &mf);
         if (contact_update(w, k, &mf)) { wake(w, ba); wake(w, bb); }
     }
 }
@@ -2083,7 +2319,7 @@ static void toi_event(const Ctx* x, W* w, Work* k, int min_slot, float min_alpha
     body_advance(w, A, min_alpha);
     body_advance(w, Bb, min_alpha);
     Manifold mf;
-    evaluate(m, fa, fb, body_xf(w, A), body_xf(w, Bb), x->s->linear_slop, &mf);
+    evaluate(m, fa, fb, body_xf(w, A), body_xf(w, Bb), x->s, &mf);
     if (contact_update(w, min_slot, &mf)) { wake(w, A); wake(w, Bb); }
     w->t_flag[min_slot] = 0;
     w->t_count[min_slot] += 1;
@@ -2118,7 +2354,7 @@ static void toi_event(const Ctx* x, W* w, Work* k, int min_slot, float min_alpha
             backup_sweep(w, k, other);
             if (!k->bflag[other]) body_advance(w, other, min_alpha);
             Manifold mc;
-            evaluate(m, w->c_fa[c], w->c_fb[c], body_xf(w, ca), body_xf(w, cb), x->s->linear_slop, &mc);
+            evaluate(m, w->c_fa[c], w->c_fb[c], body_xf(w, ca), body_xf(w, cb), x->s, &mc);
             if (contact_update(w, c, &mc)) { wake(w, ca); wake(w, cb); }
             w->t_enabled[c] = 1;
             if (!w->c_touching[c]) { restore_sweep(w, k, other); continue; }
@@ -2298,14 +2534,14 @@ int oracle_collide(const GoiModelDesc* m, void* const* leaves, int32_t n, int32_
 }
 
 /* Test hooks: the narrowphase, the GJK distance and b2TimeOfImpact on one pair, for the brute-force checks. */
-int oracle_evaluate(const GoiModelDesc* m, int fa, int fb, const float* xfa, const float* xfb, float linear_slop,
-                    int32_t* mtype_count, float* geo, int32_t* ids) {
+int oracle_evaluate(const GoiModelDesc* m, int fa, int fb, const float* xfa, const float* xfb,
+                    const GoiSettings* settings, int32_t* mtype_count, float* geo, int32_t* ids) {
     Xf a, b;
     a.p = v2(xfa[0], xfa[1]); a.q.c = xfa[2]; a.q.s = xfa[3];
     b.p = v2(xfb[0], xfb[1]); b.q.c = xfb[2]; b.q.s = xfb[3];
     Manifold mf;
     memset(&mf, 0, sizeof(mf));
-    evaluate(m, fa, fb, a, b, linear_slop, &mf);
+    evaluate(m, fa, fb, a, b, settings, &mf);
     mtype_count[0] = mf.mtype; mtype_count[1] = mf.count;
     geo[0] = mf.ln.x; geo[1] = mf.ln.y; geo[2] = mf.lp.x; geo[3] = mf.lp.y;
     geo[4] = mf.pl[0].x; geo[5] = mf.pl[0].y; geo[6] = mf.pl[1].x; geo[7] = mf.pl[1].y;

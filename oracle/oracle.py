@@ -48,7 +48,7 @@ def load(path):
     L.oracle_collide.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), P] + [ctypes.c_int32] * 5 + [
         ctypes.POINTER(_abi.GoiSettings), ctypes.c_int32]
     L.oracle_evaluate.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), ctypes.c_int, ctypes.c_int, P, P,
-                                  ctypes.c_float, P, P, P]
+                                  ctypes.POINTER(_abi.GoiSettings), P, P, P]
     L.oracle_distance.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), ctypes.c_int, ctypes.c_int, P, P]
     L.oracle_distance.restype = ctypes.c_float
     L.oracle_toi.argtypes = [ctypes.POINTER(_abi.GoiModelDesc), ctypes.c_int, ctypes.c_int, P, P,
@@ -74,7 +74,7 @@ def model_desc(model):
     for name, dt in dict(fixture_body=I, shape_type=I, radius=F, count=I, verts=F, normals=F, joint_type=I,
                          joint_a=I, joint_b=I, local_anchor_a=F, local_anchor_b=F, local_axis_a=F, local_yaxis_a=F,
                          reference_angle=F, pair_a=I, pair_b=I, fixture_slot=I, static_fat=F, static_friction=F,
-                         static_restitution=F, body_type=I).items():
+                         static_restitution=F, body_type=I, centroid=F, edge_flags=I).items():
         setattr(d, name, arr(getattr(model, name), dt))
     d.toi_bodies = arr(model.toi_bodies, U)
     return d, keep
@@ -126,12 +126,16 @@ def collide_(model, state, settings, n_threads=0):
     return state
 
 
-def evaluate(model, fa, fb, xfa, xfb, linear_slop):
-    """The narrowphase manifold of fixtures (fa, fb) at transforms (px, py, c, s)."""
+def evaluate(model, fa, fb, xfa, xfb, settings):
+    """The narrowphase manifold of fixtures (fa, fb) at transforms (px, py, c, s). `settings` is a Settings or the
+    linear slop of stock Settings."""
+    if not isinstance(settings, box2d.Settings):
+        settings = box2d.Settings(linear_slop=np.float32(settings))
     desc, keep = model_desc(model)
+    cs = settings.to_c()
     xa, xb = np.asarray(xfa, np.float32), np.asarray(xfb, np.float32)
     mc, geo, ids = np.zeros(2, np.int32), np.zeros(8, np.float32), np.zeros(2, np.int32)
-    lib().oracle_evaluate(ctypes.byref(desc), fa, fb, xa.ctypes.data, xb.ctypes.data, np.float32(linear_slop),
+    lib().oracle_evaluate(ctypes.byref(desc), fa, fb, xa.ctypes.data, xb.ctypes.data, ctypes.byref(cs),
                           mc.ctypes.data, geo.ctypes.data, ids.ctypes.data)
     return dict(mtype=int(mc[0]), count=int(mc[1]), local_normal=geo[0:2], local_point=geo[2:4],
                 point_local=geo[4:8].reshape(2, 2), point_id=ids)

@@ -45,9 +45,12 @@ def test_scene_parity_game_iterations(name, oracle):
     _run(m, perturbed(st, 16, seed=3), s, b2.GAME_DT, 60, oracle)
 
 
-@pytest.mark.parametrize("k,n,steps", [(1, 1, 200), (3, 512, 30), (4, 512, 30), (5, 128, 20)])
-def test_config_parity(k, n, steps, oracle):
-    s, m, st, cfg = b2.scenes.make_config(k, n)
+@pytest.mark.parametrize("k,n,steps,edges", [(1, 1, 200, "quad"), (3, 512, 30, "quad"), (4, 512, 30, "quad"),
+                                              (5, 128, 20, "quad"), (4, 512, 30, "native"), (5, 128, 20, "native")])
+def test_config_parity(k, n, steps, edges, oracle):
+    """The benchmark configurations; "native" builds the terrain chain from b2EdgeShape children instead of thin
+    quads (parity with the oracle only: the reference has no edge shape)."""
+    s, m, st, cfg = b2.scenes.make_config(k, n, edges=edges)
     rng = np.random.default_rng(5)
     acts = [b2.scenes.actions(rng, n) for _ in range(steps)]
     ref = _run(m, st, s, cfg.dt, steps, oracle, acts)

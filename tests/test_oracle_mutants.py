@@ -7,6 +7,7 @@ from pathlib import Path
 
 import pytest
 
+import test_edges as E
 import test_oracle_pins as P
 from oracle import oracle as O
 
@@ -30,6 +31,14 @@ MUTANTS = [
      lambda o: P.test_islands_vs_sequential_dfs(o, "pile")),
     ("circle_radius_dropped", "float r = m->radius[fa] + m->radius[fb];", "float r = m->radius[fa];",
      lambda o: P.test_narrowphase_vs_brute_force(o, P.shape_model.__wrapped__())),
+    ("edge_circle_ghost_sign", "if (dot(e1, sub(a, q)) > 0.0f) return;", "if (dot(e1, sub(a, q)) < 0.0f) return;",
+     lambda o: E.test_edge_circle_regions(o, E.edge_world.__wrapped__())),
+    ("edge_polygon_limits_swapped", "if (dot(n, perp) >= 0.0f) {", "if (dot(n, perp) < 0.0f) {",
+     lambda o: E.test_edge_polygon_closed_forms(o, E.edge_world.__wrapped__())),
+    ("edge_polygon_one_skin", "float radius = 2.0f * st->polygon_radius;", "float radius = st->polygon_radius;",
+     lambda o: E.test_edge_polygon_closed_forms(o, E.edge_world.__wrapped__())),
+    ("edge_polygon_no_hysteresis", "!(poly_sep > 0.98f * edge_sep + 0.001f)", "!(poly_sep > edge_sep)",
+     lambda o: E.test_edge_polygon_closed_forms(o, E.edge_world.__wrapped__())),
 ]
 
 
