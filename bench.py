@@ -14,9 +14,13 @@ R = 113 B + 24 F_d + 54 J + 93 C + 21 and W = 81 B + 16 F_d + 28 J + 120 C + 17 
 J joints, C contact slots); achieved = N x (R + W) / mean k_step duration (HIP events on its stream).
 
 cpu_baseline: the CPU restatement of the same step (oracle/, C, sequential per world, OpenMP over worlds) on the host
-cores, over the same initial State and actions (warmup + timed steps), repeated to at least --cpu-seconds.
+cores, over the same initial State and actions (warmup + timed steps), repeated to at least --cpu-seconds; and one
+thread over the first 1,024 worlds.
+
+sleep_off: the same workload, initial State and actions with Settings.allow_sleep off, timed the same way.
 """
 import argparse
+import dataclasses
 import json
 import os
 import re
@@ -66,10 +70,34 @@ def cpu_baseline(model, state, settings, cfg, acts, apply, min_seconds=10.0, max
         elapsed += time.perf_counter() - t0
         done += n * len(acts)
         passes += 1
+    # one thread over the first worlds of the same workload (a shorter sample: one core is ~16x slower)
+    n1 = min(n, 1024)
+    sub = O.copy(type(state)(*[_first_worlds(x, n1) for x in state]))
+    sub_acts = [a[:n1] for a in acts]
+    done1, elapsed1, passes1 = 0, 0.0, 0
+    while elapsed1 < min_seconds / 3 and passes1 < max_passes:
+        x = O.copy(sub)
+        t0 = time.perf_counter()
+        for a in sub_acts:
+            apply(x.joints.motor_speed, x.joints.max_motor, a)
+            O.step_(model, x, settings, cfg.dt, 1)
+        elapsed1 += time.perf_counter() - t0
+        done1 += n1 * len(sub_acts)
+        passes1 += 1
     return {"value": done / elapsed, "unit": "world-steps/s", "cores": threads, "kind": "port",
             "sample": f"{cfg.name}: {passes} passes x {len(acts)} steps x {n} worlds ({done} world-steps, "
                       f"{elapsed:.1f} s) of the oracle (oracle/b2_oracle.c, -O2, OpenMP over worlds), same initial "
-                      "State and actions as the timed GPU steps"}
+                      "State and actions as the timed GPU steps",
+            "single_thread": {"value": done1 / elapsed1, "cores": 1,
+                              "sample": f"{passes1} passes x {len(sub_acts)} steps x the first {n1} worlds "
+                                        f"({elapsed1:.1f} s)"}}
+
+
+def _first_worlds(x, n):
+    """The first n worlds of a batched State group or leaf (leading world axis)."""
+    if hasattr(x, "_fields"):
+        return type(x)(*[_first_worlds(y, n) for y in x])
+    return np.ascontiguousarray(np.asarray(x)[:n])
 
 
 def main():
@@ -84,6 +112,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=None,
                     help="steps per oracle pass for cpu_baseline (default: warmup + steps; 0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum CPU time of the cpu_baseline sample")
+    ap.add_argument("--sleep-off-steps", type=int, default=None,
+                    help="timed steps of the same workload with allow_sleep off (default: --steps; 0 skips)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run only a plain device copy of MIB MiB 10 times (the rocprofv3 FETCH_SIZE/WRITE_SIZE "
                          "calibration) and exit")
@@ -143,6 +173,35 @@ def main():
     achieved = n * bpw / (kern_ms / 1e3) / 1e9
     host = b2.layout.to_host(dev)
     finite = bool(np.isfinite(np.asarray(host.bodies.c)).all())
+
+    sleep_off = None
+    off_steps = args.steps if args.sleep_off_steps is None else args.sleep_off_steps
+    if off_steps > 0:
+        # the same workload from the same initial State and actions with allow_sleep off (the reference benches
+        # report both); timed the same way
+        s_off = dataclasses.replace(settings, allow_sleep=False)
+        dev2 = b2.layout.to_device(state, "cuda")
+        sp2, tq2 = dev2.joints.motor_speed, dev2.joints.max_motor
+        for i in range(min(args.warmup, acts.shape[0])):
+            scenes.apply_actions(sp2, tq2, acts[i])
+            b2.step_(model, dev2, s_off, cfg.dt)
+        off_acts = acts[args.warmup:args.warmup + off_steps]
+        ev2 = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(off_acts.shape[0])]
+        torch.cuda.synchronize()
+        start.record()
+        for k in range(off_acts.shape[0]):
+            scenes.apply_actions(sp2, tq2, off_acts[k])
+            ev2[k][0].record()
+            b2.step_(model, dev2, s_off, cfg.dt)
+            ev2[k][1].record()
+        end.record()
+        torch.cuda.synchronize()
+        t2 = start.elapsed_time(end)
+        sleep_off = {"value": n * off_acts.shape[0] / (t2 / 1e3), "unit": "world-steps/s",
+                     "steps": int(off_acts.shape[0]), "ms_per_step": t2 / off_acts.shape[0],
+                     "kernel_ms": float(np.mean([a.elapsed_time(b) for a, b in ev2]))}
+        del dev2
     workload = f"config{args.config}" + ("" if args.edges == "quad" else "_native_edges")
     traffic = traffic_from_profiles("k_step", workload)
 
@@ -175,6 +234,7 @@ def main():
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": "k_step",
                      "kernel_ms": kern_ms, "bytes_per_world_step": bpw},
         "cpu_baseline": cpu,
+        "sleep_off": sleep_off,
         "toi_events_last_step": int(np.asarray(host.toi.events).sum()),
         "overflow": int(np.asarray(host.overflow).sum()),
         "finite": finite,

@@ -46,13 +46,22 @@ class DeviceModel:
             self.handle = None
 
 
-def device_model(model, contact_capacity, device=None):
-    """Cached DeviceModel for (model object, capacity, device)."""
+def device_model(model, contact_capacity, device=None, state=None):
+    """Cached DeviceModel for (model object, capacity, device). A compact Model built without body types (the
+    reference's compact_model keeps them in the State only, world.py:437-472) takes them from `state`, whose worlds
+    must agree."""
     key = (id(model), int(contact_capacity), str(device))
     hit = _MODELS.get(key)
     if hit is not None and hit[0] is model:
         return hit[1]
-    dm = DeviceModel(model, contact_capacity, device)
+    desc_model = model
+    if model.body_type is None and state is not None:
+        bt = np.asarray(state.bodies.type.to("cpu") if torch.is_tensor(state.bodies.type) else state.bodies.type)
+        bt = bt.reshape(-1, bt.shape[-1])
+        if not (bt == bt[0]).all():
+            raise ValueError("the device step needs body types shared by every world (compact layout)")
+        desc_model = model._replace(body_type=bt[0].astype(np.int32))
+    dm = DeviceModel(desc_model, contact_capacity, device)
     _MODELS[key] = (model, dm)
     return dm
 
@@ -64,7 +73,7 @@ def step_(model, state, settings, dt, debug=None, stream=None):
     view = layout.state_view(state)
     C = state.contacts.pair.shape[-1]
     dev = state.contacts.pair.device
-    dm = device_model(model, C, dev)
+    dm = device_model(model, C, dev, state)
     cs = settings.to_c()
     st = torch.cuda.current_stream(dev).cuda_stream if stream is None else stream
     dbg = None if debug is None else ctypes.byref(debug)
@@ -85,7 +94,7 @@ def collide_(model, state, settings, stream=None):
     view = layout.state_view(state)
     C = state.contacts.pair.shape[-1]
     dev = state.contacts.pair.device
-    dm = device_model(model, C, dev)
+    dm = device_model(model, C, dev, state)
     cs = settings.to_c()
     st = torch.cuda.current_stream(dev).cuda_stream if stream is None else stream
     _abi.check(dm.L.goi_collide(dm.handle, ctypes.byref(view), ctypes.byref(cs), ctypes.c_void_p(st)), dm.L)

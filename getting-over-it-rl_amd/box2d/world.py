@@ -46,6 +46,12 @@ class Model(NamedTuple):
     static_fat: np.ndarray = None  # f32[F, 4]
     static_friction: np.ndarray = None  # f32[F]
     static_restitution: np.ndarray = None  # f32[F]
+    # The reference's culled-scan tables for its FindNewContacts kernel (world.py:57-65, scan_tables). Accepted so
+    # that a reference Model keeps its fields and their order; unused here: goi_model_create builds a BVH over the
+    # static fat AABBs instead.
+    scan_cand: np.ndarray = None
+    scan_row: np.ndarray = None
+    scan_box: np.ndarray = None
     body_type: np.ndarray = None  # i32[B] the body types every world shares (the compact layout requires it)
     centroid: np.ndarray = None  # f32[F, 2] b2PolygonShape::m_centroid (read by edge contacts only)
     edge_flags: np.ndarray = None  # i32[F] edge fixtures' ghost flags (shapes.EDGE_HAS_V0 | EDGE_HAS_V3 | EDGE_CHAIN)

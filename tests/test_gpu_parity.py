@@ -57,6 +57,20 @@ def test_config_parity(k, n, steps, edges, oracle):
     assert np.isfinite(np.asarray(ref.bodies.c)).all()
 
 
+def test_model_without_body_types(oracle):
+    """A compact Model as the reference's compact_model returns it (no body types: they stay in the State,
+    world.py:437-472) steps the same; the body types come from the State."""
+    s, m, st = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+    ref_style = m._replace(body_type=None, centroid=None, edge_flags=None)
+    st = perturbed(st, 32, seed=4)
+    dev = b2.layout.to_device(st, "cuda")
+    ref = oracle.copy(st)
+    for k in range(20):
+        b2.step_(ref_style, dev, s, 1.0 / 60.0)
+        oracle.step_(m, ref, s, 1.0 / 60.0)
+    assert leaf_mismatches(ref, b2.layout.to_host(dev)) == []
+
+
 def test_collide_config2(oracle):
     """Broadphase + narrowphase only over 4096 worlds (the collide-only workload, seed-1 terrain): candidate pairs, slots, keys, point
     counts and manifolds bit for bit."""

@@ -95,6 +95,17 @@ def test_state_fields_follow_reference_pytree():
     assert wd.ContactTOI._fields[-1] == "events"
 
 
+def test_model_fields_extend_the_reference_model():
+    """The reference's Model fields in its order (world.py:30-65), then this package's additions, so a Model built
+    positionally or by keyword for the reference is accepted."""
+    ref = ("fixture_body", "shape_type", "radius", "count", "verts", "normals", "joint_type", "joint_a", "joint_b",
+           "local_anchor_a", "local_anchor_b", "local_axis_a", "local_yaxis_a", "reference_angle", "pair_a", "pair_b",
+           "toi_bodies", "fixture_slot", "slot_fixture", "static_fat", "static_friction", "static_restitution",
+           "scan_cand", "scan_row", "scan_box")
+    assert wd.Model._fields[:len(ref)] == ref
+    assert wd.Model._fields[len(ref):] == ("body_type", "centroid", "edge_flags")
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # compact fixture layout and scene generators
 
