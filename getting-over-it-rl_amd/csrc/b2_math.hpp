@@ -80,6 +80,23 @@ GOI_D Rot rot_of(float a) {
     return q;
 }
 
+// One remembered rotation. sin/cos are pure functions of the angle's bits, so an angle met again (bit for bit)
+// reuses the rotation computed for it: the terrain's constant angle in the position solver and in b2TimeOfImpact's
+// sweeps, and a body angle that a zero impulse left unchanged. The initial key is a NaN payload (all ones) that
+// arithmetic never generates (generated NaNs are 0x7fc00000); its rotation is NaN, as rot_of's would be.
+struct RotMemo {
+    uint32_t bits = 0x7fffffffu;
+    Rot q{__uint_as_float(0x7fffffffu), __uint_as_float(0x7fffffffu)};
+    GOI_D Rot of(float a) {
+        const uint32_t b = __float_as_uint(a);
+        if (b != bits) {
+            q = rot_of(a);
+            bits = b;
+        }
+        return q;
+    }
+};
+
 // b2Mat22::Solve / b2Mat33::Solve22
 GOI_D V2 solve22(float a11, float a12, float a21, float a22, V2 b) {
     float det = a11 * a22 - a12 * a21;

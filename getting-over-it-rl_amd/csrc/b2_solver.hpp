@@ -361,9 +361,10 @@ GOI_D PRow load_prow(const Rows& R, int i) {
 }
 
 // b2ContactSolver::SolvePositionConstraints for one row (contact_solver.py:307-354); masses given (the TOI solve
-// passes zero for bodies other than the TOI pair). Returns the row's min separation, starting at 0.
+// passes zero for bodies other than the TOI pair). Returns the row's min separation, starting at 0. The callers keep
+// one rotation memo per side across rows and passes.
 GOI_D float solve_prow(const Bodies& bd, const PRow& r, float baumgarte, float mA, float mB, float iA, float iB,
-                       float linear_slop, float max_linear_correction) {
+                       float linear_slop, float max_linear_correction, RotMemo& qa, RotMemo& qb) {
     const V2 lcA = r.lcA, lcB = r.lcB, ln = r.ln, lp = r.lp;
     const float radA = r.radA, radB = r.radB;
     V2 cA = bd.c(r.ia), cB = bd.c(r.ib);
@@ -371,8 +372,8 @@ GOI_D float solve_prow(const Bodies& bd, const PRow& r, float baumgarte, float m
     float min_sep = 0.0f;
     for (int j = 0; j < r.cnt; ++j) {
         Xf xfA, xfB;
-        xfA.q = rot_of(aA);
-        xfB.q = rot_of(aB);
+        xfA.q = qa.of(aA);
+        xfB.q = qb.of(aB);
         xfA.p = cA - mul(xfA.q, lcA);
         xfB.p = cB - mul(xfB.q, lcB);
         const V2 plj = j == 0 ? r.pl0 : r.pl1;

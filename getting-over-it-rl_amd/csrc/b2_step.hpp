@@ -99,6 +99,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     }
     // position iterations with per-island early exit (step.py:197-251)
     unsigned long long done = 0ull, all = I.n >= 64 ? ~0ull : ((1ull << I.n) - 1ull);
+    RotMemo qa, qb;
     for (int it = 0; it < s.position_iterations && done != all; ++it) {
         unsigned long long jbad = 0ull;
         for (int i = 0; i < I.n; ++i) W.fwork(i) = 0.0f;  // min separation per island
@@ -107,7 +108,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
             if ((done >> isl) & 1ull) continue;
             const PRow r = load_prow(CR, i);
             W.fwork(isl) = bmin(W.fwork(isl), solve_prow(bd, r, s.baumgarte, r.mA, r.mB, r.iA, r.iB, s.linear_slop,
-                                                         s.max_linear_correction));
+                                                         s.max_linear_correction, qa, qb));
         }
         for (int i = 0; i < I.nj; ++i) {
             const int isl = I.joint_island(JRw.geti(i, JF_JID));
@@ -380,6 +381,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     }
     const float mA_ = W.f(GOI_B_INV_MASS, A), iA_ = W.f(GOI_B_INV_INERTIA, A);
     const float mB_ = W.f(GOI_B_INV_MASS, Bb), iB_ = W.f(GOI_B_INV_INERTIA, Bb);
+    RotMemo qa, qb;
     for (int it = 0; it < 20; ++it) {
         float min_sep = 0.0f;
         for (int i = 0; i < nc; ++i) {
@@ -389,7 +391,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
             const float mA = ta ? (ia == A ? mA_ : mB_) : 0.0f, iA = ta ? (ia == A ? iA_ : iB_) : 0.0f;
             const float mB = tb ? (ib == A ? mA_ : mB_) : 0.0f, iB = tb ? (ib == A ? iA_ : iB_) : 0.0f;
             min_sep = bmin(min_sep, solve_prow(bd, cur, s.toi_baumgarte, mA, mB, iA, iB, s.linear_slop,
-                                               s.max_linear_correction));
+                                               s.max_linear_correction, qa, qb));
         }
         if (min_sep >= -1.5f * s.linear_slop) break;
     }
@@ -461,26 +463,13 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     }
 }
 
-// b2World::SolveTOI (toi.py:827-865). Called by every lane of the block (the TOI searches are cooperative);
-// `valid` marks the lanes that own a world.
+// b2World::SolveTOI (toi.py:827-865). Called by every lane of the block (the reset, the TOI searches and the final
+// copy are cooperative); `valid` marks the lanes that own a world.
 GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
-                           float dt, bool valid, const Coop& co) {
+                           float dt, bool valid, const Coop& co, const BlockCopy& bc) {
     if (W.C == 0 || m.P == 0) return;
     if (s.unity_toi && !m.any_toi_body) return;
-    if (valid) {
-        for (int b = 0; b < W.B; ++b) W.f(GOI_T_ALPHA0, b) = 0.0f;
-        for (int c = 0; c < W.C; ++c) {
-            W.set_tcount(c, 0);
-            W.ttoi(c) = 1.0f;
-            W.set_tflag(c, 0);
-            W.set_ten(c, 1);
-            W.u8(GOI_T_SOLVED, c) = 0;
-            W.f(GOI_T_NORMAL_IMPULSE, 2 * c) = 0.0f;
-            W.f(GOI_T_NORMAL_IMPULSE, 2 * c + 1) = 0.0f;
-            W.f(GOI_T_TANGENT_IMPULSE, 2 * c) = 0.0f;
-            W.f(GOI_T_TANGENT_IMPULSE, 2 * c + 1) = 0.0f;
-        }
-    }
+    reset_toi_block(bc);
     int events = 0;
     if (dt > 0.0f) {
         const int max_events = s.max_events >= 0 ? s.max_events : W.C * (kMaxSubSteps + 1) + 8;
@@ -500,10 +489,8 @@ GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, co
             found = act && toi_search_pick(W, s, slot, alpha);
         }
     }
-    if (valid) {
-        W.i32(GOI_T_EVENTS, 0) = events;
-        W.store_toi();
-    }
+    if (valid) W.i32(GOI_T_EVENTS, 0) = events;
+    store_toi_block(bc);
 }
 
 }  // namespace goi

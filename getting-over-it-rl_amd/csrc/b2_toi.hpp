@@ -12,11 +12,11 @@ struct Sweep {
     float a0, a;
 };
 
-// b2Sweep::GetTransform (toi.py:73-81)
-GOI_D Xf sweep_xf(const Sweep& sw, float beta) {
+// b2Sweep::GetTransform (toi.py:73-81); the rotation through the sweep's memo
+GOI_D Xf sweep_xf(const Sweep& sw, float beta, RotMemo& memo) {
     Xf t;
     const float omb = 1.0f - beta;
-    t.q = rot_of(omb * sw.a0 + beta * sw.a);
+    t.q = memo.of(omb * sw.a0 + beta * sw.a);
     t.p = mk(omb * sw.c0.x + beta * sw.c.x, omb * sw.c0.y + beta * sw.c.y) - mul(t.q, sw.lc);
     return t;
 }
@@ -239,8 +239,8 @@ struct SepFn {
 };
 
 GOI_D SepFn sep_init(const SimplexCache& cache, const Proxy& pA, const Sweep& sA, const Proxy& pB, const Sweep& sB,
-                     float t1) {
-    const Xf xA = sweep_xf(sA, t1), xB = sweep_xf(sB, t1);
+                     float t1, RotMemo& ma, RotMemo& mb) {
+    const Xf xA = sweep_xf(sA, t1, ma), xB = sweep_xf(sB, t1, mb);
     SepFn f;
     f.lp = mk(0.0f, 0.0f);
     if (cache.count == 1) {
@@ -268,16 +268,16 @@ GOI_D SepFn sep_init(const SimplexCache& cache, const Proxy& pA, const Sweep& sA
 }
 
 GOI_D float sep_eval(const SepFn& f, const Proxy& pA, const Sweep& sA, const Proxy& pB, const Sweep& sB, int iA,
-                     int iB, float t) {
-    const Xf xA = sweep_xf(sA, t), xB = sweep_xf(sB, t);
+                     int iB, float t, RotMemo& ma, RotMemo& mb) {
+    const Xf xA = sweep_xf(sA, t, ma), xB = sweep_xf(sB, t, mb);
     if (f.type == kSepPoints) return dot(mul(xB, pB.v[iB]) - mul(xA, pA.v[iA]), f.axis);
     if (f.type == kSepFaceA) return dot(mul(xB, pB.v[iB]) - mul(xA, f.lp), mul(xA.q, f.axis));
     return dot(mul(xA, pA.v[iA]) - mul(xB, f.lp), mul(xB.q, f.axis));
 }
 
 GOI_D float sep_find_min(const SepFn& f, const Proxy& pA, const Sweep& sA, const Proxy& pB, const Sweep& sB, int& iA,
-                         int& iB, float t) {
-    const Xf xA = sweep_xf(sA, t), xB = sweep_xf(sB, t);
+                         int& iB, float t, RotMemo& ma, RotMemo& mb) {
+    const Xf xA = sweep_xf(sA, t, ma), xB = sweep_xf(sB, t, mb);
     if (f.type == kSepPoints) {
         iA = support(pA, mulT(xA.q, f.axis));
         iB = support(pB, mulT(xB.q, -f.axis));
@@ -318,26 +318,27 @@ GOI_D int time_of_impact(const Proxy& pA, Sweep sA, const Proxy& pB, Sweep sB, f
     cache.metric = 0.0f;
     int state = kToiUnknown;
     t_out = 1.0f;
+    RotMemo ma, mb;
     for (int iter = 0;;) {
-        const float dist = gjk_distance(cache, pA, sweep_xf(sA, t1), pB, sweep_xf(sB, t1));
+        const float dist = gjk_distance(cache, pA, sweep_xf(sA, t1, ma), pB, sweep_xf(sB, t1, mb));
         if (dist <= 0.0f) { state = kToiOverlapped; t_out = 0.0f; break; }
         if (dist < target + tol) { state = kToiTouching; t_out = t1; break; }
-        const SepFn f = sep_init(cache, pA, sA, pB, sB, t1);
+        const SepFn f = sep_init(cache, pA, sA, pB, sB, t1, ma, mb);
         bool done = false;
         float t2 = 1.0f;
         for (int push = 0;;) {
             int iA, iB;
-            float s2 = sep_find_min(f, pA, sA, pB, sB, iA, iB, t2);
+            float s2 = sep_find_min(f, pA, sA, pB, sB, iA, iB, t2, ma, mb);
             if (s2 > target + tol) { state = kToiSeparated; t_out = 1.0f; done = true; break; }
             if (s2 > target - tol) { t1 = t2; break; }
-            float s1 = sep_eval(f, pA, sA, pB, sB, iA, iB, t1);
+            float s1 = sep_eval(f, pA, sA, pB, sB, iA, iB, t1, ma, mb);
             if (s1 < target - tol) { state = kToiFailed; t_out = t1; done = true; break; }
             if (s1 <= target + tol) { state = kToiTouching; t_out = t1; done = true; break; }
             float a1 = t1, a2 = t2;
             for (int rc = 0;;) {
                 const float t = (rc & 1) ? a1 + (target - s1) * (a2 - a1) / (s2 - s1) : 0.5f * (a1 + a2);
                 ++rc;
-                const float s = sep_eval(f, pA, sA, pB, sB, iA, iB, t);
+                const float s = sep_eval(f, pA, sA, pB, sB, iA, iB, t, ma, mb);
                 if (babs(s - target) < tol) { t2 = t; break; }
                 if (s > target) { a1 = t; s1 = s; }
                 else { a2 = t; s2 = s; }

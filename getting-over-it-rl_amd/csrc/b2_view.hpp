@@ -203,51 +203,184 @@ struct World {
             if (t == GOI_DYNAMIC) dmask |= 1ull << b;
         }
     }
-    // the mirrored leaves from the State into the workspace (contact metadata, awake flags)
-    GOI_D void load_mirror(const DModel& m) const {
-        for (int c = 0; c < C; ++c) {
-            pair(c) = i32(GOI_C_PAIR, c);
-            key(c) = i32(GOI_C_KEY, c);
-            const int a = i32(GOI_C_FA, c), b = i32(GOI_C_FB, c);
-            fa(c) = a;
-            fb(c) = b;
-            wi(k.o_cmeta, c) = (u8(GOI_C_TOUCHING, c) ? 1 : 0) | (i32(GOI_C_COUNT, c) << 8);
-            if (pair(c) >= 0) set_bodies(c, m.fixture_body[a], m.fixture_body[b]);
-        }
-        for (int b = 0; b < B; ++b) {
-            awake(b) = u8(GOI_B_AWAKE, b);
-            active(b) = u8(GOI_B_ACTIVE, b);
-        }
-        for (int l = 0; l < 13; ++l) {
-            const int leaf = kBodyMirrorLeaves[l], n = kBodyMirrorWidth[l] * B;
-            float* dst = &wf(k.o_bm + body_mirror_coef(leaf) * B, 0);
-            for (int i = 0; i < n; ++i) dst[i * S] = at<float>(leaf, i);
-        }
-    }
-    GOI_D void store_mirror() const {
-        for (int c = 0; c < C; ++c) {
-            i32(GOI_C_PAIR, c) = pair(c);
-            i32(GOI_C_KEY, c) = key(c);
-            i32(GOI_C_FA, c) = fa(c);
-            i32(GOI_C_FB, c) = fb(c);
-        }
-        for (int b = 0; b < B; ++b) u8(GOI_B_AWAKE, b) = (uint8_t)awake(b);
-        for (int l = 0; l < kBodyMirrorMutable; ++l) {
-            const int leaf = kBodyMirrorLeaves[l], n = kBodyMirrorWidth[l] * B;
-            const float* src = &wf(k.o_bm + body_mirror_coef(leaf) * B, 0);
-            for (int i = 0; i < n; ++i) at<float>(leaf, i) = src[i * S];
-        }
-    }
-    // the TOI bookkeeping (written by SolveTOI only)
-    GOI_D void store_toi() const {
-        for (int c = 0; c < C; ++c) {
-            u8(GOI_T_FLAG, c) = (uint8_t)tflag(c);
-            u8(GOI_T_ENABLED, c) = (uint8_t)ten(c);
-            i32(GOI_T_COUNT, c) = tcount(c);
-            f(GOI_T_TOI, c) = ttoi(c);
-        }
-    }
 };
+
+// ---- block-cooperative copies between the State and the block's workspaces
+//
+// The per-world phases leave most lanes of a block idle, and a lane copying its own world's mirror would pay one
+// memory round trip per element. Instead every lane of the block copies: lane l serves world j = l % S at rows r0 =
+// l / S, r0 + stride, ... (stride = lanes / S), so one load or store instruction moves `stride` rows of every world,
+// and each batch issues all its loads before the first use. A lane whose world lies beyond the batch stays idle.
+struct BlockCopy {
+    void* const* lv;   // the State's leaf base pointers
+    int pitch, B, C, S;
+    Workspace k;
+    int* lds;          // the block's workspace base (world 0, word 0)
+    int w, j, r0, stride;
+    bool on;           // this lane copies for world w (= the block's world j)
+
+    template <typename T>
+    GOI_D T& at(int leaf, int i) const { return reinterpret_cast<T*>(lv[leaf])[(size_t)i * pitch + w]; }
+    GOI_D int& wi(int off) const { return lds[off * S + j]; }
+    GOI_D float& wf(int off) const { return reinterpret_cast<float*>(lds)[off * S + j]; }
+};
+
+// lanes: the block's lanes taking part (the whole block on the device, 1 for a sequential host build)
+GOI_HD BlockCopy block_copy(void* const* lv, int pitch, int n, int B, int C, int J, int R, int S, int* lds, int w0,
+                            int lane, int lanes) {
+    BlockCopy bc;
+    bc.lv = lv; bc.pitch = pitch; bc.B = B; bc.C = C; bc.S = S;
+    bc.k = Workspace::layout(B, C, J, R);
+    bc.lds = lds;
+    bc.stride = lanes / S > 0 ? lanes / S : 1;
+    bc.j = lane % S;
+    bc.r0 = lane / S;
+    bc.w = w0 + bc.j;
+    bc.on = bc.r0 < bc.stride && bc.w < n;
+    return bc;
+}
+
+constexpr int kCopyU = 4;  // rows per lane and leaf in one batch
+
+// The mirrored leaves of the block's worlds into their workspaces (contact metadata, awake and active flags, the
+// mirrored float body leaves, the bodies of every live slot). Called by every lane of the block.
+GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
+    const Workspace& k = bc.k;
+    if (bc.on) {
+        for (int c0 = bc.r0; c0 < bc.C; c0 += kCopyU * bc.stride) {
+            int p[kCopyU], ky[kCopyU], fa[kCopyU], fb[kCopyU], n[kCopyU];
+            uint8_t t[kCopyU];
+#pragma unroll
+            for (int u = 0; u < kCopyU; ++u) {
+                const int c = min(c0 + u * bc.stride, bc.C - 1);
+                p[u] = bc.at<int>(GOI_C_PAIR, c);
+                ky[u] = bc.at<int>(GOI_C_KEY, c);
+                fa[u] = bc.at<int>(GOI_C_FA, c);
+                fb[u] = bc.at<int>(GOI_C_FB, c);
+                t[u] = bc.at<uint8_t>(GOI_C_TOUCHING, c);
+                n[u] = bc.at<int>(GOI_C_COUNT, c);
+            }
+#pragma unroll
+            for (int u = 0; u < kCopyU; ++u) {
+                const int c = c0 + u * bc.stride;
+                if (c < bc.C) {
+                    bc.wi(k.o_pair + c) = p[u];
+                    bc.wi(k.o_key + c) = ky[u];
+                    bc.wi(k.o_fa + c) = fa[u];
+                    bc.wi(k.o_fb + c) = fb[u];
+                    bc.wi(k.o_cmeta + c) = (t[u] ? 1 : 0) | (n[u] << 8);
+                }
+            }
+        }
+        // the float body leaves: rows i < width * B of each, at word coef * B + i
+        for (int i0 = bc.r0; i0 < 2 * bc.B; i0 += 2 * bc.stride) {
+            float v[13][2];
+            uint8_t aw[2], ac[2];
+#pragma unroll
+            for (int l = 0; l < 13; ++l) {
+                const int rows = kBodyMirrorWidth[l] * bc.B;
+#pragma unroll
+                for (int u = 0; u < 2; ++u) v[l][u] = bc.at<float>(kBodyMirrorLeaves[l], min(i0 + u * bc.stride, rows - 1));
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int b = min(i0 + u * bc.stride, bc.B - 1);
+                aw[u] = bc.at<uint8_t>(GOI_B_AWAKE, b);
+                ac[u] = bc.at<uint8_t>(GOI_B_ACTIVE, b);
+            }
+#pragma unroll
+            for (int l = 0; l < 13; ++l) {
+                const int rows = kBodyMirrorWidth[l] * bc.B, off = k.o_bm + body_mirror_coef(kBodyMirrorLeaves[l]) * bc.B;
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int i = i0 + u * bc.stride;
+                    if (i < rows) bc.wf(off + i) = v[l][u];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int b = i0 + u * bc.stride;
+                if (b < bc.B) {
+                    bc.wi(k.o_awake + b) = aw[u];
+                    bc.wi(k.o_active + b) = ac[u];
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // the bodies of each live slot's fixtures
+    if (bc.on) {
+        for (int c0 = bc.r0; c0 < bc.C; c0 += kCopyU * bc.stride) {
+            int ba[kCopyU], bb[kCopyU];
+            bool live[kCopyU];
+#pragma unroll
+            for (int u = 0; u < kCopyU; ++u) {
+                const int c = c0 + u * bc.stride, cc = min(c, bc.C - 1);
+                live[u] = c < bc.C && bc.wi(k.o_pair + cc) >= 0;
+                ba[u] = m.fixture_body[live[u] ? bc.wi(k.o_fa + cc) : 0];
+                bb[u] = m.fixture_body[live[u] ? bc.wi(k.o_fb + cc) : 0];
+            }
+#pragma unroll
+            for (int u = 0; u < kCopyU; ++u)
+                if (live[u]) bc.wi(k.o_bab + c0 + u * bc.stride) = ba[u] | (bb[u] << 8);
+        }
+    }
+    __syncthreads();
+}
+
+// The workspaces' mutable mirrored leaves back into the State (contact metadata, awake flags, the first
+// kBodyMirrorMutable float body leaves). Called by every lane of the block after the worlds' last writes.
+GOI_D void store_mirror_block(const BlockCopy& bc) {
+    __syncthreads();
+    if (!bc.on) return;
+    const Workspace& k = bc.k;
+    for (int c = bc.r0; c < bc.C; c += bc.stride) {
+        bc.at<int>(GOI_C_PAIR, c) = bc.wi(k.o_pair + c);
+        bc.at<int>(GOI_C_KEY, c) = bc.wi(k.o_key + c);
+        bc.at<int>(GOI_C_FA, c) = bc.wi(k.o_fa + c);
+        bc.at<int>(GOI_C_FB, c) = bc.wi(k.o_fb + c);
+    }
+    for (int b = bc.r0; b < bc.B; b += bc.stride) bc.at<uint8_t>(GOI_B_AWAKE, b) = (uint8_t)bc.wi(k.o_awake + b);
+#pragma unroll
+    for (int l = 0; l < kBodyMirrorMutable; ++l) {
+        const int rows = kBodyMirrorWidth[l] * bc.B, off = k.o_bm + body_mirror_coef(kBodyMirrorLeaves[l]) * bc.B;
+        for (int i = bc.r0; i < rows; i += bc.stride) bc.at<float>(kBodyMirrorLeaves[l], i) = bc.wf(off + i);
+    }
+}
+
+// SolveTOI's reset (world.py:157-161, toi.py:837) of the block's worlds: alpha0 = 0, count 0, toi 1, flag off,
+// enabled, not solved, report impulses 0. Called by every lane; ends with a barrier.
+GOI_D void reset_toi_block(const BlockCopy& bc) {
+    if (bc.on) {
+        const Workspace& k = bc.k;
+        const int oa = k.o_bm + body_mirror_coef(GOI_T_ALPHA0) * bc.B;
+        for (int b = bc.r0; b < bc.B; b += bc.stride) bc.wf(oa + b) = 0.0f;
+        for (int c = bc.r0; c < bc.C; c += bc.stride) {
+            bc.wi(k.o_tmeta + c) = 2;  // count 0, enabled, no flag
+            bc.wf(k.o_ttoi + c) = 1.0f;
+            bc.at<uint8_t>(GOI_T_SOLVED, c) = 0;
+        }
+        for (int i = bc.r0; i < 2 * bc.C; i += bc.stride) {
+            bc.at<float>(GOI_T_NORMAL_IMPULSE, i) = 0.0f;
+            bc.at<float>(GOI_T_TANGENT_IMPULSE, i) = 0.0f;
+        }
+    }
+    __syncthreads();
+}
+
+// The TOI bookkeeping of the block's worlds into the State. Called by every lane after SolveTOI.
+GOI_D void store_toi_block(const BlockCopy& bc) {
+    __syncthreads();
+    if (!bc.on) return;
+    const Workspace& k = bc.k;
+    for (int c = bc.r0; c < bc.C; c += bc.stride) {
+        const int t = bc.wi(k.o_tmeta + c);
+        bc.at<uint8_t>(GOI_T_FLAG, c) = (uint8_t)(t & 1);
+        bc.at<uint8_t>(GOI_T_ENABLED, c) = (uint8_t)((t >> 1) & 1);
+        bc.at<int>(GOI_T_COUNT, c) = (t >> 8) & 0xff;
+        bc.at<float>(GOI_T_TOI, c) = bc.wf(k.o_ttoi + c);
+    }
+}
 
 // Fat AABB of a fixture in the compact layout: the world's own row, or the Model's shared static box.
 GOI_D float4 fat_of(const DModel& m, const World& W, int fixture) {

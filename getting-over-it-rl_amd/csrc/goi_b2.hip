@@ -135,14 +135,15 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
     const int w0 = xcd_group() * L.wpw;
     const bool valid = lane < L.wpw && w0 + lane < L.n;
     const World W = make_world(m, L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
+    const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
+    load_mirror_block(m, bc);
     if (valid) {
-        W.load_mirror(m);
         build_order(W);
         if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
         W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     }
     if (!start_only) collide_block(m, block_coop(L, W, lds, w0), W, valid, L.s);
-    if (valid) W.store_mirror();
+    store_mirror_block(bc);
 }
 
 // The whole b2World::Step (step.py:28-47) of one world per lane: FindNewContacts where new_fixture, Collide,
@@ -161,24 +162,26 @@ __global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) {
     bd.B = L.B;
     bd.st = W.S;
     const Rows CR = contact_rows(L, W.w);
+    const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
+    load_mirror_block(m, bc);
     if (valid) {
-        W.load_mirror(m);
         build_order(W);
         if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
         W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     }
     collide_block(m, co, W, valid, L.s);
     if (valid) solve_world(m, W, bd, CR, joint_rows(L, W.w), L.s, L.dt, L.dbg);
-    if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, co);
-    if (!valid) return;
-    const float dt = L.dt;
-    if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
-    if (L.s.auto_clear_forces)
-        for (int b = 0; b < W.B; ++b) {
-            W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
-            W.f(GOI_B_TORQUE, b) = 0.0f;
-        }
-    W.store_mirror();
+    if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, co, bc);
+    if (valid) {
+        const float dt = L.dt;
+        if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
+        if (L.s.auto_clear_forces)
+            for (int b = 0; b < W.B; ++b) {
+                W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
+                W.f(GOI_B_TORQUE, b) = 0.0f;
+            }
+    }
+    store_mirror_block(bc);
 }
 
 __global__ void k_sincos(const float* x, float* s, float* c, int n) {
