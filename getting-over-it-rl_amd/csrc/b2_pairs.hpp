@@ -10,20 +10,8 @@ namespace goi {
 constexpr int kMaxC = 64;
 
 // The contact list (Box2D's m_contactList: newest first = descending key, pairs.py:12-13) is kept in the
-// workspace as W.order(0 .. nlive-1). build_order ranks the live slots once per step; Collide's destructions and
-// FindNewContacts' creations then update it in place (see collide_walk, find_new_contacts).
-GOI_D void build_order(const World& W) {
-    int n = 0;
-    for (int k = 0; k < W.C; ++k) {
-        if (W.pair(k) < 0) continue;
-        const int key = W.key(k);
-        int rank = 0;
-        for (int j = 0; j < W.C; ++j) rank += (W.pair(j) >= 0 && W.key(j) > key) ? 1 : 0;
-        W.order(rank) = k;
-        ++n;
-    }
-    W.nlive() = n;
-}
+// workspace as W.order(0 .. nlive-1). build_order_block ranks the live slots once per step; Collide's destructions
+// and FindNewContacts' creations then update it in place (see collide_walk, find_new_contacts).
 
 // Live slots in contact-list order: W.order(0 .. n-1); returns n.
 GOI_D int list_order(const World& W) { return W.nlive(); }

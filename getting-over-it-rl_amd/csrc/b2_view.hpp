@@ -328,6 +328,30 @@ GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
     __syncthreads();
 }
 
+// Box2D's contact list of the block's worlds (newest first = descending key, pairs.py:12-13) into each workspace's
+// order(0 .. nlive-1): each live slot's position is the number of live slots with a larger key (keys of live slots
+// are distinct). Every lane ranks its rows of its world. Called by every lane after load_mirror_block.
+GOI_D void build_order_block(const BlockCopy& bc) {
+    const Workspace& k = bc.k;
+    if (bc.on) {
+        for (int c = bc.r0; c < bc.C; c += bc.stride) {
+            if (bc.wi(k.o_pair + c) < 0) continue;
+            const int key = bc.wi(k.o_key + c);
+            int rank = 0;
+#pragma unroll 8
+            for (int i = 0; i < bc.C; ++i) rank += (bc.wi(k.o_pair + i) >= 0 && bc.wi(k.o_key + i) > key) ? 1 : 0;
+            bc.wi(k.o_order + rank) = c;
+        }
+        if (bc.r0 == 0) {
+            int n = 0;
+#pragma unroll 8
+            for (int i = 0; i < bc.C; ++i) n += bc.wi(k.o_pair + i) >= 0 ? 1 : 0;
+            bc.wi(k.o_nlive) = n;
+        }
+    }
+    __syncthreads();
+}
+
 // The workspaces' mutable mirrored leaves back into the State (contact metadata, awake flags, the first
 // kBodyMirrorMutable float body leaves). Called by every lane of the block after the worlds' last writes.
 GOI_D void store_mirror_block(const BlockCopy& bc) {

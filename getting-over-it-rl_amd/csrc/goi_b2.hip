@@ -137,8 +137,8 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
     const World W = make_world(m, L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
     const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
     load_mirror_block(m, bc);
+    build_order_block(bc);
     if (valid) {
-        build_order(W);
         if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
         W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     }
@@ -164,8 +164,8 @@ __global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) {
     const Rows CR = contact_rows(L, W.w);
     const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
     load_mirror_block(m, bc);
+    build_order_block(bc);
     if (valid) {
-        build_order(W);
         if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
         W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     }
