@@ -77,14 +77,25 @@ GOI_D void restore(const World& W, int b, const SweepBackup& k) {
 
 // ---------------------------------------------------------------- distance proxies and GJK (toi.py:116-294)
 
+// b2DistanceProxy held in registers: the fixture's 8 vertex slots are loaded once, in one batch (the slots past
+// `count` are padding and never selected), so GJK's support searches and vertex lookups stay off memory.
 struct Proxy {
-    const V2* v;
+    V2 v[kPoly];
     int count;
     float radius;
+    // vertex i (0 <= i < count) without dynamic register indexing
+    GOI_D V2 at(int i) const {
+        V2 r = v[0];
+#pragma unroll
+        for (int j = 1; j < kPoly; ++j)
+            if (i == j) r = v[j];
+        return r;
+    }
 };
 GOI_D Proxy proxy_of(const DModel& m, int f) {
     Proxy p;
-    p.v = m.verts + f * kPoly;
+#pragma unroll
+    for (int j = 0; j < kPoly; ++j) p.v[j] = m.verts[f * kPoly + j];
     p.count = m.count[f];
     p.radius = m.radius[f];
     return p;
@@ -93,9 +104,10 @@ GOI_D Proxy proxy_of(const DModel& m, int f) {
 GOI_D int support(const Proxy& p, V2 d) {
     int best = 0;
     float bv = dot(p.v[0], d);
-    for (int i = 1; i < p.count; ++i) {
+#pragma unroll
+    for (int i = 1; i < kPoly; ++i) {
         const float v = dot(p.v[i], d);
-        if (v > bv) {
+        if (i < p.count && v > bv) {
             best = i;
             bv = v;
         }
@@ -123,8 +135,8 @@ GOI_D float metric(const SVert* v, int count) {
 GOI_D void set_vertex(SVert& v, const Proxy& pA, const Xf& xA, int iA, const Proxy& pB, const Xf& xB, int iB) {
     v.iA = iA;
     v.iB = iB;
-    v.wA = mul(xA, pA.v[iA]);
-    v.wB = mul(xB, pB.v[iB]);
+    v.wA = mul(xA, pA.at(iA));
+    v.wB = mul(xB, pB.at(iB));
     v.w = v.wB - v.wA;
 }
 
@@ -245,24 +257,24 @@ GOI_D SepFn sep_init(const SimplexCache& cache, const Proxy& pA, const Sweep& sA
     f.lp = mk(0.0f, 0.0f);
     if (cache.count == 1) {
         f.type = kSepPoints;
-        f.axis = mul(xB, pB.v[cache.iB[0]]) - mul(xA, pA.v[cache.iA[0]]);
+        f.axis = mul(xB, pB.at(cache.iB[0])) - mul(xA, pA.at(cache.iA[0]));
         normalize(f.axis);
     } else if (cache.iA[0] == cache.iA[1]) {
         f.type = kSepFaceB;
-        const V2 b1 = pB.v[cache.iB[0]], b2 = pB.v[cache.iB[1]];
+        const V2 b1 = pB.at(cache.iB[0]), b2 = pB.at(cache.iB[1]);
         f.axis = cross(b2 - b1, 1.0f);
         normalize(f.axis);
         const V2 n = mul(xB.q, f.axis);
         f.lp = 0.5f * (b1 + b2);
-        if (dot(mul(xA, pA.v[cache.iA[0]]) - mul(xB, f.lp), n) < 0.0f) f.axis = -f.axis;
+        if (dot(mul(xA, pA.at(cache.iA[0])) - mul(xB, f.lp), n) < 0.0f) f.axis = -f.axis;
     } else {
         f.type = kSepFaceA;
-        const V2 a1 = pA.v[cache.iA[0]], a2 = pA.v[cache.iA[1]];
+        const V2 a1 = pA.at(cache.iA[0]), a2 = pA.at(cache.iA[1]);
         f.axis = cross(a2 - a1, 1.0f);
         normalize(f.axis);
         const V2 n = mul(xA.q, f.axis);
         f.lp = 0.5f * (a1 + a2);
-        if (dot(mul(xB, pB.v[cache.iB[0]]) - mul(xA, f.lp), n) < 0.0f) f.axis = -f.axis;
+        if (dot(mul(xB, pB.at(cache.iB[0])) - mul(xA, f.lp), n) < 0.0f) f.axis = -f.axis;
     }
     return f;
 }
@@ -270,9 +282,9 @@ GOI_D SepFn sep_init(const SimplexCache& cache, const Proxy& pA, const Sweep& sA
 GOI_D float sep_eval(const SepFn& f, const Proxy& pA, const Sweep& sA, const Proxy& pB, const Sweep& sB, int iA,
                      int iB, float t, RotMemo& ma, RotMemo& mb) {
     const Xf xA = sweep_xf(sA, t, ma), xB = sweep_xf(sB, t, mb);
-    if (f.type == kSepPoints) return dot(mul(xB, pB.v[iB]) - mul(xA, pA.v[iA]), f.axis);
-    if (f.type == kSepFaceA) return dot(mul(xB, pB.v[iB]) - mul(xA, f.lp), mul(xA.q, f.axis));
-    return dot(mul(xA, pA.v[iA]) - mul(xB, f.lp), mul(xB.q, f.axis));
+    if (f.type == kSepPoints) return dot(mul(xB, pB.at(iB)) - mul(xA, pA.at(iA)), f.axis);
+    if (f.type == kSepFaceA) return dot(mul(xB, pB.at(iB)) - mul(xA, f.lp), mul(xA.q, f.axis));
+    return dot(mul(xA, pA.at(iA)) - mul(xB, f.lp), mul(xB.q, f.axis));
 }
 
 GOI_D float sep_find_min(const SepFn& f, const Proxy& pA, const Sweep& sA, const Proxy& pB, const Sweep& sB, int& iA,
@@ -281,18 +293,18 @@ GOI_D float sep_find_min(const SepFn& f, const Proxy& pA, const Sweep& sA, const
     if (f.type == kSepPoints) {
         iA = support(pA, mulT(xA.q, f.axis));
         iB = support(pB, mulT(xB.q, -f.axis));
-        return dot(mul(xB, pB.v[iB]) - mul(xA, pA.v[iA]), f.axis);
+        return dot(mul(xB, pB.at(iB)) - mul(xA, pA.at(iA)), f.axis);
     }
     if (f.type == kSepFaceA) {
         const V2 n = mul(xA.q, f.axis);
         iA = -1;
         iB = support(pB, mulT(xB.q, -n));
-        return dot(mul(xB, pB.v[iB]) - mul(xA, f.lp), n);
+        return dot(mul(xB, pB.at(iB)) - mul(xA, f.lp), n);
     }
     const V2 n = mul(xB.q, f.axis);
     iB = -1;
     iA = support(pA, mulT(xA.q, -n));
-    return dot(mul(xA, pA.v[iA]) - mul(xB, f.lp), n);
+    return dot(mul(xA, pA.at(iA)) - mul(xB, f.lp), n);
 }
 
 enum { kToiUnknown = 0, kToiFailed = 1, kToiOverlapped = 2, kToiTouching = 3, kToiSeparated = 4 };
