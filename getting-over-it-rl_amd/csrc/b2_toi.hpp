@@ -180,7 +180,9 @@ GOI_D void simplex_solve3(SVert* v, int& count) {
     count = 3;
 }
 
-// b2Distance (useRadii = false): the distance and the updated simplex cache
+// b2Distance (useRadii = false): the distance and the updated simplex cache. The simplex, the saved indices and
+// the cache are indexed only by constants once the short loops are unrolled, so they stay in registers (a runtime
+// index would put them in private scratch memory, one memory round trip per access).
 GOI_D float gjk_distance(SimplexCache& cache, const Proxy& pA, const Xf& xA, const Proxy& pB, const Xf& xB) {
     SVert v[3];
 #pragma unroll
@@ -190,7 +192,9 @@ GOI_D float gjk_distance(SimplexCache& cache, const Proxy& pA, const Xf& xA, con
         v[i].wA = mk(0.0f, 0.0f); v[i].wB = v[i].wA; v[i].w = v[i].wA;
     }
     int count = cache.count;
-    for (int i = 0; i < count; ++i) set_vertex(v[i], pA, xA, cache.iA[i], pB, xB, cache.iB[i]);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        if (i < count) set_vertex(v[i], pA, xA, cache.iA[i], pB, xB, cache.iB[i]);
     if (count > 1) {
         const float m1 = cache.metric, m2 = metric(v, count);
         if (m2 < 0.5f * m1 || 2.0f * m1 < m2 || m2 < kEps) count = 0;
@@ -203,7 +207,9 @@ GOI_D float gjk_distance(SimplexCache& cache, const Proxy& pA, const Xf& xA, con
     int saveA[3], saveB[3];
     for (int iter = 0; iter < 20;) {
         const int save = count;
-        for (int i = 0; i < save; ++i) { saveA[i] = v[i].iA; saveB[i] = v[i].iB; }
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+            if (i < save) { saveA[i] = v[i].iA; saveB[i] = v[i].iB; }
         if (count == 2) simplex_solve2(v, count);
         else if (count == 3) simplex_solve3(v, count);
         if (count == 3) break;
@@ -215,13 +221,17 @@ GOI_D float gjk_distance(SimplexCache& cache, const Proxy& pA, const Xf& xA, con
             d = cross(e12, -v[0].w) > 0.0f ? cross(1.0f, e12) : cross(e12, 1.0f);
         }
         if (dot(d, d) < kEps * kEps) break;
-        SVert& nv = v[count];
-        const float keep_a = nv.a;  // the new vertex's barycentric coordinate is left as it was
+        // the new vertex takes slot `count` (1 or 2); its barycentric coordinate is left as it was
+        SVert nv;
         set_vertex(nv, pA, xA, support(pA, mulT(xA.q, -d)), pB, xB, support(pB, mulT(xB.q, d)));
-        nv.a = keep_a;
+        nv.a = count == 1 ? v[1].a : v[2].a;
+        if (count == 1) v[1] = nv;
+        else v[2] = nv;
         ++iter;
         bool dup = false;
-        for (int i = 0; i < save; ++i) dup |= (nv.iA == saveA[i] && nv.iB == saveB[i]);
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+            if (i < save) dup |= (nv.iA == saveA[i] && nv.iB == saveB[i]);
         if (dup) break;
         ++count;
     }
@@ -238,7 +248,9 @@ GOI_D float gjk_distance(SimplexCache& cache, const Proxy& pA, const Xf& xA, con
     }
     cache.metric = metric(v, count);
     cache.count = count;
-    for (int i = 0; i < count; ++i) { cache.iA[i] = v[i].iA; cache.iB[i] = v[i].iB; }
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        if (i < count) { cache.iA[i] = v[i].iA; cache.iB[i] = v[i].iB; }
     return length(pa - pb);
 }
 
