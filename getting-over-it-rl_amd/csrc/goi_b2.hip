@@ -149,7 +149,7 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
 // The whole b2World::Step (step.py:28-47) of one world per lane: FindNewContacts where new_fixture, Collide,
 // Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to share the block's manifold and TOI work.
 // At most 256 registers (two waves per SIMD): the second wave hides the latency chains of the first.
-__global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) {
+__device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     extern __shared__ int lds[];
     stage_nodes(m, L, lds);
     const int lane = threadIdx.x;
@@ -183,6 +183,19 @@ __global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) {
     }
     store_mirror_block(bc);
 }
+
+__global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) { step_block(m, L); }
+
+// The same step with the world dimensions and the worlds per wave fixed at compile time (the 4-body rig with 32
+// contact slots, 8 worlds per wave): every workspace offset and loop bound folds into the instructions, which
+// frees the scalar registers the runtime dimensions hold. The results are those of k_step.
+template <int kB, int kC, int kJ, int kR, int kS>
+__global__ void __launch_bounds__(kBlock, 2) k_step_fixed(DModel m, Launch L) {
+    L.B = kB; L.C = kC; L.J = kJ; L.R = kR; L.wpw = kS;
+    m.B = kB; m.J = kJ; m.R = kR;
+    step_block(m, L);
+}
+constexpr int kRigB = 5, kRigC = 32, kRigJ = 3, kRigR = 4, kRigS = 8;
 
 __global__ void k_sincos(const float* x, float* s, float* c, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -561,7 +574,11 @@ int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSett
     if (debug) L.dbg = *debug;
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
     const size_t lds = block_lds_bytes(L);
-    hipLaunchKernelGGL(k_step, dim3(grid), dim3(kBlock), lds, st, M->d, L);
+    if (L.B == kRigB && L.C == kRigC && L.J == kRigJ && L.R == kRigR && L.wpw == kRigS && M->d.B == kRigB &&
+        M->d.J == kRigJ && M->d.R == kRigR)
+        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS>), dim3(grid), dim3(kBlock), lds, st, M->d, L);
+    else
+        hipLaunchKernelGGL(k_step, dim3(grid), dim3(kBlock), lds, st, M->d, L);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
 }

@@ -190,7 +190,19 @@ def test_new_fixture_forces_full_search(oracle):
     assert (np.asarray(ref.contacts.pair) >= 0).sum() > live.sum() - drop.sum()  # the search re-created contacts
 
 
-@pytest.mark.parametrize("wpw", [1, 2, 4, 32, 64])
+@pytest.mark.parametrize("edges", ["quad", "native"])
+def test_rig_kernel_parity(oracle, monkeypatch, edges):
+    """The step instance compiled for the rig's dimensions (5 bodies, 32 slots, 3 joints, 4 rows, 8 worlds per
+    wavefront), which the launch picks for the benchmark workload: config 4, 1024 worlds, 40 steps with actions."""
+    monkeypatch.setenv("GOI_WORLDS_PER_WAVE", "8")
+    s, m, st, cfg = b2.scenes.make_config(4, 1024, edges=edges)
+    assert wd.dims(st) == (5, 4, 3, 32)
+    rng = np.random.default_rng(22)
+    ref = _run(m, st, s, cfg.dt, 40, oracle, [b2.scenes.actions(rng, 1024) for _ in range(40)])
+    assert int(np.asarray(ref.toi.events).sum()) > 0
+
+
+@pytest.mark.parametrize("wpw", [1, 2, 4, 8, 32, 64])
 def test_worlds_per_wave_variants(oracle, monkeypatch, wpw):
     """The block-cooperative passes (manifolds, TOIs) for other world counts per wavefront than the default (the
     library reads GOI_WORLDS_PER_WAVE at every call): config 4, 256 worlds, 10 steps with actions, bit for bit."""
