@@ -165,9 +165,11 @@ struct World {
         return make_float4(wf(k.o_qbox, 4 * r), wf(k.o_qbox, 4 * r + 1), wf(k.o_qbox, 4 * r + 2), wf(k.o_qbox, 4 * r + 3));
     }
 
+    // element (i, w) of a leaf; the element offset fits 32 bits (checked at launch), so the address is the leaf's
+    // base plus one 32-bit product and sum
     template <typename T>
     GOI_D T& at(int leaf, int i) const {
-        return reinterpret_cast<T*>(lv[leaf])[(size_t)i * pitch + w];
+        return reinterpret_cast<T*>(lv[leaf])[(uint32_t)i * (uint32_t)pitch + (uint32_t)w];
     }
     GOI_D float& f(int leaf, int i) const {
         const int c = body_mirror_coef(leaf);  // a constant at every call site
@@ -220,7 +222,9 @@ struct BlockCopy {
     bool on;           // this lane copies for world w (= the block's world j)
 
     template <typename T>
-    GOI_D T& at(int leaf, int i) const { return reinterpret_cast<T*>(lv[leaf])[(size_t)i * pitch + w]; }
+    GOI_D T& at(int leaf, int i) const {
+        return reinterpret_cast<T*>(lv[leaf])[(uint32_t)i * (uint32_t)pitch + (uint32_t)w];
+    }
     GOI_D int& wi(int off) const { return lds[off * S + j]; }
     GOI_D float& wf(int off) const { return reinterpret_cast<float*>(lds)[off * S + j]; }
 };
@@ -429,11 +433,14 @@ GOI_D bool overlap(float4 a, float4 b) {
     return !(d1x > 0.0f || d1y > 0.0f || d2x > 0.0f || d2y > 0.0f);
 }
 
-// Per-world HBM scratch rows: element (row, field) at base[((row * nf) + field) * pitch + w].
+// Per-world HBM scratch rows: element (row, field) at base[((row * nf) + field) * pitch + w], a 32-bit word offset
+// (checked at launch).
 struct Rows {
     uint32_t* base;
     int pitch, w, nf;
-    GOI_D uint32_t& u(int row, int field) const { return base[((size_t)row * nf + field) * pitch + w]; }
+    GOI_D uint32_t& u(int row, int field) const {
+        return base[((uint32_t)row * (uint32_t)nf + (uint32_t)field) * (uint32_t)pitch + (uint32_t)w];
+    }
     GOI_D float getf(int row, int field) const { return __uint_as_float(u(row, field)); }
     GOI_D void setf(int row, int field, float v) const { u(row, field) = __float_as_uint(v); }
     GOI_D int geti(int row, int field) const { return (int)u(row, field); }

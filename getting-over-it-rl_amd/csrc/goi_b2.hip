@@ -471,6 +471,11 @@ static int check_view(const GoiModel* M, const GoiStateView* v, const char* who)
         if (!v->leaf[i] && v->n_worlds > 0 && !empty)
             return fail(GOI_E_ARG, std::string(who) + ": null leaf pointer");
     }
+    // the kernels address leaf elements and scratch-row words with 32-bit offsets
+    const uint64_t per_world = std::max<uint64_t>({4ull * v->C, 4ull * v->R, 3ull * v->J, 2ull * v->B, 1ull});
+    const uint64_t row_words = (uint64_t)v->C * CF_N + (uint64_t)v->J * JF_N;
+    if (per_world * (uint64_t)v->pitch >= (1ull << 32) || row_words * (uint64_t)v->pitch >= (1ull << 32))
+        return fail(GOI_E_UNSUPPORTED, std::string(who) + ": pitch too large for 32-bit element offsets");
     return GOI_OK;
 }
 
