@@ -18,6 +18,10 @@ cores, over the same initial State and actions (warmup + timed steps), repeated 
 thread over the first 1,024 worlds.
 
 sleep_off: the same workload, initial State and actions with Settings.allow_sleep off, timed the same way.
+
+fused_substeps: the same worlds with one action held for --substeps physics sub-steps, each action's sub-steps one
+goi_step_n launch (the game's several physics steps per action). Not the headline `value`, whose actions change
+every step.
 """
 import argparse
 import dataclasses
@@ -114,6 +118,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum CPU time of the cpu_baseline sample")
     ap.add_argument("--sleep-off-steps", type=int, default=None,
                     help="timed steps of the same workload with allow_sleep off (default: --steps; 0 skips)")
+    ap.add_argument("--substeps", type=int, default=4,
+                    help="also time goi_step_n with this many physics sub-steps per action (0 or 1 skips)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run only a plain device copy of MIB MiB 10 times (the rocprofv3 FETCH_SIZE/WRITE_SIZE "
                          "calibration) and exit")
@@ -202,6 +208,29 @@ def main():
                      "steps": int(off_acts.shape[0]), "ms_per_step": t2 / off_acts.shape[0],
                      "kernel_ms": float(np.mean([a.elapsed_time(b) for a, b in ev2]))}
         del dev2
+
+    fused = None
+    if args.substeps > 1:
+        # the same workload with one action per `substeps` physics sub-steps, each action's sub-steps fused into one
+        # launch (goi_step_n: every block keeps its worlds in LDS across them and never waits for other blocks)
+        k = args.substeps
+        dev3 = b2.layout.to_device(state, "cuda")
+        sp3, tq3 = dev3.joints.motor_speed, dev3.joints.max_motor
+        scenes.apply_actions(sp3, tq3, acts[0])
+        b2.step_n_(model, dev3, settings, cfg.dt, k)
+        launches = max(1, args.steps // k)
+        torch.cuda.synchronize()
+        start.record()
+        for i in range(launches):
+            scenes.apply_actions(sp3, tq3, acts[(args.warmup + i) % acts.shape[0]])
+            b2.step_n_(model, dev3, settings, cfg.dt, k)
+        end.record()
+        torch.cuda.synchronize()
+        t3 = start.elapsed_time(end)
+        fused = {"substeps": k, "launches": launches, "value": n * launches * k / (t3 / 1e3), "unit": "world-steps/s",
+                 "ms_per_step": t3 / (launches * k),
+                 "workload": f"the same worlds with one action held for {k} physics sub-steps (goi_step_n)"}
+        del dev3
     workload = f"config{args.config}" + ("" if args.edges == "quad" else "_native_edges")
     traffic = traffic_from_profiles("k_step", workload)
 
@@ -235,6 +264,7 @@ def main():
                      "kernel_ms": kern_ms, "bytes_per_world_step": bpw},
         "cpu_baseline": cpu,
         "sleep_off": sleep_off,
+        "fused_substeps": fused,
         "toi_events_last_step": int(np.asarray(host.toi.events).sum()),
         "overflow": int(np.asarray(host.overflow).sum()),
         "finite": finite,

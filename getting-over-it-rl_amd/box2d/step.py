@@ -82,6 +82,24 @@ def step_(model, state, settings, dt, debug=None, stream=None):
     return state
 
 
+def step_n_(model, state, settings, dt, n, debug=None, stream=None):
+    """n consecutive steps of every world of a device State in one launch, in place: the same State as n calls of
+    step_ with the joint motor commands and forces left as they are (a caller's physics sub-steps per action).
+    Returns the same State."""
+    if getattr(settings, "solver", "hip") != "hip":
+        raise ValueError(f"Settings.solver={settings.solver!r}: this package steps on the GPU only ('hip')")
+    view = layout.state_view(state)
+    C = state.contacts.pair.shape[-1]
+    dev = state.contacts.pair.device
+    dm = device_model(model, C, dev, state)
+    cs = settings.to_c()
+    st = torch.cuda.current_stream(dev).cuda_stream if stream is None else stream
+    dbg = None if debug is None else ctypes.byref(debug)
+    _abi.check(dm.L.goi_step_n(dm.handle, ctypes.byref(view), ctypes.byref(cs), ctypes.c_float(np.float32(dt)),
+                               ctypes.c_int32(int(n)), ctypes.c_void_p(st), dbg), dm.L)
+    return state
+
+
 def step(model, state, settings, dt, axis_name=None):
     """b2World::Step (step.py:28-47) of a batched device State; returns a new State (the input is unchanged)."""
     del axis_name

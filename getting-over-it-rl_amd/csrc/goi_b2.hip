@@ -48,6 +48,7 @@ struct Launch {
     uint32_t* scratch;  // contact rows then joint rows
     GoiSettings s;
     float dt;
+    int n_steps;  // consecutive steps of every world in this launch (>= 1)
     GoiDebug dbg;
 };
 
@@ -149,6 +150,7 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
 // The whole b2World::Step (step.py:28-47) of one world per lane: FindNewContacts where new_fixture, Collide,
 // Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to share the block's manifold and TOI work.
 // At most 256 registers (two waves per SIMD): the second wave hides the latency chains of the first.
+template <bool kMulti>
 __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     extern __shared__ int lds[];
     stage_nodes(m, L, lds);
@@ -164,36 +166,44 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     const Rows CR = contact_rows(L, W.w);
     const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
     load_mirror_block(m, bc);
-    build_order_block(bc);
-    if (valid) {
-        if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
-        W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
-    }
-    collide_block(m, co, W, valid, L.s);
-    if (valid) solve_world(m, W, bd, CR, joint_rows(L, W.w), L.s, L.dt, L.dbg);
-    if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, co, bc);
-    if (valid) {
-        const float dt = L.dt;
-        if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
-        if (L.s.auto_clear_forces)
-            for (int b = 0; b < W.B; ++b) {
-                W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
-                W.f(GOI_B_TORQUE, b) = 0.0f;
-            }
+    // n_steps consecutive steps: the workspace mirror stays in LDS from one to the next (it is the State's current
+    // value; every access to a mirrored leaf inside a step goes through the workspace), so the block's worlds need
+    // neither a store nor a reload between steps, and the block never waits for other blocks' steps.
+    const int n_steps = kMulti ? L.n_steps : 1;  // the single-step instances carry no loop state
+    for (int step = 0; step < n_steps; ++step) {
+        if (step > 0) __syncthreads();  // the worlds' workspace writes of the previous step
+        build_order_block(bc);
+        if (valid) {
+            if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
+            W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
+        }
+        collide_block(m, co, W, valid, L.s);
+        if (valid) solve_world(m, W, bd, CR, joint_rows(L, W.w), L.s, L.dt, L.dbg);
+        if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, co, bc);
+        if (valid) {
+            const float dt = L.dt;
+            if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
+            if (L.s.auto_clear_forces)
+                for (int b = 0; b < W.B; ++b) {
+                    W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
+                    W.f(GOI_B_TORQUE, b) = 0.0f;
+                }
+        }
     }
     store_mirror_block(bc);
 }
 
-__global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) { step_block(m, L); }
+template <bool kMulti>
+__global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) { step_block<kMulti>(m, L); }
 
 // The same step with the world dimensions and the worlds per wave fixed at compile time (the 4-body rig with 32
 // contact slots, 8 worlds per wave): every workspace offset and loop bound folds into the instructions, which
 // frees the scalar registers the runtime dimensions hold. The results are those of k_step.
-template <int kB, int kC, int kJ, int kR, int kS>
+template <int kB, int kC, int kJ, int kR, int kS, bool kMulti>
 __global__ void __launch_bounds__(kBlock, 2) k_step_fixed(DModel m, Launch L) {
     L.B = kB; L.C = kC; L.J = kJ; L.R = kR; L.wpw = kS;
     m.B = kB; m.J = kJ; m.R = kR;
-    step_block(m, L);
+    step_block<kMulti>(m, L);
 }
 constexpr int kRigB = 5, kRigC = 32, kRigJ = 3, kRigR = 4, kRigS = 8;
 
@@ -527,6 +537,7 @@ static size_t block_lds_bytes(const Launch& L) {
 
 static void fill_launch(Launch& L, const GoiModel* M, const GoiStateView* v, const GoiSettings* s, float dt) {
     std::memcpy(L.leaf, v->leaf, sizeof(L.leaf));
+    L.n_steps = 1;
     L.n = v->n_worlds;
     L.pitch = v->pitch;
     L.B = v->B;
@@ -563,12 +574,18 @@ static int ensure_scratch(GoiModel* M, const GoiStateView* state) {
 
 int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
                  void* hip_stream, const GoiDebug* debug) {
+    return goi_step_n(model, state, settings, dt, 1, hip_stream, debug);
+}
+
+int32_t goi_step_n(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
+                   int32_t n_steps, void* hip_stream, const GoiDebug* debug) {
     int rc = check_view(model, state, "goi_step");
     if (rc != GOI_OK) return rc;
     if (!settings) return fail(GOI_E_ARG, "goi_step: null settings");
     if (settings->velocity_iterations < 0 || settings->position_iterations < 0)
         return fail(GOI_E_ARG, "goi_step: negative iteration counts");
-    if (state->n_worlds == 0) return GOI_OK;
+    if (n_steps < 0) return fail(GOI_E_ARG, "goi_step_n: negative step count");
+    if (state->n_worlds == 0 || n_steps == 0) return GOI_OK;
     GoiModel* M = const_cast<GoiModel*>(model);
     rc = ensure_scratch(M, state);
     if (rc != GOI_OK) return rc;
@@ -576,14 +593,21 @@ int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSett
     Launch L;
     fill_launch(L, M, state, settings, dt);
     L.scratch = M->scratch;
+    L.n_steps = n_steps;
     if (debug) L.dbg = *debug;
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
     const size_t lds = block_lds_bytes(L);
-    if (L.B == kRigB && L.C == kRigC && L.J == kRigJ && L.R == kRigR && L.wpw == kRigS && M->d.B == kRigB &&
-        M->d.J == kRigJ && M->d.R == kRigR)
-        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS>), dim3(grid), dim3(kBlock), lds, st, M->d, L);
+    const bool rig = L.B == kRigB && L.C == kRigC && L.J == kRigJ && L.R == kRigR && L.wpw == kRigS &&
+                     M->d.B == kRigB && M->d.J == kRigJ && M->d.R == kRigR;
+    const dim3 g(grid), b(kBlock);
+    if (rig && n_steps == 1)
+        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, false>), g, b, lds, st, M->d, L);
+    else if (rig)
+        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, true>), g, b, lds, st, M->d, L);
+    else if (n_steps == 1)
+        hipLaunchKernelGGL(k_step<false>, g, b, lds, st, M->d, L);
     else
-        hipLaunchKernelGGL(k_step, dim3(grid), dim3(kBlock), lds, st, M->d, L);
+        hipLaunchKernelGGL(k_step<true>, g, b, lds, st, M->d, L);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
 }

@@ -241,6 +241,15 @@ int32_t goi_model_destroy(GoiModel* model);
 int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
                  void* hip_stream, const GoiDebug* debug);
 
+/* n_steps consecutive b2World::Steps of every world in one launch, the same as n_steps goi_step calls with the
+ * State's joint motor commands and forces left as they are between them (bit for bit). No counterpart in the
+ * reference's step(): it is the loop a caller runs for several physics sub-steps per action (the game's K physics
+ * sub-steps per environment step, goi_jax/box2d/gpu/graph.py:8). Each block keeps its worlds' workspaces in LDS
+ * across the sub-steps and never waits for other blocks. debug (may be NULL) receives the last sub-step's values.
+ * n_steps = 0 does nothing. */
+int32_t goi_step_n(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
+                   int32_t n_steps, void* hip_stream, const GoiDebug* debug);
+
 /* Broadphase and narrowphase only (the collide-only workload): start-of-step FindNewContacts where new_fixture
  * (step.py:50-70), then Collide (pairs.py:38-87). */
 int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings,

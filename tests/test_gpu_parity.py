@@ -190,6 +190,31 @@ def test_new_fixture_forces_full_search(oracle):
     assert (np.asarray(ref.contacts.pair) >= 0).sum() > live.sum() - drop.sum()  # the search re-created contacts
 
 
+@pytest.mark.parametrize("case,wpw,k", [("config4", None, 4), ("rig", "8", 3), ("pile", None, 5)])
+def test_step_n_equals_repeated_steps(oracle, monkeypatch, case, wpw, k):
+    """step_n_(k) (k steps in one launch, the workspaces kept in LDS between them) leaves the State k calls of
+    step_ leave, and the oracle's after k steps, bit for bit; three launches in a row."""
+    if wpw is not None:
+        monkeypatch.setenv("GOI_WORLDS_PER_WAVE", wpw)
+    if case == "pile":
+        s, m, st = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+        st, dt = perturbed(st, 64, seed=7), 1.0 / 60.0
+    else:
+        s, m, st, cfg = b2.scenes.make_config(4, 512 if case == "config4" else 1024)
+        dt = cfg.dt
+    fused = b2.layout.to_device(st, "cuda")
+    single = b2.layout.to_device(st, "cuda")
+    ref = oracle.copy(st)
+    for launch in range(3):
+        b2.step_n_(m, fused, s, dt, k)
+        for _ in range(k):
+            b2.step_(m, single, s, dt)
+            oracle.step_(m, ref, s, dt)
+        got_f, got_s = b2.layout.to_host(fused), b2.layout.to_host(single)
+        assert leaf_mismatches(got_s, got_f) == [], f"launch {launch}"
+        assert leaf_mismatches(ref, got_f) == [], f"launch {launch}"
+
+
 @pytest.mark.parametrize("edges", ["quad", "native"])
 def test_rig_kernel_parity(oracle, monkeypatch, edges):
     """The step instance compiled for the rig's dimensions (5 bodies, 32 slots, 3 joints, 4 rows, 8 worlds per
