@@ -119,6 +119,21 @@ def collide_(model, state, settings, stream=None):
     return state
 
 
+def world_manifolds(model, state, stream=None):
+    """b2WorldManifold of every contact slot of a device State: (normal (N, C, 2), points (N, C, 2, 2),
+    separations (N, C, 2)) float32 CUDA tensors (worlds-minor storage); zeros where a slot is free or has no point."""
+    view = layout.state_view(state)
+    n, C = state.contacts.pair.shape
+    dev = state.contacts.pair.device
+    dm = device_model(model, C, dev, state)
+    pitch = view.pitch
+    bufs = [torch.zeros(shape + (pitch,), dtype=torch.float32, device=dev) for shape in ((C, 2), (C, 2, 2), (C, 2))]
+    st = torch.cuda.current_stream(dev).cuda_stream if stream is None else stream
+    _abi.check(dm.L.goi_world_manifold(dm.handle, ctypes.byref(view), *[ctypes.c_void_p(b.data_ptr()) for b in bufs],
+                                       ctypes.c_void_p(st)), dm.L)
+    return tuple(b[..., :n].movedim(-1, 0) for b in bufs)
+
+
 def sincos(x):
     """(float)sin((double)x), (float)cos((double)x) of a float32 CUDA tensor, as the kernels compute them."""
     L = _abi.lib()

@@ -207,6 +207,71 @@ __global__ void __launch_bounds__(kBlock, 2) k_step_fixed(DModel m, Launch L) {
 }
 constexpr int kRigB = 5, kRigC = 32, kRigJ = 3, kRigR = 4, kRigS = 8;
 
+// b2WorldManifold::Initialize (Box2D 2.3.1; the solver's prepare computes the same, contact_solver.py:60-104) of
+// every slot of every world from the bodies' transforms, one thread per (slot, world): normal [C, 2], points
+// [C, 2, 2], separations [C, 2], worlds-minor with the State's pitch; zeros for a free slot, a slot without points
+// and the points past a manifold's count.
+__global__ void k_world_manifold(DModel m, Launch L, float* normal, float* points, float* seps) {
+    const int w = blockIdx.x * blockDim.x + threadIdx.x, c = blockIdx.y;
+    if (w >= L.n || c >= L.C) return;
+    const uint32_t P = (uint32_t)L.pitch;
+    const auto at_i = [&](int leaf, int i) { return reinterpret_cast<const int*>(L.leaf[leaf])[(uint32_t)i * P + w]; };
+    const auto at_f = [&](int leaf, int i) { return reinterpret_cast<const float*>(L.leaf[leaf])[(uint32_t)i * P + w]; };
+    const auto put = [&](float* out, int i, float v) { out[(uint32_t)i * P + w] = v; };
+    V2 n = mk(0.0f, 0.0f), p[2] = {mk(0.0f, 0.0f), mk(0.0f, 0.0f)};
+    float sep[2] = {0.0f, 0.0f};
+    const int cnt = at_i(GOI_C_PAIR, c) >= 0 ? at_i(GOI_C_COUNT, c) : 0;
+    if (cnt > 0) {
+        const int fa = at_i(GOI_C_FA, c), fb = at_i(GOI_C_FB, c);
+        const int ba = m.fixture_body[fa], bb = m.fixture_body[fb];
+        Xf xa, xb;
+        xa.p = mk(at_f(GOI_B_XF_P, 2 * ba), at_f(GOI_B_XF_P, 2 * ba + 1));
+        xa.q.c = at_f(GOI_B_XF_Q, 2 * ba); xa.q.s = at_f(GOI_B_XF_Q, 2 * ba + 1);
+        xb.p = mk(at_f(GOI_B_XF_P, 2 * bb), at_f(GOI_B_XF_P, 2 * bb + 1));
+        xb.q.c = at_f(GOI_B_XF_Q, 2 * bb); xb.q.s = at_f(GOI_B_XF_Q, 2 * bb + 1);
+        const float ra = m.radius[fa], rb = m.radius[fb];
+        const int mtype = at_i(GOI_C_MTYPE, c);
+        const V2 ln = mk(at_f(GOI_C_LOCAL_NORMAL, 2 * c), at_f(GOI_C_LOCAL_NORMAL, 2 * c + 1));
+        const V2 lp = mk(at_f(GOI_C_LOCAL_POINT, 2 * c), at_f(GOI_C_LOCAL_POINT, 2 * c + 1));
+        const V2 pl0 = mk(at_f(GOI_C_POINT_LOCAL, 4 * c), at_f(GOI_C_POINT_LOCAL, 4 * c + 1));
+        const V2 pl1 = mk(at_f(GOI_C_POINT_LOCAL, 4 * c + 2), at_f(GOI_C_POINT_LOCAL, 4 * c + 3));
+        if (mtype == kCircles) {
+            n = mk(1.0f, 0.0f);
+            const V2 pa = mul(xa, lp), pb = mul(xb, pl0);
+            const V2 d = pb - pa;
+            if (dot(d, d) > kEps * kEps) {
+                n = d;
+                normalize(n);
+            }
+            const V2 ca = pa + ra * n, cb = pb - rb * n;
+            p[0] = 0.5f * (ca + cb);
+            sep[0] = dot(cb - ca, n);
+        } else {
+            const bool face_a = mtype == kFaceA;
+            const Xf x1 = face_a ? xa : xb, x2 = face_a ? xb : xa;
+            const float r1 = face_a ? ra : rb, r2 = face_a ? rb : ra;
+            n = mul(x1.q, ln);
+            const V2 plane = mul(x1, lp);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                if (i < cnt) {
+                    const V2 clip = mul(x2, i == 0 ? pl0 : pl1);
+                    const V2 c1 = clip + (r1 - dot(clip - plane, n)) * n, c2 = clip - r2 * n;
+                    p[i] = 0.5f * (face_a ? c1 + c2 : c2 + c1);  // 0.5 (cA + cB)
+                    sep[i] = dot(c2 - c1, n);                     // faceA: cB - cA; faceB: cA - cB
+                }
+            }
+            if (!face_a) n = -n;
+        }
+    }
+    put(normal, 2 * c, n.x); put(normal, 2 * c + 1, n.y);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        put(points, 4 * c + 2 * i, p[i].x); put(points, 4 * c + 2 * i + 1, p[i].y);
+        put(seps, 2 * c + i, sep[i]);
+    }
+}
+
 __global__ void k_sincos(const float* x, float* s, float* c, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -625,6 +690,21 @@ int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiS
     L.scratch = model->scratch;
     const size_t lds = block_lds_bytes(L);
     hipLaunchKernelGGL(k_collide, dim3(grid), dim3(kBlock), lds, static_cast<hipStream_t>(hip_stream), model->d, L, 0);
+    HIP_TRY(hipGetLastError());
+    return GOI_OK;
+}
+
+int32_t goi_world_manifold(const GoiModel* model, const GoiStateView* state, float* normal, float* points,
+                           float* separations, void* hip_stream) {
+    int rc = check_view(model, state, "goi_world_manifold");
+    if (rc != GOI_OK) return rc;
+    if (state->n_worlds == 0 || state->C == 0) return GOI_OK;
+    if (!normal || !points || !separations) return fail(GOI_E_ARG, "goi_world_manifold: null output");
+    Launch L;
+    const GoiSettings none{};
+    fill_launch(L, model, state, &none, 0.0f);
+    hipLaunchKernelGGL(k_world_manifold, dim3((state->n_worlds + 255) / 256, state->C), dim3(256), 0,
+                       static_cast<hipStream_t>(hip_stream), model->d, L, normal, points, separations);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
 }

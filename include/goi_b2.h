@@ -255,6 +255,14 @@ int32_t goi_step_n(const GoiModel* model, const GoiStateView* state, const GoiSe
 int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings,
                     void* hip_stream);
 
+/* b2WorldManifold::Initialize of every contact slot of every world (Box2D 2.3.1; the solver computes the same
+ * in prepare, contact_solver.py:60-104), from the bodies' transforms: normal [C,2], points [C,2,2] and separations
+ * [C,2], device buffers laid out worlds-minor with the view's pitch; zeros for free slots, slots without points and
+ * points past a manifold's count. The counterpart of the reference oracle's contact readers for debugging and
+ * parity dumps (goi_jax/reference/capi.cpp:786-838). */
+int32_t goi_world_manifold(const GoiModel* model, const GoiStateView* state, float* normal, float* points,
+                           float* separations, void* hip_stream);
+
 /* Correctly rounded float32 sin/cos of n values on the device, as the step computes them (math2d.py:291-310):
  * s[i] = (float)sin((double)x[i]), c[i] = (float)cos((double)x[i]). Device pointers. */
 int32_t goi_sincos(const float* x, float* s, float* c, int32_t n, void* hip_stream);

@@ -1,0 +1,76 @@
+"""Device world manifolds against the float32 host getter, bit for bit, and DLPack interchange of device States."""
+import numpy as np
+import pytest
+
+from util import b2, leaf_mismatches, perturbed, wd
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def _host_manifolds(model, st):
+    """debug.world_manifold over every slot of every world of a numpy State: (N, C, 2), (N, C, 2, 2), (N, C, 2)."""
+    ct, bd = st.contacts, st.bodies
+    n, C = ct.pair.shape
+    nrm, pts, seps = np.zeros((n, C, 2), np.float32), np.zeros((n, C, 2, 2), np.float32), np.zeros((n, C, 2), np.float32)
+    for w in range(n):
+        for c in range(C):
+            if ct.pair[w, c] < 0 or ct.count[w, c] == 0:
+                continue
+            fa, fb = int(ct.fa[w, c]), int(ct.fb[w, c])
+            ba, bb = int(model.fixture_body[fa]), int(model.fixture_body[fb])
+            nrm[w, c], pts[w, c], seps[w, c] = b2.debug.world_manifold(
+                int(ct.mtype[w, c]), int(ct.count[w, c]), ct.local_normal[w, c], ct.local_point[w, c],
+                ct.point_local[w, c], bd.xf_p[w, ba], bd.xf_q[w, ba], bd.xf_p[w, bb], bd.xf_q[w, bb],
+                model.radius[fa], model.radius[fb])
+    return nrm, pts, seps
+
+
+@pytest.mark.parametrize("name,steps", [("pile", 40), ("circles", 40), ("edges", 40), ("polygons", 60)])
+def test_world_manifolds_match_host_getter(oracle, name, steps):
+    """Every slot of 16 perturbed worlds after some steps: the device kernel and the host getter compute
+    b2WorldManifold::Initialize with the same float32 operations, so they agree bit for bit (free slots and slots
+    without points read zero on both)."""
+    s, m, st = b2.scenes.build_test_scene(name, iterations=(8, 3))
+    dev = b2.layout.to_device(perturbed(st, 16, seed=7), "cuda")
+    for _ in range(steps):
+        b2.step_(m, dev, s, 1.0 / 60.0)
+    got = [x.cpu().numpy() for x in b2.world_manifolds(m, dev)]
+    want = _host_manifolds(m, b2.layout.to_host(dev))
+    assert (np.asarray(b2.layout.to_host(dev).contacts.count) > 0).sum() > 8
+    for g, w, what in zip(got, want, ("normal", "points", "separations")):
+        assert g.shape == w.shape and g.tobytes() == w.tobytes(), what
+
+
+def test_world_manifolds_config4(oracle):
+    """The rig workload (512 worlds, native edge terrain) after 30 steps with actions."""
+    s, m, st, cfg = b2.scenes.make_config(4, 512, edges="native")
+    dev = b2.layout.to_device(st, "cuda")
+    rng = np.random.default_rng(2)
+    for _ in range(30):
+        a = b2.scenes.actions(rng, 512)
+        b2.scenes.apply_actions(dev.joints.motor_speed, dev.joints.max_motor, torch.from_numpy(a).cuda())
+        b2.step_(m, dev, s, cfg.dt)
+    got = [x.cpu().numpy() for x in b2.world_manifolds(m, dev)]
+    want = _host_manifolds(m, b2.layout.to_host(dev))
+    for g, w in zip(got, want):
+        assert g.tobytes() == w.tobytes()
+
+
+def test_dlpack_round_trip(oracle):
+    """A batch-major State handed over by DLPack (torch tensors on the GPU, as a JAX or CuPy producer would) steps
+    like the oracle, and to_dlpack hands back batch-major copies that numpy and torch consumers read unchanged."""
+    s, m, st = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+    st = perturbed(st, 8, seed=1)
+    producer = wd.from_leaves([torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in wd.leaves(st)])
+    dev = b2.io.from_dlpack(producer, "cuda")
+    ref = oracle.copy(st)
+    for _ in range(10):
+        b2.step_(m, dev, s, 1.0 / 60.0)
+        oracle.step_(m, ref, s, 1.0 / 60.0)
+    out = b2.io.to_dlpack(dev)
+    back = wd.from_leaves([np.from_dlpack(torch.from_dlpack(x).cpu()) for x in wd.leaves(out)])
+    assert leaf_mismatches(ref, back) == []
+    bad = wd.from_leaves([x.double() if x.dtype == torch.float32 else x for x in wd.leaves(producer)])
+    with pytest.raises(TypeError):
+        b2.io.from_dlpack(bad, "cuda")
