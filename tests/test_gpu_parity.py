@@ -235,3 +235,30 @@ def test_worlds_per_wave_variants(oracle, monkeypatch, wpw):
     s, m, st, cfg = b2.scenes.make_config(4, 256)
     rng = np.random.default_rng(21)
     _run(m, st, s, cfg.dt, 10, oracle, [b2.scenes.actions(rng, 256) for _ in range(10)])
+
+
+@pytest.mark.parametrize("auto_clear", [True, False])
+def test_applied_forces_parity(oracle, auto_clear):
+    """Forces and torques written into the State between steps (every 5th step, random per world and body), with
+    and without auto_clear_forces."""
+    from dataclasses import replace
+    s, m, st = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+    s = replace(s, auto_clear_forces=auto_clear)
+    st = perturbed(st, 32, seed=9)
+    dyn = np.asarray(st.bodies.type) == wd.DYNAMIC
+    rng = np.random.default_rng(11)
+    dev = b2.layout.to_device(st, "cuda")
+    ref = oracle.copy(st)
+    for k in range(40):
+        if k % 5 == 0:
+            f = np.where(dyn[..., None], rng.normal(0, 20, ref.bodies.force.shape), 0).astype(np.float32)
+            t = np.where(dyn, rng.normal(0, 5, ref.bodies.torque.shape), 0).astype(np.float32)
+            ref.bodies.force[...] = f
+            ref.bodies.torque[...] = t
+            dev.bodies.force.copy_(torch.from_numpy(f))
+            dev.bodies.torque.copy_(torch.from_numpy(t))
+        b2.step_(m, dev, s, 1.0 / 60.0)
+        oracle.step_(m, ref, s, 1.0 / 60.0)
+        bad = leaf_mismatches(ref, b2.layout.to_host(dev))
+        assert bad == [], f"step {k + 1}: {bad[:4]}"
+    assert np.abs(np.asarray(ref.bodies.force)).sum() == 0 if auto_clear else np.abs(ref.bodies.force).sum() > 0
