@@ -97,6 +97,55 @@ struct RotMemo {
     }
 };
 
+// ---- lane groups
+//
+// The lanes that run one world together: a group of G consecutive lanes (G a power of two, aligned to G), every lane
+// on the same data. A loop over a shape's vertices splits over the group (lane `sub` takes i = sub, sub + G, ...), and
+// a reduction over the group gives every lane the result of the sequential loop. Solo is the one-lane case (a
+// block-cooperative task), for which the split loop is the plain loop and the reductions vanish.
+struct Solo {
+    GOI_D int sub() const { return 0; }
+    GOI_D int G() const { return 1; }
+};
+struct Group {
+    int s, g;
+    GOI_D int sub() const { return s; }
+    GOI_D int G() const { return g; }
+};
+
+// The sequential running maximum `if (v > best) { best = v; at = i; }` over i in ascending order, started from
+// (best, at), equals the group's combination of each lane's running maximum over its own indices (started from the
+// same (best, at)) when a larger value wins and equal values keep the smaller index: NaN never wins (its compares
+// are false), and among equal maxima the first index is the sequential winner. Same for the minimum.
+template <class Grp>
+GOI_D void group_argmax(const Grp& g, float& v, int& at) {
+    for (int d = 1; d < g.G(); d <<= 1) {
+        const float ov = __shfl_xor(v, d, 64);
+        const int oi = __shfl_xor(at, d, 64);
+        if (ov > v || (ov == v && oi < at)) {
+            v = ov;
+            at = oi;
+        }
+    }
+}
+template <class Grp>
+GOI_D void group_argmin(const Grp& g, float& v, int& at) {
+    for (int d = 1; d < g.G(); d <<= 1) {
+        const float ov = __shfl_xor(v, d, 64);
+        const int oi = __shfl_xor(at, d, 64);
+        if (ov < v || (ov == v && oi < at)) {
+            v = ov;
+            at = oi;
+        }
+    }
+}
+template <class Grp>
+GOI_D bool group_any(const Grp& g, bool p) {
+    int x = p ? 1 : 0;
+    for (int d = 1; d < g.G(); d <<= 1) x |= __shfl_xor(x, d, 64);
+    return x != 0;
+}
+
 // b2Mat22::Solve / b2Mat33::Solve22
 GOI_D V2 solve22(float a11, float a12, float a21, float a22, V2 b) {
     float det = a11 * a22 - a12 * a21;

@@ -27,8 +27,10 @@ GOI_D int feature_key(int ia, int ib, int ta, int tb) { return ia | (ib << 8) | 
 GOI_D V2 mvert(const DModel& m, int f, int i) { return m.verts[f * kPoly + i]; }
 GOI_D V2 mnorm(const DModel& m, int f, int i) { return m.normals[f * kPoly + i]; }
 
-// b2FindMaxSeparation: (edge of poly1, separation) over poly1's normals against poly2's vertices
-GOI_D float max_separation(const DModel& m, int f1, const Xf& xf1, int f2, const Xf& xf2, int& edge) {
+// b2FindMaxSeparation: (edge of poly1, separation) over poly1's normals against poly2's vertices; poly1's normals
+// split over the lane group
+template <class Grp>
+GOI_D float max_separation(const DModel& m, int f1, const Xf& xf1, int f2, const Xf& xf2, int& edge, const Grp& g) {
     const int c1 = m.count[f1], c2 = m.count[f2];
     const Xf xf = mulT(xf2, xf1);
     V2 v2s[kPoly];
@@ -36,7 +38,7 @@ GOI_D float max_separation(const DModel& m, int f1, const Xf& xf1, int f2, const
     for (int j = 0; j < kPoly; ++j) v2s[j] = j < c2 ? mvert(m, f2, j) : mk(0.0f, 0.0f);
     int best = 0;
     float maxsep = -kMaxFloat;
-    for (int i = 0; i < c1; ++i) {
+    for (int i = g.sub(); i < c1; i += g.G()) {
         const V2 n = mul(xf.q, mnorm(m, f1, i));
         const V2 v1 = mul(xf, mvert(m, f1, i));
         float si = kMaxFloat;
@@ -52,6 +54,7 @@ GOI_D float max_separation(const DModel& m, int f1, const Xf& xf1, int f2, const
             best = i;
         }
     }
+    group_argmax(g, maxsep, best);
     edge = best;
     return maxsep;
 }
@@ -80,14 +83,15 @@ GOI_D int clip_line(ClipV& o0, ClipV& o1, const ClipV& i0, const ClipV& i1, V2 n
     return num;
 }
 
+template <class Grp>
 GOI_D void collide_polygons(const DModel& m, int fa, const Xf& xfa, int fb, const Xf& xfb, float linear_slop,
-                            Manifold& out) {
+                            Manifold& out, const Grp& g) {
     out.count = 0;
     const float total_radius = m.radius[fa] + m.radius[fb];
     int edge_a, edge_b;
-    const float sep_a = max_separation(m, fa, xfa, fb, xfb, edge_a);
+    const float sep_a = max_separation(m, fa, xfa, fb, xfb, edge_a, g);
     if (sep_a > total_radius) return;
-    const float sep_b = max_separation(m, fb, xfb, fa, xfa, edge_b);
+    const float sep_b = max_separation(m, fb, xfb, fa, xfa, edge_b, g);
     if (sep_b > total_radius) return;
     const float k_tol = 0.1f * linear_slop;
     const bool flip = sep_b > sep_a + k_tol;
@@ -101,13 +105,14 @@ GOI_D void collide_polygons(const DModel& m, int fa, const Xf& xfa, int fb, cons
     const V2 n1 = mulT(xf2.q, mul(xf1.q, mnorm(m, f1, edge1)));
     int idx = 0;
     float mind = kMaxFloat;
-    for (int i = 0; i < c2; ++i) {
+    for (int i = g.sub(); i < c2; i += g.G()) {
         const float d = dot(n1, mnorm(m, f2, i));
         if (d < mind) {
             mind = d;
             idx = i;
         }
     }
+    group_argmin(g, mind, idx);
     const int i2 = idx + 1 < c2 ? idx + 1 : 0;
     ClipV inc0, inc1;
     inc0.v = mul(xf2, mvert(m, f2, idx)); inc0.ia = edge1; inc0.ib = idx; inc0.ta = 1; inc0.tb = 0;
@@ -146,21 +151,31 @@ GOI_D void collide_polygons(const DModel& m, int fa, const Xf& xfa, int fb, cons
     out.id1 = id1;
 }
 
-GOI_D void collide_polygon_circle(const DModel& m, int fa, const Xf& xfa, int fb, const Xf& xfb, Manifold& out) {
+// The face loop splits over the lane group; the early out on any separating face is the sequential one (nothing
+// but count = 0 is written before it).
+template <class Grp>
+GOI_D void collide_polygon_circle(const DModel& m, int fa, const Xf& xfa, int fb, const Xf& xfb, Manifold& out,
+                                  const Grp& g) {
     out.count = 0;
     const V2 cl = mulT(xfa, mul(xfb, mvert(m, fb, 0)));
     const float radius = m.radius[fa] + m.radius[fb];
     const int n = m.count[fa];
     int ni = 0;
     float sep = -kMaxFloat;
-    for (int i = 0; i < n; ++i) {
+    bool apart = false;
+    for (int i = g.sub(); i < n; i += g.G()) {
         const float s = dot(mnorm(m, fa, i), cl - mvert(m, fa, i));
-        if (s > radius) return;
+        if (s > radius) {
+            apart = true;
+            break;
+        }
         if (s > sep) {
             sep = s;
             ni = i;
         }
     }
+    if (group_any(g, apart)) return;
+    group_argmax(g, sep, ni);
     const int i2 = ni + 1 < n ? ni + 1 : 0;
     const V2 v1 = mvert(m, fa, ni), v2 = mvert(m, fa, i2);
     const V2 centre = mvert(m, fb, 0);
@@ -408,14 +423,19 @@ GOI_D void collide_edge_polygon(const DModel& m, int fa, const Xf& xfa, int fb, 
 }
 
 // b2Contact::Evaluate by shape types (b2Contact::Create puts a polygon before a circle and an edge before either)
+template <class Grp>
 GOI_D void evaluate(const DModel& m, int fa, int fb, const Xf& xfa, const Xf& xfb, const GoiSettings& s,
-                    Manifold& out) {
+                    Manifold& out, const Grp& g) {
     const int ta = m.shape_type[fa], tb = m.shape_type[fb];
-    if (ta == GOI_POLYGON && tb == GOI_POLYGON) collide_polygons(m, fa, xfa, fb, xfb, s.linear_slop, out);
-    else if (ta == GOI_POLYGON) collide_polygon_circle(m, fa, xfa, fb, xfb, out);
+    if (ta == GOI_POLYGON && tb == GOI_POLYGON) collide_polygons(m, fa, xfa, fb, xfb, s.linear_slop, out, g);
+    else if (ta == GOI_POLYGON) collide_polygon_circle(m, fa, xfa, fb, xfb, out, g);
     else if (ta == GOI_EDGE && tb == GOI_POLYGON) collide_edge_polygon(m, fa, xfa, fb, xfb, s, out);
     else if (ta == GOI_EDGE) collide_edge_circle(m, fa, xfa, fb, xfb, out);
     else collide_circles(m, fa, xfa, fb, xfb, out);
+}
+GOI_D void evaluate(const DModel& m, int fa, int fb, const Xf& xfa, const Xf& xfb, const GoiSettings& s,
+                    Manifold& out) {
+    evaluate(m, fa, fb, xfa, xfb, s, out, Solo{});
 }
 
 }  // namespace goi

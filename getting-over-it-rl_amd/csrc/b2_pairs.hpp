@@ -54,20 +54,25 @@ GOI_D bool contact_update(const World& W, int k, const Manifold& mf) {
 
 // ---------------------------------------------------------------- block-cooperative task runs
 //
-// A block is one wavefront: its first S lanes own worlds, and all 64 lanes share the work of task lists the worlds
-// build (TOIs to compute, manifolds to evaluate). Each world numbers its tasks 0..n-1 and keeps their inputs in its
-// workspace or its contact rows; coop_run hands task i of the world on lane o to some lane of the block.
+// A block is one wavefront of S worlds, each run by G = 64 / S consecutive lanes (its lane group: every lane of the
+// group runs the world's sequential code on the same data, and a few phases split their loops over the group). All
+// 64 lanes share the work of task lists the worlds build (TOIs to compute, manifolds to evaluate). Each world numbers
+// its tasks 0..n-1 and keeps their inputs in its workspace or its contact rows; coop_run hands task i of world o (the
+// block's o-th) to some lane of the block.
 struct Coop {
-    World base;      // lane 0's world (the fields common to the block)
-    int* lds;        // the block's LDS workspace (lane 0's base)
+    World base;      // world 0's view (the fields common to the block)
+    int* lds;        // the block's LDS workspace (world 0's base)
     int* scan;       // 64 ints after the workspaces
     uint32_t* rows;  // contact rows (Launch.scratch)
     int w0;          // the block's first world
     int lanes;       // lanes sharing the tasks (the block size)
+    int G;           // lanes per world
     GOI_D World world(int o) const {
         World W = base;
         W.ws = lds + o;
         W.w = w0 + o;
+        W.sub = 0;  // a task runs on one lane
+        W.G = 1;
         return W;
     }
     GOI_D Rows task_rows(int o) const {
@@ -77,7 +82,8 @@ struct Coop {
     }
 };
 
-// Called by all lanes of the block together; `my` = this lane's task count (0 for lanes without a world).
+// Called by all lanes of the block together; `my` = this lane's task count: the world's count on the first lane of
+// its group, 0 on every other lane.
 template <typename F>
 GOI_D void coop_run(const Coop& co, int my, F&& task) {
     const int lane = threadIdx.x;
@@ -96,7 +102,7 @@ GOI_D void coop_run(const Coop& co, int my, F&& task) {
             const int mid = (lo + hi) >> 1;
             if (co.scan[mid] > t) hi = mid; else lo = mid + 1;
         }
-        task(lo, t - (lo ? co.scan[lo - 1] : 0));
+        task(lo / co.G, t - (lo ? co.scan[lo - 1] : 0));
     }
     __syncthreads();  // the results visible to their owners
 }
@@ -180,11 +186,13 @@ GOI_D void collide_apply(const DModel& m, const World& W, const Rows& R) {
     W.nlive() = j;
 }
 
-// Collide for the block: called by all lanes together; `valid` marks the lanes that own a world.
-GOI_D void collide_block(const DModel& m, const Coop& co, const World& W, bool valid, const GoiSettings& s) {
+// Collide for the block: called by all lanes together; `valid` marks the lanes that run a world, `leader` the first
+// lane of each world's group.
+GOI_D void collide_block(const DModel& m, const Coop& co, const World& W, bool valid, bool leader,
+                         const GoiSettings& s) {
     const int nt = valid ? collide_mark(m, W) : 0;
-    coop_run(co, nt, [&](int o, int i) { collide_task(m, co, o, i, s); });
-    if (valid) collide_apply(m, W, co.task_rows(threadIdx.x));
+    coop_run(co, leader ? nt : 0, [&](int o, int i) { collide_task(m, co, o, i, s); });
+    if (valid) collide_apply(m, W, co.task_rows(W.w - co.w0));
 }
 
 // Sorted buffer (the workspace's newp array) of the smallest new candidate indices of one FindNewContacts call,

@@ -321,7 +321,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     body_advance(W, Bb, min_alpha);
     {
         Manifold mf;
-        evaluate(m, fa, fb, W.xf(A), W.xf(Bb), s, mf);
+        evaluate(m, fa, fb, W.xf(A), W.xf(Bb), s, mf, W.grp());
         if (contact_update(W, min_slot, mf)) { W.wake(A); W.wake(Bb); }
     }
     W.set_tflag(min_slot, 0);
@@ -358,7 +358,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
             const SweepBackup bk = backup(W, other);
             if (!((bflag >> other) & 1ull)) body_advance(W, other, min_alpha);
             Manifold mf;
-            evaluate(m, W.fa(c), W.fb(c), W.xf(ca), W.xf(cb), s, mf);
+            evaluate(m, W.fa(c), W.fb(c), W.xf(ca), W.xf(cb), s, mf, W.grp());
             if (contact_update(W, c, mf)) { W.wake(ca); W.wake(cb); }
             W.set_ten(c, 1);
             if (!W.touching(c)) {
@@ -464,9 +464,9 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
 }
 
 // b2World::SolveTOI (toi.py:827-865). Called by every lane of the block (the reset, the TOI searches and the final
-// copy are cooperative); `valid` marks the lanes that own a world.
+// copy are cooperative); `valid` marks the lanes that run a world, `leader` the first lane of each world's group.
 GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
-                           float dt, bool valid, const Coop& co, const BlockCopy& bc) {
+                           float dt, bool valid, bool leader, const Coop& co, const BlockCopy& bc) {
     if (W.C == 0 || m.P == 0) return;
     if (s.unity_toi && !m.any_toi_body) return;
     reset_toi_block(bc);
@@ -476,7 +476,8 @@ GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, co
         int slot = -1;
         float alpha = 1.0f;
         const auto toi = [&](int o, int i) { toi_task(m, co, o, i, s.linear_slop); };
-        coop_run(co, valid ? toi_search_prepare(m, W, CR, s) : 0, toi);
+        const int nt0 = valid ? toi_search_prepare(m, W, CR, s) : 0;
+        coop_run(co, leader ? nt0 : 0, toi);
         bool found = valid && toi_search_pick(W, s, slot, alpha);
         // the block iterates while any world has an event to process; the others take part in the searches only
         while (__any(found && events < max_events)) {
@@ -485,7 +486,8 @@ GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, co
                 toi_event(m, W, bd, CR, s, dt, slot, alpha);
                 ++events;
             }
-            coop_run(co, act ? toi_search_prepare(m, W, CR, s) : 0, toi);
+            const int nt = act ? toi_search_prepare(m, W, CR, s) : 0;
+            coop_run(co, leader ? nt : 0, toi);
             found = act && toi_search_pick(W, s, slot, alpha);
         }
     }

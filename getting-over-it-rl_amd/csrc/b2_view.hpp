@@ -113,6 +113,9 @@ struct World {
     const int2* nlink;
     int nk;
     unsigned long long smask, dmask;  // static and dynamic bodies (Model.body_type, the same in every world)
+    int sub, G;       // the lane's place in the world's lane group, and the group's size
+
+    GOI_D Group grp() const { return Group{sub, G}; }
 
     GOI_D bool is_static(int b) const { return (smask >> b) & 1ull; }
     GOI_D bool is_dynamic(int b) const { return (dmask >> b) & 1ull; }

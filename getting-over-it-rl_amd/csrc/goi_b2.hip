@@ -57,7 +57,8 @@ struct Launch {
 __host__ __device__ inline int node_offset(int words, int wpw) { return ((words * wpw + kBlock) + 3) & ~3; }
 
 // World w on lane `lane` of its block; the block's LDS workspace holds L.wpw lanes.
-__device__ __forceinline__ World make_world(const DModel& m, const Launch& L, int w, int* lds, int lane) {
+__device__ __forceinline__ World make_world(const DModel& m, const Launch& L, int w, int* lds, int lane, int sub,
+                                           int G) {
     World W;
     W.pitch = L.pitch;
     W.B = L.B;
@@ -72,6 +73,8 @@ __device__ __forceinline__ World make_world(const DModel& m, const Launch& L, in
     W.nk = L.lds_nodes;
     W.nbox = reinterpret_cast<const float4*>(lds + node_offset(W.k.words, L.wpw));
     W.nlink = reinterpret_cast<const int2*>(W.nbox + L.lds_nodes);
+    W.sub = sub;
+    W.G = G;
     W.init_masks(m);
     return W;
 }
@@ -107,6 +110,30 @@ __device__ __forceinline__ Rows joint_rows(const Launch& L, int w) {
 
 // ---------------------------------------------------------------- kernels
 
+// Lanes and worlds of a block: the block's L.wpw worlds each take G consecutive lanes (its lane group; G is the
+// largest power of two with G * wpw <= 64).
+// Every lane of a group runs the world's sequential code on the same data (same loads, same stores of the same
+// values), so the group's lanes stay together on every branch; `leader` is the group's first lane, which alone
+// reports the world's task counts to coop_run.
+struct LaneMap {
+    int G;        // lanes per world
+    int wl;       // this lane's world in the block
+    int sub;      // this lane's place in its world's group
+    bool valid;   // the lane runs a world (wl < wpw and w0 + wl < n)
+    bool leader;  // valid and sub == 0
+};
+__device__ __forceinline__ LaneMap lane_map(const Launch& L, int w0, int lane) {
+    int G = kBlock;
+    while (G * L.wpw > kBlock) G >>= 1;
+    LaneMap lm;
+    lm.G = G;
+    lm.wl = lane / G;
+    lm.sub = lane - lm.wl * G;
+    lm.valid = lm.wl < L.wpw && w0 + lm.wl < L.n;  // wpw need not divide 64: lanes past G * wpw stay idle
+    lm.leader = lm.valid && lm.sub == 0;
+    return lm;
+}
+
 // World group of this block. Blocks are dealt to the 8 XCDs round robin (block b on XCD b % 8), and each XCD has its
 // own L2; numbering the groups so that every XCD holds one contiguous range keeps neighbouring worlds, which share
 // 128-byte lines of every State leaf, behind the same L2. A bijection on [0, gridDim.x) for any grid.
@@ -124,6 +151,7 @@ __device__ __forceinline__ Coop block_coop(const Launch& L, const World& W, int*
     co.rows = L.scratch;
     co.w0 = w0;
     co.lanes = kBlock;
+    co.G = lane_map(L, w0, 0).G;
     return co;
 }
 
@@ -134,16 +162,17 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
     stage_nodes(m, L, lds);
     const int lane = threadIdx.x;
     const int w0 = xcd_group() * L.wpw;
-    const bool valid = lane < L.wpw && w0 + lane < L.n;
-    const World W = make_world(m, L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
+    const LaneMap lm = lane_map(L, w0, lane);
+    // W is used only where lm.valid
+    const World W = make_world(m, L, lm.valid ? w0 + lm.wl : w0, lds, lm.valid ? lm.wl : 0, lm.sub, lm.G);
     const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
     load_mirror_block(m, bc);
     build_order_block(bc);
-    if (valid) {
+    if (lm.valid) {
         if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
         W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     }
-    if (!start_only) collide_block(m, block_coop(L, W, lds, w0), W, valid, L.s);
+    if (!start_only) collide_block(m, block_coop(L, W, lds, w0), W, lm.valid, lm.leader, L.s);
     store_mirror_block(bc);
 }
 
@@ -156,11 +185,12 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     stage_nodes(m, L, lds);
     const int lane = threadIdx.x;
     const int w0 = xcd_group() * L.wpw;
-    const bool valid = lane < L.wpw && w0 + lane < L.n;
-    const World W = make_world(m, L, valid ? w0 + lane : w0, lds, valid ? lane : 0);  // only used when valid
+    const LaneMap lm = lane_map(L, w0, lane);
+    const bool valid = lm.valid;
+    const World W = make_world(m, L, valid ? w0 + lm.wl : w0, lds, valid ? lm.wl : 0, lm.sub, lm.G);  // used if valid
     const Coop co = block_coop(L, W, lds, w0);
     Bodies bd;
-    bd.s = reinterpret_cast<float*>(lds) + W.k.o_body * W.S + (valid ? lane : 0);
+    bd.s = reinterpret_cast<float*>(lds) + W.k.o_body * W.S + (valid ? lm.wl : 0);
     bd.B = L.B;
     bd.st = W.S;
     const Rows CR = contact_rows(L, W.w);
@@ -177,9 +207,9 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
             if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
             W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
         }
-        collide_block(m, co, W, valid, L.s);
+        collide_block(m, co, W, valid, lm.leader, L.s);
         if (valid) solve_world(m, W, bd, CR, joint_rows(L, W.w), L.s, L.dt, L.dbg);
-        if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, co, bc);
+        if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, lm.leader, co, bc);
         if (valid) {
             const float dt = L.dt;
             if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
