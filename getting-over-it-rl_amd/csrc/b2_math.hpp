@@ -113,6 +113,11 @@ struct Group {
     GOI_D int G() const { return g; }
 };
 
+// Orders the memory accesses of a lane group: what one lane of the wavefront wrote before it (global or LDS) is
+// what every lane reads after it. The lanes of a wavefront execute in lockstep, so this only keeps the compiler from
+// moving accesses across it.
+GOI_D void group_sync() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
+
 // The sequential running maximum `if (v > best) { best = v; at = i; }` over i in ascending order, started from
 // (best, at), equals the group's combination of each lane's running maximum over its own indices (started from the
 // same (best, at)) when a larger value wins and equal values keep the smaller index: NaN never wins (its compares

@@ -44,7 +44,9 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     }
     const bool warm = s.warm_starting != 0;
     const bool v24 = s.revolute_v24 != 0;
-    for (int i = 0; i < I.nc; ++i) {
+    // the constraint rows are independent of each other: the world's lane group prepares them together (one row
+    // per lane), then every lane warm-starts them in order
+    for (int i = W.sub; i < I.nc; i += W.G) {
         const int slot = I.corder(i);
         const int ia = W.ba(slot), ib = W.bb(slot);
         Rot qA, qB;
@@ -52,9 +54,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         qB.c = bd.at(6, ib); qB.s = bd.at(7, ib);
         cs_prepare(m, W, bd, CR, i, slot, warm, dt_ratio, qA, qB, s.velocity_threshold);
     }
-    if (warm)
-        for (int i = 0; i < I.nc; ++i) cs_warm_start(bd, CR, i);
-    for (int i = 0; i < I.nj; ++i) {
+    for (int i = W.sub; i < I.nj; i += W.G) {
         const int jid = I.jorder(i);
         const int ia = m.joint_a[jid], ib = m.joint_b[jid];
         Rot qA, qB;
@@ -62,6 +62,9 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         qB.c = bd.at(6, ib); qB.s = bd.at(7, ib);
         jn_prepare(m, W, bd, JRw, i, jid, s, dt, dt_ratio, warm, qA, qB);
     }
+    group_sync();  // rows written by one lane of the group are read by all
+    if (warm)
+        for (int i = 0; i < I.nc; ++i) cs_warm_start(bd, CR, i);
     for (int i = 0; i < I.nj; ++i) jn_warm_start(bd, JRw, i, v24);
     for (int it = 0; it < s.velocity_iterations; ++it) {
         for (int i = 0; i < I.nj; ++i) jn_solve_velocity(bd, JRw, i, v24);
