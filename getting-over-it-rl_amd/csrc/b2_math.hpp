@@ -113,6 +113,15 @@ struct Group {
     GOI_D int G() const { return g; }
 };
 
+template <class Grp>
+GOI_D unsigned long long group_or(const Grp& g, unsigned long long x) {
+    for (int d = 1; d < g.G(); d <<= 1) {
+        const unsigned lo = __shfl_xor((unsigned)x, d, 64), hi = __shfl_xor((unsigned)(x >> 32), d, 64);
+        x |= ((unsigned long long)hi << 32) | lo;
+    }
+    return x;
+}
+
 // Orders the memory accesses of a lane group: what one lane of the wavefront wrote before it (global or LDS) is
 // what every lane reads after it. The lanes of a wavefront execute in lockstep, so this only keeps the compiler from
 // moving accesses across it.

@@ -15,8 +15,9 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     find_islands(m, W, I);
     const float h = dt;
     const float gx = W.f(GOI_S_GRAVITY, 0), gy = W.f(GOI_S_GRAVITY, 1);
-    // integrate velocities of dynamic island bodies; the sweep starts at the current pose
-    for (int b = 0; b < W.B; ++b) {
+    // integrate velocities of dynamic island bodies; the sweep starts at the current pose (bodies are independent
+    // here and in the other per-body loops below: one body per lane of the group)
+    for (int b = W.sub; b < W.B; b += W.G) {
         V2 v = W.v2(GOI_B_V, b);
         float w = W.f(GOI_B_W, b);
         const V2 c = W.v2(GOI_B_C, b);
@@ -42,6 +43,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         bd.at(6, b) = q.c;
         bd.at(7, b) = q.s;
     }
+    group_sync();
     const bool warm = s.warm_starting != 0;
     const bool v24 = s.revolute_v24 != 0;
     // the constraint rows are independent of each other: the world's lane group prepares them together (one row
@@ -86,7 +88,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     // integrate positions with the per-step clamps (step.py:120-135)
     const float max_t = s.clamps_per_second ? s.max_translation * h : s.max_translation;
     const float max_r = s.clamps_per_second ? s.max_rotation * h : s.max_rotation;
-    for (int b = 0; b < W.B; ++b) {
+    for (int b = W.sub; b < W.B; b += W.G) {
         if (I.body_island(b) < 0) continue;
         V2 v = bd.v(b);
         float w = bd.w(b);
@@ -100,6 +102,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         bd.set_c(b, bd.c(b) + h * v, bd.a(b) + h * w);
         bd.set_v(b, v, w);
     }
+    group_sync();
     // position iterations with per-island early exit (step.py:197-251)
     unsigned long long done = 0ull, all = I.n >= 64 ? ~0ull : ((1ull << I.n) - 1ull);
     RotMemo qa, qb;
@@ -123,7 +126,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
             if (!((done >> i) & 1ull) && W.fwork(i) >= okay_sep && !((jbad >> i) & 1ull)) done |= 1ull << i;
     }
     // write back + SynchronizeTransform
-    for (int b = 0; b < W.B; ++b) {
+    for (int b = W.sub; b < W.B; b += W.G) {
         if (I.body_island(b) < 0) continue;
         const V2 c = bd.c(b);
         const float a = bd.a(b);
@@ -136,6 +139,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         W.f(GOI_B_XF_Q, 2 * b) = q.c;
         W.f(GOI_B_XF_Q, 2 * b + 1) = q.s;
     }
+    group_sync();
     // sleep per island (step.py:153-168)
     unsigned long long isl_sleep = 0ull;
     if (s.allow_sleep) {
@@ -200,10 +204,12 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     // (Collide destroys only contacts whose fat AABBs separated), so the result is the full scan's; a world that ever
     // dropped a candidate (overflow) keeps scanning all rows, since its dropped pairs may now find a slot.
     unsigned long long refat = 0ull;
-    for (int b = 0; b < W.B; ++b) {
+    for (int b = W.sub; b < W.B; b += W.G) {
         if (I.body_island(b) < 0 || W.is_static(b)) continue;
         refat |= sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
     }
+    refat = group_or(W.grp(), refat);
+    group_sync();
     find_new_contacts(m, W, W.i32(GOI_S_OVERFLOW, 0) == 0 ? refat : ~0ull);
 }
 
