@@ -114,6 +114,11 @@ struct Group {
 };
 
 template <class Grp>
+GOI_D int group_sum(const Grp& g, int x) {
+    for (int d = 1; d < g.G(); d <<= 1) x += __shfl_xor(x, d, 64);
+    return x;
+}
+template <class Grp>
 GOI_D unsigned long long group_or(const Grp& g, unsigned long long x) {
     for (int d = 1; d < g.G(); d <<= 1) {
         const unsigned lo = __shfl_xor((unsigned)x, d, 64), hi = __shfl_xor((unsigned)(x >> 32), d, 64);

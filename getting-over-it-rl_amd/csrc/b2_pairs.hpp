@@ -214,10 +214,11 @@ struct NewPairs {
     }
 };
 
+// whether a slot holds candidate p (the slots split over the lane group)
 GOI_D bool slot_has_pair(const World& W, int p) {
     bool has = false;
-    for (int k = 0; k < W.C; ++k) has |= W.pair(k) == p;
-    return has;
+    for (int k = W.sub; k < W.C; k += W.G) has |= W.pair(k) == p;
+    return group_any(W.grp(), has);
 }
 
 // b2ContactManager::FindNewContacts (pairs.py:134-178) without scanning the candidate list: one walk of the static
@@ -234,7 +235,8 @@ GOI_D bool slot_has_pair(const World& W, int p) {
 GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long query_rows = ~0ull) {
     if (m.P == 0 || query_rows == 0ull) return;
     int n_free = 0;
-    for (int k = 0; k < W.C; ++k) n_free += W.pair(k) < 0;
+    for (int k = W.sub; k < W.C; k += W.G) n_free += W.pair(k) < 0;
+    n_free = group_sum(W.grp(), n_free);
     NewPairs np{W, 0, 0, n_free};
     // the fat boxes of all rows into the workspace; the queried rows on active bodies and their union box
     unsigned long long rows = 0ull;

@@ -450,26 +450,30 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         moved |= 1ull << b;
         refat |= sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
     }
-    for (int c = 0; c < W.C; ++c) {
-        if (W.pair(c) < 0) continue;
-        const int ca = W.ba(c), cb = W.bb(c);
-        if (((moved >> ca) & 1ull) || ((moved >> cb) & 1ull)) W.set_tflag(c, 0);
-    }
-    // FindNewContacts; a slot that received a new contact starts with fresh TOI state. The keys before it go to
-    // the workspace's corder array, which Solve's island order no longer needs.
+    // the slot loops below split over the lane group (slots are independent)
     unsigned long long was_free = 0ull;
-    for (int c = 0; c < W.C; ++c) {
-        if (W.pair(c) < 0) was_free |= 1ull << c;
+    for (int c = W.sub; c < W.C; c += W.G) {
+        if (W.pair(c) < 0) {
+            was_free |= 1ull << c;
+        } else {
+            const int ca = W.ba(c), cb = W.bb(c);
+            if (((moved >> ca) & 1ull) || ((moved >> cb) & 1ull)) W.set_tflag(c, 0);
+        }
+        // FindNewContacts; a slot that received a new contact starts with fresh TOI state. The keys before it go
+        // to the workspace's corder array, which Solve's island order no longer needs.
         W.corder(c) = W.key(c);
     }
+    was_free = group_or(W.grp(), was_free);
+    group_sync();
     find_new_contacts(m, W, W.i32(GOI_S_OVERFLOW, 0) == 0 ? refat : ~0ull);
-    for (int c = 0; c < W.C; ++c) {
+    for (int c = W.sub; c < W.C; c += W.G) {
         if (W.pair(c) >= 0 && (((was_free >> c) & 1ull) || W.corder(c) != W.key(c))) {
             W.set_tcount(c, 0);
             W.set_tflag(c, 0);
             W.set_ten(c, 1);
         }
     }
+    group_sync();
 }
 
 // b2World::SolveTOI (toi.py:827-865). Called by every lane of the block (the reset, the TOI searches and the final
