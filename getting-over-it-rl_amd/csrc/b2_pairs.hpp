@@ -16,6 +16,17 @@ constexpr int kMaxC = 64;
 // Live slots in contact-list order: W.order(0 .. n-1); returns n.
 GOI_D int list_order(const World& W) { return W.nlive(); }
 
+// The list positions i < n (n <= 64) whose slot W.order(i) satisfies pred(slot), as a bit mask: the lane group tests
+// them together; a walk then visits the set bits in list order. pred must not depend on what that walk changes for
+// the other positions.
+template <class F>
+GOI_D unsigned long long list_mask(const World& W, int n, F&& pred) {
+    unsigned long long mk = 0ull;
+    for (int i = W.sub; i < n; i += W.G)
+        if (pred(W.order(i))) mk |= 1ull << i;
+    return group_or(W.grp(), mk);
+}
+
 // b2Contact::Update's manifold part: new manifold, impulses carried over from the first old point with the same
 // feature key, touching flag (pairs.py:56-83). Returns whether touching flipped.
 GOI_D bool contact_update(const World& W, int k, const Manifold& mf) {

@@ -71,11 +71,14 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
             const int b = W.stack(--sp);
             I.body_island(b) = isl;
             W.wake(b);
-            for (int i = 0; i < n; ++i) {
-                const int c = W.order(i);
+            // b's touching contacts not yet in an island, newest first (the walk below marks only the contact it
+            // visits, so the mask of the others stays exact)
+            const unsigned long long hits = list_mask(W, n, [&](int c) {
+                return (W.ba(c) == b || W.bb(c) == b) && !((cflag >> c) & 1ull) && W.touching(c);
+            });
+            for (unsigned long long left = hits; left; left &= left - 1) {
+                const int c = W.order(__builtin_ctzll(left));
                 const int ba = W.ba(c), bb = W.bb(c);
-                if (ba != b && bb != b) continue;
-                if (((cflag >> c) & 1ull) || !W.touching(c)) continue;
                 I.corder(nc++) = c;
                 cflag |= 1ull << c;
                 I.contact_island(c) = isl;

@@ -291,17 +291,29 @@ GOI_D void toi_task(const DModel& m, const Coop& co, int o, int i, float linear_
 // pass 3; returns whether an event was found
 GOI_D bool toi_search_pick(const World& W, const GoiSettings& s, int& min_slot, float& min_alpha) {
     const int n = list_order(W);
-    int best = -1;
+    // the list walk's running minimum, over the lane group: each lane walks its own positions, then the lanes combine
+    // (smaller alpha wins; equal alphas keep the earlier position, or the later one under toi_tie_oldest)
+    int at = -1;
     float best_alpha = 1.0f;
-    for (int i = 0; i < n; ++i) {
+    for (int i = W.sub; i < n; i += W.G) {
         const int c = W.order(i);
         if (!W.ten(c) || W.tcount(c) > kMaxSubSteps || !W.tflag(c)) continue;
         const float alpha = W.ttoi(c);
         if (alpha < 1.0f && (s.toi_tie_oldest ? alpha <= best_alpha : alpha < best_alpha)) {
-            best = c;
+            at = i;
             best_alpha = alpha;
         }
     }
+    for (int d = 1; d < W.G; d <<= 1) {
+        const float oa = __shfl_xor(best_alpha, d, 64);
+        const int oi = __shfl_xor(at, d, 64);
+        const bool later = oi > at;
+        if (oi >= 0 && (oa < best_alpha || (oa == best_alpha && (at < 0 || (s.toi_tie_oldest ? later : !later))))) {
+            best_alpha = oa;
+            at = oi;
+        }
+    }
+    const int best = at >= 0 ? W.order(at) : -1;
     min_slot = best;
     min_alpha = best_alpha;
     const float done_alpha = 1.0f - 10.0f * kEps;
@@ -355,10 +367,11 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     for (int pi = 0; pi < 2; ++pi) {
         const int body = pi == 0 ? A : Bb;
         if (!W.is_dynamic(body)) continue;
-        for (int i = 0; i < n; ++i) {
-            const int c = W.order(i);
+        // the contacts of `body` in list order (found by the lane group together)
+        const unsigned long long hits = list_mask(W, n, [&](int c) { return W.ba(c) == body || W.bb(c) == body; });
+        for (unsigned long long left = hits; left; left &= left - 1) {
+            const int c = W.order(__builtin_ctzll(left));
             const int ca = W.ba(c), cb = W.bb(c);
-            if (ca != body && cb != body) continue;
             if (nb == 2 * kMaxToiContacts || nc == kMaxToiContacts) break;
             if ((cflag >> c) & 1ull) continue;
             const int other = ca == body ? cb : ca;
