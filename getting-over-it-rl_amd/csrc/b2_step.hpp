@@ -320,14 +320,15 @@ GOI_D bool toi_search_pick(const World& W, const GoiSettings& s, int& min_slot, 
     return best >= 0 && !(done_alpha < best_alpha);
 }
 
-// position-constraint fields of contact slot `slot` into row i (the TOI island's b2ContactPositionConstraint)
-GOI_D void cs_position_row(const DModel& m, const World& W, const Rows& R, int i, int slot) {
+// position-constraint fields of contact slot `slot` into row i (the TOI island's b2ContactPositionConstraint); mf is
+// the touching manifold the slot was just updated with (its State leaves hold the same values)
+GOI_D void cs_position_row(const DModel& m, const World& W, const Rows& R, int i, int slot, const Manifold& mf) {
     const int fa = W.fa(slot), fb = W.fb(slot);
     const int ia = W.ba(slot), ib = W.bb(slot);
     R.seti(i, CF_SLOT, slot); R.seti(i, CF_IA, ia); R.seti(i, CF_IB, ib);
-    R.seti(i, CF_PC_COUNT, W.ccount(slot)); R.seti(i, CF_MTYPE, W.i32(GOI_C_MTYPE, slot));
-    R.set2(i, CF_LN, W.v2(GOI_C_LOCAL_NORMAL, slot)); R.set2(i, CF_LP, W.v2(GOI_C_LOCAL_POINT, slot));
-    R.set2(i, CF_PL0, W.v2(GOI_C_POINT_LOCAL, 2 * slot)); R.set2(i, CF_PL1, W.v2(GOI_C_POINT_LOCAL, 2 * slot + 1));
+    R.seti(i, CF_PC_COUNT, mf.count); R.seti(i, CF_MTYPE, mf.mtype);
+    R.set2(i, CF_LN, mf.ln); R.set2(i, CF_LP, mf.lp);
+    R.set2(i, CF_PL0, mf.pl0); R.set2(i, CF_PL1, mf.pl1);
     R.set2(i, CF_LCA, W.v2(GOI_B_LOCAL_CENTER, ia)); R.set2(i, CF_LCB, W.v2(GOI_B_LOCAL_CENTER, ib));
     R.setf(i, CF_RADA, m.radius[fa]); R.setf(i, CF_RADB, m.radius[fb]);
 }
@@ -340,11 +341,9 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     const SweepBackup bkA = backup(W, A), bkB = backup(W, Bb);
     body_advance(W, A, min_alpha);
     body_advance(W, Bb, min_alpha);
-    {
-        Manifold mf;
-        evaluate(m, fa, fb, W.xf(A), W.xf(Bb), s, mf, W.grp());
-        if (contact_update(W, min_slot, mf)) { W.wake(A); W.wake(Bb); }
-    }
+    Manifold mf0;
+    evaluate(m, fa, fb, W.xf(A), W.xf(Bb), s, mf0, W.grp());
+    if (contact_update(W, min_slot, mf0)) { W.wake(A); W.wake(Bb); }
     W.set_tflag(min_slot, 0);
     W.set_tcount(min_slot, W.tcount(min_slot) + 1);
     if (!W.touching(min_slot)) {
@@ -362,7 +361,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     unsigned long long bflag = (1ull << A) | (1ull << Bb), cflag = 1ull << min_slot;
     W.ibuf(nb++) = A;
     W.ibuf(nb++) = Bb;
-    cs_position_row(m, W, CR, nc++, min_slot);
+    cs_position_row(m, W, CR, nc++, min_slot, mf0);
     const int n = list_order(W);
     for (int pi = 0; pi < 2; ++pi) {
         const int body = pi == 0 ? A : Bb;
@@ -388,7 +387,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
                 continue;
             }
             cflag |= 1ull << c;
-            cs_position_row(m, W, CR, nc++, c);
+            cs_position_row(m, W, CR, nc++, c, mf);
             if ((bflag >> other) & 1ull) continue;
             bflag |= 1ull << other;
             if (!W.is_static(other)) W.wake(other);
