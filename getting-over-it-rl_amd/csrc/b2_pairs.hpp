@@ -86,11 +86,7 @@ struct Coop {
         W.G = 1;
         return W;
     }
-    GOI_D Rows task_rows(int o) const {
-        Rows R;
-        R.base = rows; R.pitch = base.pitch; R.w = w0 + o; R.nf = CF_N;
-        return R;
-    }
+    GOI_D Rows task_rows(int o) const { return rows_of(rows, base.C, CF_N, base.S, w0 / base.S, o); }
 };
 
 // Called by all lanes of the block together; `my` = this lane's task count: the world's count on the first lane of

@@ -4,8 +4,8 @@
 // early exit, transform sync, sleeping, fixture sync and FindNewContacts.
 //
 // Storage: the solver's body arrays (v, w, c, a per body) live in LDS as [field][body][lane] so each lane's random
-// body index hits its own bank; the prepared constraint rows live in a per-world HBM scratch laid out
-// [row][field][pitch] (one coalesced 256-byte segment per field per wavefront).
+// body index hits its own bank; the prepared constraint rows live in HBM scratch tiles, one per block
+// ([row][field][world of the block]: a row's fields for the block's worlds are contiguous).
 #pragma once
 
 #include "b2_pairs.hpp"

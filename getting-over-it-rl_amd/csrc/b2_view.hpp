@@ -436,13 +436,15 @@ GOI_D bool overlap(float4 a, float4 b) {
     return !(d1x > 0.0f || d1y > 0.0f || d2x > 0.0f || d2y > 0.0f);
 }
 
-// Per-world HBM scratch rows: element (row, field) at base[((row * nf) + field) * pitch + w], a 32-bit word offset
-// (checked at launch).
+// Per-world HBM scratch rows, in tiles: the S worlds of a block share one tile of nrows x nf x S words, and element
+// (row, field) of the block's world `lane` is tile[(row * nf + field) * S + lane]. A row's fields for the block's
+// worlds are contiguous (one row is a few 128-byte lines, not one line per field), and the field offsets fold into the
+// load and store instructions. Word offsets fit 32 bits (checked at launch).
 struct Rows {
-    uint32_t* base;
-    int pitch, w, nf;
+    uint32_t* base;  // the tile's word 0 of this world
+    int nf, S;
     GOI_D uint32_t& u(int row, int field) const {
-        return base[((uint32_t)row * (uint32_t)nf + (uint32_t)field) * (uint32_t)pitch + (uint32_t)w];
+        return base[((uint32_t)row * (uint32_t)nf + (uint32_t)field) * (uint32_t)S];
     }
     GOI_D float getf(int row, int field) const { return __uint_as_float(u(row, field)); }
     GOI_D void setf(int row, int field, float v) const { u(row, field) = __float_as_uint(v); }
@@ -451,6 +453,14 @@ struct Rows {
     GOI_D V2 get2(int row, int field) const { return mk(getf(row, field), getf(row, field + 1)); }
     GOI_D void set2(int row, int field, V2 v) const { setf(row, field, v.x); setf(row, field + 1, v.y); }
 };
+// The rows of world `lane` of tile `tile` in a region of tiles of nrows x nf x S words.
+GOI_D Rows rows_of(uint32_t* region, int nrows, int nf, int S, int tile, int lane) {
+    Rows R;
+    R.base = region + (size_t)tile * ((size_t)nrows * nf * S) + lane;
+    R.nf = nf;
+    R.S = S;
+    return R;
+}
 
 // contact constraint row fields
 enum {

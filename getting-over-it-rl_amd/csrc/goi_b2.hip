@@ -1,13 +1,16 @@
 // goi_b2.hip - the MI355X batched Box2D 2.3.1 world step (libgoi_b2.so) and its C ABI (include/goi_b2.h).
 //
-// Execution model: one lane per world; a step is one launch (k_step) over ceil(N / 64) wavefronts of 64 lanes:
+// Execution model: a step is one launch (k_step) of 64-lane wavefronts, each stepping S worlds; each world runs on a
+// group of 64 / S lanes (8 lanes at 16384 worlds) that execute its sequential code together and split its
+// independent loops (vertex, slot, body and row loops, list filters):
 //   start-of-step FindNewContacts where new_fixture, then Collide           (step.py:30-35, pairs.py:38-178)
 //   b2World::Solve: islands, solver, sleep, fixture sync, FindNewContacts   (step.py:73-182)
 //   b2World::SolveTOI's event loop, then inv_dt0 and ClearForces             (toi.py:827-865, step.py:41-46)
-// goi_collide launches k_collide (the first part only). Box2D's sequential orders inside a world (contact list newest first, island DFS, Gauss-Seidel sweeps, TOI events)
-// are kept exactly; the parallelism is across worlds. State leaves are read and written in place in the
+// goi_collide launches k_collide (the first part only). Box2D's sequential orders inside a world (contact list
+// newest first, island DFS, Gauss-Seidel sweeps, TOI events) are kept exactly; the parallelism is across worlds and
+// within the independent parts of a world's work. State leaves are read and written in place in the
 // worlds-minor layout; the solver's body arrays sit in LDS ([field][body][lane]), its constraint rows in a
-// per-world HBM scratch ([row][field][pitch]); the static terrain is a BVH over the static fixtures' fat AABBs,
+// per-block HBM scratch tile ([row][field][world]); the static terrain is a BVH over the static fixtures' fat AABBs,
 // shared by every world and read through L2.
 #include <hip/hip_runtime.h>
 
@@ -91,21 +94,14 @@ __device__ __forceinline__ void stage_nodes(const DModel& m, const Launch& L, in
     __syncthreads();
 }
 
-__device__ __forceinline__ Rows contact_rows(const Launch& L, int w) {
-    Rows R;
-    R.base = L.scratch;
-    R.pitch = L.pitch;
-    R.w = w;
-    R.nf = CF_N;
-    return R;
+// The scratch rows of world w0 + wl of this block (tile = the block's world group): the contact rows' tiles, then
+// the joint rows' tiles, each region gridDim.x tiles long.
+__device__ __forceinline__ Rows contact_rows(const Launch& L, int w0, int wl) {
+    return rows_of(L.scratch, L.C, CF_N, L.wpw, w0 / L.wpw, wl);
 }
-__device__ __forceinline__ Rows joint_rows(const Launch& L, int w) {
-    Rows R;
-    R.base = L.scratch + (size_t)L.C * CF_N * L.pitch;
-    R.pitch = L.pitch;
-    R.w = w;
-    R.nf = JF_N;
-    return R;
+__device__ __forceinline__ Rows joint_rows(const Launch& L, int w0, int wl) {
+    uint32_t* region = L.scratch + (size_t)L.C * CF_N * ((size_t)gridDim.x * L.wpw);
+    return rows_of(region, L.J, JF_N, L.wpw, w0 / L.wpw, wl);
 }
 
 // ---------------------------------------------------------------- kernels
@@ -193,7 +189,7 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     bd.s = reinterpret_cast<float*>(lds) + W.k.o_body * W.S + (valid ? lm.wl : 0);
     bd.B = L.B;
     bd.st = W.S;
-    const Rows CR = contact_rows(L, W.w);
+    const Rows CR = contact_rows(L, w0, valid ? lm.wl : 0);
     const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
     load_mirror_block(m, bc);
     // n_steps consecutive steps: the workspace mirror stays in LDS from one to the next (it is the State's current
@@ -208,7 +204,7 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
             W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
         }
         collide_block(m, co, W, valid, lm.leader, L.s);
-        if (valid) solve_world(m, W, bd, CR, joint_rows(L, W.w), L.s, L.dt, L.dbg);
+        if (valid) solve_world(m, W, bd, CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
         if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, lm.leader, co, bc);
         if (valid) {
             const float dt = L.dt;
@@ -579,7 +575,7 @@ static int check_view(const GoiModel* M, const GoiStateView* v, const char* who)
     // the kernels address leaf elements and scratch-row words with 32-bit offsets
     const uint64_t per_world = std::max<uint64_t>({4ull * v->C, 4ull * v->R, 3ull * v->J, 2ull * v->B, 1ull});
     const uint64_t row_words = (uint64_t)v->C * CF_N + (uint64_t)v->J * JF_N;
-    if (per_world * (uint64_t)v->pitch >= (1ull << 32) || row_words * (uint64_t)v->pitch >= (1ull << 32))
+    if (per_world * (uint64_t)v->pitch >= (1ull << 32) || row_words * ((uint64_t)v->pitch + 64) >= (1ull << 32))
         return fail(GOI_E_UNSUPPORTED, std::string(who) + ": pitch too large for 32-bit element offsets");
     return GOI_OK;
 }
@@ -656,7 +652,8 @@ static void fill_launch(Launch& L, const GoiModel* M, const GoiStateView* v, con
 
 // The model's scratch rows (per world: C contact rows, J joint rows), grown to the batch's pitch on demand.
 static int ensure_scratch(GoiModel* M, const GoiStateView* state) {
-    const size_t words = ((size_t)state->C * CF_N + (size_t)state->J * JF_N) * state->pitch;
+    // tiles of wpw worlds: at most pitch + 63 world columns (the kernels' 32-bit offsets are checked at launch)
+    const size_t words = ((size_t)state->C * CF_N + (size_t)state->J * JF_N) * ((size_t)state->pitch + 64);
     if (words > M->scratch_words) {
         if (M->scratch) HIP_TRY(hipFree(M->scratch));
         M->scratch = nullptr;
