@@ -339,10 +339,14 @@ GOI_D void store_vimpulses(const Rows& R, int i, const VRow& r) {
 
 // rows 0..n-1 once each, in order, each loaded in one batch
 GOI_D void cs_solve_velocity_sweep(const Bodies& bd, const Rows& R, int n) {
+    if (n <= 0) return;
+    VRow r = load_vrow(R, 0);
     for (int i = 0; i < n; ++i) {
-        VRow r = load_vrow(R, i);
+        VRow next;
+        if (i + 1 < n) next = load_vrow(R, i + 1);  // in flight while row i is solved
         solve_vrow(bd, r);
         store_vimpulses(R, i, r);
+        r = next;
     }
 }
 
