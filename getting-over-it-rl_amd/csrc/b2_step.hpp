@@ -419,11 +419,12 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     // leap of faith: the TOI pair's sweep start is the solved pose
     W.set2(GOI_B_C0, A, bd.c(A)); W.f(GOI_B_A0, A) = bd.a(A);
     W.set2(GOI_B_C0, Bb, bd.c(Bb)); W.f(GOI_B_A0, Bb) = bd.a(Bb);
-    for (int i = 0; i < nc; ++i) {
+    for (int i = W.sub; i < nc; i += W.G) {  // independent rows, one per lane of the group
         const int slot = CR.geti(i, CF_SLOT);
         const int ia = CR.geti(i, CF_IA), ib = CR.geti(i, CF_IB);
         cs_prepare(m, W, bd, CR, i, slot, false, 1.0f, rot_of(bd.a(ia)), rot_of(bd.a(ib)), s.velocity_threshold);
     }
+    group_sync();
     for (int it = 0; it < s.velocity_iterations; ++it) cs_solve_velocity_sweep(bd, CR, nc);
     const float h = (1.0f - min_alpha) * dt;
     const float max_t = s.clamps_per_second ? s.max_translation * dt : s.max_translation;
