@@ -343,20 +343,33 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
 }
 
 // b2Fixture::ComputeAABB for fixture f at transform t
-GOI_D float4 shape_aabb(const DModel& m, int f, const Xf& t) {
+// b2Shape::ComputeAABB of fixture f under transforms t1 and t2 (a1, a2). The fixture's vertex slots (all kPoly of
+// them: the Model pads every shape) load in one batch with its type, count and radius.
+GOI_D void shape_aabb2(const DModel& m, int f, const Xf& t1, const Xf& t2, float4& a1, float4& a2) {
     const float r = m.radius[f];
-    if (m.shape_type[f] == GOI_CIRCLE) {
-        const V2 p = t.p + mul(t.q, mvert(m, f, 0));
-        return make_float4(p.x - r, p.y - r, p.x + r, p.y + r);
+    const int type = m.shape_type[f], n = m.count[f];
+    V2 vs[kPoly];
+#pragma unroll
+    for (int i = 0; i < kPoly; ++i) vs[i] = mvert(m, f, i);
+    if (type == GOI_CIRCLE) {
+        const V2 p1 = t1.p + mul(t1.q, vs[0]), p2 = t2.p + mul(t2.q, vs[0]);
+        a1 = make_float4(p1.x - r, p1.y - r, p1.x + r, p1.y + r);
+        a2 = make_float4(p2.x - r, p2.y - r, p2.x + r, p2.y + r);
+        return;
     }
-    V2 lo = mul(t, mvert(m, f, 0)), hi = lo;
-    const int n = m.count[f];
-    for (int i = 1; i < n; ++i) {
-        const V2 v = mul(t, mvert(m, f, i));
-        lo.x = bmin(lo.x, v.x); lo.y = bmin(lo.y, v.y);
-        hi.x = bmax(hi.x, v.x); hi.y = bmax(hi.y, v.y);
+    V2 lo1 = mul(t1, vs[0]), hi1 = lo1, lo2 = mul(t2, vs[0]), hi2 = lo2;
+#pragma unroll
+    for (int i = 1; i < kPoly; ++i) {
+        if (i < n) {
+            const V2 v1 = mul(t1, vs[i]), v2 = mul(t2, vs[i]);
+            lo1.x = bmin(lo1.x, v1.x); lo1.y = bmin(lo1.y, v1.y);
+            hi1.x = bmax(hi1.x, v1.x); hi1.y = bmax(hi1.y, v1.y);
+            lo2.x = bmin(lo2.x, v2.x); lo2.y = bmin(lo2.y, v2.y);
+            hi2.x = bmax(hi2.x, v2.x); hi2.y = bmax(hi2.y, v2.y);
+        }
     }
-    return make_float4(lo.x - r, lo.y - r, hi.x + r, hi.y + r);
+    a1 = make_float4(lo1.x - r, lo1.y - r, hi1.x + r, hi1.y + r);
+    a2 = make_float4(lo2.x - r, lo2.y - r, hi2.x + r, hi2.y + r);
 }
 
 // b2Body::SynchronizeFixtures for body b (pairs.py:181-207): swept AABB over the sweep start and the current
@@ -368,7 +381,8 @@ GOI_D unsigned long long sync_body_fixtures(const DModel& m, const World& W, int
     for (int r = 0; r < m.R; ++r) {
         if (m.row_body[r] != b) continue;
         const int f = m.slot_fixture[r];
-        const float4 a1 = shape_aabb(m, f, x1), a2 = shape_aabb(m, f, x2);
+        float4 a1, a2;
+        shape_aabb2(m, f, x1, x2, a1, a2);
         float lx = bmin(a1.x, a2.x), ly = bmin(a1.y, a2.y);
         float ux = bmax(a1.z, a2.z), uy = bmax(a1.w, a2.w);
         const float fx0 = W.f(GOI_F_FAT, 4 * r), fy0 = W.f(GOI_F_FAT, 4 * r + 1);
