@@ -72,9 +72,14 @@ GOI_D float fsqrt(float a) { return sqrtf(a); }  // IEEE sqrt under -fhip-fp32-c
 // Evaluated on the FP64 units: the double result is within an ulp of the exact value, so rounding it to float gives
 // the correctly rounded float except when sin x lies within ~2^-53 relative of a float rounding boundary.
 GOI_D Rot rot_of(float a) {
+    Rot q;
+    if (a == 0.0f) {  // a static body at its rest angle, the common case; sin(+-0) = +-0, cos = 1
+        q.s = a;
+        q.c = 1.0f;
+        return q;
+    }
     double s, c;
     sincos((double)a, &s, &c);
-    Rot q;
     q.s = (float)s;
     q.c = (float)c;
     return q;
