@@ -425,7 +425,20 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         cs_prepare(m, W, bd, CR, i, slot, false, 1.0f, rot_of(bd.a(ia)), rot_of(bd.a(ib)), s.velocity_threshold);
     }
     group_sync();
-    for (int it = 0; it < s.velocity_iterations; ++it) cs_solve_velocity_sweep(bd, CR, nc);
+    {
+        // row 0 (the TOI contact, which every island has) stays in registers through the passes; most islands have
+        // no other row
+        VRow r0 = load_vrow(CR, 0);
+        for (int it = 0; it < s.velocity_iterations; ++it) {
+            solve_vrow(bd, r0);
+            for (int i = 1; i < nc; ++i) {
+                VRow r = load_vrow(CR, i);
+                solve_vrow(bd, r);
+                store_vimpulses(CR, i, r);
+            }
+        }
+        store_vimpulses(CR, 0, r0);
+    }
     const float h = (1.0f - min_alpha) * dt;
     const float max_t = s.clamps_per_second ? s.max_translation * dt : s.max_translation;
     const float max_r = s.clamps_per_second ? s.max_rotation * dt : s.max_rotation;
