@@ -128,17 +128,24 @@ static_assert(MT_N <= CF_N, "a manifold must fit a contact row");
 // (W.cisl(k) = task index, or -1), the block evaluates all their manifolds (coop_run), and each world walks its list
 // with the wake cascade, taking the precomputed manifold of each contact it updates. A contact the walk skips (both
 // bodies asleep) had its manifold evaluated for nothing, which changes no result.
+// The overlap tests split over the lane group; a contact's task index is the number of overlapping contacts before
+// it in the list.
 GOI_D int collide_mark(const DModel& m, const World& W) {
     const int n = list_order(W);
-    int nt = 0;
-    for (int i = 0; i < n; ++i) {
+    const unsigned long long hits =
+        list_mask(W, n, [&](int k) { return overlap(fat_of(m, W, W.fa(k)), fat_of(m, W, W.fb(k))); });
+    for (int i = W.sub; i < n; i += W.G) {
         const int k = W.order(i);
-        W.cisl(k) = -1;
-        if (!overlap(fat_of(m, W, W.fa(k)), fat_of(m, W, W.fb(k)))) continue;
-        W.newp(nt) = k;
-        W.cisl(k) = nt++;
+        if ((hits >> i) & 1ull) {
+            const int t = __popcll(hits & ((1ull << i) - 1ull));
+            W.newp(t) = k;
+            W.cisl(k) = t;
+        } else {
+            W.cisl(k) = -1;
+        }
     }
-    return nt;
+    group_sync();
+    return __popcll(hits);
 }
 
 GOI_D void collide_task(const DModel& m, const Coop& co, int o, int i, const GoiSettings& s) {
