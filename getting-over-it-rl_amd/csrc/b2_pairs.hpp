@@ -167,19 +167,42 @@ GOI_D void collide_task(const DModel& m, const Coop& co, int o, int i, const Goi
 
 GOI_D void collide_apply(const DModel& m, const World& W, const Rows& R) {
     const int n = list_order(W);
+    // 1. per list position (split over the lane group): the contact is destroyed (its fat boxes separated), and
+    //    visiting it wakes its bodies (a destroyed contact that had points; an update that flips touching)
+    unsigned long long gone = 0ull, wakes = 0ull;
+    for (int i = W.sub; i < n; i += W.G) {
+        const int k = W.order(i);
+        const int t = W.cisl(k);
+        const bool g = t < 0;
+        const bool wk = g ? W.ccount(k) > 0 : (R.geti(t, MT_COUNT) > 0) != W.touching(k);
+        gone |= (unsigned long long)g << i;
+        wakes |= (unsigned long long)wk << i;
+    }
+    gone = group_or(W.grp(), gone);
+    wakes = group_or(W.grp(), wakes);
+    // 2. Box2D's walk with its wake cascade, on bit masks: a contact is visited when one of its bodies is awake and
+    //    not static, and a visit that wakes makes both bodies awake for the rest of the walk
+    unsigned long long awake = 0ull, visit = 0ull;
+    for (int b = 0; b < W.B; ++b) awake |= (unsigned long long)(W.awake(b) != 0) << b;
+    const unsigned long long woken0 = awake;
     for (int i = 0; i < n; ++i) {
         const int k = W.order(i);
-        const int ba = W.ba(k), bb = W.bb(k);
-        const bool act_a = W.awake(ba) && !W.is_static(ba);
-        const bool act_b = W.awake(bb) && !W.is_static(bb);
-        if (!act_a && !act_b) continue;
-        const int t = W.cisl(k);
-        if (t < 0) {
-            if (W.ccount(k) > 0) { W.wake(ba); W.wake(bb); }
+        const unsigned long long pair = (1ull << W.ba(k)) | (1ull << W.bb(k));
+        if (!(awake & pair & ~W.smask)) continue;
+        visit |= 1ull << i;
+        if ((wakes >> i) & 1ull) awake |= pair;
+    }
+    // 3. the visited contacts' destructions and updates (each touches only its own slot), split over the group, then
+    //    the wakes (b2Body::SetAwake restarts the sleep timer only of a body that was asleep)
+    for (int i = W.sub; i < n; i += W.G) {
+        if (!((visit >> i) & 1ull)) continue;
+        const int k = W.order(i);
+        if ((gone >> i) & 1ull) {
             W.pair(k) = -1;
             W.set_touch_count(k, false, 0);
             continue;
         }
+        const int t = W.cisl(k);
         Manifold mf;
         mf.mtype = R.geti(t, MT_MTYPE);
         mf.count = R.geti(t, MT_COUNT);
@@ -189,15 +212,21 @@ GOI_D void collide_apply(const DModel& m, const World& W, const Rows& R) {
         mf.pl1 = R.get2(t, MT_PL1);
         mf.id0 = R.geti(t, MT_ID0);
         mf.id1 = R.geti(t, MT_ID1);
-        if (contact_update(W, k, mf)) { W.wake(ba); W.wake(bb); }
+        contact_update(W, k, mf);
     }
-    // drop the destroyed contacts from the list, keeping the order of the rest
-    int j = 0;
-    for (int i = 0; i < n; ++i) {
+    for (int b = W.sub; b < W.B; b += W.G)
+        if (((awake & ~woken0) >> b) & 1ull) W.wake(b);
+    group_sync();
+    // 4. the destroyed contacts leave the list, the rest keep their order (a position moves only down, below every
+    //    position the group has yet to read)
+    const unsigned long long dead = visit & gone;
+    for (int i = W.sub; i < n; i += W.G) {
+        if ((dead >> i) & 1ull) continue;
         const int k = W.order(i);
-        if (W.pair(k) >= 0) W.order(j++) = k;
+        W.order(i - __popcll(dead & ((1ull << i) - 1ull))) = k;
     }
-    W.nlive() = j;
+    group_sync();
+    W.nlive() = n - __popcll(dead);
 }
 
 // Collide for the block: called by all lanes together; `valid` marks the lanes that run a world, `leader` the first
