@@ -15,7 +15,7 @@ GOI_D void set_jcol(const Rows& R, int i, int f, V3 v) { R.setf(i, f, v.x); R.se
 // InitVelocityConstraints minus the velocity writes (joints.py:61-174): row i for joint jid.
 GOI_D void jn_prepare(const DModel& m, const World& W, const Bodies& bd, const Rows& R, int i, int jid,
                       const GoiSettings& s, float dt, float dt_ratio, bool warm, Rot qA, Rot qB) {
-    const int type = m.joint_type[jid];
+    const int type = m.rev_only ? (int)GOI_REVOLUTE : m.joint_type[jid];
     const int ia = m.joint_a[jid], ib = m.joint_b[jid];
     const float mA = W.f(GOI_B_INV_MASS, ia), mB = W.f(GOI_B_INV_MASS, ib);
     const float iA = W.f(GOI_B_INV_INERTIA, ia), iB = W.f(GOI_B_INV_INERTIA, ib);
@@ -142,8 +142,8 @@ GOI_D void jn_prepare(const DModel& m, const World& W, const Bodies& bd, const R
 }
 
 // the velocity part of InitVelocityConstraints (joints.py:202-248)
-GOI_D void jn_warm_start(const Bodies& bd, const Rows& R, int i, bool v24) {
-    const int type = R.geti(i, JF_TYPE), ia = R.geti(i, JF_IA), ib = R.geti(i, JF_IB);
+GOI_D void jn_warm_start(const Bodies& bd, const Rows& R, int i, bool v24, bool rev_only) {
+    const int type = rev_only ? (int)GOI_REVOLUTE : R.geti(i, JF_TYPE), ia = R.geti(i, JF_IA), ib = R.geti(i, JF_IB);
     const float mA = R.getf(i, JF_MA), mB = R.getf(i, JF_MB), iA = R.getf(i, JF_IIA), iB = R.getf(i, JF_IIB);
     const float ix = R.getf(i, JF_IMP0), iy = R.getf(i, JF_IMP1), iz = R.getf(i, JF_IMP2), mi = R.getf(i, JF_MIMP);
     V2 vA = bd.v(ia), vB = bd.v(ib);
@@ -177,8 +177,8 @@ GOI_D void jn_warm_start(const Bodies& bd, const Rows& R, int i, bool v24) {
 }
 
 // SolveVelocityConstraints for joint row i (joints.py:257-437, revolute24.patch:166-240)
-GOI_D void jn_solve_velocity(const Bodies& bd, const Rows& R, int i, bool v24) {
-    const int type = R.geti(i, JF_TYPE), ia = R.geti(i, JF_IA), ib = R.geti(i, JF_IB);
+GOI_D void jn_solve_velocity(const Bodies& bd, const Rows& R, int i, bool v24, bool rev_only) {
+    const int type = rev_only ? (int)GOI_REVOLUTE : R.geti(i, JF_TYPE), ia = R.geti(i, JF_IA), ib = R.geti(i, JF_IB);
     const float mA = R.getf(i, JF_MA), mB = R.getf(i, JF_MB), iA = R.getf(i, JF_IIA), iB = R.getf(i, JF_IIB);
     const bool emotor = R.geti(i, JF_EMOTOR) != 0, elimit = R.geti(i, JF_ELIMIT) != 0;
     const int st = R.geti(i, JF_STATE);
@@ -343,8 +343,8 @@ GOI_D bool rev_point(float mA, float mB, float iA, float iB, V2 la, V2 lb, V2& c
 }
 
 // SolvePositionConstraints for joint row i (joints.py:462-606); returns the joint's ok flag
-GOI_D bool jn_solve_position(const Bodies& bd, const Rows& R, int i, const GoiSettings& s) {
-    const int type = R.geti(i, JF_TYPE), ia = R.geti(i, JF_IA), ib = R.geti(i, JF_IB);
+GOI_D bool jn_solve_position(const Bodies& bd, const Rows& R, int i, const GoiSettings& s, bool rev_only) {
+    const int type = rev_only ? (int)GOI_REVOLUTE : R.geti(i, JF_TYPE), ia = R.geti(i, JF_IA), ib = R.geti(i, JF_IB);
     const float mA = R.getf(i, JF_MA), mB = R.getf(i, JF_MB), iA = R.getf(i, JF_IIA), iB = R.getf(i, JF_IIB);
     const bool elimit = R.geti(i, JF_ELIMIT) != 0;
     const float lower = R.getf(i, JF_LOWER), upper = R.getf(i, JF_UPPER), ref = R.getf(i, JF_REF);

@@ -429,8 +429,8 @@ GOI_D void evaluate(const DModel& m, int fa, int fb, const Xf& xfa, const Xf& xf
     const int ta = m.shape_type[fa], tb = m.shape_type[fb];
     if (ta == GOI_POLYGON && tb == GOI_POLYGON) collide_polygons(m, fa, xfa, fb, xfb, s.linear_slop, out, g);
     else if (ta == GOI_POLYGON) collide_polygon_circle(m, fa, xfa, fb, xfb, out, g);
-    else if (ta == GOI_EDGE && tb == GOI_POLYGON) collide_edge_polygon(m, fa, xfa, fb, xfb, s, out);
-    else if (ta == GOI_EDGE) collide_edge_circle(m, fa, xfa, fb, xfb, out);
+    else if (!m.no_edges && ta == GOI_EDGE && tb == GOI_POLYGON) collide_edge_polygon(m, fa, xfa, fb, xfb, s, out);
+    else if (!m.no_edges && ta == GOI_EDGE) collide_edge_circle(m, fa, xfa, fb, xfb, out);
     else collide_circles(m, fa, xfa, fb, xfb, out);
 }
 GOI_D void evaluate(const DModel& m, int fa, int fb, const Xf& xfa, const Xf& xfb, const GoiSettings& s,

@@ -67,9 +67,9 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     group_sync();  // rows written by one lane of the group are read by all
     if (warm)
         for (int i = 0; i < I.nc; ++i) cs_warm_start(bd, CR, i);
-    for (int i = 0; i < I.nj; ++i) jn_warm_start(bd, JRw, i, v24);
+    for (int i = 0; i < I.nj; ++i) jn_warm_start(bd, JRw, i, v24, m.rev_only);
     for (int it = 0; it < s.velocity_iterations; ++it) {
-        for (int i = 0; i < I.nj; ++i) jn_solve_velocity(bd, JRw, i, v24);
+        for (int i = 0; i < I.nj; ++i) jn_solve_velocity(bd, JRw, i, v24, m.rev_only);
         cs_solve_velocity_sweep(bd, CR, I.nc);
     }
     // StoreImpulses (contact_solver.py:293-304)
@@ -119,7 +119,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         for (int i = 0; i < I.nj; ++i) {
             const int isl = I.joint_island(JRw.geti(i, JF_JID));
             if ((done >> isl) & 1ull) continue;
-            if (!jn_solve_position(bd, JRw, i, s)) jbad |= 1ull << isl;
+            if (!jn_solve_position(bd, JRw, i, s, m.rev_only)) jbad |= 1ull << isl;
         }
         const float okay_sep = -3.0f * s.linear_slop;
         for (int i = 0; i < I.n; ++i)

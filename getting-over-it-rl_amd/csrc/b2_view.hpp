@@ -38,6 +38,8 @@ struct DModel {
     const V2* centroid;         // [F] polygon centroids (edge-polygon contacts); zeros when the Model has no edges
     const int* edge_flags;      // [F] edge ghost flags; zeros when absent
     int any_toi_body;           // Model.toi_bodies has a set entry (or is absent)
+    int rev_only;               // every joint is revolute
+    int no_edges;               // no edge fixture
     // Static BVH over the static fixtures' fat AABBs, nodes in preorder (node 0 = root, a node's first child is the
     // next node). node_link.x = escape: the node after this node's subtree; node_link.y = -1 for an internal node,
     // (first << 3) | count for a leaf of `count` (<= 4) entries of leaf_fixture starting at `first`.

@@ -225,10 +225,14 @@ __global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) { step_b
 // The same step with the world dimensions and the worlds per wave fixed at compile time (the 4-body rig with 32
 // contact slots, 8 worlds per wave): every workspace offset and loop bound folds into the instructions, which
 // frees the scalar registers the runtime dimensions hold. The results are those of k_step.
-template <int kB, int kC, int kJ, int kR, int kS, bool kMulti>
+template <int kB, int kC, int kJ, int kR, int kS, bool kMulti, bool kPlain>
 __global__ void __launch_bounds__(kBlock, 2) k_step_fixed(DModel m, Launch L) {
     L.B = kB; L.C = kC; L.J = kJ; L.R = kR; L.wpw = kS;
     m.B = kB; m.J = kJ; m.R = kR;
+    if (kPlain) {  // a Model with revolute joints only and no edge shapes: the other joint and collider code drops out
+        m.rev_only = 1;
+        m.no_edges = 1;
+    }
     step_block<kMulti>(m, L);
 }
 constexpr int kRigB = 5, kRigC = 32, kRigJ = 3, kRigR = 4, kRigS = 8;
@@ -488,6 +492,9 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     if (desc->toi_bodies)
         for (int b = 0; b < B; ++b) any |= desc->toi_bodies[b] ? 1 : 0;
     d.any_toi_body = any;
+    d.rev_only = 1;
+    for (int j = 0; j < J; ++j) d.rev_only &= desc->joint_type[j] == GOI_REVOLUTE ? 1 : 0;
+    d.no_edges = any_edge ? 0 : 1;
     int rc = GOI_OK;
 #define UP(field, host, n) \
     if (rc == GOI_OK) rc = upload(M, host, (size_t)(n), d.field, st)
@@ -692,10 +699,15 @@ int32_t goi_step_n(const GoiModel* model, const GoiStateView* state, const GoiSe
     const bool rig = L.B == kRigB && L.C == kRigC && L.J == kRigJ && L.R == kRigR && L.wpw == kRigS &&
                      M->d.B == kRigB && M->d.J == kRigJ && M->d.R == kRigR;
     const dim3 g(grid), b(kBlock);
-    if (rig && n_steps == 1)
-        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, false>), g, b, lds, st, M->d, L);
+    const bool plain = M->d.rev_only && M->d.no_edges;
+    if (rig && n_steps == 1 && plain)
+        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, false, true>), g, b, lds, st, M->d, L);
+    else if (rig && n_steps == 1)
+        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, false, false>), g, b, lds, st, M->d, L);
+    else if (rig && plain)
+        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, true, true>), g, b, lds, st, M->d, L);
     else if (rig)
-        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, true>), g, b, lds, st, M->d, L);
+        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, true, false>), g, b, lds, st, M->d, L);
     else if (n_steps == 1)
         hipLaunchKernelGGL(k_step<false>, g, b, lds, st, M->d, L);
     else
