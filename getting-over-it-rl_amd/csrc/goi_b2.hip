@@ -229,9 +229,10 @@ template <int kB, int kC, int kJ, int kR, int kS, bool kMulti, bool kPlain>
 __global__ void __launch_bounds__(kBlock, 2) k_step_fixed(DModel m, Launch L) {
     L.B = kB; L.C = kC; L.J = kJ; L.R = kR; L.wpw = kS;
     m.B = kB; m.J = kJ; m.R = kR;
-    if (kPlain) {  // a Model with revolute joints only and no edge shapes: the other joint and collider code drops out
+    if (kPlain) {  // revolute joints only (the v2.4.1 solver), no edge shapes: the other joint and collider code drops out
         m.rev_only = 1;
         m.no_edges = 1;
+        L.s.revolute_v24 = 1;
     }
     step_block<kMulti>(m, L);
 }
@@ -699,7 +700,7 @@ int32_t goi_step_n(const GoiModel* model, const GoiStateView* state, const GoiSe
     const bool rig = L.B == kRigB && L.C == kRigC && L.J == kRigJ && L.R == kRigR && L.wpw == kRigS &&
                      M->d.B == kRigB && M->d.J == kRigJ && M->d.R == kRigR;
     const dim3 g(grid), b(kBlock);
-    const bool plain = M->d.rev_only && M->d.no_edges;
+    const bool plain = M->d.rev_only && M->d.no_edges && settings->revolute_v24;
     if (rig && n_steps == 1 && plain)
         hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, false, true>), g, b, lds, st, M->d, L);
     else if (rig && n_steps == 1)
