@@ -307,8 +307,9 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
             continue;
         }
         nd = ln.x;
-        // a leaf's entries (at most 4; the arrays are padded by 4) load together, then the cheap box tests run
-        // first and only a hit reads its candidate index
+        // a leaf's entries (at most 4; the arrays are padded by 4) load together and take the cheap union-box test;
+        // the few that pass are then tested row by row (one copy of that code, not one per entry), and only a hit
+        // reads its candidate index
         const int first = ln.y >> 3, cnt = ln.y & 7;
         float4 sf[4];
         int info[4];
@@ -317,13 +318,18 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
             sf[j] = m.leaf_fat[first + j];
             info[j] = m.leaf_info[first + j];
         }
+        unsigned hits = 0u;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (j >= cnt || !overlap(sf[j], U) || !W.active(info[j] & 0xffff)) continue;
+        for (int j = 0; j < 4; ++j)
+            if (j < cnt && overlap(sf[j], U) && W.active(info[j] & 0xffff)) hits |= 1u << j;
+        for (; hits; hits &= hits - 1u) {
+            const int j = __builtin_ctz(hits);
+            const float4 fj = m.leaf_fat[first + j];
+            const int ij = m.leaf_info[first + j];
             for (unsigned long long left = rows; left; left &= left - 1) {
                 const int r = __builtin_ctzll(left);
-                if (!overlap(sf[j], W.get_qbox(r))) continue;
-                if (!(m.row_dynamic[r] || (info[j] >> 16))) continue;
+                if (!overlap(fj, W.get_qbox(r))) continue;
+                if (!(m.row_dynamic[r] || (ij >> 16))) continue;
                 const int p = m.leaf_cand[(size_t)(first + j) * m.R + r];
                 if (p < 0 || slot_has_pair(W, p)) continue;
                 np.add(p);
