@@ -247,16 +247,20 @@ GOI_D void put_sweep(const Rows& R, int row, int f, const Sweep& sw) {
 // pass 1; returns the number of TOI tasks, whose slots are W.newp(0 .. n-1)
 GOI_D int toi_search_prepare(const DModel& m, const World& W, const Rows& CR, const GoiSettings& s) {
     const int n = list_order(W);
-    int nt = 0;
-    for (int i = 0; i < n; ++i) {
-        const int c = W.order(i);
-        if (!W.ten(c) || W.tcount(c) > kMaxSubSteps || W.tflag(c)) continue;
-        const int fa = W.fa(c), fb = W.fb(c);
+    // the contacts that need a TOI (the lane group tests them together; the walk below changes only the flag of the
+    // contact it visits), then the alignments in list order
+    const unsigned long long need = list_mask(W, n, [&](int c) {
+        if (!W.ten(c) || W.tcount(c) > kMaxSubSteps || W.tflag(c)) return false;
         const int A = W.ba(c), Bb = W.bb(c);
         const bool act_a = W.awake(A) && !W.is_static(A);
         const bool act_b = W.awake(Bb) && !W.is_static(Bb);
-        if (!act_a && !act_b) continue;
-        if (!pair_rule(m, W, s, A, Bb)) continue;
+        return (act_a || act_b) && pair_rule(m, W, s, A, Bb);
+    });
+    int nt = 0;
+    for (unsigned long long left = need; left; left &= left - 1) {
+        const int c = W.order(__builtin_ctzll(left));
+        const int fa = W.fa(c), fb = W.fb(c);
+        const int A = W.ba(c), Bb = W.bb(c);
         const float alA = W.f(GOI_T_ALPHA0, A), alB = W.f(GOI_T_ALPHA0, Bb);
         float alpha0 = alA;
         if (alA < alB) { alpha0 = alB; sweep_advance(W, A, alpha0); }
