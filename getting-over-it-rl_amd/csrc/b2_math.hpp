@@ -171,6 +171,11 @@ struct Group {
 };
 
 template <class Grp>
+GOI_D int group_max(const Grp& g, int x) {
+    for (int d = 1; d < g.G(); d <<= 1) x = max(x, __shfl_xor(x, d, 64));
+    return x;
+}
+template <class Grp>
 GOI_D int group_sum(const Grp& g, int x) {
     for (int d = 1; d < g.G(); d <<= 1) x += __shfl_xor(x, d, 64);
     return x;

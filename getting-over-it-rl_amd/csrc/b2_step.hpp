@@ -72,8 +72,8 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         for (int i = 0; i < I.nj; ++i) jn_solve_velocity(bd, JRw, i, v24, m.rev_only);
         cs_solve_velocity_sweep(bd, CR, I.nc);
     }
-    // StoreImpulses (contact_solver.py:293-304)
-    for (int i = 0; i < I.nc; ++i) {
+    // StoreImpulses (contact_solver.py:293-304), rows split over the lane group
+    for (int i = W.sub; i < I.nc; i += W.G) {
         const int slot = CR.geti(i, CF_SLOT), cnt = CR.geti(i, CF_COUNT);
         if (cnt > 0) {
             W.f(GOI_C_NORMAL_IMPULSE, 2 * slot) = CR.getf(i, CF_NI0);
@@ -84,7 +84,8 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
             W.f(GOI_C_TANGENT_IMPULSE, 2 * slot + 1) = CR.getf(i, CF_TI1);
         }
     }
-    for (int i = 0; i < I.nj; ++i) jn_store(W, JRw, i, v24);
+    for (int i = W.sub; i < I.nj; i += W.G) jn_store(W, JRw, i, v24);
+    group_sync();
     // integrate positions with the per-step clamps (step.py:120-135)
     const float max_t = s.clamps_per_second ? s.max_translation * h : s.max_translation;
     const float max_r = s.clamps_per_second ? s.max_rotation * h : s.max_rotation;
@@ -178,11 +179,12 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     for (int b = 0; b < W.B; ++b) {
         if (!W.is_static(b)) continue;
         int last = -1;
-        for (int c = 0; c < W.C; ++c) {
+        for (int c = W.sub; c < W.C; c += W.G) {  // slots split over the lane group
             const int isl = I.contact_island(c);
             if (isl < 0) continue;
             if (W.ba(c) == b || W.bb(c) == b) last = max(last, isl);
         }
+        last = group_max(W.grp(), last);
         for (int j = 0; j < W.J; ++j) {
             const int isl = I.joint_island(j);
             if (isl >= 0 && (m.joint_a[j] == b || m.joint_b[j] == b)) last = max(last, isl);
@@ -463,8 +465,8 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         W.f(GOI_B_W, b) = w;
         sync_transform(W, b);
     }
-    // b2Island::Report
-    for (int i = 0; i < nc; ++i) {
+    // b2Island::Report, rows split over the lane group
+    for (int i = W.sub; i < nc; i += W.G) {
         const int slot = CR.geti(i, CF_SLOT), cnt = CR.geti(i, CF_COUNT);
         W.f(GOI_T_NORMAL_IMPULSE, 2 * slot) = cnt > 0 ? CR.getf(i, CF_NI0) : 0.0f;
         W.f(GOI_T_NORMAL_IMPULSE, 2 * slot + 1) = cnt > 1 ? CR.getf(i, CF_NI1) : 0.0f;
@@ -472,6 +474,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         W.f(GOI_T_TANGENT_IMPULSE, 2 * slot + 1) = cnt > 1 ? CR.getf(i, CF_TI1) : 0.0f;
         W.u8(GOI_T_SOLVED, slot) = 1;
     }
+    group_sync();
     // fixture sync of the island's dynamic bodies and TOI invalidation of their contacts
     unsigned long long moved = 0ull, refat = 0ull;
     for (int i = 0; i < nb; ++i) {
