@@ -154,19 +154,20 @@ GOI_D void cs_prepare(const DModel& m, const World& W, const Bodies& bd, const R
         const V2 ccA = pA + radA * n, ccB = pB - radB * n;
         p0 = 0.5f * (ccA + ccB);
         p1 = p0;
-    } else if (mtype == kFaceA) {
-        n = mul(qA, ln);
-        const V2 pp = mul(xfA, lp);
-        const V2 q0 = mul(xfB, pl0), q1 = mul(xfB, pl1);
-        p0 = 0.5f * ((q0 + (radA - dot(q0 - pp, n)) * n) + (q0 - radB * n));
-        p1 = 0.5f * ((q1 + (radA - dot(q1 - pp, n)) * n) + (q1 - radB * n));
     } else {
-        n = mul(qB, ln);
-        const V2 pp = mul(xfB, lp);
-        const V2 q0 = mul(xfA, pl0), q1 = mul(xfA, pl1);
-        p0 = 0.5f * ((q0 - radA * n) + (q0 + (radB - dot(q0 - pp, n)) * n));
-        p1 = 0.5f * ((q1 - radA * n) + (q1 + (radB - dot(q1 - pp, n)) * n));
-        n = -n;
+        // face A or face B: the reference face's side (x1, r1) and the incident side (x2, r2) swap; the two
+        // clip-point sums are the same float additions in either order (addition commutes exactly), so one path
+        // serves both
+        const bool fa = mtype == kFaceA;
+        const Xf& x1 = fa ? xfA : xfB;
+        const Xf& x2 = fa ? xfB : xfA;
+        const float r1 = fa ? radA : radB, r2 = fa ? radB : radA;
+        n = mul(x1.q, ln);
+        const V2 pp = mul(x1, lp);
+        const V2 q0 = mul(x2, pl0), q1 = mul(x2, pl1);
+        p0 = 0.5f * ((q0 + (r1 - dot(q0 - pp, n)) * n) + (q0 - r2 * n));
+        p1 = 0.5f * ((q1 + (r1 - dot(q1 - pp, n)) * n) + (q1 - r2 * n));
+        if (!fa) n = -n;
     }
     R.set2(i, CF_NX, n);
     const V2 t = cross(n, 1.0f);
@@ -392,17 +393,17 @@ GOI_D float solve_prow(const Bodies& bd, const PRow& r, float baumgarte, float m
             normalize(n);
             p = 0.5f * (pA + pB);
             sep = (dot(pB - pA, n) - radA) - radB;
-        } else if (r.mtype == kFaceA) {
-            n = mul(xfA.q, ln);
-            const V2 cp = mul(xfB, plj);
-            sep = (dot(cp - mul(xfA, lp), n) - radA) - radB;
-            p = cp;
         } else {
-            n = mul(xfB.q, ln);
-            const V2 cp = mul(xfA, plj);
-            sep = (dot(cp - mul(xfB, lp), n) - radA) - radB;
+            // face A or face B: the same operations with the reference and incident transforms swapped (one path
+            // for both, so lanes of different manifold types do not diverge)
+            const bool fa = r.mtype == kFaceA;
+            const Xf& x1 = fa ? xfA : xfB;
+            const Xf& x2 = fa ? xfB : xfA;
+            n = mul(x1.q, ln);
+            const V2 cp = mul(x2, plj);
+            sep = (dot(cp - mul(x1, lp), n) - radA) - radB;
             p = cp;
-            n = -n;
+            if (!fa) n = -n;
         }
         const V2 rA = p - cA, rB = p - cB;
         min_sep = bmin(min_sep, sep);
