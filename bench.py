@@ -5,8 +5,8 @@
 Workload (default, the headline): 16,384 worlds of the 4-body character rig over a seed-2 terrain (1,024 edge quads
 + 256 rocks), linear velocities N(0, 25) m/s, hammer-head spin U[-60, 60] rad/s, dt 0.02 s, g -9.81, 8 / 3
 iterations, continuous physics on with Box2D's stock TOI pair rule, random unit-disk actions written into the motor
-joint before every step. Inputs are resident in HBM before timing. One step = one k_step launch plus the two
-elementwise action writes; `value` counts every world of the timed steps.
+joint before every step. Inputs are resident in HBM before timing. One step = one k_step launch plus the action
+write (one goi_apply_motor_actions launch); `value` counts every world of the timed steps.
 
 Roofline: k_step is HBM-bound work in the roofline sense (no dense contraction). Its algorithmic bytes per world-step
 follow the reference State's field set in the compact layout, each leaf read once and each mutable leaf written once:

@@ -61,7 +61,7 @@ class GoiDebug(ctypes.Structure):
 
 
 EXPORTS = ("goi_abi_version", "goi_model_create", "goi_model_destroy", "goi_step", "goi_step_n", "goi_collide",
-           "goi_world_manifold", "goi_sincos", "goi_last_error")
+           "goi_world_manifold", "goi_apply_motor_actions", "goi_sincos", "goi_last_error")
 
 _LIB = None
 
@@ -91,6 +91,9 @@ def lib(path=None):
     L.goi_collide.restype = ctypes.c_int32
     L.goi_world_manifold.argtypes = [_P, ctypes.POINTER(GoiStateView), _P, _P, _P, _P]
     L.goi_world_manifold.restype = ctypes.c_int32
+    L.goi_apply_motor_actions.argtypes = [_P, _P, _P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_float,
+                                          ctypes.c_float, _P]
+    L.goi_apply_motor_actions.restype = ctypes.c_int32
     L.goi_sincos.argtypes = [_P, _P, _P, ctypes.c_int32, _P]
     L.goi_sincos.restype = ctypes.c_int32
     if L.goi_abi_version() != ABI_VERSION:

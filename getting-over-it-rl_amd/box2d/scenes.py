@@ -251,11 +251,38 @@ def actions(rng, n):
 
 def apply_actions(joint_speed, joint_torque, a):
     """Write actions into the motor joint's leaves (numpy or torch (N, J) views, in place):
-    motor_speed = gain * a_x, max_motor = torque * |a| on the torso-handle joint."""
+    motor_speed = gain * a_x, max_motor = torque * |a| on the torso-handle joint.
+
+    Device State leaves (worlds-minor, as layout.empty_device_state makes them) take one launch of the library's
+    goi_apply_motor_actions on torch's current stream; numpy arrays (the oracle's side) take the same float32
+    operations on the host."""
+    if _native_actions(joint_speed, joint_torque, a):
+        return
     ax = a[:, 0]
     mag = (a[:, 0] * a[:, 0] + a[:, 1] * a[:, 1]) ** 0.5
     joint_speed[:, MOTOR_JOINT] = MOTOR_GAIN * ax
     joint_torque[:, MOTOR_JOINT] = MOTOR_TORQUE * mag
+
+
+def _native_actions(speed, torque, a):
+    """goi_apply_motor_actions for CUDA float32 (N, J) leaves with the State's worlds-minor strides (1, pitch) and a
+    contiguous (N, 2) float32 action tensor on the same device; False for anything else."""
+    if not getattr(speed, "is_cuda", False):
+        return False
+    import torch
+    n, J = speed.shape
+    if not (getattr(torque, "is_cuda", False) and getattr(a, "is_cuda", False) and speed.dtype == torch.float32
+            and torque.dtype == torch.float32 and a.dtype == torch.float32 and a.shape == (n, 2)
+            and a.is_contiguous() and torque.shape == speed.shape and speed.stride() == torque.stride()
+            and speed.stride(0) == 1 and J > MOTOR_JOINT and a.device == speed.device == torque.device):
+        return False
+    from . import _abi
+    L = _abi.lib()
+    stream = torch.cuda.current_stream(speed.device).cuda_stream
+    _abi.check(L.goi_apply_motor_actions(a.data_ptr(), speed.data_ptr(), torque.data_ptr(), int(n),
+                                         int(speed.stride(1)) if J > 1 else int(n), MOTOR_JOINT,
+                                         float(MOTOR_GAIN), float(MOTOR_TORQUE), stream), L)
+    return True
 
 
 def make_config(k, n=None, edges="quad"):

@@ -303,6 +303,18 @@ __global__ void k_world_manifold(DModel m, Launch L, float* normal, float* point
     }
 }
 
+// The action-driven motor of joint `joint` in every world: motor_speed = gs * a_x, max_motor = gt * |a| (float32,
+// one rounding per operation, |a| by IEEE square root), into the State's worlds-minor joint leaves.
+__global__ void k_motor_actions(const float* a, float* speed, float* torque, int n, int pitch, int joint, float gs,
+                                float gt) {
+    const int w = blockIdx.x * blockDim.x + threadIdx.x;
+    if (w >= n) return;
+    const float ax = a[2 * w], ay = a[2 * w + 1];
+    const uint32_t i = (uint32_t)joint * (uint32_t)pitch + (uint32_t)w;
+    speed[i] = gs * ax;
+    torque[i] = gt * sqrtf(ax * ax + ay * ay);
+}
+
 __global__ void k_sincos(const float* x, float* s, float* c, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -745,6 +757,21 @@ int32_t goi_world_manifold(const GoiModel* model, const GoiStateView* state, flo
     fill_launch(L, model, state, &none, 0.0f);
     hipLaunchKernelGGL(k_world_manifold, dim3((state->n_worlds + 255) / 256, state->C), dim3(256), 0,
                        static_cast<hipStream_t>(hip_stream), model->d, L, normal, points, separations);
+    HIP_TRY(hipGetLastError());
+    return GOI_OK;
+}
+
+int32_t goi_apply_motor_actions(const float* actions, float* motor_speed, float* max_motor, int32_t n_worlds,
+                                int32_t pitch, int32_t joint, float speed_gain, float torque_gain, void* hip_stream) {
+    if (n_worlds < 0 || pitch < n_worlds || joint < 0)
+        return fail(GOI_E_ARG, "goi_apply_motor_actions: bad n_worlds/pitch/joint");
+    if (n_worlds == 0) return GOI_OK;
+    if (!actions || !motor_speed || !max_motor) return fail(GOI_E_ARG, "goi_apply_motor_actions: null pointer");
+    if ((uint64_t)(joint + 1) * (uint64_t)pitch >= (1ull << 32))
+        return fail(GOI_E_UNSUPPORTED, "goi_apply_motor_actions: pitch too large for 32-bit element offsets");
+    hipLaunchKernelGGL(k_motor_actions, dim3((n_worlds + 255) / 256), dim3(256), 0,
+                       static_cast<hipStream_t>(hip_stream), actions, motor_speed, max_motor, n_worlds, pitch, joint,
+                       speed_gain, torque_gain);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
 }

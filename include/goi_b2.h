@@ -263,6 +263,16 @@ int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiS
 int32_t goi_world_manifold(const GoiModel* model, const GoiStateView* state, float* normal, float* points,
                            float* separations, void* hip_stream);
 
+/* The action-driven motor: writes every world's action a = (a_x, a_y) into joint `joint` of the
+ * State's joint leaves, motor_speed = speed_gain * a_x and max_motor = torque_gain * |a| (float32, |a| by IEEE
+ * square root). actions: device [n_worlds, 2] contiguous; motor_speed, max_motor: the State's joints.motor_speed and
+ * joints.max_motor leaves (worlds-minor, element (j, w) at [j * pitch + w]). One launch for what a caller of the
+ * reference does by writing State.joints.motor_speed / max_motor before each step (goi_jax/box2d/world.py:105-107,
+ * used by joints.py:308-316); the mapping itself is this build's, the reference leaves it to its caller
+ * (README.md:22-24). Returns GOI_E_ARG for n_worlds < 0, pitch < n_worlds, joint < 0 or a null pointer. */
+int32_t goi_apply_motor_actions(const float* actions, float* motor_speed, float* max_motor, int32_t n_worlds,
+                                int32_t pitch, int32_t joint, float speed_gain, float torque_gain, void* hip_stream);
+
 /* Correctly rounded float32 sin/cos of n values on the device, as the step computes them (math2d.py:291-310):
  * s[i] = (float)sin((double)x[i]), c[i] = (float)cos((double)x[i]). Device pointers. */
 int32_t goi_sincos(const float* x, float* s, float* c, int32_t n, void* hip_stream);

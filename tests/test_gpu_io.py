@@ -74,3 +74,25 @@ def test_dlpack_round_trip(oracle):
     bad = wd.from_leaves([x.double() if x.dtype == torch.float32 else x for x in wd.leaves(producer)])
     with pytest.raises(TypeError):
         b2.io.from_dlpack(bad, "cuda")
+
+
+def test_motor_actions_native_equals_host():
+    """goi_apply_motor_actions (one launch on the device State's joint leaves, through scenes.apply_actions) writes
+    the host mapping's float32 bits into the motor joint and leaves the other joints' entries alone; signed zeros,
+    unit and tiny actions included."""
+    from util import b2 as B2
+    n = 1000
+    s, m, st, cfg = B2.scenes.make_config(4, n)
+    dev = B2.layout.to_device(st, "cuda")
+    a = B2.scenes.actions(np.random.default_rng(3), n)
+    a[:6] = np.array([[0.0, 0.0], [-0.0, 0.0], [1.0, 0.0], [-1.0, 0.0], [3e-20, -7e-21], [0.6, -0.8]], np.float32)
+    speed = np.asarray(st.joints.motor_speed).copy()
+    torque = np.asarray(st.joints.max_motor).copy()
+    B2.scenes.apply_actions(speed, torque, a)
+    before = B2.layout.to_host(dev)
+    B2.scenes.apply_actions(dev.joints.motor_speed, dev.joints.max_motor, torch.from_numpy(a).cuda())
+    got = B2.layout.to_host(dev)
+    assert np.asarray(got.joints.motor_speed).tobytes() == speed.tobytes()
+    assert np.asarray(got.joints.max_motor).tobytes() == torque.tobytes()
+    others = [j for j in range(speed.shape[1]) if j != B2.scenes.MOTOR_JOINT]
+    assert np.array_equal(np.asarray(got.joints.motor_speed)[:, others], np.asarray(before.joints.motor_speed)[:, others])
