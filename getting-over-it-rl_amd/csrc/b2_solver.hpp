@@ -17,9 +17,9 @@ constexpr int kMaxJ = 64;  // joints per world
 
 // Per-lane view of the solver body arrays in LDS.
 struct Bodies {
-    float* s;  // LDS base + lane
+    float* s;  // LDS base + the world's index in the block
     int B;
-    int st;    // lanes per block
+    int st;    // worlds per block
     GOI_D float& at(int field, int b) const { return s[(field * B + b) * st]; }
     GOI_D float& vx(int b) const { return at(0, b); }
     GOI_D float& vy(int b) const { return at(1, b); }

@@ -1,5 +1,5 @@
-// b2_step.hpp - the world-level phases of b2World::Step for one lane's world: Solve (step.py:73-251) and SolveTOI
-// (toi.py:462-865), on top of the narrowphase, contact, solver, joint and TOI primitives.
+// b2_step.hpp - the world-level phases of b2World::Step for one world (run by its lane group): Solve
+// (step.py:73-251) and SolveTOI (toi.py:462-865), on top of the narrowphase, contact, solver, joint and TOI primitives.
 #pragma once
 
 #include "b2_toi.hpp"
@@ -278,7 +278,7 @@ GOI_D int toi_search_prepare(const DModel& m, const World& W, const Rows& CR, co
     return nt;
 }
 
-// pass 2: the TOI of task i of the world on lane o
+// pass 2: the TOI of task i of the block's world o
 GOI_D void toi_task(const DModel& m, const Coop& co, int o, int i, float linear_slop) {
     const Rows R = co.task_rows(o);
     Sweep sa, sb;

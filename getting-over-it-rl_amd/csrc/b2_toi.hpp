@@ -1,6 +1,6 @@
 // b2_toi.hpp - continuous collision on the device: b2World::SolveTOI with b2TimeOfImpact, b2Distance (GJK),
-// b2SeparationFunction, b2Sweep::Advance and b2Island::SolveTOI (goi_jax/box2d/toi.py:73-865). Each lane runs its
-// own world's event loop; the sweeps live in the State leaves (c0, c, a0, a, toi.alpha0).
+// b2SeparationFunction, b2Sweep::Advance and b2Island::SolveTOI (goi_jax/box2d/toi.py:73-865). Each world's lane
+// group runs its event loop; the sweeps live in the State leaves (c0, c, a0, a, toi.alpha0).
 #pragma once
 
 #include "b2_joints.hpp"

@@ -71,8 +71,8 @@ constexpr int kBodyMirrorLeaves[13] = {GOI_B_C0, GOI_B_C, GOI_B_A0, GOI_B_A, GOI
 constexpr int kBodyMirrorWidth[13] = {2, 2, 1, 1, 2, 1, 2, 2, 1, 1, 2, 1, 1};
 constexpr int kBodyMirrorMutable = 10;
 
-// Per-lane workspace in LDS. Every array is [index][lane] with the block's lane count as stride: lane l's element
-// i of an array at offset o sits at base[(o + i) * S + l], so one index across a wavefront is consecutive words.
+// Per-world workspace in LDS. Every array is [index][world] with the block's world count S as stride: world l's
+// element i of an array at offset o sits at base[(o + i) * S + l], so one index across a block is consecutive words.
 // It mirrors the per-world contact metadata (pair, key, fixtures), the awake flags and the TOI bookkeeping for the
 // whole step (loaded once, written back once) and holds the per-world work arrays (contact list order, island
 // lists and stacks, new-pair buffer), which would otherwise live in private scratch memory.
@@ -102,14 +102,14 @@ struct Workspace {
     }
 };
 
-// One world's State: leaf pointers already offset by the lane's world index, plus the lane's LDS workspace.
+// One world's State: leaf pointers already offset by the world's index, plus the world's LDS workspace.
 struct World {
     int pitch;
     int B, C, R, J;
     void* const* lv;  // leaf base pointers (kernel argument block)
     int w;
-    int* ws;          // LDS workspace base + lane
-    int S;            // workspace stride (lanes per block)
+    int* ws;          // LDS workspace base + the world's index in the block
+    int S;            // workspace stride (worlds per block)
     Workspace k;
     const float4* nbox;  // the static BVH's first nk nodes, staged in LDS by the block
     const int2* nlink;

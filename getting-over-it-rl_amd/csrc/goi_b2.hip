@@ -172,8 +172,9 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
     store_mirror_block(bc);
 }
 
-// The whole b2World::Step (step.py:28-47) of one world per lane: FindNewContacts where new_fixture, Collide,
-// Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to share the block's manifold and TOI work.
+// The whole b2World::Step (step.py:28-47) of each world of the block on its lane group: FindNewContacts where
+// new_fixture, Collide, Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to share the block's
+// manifold and TOI work.
 // At most 256 registers (two waves per SIMD): the second wave hides the latency chains of the first.
 template <bool kMulti>
 __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
