@@ -3,7 +3,7 @@
 // Gauss-Seidel velocity sweeps, position integration with the per-step clamps, position sweeps with per-island
 // early exit, transform sync, sleeping, fixture sync and FindNewContacts.
 //
-// Storage: the solver's body arrays (v, w, c, a per body) live in LDS as [field][body][lane] so each lane's random
+// Storage: the solver's body arrays (v, w, c, a per body) live in LDS as [field][body][world] so each world's random
 // body index hits its own bank; the prepared constraint rows live in HBM scratch tiles, one per block
 // ([row][field][world of the block]: a row's fields for the block's worlds are contiguous).
 #pragma once
