@@ -548,6 +548,35 @@ def scene_island_walk(s):
     return d
 
 
+def scene_toi_tie(s):
+    """A ball falling at 60 m/s between two equal static circles set symmetrically about its path (fixture 0 at
+    x = -0.2, fixture 1 at x = +0.2). While the ball moves along x = 0, every float operation of the two contacts'
+    TOIs is the mirror image of the other's, so their TOIs are equal to the bit and the event order is the tie
+    rule's (toi.py:552-556)."""
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC)
+    d.add_circle(g, 0.2, center=(-0.2, 0.0))
+    d.add_circle(g, 0.2, center=(0.2, 0.0))
+    b = d.add_body(wd.DYNAMIC, (0.0, 2.5), 0.0, (0.0, -60.0), 0.0, mass=1.0, inertia=0.01)
+    d.add_circle(b, 0.1)
+    return d
+
+
+def scene_toi_plank(s, ball_bullet=False, plank_bullet=False):
+    """Zero-gravity TOI island membership (toi.py:604-716): a ball touching the top of a floating plank (body 1)
+    slides at 150 m/s into a static face that leans over the plank (normal left-down), so the TOI velocity solve
+    presses the ball into the plank. The plank joins the TOI island only if the ball or the plank is a bullet."""
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC)
+    d.add_polygon(g, [(2.3, 0.75), (2.6, 0.75), (2.6, 1.5), (1.9, 1.5)])
+    plank = d.add_body(wd.DYNAMIC, (0.0, 0.6), mass=4.0, inertia=6.0, bullet=plank_bullet)
+    d.add_box(plank, (2.25, 0.1))
+    ball = d.add_body(wd.DYNAMIC, (-1.5, 0.81), 0.0, (150.0, 0.0), 0.0, mass=0.5, inertia=0.0025,
+                      bullet=ball_bullet)
+    d.add_circle(ball, 0.1)
+    return d
+
+
 def scene_edges(s):
     """Native edge shapes: an open chain with convex and concave corners and a collinear run, a closed loop, an
     isolated two-sided segment and a segment with ghost vertices but no neighbours; boxes slide across the chain's
@@ -601,6 +630,12 @@ TEST_SCENES = {
     "stock_bullets": (scene_stock_bullets, lambda: _toi(unity=False), 16),
     "island_walk": (scene_island_walk, _toi, 32),
     "edges": (scene_edges, _toi, 32),
+    "toi_tie": (scene_toi_tie, lambda: Settings.stock(gravity=(0.0, 0.0), continuous_physics=True), 8),
+    "toi_tie_oldest": (scene_toi_tie, lambda: Settings.stock(gravity=(0.0, 0.0), continuous_physics=True,
+                                                             toi_tie_oldest=True), 8),
+    "toi_plank": (scene_toi_plank, lambda: Settings.stock(gravity=(0.0, 0.0), continuous_physics=True), 8),
+    "toi_plank_bullet": (lambda s: scene_toi_plank(s, ball_bullet=True),
+                         lambda: Settings.stock(gravity=(0.0, 0.0), continuous_physics=True), 8),
 }
 
 

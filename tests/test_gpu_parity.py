@@ -57,6 +57,25 @@ def test_config_parity(k, n, steps, edges, oracle):
     assert np.isfinite(np.asarray(ref.bodies.c)).all()
 
 
+@pytest.mark.parametrize("oldest", [False, True])
+@pytest.mark.parametrize("max_events", [1, None])
+def test_toi_tie_parity(oracle, oldest, max_events):
+    """scene_toi_tie over 64 worlds that keep its mirror symmetry (only the fall speed varies, 40 to 80 m/s), so
+    every world's two TOIs tie to the bit and the device's pick must follow the tie rule as the oracle does
+    (toi.py:552-556); max_events=1 leaves the rule's contact as the one with toi.count 1."""
+    s = b2.Settings.stock(gravity=(0.0, 0.0), continuous_physics=True, toi_tie_oldest=oldest,
+                          max_events=max_events)
+    model, state = b2.scenes.scene_toi_tie(s).build(8)
+    m = wd.compact_model(model, state)
+    st = wd.batch(wd.compact_state(m, state), 64)
+    st.bodies.v[:, 1, 1] = -np.random.default_rng(11).uniform(40.0, 80.0, 64).astype(np.float32)
+    ref = _run(m, st, s, np.float32(1.0 / 60.0), 8, oracle)
+    c = np.asarray(ref.bodies.c)[:, 1]
+    assert (c[:, 1] > 0).all()  # every ball was stopped above the circles
+    # the contact solved first pushes the ball away from its circle: fixture 1 (+x, newest) under the stock rule
+    assert (np.sign(c[:, 0]) == (1 if oldest else -1)).all()
+
+
 def test_model_without_body_types(oracle):
     """A compact Model as the reference's compact_model returns it (no body types: they stay in the State,
     world.py:437-472) steps the same; the body types come from the State."""

@@ -29,6 +29,25 @@ MUTANTS = [
     ("contact_list_oldest_first", "while (j > 0 && w->c_key[order[j - 1]] < w->c_key[k])",
      "while (j > 0 && w->c_key[order[j - 1]] > w->c_key[k])",
      lambda o: P.test_islands_vs_sequential_dfs(o, "pile")),
+    ("toi_tie_rules_swapped", "toi_tie_oldest ? alpha <= best_alpha : alpha < best_alpha",
+     "toi_tie_oldest ? alpha < best_alpha : alpha <= best_alpha", lambda o: P.test_toi_tie_rule(o)),
+    ("toi_search_slot_order", "int c = k->order[i];\n        if (!w->t_enabled[c]",
+     "int c = i;\n        if (!w->t_enabled[c]", lambda o: P.test_toi_tie_rule(o)),
+    ("toi_walk_takes_dynamic_neighbours",
+     "if (w->b_type[other] == GOI_DYNAMIC && !w->b_bullet[body] && !w->b_bullet[other]) continue;",
+     "if (0) continue;", lambda o: P.test_toi_island_membership(o)),
+    ("toi_walk_bullet_of_walked_body_only",
+     "if (w->b_type[other] == GOI_DYNAMIC && !w->b_bullet[body] && !w->b_bullet[other]) continue;",
+     "if (w->b_type[other] == GOI_DYNAMIC && !w->b_bullet[body]) continue;",
+     lambda o: P.test_toi_island_membership(o)),
+    ("toi_walk_body_a_only", "for (int pi = 0; pi < 2; ++pi) {\n        int body = pair[pi];",
+     "for (int pi = 0; pi < 1; ++pi) {\n        int body = pair[pi];", lambda o: P.test_toi_island_membership(o)),
+    ("block_solver_diagonal_inverse",
+     "c->NM[0] = det * k22; c->NM[1] = -det * k12; c->NM[2] = -det * k12; c->NM[3] = det * k11;",
+     "c->NM[0] = 1.0f / k11; c->NM[1] = 0.0f; c->NM[2] = 0.0f; c->NM[3] = 1.0f / k22;",
+     lambda o: P.test_block_solver_solves_the_two_point_lcp(o, 8)),
+    ("block_solver_warm_sign", "bx = bx - (c->K[0] * ax + c->K[2] * ay);", "bx = bx + (c->K[0] * ax + c->K[2] * ay);",
+     lambda o: P.test_block_solver_solves_the_two_point_lcp(o, 8)),
     ("circle_radius_dropped", "float r = m->radius[fa] + m->radius[fb];", "float r = m->radius[fa];",
      lambda o: P.test_narrowphase_vs_brute_force(o, P.shape_model.__wrapped__())),
     ("edge_circle_ghost_sign", "if (dot(e1, sub(a, q)) > 0.0f) return;", "if (dot(e1, sub(a, q)) < 0.0f) return;",

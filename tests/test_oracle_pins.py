@@ -84,9 +84,10 @@ def resting_box(settings=None, y=1.015):
     return d, box
 
 
-def world_points(model, st, w, slot):
-    """b2WorldManifold::Initialize for one slot: (points [count, 2], separations [count]) in float64."""
-    ct, bd = st.contacts, st.bodies
+def world_points(model, st, w, slot, bodies=None, normal=False):
+    """b2WorldManifold::Initialize for one slot: (points [count, 2], separations [count]) in float64, at the body
+    transforms of `bodies` (default st.bodies); with normal=True also the world normal."""
+    ct, bd = st.contacts, (st.bodies if bodies is None else bodies)
     fa, fb = int(ct.fa[w, slot]), int(ct.fb[w, slot])
     ba, bb = int(model.fixture_body[fa]), int(model.fixture_body[fb])
     ra, rb = float(model.radius[fa]), float(model.radius[fb])
@@ -126,6 +127,8 @@ def world_points(model, st, w, slot):
             nrm = -nrm
         pts.append(0.5 * (ca + cb))
         seps.append(float(np.dot(cb - ca, nrm)))
+    if normal:
+        return np.array(pts).reshape(-1, 2), np.array(seps), nrm
     return np.array(pts).reshape(-1, 2), np.array(seps)
 
 
@@ -155,6 +158,50 @@ def test_contact_impulses_carry_the_weight(oracle):
     assert ct.friction[0, k] == F32(np.sqrt(np.float64(F32(F32(0.5) * F32(1.0)))))  # b2MixFriction in float32
     _, seps = world_points(model, st, 0, k)
     assert -0.02 < seps.min() < 0  # rests inside the 2 x 0.01 skin
+
+
+@pytest.mark.parametrize("iterations", [8, 1])
+def test_block_solver_solves_the_two_point_lcp(oracle, iterations):
+    """The block solver (contact_solver.py:236-279) solves the two-point normal LCP exactly in each velocity
+    iteration: with x the accumulated normal impulses and vn the normal velocities at the two points, x >= 0,
+    vn >= 0 and x_i vn_i = 0. K is positive definite, so that solution is unique whichever of the four cases finds
+    it. A spinning box falls onto flat ground; after every step whose contact has two points, with the box awake and
+    no TOI event, the step's final velocities (those of the last normal solve) meet the conditions at the manifold
+    points and the transforms the solver used (the step's start). The run covers case 1 (both points push) and
+    cases 2 and 3 (one point lifts)."""
+    d = wd.WorldDef(S.stock(gravity=(0, -9.81), continuous_physics=True, velocity_iterations=iterations))
+    g = d.add_body(wd.STATIC)
+    d.add_box(g, (10, 0.5), friction=0.6)
+    box = d.add_body(wd.DYNAMIC, (0, 1.4), 0.3, (1.0, 0.0), 4.0, mass=2, inertia=F32(2) / F32(6))
+    d.add_box(box, (0.5, 0.5), friction=0.6)
+    model, st = d.build(4)
+    n = 16
+    st = wd.batch(st, n)
+    rng = np.random.default_rng(2)
+    st.bodies.w[:, box] = rng.uniform(-8, 8, n).astype(F32)
+    st.bodies.v[:, box, 0] = rng.uniform(-2, 2, n).astype(F32)
+    dt = F32(1 / 60)
+    both = one = 0
+    for _ in range(120):
+        before = oracle.copy(st).bodies  # the transforms the step's solver works at
+        oracle.step_(model, st, d.settings, dt)
+        ct = st.contacts
+        for i in range(n):
+            live = np.nonzero(ct.pair[i] >= 0)[0]
+            if len(live) != 1 or int(ct.count[i, live[0]]) != 2 or not st.bodies.awake[i, box] or st.toi.events[i]:
+                continue
+            k = int(live[0])
+            pts, _, nrm = world_points(model, st, i, k, bodies=before, normal=True)
+            c = np.asarray(before.c[i, box], np.float64)
+            v, w = st.bodies.v[i, box].astype(np.float64), float(st.bodies.w[i, box])
+            x = ct.normal_impulse[i, k].astype(np.float64)
+            vn = np.array([np.dot(v + w * np.array([-(p - c)[1], (p - c)[0]]), nrm) for p in pts])
+            tol = 2e-5 * (1 + np.abs(v).sum() + abs(w))
+            assert (x >= 0).all() and (vn >= -tol).all(), (i, x, vn)
+            assert (np.abs(vn[x > 0]) <= tol).all(), (i, x, vn)
+            both += int((x > 0).all())
+            one += int((x > 0).sum() == 1)
+    assert both >= 100 and one >= 10, (both, one)
 
 
 def test_restitution_mix_is_max(oracle):
@@ -333,6 +380,56 @@ def test_toi_pair_rules(oracle):
     assert _bullet_through_wall(oracle) > 0  # Unity rule: a discrete body tunnels
     assert _bullet_through_wall(oracle, continuous=True) < 0  # a Continuous body is stopped
     assert _bullet_through_wall(oracle, unity=False) < 0  # stock rule: every dynamic-vs-static pair gets TOI
+
+
+def test_toi_tie_rule(oracle):
+    """b2World::SolveTOI's minimum over the contact list (toi.py:552-556): of equal TOIs the stock rule takes the
+    first contact in list order (the newest, the larger key) and toi_tie_oldest the last. In scene_toi_tie the two
+    contacts' TOIs are equal to the bit (mirror images), and with one event allowed per step the event's contact
+    (toi.count) is the one the rule names. Swapping which fixture the rule favours mirrors the whole outcome, so the
+    two runs are mirror images of each other to the bit: the tie, not a difference of TOIs, decided."""
+    out = {}
+    for oldest in (False, True):
+        s = S.stock(gravity=(0, 0), continuous_physics=True, toi_tie_oldest=oldest, max_events=1)
+        model, st = b2.scenes.scene_toi_tie(s).build(4)
+        st = wd.batch(st, 1)
+        dt = F32(1.0 / 60.0)
+        for k in range(3):
+            oracle.step_(model, st, s, dt)
+            assert int(st.toi.events[0]) == (1 if k == 2 else 0)
+        keys, counts = st.contacts.key[0, :2], st.toi.count[0, :2]
+        assert sorted(st.contacts.fa[0, :2].tolist()) == [0, 1] and keys[0] != keys[1]
+        named = int(np.argmin(keys) if oldest else np.argmax(keys))
+        assert counts[named] == 1 and counts[1 - named] == 0
+        out[oldest] = st
+    a, b = out[False], out[True]
+    assert a.bodies.c[0, 1, 0] != 0
+    assert np.array_equal(a.bodies.c[0, 1] * F32([-1, 1]), b.bodies.c[0, 1])
+    assert np.array_equal(a.bodies.v[0, 1] * F32([-1, 1]), b.bodies.v[0, 1])
+
+
+def test_toi_island_membership(oracle):
+    """b2World::SolveTOI's island walk (toi.py:604-716) skips a dynamic neighbour unless the walked body or the
+    neighbour is a bullet. In scene_toi_plank the ball's TOI event (the second step) presses it into the plank it
+    touches: with no bullet the plank stays out of the TOI island, so it ends the event step exactly as with
+    continuous physics off (at rest: it never moves in Solve); with either body a bullet it joins, takes an impulse,
+    and the two bullet choices give the same step to the bit (the rule is symmetric in the two bodies)."""
+    def plank_after(cont, **bullets):
+        s = S.stock(gravity=(0, 0), continuous_physics=cont)
+        model, st = b2.scenes.scene_toi_plank(s, **bullets).build(8)
+        st = wd.batch(st, 1)
+        for k in range(2):
+            oracle.step_(model, st, s, F32(1 / 60))
+            assert int(st.toi.events[0]) == (1 if (cont and k == 1) else 0)
+        return st.bodies.c[0, 1].copy(), st.bodies.v[0, 1].copy(), st.bodies.c[0, 2].copy()
+    c_off, v_off, _ = plank_after(False)
+    c, v, ball = plank_after(True)
+    assert ball[0] < 2.3  # the ball was stopped at the face, not tunnelled
+    assert np.array_equal(c, c_off) and np.array_equal(v, v_off) and not v.any()
+    c_b, v_b, _ = plank_after(True, ball_bullet=True)
+    c_p, v_p, _ = plank_after(True, plank_bullet=True)
+    assert v_b[1] < -1.0  # pressed down by the ball in the TOI velocity solve
+    assert np.array_equal(c_b, c_p) and np.array_equal(v_b, v_p)
 
 
 def test_toi_off_tunnels(oracle):
