@@ -48,6 +48,15 @@ MUTANTS = [
      lambda o: P.test_block_solver_solves_the_two_point_lcp(o, 8)),
     ("block_solver_warm_sign", "bx = bx - (c->K[0] * ax + c->K[2] * ay);", "bx = bx + (c->K[0] * ax + c->K[2] * ay);",
      lambda o: P.test_block_solver_solves_the_two_point_lcp(o, 8)),
+    ("feature_key_types_swapped", "return ia | (ib << 8) | (ta << 16) | (tb << 24);",
+     "return ia | (ib << 8) | (tb << 16) | (ta << 24);", lambda o: P.test_polygon_manifold_known_answers(o)),
+    ("flip_keeps_feature_halves", "ids[i] = flip ? feature_key(cp2[i].ib, cp2[i].ia, cp2[i].tb, cp2[i].ta)",
+     "ids[i] = flip ? feature_key(cp2[i].ia, cp2[i].ib, cp2[i].ta, cp2[i].tb)",
+     lambda o: P.test_polygon_manifold_known_answers(o)),
+    ("clip_second_side_keyed_iv1", "np = clip_segment(cp2, cp1, tangent, side2, iv2);",
+     "np = clip_segment(cp2, cp1, tangent, side2, iv1);", lambda o: P.test_polygon_manifold_known_answers(o)),
+    ("no_reference_face_hysteresis", "int flip = sep_b > sep_a + k_tol;", "int flip = sep_b > sep_a;",
+     lambda o: P.test_polygon_manifold_known_answers(o)),
     ("circle_radius_dropped", "float r = m->radius[fa] + m->radius[fb];", "float r = m->radius[fa];",
      lambda o: P.test_narrowphase_vs_brute_force(o, P.shape_model.__wrapped__())),
     ("edge_circle_ghost_sign", "if (dot(e1, sub(a, q)) > 0.0f) return;", "if (dot(e1, sub(a, q)) < 0.0f) return;",

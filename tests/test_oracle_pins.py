@@ -572,6 +572,54 @@ def test_gjk_distance_vs_exhaustive(oracle, shape_model):
             assert got == pytest.approx(want, abs=5e-5 + 5e-5 * want), (trial, fa, fb, got, want)
 
 
+def _xf(x, y, a=0.0):
+    return np.array([x, y, np.cos(F32(a)), np.sin(F32(a))], np.float32)
+
+
+def test_polygon_manifold_known_answers(oracle):
+    """b2CollidePolygons (collide.py:65-127) worked by hand on three box contacts, from the algorithm's definition:
+    the reference face is A's unless B's separates by more than k_tol = 0.1 slop (then FACE_B and each point's
+    feature swaps its A and B halves); the incident edge is the one of the other polygon most anti-parallel to the
+    reference normal, its vertices keyed (reference edge, incident vertex, face, vertex); clipping against the
+    reference face's side planes keys a new point (side vertex iv1 or iv2, the incoming point's vertex, vertex,
+    face); key = indexA | indexB << 8 | typeA << 16 | typeB << 24 with vertex 0 and face 1 (collide.py:22-24).
+    Boxes are b2PolygonShape::SetAsBox's: vertices (-h,-h), (h,-h), (h,h), (-h,h), edge i from vertex i.
+
+    - rest: the unit box 0.015 above a (10, 0.5) slab. Reference A edge 2 (the slab's top), incident B edge 0,
+      nothing clipped: (2, 0, F, V) = 65538 and (2, 1, F, V) = 65794 at B's vertices 0 and 1.
+    - flip: the unit box turned 0.3 rad, its lowest corner (vertex 0) 0.01 above the slab, as fixture A. The box's
+      faces separate from the slab's far corners by about -3 m, the slab's top by 0.01, so FACE_B; incident box
+      edge 0; vertex 1 lies 0.31 above and drops out; one point, (2, 0, F, V) swapped to (0, 2, V, F) = 16777728.
+    - clip: the unit box resting 0.01 above a (0.3, 0.3) box (A). Reference A edge 2 from (0.3, 0.3) to
+      (-0.3, 0.3); B's edge 0 spans x = -0.5..0.5 and is clipped at x = +-(0.3 + 2 skins): side plane iv1 = 2 keys
+      (2, 0, V, F) = 16777218 at x = 0.32, then iv2 = 3 keys (3, 0, V, F) = 16777219 at x = -0.32.
+    - the k_tol hysteresis: with the unit box on the small one turned by t, B's face separates 0.2 t more than A's;
+      t = 0.001 (0.0002 < k_tol) keeps FACE_A, t = 0.004 (0.0008) gives FACE_B, either sign of t.
+    """
+    d = wd.WorldDef(S.stock())
+    g = d.add_body(wd.STATIC)
+    d.add_box(g, (10, 0.5))
+    d.add_box(g, (0.5, 0.5))
+    d.add_box(g, (0.3, 0.3))
+    model, _ = d.build(2)
+    slop = S.stock()
+    rest = oracle.evaluate(model, 0, 1, _xf(0, 0), _xf(0, 1.015), slop)
+    assert (rest["mtype"], rest["count"]) == (1, 2) and rest["point_id"].tolist() == [65538, 65794]
+    assert np.array_equal(rest["local_normal"], [0, 1]) and np.array_equal(rest["local_point"], [0, 0.5])
+    assert np.array_equal(rest["point_local"], [[-0.5, -0.5], [0.5, -0.5]])
+    t = 0.3
+    flip = oracle.evaluate(model, 1, 0, _xf(0, 0.51 + 0.5 * (np.sin(t) + np.cos(t)), t), _xf(0, 0), slop)
+    assert (flip["mtype"], flip["count"]) == (2, 1) and int(flip["point_id"][0]) == 16777728
+    assert np.array_equal(flip["local_normal"], [0, 1]) and np.array_equal(flip["local_point"], [0, 0.5])
+    assert np.allclose(flip["point_local"][0], [-0.5, -0.5], atol=1e-6)
+    clip = oracle.evaluate(model, 2, 1, _xf(0, 0), _xf(0, 0.81), slop)
+    assert (clip["mtype"], clip["count"]) == (1, 2) and clip["point_id"].tolist() == [16777218, 16777219]
+    assert np.allclose(clip["point_local"], [[0.32, -0.5], [-0.32, -0.5]], atol=1e-6)
+    for t, mtype in ((0.001, 1), (-0.001, 1), (0.004, 2), (-0.004, 2)):
+        y = 0.31 + 0.5 * (np.cos(t) + abs(np.sin(t)))
+        assert oracle.evaluate(model, 2, 1, _xf(0, 0), _xf(0, y, t), slop)["mtype"] == mtype, t
+
+
 def test_narrowphase_vs_brute_force(oracle, shape_model):
     """Manifold point count against exhaustive geometry: circles touch iff |c1 - c2| <= r1 + r2; polygon-circle iff
     the centre is within r_p + r_c of the polygon; polygon pairs: no points when the exhaustive face separation
