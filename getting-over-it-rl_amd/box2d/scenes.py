@@ -562,6 +562,25 @@ def scene_toi_tie(s):
     return d
 
 
+def scene_wake_cascade(s, xy_newer=True):
+    """Zero-gravity Collide wake cascade (pairs.py:90-117): box X (0.2 x 0.2) drifts at 0.075 m/s toward box Y
+    (0.8 x 0.2, body 1) from 0.08 m away; box Z (0.2 x 0.2) rests 0.05 m beyond Y. All three are made in one
+    FindNewContacts pass, keyed in fixture order: the fixtures are made Z, Y, X when xy_newer (X is body 2, Z body 0,
+    and the X-Y contact is the newer) and X, Y, Z otherwise (X body 0, Z body 2)."""
+    d = wd.WorldDef(s)
+    for name in ("ZYX" if xy_newer else "XYZ"):
+        if name == "X":
+            b = d.add_body(wd.DYNAMIC, (-0.58, 0.0), 0.0, (0.075, 0.0), mass=1.0, inertia=0.1)
+            d.add_box(b, (0.1, 0.1))
+        elif name == "Y":
+            b = d.add_body(wd.DYNAMIC, (0.0, 0.0), mass=1.0, inertia=0.1)
+            d.add_box(b, (0.4, 0.1))
+        else:
+            b = d.add_body(wd.DYNAMIC, (0.55, 0.0), mass=1.0, inertia=0.1)
+            d.add_box(b, (0.1, 0.1))
+    return d
+
+
 def scene_toi_plank(s, ball_bullet=False, plank_bullet=False):
     """Zero-gravity TOI island membership (toi.py:604-716): a ball touching the top of a floating plank (body 1)
     slides at 150 m/s into a static face that leans over the plank (normal left-down), so the TOI velocity solve

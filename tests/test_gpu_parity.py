@@ -76,6 +76,32 @@ def test_toi_tie_parity(oracle, oldest, max_events):
     assert (np.sign(c[:, 0]) == (1 if oldest else -1)).all()
 
 
+@pytest.mark.parametrize("xy_newer", [True, False])
+def test_wake_cascade_parity(oracle, xy_newer):
+    """scene_wake_cascade on the device and in the oracle in lockstep, bit for bit at every step, with the sleeping
+    box moved by hand between steps as the oracle pin does (test_collide_wake_cascade_in_list_order): the device's
+    Collide walk must wake Z in the step where X first touches Y only when the X-Y contact is the newer."""
+    from test_oracle_pins import wake_cascade_run
+    s = b2.Settings.stock(gravity=(0.0, 0.0))
+    model, state = b2.scenes.scene_wake_cascade(s, xy_newer).build(8)
+    m = wd.compact_model(model, state)
+    dt = np.float32(1.0 / 60.0)
+
+    def step(x):
+        dev = b2.layout.to_device(x, "cuda")
+        b2.step_(m, dev, s, dt)
+        got = b2.layout.to_host(dev)
+        ref = oracle.copy(x)
+        oracle.step_(m, ref, s, dt)
+        bad = leaf_mismatches(ref, got)
+        assert bad == [], bad[:4]
+        for dst, src in zip(wd.leaves(x), wd.leaves(got)):
+            dst[...] = src
+
+    got = wake_cascade_run(step, wd.batch(wd.compact_state(m, state), 1), xy_newer)
+    assert got == ([(True, True), (True, True)] if xy_newer else [(False, False), (True, True)])
+
+
 def test_model_without_body_types(oracle):
     """A compact Model as the reference's compact_model returns it (no body types: they stay in the State,
     world.py:437-472) steps the same; the body types come from the State."""

@@ -48,6 +48,14 @@ MUTANTS = [
      lambda o: P.test_block_solver_solves_the_two_point_lcp(o, 8)),
     ("block_solver_warm_sign", "bx = bx - (c->K[0] * ax + c->K[2] * ay);", "bx = bx + (c->K[0] * ax + c->K[2] * ay);",
      lambda o: P.test_block_solver_solves_the_two_point_lcp(o, 8)),
+    ("collide_touch_flip_wakes_nobody", "if (contact_update(w, k, &mf)) { wake(w, ba); wake(w, bb); }",
+     "contact_update(w, k, &mf);", lambda o: P.test_collide_wake_cascade_in_list_order(o, True)),
+    ("collide_walk_to_fixed_point",
+     "    for (int i = 0; i < n; ++i) {\n        int k = order[i];\n        int fa = w->c_fa[k], fb = w->c_fb[k];\n"
+     "        int ba = m->fixture_body[fa], bb = m->fixture_body[fb];\n        int act_a",
+     "    for (int i = 0; i < 2 * n; ++i) {\n        int k = order[i % n];\n        int fa = w->c_fa[k], fb = w->c_fb[k];\n"
+     "        int ba = m->fixture_body[fa], bb = m->fixture_body[fb];\n        int act_a",
+     lambda o: P.test_collide_wake_cascade_in_list_order(o, False)),
     ("feature_key_types_swapped", "return ia | (ib << 8) | (ta << 16) | (tb << 24);",
      "return ia | (ib << 8) | (tb << 16) | (ta << 24);", lambda o: P.test_polygon_manifold_known_answers(o)),
     ("flip_keeps_feature_halves", "ids[i] = flip ? feature_key(cp2[i].ib, cp2[i].ia, cp2[i].tb, cp2[i].ta)",

@@ -432,6 +432,52 @@ def test_toi_island_membership(oracle):
     assert np.array_equal(c_b, c_p) and np.array_equal(v_b, v_p)
 
 
+def wake_cascade_run(step, st, xy_newer):
+    """Drive scene_wake_cascade (one world, numpy State `st`, `step(st)` advances it in place): step until Y and Z
+    sleep, move the sleeping Z 0.04 m toward Y (inside its fat box, so that the Y-Z contact would touch if updated),
+    then step until X first touches Y and once more. Returns [(Z awake, Y-Z touching)] for those last two steps."""
+    X, Z = (2, 0) if xy_newer else (0, 2)
+    bd = st.bodies
+    for k in range(60):
+        if not bd.awake[0, 1] and not bd.awake[0, Z]:
+            break
+        step(st)
+    assert bd.awake[0, X] and not bd.awake[0, 1] and not bd.awake[0, Z]
+    for leaf in (bd.c, bd.c0, bd.xf_p):
+        leaf[0, Z, 0] -= F32(0.04)  # Z lies right of Y
+
+    def touching(b1, b2):
+        ct = st.contacts
+        for i in range(ct.pair.shape[1]):
+            bs = {int(ct.fa[0, i]), int(ct.fb[0, i])}  # one fixture per body here: fixture i is body i
+            if ct.pair[0, i] >= 0 and bs == {b1, b2}:
+                return bool(ct.touching[0, i])
+        raise AssertionError("contact missing")
+    out = []
+    for k in range(60):
+        step(st)
+        if touching(X, 1):
+            out.append((bool(bd.awake[0, Z]), touching(1, Z)))
+            step(st)
+            out.append((bool(bd.awake[0, Z]), touching(1, Z)))
+            return out
+    raise AssertionError("X never reached Y")
+
+
+@pytest.mark.parametrize("xy_newer", [True, False])
+def test_collide_wake_cascade_in_list_order(oracle, xy_newer):
+    """b2ContactManager::Collide (pairs.py:38-117) walks the contact list newest first and skips a contact whose
+    bodies are both asleep; an update whose touching flips wakes both bodies, which later contacts of the same walk
+    see and earlier ones do not. In scene_wake_cascade, in the step where X first touches the sleeping Y: when the
+    X-Y contact is the newer, the walk wakes Y before it reaches Y-Z, which then touches and wakes Z in that same
+    step; when it is the older, Y-Z was passed over asleep, so Z sleeps through that step and wakes in the next."""
+    s = S.stock(gravity=(0, 0))
+    model, st = b2.scenes.scene_wake_cascade(s, xy_newer).build(8)
+    st = wd.batch(st, 1)
+    got = wake_cascade_run(lambda x: oracle.step_(model, x, s, F32(1 / 60)), st, xy_newer)
+    assert got == ([(True, True), (True, True)] if xy_newer else [(False, False), (True, True)])
+
+
 def test_toi_off_tunnels(oracle):
     d = wd.WorldDef(S.game(gravity=(0, 0), continuous_physics=False))
     wall = d.add_body(wd.STATIC)
