@@ -56,6 +56,15 @@ MUTANTS = [
      "    for (int i = 0; i < 2 * n; ++i) {\n        int k = order[i % n];\n        int fa = w->c_fa[k], fb = w->c_fb[k];\n"
      "        int ba = m->fixture_body[fa], bb = m->fixture_body[fb];\n        int act_a",
      lambda o: P.test_collide_wake_cascade_in_list_order(o, False)),
+    ("joint_point_mass_uncoupled",
+     "(joints.py:39-47) */\n        float exx = ((mA + mB) + rA.y * rA.y * iA) + rB.y * rB.y * iB;\n"
+     "        float eyx = -rA.y * rA.x * iA - rB.y * rB.x * iB;",
+     "(joints.py:39-47) */\n        float exx = ((mA + mB) + rA.y * rA.y * iA) + rB.y * rB.y * iB;\n"
+     "        float eyx = 0.0f;",
+     lambda o: P.test_joint_velocity_rows_solve_the_constraint(o, "revolute", True)),
+    ("prismatic_mass_uncoupled", "float k12 = iA * s1 + iB * s2;\n        float k13",
+     "float k12 = 0.0f;\n        float k13",
+     lambda o: P.test_joint_velocity_rows_solve_the_constraint(o, "prismatic", True)),
     ("feature_key_types_swapped", "return ia | (ib << 8) | (ta << 16) | (tb << 24);",
      "return ia | (ib << 8) | (tb << 16) | (ta << 24);", lambda o: P.test_polygon_manifold_known_answers(o)),
     ("flip_keeps_feature_halves", "ids[i] = flip ? feature_key(cp2[i].ib, cp2[i].ia, cp2[i].tb, cp2[i].ta)",

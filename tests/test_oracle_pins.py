@@ -363,6 +363,50 @@ def test_weld_keeps_relative_pose(oracle):
     assert ang[1] - ang[0] == pytest.approx(0.0, abs=1e-2)
 
 
+@pytest.mark.parametrize("kind,v24", [("revolute", True), ("revolute", False), ("prismatic", True),
+                                      ("prismatic", False), ("weld", True)])
+def test_joint_velocity_rows_solve_the_constraint(oracle, kind, v24):
+    """A joint that is its island's only constraint is solved exactly by each velocity iteration's rows
+    (joints.py:61-622; no motor, no limit): after every step, the relative velocity the joint forbids vanishes at the
+    anchors and transforms the solver used (the step's start). Revolute (v2.4.1 and 2.3.1): the anchor points move
+    together, vB + wB x rB - vA - wA x rA = 0. Prismatic: no velocity across the axis and no relative spin,
+    perp . (vB - vA) + s2 wB - s1 wA = 0 and wB - wA = 0 with s1 = (d + rA) x perp, s2 = rB x perp. Weld: both. Two
+    spinning dynamic bodies fall under gravity, so every mass and inertia term of the rows' effective mass enters."""
+    d = wd.WorldDef(S.stock(gravity=(0, -9.81), revolute_v24=v24))
+    a = d.add_body(wd.DYNAMIC, (0, 0), 0.2, (0.3, 0.0), 2.0, mass=1, inertia=0.1)
+    b = d.add_body(wd.DYNAMIC, (1, -0.5), 0.2, (0.5, 1.0), -1.5, mass=2, inertia=0.3)
+    la, lb = np.array([0.5, -0.25]), np.array([-0.5, 0.25])
+    getattr(d, "add_" + kind)(a, b, tuple(la), tuple(lb))
+    model, st = d.build(2)
+    st = wd.batch(st, 1)
+
+    def cross_sv(w, r):
+        return np.array([-w * r[1], w * r[0]])
+
+    def rot(ang, v):
+        c, s = np.cos(ang), np.sin(ang)
+        return np.array([c * v[0] - s * v[1], s * v[0] + c * v[1]])
+    for _ in range(60):
+        before = oracle.copy(st).bodies
+        oracle.step_(model, st, d.settings, F32(1 / 60))
+        bd = st.bodies
+        aA, aB = float(before.a[0, a]), float(before.a[0, b])
+        rA, rB = rot(aA, la), rot(aB, lb)
+        vA, vB = bd.v[0, a].astype(np.float64), bd.v[0, b].astype(np.float64)
+        wA, wB = float(bd.w[0, a]), float(bd.w[0, b])
+        tol = 2e-5 * (1 + np.abs(vA).sum() + np.abs(vB).sum() + abs(wA) + abs(wB))
+        if kind in ("revolute", "weld"):
+            assert np.abs(vB + cross_sv(wB, rB) - vA - cross_sv(wA, rA)).max() <= tol
+        if kind in ("prismatic", "weld"):
+            assert abs(wB - wA) <= tol
+        if kind == "prismatic":
+            perp = rot(aA, np.array([0.0, 1.0]))
+            dd = before.c[0, b].astype(np.float64) + rB - before.c[0, a].astype(np.float64) - rA
+            s1 = (dd + rA)[0] * perp[1] - (dd + rA)[1] * perp[0]
+            s2 = rB[0] * perp[1] - rB[1] * perp[0]
+            assert abs(np.dot(perp, vB - vA) + s2 * wB - s1 * wA) <= tol
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # continuous collision   (test_box2d_reference.py:130-155, test_toi.py:23-35)
 
