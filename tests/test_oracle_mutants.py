@@ -65,6 +65,12 @@ MUTANTS = [
     ("prismatic_mass_uncoupled", "float k12 = iA * s1 + iB * s2;\n        float k13",
      "float k12 = 0.0f;\n        float k13",
      lambda o: P.test_joint_velocity_rows_solve_the_constraint(o, "prismatic", True)),
+    ("toi_root_secant_first", "if (rc & 1) t = a1 + (target - s1) * (a2 - a1) / (s2 - s1);",
+     "if (!(rc & 1)) t = a1 + (target - s1) * (a2 - a1) / (s2 - s1);",
+     lambda o: P.test_time_of_impact_head_on_circles_root_steps(o)),
+    ("toi_root_bisection_only", "if (rc & 1) t = a1 + (target - s1) * (a2 - a1) / (s2 - s1);",
+     "if (0) t = a1 + (target - s1) * (a2 - a1) / (s2 - s1);",
+     lambda o: P.test_time_of_impact_head_on_circles_root_steps(o)),
     ("feature_key_types_swapped", "return ia | (ib << 8) | (ta << 16) | (tb << 24);",
      "return ia | (ib << 8) | (tb << 16) | (ta << 24);", lambda o: P.test_polygon_manifold_known_answers(o)),
     ("flip_keeps_feature_halves", "ids[i] = flip ? feature_key(cp2[i].ib, cp2[i].ia, cp2[i].tb, cp2[i].ta)",

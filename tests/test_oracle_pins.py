@@ -541,6 +541,56 @@ def _sweep_xf(sw, t):
     return np.array([p[0], p[1], q[0], q[1]], np.float32)
 
 
+def test_time_of_impact_head_on_circles_root_steps(oracle):
+    """b2TimeOfImpact's root finder (toi.py:420-446) alternates bisection and secant steps, bisection first, and stops
+    once |s(t) - target| < tol = slop / 4. Two circles closing head-on without rotation have a separation linear in
+    t, s(t) = s0 - t travel, so the outcome is fixed in closed form: t = 1/2 when s(1/2) is already within tol of the
+    target, else the secant step that follows lands on the root, t = (s0 - target) / travel, to float rounding
+    (where the contract alone would allow any t within tol of distance). Random speeds, directions and radii, plus
+    roots placed just beside 1/2 on either side of the tolerance."""
+    d = wd.WorldDef(S.stock())
+    g = d.add_body(wd.STATIC)
+    for r in (0.05, 0.1, 0.3):
+        d.add_circle(g, r)
+    model, _ = d.build(2)
+    slop = float(S.stock().linear_slop)
+    tol = 0.25 * slop
+    rng = np.random.default_rng(21)
+    halves = roots = 0
+    for trial in range(240):
+        fa, fb = (int(x) for x in rng.integers(0, 3, 2))
+        ra, rb = float(model.radius[fa]), float(model.radius[fb])
+        target = max(slop, ra + rb - 3 * slop)
+        u = rng.normal(size=2)
+        u /= np.linalg.norm(u)
+        travel = rng.uniform(2.5, 6.0)
+        if trial % 4 == 0:  # the root beside 1/2: inside the tolerance, or just outside it
+            gap = target + travel * 0.5 + rng.choice([-0.6, 0.6, -1.6, 1.6]) * tol
+        else:
+            gap = target + travel * rng.uniform(0.1, 0.9)
+        pa = rng.uniform(-1, 1, 2)
+        pb0 = pa + u * gap
+        pb1 = pb0 - u * travel
+        sa = np.array([0, 0, pa[0], pa[1], pa[0], pa[1], 0, 0], np.float32)
+        sb = np.array([0, 0, pb0[0], pb0[1], pb1[0], pb1[1], 0, 0], np.float32)
+        st, t = oracle.time_of_impact(model, fa, fb, sa, sb, slop)
+        assert st == 3, (trial, st)  # TOUCHING
+        # the proxies are the centres; the points separation function's axis is their direction at t = 0
+        p0, p1, q = sb[2:4].astype(np.float64), sb[4:6].astype(np.float64), sa[2:4].astype(np.float64)
+        axis = (p0 - q) / np.linalg.norm(p0 - q)
+        s0, trav = float(np.dot(p0 - q, axis)), float(np.dot(p0 - p1, axis))
+        miss = abs(s0 - 0.5 * trav - target)
+        if abs(miss - tol) < 1e-5:
+            continue  # too near the stopping test's edge for float64 to say which side float32 took
+        if miss < tol:
+            assert t == 0.5, (trial, t)
+            halves += 1
+        else:
+            assert t == pytest.approx((s0 - target) / trav, rel=2e-6, abs=2e-7), (trial, t)
+            roots += 1
+    assert halves >= 20 and roots >= 150
+
+
 def test_time_of_impact_contract(oracle):
     """b2TimeOfImpact: when it reports TOUCHING at t, the core shapes' distance at t is within target +- tol, target
     = max(slop, r_A + r_B - 3 slop), tol = slop / 4 (toi.py:372-375); when it reports SEPARATED at t = 1 they never
