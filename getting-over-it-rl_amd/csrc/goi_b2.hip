@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -328,13 +329,23 @@ __global__ void k_sincos(const float* x, float* s, float* c, int n) {
 
 // ---------------------------------------------------------------- model upload and the static BVH
 
+// The constraint and task rows of the launches one stream makes with a model: allocated on the stream's first call,
+// grown (after the stream's earlier work has finished) when a larger batch arrives on it.
+struct StreamScratch {
+    hipStream_t stream;
+    uint32_t* rows;
+    size_t words;
+};
+
 struct GoiModel {
     DModel d;
     std::vector<void*> allocs;
     int C;
-    uint32_t* scratch = nullptr;
-    size_t scratch_words = 0;
     int device = 0;
+    // One scratch buffer per stream, so that calls on different streams never share rows. `mu` is held from the
+    // lookup through the launch, so a buffer is never freed between another call's lookup and its launch.
+    std::mutex mu;
+    std::vector<StreamScratch> scratch;
 };
 
 namespace {
@@ -572,8 +583,14 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
 
 int32_t goi_model_destroy(GoiModel* M) {
     if (!M) return GOI_OK;
+    // every launch that read the model's tables or its rows has finished before they are freed
+    int cur = 0;
+    const bool switch_dev = hipGetDevice(&cur) == hipSuccess && cur != M->device;
+    if (switch_dev) (void)hipSetDevice(M->device);
+    (void)hipDeviceSynchronize();
     for (void* p : M->allocs) (void)hipFree(p);
-    if (M->scratch) (void)hipFree(M->scratch);
+    for (StreamScratch& s : M->scratch) (void)hipFree(s.rows);
+    if (switch_dev) (void)hipSetDevice(cur);
     delete M;
     return GOI_OK;
 }
@@ -671,17 +688,35 @@ static void fill_launch(Launch& L, const GoiModel* M, const GoiStateView* v, con
     L.lds_nodes = (int)std::min<size_t>((size_t)M->d.n_nodes, room);
 }
 
-// The model's scratch rows (per world: C contact rows, J joint rows), grown to the batch's pitch on demand.
-static int ensure_scratch(GoiModel* M, const GoiStateView* state) {
-    // tiles of wpw worlds: at most pitch + 63 world columns (the kernels' 32-bit offsets are checked at launch)
-    const size_t words = ((size_t)state->C * CF_N + (size_t)state->J * JF_N) * ((size_t)state->pitch + 64);
-    if (words > M->scratch_words) {
-        if (M->scratch) HIP_TRY(hipFree(M->scratch));
-        M->scratch = nullptr;
-        M->scratch_words = 0;
-        HIP_TRY(hipMalloc(&M->scratch, std::max<size_t>(words, 1) * sizeof(uint32_t)));
-        M->scratch_words = words;
+// Words of constraint and task rows a launch over `state` uses: per world C contact rows and J joint rows, in tiles of
+// wpw worlds, so at most pitch + 63 world columns (the kernels' 32-bit offsets are checked by check_view).
+static size_t scratch_words(const GoiStateView* state) {
+    return ((size_t)state->C * CF_N + (size_t)state->J * JF_N) * ((size_t)state->pitch + 64);
+}
+
+// The rows of stream st's launches with model M (M->mu held): the stream's buffer, allocated on its first call and
+// replaced by a larger one when this batch needs more. The old buffer is freed only after the stream's earlier work,
+// the only work that reads it, has finished.
+static int stream_rows(GoiModel* M, const GoiStateView* state, hipStream_t st, uint32_t** rows) {
+    const size_t words = std::max<size_t>(scratch_words(state), 1);
+    StreamScratch* e = nullptr;
+    for (StreamScratch& s : M->scratch)
+        if (s.stream == st) e = &s;
+    if (!e) {
+        M->scratch.push_back(StreamScratch{st, nullptr, 0});
+        e = &M->scratch.back();
     }
+    if (words > e->words) {
+        if (e->rows) {
+            HIP_TRY(hipStreamSynchronize(st));
+            HIP_TRY(hipFree(e->rows));
+            e->rows = nullptr;
+            e->words = 0;
+        }
+        HIP_TRY(hipMalloc(&e->rows, words * sizeof(uint32_t)));
+        e->words = words;
+    }
+    *rows = e->rows;
     return GOI_OK;
 }
 
@@ -690,22 +725,23 @@ int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSett
     return goi_step_n(model, state, settings, dt, 1, hip_stream, debug);
 }
 
-int32_t goi_step_n(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
-                   int32_t n_steps, void* hip_stream, const GoiDebug* debug) {
-    int rc = check_view(model, state, "goi_step");
+static int check_step_args(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings,
+                           int32_t n_steps, const char* who) {
+    int rc = check_view(model, state, who);
     if (rc != GOI_OK) return rc;
-    if (!settings) return fail(GOI_E_ARG, "goi_step: null settings");
+    if (!settings) return fail(GOI_E_ARG, std::string(who) + ": null settings");
     if (settings->velocity_iterations < 0 || settings->position_iterations < 0)
-        return fail(GOI_E_ARG, "goi_step: negative iteration counts");
-    if (n_steps < 0) return fail(GOI_E_ARG, "goi_step_n: negative step count");
-    if (state->n_worlds == 0 || n_steps == 0) return GOI_OK;
-    GoiModel* M = const_cast<GoiModel*>(model);
-    rc = ensure_scratch(M, state);
-    if (rc != GOI_OK) return rc;
-    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+        return fail(GOI_E_ARG, std::string(who) + ": negative iteration counts");
+    if (n_steps < 0) return fail(GOI_E_ARG, std::string(who) + ": negative step count");
+    return GOI_OK;
+}
+
+// Launches n_steps steps of every world of `state` with the constraint rows at `rows` (scratch_words(state) words).
+static int launch_step(const GoiModel* M, const GoiStateView* state, const GoiSettings* settings, float dt,
+                       int32_t n_steps, hipStream_t st, const GoiDebug* debug, uint32_t* rows) {
     Launch L;
     fill_launch(L, M, state, settings, dt);
-    L.scratch = M->scratch;
+    L.scratch = rows;
     L.n_steps = n_steps;
     if (debug) L.dbg = *debug;
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
@@ -730,19 +766,36 @@ int32_t goi_step_n(const GoiModel* model, const GoiStateView* state, const GoiSe
     return GOI_OK;
 }
 
+int32_t goi_step_n(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
+                   int32_t n_steps, void* hip_stream, const GoiDebug* debug) {
+    int rc = check_step_args(model, state, settings, n_steps, "goi_step");
+    if (rc != GOI_OK) return rc;
+    if (state->n_worlds == 0 || n_steps == 0) return GOI_OK;
+    // the handle's only mutable part is its per-stream scratch table, guarded by its mutex
+    GoiModel* M = const_cast<GoiModel*>(model);
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    std::lock_guard<std::mutex> hold(M->mu);
+    uint32_t* rows = nullptr;
+    rc = stream_rows(M, state, st, &rows);
+    if (rc != GOI_OK) return rc;
+    return launch_step(M, state, settings, dt, n_steps, st, debug, rows);
+}
+
 int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, void* hip_stream) {
     int rc = check_view(model, state, "goi_collide");
     if (rc != GOI_OK) return rc;
     if (!settings) return fail(GOI_E_ARG, "goi_collide: null settings");
     if (state->n_worlds == 0) return GOI_OK;
+    GoiModel* M = const_cast<GoiModel*>(model);
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    std::lock_guard<std::mutex> hold(M->mu);
     Launch L;
-    fill_launch(L, model, state, settings, 0.0f);
+    fill_launch(L, M, state, settings, 0.0f);
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
-    rc = ensure_scratch(const_cast<GoiModel*>(model), state);
+    rc = stream_rows(M, state, st, &L.scratch);
     if (rc != GOI_OK) return rc;
-    L.scratch = model->scratch;
     const size_t lds = block_lds_bytes(L);
-    hipLaunchKernelGGL(k_collide, dim3(grid), dim3(kBlock), lds, static_cast<hipStream_t>(hip_stream), model->d, L, 0);
+    hipLaunchKernelGGL(k_collide, dim3(grid), dim3(kBlock), lds, st, M->d, L, 0);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
 }

@@ -19,8 +19,14 @@
  * leaf (world.py:173), as the reference does.
  *
  * Threading: calls are stream-ordered and asynchronous on the given hipStream_t (NULL = default stream). A model
- * handle is read-only after creation and may be shared by calls on different streams; a state must not be stepped
- * by two calls at once.
+ * handle may be shared by calls on different streams and from different host threads. Its shape tables are
+ * read-only after creation; its one mutable part is the scratch memory of goi_step, goi_step_n and goi_collide (the
+ * constraint and task rows), which it keeps per stream: one device buffer per stream handle, allocated on that
+ * stream's first call and replaced by a larger one when a larger batch arrives on that stream (the old buffer is
+ * freed after that stream's earlier work has finished). Calls on different streams therefore never share rows, and
+ * calls on one stream are ordered by it. A mutex in the handle covers the table from lookup through launch. A state
+ * must not be stepped by two calls at once. goi_model_destroy waits for the device to finish (hipDeviceSynchronize)
+ * before freeing, and must not overlap other calls on the same handle.
  */
 #ifndef GOI_B2_H
 #define GOI_B2_H

@@ -1,0 +1,42 @@
+"""One model handle shared by calls on two streams at once (the header's threading contract).
+
+The handle keeps its constraint rows per stream, so two States stepped with one Model on two streams at the same time
+never share rows: both must equal the oracle bit for bit. Stream B also grows its rows (a larger batch after a smaller
+one) while stream A's launches are in flight.
+"""
+import numpy as np
+import pytest
+
+from util import b2, leaf_mismatches, wd
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def _first(state, n):
+    return wd.from_leaves([np.ascontiguousarray(np.asarray(x)[:n]) for x in wd.leaves(state)])
+
+
+def test_model_shared_by_two_streams(oracle):
+    s, m, st, cfg = b2.scenes.make_config(4, 2048)
+    small, large = _first(st, 256), _first(st, 1024)
+    dev_a = b2.layout.to_device(st, "cuda")
+    dev_b0 = b2.layout.to_device(small, "cuda")
+    dev_b1 = b2.layout.to_device(large, "cuda")
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    steps = 8
+    for k in range(steps):
+        with torch.cuda.stream(sa):
+            b2.step_(m, dev_a, s, cfg.dt)
+        with torch.cuda.stream(sb):
+            # the smaller batch first, then the larger one: stream B's rows grow between the two
+            b2.step_(m, dev_b0 if k < steps // 2 else dev_b1, s, cfg.dt)
+    torch.cuda.synchronize()
+    ref_a, ref_b0, ref_b1 = oracle.copy(st), oracle.copy(small), oracle.copy(large)
+    for k in range(steps):
+        oracle.step_(m, ref_a, s, cfg.dt)
+        oracle.step_(m, ref_b0 if k < steps // 2 else ref_b1, s, cfg.dt)
+    for ref, dev in ((ref_a, dev_a), (ref_b0, dev_b0), (ref_b1, dev_b1)):
+        bad = leaf_mismatches(ref, b2.layout.to_host(dev))
+        assert bad == [], bad[:4]
