@@ -60,8 +60,8 @@ class GoiDebug(ctypes.Structure):
     _fields_ = [("body_island", _P), ("contact_island", _P), ("contact_order", _P), ("n_islands", _P)]
 
 
-EXPORTS = ("goi_abi_version", "goi_model_create", "goi_model_destroy", "goi_step", "goi_step_n", "goi_collide",
-           "goi_world_manifold", "goi_apply_motor_actions", "goi_sincos", "goi_last_error")
+EXPORTS = ("goi_abi_version", "goi_model_create", "goi_model_destroy", "goi_step", "goi_step_n", "goi_step_n_noalloc",
+           "goi_collide", "goi_world_manifold", "goi_apply_motor_actions", "goi_sincos", "goi_last_error")
 
 _LIB = None
 
@@ -87,6 +87,8 @@ def lib(path=None):
     L.goi_step_n.argtypes = [_P, ctypes.POINTER(GoiStateView), ctypes.POINTER(GoiSettings), ctypes.c_float,
                              ctypes.c_int32, _P, ctypes.POINTER(GoiDebug)]
     L.goi_step_n.restype = ctypes.c_int32
+    L.goi_step_n_noalloc.argtypes = L.goi_step_n.argtypes
+    L.goi_step_n_noalloc.restype = ctypes.c_int32
     L.goi_collide.argtypes = [_P, ctypes.POINTER(GoiStateView), ctypes.POINTER(GoiSettings), _P]
     L.goi_collide.restype = ctypes.c_int32
     L.goi_world_manifold.argtypes = [_P, ctypes.POINTER(GoiStateView), _P, _P, _P, _P]

@@ -348,7 +348,38 @@ struct GoiModel {
     std::vector<StreamScratch> scratch;
 };
 
+// ---------------------------------------------------------------- the allocation-free entry point's rows
+//
+// goi_step_n_noalloc keeps its constraint and task rows in this array instead of a buffer it allocates: 2^25 words
+// (128 MiB), which every device the library runs on holds until the process ends. Host code never uses the array's
+// name as an address (on the host it is only a stand-in): goi_model_create looks up its address on the model's device
+// once (static_scratch_setup) and the entry point passes that address to the kernels. Calls that overlap on one device
+// share the array and race.
+constexpr size_t kStaticScratchWords = size_t(1) << 25;
+static __device__ __align__(256) uint32_t scratch[kStaticScratchWords];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_static_mu;
+uint32_t* g_static_rows[kMaxDevices];  // the address of `scratch` on each device, once looked up
+
+// Looks up the address of `scratch` on `device`, the current device, once per device.
+int static_scratch_setup(int device) {
+    if (device < 0 || device >= kMaxDevices) return fail(GOI_E_UNSUPPORTED, "device index above 63");
+    std::lock_guard<std::mutex> hold(g_static_mu);
+    if (g_static_rows[device]) return GOI_OK;
+    void* p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_static_rows[device] = static_cast<uint32_t*>(p);
+    return GOI_OK;
+}
+
+uint32_t* static_rows(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> hold(g_static_mu);
+    return g_static_rows[device];
+}
 
 template <typename T>
 int upload(GoiModel* M, const T* host, size_t n, const T*& dev, hipStream_t st) {
@@ -573,6 +604,7 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
         hipError_t e = hipStreamSynchronize(st);
         if (e != hipSuccess) rc = fail(GOI_E_HIP, std::string("goi_model_create: ") + hipGetErrorString(e));
     }
+    if (rc == GOI_OK) rc = static_scratch_setup(M->device);
     if (rc != GOI_OK) {
         goi_model_destroy(M);
         return rc;
@@ -779,6 +811,21 @@ int32_t goi_step_n(const GoiModel* model, const GoiStateView* state, const GoiSe
     rc = stream_rows(M, state, st, &rows);
     if (rc != GOI_OK) return rc;
     return launch_step(M, state, settings, dt, n_steps, st, debug, rows);
+}
+
+int32_t goi_step_n_noalloc(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
+                           int32_t n_steps, void* hip_stream, const GoiDebug* debug) {
+    int rc = check_step_args(model, state, settings, n_steps, "goi_step_n_noalloc");
+    if (rc != GOI_OK) return rc;
+    if (state->n_worlds == 0 || n_steps == 0) return GOI_OK;
+    if (scratch_words(state) > kStaticScratchWords)
+        return fail(GOI_E_UNSUPPORTED, "goi_step_n_noalloc: the batch needs " + std::to_string(scratch_words(state)) +
+                                           " words of constraint rows, above the static maximum of " +
+                                           std::to_string(kStaticScratchWords) +
+                                           " ((C * 54 + J * 57) * (pitch + 64) words); use goi_step_n");
+    uint32_t* rows = static_rows(model->device);
+    if (!rows) return fail(GOI_E_ARG, "goi_step_n_noalloc: the model's device has no static rows set up");
+    return launch_step(model, state, settings, dt, n_steps, static_cast<hipStream_t>(hip_stream), debug, rows);
 }
 
 int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, void* hip_stream) {

@@ -256,6 +256,17 @@ int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSett
 int32_t goi_step_n(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
                    int32_t n_steps, void* hip_stream, const GoiDebug* debug);
 
+/* goi_step_n without any allocation: the same launches and results (bit for bit), with the constraint and task rows
+ * in a static device array of the library (2^25 words = 128 MiB per device, held until the process ends) instead of
+ * the handle's per-stream buffers. No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It calls no hipMalloc,
+ * hipFree or allocating library routine. A batch needing more than the maximum, (C * 54 + J * 57) * (pitch + 64)
+ * words (about 17,600 worlds of the 4-body rig with 32 slots), returns GOI_E_UNSUPPORTED. Every call on a device
+ * shares that device's array: calls that overlap on one device (on different streams, or from different threads)
+ * race and must not be made. */
+int32_t goi_step_n_noalloc(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
+                           int32_t n_steps, void* hip_stream, const GoiDebug* debug);
+
 /* Broadphase and narrowphase only (the collide-only workload): start-of-step FindNewContacts where new_fixture
  * (step.py:50-70), then Collide (pairs.py:38-87). */
 int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings,
