@@ -34,6 +34,9 @@ RIG_LOCAL = {  # body origin in the rig frame
 MOTOR_JOINT = 1  # torso-handle revolute: the action-driven motor
 MOTOR_GAIN = F32(10.0)  # motor_speed = gain * action_x (rad/s)
 MOTOR_TORQUE = F32(40.0)  # maxMotorTorque = torque * |action| (N m)
+BOX_STACKS = 3  # the extra boxes of the large-island configuration stand in this many stacks
+STACK_LIFT = 2.6  # height of the stacks' base above the pot centre (m)
+RIG_BODIES = 4
 
 
 @dataclass(frozen=True)
@@ -44,7 +47,7 @@ class Config:
     n_rocks: int
     seed: int
     steps: int
-    capacity: int = 32
+    capacity: int = 40
     v_sigma: float = 0.0
     head_w: float = 0.0
     boxes: int = 0
@@ -57,7 +60,7 @@ CONFIGS = {
     2: Config("collide-4096", 4096, 256, 64, 1, 1, collide_only=True),
     3: Config("fullstep-4096", 4096, 1024, 256, 2, 200, v_sigma=1.0),
     4: Config("toi-16384", 16384, 1024, 256, 2, 100, v_sigma=25.0, head_w=60.0),
-    5: Config("island-65536", 65536, 2048, 512, 4, 300, capacity=64, boxes=12),
+    5: Config("island-65536", 65536, 2048, 512, 4, 300, capacity=128, boxes=12),
 }
 
 
@@ -158,15 +161,22 @@ def build_world(cfg, settings=None, edges="quad"):
     for v, _ in rocks:
         d.add_polygon(g, v, raw=True, friction=0.8)
     x0 = 20.0
-    add_rig(d, (x0, float(height_at(pts, x0)) + 2.0))
+    y0 = float(height_at(pts, x0)) + 2.0
+    add_rig(d, (x0, y0))
+    # the boxes (sides U[0.2, 0.6] m, density U[0.5, 2]) in BOX_STACKS unrotated stacks, column j's boxes on top of
+    # each other, the stacks side by side with no gap, the lowest boxes STACK_LIFT m above the pot centre (clear of
+    # the rig at any angle); place_worlds keeps this layout relative to the pot without rotating it
     rng = np.random.default_rng(1000 + cfg.seed)
-    for i in range(cfg.boxes):
-        hx, hy = rng.uniform(0.1, 0.3, 2)
-        dens = rng.uniform(0.5, 2.0)
+    sizes = [(rng.uniform(0.1, 0.3, 2), rng.uniform(0.5, 2.0)) for _ in range(cfg.boxes)]
+    pitch = 2.0 * max([float(h[0]) for h, _ in sizes], default=0.0)
+    top = [STACK_LIFT] * BOX_STACKS
+    for i, ((hx, hy), dens) in enumerate(sizes):
+        col = i % BOX_STACKS
         m = F32(dens * 4 * hx * hy)
         inertia = F32(m * F32((4 * hx * hx + 4 * hy * hy) / 12.0))
-        b = d.add_body(wd.DYNAMIC, (x0 + 1.0 + 0.7 * (i % 4), float(height_at(pts, x0)) + 3.0 + 0.8 * (i // 4)),
+        b = d.add_body(wd.DYNAMIC, (x0 + (col - (BOX_STACKS - 1) / 2.0) * pitch, y0 + top[col] + hy),
                        mass=m, inertia=inertia)
+        top[col] += 2.0 * hy
         d.add_box(b, (hx, hy), friction=0.6)
     model, state = d.build(contact_capacity=cfg.capacity)
     return model, state, pts
@@ -205,9 +215,10 @@ def fat_rows(model, state_b, rows):
 
 
 def place_worlds(cfg, model, state, pts, n=None, seed=None):
-    """A batched State of n worlds: the rig (and boxes) moved rigidly to a random pose per world (x U[0, 200] m,
-    pot centre at terrain height + 0.5 + U[0.5, 2] m, rig angle U[-pi, pi]), linear velocities N(0, v_sigma) m/s,
-    head angular velocity U[-head_w, head_w] rad/s. Fat AABBs of the moved fixtures recomputed."""
+    """A batched State of n worlds: the rig moved rigidly to a random pose per world (x U[0, 200] m, pot centre at
+    terrain height + 0.5 + U[0.5, 2] m, rig angle U[-pi, pi]) and the boxes' stacks moved with the pot, unrotated;
+    linear velocities N(0, v_sigma) m/s, head angular velocity U[-head_w, head_w] rad/s. Fat AABBs of the moved
+    fixtures recomputed."""
     n = cfg.worlds if n is None else n
     rng = np.random.default_rng(7919 * (cfg.seed + 1) if seed is None else seed)
     st = wd.batch(state, n)
@@ -219,17 +230,19 @@ def place_worlds(cfg, model, state, pts, n=None, seed=None):
     c, s = _rot(ang)
     pot = int(dyn[0])
     base = bd.xf_p[0, pot].astype(np.float64)
-    for b in dyn:
+    for i, b in enumerate(dyn):
         lx, ly = bd.xf_p[0, b].astype(np.float64) - base
-        px = (x + (c.astype(np.float64) * lx - s.astype(np.float64) * ly)).astype(F32)
-        py = (y + (s.astype(np.float64) * lx + c.astype(np.float64) * ly)).astype(F32)
+        rigid = i < RIG_BODIES
+        cb, sb = (c, s) if rigid else (np.ones(n, F32), np.zeros(n, F32))
+        px = (x + (cb.astype(np.float64) * lx - sb.astype(np.float64) * ly)).astype(F32)
+        py = (y + (sb.astype(np.float64) * lx + cb.astype(np.float64) * ly)).astype(F32)
         bd.xf_p[:, b, 0], bd.xf_p[:, b, 1] = px, py
-        bd.xf_q[:, b, 0], bd.xf_q[:, b, 1] = c, s
-        bd.a[:, b] = ang
-        bd.a0[:, b] = ang
+        bd.xf_q[:, b, 0], bd.xf_q[:, b, 1] = cb, sb
+        bd.a[:, b] = ang if rigid else 0.0
+        bd.a0[:, b] = ang if rigid else 0.0
         lc = bd.local_center[:, b]
-        cx = (px + ((c * lc[:, 0]).astype(F32) - (s * lc[:, 1]).astype(F32))).astype(F32)
-        cy = (py + ((s * lc[:, 0]).astype(F32) + (c * lc[:, 1]).astype(F32))).astype(F32)
+        cx = (px + ((cb * lc[:, 0]).astype(F32) - (sb * lc[:, 1]).astype(F32))).astype(F32)
+        cy = (py + ((sb * lc[:, 0]).astype(F32) + (cb * lc[:, 1]).astype(F32))).astype(F32)
         bd.c[:, b, 0], bd.c[:, b, 1] = cx, cy
         bd.c0[:, b, 0], bd.c0[:, b, 1] = cx, cy
         if cfg.v_sigma > 0:

@@ -6,8 +6,9 @@
 
 namespace goi {
 
-// Upper bound on contact slots per world the kernels handle (State capacity C <= kMaxC).
-constexpr int kMaxC = 64;
+// Upper bound on contact slots per world the kernels handle (State capacity C <= kMaxC). Sets of list positions are
+// 64-bit masks over one chunk of 64 positions at a time, so the walks below take the list in chunks.
+constexpr int kMaxC = 256;
 
 // The contact list (Box2D's m_contactList: newest first = descending key, pairs.py:12-13) is kept in the
 // workspace as W.order(0 .. nlive-1). build_order_block ranks the live slots once per step; Collide's destructions
@@ -16,14 +17,15 @@ constexpr int kMaxC = 64;
 // Live slots in contact-list order: W.order(0 .. n-1); returns n.
 GOI_D int list_order(const World& W) { return W.nlive(); }
 
-// The list positions i < n (n <= 64) whose slot W.order(i) satisfies pred(slot), as a bit mask: the lane group tests
-// them together; a walk then visits the set bits in list order. pred must not depend on what that walk changes for
-// the other positions.
+// The list positions q0 <= i < min(q0 + 64, n) whose slot W.order(i) satisfies pred(slot), as a bit mask (bit i - q0):
+// the lane group tests them together; a walk then visits the set bits in list order. pred must not depend on what
+// that walk changes for the other positions of the chunk.
 template <class F>
-GOI_D unsigned long long list_mask(const World& W, int n, F&& pred) {
+GOI_D unsigned long long list_mask(const World& W, int q0, int n, F&& pred) {
     unsigned long long mk = 0ull;
-    for (int i = W.sub; i < n; i += W.G)
-        if (pred(W.order(i))) mk |= 1ull << i;
+    const int e = min(q0 + 64, n);
+    for (int i = q0 + W.sub; i < e; i += W.G)
+        if (pred(W.order(i))) mk |= 1ull << (i - q0);
     return group_or(W.grp(), mk);
 }
 
@@ -132,20 +134,24 @@ static_assert(MT_N <= CF_N, "a manifold must fit a contact row");
 // it in the list.
 GOI_D int collide_mark(const DModel& m, const World& W) {
     const int n = list_order(W);
-    const unsigned long long hits =
-        list_mask(W, n, [&](int k) { return overlap(fat_of(m, W, W.fa(k)), fat_of(m, W, W.fb(k))); });
-    for (int i = W.sub; i < n; i += W.G) {
-        const int k = W.order(i);
-        if ((hits >> i) & 1ull) {
-            const int t = __popcll(hits & ((1ull << i) - 1ull));
-            W.newp(t) = k;
-            W.cisl(k) = t;
-        } else {
-            W.cisl(k) = -1;
+    int t0 = 0;  // overlapping contacts before the chunk
+    for (int q0 = 0; q0 < n; q0 += 64) {
+        const unsigned long long hits =
+            list_mask(W, q0, n, [&](int k) { return overlap(fat_of(m, W, W.fa(k)), fat_of(m, W, W.fb(k))); });
+        for (int i = q0 + W.sub; i < min(q0 + 64, n); i += W.G) {
+            const int k = W.order(i), b = i - q0;
+            if ((hits >> b) & 1ull) {
+                const int t = t0 + __popcll(hits & ((1ull << b) - 1ull));
+                W.newp(t) = k;
+                W.cisl(k) = t;
+            } else {
+                W.cisl(k) = -1;
+            }
         }
+        t0 += __popcll(hits);
     }
     group_sync();
-    return __popcll(hits);
+    return t0;
 }
 
 GOI_D void collide_task(const DModel& m, const Coop& co, int o, int i, const GoiSettings& s) {
@@ -167,66 +173,76 @@ GOI_D void collide_task(const DModel& m, const Coop& co, int o, int i, const Goi
 
 GOI_D void collide_apply(const DModel& m, const World& W, const Rows& R) {
     const int n = list_order(W);
-    // 1. per list position (split over the lane group): the contact is destroyed (its fat boxes separated), and
-    //    visiting it wakes its bodies (a destroyed contact that had points; an update that flips touching)
-    unsigned long long gone = 0ull, wakes = 0ull;
-    for (int i = W.sub; i < n; i += W.G) {
-        const int k = W.order(i);
-        const int t = W.cisl(k);
-        const bool g = t < 0;
-        const bool wk = g ? W.ccount(k) > 0 : (R.geti(t, MT_COUNT) > 0) != W.touching(k);
-        gone |= (unsigned long long)g << i;
-        wakes |= (unsigned long long)wk << i;
-    }
-    gone = group_or(W.grp(), gone);
-    wakes = group_or(W.grp(), wakes);
-    // 2. Box2D's walk with its wake cascade, on bit masks: a contact is visited when one of its bodies is awake and
-    //    not static, and a visit that wakes makes both bodies awake for the rest of the walk
-    unsigned long long awake = 0ull, visit = 0ull;
+    // The list in chunks of 64 positions, in order. A chunk's passes read and write only its own positions' slots,
+    // and the walk's wake state (awake) carries from one chunk to the next, as in Box2D's single walk.
+    unsigned long long awake = 0ull;
     for (int b = 0; b < W.B; ++b) awake |= (unsigned long long)(W.awake(b) != 0) << b;
     const unsigned long long woken0 = awake;
-    for (int i = 0; i < n; ++i) {
-        const int k = W.order(i);
-        const unsigned long long pair = (1ull << W.ba(k)) | (1ull << W.bb(k));
-        if (!(awake & pair & ~W.smask)) continue;
-        visit |= 1ull << i;
-        if ((wakes >> i) & 1ull) awake |= pair;
-    }
-    // 3. the visited contacts' destructions and updates (each touches only its own slot), split over the group, then
-    //    the wakes (b2Body::SetAwake restarts the sleep timer only of a body that was asleep)
-    for (int i = W.sub; i < n; i += W.G) {
-        if (!((visit >> i) & 1ull)) continue;
-        const int k = W.order(i);
-        if ((gone >> i) & 1ull) {
-            W.pair(k) = -1;
-            W.set_touch_count(k, false, 0);
-            continue;
+    int removed = 0;  // destroyed contacts in the chunks before
+    for (int q0 = 0; q0 < n; q0 += 64) {
+        const int e = min(q0 + 64, n);
+        // 1. per list position (split over the lane group): the contact is destroyed (its fat boxes separated), and
+        //    visiting it wakes its bodies (a destroyed contact that had points; an update that flips touching)
+        unsigned long long gone = 0ull, wakes = 0ull;
+        for (int i = q0 + W.sub; i < e; i += W.G) {
+            const int k = W.order(i);
+            const int t = W.cisl(k);
+            const bool g = t < 0;
+            const bool wk = g ? W.ccount(k) > 0 : (R.geti(t, MT_COUNT) > 0) != W.touching(k);
+            gone |= (unsigned long long)g << (i - q0);
+            wakes |= (unsigned long long)wk << (i - q0);
         }
-        const int t = W.cisl(k);
-        Manifold mf;
-        mf.mtype = R.geti(t, MT_MTYPE);
-        mf.count = R.geti(t, MT_COUNT);
-        mf.ln = R.get2(t, MT_LN);
-        mf.lp = R.get2(t, MT_LP);
-        mf.pl0 = R.get2(t, MT_PL0);
-        mf.pl1 = R.get2(t, MT_PL1);
-        mf.id0 = R.geti(t, MT_ID0);
-        mf.id1 = R.geti(t, MT_ID1);
-        contact_update(W, k, mf);
+        gone = group_or(W.grp(), gone);
+        wakes = group_or(W.grp(), wakes);
+        // 2. Box2D's walk with its wake cascade, on bit masks: a contact is visited when one of its bodies is awake
+        //    and not static, and a visit that wakes makes both bodies awake for the rest of the walk
+        unsigned long long visit = 0ull;
+        for (int i = q0; i < e; ++i) {
+            const int k = W.order(i);
+            const unsigned long long pair = (1ull << W.ba(k)) | (1ull << W.bb(k));
+            if (!(awake & pair & ~W.smask)) continue;
+            visit |= 1ull << (i - q0);
+            if ((wakes >> (i - q0)) & 1ull) awake |= pair;
+        }
+        // 3. the visited contacts' destructions and updates (each touches only its own slot), split over the group
+        for (int i = q0 + W.sub; i < e; i += W.G) {
+            if (!((visit >> (i - q0)) & 1ull)) continue;
+            const int k = W.order(i);
+            if ((gone >> (i - q0)) & 1ull) {
+                W.pair(k) = -1;
+                W.set_touch_count(k, false, 0);
+                continue;
+            }
+            const int t = W.cisl(k);
+            Manifold mf;
+            mf.mtype = R.geti(t, MT_MTYPE);
+            mf.count = R.geti(t, MT_COUNT);
+            mf.ln = R.get2(t, MT_LN);
+            mf.lp = R.get2(t, MT_LP);
+            mf.pl0 = R.get2(t, MT_PL0);
+            mf.pl1 = R.get2(t, MT_PL1);
+            mf.id0 = R.geti(t, MT_ID0);
+            mf.id1 = R.geti(t, MT_ID1);
+            contact_update(W, k, mf);
+        }
+        group_sync();
+        // 4. the destroyed contacts leave the list, the rest keep their order: a position moves down by the number of
+        //    destroyed positions before it, below every position the group has yet to read (this chunk's reads are
+        //    done, later chunks start above it)
+        const unsigned long long dead = visit & gone;
+        for (int i = q0 + W.sub; i < e; i += W.G) {
+            if ((dead >> (i - q0)) & 1ull) continue;
+            const int k = W.order(i);
+            W.order(i - removed - __popcll(dead & ((1ull << (i - q0)) - 1ull))) = k;
+        }
+        group_sync();
+        removed += __popcll(dead);
     }
+    // the wakes (b2Body::SetAwake restarts the sleep timer only of a body that was asleep)
     for (int b = W.sub; b < W.B; b += W.G)
         if (((awake & ~woken0) >> b) & 1ull) W.wake(b);
     group_sync();
-    // 4. the destroyed contacts leave the list, the rest keep their order (a position moves only down, below every
-    //    position the group has yet to read)
-    const unsigned long long dead = visit & gone;
-    for (int i = W.sub; i < n; i += W.G) {
-        if ((dead >> i) & 1ull) continue;
-        const int k = W.order(i);
-        W.order(i - __popcll(dead & ((1ull << i) - 1ull))) = k;
-    }
-    group_sync();
-    W.nlive() = n - __popcll(dead);
+    W.nlive() = n - removed;
 }
 
 // Collide for the block: called by all lanes together; `valid` marks the lanes that run a world, `leader` the first

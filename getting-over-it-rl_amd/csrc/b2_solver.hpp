@@ -12,8 +12,8 @@
 
 namespace goi {
 
-constexpr int kMaxB = 64;  // bodies per world the kernels handle
-constexpr int kMaxJ = 64;  // joints per world
+constexpr int kMaxB = 64;  // bodies per world the kernels handle (body sets are 64-bit masks)
+constexpr int kMaxJ = 64;  // joints per world (joint sets are 64-bit masks)
 
 // Per-lane view of the solver body arrays in LDS.
 struct Bodies {
@@ -55,10 +55,11 @@ struct Islands {
 // first (joints to inactive bodies skipped). Contacts and joints append to one solve order across islands.
 GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
     const int n = list_order(W);
-    unsigned long long bflag = 0ull, cflag = 0ull, jflag = 0ull;
+    unsigned long long bflag = 0ull, jflag = 0ull;
     for (int b = 0; b < W.B; ++b) I.body_island(b) = -1;
-    for (int c = 0; c < W.C; ++c) I.contact_island(c) = -1;
+    for (int c = 0; c < W.C; ++c) I.contact_island(c) = -1;  // also the "in an island" flag of each contact
     for (int j = 0; j < W.J; ++j) I.joint_island(j) = -1;
+    group_sync();
     int nisl = 0, nc = 0, nj = 0;
     for (int seed = W.B - 1; seed >= 0; --seed) {
         if ((bflag >> seed) & 1ull) continue;
@@ -71,21 +72,23 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
             const int b = W.stack(--sp);
             I.body_island(b) = isl;
             W.wake(b);
-            // b's touching contacts not yet in an island, newest first (the walk below marks only the contact it
-            // visits, so the mask of the others stays exact)
-            const unsigned long long hits = list_mask(W, n, [&](int c) {
-                return (W.ba(c) == b || W.bb(c) == b) && !((cflag >> c) & 1ull) && W.touching(c);
-            });
-            for (unsigned long long left = hits; left; left &= left - 1) {
-                const int c = W.order(__builtin_ctzll(left));
-                const int ba = W.ba(c), bb = W.bb(c);
-                I.corder(nc++) = c;
-                cflag |= 1ull << c;
-                I.contact_island(c) = isl;
-                const int other = ba == b ? bb : ba;
-                if (((bflag >> other) & 1ull) || W.is_static(other)) continue;
-                W.stack(sp++) = other;
-                bflag |= 1ull << other;
+            // b's touching contacts not yet in an island, newest first, a chunk of the list at a time (the walk
+            // marks only the contact it visits, so the mask of the chunk's others stays exact)
+            for (int q0 = 0; q0 < n; q0 += 64) {
+                const unsigned long long hits = list_mask(W, q0, n, [&](int c) {
+                    return (W.ba(c) == b || W.bb(c) == b) && I.contact_island(c) < 0 && W.touching(c);
+                });
+                for (unsigned long long left = hits; left; left &= left - 1) {
+                    const int c = W.order(q0 + __builtin_ctzll(left));
+                    const int ba = W.ba(c), bb = W.bb(c);
+                    I.corder(nc++) = c;
+                    I.contact_island(c) = isl;
+                    const int other = ba == b ? bb : ba;
+                    if (((bflag >> other) & 1ull) || W.is_static(other)) continue;
+                    W.stack(sp++) = other;
+                    bflag |= 1ull << other;
+                }
+                group_sync();
             }
             for (int j = W.J - 1; j >= 0; --j) {
                 const int ja = m.joint_a[j], jb = m.joint_b[j];

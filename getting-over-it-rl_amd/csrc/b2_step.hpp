@@ -249,31 +249,34 @@ GOI_D void put_sweep(const Rows& R, int row, int f, const Sweep& sw) {
 // pass 1; returns the number of TOI tasks, whose slots are W.newp(0 .. n-1)
 GOI_D int toi_search_prepare(const DModel& m, const World& W, const Rows& CR, const GoiSettings& s) {
     const int n = list_order(W);
-    // the contacts that need a TOI (the lane group tests them together; the walk below changes only the flag of the
-    // contact it visits), then the alignments in list order
-    const unsigned long long need = list_mask(W, n, [&](int c) {
-        if (!W.ten(c) || W.tcount(c) > kMaxSubSteps || W.tflag(c)) return false;
-        const int A = W.ba(c), Bb = W.bb(c);
-        const bool act_a = W.awake(A) && !W.is_static(A);
-        const bool act_b = W.awake(Bb) && !W.is_static(Bb);
-        return (act_a || act_b) && pair_rule(m, W, s, A, Bb);
-    });
     int nt = 0;
-    for (unsigned long long left = need; left; left &= left - 1) {
-        const int c = W.order(__builtin_ctzll(left));
-        const int fa = W.fa(c), fb = W.fb(c);
-        const int A = W.ba(c), Bb = W.bb(c);
-        const float alA = W.f(GOI_T_ALPHA0, A), alB = W.f(GOI_T_ALPHA0, Bb);
-        float alpha0 = alA;
-        if (alA < alB) { alpha0 = alB; sweep_advance(W, A, alpha0); }
-        else if (alB < alA) { alpha0 = alA; sweep_advance(W, Bb, alpha0); }
-        CR.seti(nt, TT_FA, fa);
-        CR.seti(nt, TT_FB, fb);
-        CR.setf(nt, TT_ALPHA0, alpha0);
-        put_sweep(CR, nt, TT_SA, body_sweep(W, A));
-        put_sweep(CR, nt, TT_SB, body_sweep(W, Bb));
-        W.newp(nt++) = c;
-        W.set_tflag(c, 1);  // the toi itself arrives in pass 2
+    for (int q0 = 0; q0 < n; q0 += 64) {
+        // the chunk's contacts that need a TOI (the lane group tests them together; the walk below changes only the
+        // flag of the contact it visits), then the alignments in list order
+        const unsigned long long need = list_mask(W, q0, n, [&](int c) {
+            if (!W.ten(c) || W.tcount(c) > kMaxSubSteps || W.tflag(c)) return false;
+            const int A = W.ba(c), Bb = W.bb(c);
+            const bool act_a = W.awake(A) && !W.is_static(A);
+            const bool act_b = W.awake(Bb) && !W.is_static(Bb);
+            return (act_a || act_b) && pair_rule(m, W, s, A, Bb);
+        });
+        for (unsigned long long left = need; left; left &= left - 1) {
+            const int c = W.order(q0 + __builtin_ctzll(left));
+            const int fa = W.fa(c), fb = W.fb(c);
+            const int A = W.ba(c), Bb = W.bb(c);
+            const float alA = W.f(GOI_T_ALPHA0, A), alB = W.f(GOI_T_ALPHA0, Bb);
+            float alpha0 = alA;
+            if (alA < alB) { alpha0 = alB; sweep_advance(W, A, alpha0); }
+            else if (alB < alA) { alpha0 = alA; sweep_advance(W, Bb, alpha0); }
+            CR.seti(nt, TT_FA, fa);
+            CR.seti(nt, TT_FB, fb);
+            CR.setf(nt, TT_ALPHA0, alpha0);
+            put_sweep(CR, nt, TT_SA, body_sweep(W, A));
+            put_sweep(CR, nt, TT_SB, body_sweep(W, Bb));
+            W.newp(nt++) = c;
+            W.set_tflag(c, 1);  // the toi itself arrives in pass 2
+        }
+        group_sync();
     }
     return nt;
 }
@@ -339,9 +342,10 @@ GOI_D void cs_position_row(const DModel& m, const World& W, const Rows& R, int i
     R.setf(i, CF_RADA, m.radius[fa]); R.setf(i, CF_RADB, m.radius[fb]);
 }
 
-// one TOI event (toi.py:604-716) on min_slot at min_alpha
+// one TOI event (toi.py:604-716) on min_slot at min_alpha; `stamp` (negative, below -1, distinct for each event of
+// the step) marks the event island's contacts in the workspace's cisl array, whose island ids Solve no longer needs
 GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
-                          float dt, int min_slot, float min_alpha) {
+                          float dt, int min_slot, float min_alpha, int stamp) {
     const int fa = W.fa(min_slot), fb = W.fb(min_slot);
     const int A = W.ba(min_slot), Bb = W.bb(min_slot);
     const SweepBackup bkA = backup(W, A), bkB = backup(W, Bb);
@@ -364,7 +368,8 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     // the island walk: bodyA's then bodyB's contact lists, newest first, at most 32 contacts / 64 bodies; island
     // bodies (distinct, so at most B) in the workspace's ibuf
     int nb = 0, nc = 0;
-    unsigned long long bflag = (1ull << A) | (1ull << Bb), cflag = 1ull << min_slot;
+    unsigned long long bflag = (1ull << A) | (1ull << Bb);
+    W.cisl(min_slot) = stamp;
     W.ibuf(nb++) = A;
     W.ibuf(nb++) = Bb;
     cs_position_row(m, W, CR, nc++, min_slot, mf0);
@@ -372,32 +377,40 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     for (int pi = 0; pi < 2; ++pi) {
         const int body = pi == 0 ? A : Bb;
         if (!W.is_dynamic(body)) continue;
-        // the contacts of `body` in list order (found by the lane group together)
-        const unsigned long long hits = list_mask(W, n, [&](int c) { return W.ba(c) == body || W.bb(c) == body; });
-        for (unsigned long long left = hits; left; left &= left - 1) {
-            const int c = W.order(__builtin_ctzll(left));
-            const int ca = W.ba(c), cb = W.bb(c);
-            if (nb == 2 * kMaxToiContacts || nc == kMaxToiContacts) break;
-            if ((cflag >> c) & 1ull) continue;
-            const int other = ca == body ? cb : ca;
-            if (W.is_dynamic(other) && !W.u8(GOI_B_BULLET, body) && !W.u8(GOI_B_BULLET, other)) continue;
-            if (s.unity_toi && !pair_rule(m, W, s, body, other)) continue;
-            const SweepBackup bk = backup(W, other);
-            if (!((bflag >> other) & 1ull)) body_advance(W, other, min_alpha);
-            Manifold mf;
-            evaluate(m, W.fa(c), W.fb(c), W.xf(ca), W.xf(cb), s, mf, W.grp());
-            if (contact_update(W, c, mf)) { W.wake(ca); W.wake(cb); }
-            W.set_ten(c, 1);
-            if (!W.touching(c)) {
-                restore(W, other, bk);
-                continue;
+        bool full = false;
+        // the contacts of `body` in list order, a chunk of the list at a time (found by the lane group together)
+        for (int q0 = 0; q0 < n && !full; q0 += 64) {
+            const unsigned long long hits =
+                list_mask(W, q0, n, [&](int c) { return W.ba(c) == body || W.bb(c) == body; });
+            for (unsigned long long left = hits; left; left &= left - 1) {
+                const int c = W.order(q0 + __builtin_ctzll(left));
+                const int ca = W.ba(c), cb = W.bb(c);
+                if (nb == 2 * kMaxToiContacts || nc == kMaxToiContacts) {
+                    full = true;
+                    break;
+                }
+                if (W.cisl(c) == stamp) continue;
+                const int other = ca == body ? cb : ca;
+                if (W.is_dynamic(other) && !W.u8(GOI_B_BULLET, body) && !W.u8(GOI_B_BULLET, other)) continue;
+                if (s.unity_toi && !pair_rule(m, W, s, body, other)) continue;
+                const SweepBackup bk = backup(W, other);
+                if (!((bflag >> other) & 1ull)) body_advance(W, other, min_alpha);
+                Manifold mf;
+                evaluate(m, W.fa(c), W.fb(c), W.xf(ca), W.xf(cb), s, mf, W.grp());
+                if (contact_update(W, c, mf)) { W.wake(ca); W.wake(cb); }
+                W.set_ten(c, 1);
+                if (!W.touching(c)) {
+                    restore(W, other, bk);
+                    continue;
+                }
+                W.cisl(c) = stamp;
+                cs_position_row(m, W, CR, nc++, c, mf);
+                if ((bflag >> other) & 1ull) continue;
+                bflag |= 1ull << other;
+                if (!W.is_static(other)) W.wake(other);
+                W.ibuf(nb++) = other;
             }
-            cflag |= 1ull << c;
-            cs_position_row(m, W, CR, nc++, c, mf);
-            if ((bflag >> other) & 1ull) continue;
-            bflag |= 1ull << other;
-            if (!W.is_static(other)) W.wake(other);
-            W.ibuf(nb++) = other;
+            group_sync();
         }
     }
     // b2Island::SolveTOI (toi.py:719-799)
@@ -484,23 +497,22 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         refat |= sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
     }
     // the slot loops below split over the lane group (slots are independent)
-    unsigned long long was_free = 0ull;
+    // FindNewContacts; a slot that received a new contact starts with fresh TOI state. Before it, the workspace's
+    // corder array (Solve's island order is no longer needed) takes each live slot's key, and for a free slot a mark
+    // no new contact's key can equal: the search gives keys next_key, next_key + 1, ... (fewer than C of them), so
+    // next_key - 1 (unsigned wrap) differs from each; a live slot that keeps its contact keeps its key.
+    const int mark = (int)((unsigned)W.i32(GOI_S_NEXT_KEY, 0) - 1u);
     for (int c = W.sub; c < W.C; c += W.G) {
-        if (W.pair(c) < 0) {
-            was_free |= 1ull << c;
-        } else {
+        if (W.pair(c) >= 0) {
             const int ca = W.ba(c), cb = W.bb(c);
             if (((moved >> ca) & 1ull) || ((moved >> cb) & 1ull)) W.set_tflag(c, 0);
         }
-        // FindNewContacts; a slot that received a new contact starts with fresh TOI state. The keys before it go
-        // to the workspace's corder array, which Solve's island order no longer needs.
-        W.corder(c) = W.key(c);
+        W.corder(c) = W.pair(c) >= 0 ? W.key(c) : mark;
     }
-    was_free = group_or(W.grp(), was_free);
     group_sync();
     find_new_contacts(m, W, W.i32(GOI_S_OVERFLOW, 0) == 0 ? refat : ~0ull);
     for (int c = W.sub; c < W.C; c += W.G) {
-        if (W.pair(c) >= 0 && (((was_free >> c) & 1ull) || W.corder(c) != W.key(c))) {
+        if (W.pair(c) >= 0 && W.corder(c) != W.key(c)) {
             W.set_tcount(c, 0);
             W.set_tflag(c, 0);
             W.set_ten(c, 1);
@@ -529,7 +541,7 @@ GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, co
         while (__any(found && events < max_events)) {
             const bool act = found && events < max_events;
             if (act) {
-                toi_event(m, W, bd, CR, s, dt, slot, alpha);
+                toi_event(m, W, bd, CR, s, dt, slot, alpha, -2 - events);
                 ++events;
             }
             const int nt = act ? toi_search_prepare(m, W, CR, s) : 0;

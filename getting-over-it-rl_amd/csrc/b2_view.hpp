@@ -76,12 +76,20 @@ constexpr int kBodyMirrorMutable = 10;
 // It mirrors the per-world contact metadata (pair, key, fixtures), the awake flags and the TOI bookkeeping for the
 // whole step (loaded once, written back once) and holds the per-world work arrays (contact list order, island
 // lists and stacks, new-pair buffer), which would otherwise live in private scratch memory.
+//
+// A slot's small fields share one word (o_meta): its bodies (fixture_body of fa and fb), contacts.touching and
+// contacts.count, and the TOI flag, enabled flag and count (SolveTOI's reset, world.py:157-161).
+constexpr int kMetaBodyA = 0, kMetaBodyB = 6;  // 6 bits each (at most 64 bodies)
+constexpr int kMetaTouch = 12;                 // 1 bit
+constexpr int kMetaCount = 13;                 // 2 bits (manifold point count, 0..2)
+constexpr int kMetaTFlag = 15, kMetaTEn = 16;  // 1 bit each
+constexpr int kMetaTCount = 17;                // 4 bits (at most b2_maxSubSteps + 1 = 9)
 struct Workspace {
-    int o_pair, o_key, o_fa, o_fb, o_bab, o_cmeta, o_tmeta, o_ttoi, o_order, o_newp, o_corder, o_cisl;  // [C]
-    int o_awake, o_active, o_bisl, o_stack, o_fwork, o_ibuf;                                            // [B]
-    int o_qbox;                                                                                         // [4 R]
-    int o_nlive;                                                                                        // [1]
-    int o_jorder, o_jisl;                                                                               // [J]
+    int o_pair, o_key, o_fa, o_fb, o_meta, o_ttoi, o_order, o_newp, o_corder, o_cisl;  // [C]
+    int o_awake, o_active, o_bisl, o_stack, o_fwork, o_ibuf;                            // [B]
+    int o_qbox;                                                                         // [4 R]
+    int o_nlive;                                                                        // [1]
+    int o_jorder, o_jisl;                                                               // [J]
     int o_body;  // 8 solver body fields x B
     int o_bm;    // mirrored body leaves, kBodyMirrorWords x B
     int words;   // per lane
@@ -90,8 +98,8 @@ struct Workspace {
         int o = 0;
         k.o_body = o; o += 8 * B;
         k.o_bm = o; o += kBodyMirrorWords * B;
-        k.o_pair = o; o += C; k.o_key = o; o += C; k.o_fa = o; o += C; k.o_fb = o; o += C; k.o_bab = o; o += C; k.o_cmeta = o; o += C;
-        k.o_tmeta = o; o += C; k.o_ttoi = o; o += C;
+        k.o_pair = o; o += C; k.o_key = o; o += C; k.o_fa = o; o += C; k.o_fb = o; o += C; k.o_meta = o; o += C;
+        k.o_ttoi = o; o += C;
         k.o_order = o; o += C; k.o_newp = o; o += C; k.o_corder = o; o += C; k.o_cisl = o; o += C;
         k.o_awake = o; o += B; k.o_active = o; o += B; k.o_bisl = o; o += B; k.o_stack = o; o += B; k.o_fwork = o; o += B; k.o_ibuf = o; o += B;
         k.o_jorder = o; o += J; k.o_jisl = o; o += J;
@@ -129,27 +137,33 @@ struct World {
     GOI_D int& key(int c) const { return wi(k.o_key, c); }        // contacts.key
     GOI_D int& fa(int c) const { return wi(k.o_fa, c); }          // contacts.fa
     GOI_D int& fb(int c) const { return wi(k.o_fb, c); }          // contacts.fb
-    // the bodies of a live slot's fixtures (fixture_body[fa] | fixture_body[fb] << 8)
-    GOI_D int ba(int c) const { return wi(k.o_bab, c) & 0xff; }
-    GOI_D int bb(int c) const { return (wi(k.o_bab, c) >> 8) & 0xff; }
-    GOI_D void set_bodies(int c, int a, int b) const { wi(k.o_bab, c) = a | (b << 8); }
-    // contacts.touching (bit 0) and contacts.count (bits 8-15), read from the workspace and written through
-    GOI_D bool touching(int c) const { return wi(k.o_cmeta, c) & 1; }
-    GOI_D int ccount(int c) const { return (wi(k.o_cmeta, c) >> 8) & 0xff; }
+    // the slot's packed word (see Workspace): bodies of a live slot's fixtures, touching and point count, TOI state
+    GOI_D int meta(int c) const { return wi(k.o_meta, c); }
+    GOI_D void set_meta_bits(int c, int shift, int width, int v) const {
+        int& m = wi(k.o_meta, c);
+        const int mask = ((1 << width) - 1) << shift;
+        m = (m & ~mask) | ((v << shift) & mask);
+    }
+    GOI_D int ba(int c) const { return (meta(c) >> kMetaBodyA) & 63; }
+    GOI_D int bb(int c) const { return (meta(c) >> kMetaBodyB) & 63; }
+    GOI_D void set_bodies(int c, int a, int b) const { set_meta_bits(c, kMetaBodyA, 12, a | (b << 6)); }
+    // contacts.touching and contacts.count, read from the workspace and written through to the State
+    GOI_D bool touching(int c) const { return (meta(c) >> kMetaTouch) & 1; }
+    GOI_D int ccount(int c) const { return (meta(c) >> kMetaCount) & 3; }
     GOI_D void set_touch_count(int c, bool t, int n) const {
-        wi(k.o_cmeta, c) = (t ? 1 : 0) | (n << 8);
+        set_meta_bits(c, kMetaTouch, 3, (t ? 1 : 0) | (n << 1));
         u8(GOI_C_TOUCHING, c) = t ? 1 : 0;
         i32(GOI_C_COUNT, c) = n;
     }
     GOI_D int& awake(int b) const { return wi(k.o_awake, b); }    // bodies.awake
     GOI_D int& active(int b) const { return wi(k.o_active, b); }  // bodies.active (read-only in a step)
-    // toi.flag (bit 0), toi.enabled (bit 1) and toi.count (bits 8-15) of a slot, packed in one word
-    GOI_D int tflag(int c) const { return wi(k.o_tmeta, c) & 1; }
-    GOI_D int ten(int c) const { return (wi(k.o_tmeta, c) >> 1) & 1; }
-    GOI_D int tcount(int c) const { return (wi(k.o_tmeta, c) >> 8) & 0xff; }
-    GOI_D void set_tflag(int c, int v) const { int& t = wi(k.o_tmeta, c); t = (t & ~1) | (v ? 1 : 0); }
-    GOI_D void set_ten(int c, int v) const { int& t = wi(k.o_tmeta, c); t = (t & ~2) | (v ? 2 : 0); }
-    GOI_D void set_tcount(int c, int v) const { int& t = wi(k.o_tmeta, c); t = (t & 0xff) | (v << 8); }
+    // toi.flag, toi.enabled and toi.count of a slot
+    GOI_D int tflag(int c) const { return (meta(c) >> kMetaTFlag) & 1; }
+    GOI_D int ten(int c) const { return (meta(c) >> kMetaTEn) & 1; }
+    GOI_D int tcount(int c) const { return (meta(c) >> kMetaTCount) & 15; }
+    GOI_D void set_tflag(int c, int v) const { set_meta_bits(c, kMetaTFlag, 1, v ? 1 : 0); }
+    GOI_D void set_ten(int c, int v) const { set_meta_bits(c, kMetaTEn, 1, v ? 1 : 0); }
+    GOI_D void set_tcount(int c, int v) const { set_meta_bits(c, kMetaTCount, 4, v); }
     GOI_D float& ttoi(int c) const { return wf(k.o_ttoi, c); }    // toi.toi
     // work arrays
     GOI_D int& order(int i) const { return wi(k.o_order, i); }
@@ -277,7 +291,7 @@ GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
                     bc.wi(k.o_key + c) = ky[u];
                     bc.wi(k.o_fa + c) = fa[u];
                     bc.wi(k.o_fb + c) = fb[u];
-                    bc.wi(k.o_cmeta + c) = (t[u] ? 1 : 0) | (n[u] << 8);
+                    bc.wi(k.o_meta + c) = ((t[u] ? 1 : 0) << kMetaTouch) | ((n[u] & 3) << kMetaCount);
                 }
             }
         }
@@ -331,7 +345,7 @@ GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
             }
 #pragma unroll
             for (int u = 0; u < kCopyU; ++u)
-                if (live[u]) bc.wi(k.o_bab + c0 + u * bc.stride) = ba[u] | (bb[u] << 8);
+                if (live[u]) bc.wi(k.o_meta + c0 + u * bc.stride) |= (ba[u] << kMetaBodyA) | (bb[u] << kMetaBodyB);
         }
     }
     __syncthreads();
@@ -382,14 +396,18 @@ GOI_D void store_mirror_block(const BlockCopy& bc) {
 }
 
 // SolveTOI's reset (world.py:157-161, toi.py:837) of the block's worlds: alpha0 = 0, count 0, toi 1, flag off,
-// enabled, not solved, report impulses 0. Called by every lane; ends with a barrier.
+// enabled, not solved, report impulses 0. Called by every lane; the barriers order it after the worlds' last writes
+// of their slots' packed words and before their next reads.
 GOI_D void reset_toi_block(const BlockCopy& bc) {
+    __syncthreads();
     if (bc.on) {
         const Workspace& k = bc.k;
         const int oa = k.o_bm + body_mirror_coef(GOI_T_ALPHA0) * bc.B;
         for (int b = bc.r0; b < bc.B; b += bc.stride) bc.wf(oa + b) = 0.0f;
         for (int c = bc.r0; c < bc.C; c += bc.stride) {
-            bc.wi(k.o_tmeta + c) = 2;  // count 0, enabled, no flag
+            // count 0, enabled, no flag; the slot's other fields stay
+            int& mt = bc.wi(k.o_meta + c);
+            mt = (mt & ~((1 << kMetaTFlag) | (1 << kMetaTEn) | (15 << kMetaTCount))) | (1 << kMetaTEn);
             bc.wf(k.o_ttoi + c) = 1.0f;
             bc.at<uint8_t>(GOI_T_SOLVED, c) = 0;
         }
@@ -407,10 +425,10 @@ GOI_D void store_toi_block(const BlockCopy& bc) {
     if (!bc.on) return;
     const Workspace& k = bc.k;
     for (int c = bc.r0; c < bc.C; c += bc.stride) {
-        const int t = bc.wi(k.o_tmeta + c);
-        bc.at<uint8_t>(GOI_T_FLAG, c) = (uint8_t)(t & 1);
-        bc.at<uint8_t>(GOI_T_ENABLED, c) = (uint8_t)((t >> 1) & 1);
-        bc.at<int>(GOI_T_COUNT, c) = (t >> 8) & 0xff;
+        const int t = bc.wi(k.o_meta + c);
+        bc.at<uint8_t>(GOI_T_FLAG, c) = (uint8_t)((t >> kMetaTFlag) & 1);
+        bc.at<uint8_t>(GOI_T_ENABLED, c) = (uint8_t)((t >> kMetaTEn) & 1);
+        bc.at<int>(GOI_T_COUNT, c) = (t >> kMetaTCount) & 15;
         bc.at<float>(GOI_T_TOI, c) = bc.wf(k.o_ttoi + c);
     }
 }

@@ -224,7 +224,7 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
 template <bool kMulti>
 __global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) { step_block<kMulti>(m, L); }
 
-// The same step with the world dimensions and the worlds per wave fixed at compile time (the 4-body rig with 32
+// The same step with the world dimensions and the worlds per wave fixed at compile time (the 4-body rig with 40
 // contact slots, 8 worlds per wave): every workspace offset and loop bound folds into the instructions, which
 // frees the scalar registers the runtime dimensions hold. The results are those of k_step.
 template <int kB, int kC, int kJ, int kR, int kS, bool kMulti, bool kPlain>
@@ -238,7 +238,7 @@ __global__ void __launch_bounds__(kBlock, 2) k_step_fixed(DModel m, Launch L) {
     }
     step_block<kMulti>(m, L);
 }
-constexpr int kRigB = 5, kRigC = 32, kRigJ = 3, kRigR = 4, kRigS = 8;
+constexpr int kRigB = 5, kRigC = 40, kRigJ = 3, kRigR = 4, kRigS = 8;
 
 // b2WorldManifold::Initialize (Box2D 2.3.1; the solver's prepare computes the same, contact_solver.py:60-104) of
 // every slot of every world from the bodies' transforms, one thread per (slot, world): normal [C, 2], points
@@ -460,7 +460,7 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     if (B > kMaxB) return fail(GOI_E_UNSUPPORTED, "goi_model_create: more than 64 bodies per world");
     if (J > kMaxJ) return fail(GOI_E_UNSUPPORTED, "goi_model_create: more than 64 joints per world");
     if (contact_capacity < 0 || contact_capacity > kMaxC)
-        return fail(GOI_E_UNSUPPORTED, "goi_model_create: contact capacity above 64");
+        return fail(GOI_E_UNSUPPORTED, "goi_model_create: contact capacity above 256");
     for (int j = 0; j < J; ++j) {
         const int t = desc->joint_type[j];
         if (t != GOI_REVOLUTE && t != GOI_PRISMATIC && t != GOI_WELD)

@@ -193,7 +193,7 @@ def test_config_shapes(k):
     F = m.fixture_body.shape[0]
     assert J == 3 and (B, R) == ((5, 4) if k < 5 else (17, 16))
     assert F - R == cfg.n_edges + cfg.n_rocks
-    assert C == (32 if k < 5 else 64)
+    assert C == (40 if k < 5 else 128)
     assert s.continuous_physics and not s.unity_toi and s.gravity == (F32(0), F32(-9.81))
 
 
@@ -247,7 +247,7 @@ def test_bad_arguments_fail_before_the_device():
     s, m, st, cfg = b2.scenes.make_config(1, 2)
     full_model = b2.scenes.build_world(cfg, s)[0]
     desc, keep = A.model_desc(m)
-    assert L.goi_model_create(ctypes.byref(desc), 65, None, ctypes.byref(out)) == A.GOI_E_UNSUPPORTED
+    assert L.goi_model_create(ctypes.byref(desc), 257, None, ctypes.byref(out)) == A.GOI_E_UNSUPPORTED
     assert b"capacity" in L.goi_last_error()
     with pytest.raises(ValueError):
         A.model_desc(full_model)  # the device step needs the compact layout
