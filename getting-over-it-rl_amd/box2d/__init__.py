@@ -2,7 +2,7 @@
 
     box2d = importlib.import_module("getting-over-it-rl_amd.box2d")
     d = box2d.WorldDef(box2d.Settings.stock(gravity=(0, -9.81), continuous_physics=True))
-    ...; model, state = d.build(contact_capacity=32)
+    ...; model, state = d.build(contact_capacity=40)
     model, state = box2d.prepare(model, state)                   # compact fixture layout
     dev = box2d.layout.to_device(box2d.world.batch(state, 16384))
     dev = box2d.step(model, dev, settings, dt)

@@ -1,10 +1,16 @@
-"""Host-side shape construction in float32, b2PolygonShape / b2CircleShape v2.3.1 op for op (mirror of
-goi_jax/box2d/shapes.py:1-113), the thin-quad encoding of terrain edge segments, and native b2EdgeShape /
-b2ChainShape children (which the reference does not have, shapes.py:13).
+"""Shape geometry built on the host in float32: polygons (raw and hull-built), boxes, circles, the thin-quad encoding
+of terrain segments, and native b2EdgeShape / b2ChainShape children (which the reference does not have,
+goi_jax/box2d/shapes.py:13).
 
-A fixture holds one shape. Polygons store up to 8 vertices and edge normals, padded by repeating vertex 0 (pads are
-masked by `count`); a circle stores its centre in vertex 0 and count 1; an edge stores m_vertex1, m_vertex2,
-m_vertex0, m_vertex3 in vertices 0-3 with count 2, and its m_hasVertex0 / m_hasVertex3 in the fixture's edge flags.
+Arithmetic. Every value is an IEEE binary32 rounded after each operation, in the operation order of Box2D 2.3.1's
+b2PolygonShape / b2Math code that the reference restates (goi_jax/box2d/shapes.py:16-113). The code below works on
+float32 numpy arrays: an elementwise float32 operation rounds once per element, so a vectorized expression gives the
+same bits as Box2D's scalar loop as long as each element sees the same operations in the same order.
+
+Storage. A fixture holds one shape in 8 vertex and 8 normal slots: a polygon's vertices and outward edge normals,
+the unused slots repeating slot 0 (never read: `count` masks them); a circle's centre in slot 0 with count 1; an
+edge's m_vertex1, m_vertex2, m_vertex0, m_vertex3 in slots 0-3 with count 2, its ghost flags in the fixture's edge
+flags.
 """
 import math
 
@@ -13,196 +19,218 @@ import numpy as np
 from .settings import EPSILON, MAX_POLYGON_VERTICES
 
 F32 = np.float32
-CIRCLE, EDGE, POLYGON = 0, 1, 2  # b2Shape::Type (shapes.py:13; the reference leaves out edge 1)
+CIRCLE, EDGE, POLYGON = 0, 1, 2  # b2Shape::Type (the reference's shapes.py:13 leaves out edge 1)
 EDGE_HAS_V0, EDGE_HAS_V3, EDGE_CHAIN = 1, 2, 4  # edge flags; EDGE_CHAIN: a b2ChainShape child
 
 
 def host_sin_cos(a):
-    """(float)sin((double)a), (float)cos((double)a) (math2d.py:321-325)."""
-    a = float(F32(a))
-    return F32(math.sin(a)), F32(math.cos(a))
+    """(float)sin((double)a), (float)cos((double)a): the correctly rounded float pair (math2d.py:321-325)."""
+    x = float(F32(a))
+    return F32(math.sin(x)), F32(math.cos(x))
+
+
+def _unit_rows(vx, vy):
+    """b2Vec2::Normalize of each row (x, y) of two float32 arrays: length sqrt(x x + y y); a row shorter than
+    b2_epsilon stays as it is, the others are multiplied by 1 / length."""
+    vx, vy = np.asarray(vx, F32), np.asarray(vy, F32)
+    length = np.sqrt(vx * vx + vy * vy)
+    short = length < EPSILON
+    inv = F32(1.0) / np.where(short, F32(1.0), length)
+    return np.where(short, vx, vx * inv), np.where(short, vy, vy * inv)
 
 
 def normalize_host(x, y):
-    """b2Vec2::Normalize in float32 (shapes.py:19-25)."""
-    x, y = F32(x), F32(y)
-    n = F32(np.sqrt(F32(F32(x * x) + F32(y * y))))
-    if n < EPSILON:
-        return x, y
-    inv = F32(F32(1.0) / n)
-    return F32(x * inv), F32(y * inv)
+    """b2Vec2::Normalize of one vector in float32; returns (x, y)."""
+    ux, uy = _unit_rows(np.array([x], F32), np.array([y], F32))
+    return F32(ux[0]), F32(uy[0])
 
 
 def edge_normals(v):
-    """b2PolygonShape::Set's normals: Normalize(b2Cross(v[i+1] - v[i], 1.0f)) (shapes.py:28-33)."""
+    """Outward unit normals of a CCW polygon's edges, as b2PolygonShape::Set derives them: edge i runs from vertex i
+    to vertex i + 1 (wrapping), and its normal is b2Cross(edge, 1) = (edge.y, -edge.x), normalized."""
+    v = np.asarray(v, F32)
+    ahead = np.roll(v, -1, axis=0)
+    ex, ey = ahead[:, 0] - v[:, 0], ahead[:, 1] - v[:, 1]
+    nx, ny = _unit_rows(ey, -ex)
+    return np.stack([nx, ny], axis=1)
+
+
+def _check_strictly_convex_ccw(v):
+    """Every vertex j other than the ends of edge i lies strictly left of it: cross(edge_i, v_j - v_i) > 0, each
+    term rounded as Box2D's b2Cross of float32 vectors."""
     n = len(v)
-    out = np.zeros((n, 2), F32)
-    for i in range(n):
-        j = i + 1 if i + 1 < n else 0
-        ex, ey = F32(v[j][0] - v[i][0]), F32(v[j][1] - v[i][1])
-        out[i] = normalize_host(F32(F32(1.0) * ey), F32(F32(-1.0) * ex))
-    return out
+    start = v[:, None, :]                                    # (n, 1, 2): v_i
+    edge = (np.roll(v, -1, axis=0) - v)[:, None, :]          # (n, 1, 2): v_{i+1} - v_i
+    others = np.stack([np.roll(v, -k, axis=0) for k in range(2, n)], axis=1) - start  # (n, n-2, 2): v_{i+k} - v_i
+    turn = edge[..., 0] * others[..., 1] - edge[..., 1] * others[..., 0]
+    if not (turn > 0).all():
+        raise ValueError("raw polygon vertices must turn strictly left (convex, counter-clockwise)")
 
 
 def polygon_raw(vertices):
-    """Vertices verbatim (strictly convex, CCW), normals as Set derives them (shapes.py:36-47)."""
+    """A polygon whose vertices are taken as given (3 to 8, strictly convex, counter-clockwise), with the normals
+    b2PolygonShape::Set would compute (the reference oracle's raw polygons, capi.cpp:378-416). Returns
+    (vertices (n, 2), normals (n, 2)) float32."""
     v = np.asarray(vertices, F32).reshape(-1, 2)
     if not 3 <= len(v) <= MAX_POLYGON_VERTICES:
-        raise ValueError("polygon needs 3..8 vertices")
-    for i in range(len(v)):
-        e = v[(i + 1) % len(v)] - v[i]
-        for k in range(2, len(v)):
-            d = v[(i + k) % len(v)] - v[i]
-            if F32(F32(e[0] * d[1]) - F32(e[1] * d[0])) <= 0:
-                raise ValueError("polygon not strictly convex CCW")
+        raise ValueError(f"a raw polygon takes 3 to {MAX_POLYGON_VERTICES} vertices, not {len(v)}")
+    _check_strictly_convex_ccw(v)
     return v, edge_normals(v)
+
+
+def _merge_close_points(pts, tol):
+    """The points in order, skipping each one whose squared distance to a point already kept is below tol
+    (b2PolygonShape::Set's weld of points closer than sqrt(0.5 * linearSlop))."""
+    kept = np.zeros((0, 2), F32)
+    for p in pts:
+        d = kept - p
+        if len(kept) == 0 or (d[:, 0] * d[:, 0] + d[:, 1] * d[:, 1] >= tol).all():
+            kept = np.vstack([kept, p[None]])
+    return kept
+
+
+def _wrap_hull(pts):
+    """Indices of the convex hull of pts in counter-clockwise order, by Box2D 2.3.1's gift wrap: start at the
+    largest x (the lowest y among equal x); from each hull vertex h, scan the points in index order keeping a
+    candidate c, which a point p replaces when p lies right of h->c (cross < 0), or on that line farther from h; the
+    candidate is seeded with the first point other than h."""
+    count = len(pts)
+    first = 0
+    for i in range(1, count):
+        x, y = pts[i]
+        if x > pts[first][0] or (x == pts[first][0] and y < pts[first][1]):
+            first = i
+    order = [first]
+    while len(order) <= MAX_POLYGON_VERTICES:
+        here = pts[order[-1]]
+        pick = 0
+        for i in range(1, count):
+            if pick == order[-1]:
+                pick = i
+                continue
+            to_pick = pts[pick] - here
+            to_i = pts[i] - here
+            turn = to_pick[0] * to_i[1] - to_pick[1] * to_i[0]
+            if turn < 0:
+                pick = i
+            if turn == 0 and to_i[0] * to_i[0] + to_i[1] * to_i[1] > to_pick[0] * to_pick[0] + to_pick[1] * to_pick[1]:
+                pick = i
+        if pick == first:
+            return order
+        order.append(pick)
+    raise ValueError("the gift wrap did not come back to its first vertex")
 
 
 def polygon_set(vertices, linear_slop):
-    """b2PolygonShape::Set v2.3.1: weld near points, gift-wrap from the rightmost (then lowest) point, CCW
-    (shapes.py:50-89). Raises where Box2D would fall back to SetAsBox(1, 1)."""
-    pts = [tuple(F32(c) for c in p) for p in np.asarray(vertices, F32).reshape(-1, 2)[:MAX_POLYGON_VERTICES]]
-    weld = F32(F32(0.5) * F32(linear_slop))
-    ps = []
-    for v in pts:
-        keep = True
-        for q in ps:
-            dx, dy = F32(v[0] - q[0]), F32(v[1] - q[1])
-            if F32(F32(dx * dx) + F32(dy * dy)) < weld:
-                keep = False
-                break
-        if keep:
-            ps.append(v)
-    n = len(ps)
-    if n < 3:
-        raise ValueError("degenerate polygon (Box2D would use SetAsBox(1, 1))")
-    i0, x0 = 0, ps[0][0]
-    for i in range(1, n):
-        x = ps[i][0]
-        if x > x0 or (x == x0 and ps[i][1] < ps[i0][1]):
-            i0, x0 = i, x
-    hull, ih = [], i0
-    while True:
-        hull.append(ih)
-        ie = 0
-        for j in range(1, n):
-            if ie == ih:
-                ie = j
-                continue
-            rx, ry = F32(ps[ie][0] - ps[hull[-1]][0]), F32(ps[ie][1] - ps[hull[-1]][1])
-            vx, vy = F32(ps[j][0] - ps[hull[-1]][0]), F32(ps[j][1] - ps[hull[-1]][1])
-            c = F32(F32(rx * vy) - F32(ry * vx))
-            if c < 0:
-                ie = j
-            if c == 0 and F32(F32(vx * vx) + F32(vy * vy)) > F32(F32(rx * rx) + F32(ry * ry)):
-                ie = j
-        ih = ie
-        if ie == i0:
-            break
-        if len(hull) > MAX_POLYGON_VERTICES:
-            raise ValueError("hull did not close")
+    """b2PolygonShape::Set (v2.3.1): the first 8 points, close points merged, their convex hull counter-clockwise,
+    and the edge normals. Raises ValueError where Box2D would give up and build SetAsBox(1, 1) instead (fewer than 3
+    distinct points, or a hull of fewer than 3 vertices). Returns (vertices, normals) float32."""
+    pts = np.asarray(vertices, F32).reshape(-1, 2)[:MAX_POLYGON_VERTICES]
+    pts = _merge_close_points(pts, F32(0.5) * F32(linear_slop))
+    if len(pts) < 3:
+        raise ValueError("fewer than 3 distinct points: b2PolygonShape::Set would fall back to a 1 x 1 box")
+    hull = _wrap_hull(pts)
     if len(hull) < 3:
-        raise ValueError("degenerate hull")
-    v = np.array([ps[i] for i in hull], F32)
+        raise ValueError("the points are collinear: b2PolygonShape::Set would fall back to a 1 x 1 box")
+    v = pts[hull]
     return v, edge_normals(v)
 
 
+def _rotate_rows(c, s, pts):
+    """b2Mul(b2Rot, v) of each row: (c x - s y, s x + c y)."""
+    x, y = pts[:, 0], pts[:, 1]
+    return np.stack([c * x - s * y, s * x + c * y], axis=1)
+
+
 def box(hx, hy, center=(0.0, 0.0), angle=0.0):
-    """b2PolygonShape::SetAsBox(hx, hy, center, angle) (shapes.py:92-104)."""
+    """b2PolygonShape::SetAsBox(hx, hy, center, angle): the corners (-hx, -hy), (hx, -hy), (hx, hy), (-hx, hy) and
+    the normals -y, +x, +y, -x, rotated by the correctly rounded b2Rot(angle), the corners then moved by center.
+    Returns (vertices, normals) float32."""
     hx, hy = F32(hx), F32(hy)
-    v = np.array([(-hx, -hy), (hx, -hy), (hx, hy), (-hx, hy)], F32)
-    n = np.array([(0, -1), (1, 0), (0, 1), (-1, 0)], F32)
+    corners = np.array([[-hx, -hy], [hx, -hy], [hx, hy], [-hx, hy]], F32)
+    normals = np.array([[0, -1], [1, 0], [0, 1], [-1, 0]], F32)
     s, c = host_sin_cos(angle)
-    px, py = F32(center[0]), F32(center[1])
-    for i in range(4):
-        x, y = v[i]
-        v[i] = (F32(F32(F32(c * x) - F32(s * y)) + px), F32(F32(F32(s * x) + F32(c * y)) + py))
-        x, y = n[i]
-        n[i] = (F32(F32(c * x) - F32(s * y)), F32(F32(s * x) + F32(c * y)))
-    return v, n
+    shift = np.array([center[0], center[1]], F32)
+    return _rotate_rows(c, s, corners) + shift, _rotate_rows(c, s, normals)
 
 
 def edge_quad(p0, p1, thickness=0.1):
-    """A terrain edge segment [p0, p1] as a thin CCW quad {p0, p1, p1 - t n, p0 - t n} (n the segment's left normal,
-    t the thickness), so the contact uses reference-defined polygon code. Raw vertices, Set's normals."""
-    p0 = np.asarray(p0, np.float64)
-    p1 = np.asarray(p1, np.float64)
-    d = p1 - p0
-    n = np.array([-d[1], d[0]]) / np.hypot(d[0], d[1])
-    q = np.array([p0 - thickness * n, p1 - thickness * n, p1, p0], np.float64)  # CCW: bottom edge first
-    return polygon_raw(q.astype(F32))
+    """A terrain segment [p0, p1] as a thin counter-clockwise quad {p0 - t n, p1 - t n, p1, p0} (n the segment's
+    unit left normal, t the thickness; computed in float64, then rounded to float32), so that its contacts use
+    reference-defined polygon code. Raw vertices, with Set's normals."""
+    a, b = np.asarray(p0, np.float64), np.asarray(p1, np.float64)
+    along = b - a
+    left = np.array([-along[1], along[0]]) / np.hypot(along[0], along[1])
+    drop = thickness * left
+    return polygon_raw(np.array([a - drop, b - drop, b, a]).astype(F32))
 
 
 def centroid_raw(v):
-    """m_centroid of a raw polygon as the reference oracle's builder accumulates it: sum of (1/n) * v[i] in order
-    (goi_jax/reference/capi.cpp:386-401)."""
-    n = len(v)
-    inv = F32(F32(1.0) / F32(n))
-    cx, cy = F32(0), F32(0)
-    for x, y in np.asarray(v, F32):
-        cx, cy = F32(cx + F32(inv * x)), F32(cy + F32(inv * y))
-    return np.array([cx, cy], F32)
+    """m_centroid of a raw polygon as the reference oracle's builder accumulates it: a running float32 sum of
+    (1 / n) v_i over the vertices in order (capi.cpp:386-401)."""
+    v = np.asarray(v, F32)
+    weight = F32(1.0) / F32(len(v))
+    acc = np.zeros(2, F32)
+    for p in v:
+        acc = acc + weight * p
+    return acc
 
 
 def centroid_set(v):
-    """ComputeCentroid of b2PolygonShape::Set v2.3.1: area-weighted triangle fan from the origin."""
+    """ComputeCentroid of b2PolygonShape::Set (v2.3.1): triangles fanned from the origin (its reference point p1 =
+    (0, 0)), each of signed area 0.5 cross(v_i, v_{i+1}) adding area / 3 times (p1 + v_i + v_{i+1}); the sum over
+    the total area."""
     v = np.asarray(v, F32)
-    n = len(v)
-    cx, cy, area = F32(0), F32(0), F32(0)
-    inv3 = F32(F32(1.0) / F32(3.0))
-    for i in range(n):
-        p2, p3 = v[i], v[i + 1] if i + 1 < n else v[0]
-        e1x, e1y, e2x, e2y = p2[0], p2[1], p3[0], p3[1]  # p1 = (0, 0)
-        d = F32(F32(e1x * e2y) - F32(e1y * e2x))
-        tri = F32(F32(0.5) * d)
-        area = F32(area + tri)
-        w = F32(tri * inv3)
-        sx, sy = F32(F32(F32(0) + p2[0]) + p3[0]), F32(F32(F32(0) + p2[1]) + p3[1])
-        cx, cy = F32(cx + F32(w * sx)), F32(cy + F32(w * sy))
-    inv = F32(F32(1.0) / area)
-    return np.array([F32(inv * cx), F32(inv * cy)], F32)
+    third = F32(1.0) / F32(3.0)
+    acc, area = np.zeros(2, F32), F32(0.0)
+    for p, q in zip(v, np.roll(v, -1, axis=0)):
+        tri = F32(0.5) * (p[0] * q[1] - p[1] * q[0])
+        area = area + tri
+        acc = acc + (tri * third) * ((F32(0.0) + p) + q)
+    return (F32(1.0) / area) * acc
 
 
 def edge_shape(v1, v2, v0=None, v3=None):
-    """b2EdgeShape::Set(v1, v2) with optional ghost vertices: ((4, 2) vertices v1, v2, v0, v3; flags)."""
-    v = np.zeros((4, 2), F32)
-    v[0], v[1] = v1, v2
+    """b2EdgeShape::Set(v1, v2) with the optional ghost vertices v0 (before v1) and v3 (after v2): ((4, 2) float32
+    slots v1, v2, v0, v3; the EDGE_HAS_V0 / EDGE_HAS_V3 flags of the ghosts given)."""
+    slots = np.zeros((4, 2), F32)
+    slots[0], slots[1] = v1, v2
     flags = 0
-    if v0 is not None:
-        v[2], flags = v0, flags | EDGE_HAS_V0
-    if v3 is not None:
-        v[3], flags = v3, flags | EDGE_HAS_V3
-    if v[0][0] == v[1][0] and v[0][1] == v[1][1]:
-        raise ValueError("degenerate edge")
-    return v, flags
+    for slot, ghost, flag in ((2, v0, EDGE_HAS_V0), (3, v3, EDGE_HAS_V3)):
+        if ghost is not None:
+            slots[slot] = ghost
+            flags |= flag
+    if (slots[0] == slots[1]).all():
+        raise ValueError("an edge needs two distinct end points")
+    return slots, flags
 
 
 def chain_edges(points, loop=False, prev_vertex=None, next_vertex=None):
-    """The child edges of b2ChainShape::CreateChain / CreateLoop (GetChildEdge): edge i runs from point i to i + 1,
-    with ghosts at points i - 1 and i + 2 where they exist (the loop wraps; an open chain takes prev_vertex /
-    next_vertex, b2ChainShape::SetPrevVertex / SetNextVertex, at its ends)."""
-    p = [np.asarray(x, F32) for x in np.asarray(points, F32).reshape(-1, 2)]
+    """The child edges of b2ChainShape::CreateChain / CreateLoop (GetChildEdge): edge i runs from point i to point
+    i + 1, with ghosts at points i - 1 and i + 2 where they exist. A loop closes back to its first point and wraps its
+    ghosts; an open chain takes prev_vertex / next_vertex (b2ChainShape::SetPrevVertex / SetNextVertex) as the ghosts
+    of its end edges. Returns [(slots, flags)], each flagged EDGE_CHAIN."""
+    p = np.asarray(points, F32).reshape(-1, 2)
     if loop:
         if len(p) < 3:
-            raise ValueError("a loop needs 3 points")
+            raise ValueError("a chain loop needs at least 3 points")
         prev_vertex, next_vertex = p[-1], p[1]
-        p = p + [p[0]]
+        p = np.vstack([p, p[:1]])
     if len(p) < 2:
-        raise ValueError("a chain needs 2 points")
-    n = len(p)
-    out = []
-    for i in range(n - 1):
-        v0 = p[i - 1] if i > 0 else prev_vertex
-        v3 = p[i + 2] if i < n - 2 else next_vertex
-        v, flags = edge_shape(p[i], p[i + 1], v0, v3)
-        out.append((v, flags | EDGE_CHAIN))
-    return out
+        raise ValueError("a chain needs at least 2 points")
+    last = len(p) - 2  # index of the last edge
+    children = []
+    for i in range(last + 1):
+        before = p[i - 1] if i > 0 else prev_vertex
+        after = p[i + 2] if i < last else next_vertex
+        slots, flags = edge_shape(p[i], p[i + 1], before, after)
+        children.append((slots, flags | EDGE_CHAIN))
+    return children
 
 
 def pad(v, n):
-    """(8, 2) vertex and normal arrays, padded with vertex/normal 0 (shapes.py:107-113)."""
-    k = len(v)
-    vv = np.repeat(np.asarray(v, F32)[:1], MAX_POLYGON_VERTICES, axis=0)
-    nn = np.repeat(np.asarray(n, F32)[:1], MAX_POLYGON_VERTICES, axis=0)
-    vv[:k], nn[:k] = v, n
-    return vv, nn
+    """The (8, 2) vertex and normal slots of a shape: its rows, then copies of row 0."""
+    v, n = np.asarray(v, F32), np.asarray(n, F32)
+    fill = MAX_POLYGON_VERTICES - len(v)
+    return (np.concatenate([v, np.repeat(v[:1], fill, axis=0)]),
+            np.concatenate([n, np.repeat(n[:1], fill, axis=0)]))

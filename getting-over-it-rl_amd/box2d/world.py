@@ -8,6 +8,7 @@ Indices follow creation order, which Box2D uses for its orderings (world.py:7-11
 body list is newest first, so islands are seeded from the highest index); fixture i gets broad-phase proxy id order i;
 joint i is the i-th created (each body's joint list is newest first).
 """
+from dataclasses import dataclass
 from typing import NamedTuple
 
 import numpy as np
@@ -222,113 +223,214 @@ def from_leaves(vals):
                  **scal)
 
 
-def _filter_ok(fa, fb, masks):
-    """Filter::ShouldCollide (world.py:177-183): the layer matrix when given, else b2ContactFilter's groups."""
-    if masks is not None:
-        return bool((int(masks[fa["layer"]]) & 0xFFFFFFFF) >> fb["layer"] & 1)
-    if fa["group"] == fb["group"] and fa["group"] != 0:
-        return fa["group"] > 0
-    return (fa["mask"] & fb["category"]) != 0 and (fa["category"] & fb["mask"]) != 0
+# ---------------------------------------------------------------- the host builder
+
+@dataclass
+class BodyRecord:
+    """One body as the builder holds it before build(): the b2Body fields the State starts from (float32)."""
+    type: int
+    origin: np.ndarray          # b2Transform.p
+    rot: tuple                  # b2Rot (cos, sin) of `angle`, correctly rounded
+    angle: np.float32
+    center: np.ndarray          # world centre of mass (b2Sweep.c)
+    local_center: np.ndarray
+    v: np.ndarray
+    w: np.float32
+    mass: np.float32
+    inv_mass: np.float32
+    inertia: np.float32
+    inv_inertia: np.float32
+    linear_damping: np.float32
+    angular_damping: np.float32
+    gravity_scale: np.float32
+    fixed_rotation: bool
+    bullet: bool
+    continuous: bool
+    awake: bool
+    allow_sleep: bool
+    active: bool
+
+
+@dataclass
+class FixtureRecord:
+    body: int
+    shape_type: int
+    verts: np.ndarray           # (8, 2) slots
+    normals: np.ndarray         # (8, 2) slots
+    count: int
+    radius: np.float32
+    friction: np.float32
+    restitution: np.float32
+    sensor: bool
+    layer: int
+    category: int
+    mask: int
+    group: int
+    centroid: np.ndarray
+    edge_flags: int
+
+
+@dataclass
+class JointRecord:
+    type: int
+    body_a: int
+    body_b: int
+    anchor_a: tuple
+    anchor_b: tuple
+    reference_angle: float
+    axis: tuple
+    enable_limit: bool
+    lower: float
+    upper: float
+    motor_speed: float
+    max_motor: float
+    enable_motor: bool
+    frequency: float
+    damping: float
+    collide_connected: bool
+
+
+def mass_update(body, mass, center, inertia, exact=True):
+    """The reference oracle's goi_b2_body_set_mass on a dynamic BodyRecord (world.py:220-244, capi.cpp:234-252):
+    b2MassData {mass, center, I = inertia + mass |center|^2} through b2Body::SetMassData (a non-positive mass counts
+    as 1; the rotational inertia about the centre I - m |c|^2 only when positive and the rotation is free), then, with
+    `exact`, the given centroidal inertia verbatim; the centre of mass moves with the new local centre and the
+    velocity picks up b2Cross(w, centre shift). float32, one rounding per operation in that order."""
+    if body.type != DYNAMIC:
+        return
+    m_in, i_com = F32(mass), F32(inertia)
+    lc = np.array([center[0], center[1]], F32)
+    c2 = lc[0] * lc[0] + lc[1] * lc[1]
+    i_total = i_com + m_in * c2
+    m = m_in if m_in > 0 else F32(1)
+    body.mass, body.inv_mass = m, F32(1) / m
+    body.inertia = body.inv_inertia = F32(0)
+    if i_total > 0 and not body.fixed_rotation:
+        body.inertia = i_total - m * c2
+        body.inv_inertia = F32(1) / body.inertia
+    if exact and body.inertia > 0:
+        body.inertia, body.inv_inertia = i_com, F32(1) / i_com
+    cos, sin = body.rot
+    moved = np.array([(cos * lc[0] - sin * lc[1]) + body.origin[0], (sin * lc[0] + cos * lc[1]) + body.origin[1]],
+                     F32)
+    shift = moved - body.center
+    body.local_center, body.center = lc, moved
+    body.v = np.array([body.v[0] - body.w * shift[1], body.v[1] + body.w * shift[0]], F32)
+
+
+def _collide_filter(fx, layer_masks, rows):
+    """Filter::ShouldCollide of fixtures `rows` (a slice) against every fixture (the reference oracle's contact
+    filter, world.py:177-183), as a (len(rows), F) boolean matrix: with a layer matrix, bit layer(b) of
+    layer_masks[layer(a)]; otherwise b2ContactFilter: a shared non-zero group decides by its sign, else category and
+    mask must match both ways."""
+    layer = np.array([f.layer for f in fx], np.int64)
+    if layer_masks is not None:
+        mine = np.array([int(layer_masks[x]) & 0xFFFFFFFF for x in layer[rows]], np.int64)
+        return ((mine[:, None] >> layer[None, :]) & 1) == 1
+    group = np.array([f.group for f in fx], np.int64)
+    cat = np.array([f.category for f in fx], np.int64)
+    msk = np.array([f.mask for f in fx], np.int64)
+    g = group[rows][:, None]
+    same_group = (g == group[None, :]) & (g != 0)
+    by_bits = ((msk[rows][:, None] & cat[None, :]) != 0) & ((cat[rows][:, None] & msk[None, :]) != 0)
+    return np.where(same_group, g > 0, by_bits)
 
 
 class WorldDef:
-    """Host-side builder (world.py:186-387): same methods, defaults and float32 arithmetic."""
+    """Host-side builder with the reference's methods and defaults (world.py:186-387): bodies, fixtures and joints are
+    recorded in creation order (which Box2D's orderings follow) and laid out as the Model and State by build()."""
 
     def __init__(self, settings=None, layer_masks=None):
         self.settings = settings or Settings()
         self.layer_masks = layer_masks
-        self.bodies, self.fixtures, self.joints = [], [], []
+        self.bodies: list = []    # BodyRecord
+        self.fixtures: list = []  # FixtureRecord
+        self.joints: list = []    # JointRecord
+
+    # ---- bodies
 
     def add_body(self, type=DYNAMIC, position=(0, 0), angle=0.0, velocity=(0, 0), angular_velocity=0.0, *,
                  mass=None, center=(0, 0), inertia=0.0, exact_inertia=True, linear_damping=0.0,
                  angular_damping=0.0, gravity_scale=1.0, fixed_rotation=False, bullet=False, continuous=False,
                  awake=True, allow_sleep=True, active=True):
-        a = F32(angle)
-        s, c = shapes.host_sin_cos(a)
-        b = dict(type=type, active=active, awake=awake, allow_sleep=allow_sleep, bullet=bullet,
-                 continuous=continuous, fixed_rotation=fixed_rotation, p=np.array(position, F32), q=(c, s),
-                 local_center=np.zeros(2, F32), c=np.array(position, F32), a=a, v=np.zeros(2, F32), w=F32(0),
-                 mass=F32(1 if type == DYNAMIC else 0), inv_mass=F32(1 if type == DYNAMIC else 0),
-                 inertia=F32(0), inv_inertia=F32(0), linear_damping=F32(linear_damping),
-                 angular_damping=F32(angular_damping), gravity_scale=F32(gravity_scale), sleep_time=F32(0))
-        self.bodies.append(b)
-        bid = len(self.bodies) - 1
+        """A body at `position` and `angle`; a dynamic body starts with unit mass until set_mass (or `mass`) gives
+        its mass data. A non-static body given a velocity is woken to take it, unless awake=False asks it to sleep,
+        which zeroes the velocity again (b2Body::SetAwake(false)). Returns the body id."""
+        ang = F32(angle)
+        sin, cos = shapes.host_sin_cos(ang)
+        unit = F32(1 if type == DYNAMIC else 0)
+        here = np.array(position, F32)
+        rec = BodyRecord(type=type, origin=here, rot=(cos, sin), angle=ang, center=here.copy(),
+                         local_center=np.zeros(2, F32), v=np.zeros(2, F32), w=F32(0), mass=unit, inv_mass=unit,
+                         inertia=F32(0), inv_inertia=F32(0), linear_damping=F32(linear_damping),
+                         angular_damping=F32(angular_damping), gravity_scale=F32(gravity_scale),
+                         fixed_rotation=bool(fixed_rotation), bullet=bool(bullet), continuous=bool(continuous),
+                         awake=bool(awake), allow_sleep=bool(allow_sleep), active=bool(active))
+        self.bodies.append(rec)
         if mass is not None:
-            self.set_mass(bid, mass, center, inertia, exact_inertia)
-        if type != STATIC and (velocity[0] or velocity[1] or angular_velocity):
-            b["v"], b["w"] = np.array(velocity, F32), F32(angular_velocity)
-            b["awake"] = True
-            if not awake:  # the reference builder re-sleeps it: SetAwake(false) zeroes the velocity
-                b["awake"], b["v"], b["w"] = False, np.zeros(2, F32), F32(0)
-        return bid
+            mass_update(rec, mass, center, inertia, exact_inertia)
+        moving = velocity[0] or velocity[1] or angular_velocity
+        if type != STATIC and moving:
+            rec.awake = bool(awake)
+            if awake:
+                rec.v, rec.w = np.array(velocity, F32), F32(angular_velocity)
+            else:
+                rec.v, rec.w = np.zeros(2, F32), F32(0)
+        return len(self.bodies) - 1
 
     def set_mass(self, body, mass, center=(0, 0), inertia=0.0, exact=True):
-        """goi_b2_body_set_mass (world.py:220-244): b2MassData.I = I_com + m |c|^2, b2Body::SetMassData, then
-        (exact) the given I_com verbatim."""
-        b = self.bodies[body]
-        if b["type"] != DYNAMIC:
-            return
-        mass, cx, cy, icom = F32(mass), F32(center[0]), F32(center[1]), F32(inertia)
-        cc = F32(F32(cx * cx) + F32(cy * cy))
-        md_i = F32(icom + F32(mass * cc))
-        m = mass if mass > 0 else F32(1)
-        b["mass"], b["inv_mass"] = m, F32(F32(1) / m)
-        b["inertia"], b["inv_inertia"] = F32(0), F32(0)
-        if md_i > 0 and not b["fixed_rotation"]:
-            b["inertia"] = F32(md_i - F32(m * cc))
-            b["inv_inertia"] = F32(F32(1) / b["inertia"])
-        if exact and b["inertia"] > 0:
-            b["inertia"], b["inv_inertia"] = icom, F32(F32(1) / icom)
-        old = b["c"].copy()
-        c, s = b["q"]
-        px, py = b["p"]
-        b["local_center"] = np.array([cx, cy], F32)
-        b["c"] = np.array([F32(F32(F32(c * cx) - F32(s * cy)) + px), F32(F32(F32(s * cx) + F32(c * cy)) + py)], F32)
-        dx, dy = F32(b["c"][0] - old[0]), F32(b["c"][1] - old[1])
-        w = b["w"]
-        b["v"] = np.array([F32(b["v"][0] + F32(-w * dy)), F32(b["v"][1] + F32(w * dx))], F32)
+        """Mass data of a dynamic body (goi_b2_body_set_mass; see mass_update). No effect on other bodies."""
+        mass_update(self.bodies[body], mass, center, inertia, exact)
+
+    # ---- fixtures
 
     def _add_fixture(self, body, shape_type, verts, normals, radius, friction, restitution, sensor, layer,
                      category, mask, group, centroid=(0.0, 0.0), edge_flags=0, count=None):
-        vv, nn = shapes.pad(verts, normals)
-        self.fixtures.append(dict(body=body, shape_type=shape_type, verts=vv, normals=nn,
-                                  count=len(verts) if count is None else count, radius=F32(radius),
-                                  friction=F32(friction), restitution=F32(restitution), sensor=bool(sensor),
-                                  layer=int(layer) & 31, category=category, mask=mask, group=group,
-                                  centroid=np.asarray(centroid, F32), edge_flags=int(edge_flags)))
+        slots_v, slots_n = shapes.pad(verts, normals)
+        self.fixtures.append(FixtureRecord(
+            body=body, shape_type=shape_type, verts=slots_v, normals=slots_n,
+            count=len(verts) if count is None else count, radius=F32(radius), friction=F32(friction),
+            restitution=F32(restitution), sensor=bool(sensor), layer=int(layer) & 31, category=category, mask=mask,
+            group=group, centroid=np.asarray(centroid, F32), edge_flags=int(edge_flags)))
         return len(self.fixtures) - 1
 
     def add_polygon(self, body, vertices, radius=None, raw=False, *, friction=0.2, restitution=0.0, density=0.0,
                     sensor=False, layer=0, category=1, mask=0xFFFF, group=0):
-        v, n = shapes.polygon_raw(vertices) if raw else shapes.polygon_set(vertices, self.settings.linear_slop)
-        r = self.settings.polygon_radius if radius is None else radius
-        c = shapes.centroid_raw(v) if raw else shapes.centroid_set(v)
-        return self._add_fixture(body, shapes.POLYGON, v, n, r, friction, restitution, sensor, layer, category,
-                                 mask, group, centroid=c)
+        """A polygon: vertices as given (raw; strictly convex CCW) or through b2PolygonShape::Set's hull."""
+        if raw:
+            v, n = shapes.polygon_raw(vertices)
+            centroid = shapes.centroid_raw(v)
+        else:
+            v, n = shapes.polygon_set(vertices, self.settings.linear_slop)
+            centroid = shapes.centroid_set(v)
+        skin = self.settings.polygon_radius if radius is None else radius
+        return self._add_fixture(body, shapes.POLYGON, v, n, skin, friction, restitution, sensor, layer, category,
+                                 mask, group, centroid=centroid)
 
     def add_box(self, body, half_extents, center=(0, 0), angle=0.0, radius=None, *, friction=0.2, restitution=0.0,
                 density=0.0, sensor=False, layer=0, category=1, mask=0xFFFF, group=0):
+        """b2PolygonShape::SetAsBox(hx, hy, center, angle)."""
         v, n = shapes.box(half_extents[0], half_extents[1], center, angle)
-        r = self.settings.polygon_radius if radius is None else radius
-        return self._add_fixture(body, shapes.POLYGON, v, n, r, friction, restitution, sensor, layer, category,
+        skin = self.settings.polygon_radius if radius is None else radius
+        return self._add_fixture(body, shapes.POLYGON, v, n, skin, friction, restitution, sensor, layer, category,
                                  mask, group, centroid=center)
 
     def add_circle(self, body, radius, center=(0, 0), *, friction=0.2, restitution=0.0, density=0.0, sensor=False,
                    layer=0, category=1, mask=0xFFFF, group=0):
-        v = np.array([center], F32)
-        return self._add_fixture(body, shapes.CIRCLE, v, np.zeros((1, 2), F32), radius, friction, restitution,
-                                 sensor, layer, category, mask, group)
+        """A circle of `radius` centred at `center` in body coordinates."""
+        return self._add_fixture(body, shapes.CIRCLE, np.array([center], F32), np.zeros((1, 2), F32), radius,
+                                 friction, restitution, sensor, layer, category, mask, group)
 
     def add_edge(self, body, p0, p1, thickness=0.1, *, friction=0.2, restitution=0.0, layer=0, category=1,
                  mask=0xFFFF, group=0):
-        """A terrain edge segment as a thin polygon quad (shapes.edge_quad)."""
+        """A terrain segment as a thin polygon quad (shapes.edge_quad)."""
         v, n = shapes.edge_quad(p0, p1, thickness)
         return self._add_fixture(body, shapes.POLYGON, v, n, self.settings.polygon_radius, friction, restitution,
                                  False, layer, category, mask, group, centroid=shapes.centroid_raw(v))
 
     def _add_edge_shape(self, body, v, flags, friction, restitution, layer, category, mask, group):
-        if self.bodies[body]["type"] != STATIC:
-            raise ValueError("edge shapes belong to static bodies (the terrain)")
+        if self.bodies[body].type != STATIC:
+            raise ValueError("edge and chain shapes go on static bodies only (they are terrain)")
         return self._add_fixture(body, shapes.EDGE, v, np.zeros((4, 2), F32), self.settings.polygon_radius,
                                  friction, restitution, False, layer, category, mask, group, edge_flags=flags,
                                  count=2)
@@ -346,108 +448,129 @@ class WorldDef:
         return [self._add_edge_shape(body, v, flags, friction, restitution, layer, category, mask, group)
                 for v, flags in shapes.chain_edges(points, loop, prev_vertex, next_vertex)]
 
-    def _add_joint(self, **j):
-        self.joints.append(j)
+    # ---- joints (anchors in each body's frame, angles in radians)
+
+    def _joint(self, kind, body_a, body_b, anchor_a, anchor_b, reference_angle, collide, axis=(1, 0),
+               limits=None, motor_speed=0.0, max_motor=0.0, enable_motor=False, frequency=0.0, damping=0.0):
+        lo, hi = (0.0, 0.0) if limits is None else limits
+        self.joints.append(JointRecord(
+            type=kind, body_a=body_a, body_b=body_b, anchor_a=anchor_a, anchor_b=anchor_b,
+            reference_angle=reference_angle, axis=axis, enable_limit=limits is not None, lower=lo, upper=hi,
+            motor_speed=motor_speed, max_motor=max_motor, enable_motor=enable_motor, frequency=frequency,
+            damping=damping, collide_connected=collide))
         return len(self.joints) - 1
 
     def add_revolute(self, body_a, body_b, anchor_a=(0, 0), anchor_b=(0, 0), reference_angle=0.0, *,
                      limits=None, motor_speed=0.0, max_motor_torque=0.0, enable_motor=False, collide=False):
-        lo, hi = limits if limits is not None else (0.0, 0.0)
-        return self._add_joint(type=REVOLUTE, a=body_a, b=body_b, la=anchor_a, lb=anchor_b, ref=reference_angle,
-                               axis=(1, 0), enable_limit=limits is not None, lower=lo, upper=hi,
-                               motor_speed=motor_speed, max_motor=max_motor_torque, enable_motor=enable_motor,
-                               frequency=0.0, damping=0.0, collide=collide)
+        return self._joint(REVOLUTE, body_a, body_b, anchor_a, anchor_b, reference_angle, collide, limits=limits,
+                           motor_speed=motor_speed, max_motor=max_motor_torque, enable_motor=enable_motor)
 
     def add_prismatic(self, body_a, body_b, anchor_a=(0, 0), anchor_b=(0, 0), axis=(1, 0), reference_angle=0.0, *,
                       limits=None, motor_speed=0.0, max_motor_force=0.0, enable_motor=False, collide=False):
-        lo, hi = limits if limits is not None else (0.0, 0.0)
-        return self._add_joint(type=PRISMATIC, a=body_a, b=body_b, la=anchor_a, lb=anchor_b, ref=reference_angle,
-                               axis=axis, enable_limit=limits is not None, lower=lo, upper=hi,
-                               motor_speed=motor_speed, max_motor=max_motor_force, enable_motor=enable_motor,
-                               frequency=0.0, damping=0.0, collide=collide)
+        return self._joint(PRISMATIC, body_a, body_b, anchor_a, anchor_b, reference_angle, collide, axis=axis,
+                           limits=limits, motor_speed=motor_speed, max_motor=max_motor_force,
+                           enable_motor=enable_motor)
 
     def add_weld(self, body_a, body_b, anchor_a=(0, 0), anchor_b=(0, 0), reference_angle=0.0, *, frequency=0.0,
                  damping=0.0, collide=False):
-        return self._add_joint(type=WELD, a=body_a, b=body_b, la=anchor_a, lb=anchor_b, ref=reference_angle,
-                               axis=(1, 0), enable_limit=False, lower=0.0, upper=0.0, motor_speed=0.0,
-                               max_motor=0.0, enable_motor=False, frequency=frequency, damping=damping,
-                               collide=collide)
+        return self._joint(WELD, body_a, body_b, anchor_a, anchor_b, reference_angle, collide, frequency=frequency,
+                           damping=damping)
+
+    # ---- build
 
     def candidate_pairs(self):
-        """b2BroadPhase::UpdatePairs order with b2Contact::Create's swap (world.py:308-329): a polygon before a
-        circle, an edge before either (b2Contact's registry); no contact between two edges."""
-        no_collide = {frozenset((j["a"], j["b"])) for j in self.joints if not j["collide"]}
+        """Every fixture pair that can ever make a contact, in b2BroadPhase::UpdatePairs order (ascending lower
+        fixture, then higher), as an (P, 2) int32 array of (fixture A, fixture B) in b2Contact::Create's order: an
+        edge before any other shape, a polygon before a circle, else the lower index first (world.py:308-329 and
+        b2Contact's registry for edges). Left out for good: two fixtures of one body, a sensor, two static bodies,
+        bodies joined with collideConnected false, the contact filter, and two edges."""
+        fx = self.fixtures
+        F = len(fx)
+        if F == 0:
+            return np.zeros((0, 2), I32)
+        body = np.array([f.body for f in fx], np.int64)
+        kind = np.array([f.shape_type for f in fx], np.int64)
+        sensor = np.array([f.sensor for f in fx], bool)
+        static = np.array([self.bodies[b].type == STATIC for b in body], bool)
+        joined = np.zeros((len(self.bodies),) * 2, bool)
+        for j in self.joints:
+            if not j.collide_connected:
+                joined[j.body_a, j.body_b] = joined[j.body_b, j.body_a] = True
         out = []
-        fs, bs = self.fixtures, self.bodies
-        static_body = [b["type"] == STATIC for b in bs]
-        for i, fi in enumerate(fs):
-            for k in range(i + 1, len(fs)):
-                fk = fs[k]
-                if fi["body"] == fk["body"] or fi["sensor"] or fk["sensor"]:
-                    continue
-                if static_body[fi["body"]] and static_body[fk["body"]]:
-                    continue
-                if frozenset((fi["body"], fk["body"])) in no_collide or not _filter_ok(fi, fk, self.layer_masks):
-                    continue
-                ti, tk = fi["shape_type"], fk["shape_type"]
-                if ti == shapes.EDGE and tk == shapes.EDGE:
-                    continue
-                if (ti == shapes.CIRCLE and tk == shapes.POLYGON) or (tk == shapes.EDGE and ti != shapes.EDGE):
-                    out.append((k, i))
-                else:
-                    out.append((i, k))
-        return out
+        for r0 in range(0, F, 512):  # row blocks bound the (rows, F) temporaries
+            rows = slice(r0, min(r0 + 512, F))
+            ok = _collide_filter(fx, self.layer_masks, rows)
+            ok &= body[rows, None] != body[None, :]
+            ok &= ~(sensor[rows, None] | sensor[None, :])
+            ok &= ~(static[rows, None] & static[None, :])
+            ok &= ~joined[body[rows, None], body[None, :]]
+            ok &= ~((kind[rows, None] == shapes.EDGE) & (kind[None, :] == shapes.EDGE))
+            ok &= np.arange(r0, rows.stop)[:, None] < np.arange(F)[None, :]  # each pair once, lower index first
+            lo, hi = np.nonzero(ok)  # row-major: ascending lower index, then higher
+            lo = lo + r0
+            swap = ((kind[lo] == shapes.CIRCLE) & (kind[hi] == shapes.POLYGON)) | \
+                   ((kind[hi] == shapes.EDGE) & (kind[lo] != shapes.EDGE))
+            out.append(np.stack([np.where(swap, hi, lo), np.where(swap, lo, hi)], axis=1))
+        return np.concatenate(out).astype(I32)
 
     def build(self, contact_capacity=16):
-        """(Model, State) as numpy (no batch axis); fat AABBs as b2BroadPhase::CreateProxy gives them; contacts start
-        empty with new_fixture set (world.py:331-386)."""
-        B, F, J, C = len(self.bodies), len(self.fixtures), len(self.joints), contact_capacity
-        bs, fs, js = self.bodies, self.fixtures, self.joints
+        """(Model, State) as numpy arrays without a batch axis: fat AABBs as b2BroadPhase::CreateProxy gives them,
+        an empty contact table of `contact_capacity` slots and new_fixture set, as after CreateFixture
+        (world.py:331-386)."""
+        bodies, fixtures, joints = self.bodies, self.fixtures, self.joints
+        B, F, J = len(bodies), len(fixtures), len(joints)
+
+        def col(records, pick, dtype, tail=()):
+            return np.array([pick(r) for r in records], dtype).reshape((len(records),) + tail)
+
         pairs = self.candidate_pairs()
-        arr = lambda key, dt=F32: np.array([x[key] for x in bs], dt)  # noqa: E731
-        q = np.array([b["q"] for b in bs], F32).reshape(B, 2)
-        bodies = Bodies(
-            type=arr("type", I32), active=arr("active", bool), awake=arr("awake", bool),
-            allow_sleep=arr("allow_sleep", bool), bullet=arr("bullet", bool), continuous=arr("continuous", bool),
-            sleep_time=arr("sleep_time"), xf_p=np.array([b["p"] for b in bs], F32).reshape(B, 2), xf_q=q,
-            local_center=np.array([b["local_center"] for b in bs], F32).reshape(B, 2),
-            c0=np.array([b["c"] for b in bs], F32).reshape(B, 2), c=np.array([b["c"] for b in bs], F32).reshape(B, 2),
-            a0=arr("a"), a=arr("a"), v=np.array([b["v"] for b in bs], F32).reshape(B, 2), w=arr("w"),
-            force=np.zeros((B, 2), F32), torque=np.zeros(B, F32), mass=arr("mass"), inv_mass=arr("inv_mass"),
-            inertia=arr("inertia"), inv_inertia=arr("inv_inertia"), linear_damping=arr("linear_damping"),
-            angular_damping=arr("angular_damping"), gravity_scale=arr("gravity_scale"))
-        farr = lambda key, dt=F32, shape=(): np.array([f[key] for f in fs], dt).reshape((F,) + shape)  # noqa: E731
-        jarr = lambda key, dt=F32, shape=(): np.array([j[key] for j in js], dt).reshape((J,) + shape)  # noqa: E731
-        axes = []
-        for j in js:  # prismatic axis normalized twice, as the reference oracle does (world.py:352-356)
-            x, y = shapes.normalize_host(*shapes.normalize_host(F32(j["axis"][0]), F32(j["axis"][1])))
-            axes.append(((x, y), (F32(-F32(1) * y), F32(F32(1) * x))))
+        centers = col(bodies, lambda b: b.center, F32, (2,))
+        bd = Bodies(
+            type=col(bodies, lambda b: b.type, I32), active=col(bodies, lambda b: b.active, bool),
+            awake=col(bodies, lambda b: b.awake, bool), allow_sleep=col(bodies, lambda b: b.allow_sleep, bool),
+            bullet=col(bodies, lambda b: b.bullet, bool), continuous=col(bodies, lambda b: b.continuous, bool),
+            sleep_time=np.zeros(B, F32), xf_p=col(bodies, lambda b: b.origin, F32, (2,)),
+            xf_q=col(bodies, lambda b: b.rot, F32, (2,)), local_center=col(bodies, lambda b: b.local_center, F32, (2,)),
+            c0=centers.copy(), c=centers, a0=col(bodies, lambda b: b.angle, F32), a=col(bodies, lambda b: b.angle, F32),
+            v=col(bodies, lambda b: b.v, F32, (2,)), w=col(bodies, lambda b: b.w, F32), force=np.zeros((B, 2), F32),
+            torque=np.zeros(B, F32), mass=col(bodies, lambda b: b.mass, F32),
+            inv_mass=col(bodies, lambda b: b.inv_mass, F32), inertia=col(bodies, lambda b: b.inertia, F32),
+            inv_inertia=col(bodies, lambda b: b.inv_inertia, F32),
+            linear_damping=col(bodies, lambda b: b.linear_damping, F32),
+            angular_damping=col(bodies, lambda b: b.angular_damping, F32),
+            gravity_scale=col(bodies, lambda b: b.gravity_scale, F32))
+        # prismatic axis: normalized twice, as the reference oracle does (its builder, then the b2PrismaticJoint
+        # constructor; world.py:352-356); the y axis is b2Cross(1, x axis) = (-x.y, x.x)
+        ax = np.array([shapes.normalize_host(*shapes.normalize_host(j.axis[0], j.axis[1])) for j in joints],
+                      F32).reshape(J, 2)
         model = Model(
-            fixture_body=farr("body", I32), shape_type=farr("shape_type", I32), radius=farr("radius"),
-            count=farr("count", I32), verts=farr("verts", F32, (MAX_POLYGON_VERTICES, 2)),
-            normals=farr("normals", F32, (MAX_POLYGON_VERTICES, 2)),
-            joint_type=jarr("type", I32), joint_a=jarr("a", I32), joint_b=jarr("b", I32),
-            local_anchor_a=jarr("la", F32, (2,)), local_anchor_b=jarr("lb", F32, (2,)),
-            local_axis_a=np.array([a[0] for a in axes], F32).reshape(J, 2),
-            local_yaxis_a=np.array([a[1] for a in axes], F32).reshape(J, 2),
-            reference_angle=jarr("ref"),
-            pair_a=np.array([p[0] for p in pairs], I32).reshape(-1),
-            pair_b=np.array([p[1] for p in pairs], I32).reshape(-1),
-            toi_bodies=bodies.bullet | bodies.continuous, body_type=bodies.type.copy(),
-            centroid=farr("centroid", F32, (2,)), edge_flags=farr("edge_flags", I32))
-        fb = model.fixture_body
-        fat = fixture_fat_host(model, bodies.xf_p[fb, 0], bodies.xf_p[fb, 1], q[fb, 0], q[fb, 1])
-        fixtures = Fixtures(friction=farr("friction"), restitution=farr("restitution"), fat=fat)
-        joints = Joints(
-            enable_motor=jarr("enable_motor", bool), motor_speed=jarr("motor_speed"), max_motor=jarr("max_motor"),
-            enable_limit=jarr("enable_limit", bool), lower=jarr("lower"), upper=jarr("upper"),
-            frequency=jarr("frequency"), damping=jarr("damping"), impulse=np.zeros((J, 3), F32),
-            motor_impulse=np.zeros(J, F32), limit_state=np.zeros(J, I32), lower_impulse=np.zeros(J, F32),
-            upper_impulse=np.zeros(J, F32))
-        state = State(bodies=bodies, fixtures=fixtures, joints=joints, contacts=empty_contacts(C),
+            fixture_body=col(fixtures, lambda f: f.body, I32), shape_type=col(fixtures, lambda f: f.shape_type, I32),
+            radius=col(fixtures, lambda f: f.radius, F32), count=col(fixtures, lambda f: f.count, I32),
+            verts=col(fixtures, lambda f: f.verts, F32, (MAX_POLYGON_VERTICES, 2)),
+            normals=col(fixtures, lambda f: f.normals, F32, (MAX_POLYGON_VERTICES, 2)),
+            joint_type=col(joints, lambda j: j.type, I32), joint_a=col(joints, lambda j: j.body_a, I32),
+            joint_b=col(joints, lambda j: j.body_b, I32), local_anchor_a=col(joints, lambda j: j.anchor_a, F32, (2,)),
+            local_anchor_b=col(joints, lambda j: j.anchor_b, F32, (2,)), local_axis_a=ax,
+            local_yaxis_a=np.stack([-ax[:, 1], ax[:, 0]], axis=1).reshape(J, 2),
+            reference_angle=col(joints, lambda j: j.reference_angle, F32),
+            pair_a=np.ascontiguousarray(pairs[:, 0]), pair_b=np.ascontiguousarray(pairs[:, 1]),
+            toi_bodies=bd.bullet | bd.continuous, body_type=bd.type.copy(),
+            centroid=col(fixtures, lambda f: f.centroid, F32, (2,)), edge_flags=col(fixtures, lambda f: f.edge_flags, I32))
+        owner = model.fixture_body
+        fat = fixture_fat_host(model, bd.xf_p[owner, 0], bd.xf_p[owner, 1], bd.xf_q[owner, 0], bd.xf_q[owner, 1])
+        fxs = Fixtures(friction=col(fixtures, lambda f: f.friction, F32),
+                       restitution=col(fixtures, lambda f: f.restitution, F32), fat=fat)
+        jn = Joints(
+            enable_motor=col(joints, lambda j: j.enable_motor, bool), motor_speed=col(joints, lambda j: j.motor_speed, F32),
+            max_motor=col(joints, lambda j: j.max_motor, F32), enable_limit=col(joints, lambda j: j.enable_limit, bool),
+            lower=col(joints, lambda j: j.lower, F32), upper=col(joints, lambda j: j.upper, F32),
+            frequency=col(joints, lambda j: j.frequency, F32), damping=col(joints, lambda j: j.damping, F32),
+            impulse=np.zeros((J, 3), F32), motor_impulse=np.zeros(J, F32), limit_state=np.zeros(J, I32),
+            lower_impulse=np.zeros(J, F32), upper_impulse=np.zeros(J, F32))
+        state = State(bodies=bd, fixtures=fxs, joints=jn, contacts=empty_contacts(contact_capacity),
                       gravity=np.array(self.settings.gravity, F32), inv_dt0=np.asarray(F32(0)),
-                      next_key=np.asarray(I32(0)), new_fixture=np.asarray(len(fs) > 0),
-                      overflow=np.asarray(I32(0)), toi=empty_toi(B, C))
+                      next_key=np.asarray(I32(0)), new_fixture=np.asarray(F > 0), overflow=np.asarray(I32(0)),
+                      toi=empty_toi(B, contact_capacity))
         return model, state
 
 
@@ -478,21 +601,21 @@ def fixture_fat_host(model, px, py, c, s):
     return out
 
 
+def _blank(group, dims, fill):
+    """The leaves of one State group (in LEAVES order) for capacities dims = (B, R, J, C), zero except the given fill
+    values by leaf name."""
+    return [np.full(leaf_shape(inner, dims), fill.get(name, 0), dt)
+            for g, name, dt, inner in LEAVES if g == group]
+
+
 def empty_contacts(C):
-    z = lambda *s: np.zeros((C,) + s, F32)  # noqa: E731
-    zi = lambda *s: np.zeros((C,) + s, I32)  # noqa: E731
-    return Contacts(pair=np.full((C,), -1, I32), fa=zi(), fb=zi(), key=zi(), touching=np.zeros((C,), bool),
-                    mtype=zi(), count=zi(), local_normal=z(2), local_point=z(2), point_local=z(2, 2),
-                    point_id=zi(2), normal_impulse=z(2), tangent_impulse=z(2), friction=z(), restitution=z(),
-                    tangent_speed=z())
+    """An empty contact table of C slots: every slot free (pair -1), everything else zero."""
+    return Contacts(*_blank("contacts", (0, 0, 0, C), {"pair": -1}))
 
 
 def empty_toi(B, C):
-    """ContactTOI as SolveTOI resets it (world.py:157-161)."""
-    return ContactTOI(alpha0=np.zeros((B,), F32), count=np.zeros((C,), I32), toi=np.ones((C,), F32),
-                      flag=np.zeros((C,), bool), enabled=np.ones((C,), bool), solved=np.zeros((C,), bool),
-                      normal_impulse=np.zeros((C, 2), F32), tangent_impulse=np.zeros((C, 2), F32),
-                      events=np.asarray(I32(0)))
+    """ContactTOI as SolveTOI resets it (world.py:157-161): toi 1 and enabled, everything else zero or false."""
+    return ContactTOI(*_blank("toi", (B, 0, 0, C), {"toi": 1, "enabled": True}))
 
 
 # ---------------------------------------------------------------- compact fixture layout (world.py:400-563)
@@ -502,28 +625,36 @@ def is_compact(model, state):
 
 
 def compact_model(model, state):
-    """The Model with the compact fixture tables (world.py:437-472) from a full-layout State (any leading batch
-    axes) whose static-body fixture rows agree in every world. Idempotent."""
+    """The Model with the compact fixture tables (world.py:437-472), from a full-layout State with any leading batch
+    axes: static bodies' fixtures keep their fat AABB, friction and restitution once in the Model (fixture_slot -1),
+    the others get State rows in fixture order. Requires body types and the static fixtures' rows to be the same in
+    every world (a step never changes them). A Model that already has the tables is returned as it is."""
     if model.fixture_slot is not None:
         return model
-    btype = np.asarray(state.bodies.type).reshape(-1, np.asarray(state.bodies.type).shape[-1])
-    if not (btype == btype[0]).all():
-        raise ValueError("compact_model: body types differ between worlds")
-    fb = np.asarray(model.fixture_body)
-    static = btype[0][fb] == STATIC
-    F = fb.shape[0]
-    fat = np.asarray(state.fixtures.fat).reshape(-1, F, 4)
-    fr = np.asarray(state.fixtures.friction).reshape(-1, F)
-    rs = np.asarray(state.fixtures.restitution).reshape(-1, F)
-    for name, a in (("fat", fat), ("friction", fr), ("restitution", rs)):
-        if not (a[:, static] == a[:1, static]).all():
-            raise ValueError(f"compact_model: static fixtures' {name} differs between worlds")
-    rows = np.nonzero(~static)[0].astype(I32)
+    types = np.asarray(state.bodies.type)
+    types = types.reshape(-1, types.shape[-1])
+    shared = types[0]
+    if (types != shared).any():
+        raise ValueError("compact_model: the worlds' body types differ, so static fixtures cannot be shared")
+    owner = np.asarray(model.fixture_body)
+    F = owner.shape[0]
+    on_static = shared[owner] == STATIC
+    per_world = {"fat": np.asarray(state.fixtures.fat).reshape(-1, F, 4),
+                 "friction": np.asarray(state.fixtures.friction).reshape(-1, F),
+                 "restitution": np.asarray(state.fixtures.restitution).reshape(-1, F)}
+    tables = {}
+    for name, rows in per_world.items():
+        if (rows[:, on_static] != rows[:1, on_static]).any():
+            raise ValueError(f"compact_model: a static fixture's {name} differs between worlds")
+        table = np.zeros_like(rows[0])
+        table[on_static] = rows[0][on_static]
+        tables[name] = table
+    moving = np.flatnonzero(~on_static).astype(I32)
     slot = np.full(F, -1, I32)
-    slot[rows] = np.arange(len(rows), dtype=I32)
-    keep = lambda a: np.where(static.reshape((F,) + (1,) * (a.ndim - 1)), a, 0).astype(a.dtype)  # noqa: E731
-    return model._replace(fixture_slot=slot, slot_fixture=rows, static_fat=keep(fat[0]),
-                          static_friction=keep(fr[0]), static_restitution=keep(rs[0]), body_type=btype[0].copy())
+    slot[moving] = np.arange(moving.size, dtype=I32)
+    return model._replace(fixture_slot=slot, slot_fixture=moving, static_fat=tables["fat"],
+                          static_friction=tables["friction"], static_restitution=tables["restitution"],
+                          body_type=shared.copy())
 
 
 def compact_state(model, state):

@@ -160,10 +160,10 @@ def test_edge_polygon_matches_thin_quad(oracle):
     collider as from b2CollidePolygons against the thin quad under the same segment (both skins are b2_polygonRadius);
     the incident vertices (feature index B) agree too."""
     rng = np.random.default_rng(5)
-    d = wd.WorldDef(S.stock())
-    g = d.add_body(wd.STATIC)
-    shapes = [d.add_box(g, (0.4, 0.2)), d.add_polygon(g, [(0, 0), (0.6, 0.1), (0.2, 0.5)]),
-              d.add_polygon(g, [(0.3 * np.cos(a), 0.3 * np.sin(a)) for a in np.arange(5) * 2 * np.pi / 5])]
+
+    def add_shapes(d, g):
+        return [d.add_box(g, (0.4, 0.2)), d.add_polygon(g, [(0, 0), (0.6, 0.1), (0.2, 0.5)]),
+                d.add_polygon(g, [(0.3 * np.cos(a), 0.3 * np.sin(a)) for a in np.arange(5) * 2 * np.pi / 5])]
     found = 0
     for ang in (0.0, 0.3):
         p0, p1 = np.array([-3 * np.cos(ang), -3 * np.sin(ang)]), np.array([3 * np.cos(ang), 3 * np.sin(ang)])
@@ -171,10 +171,7 @@ def test_edge_polygon_matches_thin_quad(oracle):
         g2 = d2.add_body(wd.STATIC)
         e = d2.add_segment(g2, p0, p1)
         q = d2.add_edge(g2, p0, p1)
-        for fi in shapes:
-            fx = d.fixtures[fi]
-            d2._add_fixture(g2, fx["shape_type"], fx["verts"][:fx["count"]], fx["normals"][:fx["count"]],
-                            fx["radius"], 0.2, 0.0, False, 0, 1, 0xFFFF, 0, centroid=fx["centroid"])
+        assert add_shapes(d2, g2) == [2, 3, 4]
         m, _ = d2.build(2)
         t, nrm = p1 / 3.0, np.array([-np.sin(ang), np.cos(ang)])
         for _ in range(300):

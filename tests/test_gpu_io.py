@@ -3,6 +3,7 @@ import numpy as np
 import pytest
 
 from util import b2, leaf_mismatches, perturbed, wd
+import scene_defs
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -31,7 +32,7 @@ def test_world_manifolds_match_host_getter(oracle, name, steps):
     """Every slot of 16 perturbed worlds after some steps: the device kernel and the host getter compute
     b2WorldManifold::Initialize with the same float32 operations, so they agree bit for bit (free slots and slots
     without points read zero on both)."""
-    s, m, st = b2.scenes.build_test_scene(name, iterations=(8, 3))
+    s, m, st = scene_defs.build_test_scene(name, iterations=(8, 3))
     dev = b2.layout.to_device(perturbed(st, 16, seed=7), "cuda")
     for _ in range(steps):
         b2.step_(m, dev, s, 1.0 / 60.0)
@@ -60,7 +61,7 @@ def test_world_manifolds_config4(oracle):
 def test_dlpack_round_trip(oracle):
     """A batch-major State handed over by DLPack (torch tensors on the GPU, as a JAX or CuPy producer would) steps
     like the oracle, and to_dlpack hands back batch-major copies that numpy and torch consumers read unchanged."""
-    s, m, st = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+    s, m, st = scene_defs.build_test_scene("pile", iterations=(8, 3))
     st = perturbed(st, 8, seed=1)
     producer = wd.from_leaves([torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in wd.leaves(st)])
     dev = b2.io.from_dlpack(producer, "cuda")

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 from util import b2, leaf_mismatches, perturbed, wd
+import scene_defs
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -36,17 +37,17 @@ def _run(model, state, settings, dt, steps, oracle, actions=None, every=1, on_st
     return ref
 
 
-@pytest.mark.parametrize("name", list(b2.scenes.TEST_SCENES))
+@pytest.mark.parametrize("name", list(scene_defs.TEST_SCENES))
 def test_scene_parity(name, oracle):
     """Every test scene, 64 perturbed copies, 90 steps, stock iteration counts."""
-    s, m, st = b2.scenes.build_test_scene(name, iterations=(8, 3))
+    s, m, st = scene_defs.build_test_scene(name, iterations=(8, 3))
     _run(m, perturbed(st, 64), s, 1.0 / 60.0, 90, oracle)
 
 
 @pytest.mark.parametrize("name", ["pile", "hammer_chain", "island_walk", "joints"])
 def test_scene_parity_game_iterations(name, oracle):
     """The game's 300 / 30 iterations on the heavier scenes."""
-    s, m, st = b2.scenes.build_test_scene(name)
+    s, m, st = scene_defs.build_test_scene(name)
     _run(m, perturbed(st, 16, seed=3), s, b2.GAME_DT, 60, oracle)
 
 
@@ -131,7 +132,7 @@ def test_toi_tie_parity(oracle, oldest, max_events):
     (toi.py:552-556); max_events=1 leaves the rule's contact as the one with toi.count 1."""
     s = b2.Settings.stock(gravity=(0.0, 0.0), continuous_physics=True, toi_tie_oldest=oldest,
                           max_events=max_events)
-    model, state = b2.scenes.scene_toi_tie(s).build(8)
+    model, state = scene_defs.scene_toi_tie(s).build(8)
     m = wd.compact_model(model, state)
     st = wd.batch(wd.compact_state(m, state), 64)
     st.bodies.v[:, 1, 1] = -np.random.default_rng(11).uniform(40.0, 80.0, 64).astype(np.float32)
@@ -149,7 +150,7 @@ def test_wake_cascade_parity(oracle, xy_newer):
     Collide walk must wake Z in the step where X first touches Y only when the X-Y contact is the newer."""
     from test_oracle_pins import wake_cascade_run
     s = b2.Settings.stock(gravity=(0.0, 0.0))
-    model, state = b2.scenes.scene_wake_cascade(s, xy_newer).build(8)
+    model, state = scene_defs.scene_wake_cascade(s, xy_newer).build(8)
     m = wd.compact_model(model, state)
     dt = np.float32(1.0 / 60.0)
 
@@ -171,7 +172,7 @@ def test_wake_cascade_parity(oracle, xy_newer):
 def test_model_without_body_types(oracle):
     """A compact Model as the reference's compact_model returns it (no body types: they stay in the State,
     world.py:437-472) steps the same; the body types come from the State."""
-    s, m, st = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+    s, m, st = scene_defs.build_test_scene("pile", iterations=(8, 3))
     ref_style = m._replace(body_type=None, centroid=None, edge_flags=None)
     st = perturbed(st, 32, seed=4)
     dev = b2.layout.to_device(st, "cuda")
@@ -198,7 +199,7 @@ def test_collide_config2(oracle):
 
 def test_island_debug_outputs(oracle):
     """Island ids and solve order of the device Solve equal the oracle's."""
-    s, m, st = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+    s, m, st = scene_defs.build_test_scene("pile", iterations=(8, 3))
     st = perturbed(st, 64, seed=9)
     dev = b2.layout.to_device(st, "cuda")
     ref = oracle.copy(st)
@@ -320,7 +321,7 @@ def test_step_n_equals_repeated_steps(oracle, monkeypatch, case, wpw, k):
     if wpw is not None:
         monkeypatch.setenv("GOI_WORLDS_PER_WAVE", wpw)
     if case == "pile":
-        s, m, st = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+        s, m, st = scene_defs.build_test_scene("pile", iterations=(8, 3))
         st, dt = perturbed(st, 64, seed=7), 1.0 / 60.0
     else:
         s, m, st, cfg = b2.scenes.make_config(4, 512 if case == "config4" else 1024)
@@ -365,7 +366,7 @@ def test_applied_forces_parity(oracle, auto_clear):
     """Forces and torques written into the State between steps (every 5th step, random per world and body), with
     and without auto_clear_forces."""
     from dataclasses import replace
-    s, m, st = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+    s, m, st = scene_defs.build_test_scene("pile", iterations=(8, 3))
     s = replace(s, auto_clear_forces=auto_clear)
     st = perturbed(st, 32, seed=9)
     dyn = np.asarray(st.bodies.type) == wd.DYNAMIC

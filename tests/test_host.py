@@ -149,9 +149,10 @@ def test_candidate_pairs_rules():
     c = d.add_body(wd.DYNAMIC, (2, 2), mass=1, inertia=0.1)
     d.add_box(c, (0.2, 0.2))
     d.add_revolute(a, b)
-    pairs = d.candidate_pairs()
-    fb = [f["body"] for f in d.fixtures]
-    st = [f["shape_type"] for f in d.fixtures]
+    pairs = [tuple(int(x) for x in p) for p in d.candidate_pairs()]
+    m, _ = d.build(4)
+    fb, st = m.fixture_body.tolist(), m.shape_type.tolist()
+    assert list(zip(m.pair_a.tolist(), m.pair_b.tolist())) == pairs
     for i, k in pairs:
         assert fb[i] != fb[k]
         assert not (fb[i] == g and fb[k] == g)
@@ -161,6 +162,55 @@ def test_candidate_pairs_rules():
     want = {frozenset((i, k)) for i in range(6) for k in range(i + 1, 6)
             if fb[i] != fb[k] and not (fb[i] == g and fb[k] == g) and {fb[i], fb[k]} != {a, b}}
     assert {frozenset(p) for p in pairs} == want
+
+
+@pytest.mark.parametrize("layers", [False, True])
+def test_candidate_pairs_filters_vs_brute_force(layers):
+    """Random fixtures with sensors, filter groups, category/mask bits (or a layer matrix), joints with and without
+    collide_connected: the candidate list equals a pair-by-pair scan of the rules (the reference oracle's
+    Filter::ShouldCollide, world.py:177-183, and UpdatePairs order, world.py:308-329)."""
+    rng = np.random.default_rng(17 + layers)
+    masks = [int(x) for x in rng.integers(0, 2**32, 32)] if layers else None
+    d = wd.WorldDef(b2.Settings.stock(), layer_masks=masks)
+    bodies = [d.add_body(wd.STATIC)] + [d.add_body(wd.DYNAMIC, (i, 2), mass=1, inertia=0.1) for i in range(6)]
+    spec = []
+    for _ in range(40):
+        body = int(rng.choice(bodies))
+        kw = dict(sensor=bool(rng.random() < 0.1), layer=int(rng.integers(0, 32)), group=int(rng.integers(-2, 3)),
+                  category=int(1 << rng.integers(0, 4)), mask=int(rng.integers(0, 16)))
+        if rng.random() < 0.5:
+            d.add_circle(body, 0.2, **kw)
+            kind = b2.shapes.CIRCLE
+        else:
+            d.add_box(body, (0.2, 0.1), **kw)
+            kind = b2.shapes.POLYGON
+        spec.append((body, kind, kw))
+    joined = set()
+    for _ in range(4):
+        x, y = (int(v) for v in rng.choice(bodies[1:], 2, replace=False))
+        collide = bool(rng.random() < 0.5)
+        d.add_revolute(x, y, collide=collide)
+        if not collide:
+            joined.add(frozenset((x, y)))
+
+    def should(fa, fb):
+        if masks is not None:
+            return ((masks[fa["layer"]] >> fb["layer"]) & 1) == 1
+        if fa["group"] == fb["group"] and fa["group"] != 0:
+            return fa["group"] > 0
+        return (fa["mask"] & fb["category"]) != 0 and (fa["category"] & fb["mask"]) != 0
+
+    want = []
+    for i in range(len(spec)):
+        for k in range(i + 1, len(spec)):
+            (bi, ti, fi), (bk, tk, fk) = spec[i], spec[k]
+            if bi == bk or fi["sensor"] or fk["sensor"] or (bi == 0 and bk == 0):
+                continue
+            if frozenset((bi, bk)) in joined or not should(fi, fk):
+                continue
+            want.append((k, i) if (ti, tk) == (b2.shapes.CIRCLE, b2.shapes.POLYGON) else (i, k))
+    got = [tuple(int(x) for x in p) for p in d.candidate_pairs()]
+    assert got == want and len(want) > 50
 
 
 def test_polygon_set_hull_and_normals():

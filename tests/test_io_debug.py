@@ -5,6 +5,7 @@ import numpy as np
 import pytest
 
 from util import b2
+import scene_defs
 
 F32 = np.float32
 wd = b2.world
@@ -13,7 +14,7 @@ dbg = b2.debug
 
 
 def _scene_state(name, steps, oracle):
-    s, m, st = b2.scenes.build_test_scene(name, iterations=(8, 3))
+    s, m, st = scene_defs.build_test_scene(name, iterations=(8, 3))
     st = wd.batch(st, 2)
     for _ in range(steps):
         oracle.step_(m, st, s, 1.0 / 60.0)
@@ -67,7 +68,7 @@ def test_model_file_round_trip(tmp_path):
 
 
 def test_body_record():
-    s, m, st = b2.scenes.build_test_scene("free_fall")
+    s, m, st = scene_defs.build_test_scene("free_fall")
     st = wd.batch(st, 1)
     r = dbg.body_record(st, 0, 1)
     bd = st.bodies

@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 
 from util import b2
+import scene_defs
 
 F32 = np.float32
 H = b2.GAME_DT
@@ -238,7 +239,7 @@ def test_bounce_with_restitution_one(oracle):
 
 def test_normal_impulses_non_negative(oracle):
     """Accumulated normal impulses are clamped at 0 (contact_solver.py:194-290), over a pile of boxes."""
-    s, m, st = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+    s, m, st = scene_defs.build_test_scene("pile", iterations=(8, 3))
     st = wd.batch(st, 4)
     for _ in range(60):
         oracle.step_(m, st, s, F32(1 / 60))
@@ -435,7 +436,7 @@ def test_toi_tie_rule(oracle):
     out = {}
     for oldest in (False, True):
         s = S.stock(gravity=(0, 0), continuous_physics=True, toi_tie_oldest=oldest, max_events=1)
-        model, st = b2.scenes.scene_toi_tie(s).build(4)
+        model, st = scene_defs.scene_toi_tie(s).build(4)
         st = wd.batch(st, 1)
         dt = F32(1.0 / 60.0)
         for k in range(3):
@@ -460,7 +461,7 @@ def test_toi_island_membership(oracle):
     and the two bullet choices give the same step to the bit (the rule is symmetric in the two bodies)."""
     def plank_after(cont, **bullets):
         s = S.stock(gravity=(0, 0), continuous_physics=cont)
-        model, st = b2.scenes.scene_toi_plank(s, **bullets).build(8)
+        model, st = scene_defs.scene_toi_plank(s, **bullets).build(8)
         st = wd.batch(st, 1)
         for k in range(2):
             oracle.step_(model, st, s, F32(1 / 60))
@@ -516,7 +517,7 @@ def test_collide_wake_cascade_in_list_order(oracle, xy_newer):
     X-Y contact is the newer, the walk wakes Y before it reaches Y-Z, which then touches and wakes Z in that same
     step; when it is the older, Y-Z was passed over asleep, so Z sleeps through that step and wakes in the next."""
     s = S.stock(gravity=(0, 0))
-    model, st = b2.scenes.scene_wake_cascade(s, xy_newer).build(8)
+    model, st = scene_defs.scene_wake_cascade(s, xy_newer).build(8)
     st = wd.batch(st, 1)
     got = wake_cascade_run(lambda x: oracle.step_(model, x, s, F32(1 / 60)), st, xy_newer)
     assert got == ([(True, True), (True, True)] if xy_newer else [(False, False), (True, True)])
@@ -841,7 +842,7 @@ def test_find_new_contacts_keys_follow_candidate_order(oracle):
     """Later FindNewContacts calls (one per step with TOI off): surviving contacts keep their slot and key, and the
     contacts created in one call take keys next_key, next_key + 1, ... in candidate (pair index) order."""
     import dataclasses
-    s, m, st0 = b2.scenes.build_test_scene("pile", iterations=(8, 3))
+    s, m, st0 = scene_defs.build_test_scene("pile", iterations=(8, 3))
     s = dataclasses.replace(s, continuous_physics=False)
     st = wd.batch(st0, 1)
     oracle.step_(m, st, s, F32(1 / 60))
@@ -912,7 +913,7 @@ def _dfs_islands(model, st, w):
 
 @pytest.mark.parametrize("scene", ["pile", "joints", "island_walk"])
 def test_islands_vs_sequential_dfs(oracle, scene):
-    s, m, st0 = b2.scenes.build_test_scene(scene, iterations=(8, 3))
+    s, m, st0 = scene_defs.build_test_scene(scene, iterations=(8, 3))
     st = wd.batch(st0, 1)
     B, R, J, C = wd.dims(st)
     checked = 0
