@@ -12,7 +12,7 @@ import numpy as np
 PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = PKG / "lib" / "libgoi_b2.so"
 NUM_LEAVES = 71
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 GOI_OK, GOI_E_ARG, GOI_E_SHAPE, GOI_E_HIP, GOI_E_UNSUPPORTED = 0, -1, -2, -3, -4
 
@@ -56,8 +56,12 @@ class GoiStateView(ctypes.Structure):
                 ("C", ctypes.c_int32), ("R", ctypes.c_int32), ("J", ctypes.c_int32), ("leaf", _P * NUM_LEAVES)]
 
 
+DEBUG_TOI_EVENTS, DEBUG_TOI_ROWS = 8, 32  # GOI_DEBUG_TOI_EVENTS, GOI_DEBUG_TOI_ROWS
+
+
 class GoiDebug(ctypes.Structure):
-    _fields_ = [("body_island", _P), ("contact_island", _P), ("contact_order", _P), ("n_islands", _P)]
+    _fields_ = [("body_island", _P), ("contact_island", _P), ("contact_order", _P), ("n_islands", _P),
+                ("toi_event_slot", _P), ("toi_event_alpha", _P), ("toi_event_island", _P), ("toi_island_rows", _P)]
 
 
 EXPORTS = ("goi_abi_version", "goi_model_create", "goi_model_destroy", "goi_step", "goi_step_n", "goi_step_n_noalloc",

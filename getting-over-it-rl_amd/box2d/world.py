@@ -639,9 +639,10 @@ def compact_model(model, state):
     owner = np.asarray(model.fixture_body)
     F = owner.shape[0]
     on_static = shared[owner] == STATIC
-    per_world = {"fat": np.asarray(state.fixtures.fat).reshape(-1, F, 4),
-                 "friction": np.asarray(state.fixtures.friction).reshape(-1, F),
-                 "restitution": np.asarray(state.fixtures.restitution).reshape(-1, F)}
+    n = len(types)
+    per_world = {"fat": np.asarray(state.fixtures.fat).reshape(n, F, 4),
+                 "friction": np.asarray(state.fixtures.friction).reshape(n, F),
+                 "restitution": np.asarray(state.fixtures.restitution).reshape(n, F)}
     tables = {}
     for name, rows in per_world.items():
         if (rows[:, on_static] != rows[:1, on_static]).any():

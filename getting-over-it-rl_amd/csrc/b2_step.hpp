@@ -342,10 +342,39 @@ GOI_D void cs_position_row(const DModel& m, const World& W, const Rows& R, int i
     R.setf(i, CF_RADA, m.radius[fa]); R.setf(i, CF_RADB, m.radius[fb]);
 }
 
-// one TOI event (toi.py:604-716) on min_slot at min_alpha; `stamp` (negative, below -1, distinct for each event of
-// the step) marks the event island's contacts in the workspace's cisl array, whose island ids Solve no longer needs
+// The debug trace of event `ev` of a world (GoiDebug's toi_* arrays, when given): its slot, alpha and island size,
+// and the slots of its nc island rows (-1 beyond them); the group's lanes split the rows.
+GOI_D void record_toi_event(const World& W, const GoiDebug& dbg, int ev, int slot, float alpha, int nc, int nb,
+                            const Rows& CR) {
+    if (!dbg.toi_event_slot || ev >= GOI_DEBUG_TOI_EVENTS) return;
+    const size_t P = (size_t)W.pitch;
+    if (W.sub == 0) {
+        dbg.toi_event_slot[ev * P + W.w] = slot;
+        dbg.toi_event_alpha[ev * P + W.w] = (int)__float_as_uint(alpha);
+        dbg.toi_event_island[ev * P + W.w] = nc | (nb << 16);
+    }
+    for (int i = W.sub; i < GOI_DEBUG_TOI_ROWS; i += W.G)
+        dbg.toi_island_rows[((size_t)ev * GOI_DEBUG_TOI_ROWS + i) * P + W.w] = i < nc ? CR.geti(i, CF_SLOT) : -1;
+}
+
+// The blank trace (no event) of every event entry of a world, written before SolveTOI.
+GOI_D void clear_toi_trace(const World& W, const GoiDebug& dbg) {
+    if (!dbg.toi_event_slot) return;
+    const size_t P = (size_t)W.pitch;
+    for (int e = W.sub; e < GOI_DEBUG_TOI_EVENTS; e += W.G) {
+        dbg.toi_event_slot[e * P + W.w] = -1;
+        dbg.toi_event_alpha[e * P + W.w] = 0;
+        dbg.toi_event_island[e * P + W.w] = 0;
+    }
+    for (int i = W.sub; i < GOI_DEBUG_TOI_EVENTS * GOI_DEBUG_TOI_ROWS; i += W.G) dbg.toi_island_rows[i * P + W.w] = -1;
+}
+
+// one TOI event (toi.py:604-716) on min_slot at min_alpha, the step's event number `ev`: the event island's contacts
+// are marked with a stamp distinct for each event of the step (-2 - ev) in the workspace's cisl array, whose island
+// ids Solve no longer needs
 GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
-                          float dt, int min_slot, float min_alpha, int stamp) {
+                          float dt, int min_slot, float min_alpha, int ev, const GoiDebug& dbg) {
+    const int stamp = -2 - ev;
     const int fa = W.fa(min_slot), fb = W.fb(min_slot);
     const int A = W.ba(min_slot), Bb = W.bb(min_slot);
     const SweepBackup bkA = backup(W, A), bkB = backup(W, Bb);
@@ -360,6 +389,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         W.set_ten(min_slot, 0);
         restore(W, A, bkA);
         restore(W, Bb, bkB);
+        record_toi_event(W, dbg, ev, min_slot, min_alpha, 0, 0, CR);
         return;
     }
     W.set_ten(min_slot, 1);
@@ -413,6 +443,8 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
             group_sync();
         }
     }
+    group_sync();
+    record_toi_event(W, dbg, ev, min_slot, min_alpha, nc, nb, CR);
     // b2Island::SolveTOI (toi.py:719-799)
     for (int i = 0; i < nb; ++i) {
         const int b = W.ibuf(i);
@@ -524,7 +556,8 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
 // b2World::SolveTOI (toi.py:827-865). Called by every lane of the block (the reset, the TOI searches and the final
 // copy are cooperative); `valid` marks the lanes that run a world, `leader` the first lane of each world's group.
 GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
-                           float dt, bool valid, bool leader, const Coop& co, const BlockCopy& bc) {
+                           float dt, bool valid, bool leader, const Coop& co, const BlockCopy& bc,
+                           const GoiDebug& dbg) {
     if (W.C == 0 || m.P == 0) return;
     if (s.unity_toi && !m.any_toi_body) return;
     reset_toi_block(bc);
@@ -541,7 +574,7 @@ GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, co
         while (__any(found && events < max_events)) {
             const bool act = found && events < max_events;
             if (act) {
-                toi_event(m, W, bd, CR, s, dt, slot, alpha, -2 - events);
+                toi_event(m, W, bd, CR, s, dt, slot, alpha, events, dbg);
                 ++events;
             }
             const int nt = act ? toi_search_prepare(m, W, CR, s) : 0;

@@ -206,8 +206,11 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
             W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
         }
         collide_block(m, co, W, valid, lm.leader, L.s);
-        if (valid) solve_world(m, W, bd, CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
-        if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, lm.leader, co, bc);
+        if (valid) {
+            solve_world(m, W, bd, CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
+            clear_toi_trace(W, L.dbg);
+        }
+        if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, lm.leader, co, bc, L.dbg);
         if (valid) {
             const float dt = L.dt;
             if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;

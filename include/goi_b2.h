@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define GOI_ABI_VERSION 2
+#define GOI_ABI_VERSION 3
 
 #define GOI_OK 0
 #define GOI_E_ARG (-1)
@@ -223,13 +223,22 @@ typedef struct GoiStateView {
     void* leaf[GOI_NUM_LEAVES];
 } GoiStateView;
 
-/* Optional per-world integer outputs that are not State leaves (island ids, solve order, TOI event counts),
- * written worlds-minor with the view's pitch when non-NULL. */
+/* Optional per-world integer outputs that are not State leaves: Solve's islands and solve order, and a trace of
+ * SolveTOI's first GOI_DEBUG_TOI_EVENTS events (which contact, when, and the island the event's walk built,
+ * toi.py:604-716). Each pointer may be NULL; a non-NULL one receives its array worlds-minor with the view's pitch
+ * (element (i, w) at [i * pitch + w]; the rows of event e at i = e * GOI_DEBUG_TOI_ROWS + row). Event entries past
+ * the step's last event hold slot -1, alpha 0, island 0 and rows -1. */
+#define GOI_DEBUG_TOI_EVENTS 8
+#define GOI_DEBUG_TOI_ROWS 32 /* b2_maxTOIContacts: an event island's contact cap */
 typedef struct GoiDebug {
     int32_t* body_island;      /* [B] island of each body after Solve's search, -1 none (island.py:33) */
     int32_t* contact_island;   /* [C] (island.py:34) */
     int32_t* contact_order;    /* [C] slots in solve order, -1 padded (island.py:29) */
     int32_t* n_islands;        /* [] */
+    int32_t* toi_event_slot;   /* [E] the event's contact slot (the TOI search's minimum) */
+    int32_t* toi_event_alpha;  /* [E] the bits of its float minAlpha */
+    int32_t* toi_event_island; /* [E] island contacts | island bodies << 16; 0 when the contact stopped touching */
+    int32_t* toi_island_rows;  /* [E, 32] the island's contact slots in walk order (the event's contact first), -1 padded */
 } GoiDebug;
 
 typedef struct GoiModel GoiModel;

@@ -19,22 +19,26 @@
  * kept, sin/cos = (float)sin((double)x) from the C library (the reference oracle's trig_mode=1,
  * scripts/patches/box2d-2.3.1-trig.patch:17-23; math2d.py:291-310 reproduces it).
  *
- * Parity pinning (tests/test_oracle_*.py): semi-implicit Euler closed form (tests/reference/test_box2d_reference.py
- * :22-35), resting-contact impulse m*g*dt and sqrt friction mix (:49-63), sleeping (:38-46), pendulum radius/energy
- * (:90-110), revolute limit and motor (:112-127), TOI ball stopped / discrete ball tunnels (test_toi.py:181-185,
- * test_box2d_reference.py:130-155), narrowphase against brute-force distances, GJK against exhaustive distances,
- * broadphase candidate scan against a brute-force scan, and the b2TimeOfImpact target contract (toi.py:372-375).
+ * Parity pinning (tests/test_oracle_pins.py, tests/test_edges.py; tests/test_oracle_mutants.py plants 50 slips and
+ * shows each pin catching its slip): semi-implicit Euler closed form (tests/reference/test_box2d_reference.py:22-35),
+ * resting-contact impulse m*g*dt and sqrt friction mix (:49-63), sleeping (:38-46), pendulum radius/energy (:90-110),
+ * revolute limit and motor (:112-127), TOI ball stopped / discrete ball tunnels (test_toi.py:181-185,
+ * test_box2d_reference.py:130-155); one pass of each position row (contact, revolute point and limit, prismatic,
+ * rigid and soft weld) checked by the defining conditions of a non-linear Gauss-Seidel step (the linearized error
+ * reaches the row's target, the move is along M^-1 J^T); the revolute velocity rows' motor and limit impulses; the
+ * velocity rows' result by the constraint invariant; the block solver's result by the two-point LCP conditions and
+ * its condition-number fallback; b2CollidePolygons known answers, exact face ties and incident-edge ties included;
+ * the Collide wake cascade in list order; the TOI event island walk's order and 32-contact cap (with its trace), its
+ * membership rule and the tie rules; b2TimeOfImpact's root steps and target contract; narrowphase, GJK and the
+ * broadphase candidate scan against brute force; islands against an independent DFS.
  *
  * Parity unpinned: the reference commits no golden vectors for this path and can be run neither here (jax absent)
- * nor from source (Box2D 2.3.1 is fetched over the network), so these parts are right only by faithful reading of
- * the cited reference text; no closed form fixes their exact bits:
- *   - collide_polygons' feature ids and clip order under ties (collide.py:65-127);
- *   - the wake cascade of collide() in list order (pairs.py:90-117);
- *   - cs_solve_velocity's block-solver case selection path (contact_solver.py:236-279);
- *   - the revolute v2.4.1 velocity/position rows, prismatic and weld rows (joints.py:302-343, 482-498);
- *   - time_of_impact / distance iteration paths (toi.py:230-459);
- *   - toi_event's island walk membership and break (toi.py:604-716);
- *   - the min-TOI tie rule in toi_search (toi.py:552-556);
+ * nor from source (Box2D 2.3.1 is fetched over the network). These parts are right only by faithful reading of the
+ * cited reference text:
+ *   - the block solver's choice among its four cases where two of them accept (only at exact float boundaries of
+ *     the LCP's active set; the result is pinned by the LCP conditions) (contact_solver.py:236-279);
+ *   - time_of_impact / distance iteration paths beyond the head-on root steps and the target contract
+ *     (toi.py:230-459);
  *   - the native edge colliders collide_edge_circle / collide_edge_polygon, which have no reference function (the
  *     reference has no edge shape, shapes.py:13): they restate Box2D 2.3.1's b2CollideEdge.cpp and are pinned by
  *     closed forms, brute force and the thin-quad polygon path only (tests/test_edges.py).
@@ -2309,7 +2313,23 @@ static void toi_solve_island(const Ctx* x, W* w, Work* k, int nb, int nc, float 
 /* One TOI event (toi.py:604-716): advance the pair to min_alpha, update its contact; if it touches, the island walk
  * over bodyA's then bodyB's contact lists (at most 32 contacts / 64 bodies), b2Island::SolveTOI, fixture sync with
  * TOI invalidation of the moved bodies' contacts, FindNewContacts. */
-static void toi_event(const Ctx* x, W* w, Work* k, int min_slot, float min_alpha) {
+/* The debug trace of event ev of world wi (GoiDebug's toi_* arrays, when given): slot, alpha bits, island size
+ * (contacts | bodies << 16) and the island's contact slots in walk order, -1 beyond them. */
+static void record_toi_event(GoiDebug* dbg, int wi, int pitch, int ev, int slot, float alpha, const int* rows, int nc,
+                             int nb) {
+    if (!dbg || !dbg->toi_event_slot || ev >= GOI_DEBUG_TOI_EVENTS) return;
+    size_t P = (size_t)pitch;
+    union { float f; int32_t i; } bits;
+    bits.f = alpha;
+    dbg->toi_event_slot[ev * P + wi] = slot;
+    dbg->toi_event_alpha[ev * P + wi] = bits.i;
+    dbg->toi_event_island[ev * P + wi] = nc | (nb << 16);
+    for (int i = 0; i < GOI_DEBUG_TOI_ROWS; ++i)
+        dbg->toi_island_rows[((size_t)ev * GOI_DEBUG_TOI_ROWS + i) * P + wi] = i < nc ? rows[i] : -1;
+}
+
+static void toi_event(const Ctx* x, W* w, Work* k, int min_slot, float min_alpha, int ev, GoiDebug* dbg, int wi,
+                      int pitch) {
     const GoiModelDesc* m = x->m;
     int B = w->B, C = w->C;
     int fa = w->c_fa[min_slot], fb = w->c_fb[min_slot];
@@ -2327,6 +2347,7 @@ static void toi_event(const Ctx* x, W* w, Work* k, int min_slot, float min_alpha
         w->t_enabled[min_slot] = 0;
         restore_sweep(w, k, A);
         restore_sweep(w, k, Bb);
+        record_toi_event(dbg, wi, pitch, ev, min_slot, min_alpha, k->corder, 0, 0);
         return;
     }
     w->t_enabled[min_slot] = 1;
@@ -2366,6 +2387,7 @@ static void toi_event(const Ctx* x, W* w, Work* k, int min_slot, float min_alpha
             k->isl_bodies[nb++] = other;
         }
     }
+    record_toi_event(dbg, wi, pitch, ev, min_slot, min_alpha, k->corder, nc, nb);
     toi_solve_island(x, w, k, nb, nc, min_alpha);
     for (int b = 0; b < B; ++b) k->moved[b] = 0;
     for (int i = 0; i < nb; ++i) {
@@ -2390,7 +2412,7 @@ static void toi_event(const Ctx* x, W* w, Work* k, int min_slot, float min_alpha
     }
 }
 
-static void solve_toi(const Ctx* x, W* w, Work* k, float dt) {
+static void solve_toi(const Ctx* x, W* w, Work* k, float dt, GoiDebug* dbg, int wi, int pitch) {
     const GoiModelDesc* m = x->m;
     int B = w->B, C = w->C;
     if (C == 0 || m->P == 0) return;
@@ -2411,7 +2433,7 @@ static void solve_toi(const Ctx* x, W* w, Work* k, float dt) {
     float alpha;
     int found = toi_search(x, w, k, &slot, &alpha);
     while (found && *w->t_events < max_events) {
-        toi_event(x, w, k, slot, alpha);
+        toi_event(x, w, k, slot, alpha, *w->t_events, dbg, wi, pitch);
         *w->t_events += 1;
         found = toi_search(x, w, k, &slot, &alpha);
     }
@@ -2427,7 +2449,9 @@ static void step_world(const Ctx* x, W* w, Work* k, GoiDebug* dbg, int wi, int p
     float dt_ratio = *w->inv_dt0 * dt;
     collide(x, w, k->order);
     solve(x, w, k, dt, dt_ratio, dbg, wi, pitch);
-    if (x->s->continuous_physics) solve_toi(x, w, k, dt);
+    if (dbg && dbg->toi_event_slot) /* the blank trace; SolveTOI's events overwrite their entries */
+        for (int e = 0; e < GOI_DEBUG_TOI_EVENTS; ++e) record_toi_event(dbg, wi, pitch, e, -1, 0.0f, k->corder, 0, 0);
+    if (x->s->continuous_physics) solve_toi(x, w, k, dt, dbg, wi, pitch);
     if (dt > 0.0f) *w->inv_dt0 = inv_dt;
     if (x->s->auto_clear_forces) {
         for (int b = 0; b < w->B; ++b) { w->b_force[2 * b] = 0.0f; w->b_force[2 * b + 1] = 0.0f; w->b_torque[b] = 0.0f; }

@@ -214,6 +214,44 @@ def test_island_debug_outputs(oracle):
             assert np.array_equal(d[k], t[k].cpu().numpy()), k
 
 
+def _debug_parity(m, st, s, dt, steps, oracle, actions=None):
+    """Steps device and oracle side by side with GoiDebug outputs, comparing every debug array and every leaf after
+    each step; returns the number of TOI events traced."""
+    n = st.bodies.type.shape[0]
+    dims = wd.dims(st)
+    dev = b2.layout.to_device(st, "cuda")
+    ref = oracle.copy(st)
+    traced = 0
+    for k in range(steps):
+        if actions is not None:
+            b2.scenes.apply_actions(ref.joints.motor_speed, ref.joints.max_motor, actions[k])
+            b2.scenes.apply_actions(dev.joints.motor_speed, dev.joints.max_motor, torch.from_numpy(actions[k]).cuda())
+        dbg, t = b2.make_debug(n, dims)
+        b2.step_(m, dev, s, dt, debug=dbg)
+        d = {key: np.full(v.shape, -9, np.int32) for key, v in t.items()}
+        oracle.step_(m, ref, s, dt, debug=d)
+        torch.cuda.synchronize()
+        for key in d:
+            assert np.array_equal(d[key], t[key].cpu().numpy()), (k + 1, key)
+        assert leaf_mismatches(ref, b2.layout.to_host(dev)) == [], k + 1
+        traced += int((d["toi_event_slot"] >= 0).sum())
+    return traced
+
+
+def test_toi_event_traces(oracle):
+    """The TOI events of each step, traced through GoiDebug (the event's slot and alpha, its island's size and its
+    rows in walk order) on the device and in the oracle: config 4 (256 worlds, 15 steps with actions, thousands of
+    events) and the plank falling onto 40 bumps, whose event walk stops at the 32-contact cap."""
+    s, m, st, cfg = b2.scenes.make_config(4, 256)
+    rng = np.random.default_rng(8)
+    acts = [b2.scenes.actions(rng, 256) for _ in range(15)]
+    assert _debug_parity(m, st, s, cfg.dt, 15, oracle, acts) > 500
+    from test_oracle_pins import plank_over_bumps
+    s, m, st = plank_over_bumps()
+    st = wd.batch(wd.from_leaves([np.asarray(x)[0] for x in wd.leaves(st)]), 8)
+    assert _debug_parity(m, st, s, np.float32(1 / 60), 3, oracle) >= 8
+
+
 def test_sincos_correctly_rounded(oracle):
     """The kernels' sin/cos equal (float)sin((double)x) on the reference's sample design (20k U[-8, 8], 5k
     U[-300, 300], +-0, pi; tests/box2d/test_box2d_parity.py:44-50) plus 4M uniform samples in [-100, 100]."""

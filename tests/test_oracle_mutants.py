@@ -90,7 +90,76 @@ MUTANTS = [
      lambda o: E.test_edge_polygon_closed_forms(o, E.edge_world.__wrapped__())),
     ("edge_polygon_no_hysteresis", "!(poly_sep > 0.98f * edge_sep + 0.001f)", "!(poly_sep > edge_sep)",
      lambda o: E.test_edge_polygon_closed_forms(o, E.edge_world.__wrapped__())),
+    # position rows (one pass of non-linear Gauss-Seidel)
+    ("revolute_point_mass_uncoupled", "float kxy = -iA * rA.x * rA.y - iB * rB.x * rB.y;", "float kxy = 0.0f;",
+     lambda o: P.test_revolute_point_row_is_one_newton_step(o, True)),
+    ("revolute_point_sign", "    j = neg(j);\n", "    (void)0;\n",
+     lambda o: P.test_revolute_point_row_is_one_newton_step(o, False)),
+    ("revolute_point_angular_operands", "*aB = *aB + iB * crs(rB, j);", "*aB = *aB + iB * crs(j, rB);",
+     lambda o: P.test_revolute_point_row_is_one_newton_step(o, True)),
+    ("revolute_limit_slop_omitted", "C = bclamp((angle - r->lower) + s->angular_slop, -mac, 0.0f);",
+     "C = bclamp(angle - r->lower, -mac, 0.0f);",
+     lambda o: P.test_revolute_limit_row(o, True, "below", -0.08, (-0.5, 0.4))),
+    ("revolute_limit_unclamped", "C = bclamp((angle - r->upper) - s->angular_slop, 0.0f, mac);",
+     "C = (angle - r->upper) - s->angular_slop;",
+     lambda o: P.test_revolute_limit_row(o, True, "above_far", 0.5, (-0.5, 0.4))),
+    ("revolute_limit_sign", "float li = -r->motor_mass * C;", "float li = r->motor_mass * C;",
+     lambda o: P.test_revolute_limit_row(o, True, "below", -0.08, (-0.5, 0.4))),
+    ("prismatic_position_unclamped", "C2 = bclamp((t - r->lower) + s->linear_slop, -mlc, 0.0f);",
+     "C2 = (t - r->lower) + s->linear_slop;", lambda o: P.test_prismatic_position_row(o, "lower_far")),
+    ("prismatic_position_uncoupled", "float k12 = iA * s1 + iB * s2;\n        float k22 = iA + iB;",
+     "float k12 = 0.0f;\n        float k22 = iA + iB;", lambda o: P.test_prismatic_position_row(o, "free")),
+    ("weld_position_diagonal_mass",
+     "V3 ex = v3(exx, eyx, ezx), ey = v3(eyx, eyy, ezy), ez = v3(ezx, ezy, ezz);\n        V2 C1",
+     "V3 ex = v3(exx, 0.0f, 0.0f), ey = v3(0.0f, eyy, 0.0f), ez = v3(0.0f, 0.0f, ezz);\n        V2 C1",
+     lambda o: P.test_weld_position_row(o, False)),
+    ("position_uses_toi_baumgarte",
+     "float ms = cs_solve_position(x, c, k, s->baumgarte, c->mA, c->mB, c->iA, c->iB);",
+     "float ms = cs_solve_position(x, c, k, s->toi_baumgarte, c->mA, c->mB, c->iA, c->iB);",
+     lambda o: P.test_contact_position_row_circle(o, 0.03, False)),
+    ("position_slop_omitted",
+     "float C = bclamp(baumgarte * (sep + s->linear_slop), -s->max_linear_correction, 0.0f);",
+     "float C = bclamp(baumgarte * sep, -s->max_linear_correction, 0.0f);",
+     lambda o: P.test_contact_position_row_circle(o, 0.03, False)),
+    ("position_unclamped",
+     "float C = bclamp(baumgarte * (sep + s->linear_slop), -s->max_linear_correction, 0.0f);",
+     "float C = bmin(baumgarte * (sep + s->linear_slop), 0.0f);",
+     lambda o: P.test_contact_position_row_circle(o, 1.3, True)),
+    ("position_mass_without_rotation", "float K = ((mA + mB) + iA * rnA * rnA) + iB * rnB * rnB;",
+     "float K = mA + mB;", lambda o: P.test_contact_position_row_tilted_box(o)),
+    # the block solver's condition test, exact ties, the TOI island walk
+    ("block_solver_condition_inverted", "k11 * k11 < 1000.0f * (k11 * k22 - k12 * k12)",
+     "k11 * k11 >= 1000.0f * (k11 * k22 - k12 * k12)", lambda o: P.test_block_solver_condition_fallback(o)),
+    ("max_separation_last_index_wins", "if (si > maxsep) { maxsep = si; best = i; }",
+     "if (si >= maxsep) { maxsep = si; best = i; }", lambda o: P.test_polygon_manifold_exact_ties(o)),
+    ("incident_edge_last_index_wins", "if (d < mind) { mind = d; index = i; }",
+     "if (d <= mind) { mind = d; index = i; }", lambda o: P.test_polygon_manifold_exact_ties(o)),
+    ("toi_walk_oldest_first",
+     "for (int i = 0; i < n; ++i) {\n            int c = k->order[i];\n            int ca = m->fixture_body",
+     "for (int i = n - 1; i >= 0; --i) {\n            int c = k->order[i];\n            int ca = m->fixture_body",
+     lambda o: P.test_toi_island_walk_order_and_cap(o)),
+    ("toi_walk_cap_31", "nc == MAX_TOI_CONTACTS", "nc == MAX_TOI_CONTACTS - 1",
+     lambda o: P.test_toi_island_walk_order_and_cap(o)),
+    ("toi_walk_cap_33", "nc == MAX_TOI_CONTACTS", "nc == MAX_TOI_CONTACTS + 1",
+     lambda o: P.test_toi_island_walk_order_and_cap(o)),
+    # revolute velocity rows
+    ("revolute_limit_not_speculative", "float impulse = -am * ((wB - wA) + bmax(C, 0.0f) * r->inv_dt);",
+     "float impulse = -am * (wB - wA);", lambda o: P.test_revolute_velocity_rows(o, *_vel("lower_closing"))),
+    ("revolute_lower_impulse_may_pull", "imp[3] = bmax(imp[3] + impulse, 0.0f);", "imp[3] = imp[3] + impulse;",
+     lambda o: P.test_revolute_velocity_rows(o, *_vel("lower_opening"))),
+    ("revolute_motor_unclamped",
+     "float impulse = -am * cdot;\n            float old = r->mimp;\n"
+     "            r->mimp = bclamp(r->mimp + impulse, -r->max_impulse, r->max_impulse);",
+     "float impulse = -am * cdot;\n            float old = r->mimp;\n            r->mimp = r->mimp + impulse;",
+     lambda o: P.test_revolute_velocity_rows(o, *_vel("motor_saturated"))),
+    ("revolute_v23_limit_never_releases",
+     "int redo = (st == AT_LOWER && new_z < 0.0f) || (st == AT_UPPER && new_z > 0.0f);", "int redo = 0;",
+     lambda o: P.test_revolute_velocity_rows(o, *_vel("leaving_lower_v23"))),
 ]
+
+
+def _vel(name):
+    return next(c for c in P._VEL_CASES if c[0] == name)
 
 
 def _build(tmp, name, old, new):

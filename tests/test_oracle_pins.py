@@ -932,3 +932,354 @@ def test_islands_vs_sequential_dfs(oracle, scene):
         assert dbg["contact_order"][:len(order), 0].tolist() == order
         checked += 1
     assert checked > 10
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# position rows: one pass of non-linear Gauss-Seidel   (contact_solver.py:307-354, joints.py:462-606)
+#
+# A position row moves its bodies by M^-1 J^T lambda, lambda chosen so that the constraint error, linearized at the
+# current pose, becomes the row's target (zero for a joint's point and angle rows; the Baumgarte-scaled, slop-shifted
+# and clamped separation for a contact point and a limit). These pins step one world once with no velocity pass and
+# one position pass, a static body A and a dynamic body B placed with a known error, so that B's move is exactly that
+# pass; they then check the two defining conditions on B's move (dc, da): the linearized error after it, and the
+# direction M^-1 J^T (a rotation iB / mB times the moment of the linear move about the anchor). These conditions fix
+# the move whatever the formula; a wrong effective mass, a sign, a dropped clamp or slop changes it.
+
+def _pass_settings(**kw):
+    import dataclasses
+    return dataclasses.replace(S.stock(gravity=(0.0, 0.0), **kw), velocity_iterations=0, position_iterations=1,
+                               allow_sleep=False)
+
+
+def _one_pass(oracle, d, settings, body=1, capacity=4):
+    """(c, a) of `body` before and after one step of a single world, float64."""
+    model, state = d.build(capacity)
+    cm = wd.compact_model(model, state)
+    st = wd.batch(wd.compact_state(cm, state), 1)
+    before = (st.bodies.c[0, body].astype(np.float64), float(st.bodies.a[0, body]))
+    oracle.step_(cm, st, settings, F32(1 / 60))
+    return before, (st.bodies.c[0, body].astype(np.float64), float(st.bodies.a[0, body])), st
+
+
+def _rot(a, v):
+    c, s = np.cos(np.float64(F32(a))), np.sin(np.float64(F32(a)))
+    return np.array([c * v[0] - s * v[1], s * v[0] + c * v[1]])
+
+
+def _perp(r):
+    return np.array([-r[1], r[0]])
+
+
+def _cross(a, b):
+    return a[0] * b[1] - a[1] * b[0]
+
+
+@pytest.mark.parametrize("v24", [True, False])
+def test_revolute_point_row_is_one_newton_step(oracle, v24):
+    """The revolute point row (joints.py:501-520, both solver versions): B's anchor misses A's by e = (0.04, -0.03),
+    B's anchor offset rB = R(0.7)(0.6, 0.25), inverse mass 0.5, inverse inertia 4. After the pass the linearized
+    anchor gap C + dc + da perp(rB) is zero and da = (iB / mB) cross(rB, dc)."""
+    s = _pass_settings(revolute_v24=v24)
+    d = wd.WorldDef(s)
+    anchor = np.array([0.3, -0.2])
+    a = d.add_body(wd.STATIC, tuple(anchor))
+    lb, ang, e = (0.6, 0.25), 0.7, np.array([0.04, -0.03])
+    rb = _rot(ang, lb)
+    b = d.add_body(wd.DYNAMIC, tuple(anchor - rb + e), ang, mass=2.0, inertia=0.25)
+    d.add_revolute(a, b, (0, 0), lb)
+    (c0, a0), (c1, a1), _ = _one_pass(oracle, d, s)
+    dc, da = c1 - c0, a1 - a0
+    C = c0 + rb - anchor
+    assert np.linalg.norm(C - e) < 1e-6 and np.linalg.norm(dc) > 1e-3
+    assert np.linalg.norm(C + dc + da * _perp(rb)) < 2e-6
+    assert abs(da - (4.0 / 0.5) * _cross(rb, dc)) < 2e-5
+
+
+# (offset of the joint angle from the limit, limits) -> the angle after the pass: a violation beyond the slop is
+# pulled back to the slop, a large one by at most max_angular_correction, equal limits to the limit itself
+_LIMIT_CASES = [("below", -0.08, (-0.5, 0.4)), ("below_far", -0.5, (-0.5, 0.4)), ("above", 0.08, (-0.5, 0.4)),
+                ("above_far", 0.5, (-0.5, 0.4)), ("inside", 0.3, (-0.5, 0.4)), ("equal", 0.05, (0.2, 0.2)),
+                ("equal_far", 0.7, (0.2, 0.2))]
+
+
+@pytest.mark.parametrize("v24", [True, False])
+@pytest.mark.parametrize("name,off,limits", _LIMIT_CASES, ids=[c[0] for c in _LIMIT_CASES])
+def test_revolute_limit_row(oracle, v24, name, off, limits):
+    """The revolute limit row (joints.py:462-498): with B's anchor at its centre (rB = 0, so the point row leaves the
+    angle alone) and static A, one pass moves the joint angle to lower - angular_slop (upper + slop) when it was
+    below (above) by more than the slop, by at most max_angular_correction (8 degrees) when far, to the limit when
+    lower == upper, and not at all inside the limits."""
+    s = _pass_settings(revolute_v24=v24)
+    lo, hi = limits
+    ref = 0.1
+    angle = (lo if off < 0 or name.startswith("equal") else hi if off > 0 and name != "inside" else 0.0) + off
+    if name == "inside":
+        angle = off
+    d = wd.WorldDef(s)
+    a = d.add_body(wd.STATIC, (1.0, 2.0))
+    b = d.add_body(wd.DYNAMIC, (1.0, 2.0), ref + angle, mass=2.0, inertia=0.25)
+    d.add_revolute(a, b, (0, 0), (0, 0), ref, limits=limits)
+    (c0, a0), (c1, a1), _ = _one_pass(oracle, d, s)
+    got = a1 - ref
+    start = a0 - ref
+    slop, mac = float(s.angular_slop), float(s.max_angular_correction)
+    want = {"below": lo - slop, "below_far": start + mac, "above": hi + slop, "above_far": start - mac,
+            "inside": start, "equal": lo, "equal_far": start - mac}[name]
+    assert abs(got - want) < 2e-6, (got, want)
+    assert np.array_equal(c1, c0)
+
+
+@pytest.mark.parametrize("case", ["free", "lower", "lower_far", "upper"])
+def test_prismatic_position_row(oracle, case):
+    """The prismatic position row (joints.py:523-566): axis u at 0.7 rad on static A, B off the axis by 0.03, turned
+    0.04 past the reference angle, at translation t along u. After the pass, the linearized perpendicular gap and
+    angle error are zero: perp.d + perp.dc + cross(rB, perp) da = 0 and angle + da = 0; a slider inside its limits
+    gets no impulse along u (u.dc = 0), one beyond a limit has its linearized translation change
+    u.dc + cross(rB, u) da equal to minus the limit row's target clamp((t - lower) + slop, -0.2, 0) (or the upper
+    one)."""
+    s = _pass_settings()
+    th = 0.7
+    u = np.array([np.cos(th), np.sin(th)])
+    pp = _perp(u)
+    la, lb, ref = np.array([0.1, -0.2]), (0.2, -0.1), 0.3
+    t = {"free": 0.4, "lower": -0.6, "lower_far": -1.2, "upper": 1.1}[case]
+    lo, hi = -0.5, 1.0
+    d = wd.WorldDef(s)
+    a = d.add_body(wd.STATIC, (0.0, 0.0))
+    ab = ref + 0.04
+    rb = _rot(ab, lb)
+    c_b = la + t * u + 0.03 * pp - rb
+    b = d.add_body(wd.DYNAMIC, tuple(c_b), ab, mass=2.0, inertia=0.25)
+    d.add_prismatic(a, b, tuple(la), lb, (np.cos(th), np.sin(th)), ref, limits=(lo, hi))
+    (c0, a0), (c1, a1), _ = _one_pass(oracle, d, s)
+    dc, da = c1 - c0, a1 - a0
+    dvec = c0 + rb - la
+    assert abs(pp @ dvec + pp @ dc + _cross(rb, pp) * da) < 3e-6
+    assert abs((a0 - ref) + da) < 2e-6
+    along = u @ dc + _cross(rb, u) * da
+    tt = u @ dvec
+    slop, mlc = float(s.linear_slop), float(s.max_linear_correction)
+    if case == "free":
+        assert abs(u @ dc) < 3e-6  # no impulse along the axis
+    elif case == "upper":
+        assert abs(along + min(max((tt - hi) - slop, 0.0), mlc)) < 3e-6
+    else:
+        assert abs(along + min(max((tt - lo) + slop, -mlc), 0.0)) < 3e-6
+    assert np.linalg.norm(dc) > 1e-3
+
+
+@pytest.mark.parametrize("soft", [False, True])
+def test_weld_position_row(oracle, soft):
+    """The weld position row (joints.py:569-595): B's anchor misses A's by (0.04, -0.03) and B is turned 0.05 past
+    the reference angle. Rigid: the linearized anchor gap and angle error are both zero after the pass (three
+    conditions for three unknowns). Soft (frequency > 0): only the anchor gap is corrected, along M^-1 J^T of the
+    point row: da = (iB / mB) cross(rB, dc)."""
+    s = _pass_settings()
+    d = wd.WorldDef(s)
+    anchor = np.array([-0.4, 0.5])
+    a = d.add_body(wd.STATIC, tuple(anchor))
+    lb, ref = (0.5, 0.3), 0.2
+    ab = ref + 0.05
+    rb = _rot(ab, lb)
+    e = np.array([0.04, -0.03])
+    b = d.add_body(wd.DYNAMIC, tuple(anchor - rb + e), ab, mass=2.0, inertia=0.25)
+    d.add_weld(a, b, (0, 0), lb, ref, frequency=4.0 if soft else 0.0, damping=0.5)
+    (c0, a0), (c1, a1), _ = _one_pass(oracle, d, s)
+    dc, da = c1 - c0, a1 - a0
+    C = c0 + rb - anchor
+    assert np.linalg.norm(C + dc + da * _perp(rb)) < 3e-6
+    if soft:
+        assert abs(da - (4.0 / 0.5) * _cross(rb, dc)) < 2e-5
+    else:
+        assert abs((a0 - ref) + da) < 2e-6
+
+
+@pytest.mark.parametrize("depth,clamped", [(0.03, False), (1.3, True)])
+def test_contact_position_row_circle(oracle, depth, clamped):
+    """The contact position row (contact_solver.py:307-354) on a circle (radius 1.5, inverse mass 1) embedded `depth`
+    in a static slab's top face: separation sep = -depth - 0.01 (the slab's skin); the one point's target is
+    clamp(baumgarte (sep + linear_slop), -max_linear_correction, 0) with Baumgarte 0.2 in Solve (not the TOI's 0.75);
+    the contact point is the circle's centre, so the circle rises by exactly minus the target and does not turn."""
+    s = _pass_settings()
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (0.0, -0.5))
+    d.add_box(g, (10.0, 0.5))
+    r = 1.5
+    b = d.add_body(wd.DYNAMIC, (0.0, r - depth), mass=1.0, inertia=1.0)
+    d.add_circle(b, r)
+    (c0, a0), (c1, a1), _ = _one_pass(oracle, d, s)
+    sep = c0[1] - r - float(s.polygon_radius)
+    target = min(max(float(s.baumgarte) * (sep + float(s.linear_slop)), -float(s.max_linear_correction)), 0.0)
+    assert (target == -float(s.max_linear_correction)) == clamped
+    assert abs((c1[1] - c0[1]) + target) < 1e-6 and c1[0] == c0[0] and a1 == a0
+
+
+def test_contact_position_row_tilted_box(oracle):
+    """The contact position row with rotation: a box (half extents 0.5 x 0.25, inverse mass 0.5, inverse inertia 10)
+    turned 0.4 rad with its lowest corner 0.04 into a slab (one manifold point: the next corner is 0.35 above).
+    The corner p is the contact point, n = +y, rB = p - cB. After the pass: dc is along n, da = (iB / mB)
+    cross(rB, dc), and the corner's linearized rise n.dc + da n.perp(rB) equals minus the target
+    clamp(0.2 (sep + slop), -0.2, 0), sep = -0.04 - 2 skins."""
+    s = _pass_settings()
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (0.0, -0.5))
+    d.add_box(g, (10.0, 0.5))
+    th, half = 0.4, (0.5, 0.25)
+    corner = _rot(th, (-half[0], -half[1]))
+    b = d.add_body(wd.DYNAMIC, (0.0, -corner[1] - 0.04), th, mass=2.0, inertia=0.1)
+    d.add_box(b, half)
+    (c0, a0), (c1, a1), st = _one_pass(oracle, d, s)
+    assert int(st.contacts.count[0][st.contacts.pair[0] >= 0][0]) == 1
+    dc, da = c1 - c0, a1 - a0
+    rb = _rot(a0, (-half[0], -half[1]))
+    sep = (c0[1] + rb[1]) - 2 * float(s.polygon_radius)
+    target = min(max(0.2 * (sep + float(s.linear_slop)), -0.2), 0.0)
+    assert abs(dc[0]) < 1e-7 and dc[1] > 1e-3
+    assert abs(da - (10.0 / 0.5) * _cross(rb, dc)) < 2e-5
+    assert abs(dc[1] + da * rb[0] + target) < 2e-6
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the block solver's condition test   (contact_solver.py:116-130)
+
+def test_block_solver_condition_fallback(oracle):
+    """A two-point contact uses the 2x2 block solver only while K is well conditioned (k11^2 < 1000 det K), else
+    only its first point (contact_solver.py:116-130). A box 0.002 m wide on a slab has two manifold points 0.002 m
+    apart: with inverse mass and inertia 1, det K = 4e-6 against k11^2 = 1, so one point carries the whole weight and
+    the second point's normal impulse stays 0. A box 1 m wide (det K = 1) uses both points."""
+    out = {}
+    for name, hx in (("narrow", 0.001), ("wide", 0.5)):
+        s = S.stock(gravity=(0.0, -10.0))
+        d = wd.WorldDef(s)
+        g = d.add_body(wd.STATIC, (0.0, -0.5))
+        d.add_box(g, (10.0, 0.5))
+        b = d.add_body(wd.DYNAMIC, (0.0, 0.2 + 0.015), mass=1.0, inertia=1.0)
+        d.add_box(b, (hx, 0.2))
+        model, state = d.build(4)
+        st = wd.batch(state, 1)
+        oracle.step_(model, st, s, F32(1 / 60))
+        k = int(np.nonzero(st.contacts.pair[0] >= 0)[0][0])
+        assert int(st.contacts.count[0, k]) == 2
+        out[name] = st.contacts.normal_impulse[0, k]
+    assert out["narrow"][0] > 0 and out["narrow"][1] == 0
+    assert out["wide"][0] > 0 and out["wide"][1] > 0
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# b2CollidePolygons under exact ties   (collide.py:32-42, 65-127)
+
+def test_polygon_manifold_exact_ties(oracle):
+    """Known answers worked by hand where the running maxima tie exactly (b2FindMaxSeparation keeps the first of equal
+    separations, the incident edge search the first of equal dot products):
+
+    - two unit boxes at the same pose: all eight face separations are -1, so the reference face is A's edge 0
+      (normal -y, local point (0, -0.5)), no flip (B's -1 is not more than A's -1 + k_tol); B's incident edge is
+      edge 2 (normal +y), both its vertices survive the side planes: points (0.5, 0.5) and (-0.5, 0.5) of B, keys
+      (0, 2, F, V) = 66048 and (0, 3, F, V) = 66304;
+    - a diamond (vertices (0.3, 0), (0, 0.3), (-0.3, 0), (0, -0.3)) centred on the top face of a unit box: A's top
+      face (edge 2) separates by -0.3, the diamond's faces by -0.566; the diamond's lower edges 2 and 3 are equally
+      anti-parallel to +y (normals (-k, -k) and (k, -k)), so edge 2 is incident: points (-0.3, 0) and (0, -0.3) of B
+      (its vertices 2 and 3), keys (2, 2, F, V) = 66050 and (2, 3, F, V) = 66306."""
+    d = wd.WorldDef(S.stock())
+    g = d.add_body(wd.STATIC)
+    d.add_box(g, (0.5, 0.5))
+    d.add_box(g, (0.5, 0.5))
+    d.add_polygon(g, [(0.3, 0.0), (0.0, 0.3), (-0.3, 0.0), (0.0, -0.3)], raw=True)
+    model, _ = d.build(2)
+    s = S.stock()
+    same = oracle.evaluate(model, 0, 1, _xf(0.7, -0.4), _xf(0.7, -0.4), s)
+    assert (same["mtype"], same["count"]) == (1, 2) and same["point_id"].tolist() == [66048, 66304]
+    assert np.array_equal(same["local_normal"], [0, -1]) and np.array_equal(same["local_point"], [0, -0.5])
+    assert np.allclose(same["point_local"], [[0.5, 0.5], [-0.5, 0.5]], atol=1e-6)  # rounding of the world round trip
+    dia = oracle.evaluate(model, 0, 2, _xf(0.0, 0.0), _xf(0.0, 0.5), s)
+    assert (dia["mtype"], dia["count"]) == (1, 2) and dia["point_id"].tolist() == [66050, 66306]
+    assert np.array_equal(dia["local_normal"], [0, 1]) and np.array_equal(dia["local_point"], [0, 0.5])
+    assert np.allclose(dia["point_local"], [[-0.3, 0.0], [0.0, -0.3]], atol=1e-7)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the TOI event's island walk: order and contact cap   (toi.py:604-716)
+
+def plank_over_bumps(n_bumps=40, capacity=48):
+    """A flat plank (half extents 5.2 x 0.05) falling at 60 m/s onto a row of n_bumps equal static bumps 0.25 m
+    apart, continuous physics on, one TOI event per step: the event's walk meets every bump's contact touching."""
+    s = S.stock(gravity=(0.0, 0.0), continuous_physics=True, max_events=1)
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC)
+    for i in range(n_bumps):
+        d.add_box(g, (0.05, 0.05), ((i - (n_bumps - 1) / 2) * 0.25, 0.0))
+    p = d.add_body(wd.DYNAMIC, (0.0, 0.5), velocity=(0.0, -60.0), mass=1.0, inertia=1.0)
+    d.add_box(p, (5.2, 0.05))
+    model, state = d.build(capacity)
+    cm = wd.compact_model(model, state)
+    return s, cm, wd.batch(wd.compact_state(cm, state), 1)
+
+
+def toi_trace(n, dims):
+    return {k: np.full(shape, -7, np.int32) for k, shape in b2.debug_shapes(n, dims).items()}
+
+
+def test_toi_island_walk_order_and_cap(oracle):
+    """b2World::SolveTOI's island walk (toi.py:604-716): the event's contact is row 0, then bodyA's contacts and then
+    bodyB's, each list newest first (descending key), skipping contacts already in the island and those that do not
+    touch after the update, until the island holds b2_maxTOIContacts = 32 contacts. Here bodyA is the static ground
+    (not walked) and bodyB the plank, whose 40 bump contacts all touch at the event's pose: the rows are the event's
+    contact and then the 31 newest others. toi.solved marks exactly those 32 contacts. (The island's body cap,
+    2 x 32, can never bind: each row adds at most one body to the pair.)"""
+    s, m, st = plank_over_bumps()
+    B, R, J, C = wd.dims(st)
+    dbg = toi_trace(1, (B, R, J, C))
+    oracle.step_(m, st, s, F32(1 / 60), debug=dbg)
+    assert int(st.toi.events[0]) == 1
+    slot = int(dbg["toi_event_slot"][0, 0])
+    rows = dbg["toi_island_rows"][:32, 0].tolist()
+    live = np.nonzero(st.contacts.pair[0] >= 0)[0]
+    assert len(live) == 40 and slot in live.tolist()
+    newest_first = sorted(live.tolist(), key=lambda c: -int(st.contacts.key[0, c]))
+    want = [slot] + [c for c in newest_first if c != slot][:31]
+    assert rows == want
+    assert int(dbg["toi_event_island"][0, 0]) == 32 | (2 << 16)
+    assert np.nonzero(st.toi.solved[0])[0].tolist() == sorted(want)
+    assert dbg["toi_event_slot"][1:, 0].tolist() == [-1] * 7
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# revolute velocity rows: the motor and the limits   (joints.py:257-343)
+#
+# With B's anchor at its centre (rB = 0) on a static A, the point row leaves B's spin alone, so one velocity pass
+# (no position pass) shows the motor and limit rows alone in B's angular velocity after the step: the motor row
+# drives the relative spin to the motor speed unless its accumulated impulse reaches max_motor_torque * dt; the
+# v2.4.1 limits are speculative, their impulses never negative: a joint closing on a limit at distance C ahead ends
+# the pass at -C / dt (it reaches the limit exactly at the step's end), one moving away is left alone; the v2.3.1
+# limit at AT_LOWER / AT_UPPER stops the relative spin into the limit and releases a joint moving out of it.
+
+_VEL_CASES = [  # (name, v24, angle offset from a limit, w0, motor (speed, max torque) or None, expected w)
+    ("motor", True, None, -2.0, (3.0, 1000.0), lambda h: 3.0),
+    ("motor_v23", False, None, -2.0, (3.0, 1000.0), lambda h: 3.0),
+    ("motor_saturated", True, None, -2.0, (3.0, 6.0), lambda h: -2.0 + 4.0 * 6.0 * h),
+    ("lower_closing", True, ("lower", 0.02), -5.0, None, lambda h: -0.02 / h),
+    ("upper_closing", True, ("upper", -0.02), 5.0, None, lambda h: 0.02 / h),
+    ("lower_opening", True, ("lower", 0.02), 1.0, None, lambda h: 1.0),
+    ("at_lower_v23", False, ("lower", -0.01), -5.0, None, lambda h: 0.0),
+    ("leaving_lower_v23", False, ("lower", -0.01), 2.0, None, lambda h: 2.0),
+    ("at_upper_v23", False, ("upper", 0.01), 5.0, None, lambda h: 0.0),
+]
+
+
+@pytest.mark.parametrize("name,v24,where,w0,motor,want", _VEL_CASES, ids=[c[0] for c in _VEL_CASES])
+def test_revolute_velocity_rows(oracle, name, v24, where, w0, motor, want):
+    import dataclasses
+    s = dataclasses.replace(S.stock(gravity=(0.0, 0.0), revolute_v24=v24), velocity_iterations=1,
+                            position_iterations=0, allow_sleep=False)
+    lo, hi, ref = -0.3, 0.5, 0.1
+    angle = 0.0 if where is None else (lo if where[0] == "lower" else hi) + where[1]
+    d = wd.WorldDef(s)
+    a = d.add_body(wd.STATIC, (0.5, 0.5))
+    b = d.add_body(wd.DYNAMIC, (0.5, 0.5), ref + angle, angular_velocity=w0, mass=2.0, inertia=0.25)
+    kw = {} if motor is None else dict(motor_speed=motor[0], max_motor_torque=motor[1], enable_motor=True)
+    d.add_revolute(a, b, (0, 0), (0, 0), ref, limits=None if where is None else (lo, hi), **kw)
+    h = F32(1 / 60)
+    model, state = d.build(4)
+    st = wd.batch(state, 1)
+    oracle.step_(model, st, s, h)
+    assert abs(float(st.bodies.w[0, 1]) - want(float(h))) < 2e-5
