@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "b2_sincos_table.h"
+
 #define GOI_D __device__ __forceinline__
 #define GOI_HD __host__ __device__ __forceinline__
 
@@ -74,26 +76,30 @@ __device__ __noinline__ double2 sincos_lib(double x) {
     return make_double2(s, c);
 }
 
+// sin(j pi/32), cos(j pi/32) for j = 0..63 (b2_sincos_table.h), and the block's copy in LDS, which every kernel that
+// evaluates rot_of loads first (sincos_table_load).
+__device__ const double kSinCosTable[128] = {GOI_SINCOS_TABLE};
+__shared__ __align__(16) double g_sincos_lds[128];
+
+// Copies the table into the block's LDS; called by every lane of the block before its first rot_of.
+GOI_D void sincos_table_load() {
+    for (int i = threadIdx.x; i < 128; i += blockDim.x) g_sincos_lds[i] = kSinCosTable[i];
+    __syncthreads();
+}
+
 // Correctly rounded float32 sin/cos: (float)sin((double)x), the value the reference computes with a float-float
 // series (math2d.py:291-310) and its oracle with the C library (scripts/patches/box2d-2.3.1-trig.patch:17-23).
-// Evaluated on the FP64 units: the double result is within about an ulp of the exact value, so rounding it to float
-// gives the correctly rounded float except when sin x lies within ~2^-52 relative of a float rounding boundary.
 //
-// Method (Cody and Waite's additive range reduction, then Taylor series): k = nearest integer to x * 2/pi and
-// r = x - k * pi/2 with pi/2 split into three doubles, each step one fused multiply-add (exact for the first part,
-// since x and k * P1 agree in their leading bits; then one rounding of the exact remainder per part, so r keeps about
-// an ulp of relative accuracy even when x is close to a multiple of pi/2); on |r| <= pi/4 the series of sin to r^17
-// and of cos to r^16 (truncation below 2^-62 relative) by Horner's rule in fused multiply-adds; the quadrant k mod 4
-// picks and signs the pair. Inline everywhere (about 30 double operations); |x| >= 2^20 calls the library. Checked
-// bit for bit against (float)sin((double)x) of the C library on 24M inputs over +-8 .. +-1e6 and sweeps of every
-// exponent (no difference), and by the known-answer test on the device.
+// Method (constants in b2_sincos_table.h): k = nearest integer to x * 32/pi, r = x - k pi/32 by Cody and Waite's
+// three-part reduction in fused multiply-adds (the first exact: x and k * P1 agree in their leading bits and the
+// difference fits 53 bits for |x| < 2^20); short series of sin r and cos r - 1 on |r| <= pi/64; then the addition
+// formulas with the tabulated St = sin(k pi/32), Ct = cos(k pi/32) (k mod 64), the table value added last:
+// sin x = St + (St (cos r - 1) + Ct sin r), cos x = Ct + (Ct (cos r - 1) - St sin r). Rounded to float, the result
+// equals the C library's (float)sin((double)x) and (float)cos((double)x) for every float with |x| < 2^20 (all
+// 2 x 1.23e9 of them, checked by tests/sincos_check.c, which restates these operations on the CPU; the factored form
+// St cos r + Ct sin r misses one). sin(-0) = -0 is kept by returning a zero angle itself. Angles of magnitude 2^20
+// and above, infinities and NaN call the library's double sin/cos.
 GOI_D Rot rot_of(float a) {
-    Rot q;
-    if (a == 0.0f) {  // a static body at its rest angle, the common case; sin(+-0) = +-0, cos = 1
-        q.s = a;
-        q.c = 1.0f;
-        return q;
-    }
     const double x = (double)a;
     double s, c;
     if (!(fabs(x) < 1048576.0)) {
@@ -101,38 +107,26 @@ GOI_D Rot rot_of(float a) {
         s = sc.x;
         c = sc.y;
     } else {
-        constexpr double kTwoOverPi = 0x1.45f306dc9c883p-1;
-        constexpr double kP1 = 0x1.921fb54442d18p+0, kP2 = 0x1.1a62633145c07p-54, kP3 = -0x1.f1976b7ed8fbcp-110;
-        const double k = rint(x * kTwoOverPi);
-        double r = fma(-k, kP1, x);
-        r = fma(-k, kP2, r);
-        r = fma(-k, kP3, r);
+        const double k = rint(x * GOI_SC_32_OVER_PI);
+        double r = fma(-k, GOI_SC_P1, x);
+        r = fma(-k, GOI_SC_P2, r);
+        r = fma(-k, GOI_SC_P3, r);
         const double r2 = r * r;
-        // sin r = r + r^3 (-1/3! + r^2 (1/5! - ...)), cos r = 1 + r^2 (-1/2! + r^2 (1/4! - ...)): coefficients 1/n!
-        double ps = 0x1.952c77030ad4ap-49;           //  1/17!
-        ps = fma(ps, r2, -0x1.ae7f3e733b81fp-41);    // -1/15!
-        ps = fma(ps, r2, 0x1.6124613a86d09p-33);     //  1/13!
-        ps = fma(ps, r2, -0x1.ae64567f544e4p-26);    // -1/11!
-        ps = fma(ps, r2, 0x1.71de3a556c734p-19);     //  1/9!
-        ps = fma(ps, r2, -0x1.a01a01a01a01ap-13);    // -1/7!
-        ps = fma(ps, r2, 0x1.1111111111111p-7);      //  1/5!
-        ps = fma(ps, r2, -0x1.5555555555555p-3);     // -1/3!
-        double pc = 0x1.ae7f3e733b81fp-45;           //  1/16!
-        pc = fma(pc, r2, -0x1.93974a8c07c9dp-37);    // -1/14!
-        pc = fma(pc, r2, 0x1.1eed8eff8d898p-29);     //  1/12!
-        pc = fma(pc, r2, -0x1.27e4fb7789f5cp-22);    // -1/10!
-        pc = fma(pc, r2, 0x1.a01a01a01a01ap-16);     //  1/8!
-        pc = fma(pc, r2, -0x1.6c16c16c16c17p-10);    // -1/6!
-        pc = fma(pc, r2, 0x1.5555555555555p-5);      //  1/4!
-        pc = fma(pc, r2, -0.5);                      // -1/2!
-        const double sr = fma(r * r2, ps, r), cr = fma(r2, pc, 1.0);
-        const int qd = (int)k & 3;
-        s = (qd & 1) ? cr : sr;
-        c = (qd & 1) ? sr : cr;
-        if (qd == 1 || qd == 2) c = -c;
-        if (qd >= 2) s = -s;
+        double ps = GOI_SC_S9;
+        ps = fma(ps, r2, GOI_SC_S7);
+        ps = fma(ps, r2, GOI_SC_S5);
+        ps = fma(ps, r2, GOI_SC_S3);
+        double pc = GOI_SC_C8;
+        pc = fma(pc, r2, GOI_SC_C6);
+        pc = fma(pc, r2, GOI_SC_C4);
+        pc = fma(pc, r2, GOI_SC_C2);
+        const double sr = fma(r * r2, ps, r), cm1 = r2 * pc;
+        const double2 t = reinterpret_cast<const double2*>(g_sincos_lds)[(int)k & 63];  // St, Ct
+        s = t.x + fma(t.x, cm1, t.y * sr);
+        c = t.y + fma(t.y, cm1, -(t.x * sr));
     }
-    q.s = (float)s;
+    Rot q;
+    q.s = a == 0.0f ? a : (float)s;
     q.c = (float)c;
     return q;
 }

@@ -453,11 +453,16 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     }
     const float mA_ = W.f(GOI_B_INV_MASS, A), iA_ = W.f(GOI_B_INV_INERTIA, A);
     const float mB_ = W.f(GOI_B_INV_MASS, Bb), iB_ = W.f(GOI_B_INV_INERTIA, Bb);
+    // The rows do not change across the passes: the island's first two (most islands have one or two; a world whose
+    // passes run to the cap of 20 spends most of its events here) stay in registers, loaded once; rows past them
+    // are read from the row tile in each pass.
+    const PRow r0 = load_prow(CR, 0);
+    const PRow r1 = nc > 1 ? load_prow(CR, 1) : r0;
     RotMemo qa, qb;
     for (int it = 0; it < 20; ++it) {
         float min_sep = 0.0f;
         for (int i = 0; i < nc; ++i) {
-            const PRow cur = load_prow(CR, i);
+            const PRow cur = i == 0 ? r0 : i == 1 ? r1 : load_prow(CR, i);
             const int ia = cur.ia, ib = cur.ib;
             const bool ta = ia == A || ia == Bb, tb = ib == A || ib == Bb;
             const float mA = ta ? (ia == A ? mA_ : mB_) : 0.0f, iA = ta ? (ia == A ? iA_ : iB_) : 0.0f;

@@ -156,6 +156,7 @@ __device__ __forceinline__ Coop block_coop(const Launch& L, const World& W, int*
 // part in Collide's manifold evaluations.
 __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int start_only) {
     extern __shared__ int lds[];
+    sincos_table_load();
     stage_nodes(m, L, lds);
     const int lane = threadIdx.x;
     const int w0 = xcd_group() * L.wpw;
@@ -180,6 +181,7 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
 template <bool kMulti>
 __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     extern __shared__ int lds[];
+    sincos_table_load();
     stage_nodes(m, L, lds);
     const int lane = threadIdx.x;
     const int w0 = xcd_group() * L.wpw;
@@ -321,6 +323,7 @@ __global__ void k_motor_actions(const float* a, float* speed, float* torque, int
 }
 
 __global__ void k_sincos(const float* x, float* s, float* c, int n) {
+    sincos_table_load();
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const Rot q = rot_of(x[i]);
@@ -668,8 +671,9 @@ static int cu_count() {
 }
 
 // LDS workspace bytes per world (Workspace::layout) and the block budget it is held to.
-constexpr size_t kMaxLdsBytes = 64 * 1024;   // workspaces + scan space of one block
-constexpr size_t kCuLdsBytes = 160 * 1024;    // LDS of one CU, shared by the blocks resident on it
+constexpr size_t kStaticLdsBytes = sizeof(g_sincos_lds);      // each block's static LDS: the sin/cos table
+constexpr size_t kMaxLdsBytes = 64 * 1024 - kStaticLdsBytes;   // workspaces + scan space of one block
+constexpr size_t kCuLdsBytes = 160 * 1024;                      // LDS of one CU, shared by the blocks resident on it
 static size_t workspace_bytes(int B, int C, int J, int R) {
     return (size_t)Workspace::layout(B, C, J, R).words * sizeof(int);
 }
@@ -717,7 +721,7 @@ static void fill_launch(Launch& L, const GoiModel* M, const GoiStateView* v, con
     // when every block of the launch is resident at once (ceil(blocks / CUs) per CU).
     const long blocks = (v->n_worlds + L.wpw - 1) / L.wpw;
     const long per_cu = std::max<long>(1, (blocks + cu_count() - 1) / cu_count());
-    const size_t budget = kCuLdsBytes / per_cu;
+    const size_t budget = kCuLdsBytes / per_cu - kStaticLdsBytes;
     const size_t base = (size_t)node_offset(Workspace::layout(v->B, v->C, v->J, v->R).words, L.wpw) * sizeof(int);
     const size_t room = base < budget ? (budget - base) / (sizeof(float4) + sizeof(int2)) : 0;
     L.lds_nodes = (int)std::min<size_t>((size_t)M->d.n_nodes, room);
