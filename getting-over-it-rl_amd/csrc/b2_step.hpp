@@ -454,19 +454,32 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     const float mA_ = W.f(GOI_B_INV_MASS, A), iA_ = W.f(GOI_B_INV_INERTIA, A);
     const float mB_ = W.f(GOI_B_INV_MASS, Bb), iB_ = W.f(GOI_B_INV_INERTIA, Bb);
     // The rows do not change across the passes: the island's first two (most islands have one or two; a world whose
-    // passes run to the cap of 20 spends most of its events here) stay in registers, loaded once; rows past them
-    // are read from the row tile in each pass.
+    // passes run to the cap of 20 spends most of its events here) stay in registers, loaded once, each with its own
+    // rotation memos (a static side's rotation is then computed once per event); rows past them are read from the row
+    // tile in each pass and share a pair of memos.
     const PRow r0 = load_prow(CR, 0);
     const PRow r1 = nc > 1 ? load_prow(CR, 1) : r0;
-    RotMemo qa, qb;
+    const auto masses = [&](const PRow& r, float& mA, float& mB, float& iA, float& iB) {
+        const bool ta = r.ia == A || r.ia == Bb, tb = r.ib == A || r.ib == Bb;
+        mA = ta ? (r.ia == A ? mA_ : mB_) : 0.0f;
+        iA = ta ? (r.ia == A ? iA_ : iB_) : 0.0f;
+        mB = tb ? (r.ib == A ? mA_ : mB_) : 0.0f;
+        iB = tb ? (r.ib == A ? iA_ : iB_) : 0.0f;
+    };
+    float m0A, m0B, i0A, i0B, m1A, m1B, i1A, i1B;
+    masses(r0, m0A, m0B, i0A, i0B);
+    masses(r1, m1A, m1B, i1A, i1B);
+    RotMemo qa0, qb0, qa1, qb1, qa, qb;
     for (int it = 0; it < 20; ++it) {
-        float min_sep = 0.0f;
-        for (int i = 0; i < nc; ++i) {
-            const PRow cur = i == 0 ? r0 : i == 1 ? r1 : load_prow(CR, i);
-            const int ia = cur.ia, ib = cur.ib;
-            const bool ta = ia == A || ia == Bb, tb = ib == A || ib == Bb;
-            const float mA = ta ? (ia == A ? mA_ : mB_) : 0.0f, iA = ta ? (ia == A ? iA_ : iB_) : 0.0f;
-            const float mB = tb ? (ib == A ? mA_ : mB_) : 0.0f, iB = tb ? (ib == A ? iA_ : iB_) : 0.0f;
+        float min_sep = solve_prow(bd, r0, s.toi_baumgarte, m0A, m0B, i0A, i0B, s.linear_slop, s.max_linear_correction,
+                                   qa0, qb0);
+        if (nc > 1)
+            min_sep = bmin(min_sep, solve_prow(bd, r1, s.toi_baumgarte, m1A, m1B, i1A, i1B, s.linear_slop,
+                                               s.max_linear_correction, qa1, qb1));
+        for (int i = 2; i < nc; ++i) {
+            const PRow cur = load_prow(CR, i);
+            float mA, mB, iA, iB;
+            masses(cur, mA, mB, iA, iB);
             min_sep = bmin(min_sep, solve_prow(bd, cur, s.toi_baumgarte, mA, mB, iA, iB, s.linear_slop,
                                                s.max_linear_correction, qa, qb));
         }

@@ -83,11 +83,13 @@ struct Proxy {
     V2 v[kPoly];
     int count;
     float radius;
-    // vertex i (0 <= i < count) without dynamic register indexing
+    // vertex i (0 <= i < count) without dynamic register indexing: a chain of selects that starts from a constant
+    // (a chain of selects between loads would fold into one load from a selected address, which keeps the vertex
+    // array in private scratch memory)
     GOI_D V2 at(int i) const {
-        V2 r = v[0];
+        V2 r = mk(0.0f, 0.0f);
 #pragma unroll
-        for (int j = 1; j < kPoly; ++j)
+        for (int j = 0; j < kPoly; ++j)
             if (i == j) r = v[j];
         return r;
     }
