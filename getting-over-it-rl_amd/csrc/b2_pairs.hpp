@@ -308,47 +308,64 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         rows |= 1ull << r;
         U.x = fminf(U.x, q.x); U.y = fminf(U.y, q.y); U.z = fmaxf(U.z, q.z); U.w = fmaxf(U.w, q.w);
     }
-    // stackless preorder walk: descend into a node the union overlaps, else jump past its subtree
-    int nd = rows ? 0 : m.n_nodes;
-    while (nd < m.n_nodes) {
-        const bool staged = nd < W.nk;  // the first nodes come from LDS, the rest from global memory
-        const int2 ln = staged ? W.nlink[nd] : m.node_link[nd];
-        const float4 nb = staged ? W.nbox[nd] : m.node_box[nd];
-        if (!overlap(U, nb)) {
-            nd = ln.x;
-            continue;
-        }
-        if (ln.y < 0) {
-            ++nd;
-            continue;
-        }
-        nd = ln.x;
-        // a leaf's entries (at most 4; the arrays are padded by 4) load together and take the cheap union-box test;
-        // the few that pass are then tested row by row (one copy of that code, not one per entry), and only a hit
-        // reads its candidate index
-        const int first = ln.y >> 3, cnt = ln.y & 7;
-        float4 sf[4];
-        int info[4];
+    // the static tree, depth first: the lane group tests a node's 8 child boxes together against the union box; per
+    // level, the node and the mask of its overlapping children not yet visited (registers, selected by level)
+    if (rows && m.n_wnodes > 0) {
+        int path[kWideDepth];
+        unsigned masks[kWideDepth];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            sf[j] = m.leaf_fat[first + j];
-            info[j] = m.leaf_info[first + j];
-        }
-        unsigned hits = 0u;
+        for (int l = 0; l < kWideDepth; ++l) { path[l] = 0; masks[l] = 0u; }
+        const auto children = [&](int nd) {
+            unsigned hit = 0u;
+            for (int j = W.sub; j < 8; j += W.G)
+                if (overlap(U, m.wbox[8 * nd + j])) hit |= 1u << j;
+            return group_or(W.grp(), hit);
+        };
+        masks[0] = children(0);
+        int level = 0;
+        for (;;) {
+            int nd = 0;
+            unsigned cm = 0u;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (j < cnt && overlap(sf[j], U) && W.active(info[j] & 0xffff)) hits |= 1u << j;
-        for (; hits; hits &= hits - 1u) {
-            const int j = __builtin_ctz(hits);
-            const float4 fj = m.leaf_fat[first + j];
-            const int ij = m.leaf_info[first + j];
-            for (unsigned long long left = rows; left; left &= left - 1) {
-                const int r = __builtin_ctzll(left);
-                if (!overlap(fj, W.get_qbox(r))) continue;
-                if (!(m.row_dynamic[r] || (ij >> 16))) continue;
-                const int p = m.leaf_cand[(size_t)(first + j) * m.R + r];
-                if (p < 0 || slot_has_pair(W, p)) continue;
-                np.add(p);
+            for (int l = 0; l < kWideDepth; ++l)
+                if (l == level) { nd = path[l]; cm = masks[l]; }
+            if (cm == 0u) {
+                if (level == 0) break;
+                --level;
+                continue;
+            }
+            const int k = __builtin_ctz(cm);
+#pragma unroll
+            for (int l = 0; l < kWideDepth; ++l)
+                if (l == level) masks[l] = cm & (cm - 1u);
+            const int ref = m.wref[8 * nd + k];
+            if (ref >= 0) {  // an inner node one level down
+                const unsigned hit = children(ref);
+                ++level;
+#pragma unroll
+                for (int l = 0; l < kWideDepth; ++l)
+                    if (l == level) { path[l] = ref; masks[l] = hit; }
+                continue;
+            }
+            // a leaf's entries (at most 8, one per lane) take the cheap union-box test; the few that pass are then
+            // tested row by row (one copy of that code, not one per entry), and only a hit reads its candidate index
+            const int first = (~ref) >> 4, cnt = (~ref) & 15;
+            unsigned hits = 0u;
+            for (int j = W.sub; j < cnt; j += W.G)
+                if (overlap(m.leaf_fat[first + j], U) && W.active(m.leaf_info[first + j] & 0xffff)) hits |= 1u << j;
+            hits = group_or(W.grp(), hits);
+            for (; hits; hits &= hits - 1u) {
+                const int j = __builtin_ctz(hits);
+                const float4 fj = m.leaf_fat[first + j];
+                const int ij = m.leaf_info[first + j];
+                for (unsigned long long left = rows; left; left &= left - 1) {
+                    const int r = __builtin_ctzll(left);
+                    if (!overlap(fj, W.get_qbox(r))) continue;
+                    if (!(m.row_dynamic[r] || (ij >> 16))) continue;
+                    const int p = m.leaf_cand[(size_t)(first + j) * m.R + r];
+                    if (p < 0 || slot_has_pair(W, p)) continue;
+                    np.add(p);
+                }
             }
         }
     }

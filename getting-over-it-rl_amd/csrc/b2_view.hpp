@@ -11,6 +11,8 @@
 namespace goi {
 
 // Device copy of the Model plus the static-terrain acceleration structures built by goi_model_create.
+constexpr int kWideDepth = 8;  // levels of the static tree below its root, at most
+
 struct DModel {
     int F, J, P, B, R;  // R = non-static fixture rows (compact layout)
     const int* fixture_body;
@@ -40,14 +42,15 @@ struct DModel {
     int any_toi_body;           // Model.toi_bodies has a set entry (or is absent)
     int rev_only;               // every joint is revolute
     int no_edges;               // no edge fixture
-    // Static BVH over the static fixtures' fat AABBs, nodes in preorder (node 0 = root, a node's first child is the
-    // next node). node_link.x = escape: the node after this node's subtree; node_link.y = -1 for an internal node,
-    // (first << 3) | count for a leaf of `count` (<= 4) entries of leaf_fixture starting at `first`.
-    int n_nodes;
-    const float4* node_box;     // [n_nodes] lx ly ux uy
-    const int2* node_link;      // [n_nodes]
-    const float4* leaf_fat;     // [n_leaf + 4] fat AABB of each leaf entry (a static fixture); 4 padding records
-    const int* leaf_info;       // [n_leaf + 4] the entry's body | (body is dynamic) << 16
+    // Static 8-wide tree over the static fixtures' fat AABBs (node 0 = the root): child j of node k has the box
+    // wbox[8k + j] and the reference wref[8k + j], either a child node (>= 0) or a leaf, ~(first << 4 | count), of
+    // count (1..8) consecutive entries of the leaf_* arrays from first; an unused child slot holds an empty box
+    // (lx > ux), which overlaps nothing. Nodes lie at most kWideDepth levels below the root.
+    int n_wnodes;               // 0 without static fixtures
+    const float4* wbox;         // [8 n_wnodes] lx ly ux uy
+    const int* wref;            // [8 n_wnodes]
+    const float4* leaf_fat;     // [n_leaf] fat AABB of each leaf entry (a static fixture)
+    const int* leaf_info;       // [n_leaf] the entry's body | (body is dynamic) << 16
     const int* leaf_cand;       // [n_leaf * R]: candidate index of (leaf entry i, row r), -1 if none
     const int* row_dynamic;     // [R] the row's body is dynamic
     const int* row_body;        // [R] the row's body
@@ -119,9 +122,6 @@ struct World {
     int* ws;          // LDS workspace base + the world's index in the block
     int S;            // workspace stride (worlds per block)
     Workspace k;
-    const float4* nbox;  // the static BVH's first nk nodes, staged in LDS by the block
-    const int2* nlink;
-    int nk;
     unsigned long long smask, dmask;  // static and dynamic bodies (Model.body_type, the same in every world)
     int sub, G;       // the lane's place in the world's lane group, and the group's size
 

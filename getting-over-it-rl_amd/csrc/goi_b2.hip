@@ -48,7 +48,6 @@ struct Launch {
     void* leaf[GOI_NUM_LEAVES];
     int n, pitch, B, C, R, J;
     int wpw;  // worlds per wavefront: lanes >= wpw idle, so small batches still spread over every SIMD
-    int lds_nodes;  // BVH nodes staged in LDS per block
     uint32_t* scratch;  // contact rows then joint rows
     GoiSettings s;
     float dt;
@@ -56,9 +55,6 @@ struct Launch {
     GoiDebug dbg;
 };
 
-// The block's LDS: the worlds' workspaces (words x wpw ints), 64 ints of scan space, then the staged BVH nodes
-// (float4 boxes, then int2 links) at a 16-byte aligned offset.
-__host__ __device__ inline int node_offset(int words, int wpw) { return ((words * wpw + kBlock) + 3) & ~3; }
 
 // World w on lane `lane` of its block; the block's LDS workspace holds L.wpw lanes.
 __device__ __forceinline__ World make_world(const DModel& m, const Launch& L, int w, int* lds, int lane, int sub,
@@ -74,25 +70,10 @@ __device__ __forceinline__ World make_world(const DModel& m, const Launch& L, in
     W.k = Workspace::layout(L.B, L.C, L.J, L.R);
     W.ws = lds + lane;
     W.S = L.wpw;
-    W.nk = L.lds_nodes;
-    W.nbox = reinterpret_cast<const float4*>(lds + node_offset(W.k.words, L.wpw));
-    W.nlink = reinterpret_cast<const int2*>(W.nbox + L.lds_nodes);
     W.sub = sub;
     W.G = G;
     W.init_masks(m);
     return W;
-}
-
-// All lanes of the block copy the first L.lds_nodes BVH nodes into LDS.
-__device__ __forceinline__ void stage_nodes(const DModel& m, const Launch& L, int* lds) {
-    const int words = Workspace::layout(L.B, L.C, L.J, L.R).words;
-    float4* box = reinterpret_cast<float4*>(lds + node_offset(words, L.wpw));
-    int2* link = reinterpret_cast<int2*>(box + L.lds_nodes);
-    for (int i = threadIdx.x; i < L.lds_nodes; i += kBlock) {
-        box[i] = m.node_box[i];
-        link[i] = m.node_link[i];
-    }
-    __syncthreads();
 }
 
 // The scratch rows of world w0 + wl of this block (tile = the block's world group): the contact rows' tiles, then
@@ -157,7 +138,6 @@ __device__ __forceinline__ Coop block_coop(const Launch& L, const World& W, int*
 __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int start_only) {
     extern __shared__ int lds[];
     sincos_table_load();
-    stage_nodes(m, L, lds);
     const int lane = threadIdx.x;
     const int w0 = xcd_group() * L.wpw;
     const LaneMap lm = lane_map(L, w0, lane);
@@ -182,7 +162,6 @@ template <bool kMulti>
 __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     extern __shared__ int lds[];
     sincos_table_load();
-    stage_nodes(m, L, lds);
     const int lane = threadIdx.x;
     const int w0 = xcd_group() * L.wpw;
     const LaneMap lm = lane_map(L, w0, lane);
@@ -401,11 +380,14 @@ int upload(GoiModel* M, const T* host, size_t n, const T*& dev, hipStream_t st) 
     return GOI_OK;
 }
 
-struct BvhBuild {
+// The static fixtures' 8-wide tree (DModel::wbox / wref): a node splits its entries by three rounds of median
+// splits on the longer axis of their centroid bounds (a range of at most 8 entries is not split further) into up to
+// 8 children; a child of at most 8 entries is a leaf, a larger one an inner node. Entries end in leaf order.
+struct WideBuild {
     const float* fat;  // [F, 4]
     std::vector<int> leaf;
-    std::vector<float4> box;
-    std::vector<int2> link;  // (escape, -1) internal; (escape, first << 3 | count) leaf
+    std::vector<float4> box;  // 8 per node
+    std::vector<int> ref;     // 8 per node
     int max_depth = 0;
 
     float4 bounds(int lo, int hi) const {
@@ -417,16 +399,7 @@ struct BvhBuild {
         }
         return b;
     }
-    // median split on the longer axis of the centroid bounds; leaves of up to 4 fixtures; nodes in preorder
-    void build(int lo, int hi, int depth) {
-        max_depth = std::max(max_depth, depth);
-        const int node = (int)box.size();
-        box.push_back(bounds(lo, hi));
-        link.push_back(make_int2(0, -1));
-        if (hi - lo <= 4) {
-            link[node] = make_int2(node + 1, (lo << 3) | (hi - lo));
-            return;
-        }
+    int split(int lo, int hi) {
         float cx0 = 3.4e38f, cy0 = 3.4e38f, cx1 = -3.4e38f, cy1 = -3.4e38f;
         for (int i = lo; i < hi; ++i) {
             const float* f = fat + 4 * leaf[i];
@@ -442,9 +415,35 @@ struct BvhBuild {
             const float ca = fa[axis] + fa[axis + 2], cb = fb[axis] + fb[axis + 2];
             return ca < cb || (ca == cb && a < b);
         });
-        build(lo, mid, depth + 1);
-        build(mid, hi, depth + 1);
-        link[node] = make_int2((int)box.size(), -1);
+        return mid;
+    }
+    // node over entries [lo, hi) at `depth` levels below the root; returns its index
+    int build(int lo, int hi, int depth) {
+        max_depth = std::max(max_depth, depth);
+        const int node = (int)(box.size() / 8);
+        box.resize(box.size() + 8, make_float4(3.4e38f, 3.4e38f, -3.4e38f, -3.4e38f));
+        ref.resize(ref.size() + 8, 0);
+        std::vector<int2> parts{make_int2(lo, hi)};
+        for (int round = 0; round < 3; ++round) {
+            std::vector<int2> next;
+            for (const int2 r : parts) {
+                if (r.y - r.x <= 8) {
+                    next.push_back(r);
+                    continue;
+                }
+                const int mid = split(r.x, r.y);
+                next.push_back(make_int2(r.x, mid));
+                next.push_back(make_int2(mid, r.y));
+            }
+            parts.swap(next);
+        }
+        for (size_t j = 0; j < parts.size(); ++j) {
+            const int a = parts[j].x, b = parts[j].y;
+            const int child = b - a <= 8 ? ~((a << 4) | (b - a)) : build(a, b, depth + 1);
+            box[8 * node + j] = bounds(a, b);
+            ref[8 * node + j] = child;
+        }
+        return node;
     }
 };
 
@@ -521,24 +520,28 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
         else if (rb < 0 && ra >= 0) cand[(size_t)b * R + ra] = p;
         else { delete M; return fail(GOI_E_UNSUPPORTED, "goi_model_create: candidate between two static fixtures"); }
     }
-    // static BVH
-    BvhBuild bvh;
-    bvh.fat = desc->static_fat;
+    // the static tree
+    WideBuild tree;
+    tree.fat = desc->static_fat;
     for (int f = 0; f < F; ++f)
-        if (desc->fixture_slot[f] < 0) bvh.leaf.push_back(f);
-    if (!bvh.leaf.empty()) bvh.build(0, (int)bvh.leaf.size(), 1);
-    if (bvh.max_depth > 30 || bvh.leaf.size() >= (1u << 27)) {
+        if (desc->fixture_slot[f] < 0) tree.leaf.push_back(f);
+    if (tree.leaf.size() >= (1u << 26)) {
         delete M;
-        return fail(GOI_E_UNSUPPORTED, "goi_model_create: static terrain too large for the BVH");
+        return fail(GOI_E_UNSUPPORTED, "goi_model_create: static terrain too large for the tree");
     }
-    d.n_nodes = (int)bvh.box.size();
+    if (!tree.leaf.empty()) tree.build(0, (int)tree.leaf.size(), 0);
+    if (tree.max_depth >= kWideDepth) {
+        delete M;
+        return fail(GOI_E_UNSUPPORTED, "goi_model_create: static tree deeper than its traversal allows");
+    }
+    d.n_wnodes = (int)(tree.box.size() / 8);
     // per leaf entry: fat box, body, candidate row; per row: dynamic body
-    const size_t n_leaf = bvh.leaf.size();
-    // entry records padded by 4 so that a leaf's 4 records always load in bounds
-    std::vector<float4> leaf_fat(n_leaf + 4, make_float4(0.f, 0.f, 0.f, 0.f));
-    std::vector<int> leaf_info(n_leaf + 4, 0), leaf_cand(std::max<size_t>(n_leaf * R, 1), -1), row_dyn(std::max(R, 1), 0);
+    const size_t n_leaf = tree.leaf.size();
+    std::vector<float4> leaf_fat(std::max<size_t>(n_leaf, 1), make_float4(0.f, 0.f, 0.f, 0.f));
+    std::vector<int> leaf_info(std::max<size_t>(n_leaf, 1), 0), leaf_cand(std::max<size_t>(n_leaf * R, 1), -1),
+        row_dyn(std::max(R, 1), 0);
     for (size_t i = 0; i < n_leaf; ++i) {
-        const int f = bvh.leaf[i], b = desc->fixture_body[f];
+        const int f = tree.leaf[i], b = desc->fixture_body[f];
         leaf_fat[i] = make_float4(desc->static_fat[4 * f], desc->static_fat[4 * f + 1], desc->static_fat[4 * f + 2],
                                   desc->static_fat[4 * f + 3]);
         leaf_info[i] = b | ((desc->body_type[b] == GOI_DYNAMIC ? 1 : 0) << 16);
@@ -591,10 +594,10 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     }
     UP(centroid, cen.data(), F);
     UP(edge_flags, eflags.data(), F);
-    UP(node_box, bvh.box.data(), bvh.box.size());
-    UP(node_link, bvh.link.data(), bvh.link.size());
-    UP(leaf_fat, leaf_fat.data(), leaf_fat.size());
-    UP(leaf_info, leaf_info.data(), leaf_info.size());
+    UP(wbox, tree.box.data(), tree.box.size());
+    UP(wref, tree.ref.data(), tree.ref.size());
+    UP(leaf_fat, leaf_fat.data(), n_leaf);
+    UP(leaf_info, leaf_info.data(), n_leaf);
     UP(leaf_cand, leaf_cand.data(), n_leaf * R);
     UP(row_dynamic, row_dyn.data(), R);
     UP(row_body, row_body.data(), R);
@@ -673,7 +676,6 @@ static int cu_count() {
 // LDS workspace bytes per world (Workspace::layout) and the block budget it is held to.
 constexpr size_t kStaticLdsBytes = sizeof(g_sincos_lds);      // each block's static LDS: the sin/cos table
 constexpr size_t kMaxLdsBytes = 64 * 1024 - kStaticLdsBytes;   // workspaces + scan space of one block
-constexpr size_t kCuLdsBytes = 160 * 1024;                      // LDS of one CU, shared by the blocks resident on it
 static size_t workspace_bytes(int B, int C, int J, int R) {
     return (size_t)Workspace::layout(B, C, J, R).words * sizeof(int);
 }
@@ -697,10 +699,10 @@ static int worlds_per_wave(int n, size_t ws_bytes_per_world) {
     return wpw;
 }
 
-// LDS bytes of one block of launch L
+// The dynamic LDS of one block of launch L: the worlds' workspaces (words x wpw ints), then 64 ints of scan space.
 static size_t block_lds_bytes(const Launch& L) {
     const int words = Workspace::layout(L.B, L.C, L.J, L.R).words;
-    return (size_t)node_offset(words, L.wpw) * sizeof(int) + (size_t)L.lds_nodes * (sizeof(float4) + sizeof(int2));
+    return ((size_t)words * L.wpw + kBlock) * sizeof(int);
 }
 
 static void fill_launch(Launch& L, const GoiModel* M, const GoiStateView* v, const GoiSettings* s, float dt) {
@@ -717,14 +719,6 @@ static void fill_launch(Launch& L, const GoiModel* M, const GoiStateView* v, con
     std::memset(&L.dbg, 0, sizeof(L.dbg));
     L.scratch = nullptr;
     L.wpw = worlds_per_wave(v->n_worlds, workspace_bytes(v->B, v->C, v->J, v->R));
-    // Stage as many BVH nodes (preorder: the root and the tree's upper-left part first) as the LDS left over allows
-    // when every block of the launch is resident at once (ceil(blocks / CUs) per CU).
-    const long blocks = (v->n_worlds + L.wpw - 1) / L.wpw;
-    const long per_cu = std::max<long>(1, (blocks + cu_count() - 1) / cu_count());
-    const size_t budget = kCuLdsBytes / per_cu - kStaticLdsBytes;
-    const size_t base = (size_t)node_offset(Workspace::layout(v->B, v->C, v->J, v->R).words, L.wpw) * sizeof(int);
-    const size_t room = base < budget ? (budget - base) / (sizeof(float4) + sizeof(int2)) : 0;
-    L.lds_nodes = (int)std::min<size_t>((size_t)M->d.n_nodes, room);
 }
 
 // Words of constraint and task rows a launch over `state` uses: per world C contact rows and J joint rows, in tiles of
