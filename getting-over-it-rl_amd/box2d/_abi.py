@@ -12,7 +12,7 @@ import numpy as np
 PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = PKG / "lib" / "libgoi_b2.so"
 NUM_LEAVES = 71
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 GOI_OK, GOI_E_ARG, GOI_E_SHAPE, GOI_E_HIP, GOI_E_UNSUPPORTED = 0, -1, -2, -3, -4
 
@@ -65,7 +65,8 @@ class GoiDebug(ctypes.Structure):
 
 
 EXPORTS = ("goi_abi_version", "goi_model_create", "goi_model_destroy", "goi_step", "goi_step_n", "goi_step_n_noalloc",
-           "goi_collide", "goi_world_manifold", "goi_apply_motor_actions", "goi_sincos", "goi_last_error")
+           "goi_collide", "goi_world_manifold", "goi_apply_motor_actions", "goi_sincos", "goi_packed_layout",
+           "goi_last_error")
 
 _LIB = None
 
@@ -102,6 +103,9 @@ def lib(path=None):
     L.goi_apply_motor_actions.restype = ctypes.c_int32
     L.goi_sincos.argtypes = [_P, _P, _P, ctypes.c_int32, _P]
     L.goi_sincos.restype = ctypes.c_int32
+    L.goi_packed_layout.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                    ctypes.POINTER(ctypes.c_int32)]
+    L.goi_packed_layout.restype = ctypes.c_int32
     if L.goi_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{p}: ABI version {L.goi_abi_version()} != {ABI_VERSION}")
     if path is None:

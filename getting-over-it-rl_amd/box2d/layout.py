@@ -17,10 +17,33 @@ def _dtype(dt):
     return _TORCH[np.dtype(dt)]
 
 
-def empty_device_state(n, dims, device="cuda", pitch=None):
-    """An uninitialised device State of n worlds with capacities dims = (B, R, J, C)."""
+def packed_words(dims):
+    """The packed layout of capacities dims = (B, R, J, C): words[l] = 4-byte words per unit of pitch before leaf l
+    (each leaf's per-world bytes rounded up to a multiple of 4), words[-1] the whole; the library's goi_packed_layout
+    gives the same table."""
+    words = [0]
+    for _, _, dt, inner in wd.LEAVES:
+        nbytes = int(np.prod(wd.leaf_shape(inner, dims), dtype=np.int64)) * np.dtype(dt).itemsize
+        words.append(words[-1] + (nbytes + 3) // 4)
+    return words
+
+
+def empty_device_state(n, dims, device="cuda", pitch=None, packed=True):
+    """An uninitialised device State of n worlds with capacities dims = (B, R, J, C), pitch n by default. With a pitch
+    that is a multiple of 64 the leaves are by default the consecutive parts of one buffer (the packed layout), which
+    lets the step address every leaf from one base pointer; packed=False, or another pitch, gives one buffer per
+    leaf."""
     pitch = n if pitch is None else pitch
     vals = []
+    if packed and pitch > 0 and pitch % 64 == 0:
+        words = packed_words(dims)
+        buf = torch.empty(words[-1] * 4 * pitch, dtype=torch.uint8, device=device)
+        for (_, _, dt, inner), w in zip(wd.LEAVES, words):
+            shape = wd.leaf_shape(inner, dims)
+            nbytes = int(np.prod(shape, dtype=np.int64)) * np.dtype(dt).itemsize * pitch
+            part = buf[4 * w * pitch:4 * w * pitch + nbytes].view(_dtype(dt)).view(tuple(shape) + (pitch,))
+            vals.append(part[..., :n].movedim(-1, 0))
+        return wd.from_leaves(vals)
     for _, _, dt, inner in wd.LEAVES:
         shape = wd.leaf_shape(inner, dims)
         buf = torch.empty(tuple(shape) + (pitch,), dtype=_dtype(dt), device=device)
@@ -28,12 +51,12 @@ def empty_device_state(n, dims, device="cuda", pitch=None):
     return wd.from_leaves(vals)
 
 
-def to_device(state, device="cuda", pitch=None):
-    """A batched numpy State (leading world axis) to a device State."""
+def to_device(state, device="cuda", pitch=None, packed=True):
+    """A batched numpy State (leading world axis) to a device State (packed by default, as empty_device_state)."""
     leaves = wd.leaves(state)
     n = np.asarray(leaves[0]).shape[0]
     dims = wd.dims(state)
-    out = empty_device_state(n, dims, device, pitch)
+    out = empty_device_state(n, dims, device, pitch, packed)
     for dst, src in zip(wd.leaves(out), leaves):
         src = np.asarray(src)
         dst.copy_(torch.from_numpy(np.ascontiguousarray(src)).to(device))
@@ -54,6 +77,12 @@ def clone(state):
     for dst, src in zip(wd.leaves(out), leaves):
         dst.copy_(src)
     return out
+
+
+def pitch_of(state):
+    """The worlds-minor pitch of a device State's leaves."""
+    t = state.bodies.xf_p
+    return t.stride(-1) if t.dim() > 1 else t.shape[0]
 
 
 def state_view(state):

@@ -146,17 +146,20 @@ def sincos(x):
 
 
 def debug_shapes(n, dims):
-    """{GoiDebug field: (rows, n)} of the debug arrays for n worlds of capacities dims = (B, R, J, C)."""
+    """{GoiDebug field: (rows, n)} of the debug arrays for n worlds (or a pitch of n) of capacities dims = (B, R, J,
+    C)."""
     B, _, _, C = dims
     E, Rw = _abi.DEBUG_TOI_EVENTS, _abi.DEBUG_TOI_ROWS
     return dict(body_island=(B, n), contact_island=(C, n), contact_order=(C, n), n_islands=(n,),
                 toi_event_slot=(E, n), toi_event_alpha=(E, n), toi_event_island=(E, n), toi_island_rows=(E * Rw, n))
 
 
-def make_debug(n, dims, device="cuda"):
-    """GoiDebug buffers (islands, solve order, TOI event traces) for a device State of n worlds; returns (struct,
-    tensors)."""
-    t = {k: torch.full(shape, -7, dtype=torch.int32, device=device) for k, shape in debug_shapes(n, dims).items()}
+def make_debug(n, dims, device="cuda", pitch=None):
+    """GoiDebug buffers (islands, solve order, TOI event traces) for a device State of n worlds whose leaves have the
+    given pitch (n by default; the kernels write element (i, w) at [i * pitch + w]); returns (struct, tensors) with
+    the tensors as (rows, pitch)."""
+    t = {k: torch.full(shape, -7, dtype=torch.int32, device=device)
+         for k, shape in debug_shapes(n if pitch is None else pitch, dims).items()}
     d = _abi.GoiDebug()
     for k, v in t.items():
         setattr(d, k, ctypes.c_void_p(v.data_ptr()))

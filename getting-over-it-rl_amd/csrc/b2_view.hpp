@@ -113,6 +113,95 @@ struct Workspace {
     }
 };
 
+// ---- State leaf shapes and the packed layout
+//
+// Per-world element count of each leaf: dim (0 = B, 1 = R, 2 = J, 3 = C, 4 = one per world) times mult, of `bytes`
+// each (the enum GoiLeaf table of goi_b2.h). A packed State holds its leaves as consecutive parts of one device
+// buffer in leaf order, leaf l taking leaf_words(l) x pitch 4-byte words (its per-world bytes rounded up to a
+// multiple of 4); with the pitch a multiple of 64, element (i, w) of leaf l is then element
+// ((4 / bytes) packed_word(l) + i) x pitch + w of the buffer viewed with the leaf's element type, one base pointer
+// for every leaf.
+struct LeafDim {
+    unsigned char dim, mult, bytes;
+};
+constexpr LeafDim kLeafDims[GOI_NUM_LEAVES] = {
+    {0, 1, 4}, {0, 1, 1}, {0, 1, 1}, {0, 1, 1}, {0, 1, 1}, {0, 1, 1}, {0, 1, 4}, {0, 2, 4}, {0, 2, 4}, {0, 2, 4},
+    {0, 2, 4}, {0, 2, 4}, {0, 1, 4}, {0, 1, 4}, {0, 2, 4}, {0, 1, 4}, {0, 2, 4}, {0, 1, 4}, {0, 1, 4}, {0, 1, 4},
+    {0, 1, 4}, {0, 1, 4}, {0, 1, 4}, {0, 1, 4}, {0, 1, 4},                                    // bodies
+    {1, 1, 4}, {1, 1, 4}, {1, 4, 4},                                                          // fixtures
+    {2, 1, 1}, {2, 1, 4}, {2, 1, 4}, {2, 1, 1}, {2, 1, 4}, {2, 1, 4}, {2, 1, 4}, {2, 1, 4}, {2, 3, 4}, {2, 1, 4},
+    {2, 1, 4}, {2, 1, 4}, {2, 1, 4},                                                          // joints
+    {3, 1, 4}, {3, 1, 4}, {3, 1, 4}, {3, 1, 4}, {3, 1, 1}, {3, 1, 4}, {3, 1, 4}, {3, 2, 4}, {3, 2, 4}, {3, 4, 4},
+    {3, 2, 4}, {3, 2, 4}, {3, 2, 4}, {3, 1, 4}, {3, 1, 4}, {3, 1, 4},                         // contacts
+    {4, 2, 4}, {4, 1, 4}, {4, 1, 4}, {4, 1, 1}, {4, 1, 4},                                    // world scalars
+    {0, 1, 4}, {3, 1, 4}, {3, 1, 4}, {3, 1, 1}, {3, 1, 1}, {3, 1, 1}, {3, 2, 4}, {3, 2, 4}, {4, 1, 4},  // ContactTOI
+};
+static_assert(kLeafDims[GOI_S_NEW_FIXTURE].bytes == 1 && kLeafDims[GOI_C_POINT_LOCAL].mult == 4 &&
+                  kLeafDims[GOI_J_IMPULSE].mult == 3 && kLeafDims[GOI_T_EVENTS].dim == 4 &&
+                  kLeafDims[GOI_T_EVENTS].bytes == 4 && kLeafDims[GOI_T_SOLVED].bytes == 1,
+              "kLeafDims follows enum GoiLeaf");
+GOI_HD constexpr int leaf_count(int l, int B, int C, int J, int R) {
+    const int d = kLeafDims[l].dim;
+    return (d == 0 ? B : d == 1 ? R : d == 2 ? J : d == 3 ? C : 1) * kLeafDims[l].mult;
+}
+GOI_HD constexpr int leaf_words(int l, int B, int C, int J, int R) {
+    return (leaf_count(l, B, C, J, R) * kLeafDims[l].bytes + 3) / 4;
+}
+// Words per unit of pitch before leaf l, as a closed form (coefficients of B, C, J, R, of the rounded-up quarters of
+// the u8 leaves' counts, and a constant), so that it folds to a constant wherever the dimensions are constants.
+struct PackedCoef {
+    int b, c, j, r, one, ub, uc, uj;
+};
+struct PackedTable {
+    PackedCoef k[GOI_NUM_LEAVES + 1];
+};
+constexpr PackedTable make_packed_table() {
+    PackedTable t{};
+    PackedCoef acc{};
+    for (int l = 0; l < GOI_NUM_LEAVES; ++l) {
+        t.k[l] = acc;
+        const LeafDim d = kLeafDims[l];
+        if (d.bytes == 4) {
+            if (d.dim == 0) acc.b += d.mult;
+            else if (d.dim == 1) acc.r += d.mult;
+            else if (d.dim == 2) acc.j += d.mult;
+            else if (d.dim == 3) acc.c += d.mult;
+            else acc.one += d.mult;
+        } else {  // u8 leaves have mult 1
+            if (d.dim == 0) acc.ub += 1;
+            else if (d.dim == 2) acc.uj += 1;
+            else if (d.dim == 3) acc.uc += 1;
+            else acc.one += (d.mult + 3) / 4;
+        }
+    }
+    t.k[GOI_NUM_LEAVES] = acc;
+    return t;
+}
+constexpr PackedTable kPackedTable = make_packed_table();
+GOI_HD constexpr int packed_word(int l, int B, int C, int J, int R) {
+    const PackedCoef& k = kPackedTable.k[l];
+    return k.b * B + k.c * C + k.j * J + k.r * R + k.one + k.ub * ((B + 3) / 4) + k.uc * ((C + 3) / 4) +
+           k.uj * ((J + 3) / 4);
+}
+constexpr int packed_word_sum(int l, int B, int C, int J, int R) {
+    int k = 0;
+    for (int j = 0; j < l; ++j) k += leaf_words(j, B, C, J, R);
+    return k;
+}
+static_assert(packed_word(GOI_NUM_LEAVES, 5, 40, 3, 4) == packed_word_sum(GOI_NUM_LEAVES, 5, 40, 3, 4) &&
+                  packed_word(GOI_C_TOUCHING, 7, 13, 2, 9) == packed_word_sum(GOI_C_TOUCHING, 7, 13, 2, 9) &&
+                  packed_word(GOI_T_EVENTS, 1, 1, 1, 1) == packed_word_sum(GOI_T_EVENTS, 1, 1, 1, 1),
+              "the closed form sums the leaves' words");
+constexpr bool u8_leaves_have_mult_1() {
+    for (int l = 0; l < GOI_NUM_LEAVES; ++l)
+        if (kLeafDims[l].bytes == 1 && kLeafDims[l].dim != 4 && kLeafDims[l].mult != 1) return false;
+    return true;
+}
+static_assert(u8_leaves_have_mult_1(), "the closed form assumes single-element u8 leaves");
+
+#ifndef GOI_PACKED_STATE
+#define GOI_PACKED_STATE 0  // 1 in the translation unit of the kernels that take packed States only
+#endif
 // One world's State: leaf pointers already offset by the world's index, plus the world's LDS workspace.
 struct World {
     int pitch;
@@ -188,7 +277,13 @@ struct World {
     // base plus one 32-bit product and sum
     template <typename T>
     GOI_D T& at(int leaf, int i) const {
+#if GOI_PACKED_STATE
+        // a packed State: every leaf from leaf 0's base, at its constant packed offset
+        const uint32_t row = (uint32_t)(4 / sizeof(T)) * (uint32_t)packed_word(leaf, B, C, J, R) + (uint32_t)i;
+        return reinterpret_cast<T*>(lv[0])[row * (uint32_t)pitch + (uint32_t)w];
+#else
         return reinterpret_cast<T*>(lv[leaf])[(uint32_t)i * (uint32_t)pitch + (uint32_t)w];
+#endif
     }
     GOI_D float& f(int leaf, int i) const {
         const int c = body_mirror_coef(leaf);  // a constant at every call site
@@ -234,7 +329,7 @@ struct World {
 // and each batch issues all its loads before the first use. A lane whose world lies beyond the batch stays idle.
 struct BlockCopy {
     void* const* lv;   // the State's leaf base pointers
-    int pitch, B, C, S;
+    int pitch, B, C, J, R, S;
     Workspace k;
     int* lds;          // the block's workspace base (world 0, word 0)
     int w, j, r0, stride;
@@ -242,7 +337,12 @@ struct BlockCopy {
 
     template <typename T>
     GOI_D T& at(int leaf, int i) const {
+#if GOI_PACKED_STATE
+        const uint32_t row = (uint32_t)(4 / sizeof(T)) * (uint32_t)packed_word(leaf, B, C, J, R) + (uint32_t)i;
+        return reinterpret_cast<T*>(lv[0])[row * (uint32_t)pitch + (uint32_t)w];
+#else
         return reinterpret_cast<T*>(lv[leaf])[(uint32_t)i * (uint32_t)pitch + (uint32_t)w];
+#endif
     }
     GOI_D int& wi(int off) const { return lds[off * S + j]; }
     GOI_D float& wf(int off) const { return reinterpret_cast<float*>(lds)[off * S + j]; }
@@ -252,7 +352,7 @@ struct BlockCopy {
 GOI_HD BlockCopy block_copy(void* const* lv, int pitch, int n, int B, int C, int J, int R, int S, int* lds, int w0,
                             int lane, int lanes) {
     BlockCopy bc;
-    bc.lv = lv; bc.pitch = pitch; bc.B = B; bc.C = C; bc.S = S;
+    bc.lv = lv; bc.pitch = pitch; bc.B = B; bc.C = C; bc.J = J; bc.R = R; bc.S = S;
     bc.k = Workspace::layout(B, C, J, R);
     bc.lds = lds;
     bc.stride = lanes / S > 0 ? lanes / S : 1;

@@ -23,7 +23,7 @@
 #include <vector>
 
 #include "../../include/goi_b2.h"
-#include "b2_step.hpp"
+#include "b2_launch.hpp"
 
 using namespace goi;
 
@@ -42,96 +42,7 @@ int fail(int code, const std::string& msg) {
         if (e_ != hipSuccess) return fail(GOI_E_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
     } while (0)
 
-constexpr int kBlock = 64;
-
-struct Launch {
-    void* leaf[GOI_NUM_LEAVES];
-    int n, pitch, B, C, R, J;
-    int wpw;  // worlds per wavefront: lanes >= wpw idle, so small batches still spread over every SIMD
-    uint32_t* scratch;  // contact rows then joint rows
-    GoiSettings s;
-    float dt;
-    int n_steps;  // consecutive steps of every world in this launch (>= 1)
-    GoiDebug dbg;
-};
-
-
-// World w on lane `lane` of its block; the block's LDS workspace holds L.wpw lanes.
-__device__ __forceinline__ World make_world(const DModel& m, const Launch& L, int w, int* lds, int lane, int sub,
-                                           int G) {
-    World W;
-    W.pitch = L.pitch;
-    W.B = L.B;
-    W.C = L.C;
-    W.R = L.R;
-    W.J = L.J;
-    W.lv = L.leaf;
-    W.w = w;
-    W.k = Workspace::layout(L.B, L.C, L.J, L.R);
-    W.ws = lds + lane;
-    W.S = L.wpw;
-    W.sub = sub;
-    W.G = G;
-    W.init_masks(m);
-    return W;
-}
-
-// The scratch rows of world w0 + wl of this block (tile = the block's world group): the contact rows' tiles, then
-// the joint rows' tiles, each region gridDim.x tiles long.
-__device__ __forceinline__ Rows contact_rows(const Launch& L, int w0, int wl) {
-    return rows_of(L.scratch, L.C, CF_N, L.wpw, w0 / L.wpw, wl);
-}
-__device__ __forceinline__ Rows joint_rows(const Launch& L, int w0, int wl) {
-    uint32_t* region = L.scratch + (size_t)L.C * CF_N * ((size_t)gridDim.x * L.wpw);
-    return rows_of(region, L.J, JF_N, L.wpw, w0 / L.wpw, wl);
-}
-
 // ---------------------------------------------------------------- kernels
-
-// Lanes and worlds of a block: the block's L.wpw worlds each take G consecutive lanes (its lane group; G is the
-// largest power of two with G * wpw <= 64).
-// Every lane of a group runs the world's sequential code on the same data (same loads, same stores of the same
-// values), so the group's lanes stay together on every branch; `leader` is the group's first lane, which alone
-// reports the world's task counts to coop_run.
-struct LaneMap {
-    int G;        // lanes per world
-    int wl;       // this lane's world in the block
-    int sub;      // this lane's place in its world's group
-    bool valid;   // the lane runs a world (wl < wpw and w0 + wl < n)
-    bool leader;  // valid and sub == 0
-};
-__device__ __forceinline__ LaneMap lane_map(const Launch& L, int w0, int lane) {
-    int G = kBlock;
-    while (G * L.wpw > kBlock) G >>= 1;
-    LaneMap lm;
-    lm.G = G;
-    lm.wl = lane / G;
-    lm.sub = lane - lm.wl * G;
-    lm.valid = lm.wl < L.wpw && w0 + lm.wl < L.n;  // wpw need not divide 64: lanes past G * wpw stay idle
-    lm.leader = lm.valid && lm.sub == 0;
-    return lm;
-}
-
-// World group of this block. Blocks are dealt to the 8 XCDs round robin (block b on XCD b % 8), and each XCD has its
-// own L2; numbering the groups so that every XCD holds one contiguous range keeps neighbouring worlds, which share
-// 128-byte lines of every State leaf, behind the same L2. A bijection on [0, gridDim.x) for any grid.
-__device__ __forceinline__ int xcd_group() {
-    const int nb = gridDim.x, b = blockIdx.x, x = b & 7, q = nb >> 3, r = nb & 7;
-    return x * q + min(x, r) + (b >> 3);
-}
-
-// The block's cooperative view (Coop) for lanes whose world is W (or lane 0's, for lanes without one).
-__device__ __forceinline__ Coop block_coop(const Launch& L, const World& W, int* lds, int w0) {
-    Coop co;
-    co.base = W;
-    co.lds = lds;
-    co.scan = lds + W.k.words * L.wpw;
-    co.rows = L.scratch;
-    co.w0 = w0;
-    co.lanes = kBlock;
-    co.G = lane_map(L, w0, 0).G;
-    return co;
-}
 
 // Start-of-step FindNewContacts where new_fixture, then Collide (unless start_only). All lanes of the block take
 // part in Collide's manifold evaluations.
@@ -154,75 +65,8 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
     store_mirror_block(bc);
 }
 
-// The whole b2World::Step (step.py:28-47) of each world of the block on its lane group: FindNewContacts where
-// new_fixture, Collide, Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to share the block's
-// manifold and TOI work.
-// At most 256 registers (two waves per SIMD): the second wave hides the latency chains of the first.
-template <bool kMulti>
-__device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
-    extern __shared__ int lds[];
-    sincos_table_load();
-    const int lane = threadIdx.x;
-    const int w0 = xcd_group() * L.wpw;
-    const LaneMap lm = lane_map(L, w0, lane);
-    const bool valid = lm.valid;
-    const World W = make_world(m, L, valid ? w0 + lm.wl : w0, lds, valid ? lm.wl : 0, lm.sub, lm.G);  // used if valid
-    const Coop co = block_coop(L, W, lds, w0);
-    Bodies bd;
-    bd.s = reinterpret_cast<float*>(lds) + W.k.o_body * W.S + (valid ? lm.wl : 0);
-    bd.B = L.B;
-    bd.st = W.S;
-    const Rows CR = contact_rows(L, w0, valid ? lm.wl : 0);
-    const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
-    load_mirror_block(m, bc);
-    // n_steps consecutive steps: the workspace mirror stays in LDS from one to the next (it is the State's current
-    // value; every access to a mirrored leaf inside a step goes through the workspace), so the block's worlds need
-    // neither a store nor a reload between steps, and the block never waits for other blocks' steps.
-    const int n_steps = kMulti ? L.n_steps : 1;  // the single-step instances carry no loop state
-    for (int step = 0; step < n_steps; ++step) {
-        if (step > 0) __syncthreads();  // the worlds' workspace writes of the previous step
-        build_order_block(bc);
-        if (valid) {
-            if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
-            W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
-        }
-        collide_block(m, co, W, valid, lm.leader, L.s);
-        if (valid) {
-            solve_world(m, W, bd, CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
-            clear_toi_trace(W, L.dbg);
-        }
-        if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, lm.leader, co, bc, L.dbg);
-        if (valid) {
-            const float dt = L.dt;
-            if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
-            if (L.s.auto_clear_forces)
-                for (int b = 0; b < W.B; ++b) {
-                    W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
-                    W.f(GOI_B_TORQUE, b) = 0.0f;
-                }
-        }
-    }
-    store_mirror_block(bc);
-}
-
 template <bool kMulti>
 __global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) { step_block<kMulti>(m, L); }
-
-// The same step with the world dimensions and the worlds per wave fixed at compile time (the 4-body rig with 40
-// contact slots, 8 worlds per wave): every workspace offset and loop bound folds into the instructions, which
-// frees the scalar registers the runtime dimensions hold. The results are those of k_step.
-template <int kB, int kC, int kJ, int kR, int kS, bool kMulti, bool kPlain>
-__global__ void __launch_bounds__(kBlock, 2) k_step_fixed(DModel m, Launch L) {
-    L.B = kB; L.C = kC; L.J = kJ; L.R = kR; L.wpw = kS;
-    m.B = kB; m.J = kJ; m.R = kR;
-    if (kPlain) {  // revolute joints only (the v2.4.1 solver), no edge shapes: the other joint and collider code drops out
-        m.rev_only = 1;
-        m.no_edges = 1;
-        L.s.revolute_v24 = 1;
-    }
-    step_block<kMulti>(m, L);
-}
-constexpr int kRigB = 5, kRigC = 40, kRigJ = 3, kRigR = 4, kRigS = 8;
 
 // b2WorldManifold::Initialize (Box2D 2.3.1; the solver's prepare computes the same, contact_solver.py:60-104) of
 // every slot of every world from the bodies' transforms, one thread per (slot, world): normal [C, 2], points
@@ -699,6 +543,19 @@ static int worlds_per_wave(int n, size_t ws_bytes_per_world) {
     return wpw;
 }
 
+// The buffer of a packed State (all leaves at their packed_word offsets from leaf 0, pitch a multiple of 64, every
+// element offset within 32 bits), else null.
+static char* packed_state(const GoiStateView* v) {
+    if (v->pitch <= 0 || v->pitch % 64 != 0) return nullptr;
+    const uint64_t words = (uint64_t)packed_word(GOI_NUM_LEAVES, v->B, v->C, v->J, v->R);
+    if (4u * words * (uint64_t)v->pitch > 0xffffffffull) return nullptr;
+    char* base = static_cast<char*>(v->leaf[0]);
+    for (int l = 0; l < GOI_NUM_LEAVES; ++l)
+        if (static_cast<char*>(v->leaf[l]) != base + 4 * (size_t)packed_word(l, v->B, v->C, v->J, v->R) * v->pitch)
+            return nullptr;
+    return base;
+}
+
 // The dynamic LDS of one block of launch L: the worlds' workspaces (words x wpw ints), then 64 ints of scan space.
 static size_t block_lds_bytes(const Launch& L) {
     const int words = Workspace::layout(L.B, L.C, L.J, L.R).words;
@@ -719,6 +576,7 @@ static void fill_launch(Launch& L, const GoiModel* M, const GoiStateView* v, con
     std::memset(&L.dbg, 0, sizeof(L.dbg));
     L.scratch = nullptr;
     L.wpw = worlds_per_wave(v->n_worlds, workspace_bytes(v->B, v->C, v->J, v->R));
+    L.packed = packed_state(v) != nullptr;
 }
 
 // Words of constraint and task rows a launch over `state` uses: per world C contact rows and J joint rows, in tiles of
@@ -780,21 +638,17 @@ static int launch_step(const GoiModel* M, const GoiStateView* state, const GoiSe
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
     const size_t lds = block_lds_bytes(L);
     const bool rig = L.B == kRigB && L.C == kRigC && L.J == kRigJ && L.R == kRigR && L.wpw == kRigS &&
-                     M->d.B == kRigB && M->d.J == kRigJ && M->d.R == kRigR;
+                     M->d.B == kRigB && M->d.J == kRigJ && M->d.R == kRigR && L.packed;
     const dim3 g(grid), b(kBlock);
     const bool plain = M->d.rev_only && M->d.no_edges && settings->revolute_v24;
-    if (rig && n_steps == 1 && plain)
-        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, false, true>), g, b, lds, st, M->d, L);
-    else if (rig && n_steps == 1)
-        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, false, false>), g, b, lds, st, M->d, L);
-    else if (rig && plain)
-        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, true, true>), g, b, lds, st, M->d, L);
-    else if (rig)
-        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, true, false>), g, b, lds, st, M->d, L);
-    else if (n_steps == 1)
+    if (rig) {
+        const hipError_t e = launch_rig_step(M->d, L, n_steps != 1, plain, g, lds, st);
+        if (e != hipSuccess) return fail(GOI_E_HIP, std::string("launch_rig_step: ") + hipGetErrorString(e));
+    } else if (n_steps == 1) {
         hipLaunchKernelGGL(k_step<false>, g, b, lds, st, M->d, L);
-    else
+    } else {
         hipLaunchKernelGGL(k_step<true>, g, b, lds, st, M->d, L);
+    }
     HIP_TRY(hipGetLastError());
     return GOI_OK;
 }
@@ -875,6 +729,12 @@ int32_t goi_apply_motor_actions(const float* actions, float* motor_speed, float*
                        static_cast<hipStream_t>(hip_stream), actions, motor_speed, max_motor, n_worlds, pitch, joint,
                        speed_gain, torque_gain);
     HIP_TRY(hipGetLastError());
+    return GOI_OK;
+}
+
+int32_t goi_packed_layout(int32_t B, int32_t C, int32_t J, int32_t R, int32_t* words) {
+    if (B < 0 || C < 0 || J < 0 || R < 0 || !words) return fail(GOI_E_ARG, "goi_packed_layout: bad arguments");
+    for (int l = 0; l <= GOI_NUM_LEAVES; ++l) words[l] = packed_word(l, B, C, J, R);
     return GOI_OK;
 }
 

@@ -11,7 +11,9 @@
  * Data layout. A State is the reference pytree (goi_jax/box2d/world.py:70-174) flattened in field order into
  * GOI_NUM_LEAVES leaves (enum GoiLeaf below). Each leaf of per-world inner shape S (e.g. contacts.point_local has
  * S = [C, 2, 2]) is one device array stored worlds-minor: element (inner index i, world w) lives at
- * leaf[i * pitch + w]. Bools are uint8 (0/1), ints int32, floats IEEE binary32.
+ * leaf[i * pitch + w]. Bools are uint8 (0/1), ints int32, floats IEEE binary32. The leaves may live anywhere; a
+ * State whose leaves are the consecutive parts of one buffer (goi_packed_layout) with a pitch that is a multiple of 64
+ * is "packed", and the step addresses every leaf from one base pointer (the fast instance of the 4-body rig needs it).
  *
  * Return codes (capi.cpp style): 0 ok, GOI_E_ARG bad argument, GOI_E_SHAPE capacity/shape mismatch, GOI_E_HIP a HIP
  * runtime error, GOI_E_UNSUPPORTED settings or model the kernels do not cover. goi_last_error() returns a
@@ -37,7 +39,7 @@
 extern "C" {
 #endif
 
-#define GOI_ABI_VERSION 3
+#define GOI_ABI_VERSION 4
 
 #define GOI_OK 0
 #define GOI_E_ARG (-1)
@@ -302,6 +304,14 @@ int32_t goi_apply_motor_actions(const float* actions, float* motor_speed, float*
 /* Correctly rounded float32 sin/cos of n values on the device, as the step computes them (math2d.py:291-310):
  * s[i] = (float)sin((double)x[i]), c[i] = (float)cos((double)x[i]). Device pointers. */
 int32_t goi_sincos(const float* x, float* s, float* c, int32_t n, void* hip_stream);
+
+/* The packed State layout for capacities B, C, J, R: words[l] (l = 0 .. GOI_NUM_LEAVES) = the 4-byte words per unit of
+ * pitch before leaf l, each leaf taking its per-world bytes rounded up to a multiple of 4 (words[0] = 0, words[l + 1]
+ * - words[l] = that rounding for leaf l, words[GOI_NUM_LEAVES] = the whole). A packed State's leaf l starts at byte
+ * 4 * words[l] * pitch of one device buffer, with the pitch a multiple of 64. No counterpart in the reference (whose
+ * State is a pytree of separate arrays): it describes this library's fast layout, for callers that allocate States.
+ * Returns GOI_E_ARG for a negative capacity or a null `words`. */
+int32_t goi_packed_layout(int32_t B, int32_t C, int32_t J, int32_t R, int32_t* words);
 
 /* Thread-local message of the last failed call ("" if none). */
 const char* goi_last_error(void);

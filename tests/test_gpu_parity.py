@@ -109,13 +109,13 @@ def test_config5_large_islands(oracle):
         b2.scenes.apply_actions(ref.joints.motor_speed, ref.joints.max_motor, acts[k])
         b2.scenes.apply_actions(dev.joints.motor_speed, dev.joints.max_motor, torch.from_numpy(acts[k]).cuda())
         if k % 10 == 9:
-            dbg, t = b2.make_debug(n, (B, R, J, C))
+            dbg, t = b2.make_debug(n, (B, R, J, C), pitch=b2.layout.pitch_of(dev))
             b2.step_(m, dev, s, cfg.dt, debug=dbg)
-            d = {key: np.zeros(v.shape, np.int32) for key, v in t.items()}
+            d = {key: np.zeros(v.shape[:-1] + (n,), np.int32) for key, v in t.items()}
             oracle.step_(m, ref, s, cfg.dt, debug=d)
             torch.cuda.synchronize()
             for key in d:
-                assert np.array_equal(d[key], t[key].cpu().numpy()), (k + 1, key)
+                assert np.array_equal(d[key], t[key][..., :n].cpu().numpy()), (k + 1, key)
             bad = leaf_mismatches(ref, b2.layout.to_host(dev))
             assert bad == [], f"step {k + 1}: {bad[:4]}"
         else:
@@ -205,13 +205,13 @@ def test_island_debug_outputs(oracle):
     ref = oracle.copy(st)
     B, R, J, C = wd.dims(st)
     for _ in range(40):
-        dbg, t = b2.make_debug(64, (B, R, J, C))
+        dbg, t = b2.make_debug(64, (B, R, J, C), pitch=b2.layout.pitch_of(dev))
         b2.step_(m, dev, s, 1.0 / 60.0, debug=dbg)
-        d = {k: np.zeros(v.shape, np.int32) for k, v in t.items()}
+        d = {k: np.zeros(v.shape[:-1] + (64,), np.int32) for k, v in t.items()}
         oracle.step_(m, ref, s, 1.0 / 60.0, debug=d)
         torch.cuda.synchronize()
         for k in d:
-            assert np.array_equal(d[k], t[k].cpu().numpy()), k
+            assert np.array_equal(d[k], t[k][..., :64].cpu().numpy()), k
 
 
 def _debug_parity(m, st, s, dt, steps, oracle, actions=None):
@@ -226,13 +226,13 @@ def _debug_parity(m, st, s, dt, steps, oracle, actions=None):
         if actions is not None:
             b2.scenes.apply_actions(ref.joints.motor_speed, ref.joints.max_motor, actions[k])
             b2.scenes.apply_actions(dev.joints.motor_speed, dev.joints.max_motor, torch.from_numpy(actions[k]).cuda())
-        dbg, t = b2.make_debug(n, dims)
+        dbg, t = b2.make_debug(n, dims, pitch=b2.layout.pitch_of(dev))
         b2.step_(m, dev, s, dt, debug=dbg)
-        d = {key: np.full(v.shape, -9, np.int32) for key, v in t.items()}
+        d = {key: np.full(v.shape[:-1] + (n,), -9, np.int32) for key, v in t.items()}
         oracle.step_(m, ref, s, dt, debug=d)
         torch.cuda.synchronize()
         for key in d:
-            assert np.array_equal(d[key], t[key].cpu().numpy()), (k + 1, key)
+            assert np.array_equal(d[key], t[key][..., :n].cpu().numpy()), (k + 1, key)
         assert leaf_mismatches(ref, b2.layout.to_host(dev)) == [], k + 1
         traced += int((d["toi_event_slot"] >= 0).sum())
     return traced
@@ -250,6 +250,29 @@ def test_toi_event_traces(oracle):
     s, m, st = plank_over_bumps()
     st = wd.batch(wd.from_leaves([np.asarray(x)[0] for x in wd.leaves(st)]), 8)
     assert _debug_parity(m, st, s, np.float32(1 / 60), 3, oracle) >= 8
+
+
+@pytest.mark.parametrize("n_steps", [1, 4])
+def test_packed_and_unpacked_states_agree(n_steps, monkeypatch):
+    """The 4-body rig on a packed State (one buffer, every leaf at its packed offset: the fixed-dimension kernel of
+    goi_b2_rig.hip) and on the same State with one buffer per leaf (the general kernel) step to identical States, for
+    single steps and for goi_step_n."""
+    monkeypatch.setenv("GOI_WORLDS_PER_WAVE", "8")  # the rig kernel's 8 worlds per wave at this batch size
+    s, m, st, cfg = b2.scenes.make_config(4, 512)
+    rng = np.random.default_rng(3)
+    acts = np.stack([b2.scenes.actions(rng, 512) for _ in range(24)])
+    devs = [b2.layout.to_device(st, "cuda", packed=p) for p in (True, False)]
+    for k in range(0, 24, n_steps):
+        for d in devs:
+            b2.scenes.apply_actions(d.joints.motor_speed, d.joints.max_motor, torch.from_numpy(acts[k]).cuda())
+            if n_steps == 1:
+                b2.step_(m, d, s, cfg.dt)
+            else:
+                b2.step_n_(m, d, s, cfg.dt, n_steps)
+    torch.cuda.synchronize()
+    a, b = (b2.layout.to_host(d) for d in devs)
+    assert leaf_mismatches(a, b) == []
+    assert int(np.asarray(a.toi.events).sum()) > 0  # the steps ran TOI events
 
 
 def test_sincos_correctly_rounded(oracle):

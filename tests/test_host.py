@@ -282,6 +282,20 @@ def test_library_exports_every_declared_symbol():
     assert set(names) <= exported
 
 
+def test_packed_layout_matches_the_library():
+    """The Python allocator's packed State layout (layout.packed_words) is the library's goi_packed_layout, for the rig
+    and for other capacities (u8 leaves rounded up to whole words, scalars, R-only leaves)."""
+    A = abi()
+    L = A.lib()
+    layout = b2.layout
+    for B, R, J, C in ((5, 4, 3, 40), (1, 1, 0, 1), (7, 9, 2, 13), (17, 33, 5, 256), (0, 0, 0, 0)):
+        words = (ctypes.c_int32 * (A.NUM_LEAVES + 1))()
+        assert L.goi_packed_layout(B, C, J, R, words) == A.GOI_OK
+        assert list(words) == layout.packed_words((B, R, J, C)), (B, R, J, C)
+    assert L.goi_packed_layout(-1, 1, 1, 1, words) == A.GOI_E_ARG
+    assert L.goi_packed_layout(1, 1, 1, 1, None) == A.GOI_E_ARG
+
+
 def test_library_is_built_for_gfx950():
     data = Path(abi().LIB_PATH).read_bytes()
     assert b"gfx950" in data
