@@ -164,20 +164,40 @@ struct Group {
     GOI_D int G() const { return g; }
 };
 
+// The partner's value in round d (1, 2, 4, ...) of a lane group's butterfly. Groups are aligned runs of G lanes
+// (G a power of two). Up to G = 16 the exchange is one DPP move inside the lane's row of 16: lanes i and i ^ 1, then
+// i ^ 2 (quad permutes), then the mirror inside 8 lanes (i and 7 - i), then inside 16 (i and 15 - i). After the
+// rounds below d every lane of an aligned run of d lanes holds that run's combination, so any pairing that joins two
+// such runs completes the next level, and every combiner here is commutative and associative (or a total order on
+// its (value, index) pairs). Wider rounds go through the LDS crossbar (ds_bpermute).
+template <int kCtrl>
+GOI_D int dpp_mov(int v) { return __builtin_amdgcn_update_dpp(0, v, kCtrl, 0xf, 0xf, false); }
+GOI_D int lane_partner(int v, int d) {
+    switch (d) {
+        case 1: return dpp_mov<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+        case 2: return dpp_mov<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+        case 4: return dpp_mov<0x141>(v);  // row_half_mirror
+        case 8: return dpp_mov<0x140>(v);  // row_mirror
+        default: return __shfl_xor(v, d, 64);
+    }
+}
+GOI_D float lane_partner(float v, int d) { return __int_as_float(lane_partner(__float_as_int(v), d)); }
+GOI_D unsigned lane_partner(unsigned v, int d) { return (unsigned)lane_partner((int)v, d); }
+
 template <class Grp>
 GOI_D int group_max(const Grp& g, int x) {
-    for (int d = 1; d < g.G(); d <<= 1) x = max(x, __shfl_xor(x, d, 64));
+    for (int d = 1; d < g.G(); d <<= 1) x = max(x, lane_partner(x, d));
     return x;
 }
 template <class Grp>
 GOI_D int group_sum(const Grp& g, int x) {
-    for (int d = 1; d < g.G(); d <<= 1) x += __shfl_xor(x, d, 64);
+    for (int d = 1; d < g.G(); d <<= 1) x += lane_partner(x, d);
     return x;
 }
 template <class Grp>
 GOI_D unsigned long long group_or(const Grp& g, unsigned long long x) {
     for (int d = 1; d < g.G(); d <<= 1) {
-        const unsigned lo = __shfl_xor((unsigned)x, d, 64), hi = __shfl_xor((unsigned)(x >> 32), d, 64);
+        const unsigned lo = lane_partner((unsigned)x, d), hi = lane_partner((unsigned)(x >> 32), d);
         x |= ((unsigned long long)hi << 32) | lo;
     }
     return x;
@@ -195,8 +215,8 @@ GOI_D void group_sync() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 template <class Grp>
 GOI_D void group_argmax(const Grp& g, float& v, int& at) {
     for (int d = 1; d < g.G(); d <<= 1) {
-        const float ov = __shfl_xor(v, d, 64);
-        const int oi = __shfl_xor(at, d, 64);
+        const float ov = lane_partner(v, d);
+        const int oi = lane_partner(at, d);
         if (ov > v || (ov == v && oi < at)) {
             v = ov;
             at = oi;
@@ -206,8 +226,8 @@ GOI_D void group_argmax(const Grp& g, float& v, int& at) {
 template <class Grp>
 GOI_D void group_argmin(const Grp& g, float& v, int& at) {
     for (int d = 1; d < g.G(); d <<= 1) {
-        const float ov = __shfl_xor(v, d, 64);
-        const int oi = __shfl_xor(at, d, 64);
+        const float ov = lane_partner(v, d);
+        const int oi = lane_partner(at, d);
         if (ov < v || (ov == v && oi < at)) {
             v = ov;
             at = oi;
@@ -217,7 +237,7 @@ GOI_D void group_argmin(const Grp& g, float& v, int& at) {
 template <class Grp>
 GOI_D bool group_any(const Grp& g, bool p) {
     int x = p ? 1 : 0;
-    for (int d = 1; d < g.G(); d <<= 1) x |= __shfl_xor(x, d, 64);
+    for (int d = 1; d < g.G(); d <<= 1) x |= lane_partner(x, d);
     return x != 0;
 }
 

@@ -314,8 +314,8 @@ GOI_D bool toi_search_pick(const World& W, const GoiSettings& s, int& min_slot, 
         }
     }
     for (int d = 1; d < W.G; d <<= 1) {
-        const float oa = __shfl_xor(best_alpha, d, 64);
-        const int oi = __shfl_xor(at, d, 64);
+        const float oa = lane_partner(best_alpha, d);
+        const int oi = lane_partner(at, d);
         const bool later = oi > at;
         if (oi >= 0 && (oa < best_alpha || (oa == best_alpha && (at < 0 || (s.toi_tie_oldest ? later : !later))))) {
             best_alpha = oa;
