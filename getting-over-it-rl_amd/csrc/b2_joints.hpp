@@ -327,6 +327,84 @@ GOI_D void jn_solve_velocity(const Bodies& bd, const Rows& R, int i, bool v24, b
     bd.set_v(ib, vB, wB);
 }
 
+// A revolute joint's velocity-solve fields for the v2.4.1 solver (revolute24.patch:166-240), loaded in one batch.
+// A revolute-only model's joint passes load joint i + 1's row while joint i is solved (rev_velocity_sweep); the
+// operations are those of jn_solve_velocity's v2.4.1 revolute branch.
+struct RevVRow {
+    int ia, ib;
+    bool emotor, elimit;
+    float mA, mB, iA, iB, k11, k12, k21, k22, i0, i1, i3, i4, mi, maximp, mspeed, mmass, angle, inv_dt, lower, upper;
+    V2 rA, rB;
+};
+GOI_D RevVRow load_rev_vrow(const Rows& R, int i) {
+    RevVRow r;
+    r.ia = R.geti(i, JF_IA); r.ib = R.geti(i, JF_IB);
+    r.emotor = R.geti(i, JF_EMOTOR) != 0; r.elimit = R.geti(i, JF_ELIMIT) != 0;
+    r.mA = R.getf(i, JF_MA); r.mB = R.getf(i, JF_MB); r.iA = R.getf(i, JF_IIA); r.iB = R.getf(i, JF_IIB);
+    r.k11 = R.getf(i, JF_EXX); r.k21 = R.getf(i, JF_EXX + 1); r.k12 = R.getf(i, JF_EYX); r.k22 = R.getf(i, JF_EYX + 1);
+    r.i0 = R.getf(i, JF_IMP0); r.i1 = R.getf(i, JF_IMP1); r.i3 = R.getf(i, JF_IMP3); r.i4 = R.getf(i, JF_IMP4);
+    r.mi = R.getf(i, JF_MIMP);
+    r.maximp = R.getf(i, JF_MAXIMP); r.mspeed = R.getf(i, JF_MSPEED); r.mmass = R.getf(i, JF_MMASS);
+    r.rA = R.get2(i, JF_RA); r.rB = R.get2(i, JF_RB);
+    r.angle = R.getf(i, JF_ANGLE); r.inv_dt = R.getf(i, JF_INVDT);
+    r.lower = R.getf(i, JF_LOWER); r.upper = R.getf(i, JF_UPPER);
+    return r;
+}
+GOI_D void solve_rev_vrow(const Bodies& bd, RevVRow& r) {
+    V2 vA = bd.v(r.ia), vB = bd.v(r.ib);
+    float wA = bd.w(r.ia), wB = bd.w(r.ib);
+    const float mA = r.mA, mB = r.mB, iA = r.iA, iB = r.iB;
+    const bool fixed = (iA + iB) == 0.0f;
+    if (r.emotor && !fixed) {
+        float impulse = -r.mmass * ((wB - wA) - r.mspeed);
+        const float old = r.mi;
+        r.mi = bclamp(r.mi + impulse, -r.maximp, r.maximp);
+        impulse = r.mi - old;
+        wA = wA - iA * impulse;
+        wB = wB + iB * impulse;
+    }
+    if (r.elimit && !fixed) {
+        float C = r.angle - r.lower;
+        float impulse = -r.mmass * ((wB - wA) + bmax(C, 0.0f) * r.inv_dt);
+        float old = r.i3;
+        r.i3 = bmax(r.i3 + impulse, 0.0f);
+        impulse = r.i3 - old;
+        wA = wA - iA * impulse;
+        wB = wB + iB * impulse;
+        C = r.upper - r.angle;
+        impulse = -r.mmass * ((wA - wB) + bmax(C, 0.0f) * r.inv_dt);
+        old = r.i4;
+        r.i4 = bmax(r.i4 + impulse, 0.0f);
+        impulse = r.i4 - old;
+        wA = wA + iA * impulse;
+        wB = wB - iB * impulse;
+    }
+    const V2 p = solve22(r.k11, r.k12, r.k21, r.k22, -rel_vel(vB, wB, r.rB, vA, wA, r.rA));
+    r.i0 = r.i0 + p.x;
+    r.i1 = r.i1 + p.y;
+    vA = vA - mA * p; wA = wA - iA * cross(r.rA, p);
+    vB = vB + mB * p; wB = wB + iB * cross(r.rB, p);
+    bd.set_v(r.ia, vA, wA);
+    bd.set_v(r.ib, vB, wB);
+}
+// the impulses the solve changes (the revolute v2.4.1 branch leaves impulse z as it is)
+GOI_D void store_rev_impulses(const Rows& R, int i, const RevVRow& r) {
+    R.setf(i, JF_IMP0, r.i0); R.setf(i, JF_IMP1, r.i1);
+    R.setf(i, JF_IMP3, r.i3); R.setf(i, JF_IMP4, r.i4); R.setf(i, JF_MIMP, r.mi);
+}
+// joint rows 0..n-1 of a revolute-only model under the v2.4.1 solver, once each, in order
+GOI_D void rev_velocity_sweep(const Bodies& bd, const Rows& R, int n) {
+    if (n <= 0) return;
+    RevVRow r = load_rev_vrow(R, 0);
+    for (int i = 0; i < n; ++i) {
+        RevVRow next;
+        if (i + 1 < n) next = load_rev_vrow(R, i + 1);  // in flight while joint i is solved
+        solve_rev_vrow(bd, r);
+        store_rev_impulses(R, i, r);
+        r = next;
+    }
+}
+
 // the point part of the revolute position solve (joints.py:501-520)
 GOI_D bool rev_point(float mA, float mB, float iA, float iB, V2 la, V2 lb, V2& cA, float& aA, V2& cB, float& aB,
                      float ang_err, const GoiSettings& s) {

@@ -69,7 +69,10 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         for (int i = 0; i < I.nc; ++i) cs_warm_start(bd, CR, i);
     for (int i = 0; i < I.nj; ++i) jn_warm_start(bd, JRw, i, v24, m.rev_only);
     for (int it = 0; it < s.velocity_iterations; ++it) {
-        for (int i = 0; i < I.nj; ++i) jn_solve_velocity(bd, JRw, i, v24, m.rev_only);
+        if (m.rev_only && v24)
+            rev_velocity_sweep(bd, JRw, I.nj);
+        else
+            for (int i = 0; i < I.nj; ++i) jn_solve_velocity(bd, JRw, i, v24, m.rev_only);
         cs_solve_velocity_sweep(bd, CR, I.nc);
     }
     // StoreImpulses (contact_solver.py:293-304), rows split over the lane group
@@ -495,18 +498,21 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     }
     group_sync();
     {
-        // row 0 (the TOI contact, which every island has) stays in registers through the passes; most islands have
-        // no other row
+        // rows 0 (the TOI contact, which every island has) and 1 stay in registers through the passes; rows past them
+        // are read from the row tile in each pass
         VRow r0 = load_vrow(CR, 0);
+        VRow r1 = nc > 1 ? load_vrow(CR, 1) : r0;
         for (int it = 0; it < s.velocity_iterations; ++it) {
             solve_vrow(bd, r0);
-            for (int i = 1; i < nc; ++i) {
+            if (nc > 1) solve_vrow(bd, r1);
+            for (int i = 2; i < nc; ++i) {
                 VRow r = load_vrow(CR, i);
                 solve_vrow(bd, r);
                 store_vimpulses(CR, i, r);
             }
         }
         store_vimpulses(CR, 0, r0);
+        if (nc > 1) store_vimpulses(CR, 1, r1);
     }
     const float h = (1.0f - min_alpha) * dt;
     const float max_t = s.clamps_per_second ? s.max_translation * dt : s.max_translation;
