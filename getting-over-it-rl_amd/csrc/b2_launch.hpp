@@ -4,14 +4,19 @@
 // the 4-body rig's fixed dimensions on packed States.
 #pragma once
 
-#include <hip/hip_runtime.h>
-
 #include "../../include/goi_b2.h"
 #include "b2_step.hpp"
 
 namespace goi {
 
+#ifdef GOI_HOST_BUILD
+constexpr int kBlock = 1;  // the sequential host build runs one lane per block
+#define GOI_DYNAMIC_LDS(name) int* const name = goi_host_lds
+#else
 constexpr int kBlock = 64;
+#define GOI_DYNAMIC_LDS(name) extern __shared__ int name[]
+#endif
+static_assert(kBlock == kCoopLanes, "the cooperative passes span the block");
 
 struct Launch {
     void* leaf[GOI_NUM_LEAVES];
@@ -109,7 +114,7 @@ __device__ __forceinline__ Coop block_coop(const Launch& L, const World& W, int*
 // At most 256 registers (two waves per SIMD): the second wave hides the latency chains of the first.
 template <bool kMulti>
 __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
-    extern __shared__ int lds[];
+    GOI_DYNAMIC_LDS(lds);
     sincos_table_load();
     const int lane = threadIdx.x;
     const int w0 = xcd_group() * L.wpw;
@@ -157,7 +162,8 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
 // The 4-body rig's dimensions (5 bodies, 40 contact slots, 3 joints, 4 fixture rows, 8 worlds per wave) and its
 // fixed-dimension step on a packed State (goi_b2_rig.hip): kernel instance per (n_steps > 1, revolute-only plain
 // model). Returns the launch's HIP error.
-constexpr int kRigB = 5, kRigC = 40, kRigJ = 3, kRigR = 4, kRigS = 8;
+constexpr int kRigB = 5, kRigC = 40, kRigJ = 3, kRigR = 4;
+constexpr int kRigS = kBlock == 64 ? 8 : 1;  // one world a block in the sequential host build
 hipError_t launch_rig_step(const DModel& d, const Launch& L, bool multi, bool plain, dim3 grid, size_t lds,
                            hipStream_t st);
 

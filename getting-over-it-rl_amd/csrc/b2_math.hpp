@@ -6,7 +6,11 @@
 // in the source order of b2Math.h.
 #pragma once
 
+#ifdef GOI_HOST_BUILD
+#include "host_shim.hpp"  // the sequential host build (tests): host definitions of the HIP surface used below
+#else
 #include <hip/hip_runtime.h>
+#endif
 #include <stdint.h>
 
 #include "b2_sincos_table.h"
@@ -70,7 +74,7 @@ GOI_D float fdiv(float a, float b) { return a / b; }
 GOI_D float fsqrt(float a) { return sqrtf(a); }  // IEEE sqrt under -fhip-fp32-correctly-rounded-divide-sqrt
 
 // The library's double sin/cos, out of line: only angles of magnitude 2^20 and above, infinities and NaN take it.
-__device__ __noinline__ double2 sincos_lib(double x) {
+static __device__ __noinline__ double2 sincos_lib(double x) {
     double s, c;
     sincos(x, &s, &c);
     return make_double2(s, c);
@@ -79,12 +83,19 @@ __device__ __noinline__ double2 sincos_lib(double x) {
 // sin(j pi/32), cos(j pi/32) for j = 0..63 (b2_sincos_table.h), and the block's copy in LDS, which every kernel that
 // evaluates rot_of loads first (sincos_table_load).
 __device__ const double kSinCosTable[128] = {GOI_SINCOS_TABLE};
+#ifdef GOI_HOST_BUILD
+inline
+#endif
 __shared__ __align__(16) double g_sincos_lds[128];
 
 // Copies the table into the block's LDS; called by every lane of the block before its first rot_of.
 GOI_D void sincos_table_load() {
+#ifdef GOI_HOST_BUILD
+    for (int i = 0; i < 128; ++i) g_sincos_lds[i] = kSinCosTable[i];  // threads run one after another there
+#else
     for (int i = threadIdx.x; i < 128; i += blockDim.x) g_sincos_lds[i] = kSinCosTable[i];
     __syncthreads();
+#endif
 }
 
 // Correctly rounded float32 sin/cos: (float)sin((double)x), the value the reference computes with a float-float

@@ -93,20 +93,25 @@ struct Coop {
 
 // Called by all lanes of the block together; `my` = this lane's task count: the world's count on the first lane of
 // its group, 0 on every other lane.
+#ifdef GOI_HOST_BUILD
+constexpr int kCoopLanes = 1;  // the block's lanes (one in the sequential host build)
+#else
+constexpr int kCoopLanes = 64;
+#endif
 template <typename F>
 GOI_D void coop_run(const Coop& co, int my, F&& task) {
     const int lane = threadIdx.x;
     int incl = my;
-    for (int d = 1; d < 64; d <<= 1) {
+    for (int d = 1; d < kCoopLanes; d <<= 1) {
         const int v = __shfl_up(incl, d, 64);
         if (lane >= d) incl += v;
     }
-    const int total = __shfl(incl, 63, 64);
+    const int total = __shfl(incl, kCoopLanes - 1, 64);
     if (total == 0) return;
     co.scan[lane] = incl;
     __syncthreads();  // scan entries and the owners' task inputs visible to the whole block
     for (int t = lane; t < total; t += co.lanes) {
-        int lo = 0, hi = 63;  // owner: the first lane whose inclusive count exceeds t
+        int lo = 0, hi = kCoopLanes - 1;  // owner: the first lane whose inclusive count exceeds t
         while (lo < hi) {
             const int mid = (lo + hi) >> 1;
             if (co.scan[mid] > t) hi = mid; else lo = mid + 1;

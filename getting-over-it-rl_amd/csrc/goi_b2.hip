@@ -12,8 +12,6 @@
 // worlds-minor layout; the solver's body arrays sit in LDS ([field][body][lane]), its constraint rows in a
 // per-block HBM scratch tile ([row][field][world]); the static terrain is a BVH over the static fixtures' fat AABBs,
 // shared by every world and read through L2.
-#include <hip/hip_runtime.h>
-
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
@@ -47,7 +45,7 @@ int fail(int code, const std::string& msg) {
 // Start-of-step FindNewContacts where new_fixture, then Collide (unless start_only). All lanes of the block take
 // part in Collide's manifold evaluations.
 __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int start_only) {
-    extern __shared__ int lds[];
+    GOI_DYNAMIC_LDS(lds);
     sincos_table_load();
     const int lane = threadIdx.x;
     const int w0 = xcd_group() * L.wpw;

@@ -1,0 +1,149 @@
+"""The step's own code on the CPU under AddressSanitizer and UBSan: the library's two translation units compiled for
+the host (GOI_HOST_BUILD: blocks and lanes run one after another, every workspace, row tile and State leaf an
+exactly-sized heap block) step the same worlds as the oracle (also sanitized), and every State leaf is compared bit
+for bit after every launch (tests/host_step). An out-of-bounds access or an undefined operation in the step stops
+the run with its source line; a wrong result shows as a mismatch. This is where a device fault is localised: the
+same code, the same scenario, on the CPU.
+
+Covers the general step (one buffer per leaf), the fixed-dimension rig step (packed State), goi_step_n and
+goi_step_n_noalloc, the TOI and edge scenes and the island-heavy configuration. The host build runs one world per
+one-lane block, so the lane-group exchanges it checks are those of groups of one lane; the device's wider groups
+are covered by the GPU parity tests."""
+import importlib
+import os
+import shutil
+import struct
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from util import b2, perturbed, wd
+import scene_defs
+
+_abi = importlib.import_module("getting-over-it-rl_amd.box2d._abi")
+
+HOST = Path(__file__).resolve().parent / "host_step"
+EXE = HOST / "_build" / "host_step"
+
+I32, F32, U8 = np.int32, np.float32, np.uint8
+DESC_DTYPES = dict(fixture_body=I32, shape_type=I32, radius=F32, count=I32, verts=F32, normals=F32, joint_type=I32,
+                   joint_a=I32, joint_b=I32, local_anchor_a=F32, local_anchor_b=F32, local_axis_a=F32,
+                   local_yaxis_a=F32, reference_angle=F32, pair_a=I32, pair_b=I32, fixture_slot=I32, static_fat=F32,
+                   static_friction=F32, static_restitution=F32, body_type=I32, toi_bodies=U8, centroid=F32,
+                   edge_flags=I32)
+
+
+@pytest.fixture(scope="module")
+def host_step():
+    if shutil.which("g++") is None or shutil.which("make") is None:
+        pytest.skip("g++ and make are needed for the host build")
+    r = subprocess.run(["make", "-C", str(HOST), "-j4"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    return EXE
+
+
+def write_scenario(path, model, state, settings, dt, steps, packed, actions=None):
+    """The scenario file host_step reads (its header comment gives the format)."""
+    B, R, J, C = wd.dims(state)
+    n = np.asarray(state.bodies.type).shape[0]
+    with open(path, "wb") as f:
+        f.write(b"GOISCN01")
+        f.write(struct.pack("<4i", model.fixture_body.shape[0], model.joint_type.shape[0], model.pair_a.shape[0],
+                            0 if model.body_type is None else model.body_type.shape[0]))
+        names = [name for name, _ in _abi.GoiModelDesc._fields_[4:]]
+        assert sorted(names) == sorted(DESC_DTYPES)
+        for name in names:
+            a = getattr(model, name)
+            if a is None:
+                f.write(struct.pack("<q", -1))
+                continue
+            x = np.ascontiguousarray(np.asarray(a), dtype=DESC_DTYPES[name]).tobytes()
+            f.write(struct.pack("<q", len(x)) + x)
+        cs = bytes(settings.to_c())
+        f.write(struct.pack("<i", len(cs)) + cs)
+        f.write(np.float32(dt).tobytes())
+        f.write(struct.pack("<9i", steps, n, B, R, J, C, C, int(packed), len(wd.LEAVES)))
+        for (group, name, _, _), leaf in zip(wd.LEAVES, wd.leaves(state)):
+            a = np.ascontiguousarray(np.asarray(leaf))
+            full = (f"{group}.{name}" if group else name).encode()
+            per_world = int(np.prod(a.shape[1:], dtype=np.int64))
+            f.write(struct.pack("<i", len(full)) + full + struct.pack("<iq", a.itemsize, per_world) + a.tobytes())
+        if actions is None:
+            f.write(struct.pack("<i", -1) + np.float32(0).tobytes() * 2)
+        else:
+            f.write(struct.pack("<i", b2.scenes.MOTOR_JOINT) + np.float32(b2.scenes.MOTOR_GAIN).tobytes()
+                    + np.float32(b2.scenes.MOTOR_TORQUE).tobytes())
+            f.write(np.ascontiguousarray(actions, dtype=F32).tobytes())
+
+
+def run(exe, scenario, mode, plant=False):
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:halt_on_error=1",
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1", GOI_HOST_LAUNCH_LOG="1")
+    cmd = [str(exe), str(scenario), mode] + (["plant"] if plant else [])
+    return subprocess.run(cmd, capture_output=True, text=True, env=env, timeout=600)
+
+
+def check(r):
+    assert r.returncode == 0 and "PASS" in r.stdout, (
+        f"exit {r.returncode}\n{r.stdout[-1500:]}\n{r.stderr[-6000:]}")
+
+
+def config_case(k, n, steps, edges="quad", seed=7):
+    s, m, st, cfg = b2.scenes.make_config(k, n, edges=edges)
+    rng = np.random.default_rng(seed)
+    acts = np.stack([b2.scenes.actions(rng, n) for _ in range(steps)])
+    return m, st, s, cfg.dt, acts
+
+
+@pytest.mark.parametrize("packed", [True, False], ids=["packed-rig", "per-leaf-general"])
+@pytest.mark.parametrize("edges", ["quad", "native"])
+def test_config4_sanitized(host_step, tmp_path, packed, edges):
+    """The benchmark rig (config 4) with actions: the packed State takes the fixed-dimension rig kernel, the State
+    with one buffer per leaf the general kernel."""
+    m, st, s, dt, acts = config_case(4, 256, 60, edges)
+    p = tmp_path / "scn.bin"
+    write_scenario(p, m, st, s, dt, 60, packed, acts)
+    r = run(host_step, p, "step")
+    check(r)
+    assert "60 steps" in r.stdout
+    launches = [ln for ln in r.stderr.splitlines() if ln.startswith("launch ") and "k_step" in ln]
+    assert len(launches) == 60
+    assert all(("k_step_fixed" in ln) == packed for ln in launches), launches[:2]
+
+
+@pytest.mark.parametrize("mode", ["step_n:4", "noalloc:5"])
+def test_multi_step_launches_sanitized(host_step, tmp_path, mode):
+    """goi_step_n and goi_step_n_noalloc on the rig's packed State (no actions between the steps of a launch)."""
+    m, st, s, dt, _ = config_case(4, 64, 24)
+    p = tmp_path / "scn.bin"
+    write_scenario(p, m, st, s, dt, 24, True)
+    check(run(host_step, p, mode))
+
+
+def test_config5_sanitized(host_step, tmp_path):
+    """Config 5's box piles: 128 contact slots a world, large islands."""
+    m, st, s, dt, _ = config_case(5, 8, 60)
+    p = tmp_path / "scn.bin"
+    write_scenario(p, m, st, s, dt, 60, False)
+    check(run(host_step, p, "step"))
+
+
+@pytest.mark.parametrize("name", ["pile", "joints", "joints_v23", "misc", "hammer_chain", "multi_event",
+                                  "island_walk", "toi_tie", "edges", "poly_angles"])
+def test_scenes_sanitized(host_step, tmp_path, name):
+    """The test scenes, a few perturbed copies each: every shape pair, joint type, TOI path and edge case."""
+    s, m, st = scene_defs.build_test_scene(name, iterations=(8, 3))
+    p = tmp_path / "scn.bin"
+    write_scenario(p, m, perturbed(st, 16), s, 1.0 / 60.0, 90, False)
+    check(run(host_step, p, "step"))
+
+
+def test_planted_mismatch_is_reported(host_step, tmp_path):
+    """One ulp moved in the oracle's input alone must end the run with a mismatch (the comparison is live)."""
+    m, st, s, dt, acts = config_case(4, 8, 3)
+    p = tmp_path / "scn.bin"
+    write_scenario(p, m, st, s, dt, 3, True, acts)
+    r = run(host_step, p, "step", plant=True)
+    assert r.returncode == 1 and "MISMATCH after step 1" in r.stdout, r.stdout + r.stderr[-3000:]
