@@ -57,6 +57,46 @@ def traffic_from_profiles(kernel, workload):
     return float(m.group(1)) if m else None
 
 
+def toi_tail(host, act, step, dev, steps, first):
+    """Where the step's time goes under TOI: the per-world event histogram of the window's last step, how the worlds of
+    each 64-lane wave (8 consecutive worlds) share their wave's events, and, over `steps` further untimed steps
+    (continuing the same worlds), each step's kernel time beside its largest per-world event count. The kernel ends
+    with its slowest world, whose events run one after another."""
+    import torch
+    ev = np.asarray(host.toi.events).astype(np.int64)
+    waves = ev[: ev.size // 8 * 8].reshape(-1, 8)
+    wmax = waves.max(1)
+    busy = wmax > 0
+    out = {"events_hist_last_step": np.bincount(ev).tolist(),
+           "wave_max_hist_last_step": np.bincount(wmax).tolist(),
+           # over waves with an event: the fraction of the wave's world-event slots (8 x its maximum) left unused
+           "wave_idle_frac": float(1.0 - waves[busy].sum() / (8.0 * wmax[busy].sum())) if busy.any() else 0.0}
+    if steps <= 0:
+        return out
+    # back to back like the timed window (no host synchronisation between the steps); each step's event counts are
+    # reduced on the device after its end event
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    stats = torch.zeros((steps, 2), dtype=torch.int64, device="cuda")
+    for k in range(steps):
+        act(first + k)
+        evs[k][0].record()
+        step()
+        evs[k][1].record()
+        e = dev.toi.events
+        stats[k, 0] = e.max()
+        stats[k, 1] = e.sum()
+    torch.cuda.synchronize()
+    st = stats.cpu().numpy()
+    pairs = [(int(st[k, 0]), int(st[k, 1]), a.elapsed_time(b)) for k, (a, b) in enumerate(evs)]
+    by = {}
+    for m, _, ms in pairs:
+        by.setdefault(m, []).append(ms)
+    out["steps"] = steps
+    out["kernel_ms_by_max_events"] = {str(m): round(float(np.mean(v)), 4) for m, v in sorted(by.items())}
+    out["step_max_events_total_events_ms"] = [[m, s, round(ms, 4)] for m, s, ms in pairs]
+    return out
+
+
 def cpu_baseline(model, state, settings, cfg, acts, apply, min_seconds=10.0, max_passes=20):
     """The oracle on the host cores over the same workload: passes of the same action-driven steps from the same
     initial State, repeated until at least min_seconds of CPU work (a bounded sample, a few tens of seconds)."""
@@ -121,6 +161,8 @@ def main():
                     help="timed steps of the same workload with allow_sleep off (default: --steps; 0 skips)")
     ap.add_argument("--substeps", type=int, default=4,
                     help="also time goi_step_n with this many physics sub-steps per action (0 or 1 skips)")
+    ap.add_argument("--tail-steps", type=int, default=20,
+                    help="untimed steps after the window that pair each step's kernel time with its TOI event counts")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run only a plain device copy of MIB MiB 10 times (the rocprofv3 FETCH_SIZE/WRITE_SIZE "
                          "calibration) and exit")
@@ -181,6 +223,8 @@ def main():
     achieved = n * bpw / (kern_ms / 1e3) / 1e9
     host = b2.layout.to_host(dev)
     finite = bool(np.isfinite(np.asarray(host.bodies.c)).all())
+    tail = toi_tail(host, lambda i: scenes.apply_actions(speed, torque, acts[i % acts.shape[0]]),
+                    lambda: b2.step_(model, dev, settings, cfg.dt), dev, args.tail_steps, args.warmup + args.steps)
 
     sleep_off = None
     off_steps = args.steps if args.sleep_off_steps is None else args.sleep_off_steps
@@ -274,6 +318,7 @@ def main():
         "sleep_off": sleep_off,
         "fused_substeps": fused,
         "toi_events_last_step": int(np.asarray(host.toi.events).sum()),
+        "toi_tail": tail,
         # contacts dropped because a world's table was full, summed over worlds (the reference requires 0)
         "overflow": int(np.asarray(host.overflow).sum()),
         "finite": finite,

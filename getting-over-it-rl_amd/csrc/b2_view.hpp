@@ -344,6 +344,13 @@ struct BlockCopy {
         return reinterpret_cast<T*>(lv[leaf])[(uint32_t)i * (uint32_t)pitch + (uint32_t)w];
 #endif
     }
+    // Streaming reads and writes of State words that the step touches once here (the mirror's load and store, the
+    // TOI reset and store): non-temporal, so the L2 evicts these lines before the constraint rows and contact data
+    // that the step reuses.
+    template <typename T>
+    GOI_D T ld(int leaf, int i) const { return __builtin_nontemporal_load(&at<T>(leaf, i)); }
+    template <typename T>
+    GOI_D void st(int leaf, int i, T v) const { __builtin_nontemporal_store(v, &at<T>(leaf, i)); }
     GOI_D int& wi(int off) const { return lds[off * S + j]; }
     GOI_D float& wf(int off) const { return reinterpret_cast<float*>(lds)[off * S + j]; }
 };
@@ -376,12 +383,12 @@ GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
 #pragma unroll
             for (int u = 0; u < kCopyU; ++u) {
                 const int c = min(c0 + u * bc.stride, bc.C - 1);
-                p[u] = bc.at<int>(GOI_C_PAIR, c);
-                ky[u] = bc.at<int>(GOI_C_KEY, c);
-                fa[u] = bc.at<int>(GOI_C_FA, c);
-                fb[u] = bc.at<int>(GOI_C_FB, c);
-                t[u] = bc.at<uint8_t>(GOI_C_TOUCHING, c);
-                n[u] = bc.at<int>(GOI_C_COUNT, c);
+                p[u] = bc.ld<int>(GOI_C_PAIR, c);
+                ky[u] = bc.ld<int>(GOI_C_KEY, c);
+                fa[u] = bc.ld<int>(GOI_C_FA, c);
+                fb[u] = bc.ld<int>(GOI_C_FB, c);
+                t[u] = bc.ld<uint8_t>(GOI_C_TOUCHING, c);
+                n[u] = bc.ld<int>(GOI_C_COUNT, c);
             }
 #pragma unroll
             for (int u = 0; u < kCopyU; ++u) {
@@ -403,13 +410,13 @@ GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
             for (int l = 0; l < 13; ++l) {
                 const int rows = kBodyMirrorWidth[l] * bc.B;
 #pragma unroll
-                for (int u = 0; u < 2; ++u) v[l][u] = bc.at<float>(kBodyMirrorLeaves[l], min(i0 + u * bc.stride, rows - 1));
+                for (int u = 0; u < 2; ++u) v[l][u] = bc.ld<float>(kBodyMirrorLeaves[l], min(i0 + u * bc.stride, rows - 1));
             }
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int b = min(i0 + u * bc.stride, bc.B - 1);
-                aw[u] = bc.at<uint8_t>(GOI_B_AWAKE, b);
-                ac[u] = bc.at<uint8_t>(GOI_B_ACTIVE, b);
+                aw[u] = bc.ld<uint8_t>(GOI_B_AWAKE, b);
+                ac[u] = bc.ld<uint8_t>(GOI_B_ACTIVE, b);
             }
 #pragma unroll
             for (int l = 0; l < 13; ++l) {
@@ -482,16 +489,16 @@ GOI_D void store_mirror_block(const BlockCopy& bc) {
     if (!bc.on) return;
     const Workspace& k = bc.k;
     for (int c = bc.r0; c < bc.C; c += bc.stride) {
-        bc.at<int>(GOI_C_PAIR, c) = bc.wi(k.o_pair + c);
-        bc.at<int>(GOI_C_KEY, c) = bc.wi(k.o_key + c);
-        bc.at<int>(GOI_C_FA, c) = bc.wi(k.o_fa + c);
-        bc.at<int>(GOI_C_FB, c) = bc.wi(k.o_fb + c);
+        bc.st<int>(GOI_C_PAIR, c, bc.wi(k.o_pair + c));
+        bc.st<int>(GOI_C_KEY, c, bc.wi(k.o_key + c));
+        bc.st<int>(GOI_C_FA, c, bc.wi(k.o_fa + c));
+        bc.st<int>(GOI_C_FB, c, bc.wi(k.o_fb + c));
     }
-    for (int b = bc.r0; b < bc.B; b += bc.stride) bc.at<uint8_t>(GOI_B_AWAKE, b) = (uint8_t)bc.wi(k.o_awake + b);
+    for (int b = bc.r0; b < bc.B; b += bc.stride) bc.st<uint8_t>(GOI_B_AWAKE, b, (uint8_t)bc.wi(k.o_awake + b));
 #pragma unroll
     for (int l = 0; l < kBodyMirrorMutable; ++l) {
         const int rows = kBodyMirrorWidth[l] * bc.B, off = k.o_bm + body_mirror_coef(kBodyMirrorLeaves[l]) * bc.B;
-        for (int i = bc.r0; i < rows; i += bc.stride) bc.at<float>(kBodyMirrorLeaves[l], i) = bc.wf(off + i);
+        for (int i = bc.r0; i < rows; i += bc.stride) bc.st<float>(kBodyMirrorLeaves[l], i, bc.wf(off + i));
     }
 }
 
@@ -509,11 +516,11 @@ GOI_D void reset_toi_block(const BlockCopy& bc) {
             int& mt = bc.wi(k.o_meta + c);
             mt = (mt & ~((1 << kMetaTFlag) | (1 << kMetaTEn) | (15 << kMetaTCount))) | (1 << kMetaTEn);
             bc.wf(k.o_ttoi + c) = 1.0f;
-            bc.at<uint8_t>(GOI_T_SOLVED, c) = 0;
+            bc.st<uint8_t>(GOI_T_SOLVED, c, 0);
         }
         for (int i = bc.r0; i < 2 * bc.C; i += bc.stride) {
-            bc.at<float>(GOI_T_NORMAL_IMPULSE, i) = 0.0f;
-            bc.at<float>(GOI_T_TANGENT_IMPULSE, i) = 0.0f;
+            bc.st<float>(GOI_T_NORMAL_IMPULSE, i, 0.0f);
+            bc.st<float>(GOI_T_TANGENT_IMPULSE, i, 0.0f);
         }
     }
     __syncthreads();
@@ -526,10 +533,10 @@ GOI_D void store_toi_block(const BlockCopy& bc) {
     const Workspace& k = bc.k;
     for (int c = bc.r0; c < bc.C; c += bc.stride) {
         const int t = bc.wi(k.o_meta + c);
-        bc.at<uint8_t>(GOI_T_FLAG, c) = (uint8_t)((t >> kMetaTFlag) & 1);
-        bc.at<uint8_t>(GOI_T_ENABLED, c) = (uint8_t)((t >> kMetaTEn) & 1);
-        bc.at<int>(GOI_T_COUNT, c) = (t >> kMetaTCount) & 15;
-        bc.at<float>(GOI_T_TOI, c) = bc.wf(k.o_ttoi + c);
+        bc.st<uint8_t>(GOI_T_FLAG, c, (uint8_t)((t >> kMetaTFlag) & 1));
+        bc.st<uint8_t>(GOI_T_ENABLED, c, (uint8_t)((t >> kMetaTEn) & 1));
+        bc.st<int>(GOI_T_COUNT, c, (t >> kMetaTCount) & 15);
+        bc.st<float>(GOI_T_TOI, c, bc.wf(k.o_ttoi + c));
     }
 }
 

@@ -65,6 +65,8 @@ template <typename T> inline T __shfl_up(T v, unsigned, int = 64) { return v; }
 template <typename T> inline T __shfl(T v, int, int = 64) { return v; }
 #define __builtin_amdgcn_update_dpp(old, v, ctrl, rm, bm, bc) (v)
 #define __builtin_amdgcn_fence(order, scope) ((void)0)
+#define __builtin_nontemporal_load(p) (*(p))
+#define __builtin_nontemporal_store(v, p) (*(p) = (v))
 
 // the runtime API the library calls, on host memory
 enum hipError_t { hipSuccess = 0, hipErrorMemoryAllocation = 2 };
