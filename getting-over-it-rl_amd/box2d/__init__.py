@@ -12,7 +12,7 @@ step runs hand-written HIP kernels for gfx950 (libgoi_b2.so through the C ABI in
 """
 import numpy as np
 
-from . import debug, io, layout, scenes, shapes, world
+from . import debug, io, layout, record, scenes, shapes, world
 from .settings import Settings
 from .step import collide_, debug_shapes, make_debug, prepare, sincos, step, step_, step_n_, world_manifolds
 from .world import (DYNAMIC, KINEMATIC, PRISMATIC, REVOLUTE, STATIC, WELD, Model, State, WorldDef, compact_model,
@@ -23,4 +23,4 @@ GAME_DT = np.float32(0.008333334)  # Time.fixedDeltaTime (float32 nearest 1/120)
 __all__ = ["Settings", "step", "step_", "step_n_", "collide_", "debug_shapes", "make_debug", "prepare", "sincos", "world_manifolds",
            "Model", "State",
            "WorldDef", "GAME_DT", "STATIC", "KINEMATIC", "DYNAMIC", "REVOLUTE", "PRISMATIC", "WELD", "compact_model",
-           "compact_state", "expand_state", "debug", "io", "layout", "scenes", "shapes", "world"]
+           "compact_state", "expand_state", "debug", "io", "layout", "record", "scenes", "shapes", "world"]
