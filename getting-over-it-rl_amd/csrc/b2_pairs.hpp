@@ -58,10 +58,11 @@ GOI_D bool contact_update(const World& W, int k, const Manifold& mf) {
         W.i32(GOI_C_POINT_ID, 2 * k) = mf.id0;
         W.i32(GOI_C_POINT_ID, 2 * k + 1) = mf.id1;
     }
-    W.f(GOI_C_NORMAL_IMPULSE, 2 * k) = ni0;
-    W.f(GOI_C_NORMAL_IMPULSE, 2 * k + 1) = ni1;
-    W.f(GOI_C_TANGENT_IMPULSE, 2 * k) = ti0;
-    W.f(GOI_C_TANGENT_IMPULSE, 2 * k + 1) = ti1;
+    // written only where the bits change (a contact that stays apart keeps its zeros): no store, no dirty line
+    if (__float_as_uint(ni0) != __float_as_uint(n0)) W.f(GOI_C_NORMAL_IMPULSE, 2 * k) = ni0;
+    if (__float_as_uint(ni1) != __float_as_uint(n1)) W.f(GOI_C_NORMAL_IMPULSE, 2 * k + 1) = ni1;
+    if (__float_as_uint(ti0) != __float_as_uint(t0)) W.f(GOI_C_TANGENT_IMPULSE, 2 * k) = ti0;
+    if (__float_as_uint(ti1) != __float_as_uint(t1)) W.f(GOI_C_TANGENT_IMPULSE, 2 * k + 1) = ti1;
     return flip;
 }
 
@@ -215,6 +216,7 @@ GOI_D void collide_apply(const DModel& m, const World& W, const Rows& R) {
             const int k = W.order(i);
             if ((gone >> (i - q0)) & 1ull) {
                 W.pair(k) = -1;
+                W.mark_slot_changed(k);
                 W.set_touch_count(k, false, 0);
                 continue;
             }
@@ -401,6 +403,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         W.fa(k) = a;
         W.fb(k) = b;
         W.key(k) = base_key + i;
+        W.mark_slot_changed(k);
         W.set_touch_count(k, false, 0);
         W.f(GOI_C_NORMAL_IMPULSE, 2 * k) = 0.0f;
         W.f(GOI_C_NORMAL_IMPULSE, 2 * k + 1) = 0.0f;

@@ -87,6 +87,8 @@ constexpr int kMetaTouch = 12;                 // 1 bit
 constexpr int kMetaCount = 13;                 // 2 bits (manifold point count, 0..2)
 constexpr int kMetaTFlag = 15, kMetaTEn = 16;  // 1 bit each
 constexpr int kMetaTCount = 17;                // 4 bits (at most b2_maxSubSteps + 1 = 9)
+constexpr int kMetaSlotChanged = 21;           // 1 bit: the slot's contact was created or destroyed since the load
+constexpr int kMetaOddLoad = 22;               // 1 bit: the State's touching or count was not 0/1, 0..2 at the load
 struct Workspace {
     int o_pair, o_key, o_fa, o_fb, o_meta, o_ttoi, o_order, o_newp, o_corder, o_cisl;  // [C]
     int o_awake, o_active, o_bisl, o_stack, o_fwork, o_ibuf;                            // [B]
@@ -236,13 +238,19 @@ struct World {
     GOI_D int ba(int c) const { return (meta(c) >> kMetaBodyA) & 63; }
     GOI_D int bb(int c) const { return (meta(c) >> kMetaBodyB) & 63; }
     GOI_D void set_bodies(int c, int a, int b) const { set_meta_bits(c, kMetaBodyA, 12, a | (b << 6)); }
+    // contacts.pair / key / fa / fb of the slot changed (the mirror's store writes back only such slots)
+    GOI_D void mark_slot_changed(int c) const { set_meta_bits(c, kMetaSlotChanged, 1, 1); }
     // contacts.touching and contacts.count, read from the workspace and written through to the State
     GOI_D bool touching(int c) const { return (meta(c) >> kMetaTouch) & 1; }
     GOI_D int ccount(int c) const { return (meta(c) >> kMetaCount) & 3; }
     GOI_D void set_touch_count(int c, bool t, int n) const {
+        // the State holds what the workspace held (both loaded together, every change made here): write only changes
+        const int was = meta(c);
+        const bool odd = (was >> kMetaOddLoad) & 1;
         set_meta_bits(c, kMetaTouch, 3, (t ? 1 : 0) | (n << 1));
-        u8(GOI_C_TOUCHING, c) = t ? 1 : 0;
-        i32(GOI_C_COUNT, c) = n;
+        set_meta_bits(c, kMetaOddLoad, 1, 0);
+        if (odd || ((was >> kMetaTouch) & 1) != (t ? 1 : 0)) u8(GOI_C_TOUCHING, c) = t ? 1 : 0;
+        if (odd || ((was >> kMetaCount) & 3) != n) i32(GOI_C_COUNT, c) = n;
     }
     GOI_D int& awake(int b) const { return wi(k.o_awake, b); }    // bodies.awake
     GOI_D int& active(int b) const { return wi(k.o_active, b); }  // bodies.active (read-only in a step)
@@ -398,7 +406,9 @@ GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
                     bc.wi(k.o_key + c) = ky[u];
                     bc.wi(k.o_fa + c) = fa[u];
                     bc.wi(k.o_fb + c) = fb[u];
-                    bc.wi(k.o_meta + c) = ((t[u] ? 1 : 0) << kMetaTouch) | ((n[u] & 3) << kMetaCount);
+                    const bool odd = t[u] > 1 || (unsigned)n[u] > 2u;
+                    bc.wi(k.o_meta + c) = ((t[u] ? 1 : 0) << kMetaTouch) | ((n[u] & 3) << kMetaCount) |
+                                          ((odd ? 1 : 0) << kMetaOddLoad);
                 }
             }
         }
@@ -489,6 +499,8 @@ GOI_D void store_mirror_block(const BlockCopy& bc) {
     if (!bc.on) return;
     const Workspace& k = bc.k;
     for (int c = bc.r0; c < bc.C; c += bc.stride) {
+        // a slot whose contact was neither created nor destroyed holds the values the State already has
+        if (!((bc.wi(k.o_meta + c) >> kMetaSlotChanged) & 1)) continue;
         bc.st<int>(GOI_C_PAIR, c, bc.wi(k.o_pair + c));
         bc.st<int>(GOI_C_KEY, c, bc.wi(k.o_key + c));
         bc.st<int>(GOI_C_FA, c, bc.wi(k.o_fa + c));
