@@ -385,18 +385,26 @@ constexpr int kCopyU = 4;  // rows per lane and leaf in one batch
 GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
     const Workspace& k = bc.k;
     if (bc.on) {
+        // pair first; a free slot's other fields are never read in a step (every use is behind pair >= 0) and are
+        // written back only if a contact is created there, so only live slots load them. A free slot starts with
+        // the load-time flag set, so its first touching / count write goes through whatever the State held.
         for (int c0 = bc.r0; c0 < bc.C; c0 += kCopyU * bc.stride) {
             int p[kCopyU], ky[kCopyU], fa[kCopyU], fb[kCopyU], n[kCopyU];
             uint8_t t[kCopyU];
 #pragma unroll
+            for (int u = 0; u < kCopyU; ++u) p[u] = bc.ld<int>(GOI_C_PAIR, min(c0 + u * bc.stride, bc.C - 1));
+#pragma unroll
             for (int u = 0; u < kCopyU; ++u) {
                 const int c = min(c0 + u * bc.stride, bc.C - 1);
-                p[u] = bc.ld<int>(GOI_C_PAIR, c);
-                ky[u] = bc.ld<int>(GOI_C_KEY, c);
-                fa[u] = bc.ld<int>(GOI_C_FA, c);
-                fb[u] = bc.ld<int>(GOI_C_FB, c);
-                t[u] = bc.ld<uint8_t>(GOI_C_TOUCHING, c);
-                n[u] = bc.ld<int>(GOI_C_COUNT, c);
+                ky[u] = fa[u] = fb[u] = n[u] = 0;
+                t[u] = 2;  // a free slot: flagged below
+                if (p[u] >= 0) {
+                    ky[u] = bc.ld<int>(GOI_C_KEY, c);
+                    fa[u] = bc.ld<int>(GOI_C_FA, c);
+                    fb[u] = bc.ld<int>(GOI_C_FB, c);
+                    t[u] = bc.ld<uint8_t>(GOI_C_TOUCHING, c);
+                    n[u] = bc.ld<int>(GOI_C_COUNT, c);
+                }
             }
 #pragma unroll
             for (int u = 0; u < kCopyU; ++u) {
@@ -407,7 +415,8 @@ GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
                     bc.wi(k.o_fa + c) = fa[u];
                     bc.wi(k.o_fb + c) = fb[u];
                     const bool odd = t[u] > 1 || (unsigned)n[u] > 2u;
-                    bc.wi(k.o_meta + c) = ((t[u] ? 1 : 0) << kMetaTouch) | ((n[u] & 3) << kMetaCount) |
+                    const bool touch = p[u] >= 0 && t[u] != 0;
+                    bc.wi(k.o_meta + c) = ((touch ? 1 : 0) << kMetaTouch) | ((n[u] & 3) << kMetaCount) |
                                           ((odd ? 1 : 0) << kMetaOddLoad);
                 }
             }
