@@ -33,14 +33,19 @@ template <class Grp>
 GOI_D float max_separation(const DModel& m, int f1, const Xf& xf1, int f2, const Xf& xf2, int& edge, const Grp& g) {
     const int c1 = m.count[f1], c2 = m.count[f2];
     const Xf xf = mulT(xf2, xf1);
+    // every slot of the padded [F, 8] tables is loaded, so the loads issue together with the counts' instead of
+    // after them; the slots at or past a count are never used
     V2 v2s[kPoly];
 #pragma unroll
-    for (int j = 0; j < kPoly; ++j) v2s[j] = j < c2 ? mvert(m, f2, j) : mk(0.0f, 0.0f);
+    for (int j = 0; j < kPoly; ++j) v2s[j] = mvert(m, f2, j);
     int best = 0;
     float maxsep = -kMaxFloat;
-    for (int i = g.sub(); i < c1; i += g.G()) {
-        const V2 n = mul(xf.q, mnorm(m, f1, i));
-        const V2 v1 = mul(xf, mvert(m, f1, i));
+#pragma unroll
+    for (int i = g.sub(); i < kPoly; i += g.G()) {
+        const V2 ni = mnorm(m, f1, i), vi = mvert(m, f1, i);
+        if (i >= c1) break;
+        const V2 n = mul(xf.q, ni);
+        const V2 v1 = mul(xf, vi);
         float si = kMaxFloat;
 #pragma unroll
         for (int j = 0; j < kPoly; ++j) {
@@ -105,8 +110,11 @@ GOI_D void collide_polygons(const DModel& m, int fa, const Xf& xfa, int fb, cons
     const V2 n1 = mulT(xf2.q, mul(xf1.q, mnorm(m, f1, edge1)));
     int idx = 0;
     float mind = kMaxFloat;
-    for (int i = g.sub(); i < c2; i += g.G()) {
-        const float d = dot(n1, mnorm(m, f2, i));
+#pragma unroll
+    for (int i = g.sub(); i < kPoly; i += g.G()) {
+        const V2 ni = mnorm(m, f2, i);
+        if (i >= c2) break;
+        const float d = dot(n1, ni);
         if (d < mind) {
             mind = d;
             idx = i;
