@@ -518,6 +518,8 @@ static int cu_count() {
 // LDS workspace bytes per world (Workspace::layout) and the block budget it is held to.
 constexpr size_t kStaticLdsBytes = sizeof(g_sincos_lds);      // each block's static LDS: the sin/cos table
 constexpr size_t kMaxLdsBytes = 64 * 1024 - kStaticLdsBytes;   // workspaces + scan space of one block
+constexpr size_t kCuLdsBytes = 160 * 1024;                      // LDS per CU (gfx950)
+constexpr long kBlocksPerCu = 8;                                // k_step's register budget: two waves per SIMD
 static size_t workspace_bytes(int B, int C, int J, int R) {
     return (size_t)Workspace::layout(B, C, J, R).words * sizeof(int);
 }
@@ -535,10 +537,27 @@ static int worlds_per_wave(int n, size_t ws_bytes_per_world) {
     // in the block-cooperative passes, but past the waves a SIMD can hold (k_step's register budget allows two) the
     // launch needs a second round. Measured at 16384 worlds of the 4-body rig, two waves per SIMD: 16 -> 1.32 ms,
     // 8 -> 1.25 (one wave per SIMD: 32 -> 1.56, 16 -> 1.48). Aim for two waves per SIMD (8 per CU).
-    int wpw = kBlock;
-    while (wpw > 1 && (long)n / wpw < 8L * cu_count()) wpw /= 2;
-    while (wpw > 1 && ws_bytes_per_world * wpw + kBlock * sizeof(int) > kMaxLdsBytes) wpw /= 2;
-    return wpw;
+    //
+    // A CU's 160 KB of LDS can hold fewer blocks than that when the worlds' workspaces are large, so among the wave
+    // sizes that fit, take the one with the most worlds resident per CU (blocks per CU x worlds per block), the
+    // smaller on a tie (more lanes per world). The 4-body rig with 40 slots: 8 worlds per wave, 8 blocks per CU. The
+    // rig with 12 boxes and 128 slots: 4 worlds per wave (30.6 KB, 5 blocks per CU: 20 worlds) rather than 8 (61 KB,
+    // 2 blocks: 16 worlds), measured 35% faster at 65536 worlds.
+    int top = kBlock;
+    while (top > 1 && (long)n / top < 8L * cu_count()) top /= 2;
+    int wpw = 0;
+    long best = -1;
+    for (int w = top; w >= 1; w /= 2) {
+        const size_t lds = ws_bytes_per_world * w + kBlock * sizeof(int);
+        if (lds > kMaxLdsBytes) continue;
+        const long blocks = std::min<long>(kBlocksPerCu, (long)(kCuLdsBytes / (lds + kStaticLdsBytes)));
+        const long resident = blocks * w;
+        if (resident >= best) {  // >=: the smaller wave wins a tie
+            best = resident;
+            wpw = w;
+        }
+    }
+    return wpw > 0 ? wpw : 1;
 }
 
 // The buffer of a packed State (all leaves at their packed_word offsets from leaf 0, pitch a multiple of 64, every
