@@ -10,7 +10,7 @@ import sys
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
-SRC = [HERE / "csrc" / "goi_b2.hip", HERE / "csrc" / "goi_b2_rig.hip"]
+SRC = [HERE / "csrc" / "goi_b2.hip", HERE / "csrc" / "goi_b2_rig.hip", HERE / "csrc" / "goi_b2_island.hip"]
 OUT = HERE / "lib" / "libgoi_b2.so"
 
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-shared", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",
@@ -28,7 +28,7 @@ def build(out=OUT, extra=()):
     out = Path(out)
     out.parent.mkdir(parents=True, exist_ok=True)
     tmp = out.with_suffix(".so.tmp")
-    cmd = [hipcc(), *FLAGS, *extra, "-parallel-jobs=2", "-o", str(tmp), *map(str, SRC)]
+    cmd = [hipcc(), *FLAGS, *extra, "-parallel-jobs=3", "-o", str(tmp), *map(str, SRC)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stderr)

@@ -161,10 +161,17 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
 
 // The 4-body rig's dimensions (5 bodies, 40 contact slots, 3 joints, 4 fixture rows, 8 worlds per wave) and its
 // fixed-dimension step on a packed State (goi_b2_rig.hip): kernel instance per (n_steps > 1, revolute-only plain
-// model). Returns the launch's HIP error.
+// model). Returns the launch's HIP error. The fixed-dimension instances need the worlds per wave they were compiled
+// for; worlds_per_wave picks it for these dimensions at full batches.
 constexpr int kRigB = 5, kRigC = 40, kRigJ = 3, kRigR = 4;
 constexpr int kRigS = kBlock == 64 ? 8 : 1;  // one world a block in the sequential host build
 hipError_t launch_rig_step(const DModel& d, const Launch& L, bool multi, bool plain, dim3 grid, size_t lds,
                            hipStream_t st);
+
+// The rig with 12 boxes (17 bodies, 128 contact slots, 3 joints, 16 fixture rows, 4 worlds per wave) and its
+// fixed-dimension step on a packed State with a plain Model (goi_b2_island.hip), per n_steps > 1.
+constexpr int kIslandB = 17, kIslandC = 128, kIslandJ = 3, kIslandR = 16;
+constexpr int kIslandS = kBlock == 64 ? 4 : 1;
+hipError_t launch_island_step(const DModel& d, const Launch& L, bool multi, dim3 grid, size_t lds, hipStream_t st);
 
 }  // namespace goi

@@ -658,9 +658,15 @@ static int launch_step(const GoiModel* M, const GoiStateView* state, const GoiSe
                      M->d.B == kRigB && M->d.J == kRigJ && M->d.R == kRigR && L.packed;
     const dim3 g(grid), b(kBlock);
     const bool plain = M->d.rev_only && M->d.no_edges && settings->revolute_v24;
+    const bool island = L.B == kIslandB && L.C == kIslandC && L.J == kIslandJ && L.R == kIslandR &&
+                        L.wpw == kIslandS && M->d.B == kIslandB && M->d.J == kIslandJ && M->d.R == kIslandR &&
+                        L.packed && plain;
     if (rig) {
         const hipError_t e = launch_rig_step(M->d, L, n_steps != 1, plain, g, lds, st);
         if (e != hipSuccess) return fail(GOI_E_HIP, std::string("launch_rig_step: ") + hipGetErrorString(e));
+    } else if (island) {
+        const hipError_t e = launch_island_step(M->d, L, n_steps != 1, g, lds, st);
+        if (e != hipSuccess) return fail(GOI_E_HIP, std::string("launch_island_step: ") + hipGetErrorString(e));
     } else if (n_steps == 1) {
         hipLaunchKernelGGL(k_step<false>, g, b, lds, st, M->d, L);
     } else {

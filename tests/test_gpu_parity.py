@@ -412,6 +412,18 @@ def test_rig_kernel_parity(oracle, monkeypatch, edges):
     assert int(np.asarray(ref.toi.events).sum()) > 0
 
 
+def test_island_kernel_parity(oracle, monkeypatch):
+    """The step instance compiled for config 5's dimensions (17 bodies, 128 slots, 3 joints, 16 rows, 4 worlds per
+    wavefront, plain Model), which the launch picks for the island workload at full size: 512 worlds, 30 steps with
+    actions, on the thin-quad terrain."""
+    monkeypatch.setenv("GOI_WORLDS_PER_WAVE", "4")
+    s, m, st, cfg = b2.scenes.make_config(5, 512, edges="quad")
+    assert wd.dims(st) == (17, 16, 3, 128)
+    rng = np.random.default_rng(23)
+    ref = _run(m, st, s, cfg.dt, 30, oracle, [b2.scenes.actions(rng, 512) for _ in range(30)], every=5)
+    assert int(np.asarray(ref.overflow).sum()) == 0
+
+
 @pytest.mark.parametrize("wpw", [1, 2, 4, 8, 32, 64])
 def test_worlds_per_wave_variants(oracle, monkeypatch, wpw):
     """The block-cooperative passes (manifolds, TOIs) for other world counts per wavefront than the default (the

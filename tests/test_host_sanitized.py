@@ -5,7 +5,7 @@ for bit after every launch (tests/host_step). An out-of-bounds access or an unde
 the run with its source line; a wrong result shows as a mismatch. This is where a device fault is localised: the
 same code, the same scenario, on the CPU.
 
-Covers the general step (one buffer per leaf), the fixed-dimension rig step (packed State), goi_step_n and
+Covers the general step (one buffer per leaf), the fixed-dimension rig and island steps (packed States), goi_step_n and
 goi_step_n_noalloc, the TOI and edge scenes and the island-heavy configuration. The host build runs one world per
 one-lane block, so the lane-group exchanges it checks are those of groups of one lane; the device's wider groups
 are covered by the GPU parity tests."""
@@ -122,12 +122,17 @@ def test_multi_step_launches_sanitized(host_step, tmp_path, mode):
     check(run(host_step, p, mode))
 
 
-def test_config5_sanitized(host_step, tmp_path):
-    """Config 5's box piles: 128 contact slots a world, large islands."""
+@pytest.mark.parametrize("packed", [True, False], ids=["packed-island", "per-leaf-general"])
+def test_config5_sanitized(host_step, tmp_path, packed):
+    """Config 5's box piles: 128 contact slots a world, large islands. The packed State takes the instance compiled
+    for these dimensions, one buffer per leaf the general kernel."""
     m, st, s, dt, _ = config_case(5, 8, 60)
     p = tmp_path / "scn.bin"
-    write_scenario(p, m, st, s, dt, 60, False)
-    check(run(host_step, p, "step"))
+    write_scenario(p, m, st, s, dt, 60, packed)
+    r = run(host_step, p, "step")
+    check(r)
+    launches = [ln for ln in r.stderr.splitlines() if ln.startswith("launch ") and "k_step" in ln]
+    assert len(launches) == 60 and all(("k_step_fixed<kIsland" in ln) == packed for ln in launches), launches[:2]
 
 
 @pytest.mark.parametrize("name", ["pile", "joints", "joints_v23", "misc", "hammer_chain", "multi_event",
