@@ -517,7 +517,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     const float h = (1.0f - min_alpha) * dt;
     const float max_t = s.clamps_per_second ? s.max_translation * dt : s.max_translation;
     const float max_r = s.clamps_per_second ? s.max_rotation * dt : s.max_rotation;
-    for (int i = 0; i < nb; ++i) {
+    for (int i = W.sub; i < nb; i += W.G) {  // the island's bodies are independent here: one per lane of the group
         const int b = W.ibuf(i);
         V2 v = bd.v(b);
         float w = bd.w(b);
@@ -534,6 +534,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         W.f(GOI_B_W, b) = w;
         sync_transform(W, b);
     }
+    group_sync();
     // b2Island::Report, rows split over the lane group
     for (int i = W.sub; i < nc; i += W.G) {
         const int slot = CR.geti(i, CF_SLOT), cnt = CR.geti(i, CF_COUNT);
@@ -546,12 +547,14 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     group_sync();
     // fixture sync of the island's dynamic bodies and TOI invalidation of their contacts
     unsigned long long moved = 0ull, refat = 0ull;
-    for (int i = 0; i < nb; ++i) {
+    for (int i = W.sub; i < nb; i += W.G) {  // one body per lane of the group, the sets combined after
         const int b = W.ibuf(i);
         if (!W.is_dynamic(b)) continue;
         moved |= 1ull << b;
         refat |= sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
     }
+    moved = group_or(W.grp(), moved);
+    refat = group_or(W.grp(), refat);
     // the slot loops below split over the lane group (slots are independent)
     // FindNewContacts; a slot that received a new contact starts with fresh TOI state. Before it, the workspace's
     // corder array (Solve's island order is no longer needed) takes each live slot's key, and for a free slot a mark
