@@ -22,6 +22,9 @@ What a record does not carry, and what stands in for it:
   - the broad-phase fat AABBs: recomputed from the recorded pose as b2BroadPhase::CreateProxy makes them (the game's
     tree is history-dependent; this only moves when a new contact begins);
   - a joint's collideConnected flag: false (the game's joints);
+  - a body's own address: each recorded body's list links give its neighbours' addresses, so a joint can be
+    attached to every body next to a recorded one; a body whose neighbours are both unrecorded (static) cannot be
+    found, and a joint on it is refused;
   - Unity's Continuous mode per body: bit 0x0080 of b2Body::m_flags, the bit the reference's Box2D patch gives it
     (scripts/patches/box2d-2.3.1-goi.patch: e_continuousFlag).
 No recordings exist to check this against: parity of the decoder is unpinned. The tests pin it against an encoder
@@ -350,28 +353,21 @@ class Maps:
 
 
 def _body_addresses(snap, geo_order):
-    """Native addresses of the bodies, recovered from the recorded list links: for consecutive recorded (non-static)
-    bodies a, b: a.next == b.prev means exactly one (static) body lies between them at that address; otherwise they
-    are neighbours and a.next, b.prev are b's and a's addresses. geo_order: the full body list (GeoBody) in list order,
-    which places the static bodies between the recorded ones. Returns {address: position in geo_order}."""
+    """Native addresses of the bodies, recovered from the recorded list links. geo_order is the full body list
+    (GeoBody) in list order; the recorded (non-static) bodies sit in it at their Rigidbody2D's positions, and the
+    bodies between two recorded ones are static. For consecutive recorded bodies a, b: if they are neighbours in the
+    list, a.next is b's address and b.prev is a's; otherwise a.next is the address of the body right after a and
+    b.prev that of the body right before b. The last recorded body's next and the first one's prev name their
+    neighbours the same way. Returns {address: position in geo_order}."""
     rb_pos = {g.rb: k for k, g in enumerate(geo_order) if g.rb >= 0}
     addr = {}
-    R = snap.bodies
-    pos = [rb_pos.get(b.rb) for b in R]
+    R = [b for b in snap.bodies if b.rb in rb_pos]
     for k, b in enumerate(R):
-        if pos[k] is None:
-            continue
-        if k + 1 < len(R) and pos[k + 1] is not None:
-            nb = R[k + 1]
-            if b.next != nb.prev:
-                addr[nb.prev] = pos[k]
-                addr[b.next] = pos[k + 1]
-            elif b.next:
-                addr[b.next] = pos[k] + 1  # the body between them
-        if k + 1 == len(R) and b.next and pos[k] + 1 < len(geo_order):
-            addr[b.next] = pos[k] + 1
-        if k == 0 and b.prev and pos[k] > 0:
-            addr[b.prev] = pos[k] - 1
+        pk = rb_pos[b.rb]
+        if b.next and pk + 1 < len(geo_order):
+            addr[b.next] = pk + 1
+        if b.prev and pk > 0:
+            addr[b.prev] = pk - 1
     return addr
 
 

@@ -276,6 +276,22 @@ def test_decoded_state_steps_like_the_original(stepped):
     assert events > 0  # the TOI path ran on the decoded States
 
 
+def test_body_addresses_from_list_links():
+    """List [D0, S1, D2, D3, S4] (D recorded with Rigidbody2D indices 0, 2, 3; S static, unrecorded): each recorded
+    body names its neighbours' addresses; D0's own address is known to no recorded neighbour."""
+    A = [0x1000 * (k + 1) for k in range(5)]
+
+    def body(rb, k):
+        raw = bytearray(R.BODY_BYTES)
+        struct.pack_into("<iIi", raw, 0, wd.DYNAMIC, 0x22, -1)
+        struct.pack_into("<qq", raw, 0x60, A[k - 1] if k > 0 else 0, A[k + 1] if k + 1 < 5 else 0)
+        return R.NativeBody(rb, bytes(raw))
+    geo = [R.GeoBody(0, wd.DYNAMIC, []), R.GeoBody(-1, wd.STATIC, []), R.GeoBody(2, wd.DYNAMIC, []),
+           R.GeoBody(3, wd.DYNAMIC, []), R.GeoBody(-1, wd.STATIC, [])]
+    snap = R.NativeSnapshot(None, [body(0, 0), body(2, 2), body(3, 3)], [], [])
+    assert R._body_addresses(snap, geo) == {A[1]: 1, A[2]: 2, A[3]: 3, A[4]: 4}
+
+
 def test_unmapped_objects_are_refused(stepped):
     O, s, model, st, cfg = stepped
     one = _world(st, 2)
