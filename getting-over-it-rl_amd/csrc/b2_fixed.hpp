@@ -14,10 +14,12 @@ namespace {
 // Every workspace offset, loop bound and leaf offset folds into the instructions, which frees the scalar registers
 // the runtime dimensions and the 71 leaf pointers would hold (spilled scalars come back through v_readlane on every
 // use). kPlain: revolute joints only (the v2.4.1 solver) and no edge shapes, so the other joint and collider code
-// drops out. The results are those of k_step.
+// drops out. Launches with debug arrays take k_step, so the debug writes drop out too. The results are those of
+// k_step.
 template <int kB, int kC, int kJ, int kR, int kS, bool kMulti, bool kPlain>
 __global__ void __launch_bounds__(kBlock, 2) k_step_fixed(DModel m, Launch L) {
     L.B = kB; L.C = kC; L.J = kJ; L.R = kR; L.wpw = kS;
+    L.dbg = GoiDebug{};
     m.B = kB; m.J = kJ; m.R = kR;
     if (kPlain) {
         m.rev_only = 1;

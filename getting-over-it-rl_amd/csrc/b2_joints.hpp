@@ -15,14 +15,14 @@ GOI_D void set_jcol(const Rows& R, int i, int f, V3 v) { R.setf(i, f, v.x); R.se
 // InitVelocityConstraints minus the velocity writes (joints.py:61-174): row i for joint jid.
 GOI_D void jn_prepare(const DModel& m, const World& W, const Bodies& bd, const Rows& R, int i, int jid,
                       const GoiSettings& s, float dt, float dt_ratio, bool warm, Rot qA, Rot qB) {
-    const int type = m.rev_only ? (int)GOI_REVOLUTE : m.joint_type[jid];
-    const int ia = m.joint_a[jid], ib = m.joint_b[jid];
+    const int type = m.rev_only ? (int)GOI_REVOLUTE : m.joint[jid].type;
+    const int ia = m.joint[jid].a, ib = m.joint[jid].b;
     const float mA = W.f(GOI_B_INV_MASS, ia), mB = W.f(GOI_B_INV_MASS, ib);
     const float iA = W.f(GOI_B_INV_INERTIA, ia), iB = W.f(GOI_B_INV_INERTIA, ib);
-    const V2 la = m.local_anchor_a[jid] - W.v2(GOI_B_LOCAL_CENTER, ia);
-    const V2 lb = m.local_anchor_b[jid] - W.v2(GOI_B_LOCAL_CENTER, ib);
+    const V2 la = m.joint[jid].anchor_a - W.v2(GOI_B_LOCAL_CENTER, ia);
+    const V2 lb = m.joint[jid].anchor_b - W.v2(GOI_B_LOCAL_CENTER, ib);
     const V2 rA = mul(qA, la), rB = mul(qB, lb);
-    const float ref = m.reference_angle[jid];
+    const float ref = m.joint[jid].reference_angle;
     const bool emotor = W.u8(GOI_J_ENABLE_MOTOR, jid) != 0, elimit = W.u8(GOI_J_ENABLE_LIMIT, jid) != 0;
     const float lower = W.f(GOI_J_LOWER, jid), upper = W.f(GOI_J_UPPER, jid);
     const int state_in = W.i32(GOI_J_LIMIT_STATE, jid);
@@ -35,7 +35,7 @@ GOI_D void jn_prepare(const DModel& m, const World& W, const Bodies& bd, const R
     R.seti(i, JF_EMOTOR, emotor); R.seti(i, JF_ELIMIT, elimit);
     R.setf(i, JF_MA, mA); R.setf(i, JF_MB, mB); R.setf(i, JF_IIA, iA); R.setf(i, JF_IIB, iB);
     R.set2(i, JF_RA, rA); R.set2(i, JF_RB, rB); R.set2(i, JF_LA, la); R.set2(i, JF_LB, lb);
-    R.set2(i, JF_LX, m.local_axis_a[jid]); R.set2(i, JF_LY, m.local_yaxis_a[jid]);
+    R.set2(i, JF_LX, m.joint[jid].axis_a); R.set2(i, JF_LY, m.joint[jid].yaxis_a);
     R.setf(i, JF_REF, ref); R.setf(i, JF_LOWER, lower); R.setf(i, JF_UPPER, upper);
     R.setf(i, JF_MSPEED, W.f(GOI_J_MOTOR_SPEED, jid));
     R.setf(i, JF_MAXIMP, dt * W.f(GOI_J_MAX_MOTOR, jid));
@@ -107,11 +107,11 @@ GOI_D void jn_prepare(const DModel& m, const World& W, const Bodies& bd, const R
         set_jcol(R, i, JF_EXX, ex); set_jcol(R, i, JF_EYX, ey); set_jcol(R, i, JF_EZX, ez);
     } else {  // prismatic
         const V2 d = ((cB - cA) + rB) - rA;
-        const V2 axis = mul(qA, m.local_axis_a[jid]);
+        const V2 axis = mul(qA, m.joint[jid].axis_a);
         const float a1 = cross(d + rA, axis), a2 = cross(rB, axis);
         const float mm = ((mA + mB) + iA * a1 * a1) + iB * a2 * a2;
         mmass = mm > 0.0f ? 1.0f / mm : mm;
-        const V2 perp = mul(qA, m.local_yaxis_a[jid]);
+        const V2 perp = mul(qA, m.joint[jid].yaxis_a);
         const float s1 = cross(d + rA, perp), s2 = cross(rB, perp);
         const float k11 = ((mA + mB) + iA * s1 * s1) + iB * s2 * s2;
         const float k12 = iA * s1 + iB * s2;

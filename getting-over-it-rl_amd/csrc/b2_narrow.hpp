@@ -24,14 +24,14 @@ struct Manifold {
 
 GOI_D int feature_key(int ia, int ib, int ta, int tb) { return ia | (ib << 8) | (ta << 16) | (tb << 24); }
 
-GOI_D V2 mvert(const DModel& m, int f, int i) { return m.verts[f * kPoly + i]; }
-GOI_D V2 mnorm(const DModel& m, int f, int i) { return m.normals[f * kPoly + i]; }
+GOI_D V2 mvert(const DModel& m, int f, int i) { return m.poly[16 * f + i]; }
+GOI_D V2 mnorm(const DModel& m, int f, int i) { return m.poly[16 * f + 8 + i]; }
 
 // b2FindMaxSeparation: (edge of poly1, separation) over poly1's normals against poly2's vertices; poly1's normals
 // split over the lane group
 template <class Grp>
 GOI_D float max_separation(const DModel& m, int f1, const Xf& xf1, int f2, const Xf& xf2, int& edge, const Grp& g) {
-    const int c1 = m.count[f1], c2 = m.count[f2];
+    const int c1 = m.fix[f1].count, c2 = m.fix[f2].count;
     const Xf xf = mulT(xf2, xf1);
     // every slot of the padded [F, 8] tables is loaded, so the loads issue together with the counts' instead of
     // after them; the slots at or past a count are never used
@@ -92,7 +92,7 @@ template <class Grp>
 GOI_D void collide_polygons(const DModel& m, int fa, const Xf& xfa, int fb, const Xf& xfb, float linear_slop,
                             Manifold& out, const Grp& g) {
     out.count = 0;
-    const float total_radius = m.radius[fa] + m.radius[fb];
+    const float total_radius = m.fix[fa].radius + m.fix[fb].radius;
     int edge_a, edge_b;
     const float sep_a = max_separation(m, fa, xfa, fb, xfb, edge_a, g);
     if (sep_a > total_radius) return;
@@ -106,7 +106,7 @@ GOI_D void collide_polygons(const DModel& m, int fa, const Xf& xfa, int fb, cons
     out.mtype = flip ? kFaceB : kFaceA;
 
     // b2FindIncidentEdge
-    const int c2 = m.count[f2];
+    const int c2 = m.fix[f2].count;
     const V2 n1 = mulT(xf2.q, mul(xf1.q, mnorm(m, f1, edge1)));
     int idx = 0;
     float mind = kMaxFloat;
@@ -126,7 +126,7 @@ GOI_D void collide_polygons(const DModel& m, int fa, const Xf& xfa, int fb, cons
     inc0.v = mul(xf2, mvert(m, f2, idx)); inc0.ia = edge1; inc0.ib = idx; inc0.ta = 1; inc0.tb = 0;
     inc1.v = mul(xf2, mvert(m, f2, i2));  inc1.ia = edge1; inc1.ib = i2;  inc1.ta = 1; inc1.tb = 0;
 
-    const int c1 = m.count[f1];
+    const int c1 = m.fix[f1].count;
     const int iv1 = edge1, iv2 = edge1 + 1 < c1 ? edge1 + 1 : 0;
     V2 v11 = mvert(m, f1, iv1), v12 = mvert(m, f1, iv2);
     V2 lt = v12 - v11;
@@ -166,8 +166,8 @@ GOI_D void collide_polygon_circle(const DModel& m, int fa, const Xf& xfa, int fb
                                   const Grp& g) {
     out.count = 0;
     const V2 cl = mulT(xfa, mul(xfb, mvert(m, fb, 0)));
-    const float radius = m.radius[fa] + m.radius[fb];
-    const int n = m.count[fa];
+    const float radius = m.fix[fa].radius + m.fix[fb].radius;
+    const int n = m.fix[fa].count;
     int ni = 0;
     float sep = -kMaxFloat;
     bool apart = false;
@@ -219,7 +219,7 @@ GOI_D void collide_polygon_circle(const DModel& m, int fa, const Xf& xfa, int fb
 GOI_D void collide_circles(const DModel& m, int fa, const Xf& xfa, int fb, const Xf& xfb, Manifold& out) {
     out.count = 0;
     const V2 d = mul(xfb, mvert(m, fb, 0)) - mul(xfa, mvert(m, fa, 0));
-    const float r = m.radius[fa] + m.radius[fb];
+    const float r = m.fix[fa].radius + m.fix[fb].radius;
     if (dot(d, d) > r * r) return;
     out.mtype = kCircles;
     out.count = 1;
@@ -242,8 +242,8 @@ GOI_D void collide_edge_circle(const DModel& m, int fa, const Xf& xfa, int fb, c
     const V2 a = mvert(m, fa, 0), b = mvert(m, fa, 1);
     const V2 e = b - a;
     const float u = dot(e, b - q), v = dot(e, q - a);  // barycentric coordinates
-    const float radius = m.radius[fa] + m.radius[fb];
-    const int flags = m.edge_flags[fa];
+    const float radius = m.fix[fa].radius + m.fix[fb].radius;
+    const int flags = m.fix[fa].edge_flags;
     out.pl0 = mvert(m, fb, 0); out.pl1 = out.pl0;
     out.mtype = kCircles;
     out.ln = mk(0.0f, 0.0f);
@@ -284,9 +284,9 @@ GOI_D void collide_edge_polygon(const DModel& m, int fa, const Xf& xfa, int fb, 
                                 Manifold& out) {
     out.count = 0;
     const Xf xf = mulT(xfa, xfb);
-    const V2 cb = mul(xf, m.centroid[fb]);
+    const V2 cb = mul(xf, m.fix[fb].centroid);
     const V2 v1 = mvert(m, fa, 0), v2 = mvert(m, fa, 1);
-    const int flags = m.edge_flags[fa];
+    const int flags = m.fix[fa].edge_flags;
     const bool has0 = (flags & GOI_EDGE_HAS_V0) != 0, has3 = (flags & GOI_EDGE_HAS_V3) != 0;
     V2 edge1 = v2 - v1;
     normalize(edge1);
@@ -347,7 +347,7 @@ GOI_D void collide_edge_polygon(const DModel& m, int fa, const Xf& xfa, int fb, 
         lower = front ? -n1 : n1; upper = lower;
     }
     const V2 normal = front ? n1 : -n1;
-    const int cnt = m.count[fb];
+    const int cnt = m.fix[fb].count;
     const float radius = 2.0f * s.polygon_radius;
 
     // ComputeEdgeSeparation (the edge axis is always known)
@@ -434,7 +434,7 @@ GOI_D void collide_edge_polygon(const DModel& m, int fa, const Xf& xfa, int fb, 
 template <class Grp>
 GOI_D void evaluate(const DModel& m, int fa, int fb, const Xf& xfa, const Xf& xfb, const GoiSettings& s,
                     Manifold& out, const Grp& g) {
-    const int ta = m.shape_type[fa], tb = m.shape_type[fb];
+    const int ta = m.fix[fa].type, tb = m.fix[fb].type;
     if (ta == GOI_POLYGON && tb == GOI_POLYGON) collide_polygons(m, fa, xfa, fb, xfb, s.linear_slop, out, g);
     else if (ta == GOI_POLYGON) collide_polygon_circle(m, fa, xfa, fb, xfb, out, g);
     else if (!m.no_edges && ta == GOI_EDGE && tb == GOI_POLYGON) collide_edge_polygon(m, fa, xfa, fb, xfb, s, out);

@@ -311,7 +311,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         const float4 q = make_float4(W.f(GOI_F_FAT, 4 * r), W.f(GOI_F_FAT, 4 * r + 1), W.f(GOI_F_FAT, 4 * r + 2),
                                      W.f(GOI_F_FAT, 4 * r + 3));
         W.set_qbox(r, q);
-        if (!((query_rows >> r) & 1ull) || !W.active(m.row_body[r])) continue;
+        if (!((query_rows >> r) & 1ull) || !W.active(m.row[r].body)) continue;
         rows |= 1ull << r;
         U.x = fminf(U.x, q.x); U.y = fminf(U.y, q.y); U.z = fmaxf(U.z, q.z); U.w = fmaxf(U.w, q.w);
     }
@@ -325,7 +325,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         const auto children = [&](int nd) {
             unsigned hit = 0u;
             for (int j = W.sub; j < 8; j += W.G)
-                if (overlap(U, m.wbox[8 * nd + j])) hit |= 1u << j;
+                if (overlap(U, m.wnode[nd].box[j])) hit |= 1u << j;
             return group_or(W.grp(), hit);
         };
         masks[0] = children(0);
@@ -345,7 +345,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
 #pragma unroll
             for (int l = 0; l < kWideDepth; ++l)
                 if (l == level) masks[l] = cm & (cm - 1u);
-            const int ref = m.wref[8 * nd + k];
+            const int ref = m.wnode[nd].ref[k];
             if (ref >= 0) {  // an inner node one level down
                 const unsigned hit = children(ref);
                 ++level;
@@ -359,16 +359,16 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
             const int first = (~ref) >> 4, cnt = (~ref) & 15;
             unsigned hits = 0u;
             for (int j = W.sub; j < cnt; j += W.G)
-                if (overlap(m.leaf_fat[first + j], U) && W.active(m.leaf_info[first + j] & 0xffff)) hits |= 1u << j;
+                if (overlap(m.leaf[first + j].fat, U) && W.active(m.leaf[first + j].info & 0xffff)) hits |= 1u << j;
             hits = group_or(W.grp(), hits);
             for (; hits; hits &= hits - 1u) {
                 const int j = __builtin_ctz(hits);
-                const float4 fj = m.leaf_fat[first + j];
-                const int ij = m.leaf_info[first + j];
+                const float4 fj = m.leaf[first + j].fat;
+                const int ij = m.leaf[first + j].info;
                 for (unsigned long long left = rows; left; left &= left - 1) {
                     const int r = __builtin_ctzll(left);
                     if (!overlap(fj, W.get_qbox(r))) continue;
-                    if (!(m.row_dynamic[r] || (ij >> 16))) continue;
+                    if (!(m.row[r].dynamic || (ij >> 16))) continue;
                     const int p = m.leaf_cand[(size_t)(first + j) * m.R + r];
                     if (p < 0 || slot_has_pair(W, p)) continue;
                     np.add(p);
@@ -398,7 +398,8 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         while (W.pair(k) >= 0) ++k;
         W.order(np.kept - 1 - i) = k;
         const int p = W.newp(i);
-        const int a = m.pair_a[p], b = m.pair_b[p];
+        const int2 ab = m.pair[p];
+        const int a = ab.x, b = ab.y;
         W.pair(k) = p;
         W.fa(k) = a;
         W.fb(k) = b;
@@ -415,7 +416,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         const float ra = restitution_of(m, W, a), rb = restitution_of(m, W, b);
         W.f(GOI_C_RESTITUTION, k) = ra > rb ? ra : rb;                                // b2MixRestitution
         W.f(GOI_C_TANGENT_SPEED, k) = 0.0f;
-        const int ba = m.fixture_body[a], bb = m.fixture_body[b];
+        const int ba = m.fix[a].body, bb = m.fix[b].body;
         W.set_bodies(k, ba, bb);
         W.wake(ba);
         W.wake(bb);
@@ -429,8 +430,8 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
 // b2Shape::ComputeAABB of fixture f under transforms t1 and t2 (a1, a2). The fixture's vertex slots (all kPoly of
 // them: the Model pads every shape) load in one batch with its type, count and radius.
 GOI_D void shape_aabb2(const DModel& m, int f, const Xf& t1, const Xf& t2, float4& a1, float4& a2) {
-    const float r = m.radius[f];
-    const int type = m.shape_type[f], n = m.count[f];
+    const float r = m.fix[f].radius;
+    const int type = m.fix[f].type, n = m.fix[f].count;
     V2 vs[kPoly];
 #pragma unroll
     for (int i = 0; i < kPoly; ++i) vs[i] = mvert(m, f, i);
@@ -462,8 +463,9 @@ GOI_D unsigned long long sync_body_fixtures(const DModel& m, const World& W, int
     unsigned long long moved = 0ull;
     const Xf x2 = W.xf(b);
     for (int r = 0; r < m.R; ++r) {
-        if (m.row_body[r] != b) continue;
-        const int f = m.slot_fixture[r];
+        const MRow row = m.row[r];
+        if (row.body != b) continue;
+        const int f = row.fixture;
         float4 a1, a2;
         shape_aabb2(m, f, x1, x2, a1, a2);
         float lx = bmin(a1.x, a2.x), ly = bmin(a1.y, a2.y);

@@ -91,7 +91,7 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
                 group_sync();
             }
             for (int j = W.J - 1; j >= 0; --j) {
-                const int ja = m.joint_a[j], jb = m.joint_b[j];
+                const int ja = m.joint[j].a, jb = m.joint[j].b;
                 if (ja != b && jb != b) continue;
                 if ((jflag >> j) & 1ull) continue;
                 const int other = ja == b ? jb : ja;
@@ -121,7 +121,7 @@ GOI_D void cs_prepare(const DModel& m, const World& W, const Bodies& bd, const R
     const float mA = W.f(GOI_B_INV_MASS, ia), mB = W.f(GOI_B_INV_MASS, ib);
     const float iA = W.f(GOI_B_INV_INERTIA, ia), iB = W.f(GOI_B_INV_INERTIA, ib);
     const V2 lcA = W.v2(GOI_B_LOCAL_CENTER, ia), lcB = W.v2(GOI_B_LOCAL_CENTER, ib);
-    const float radA = m.radius[fa], radB = m.radius[fb];
+    const float radA = m.fix[fa].radius, radB = m.fix[fb].radius;
     const int mtype = W.i32(GOI_C_MTYPE, slot);
     const int cnt = W.ccount(slot);
     const V2 ln = W.v2(GOI_C_LOCAL_NORMAL, slot), lp = W.v2(GOI_C_LOCAL_POINT, slot);

@@ -58,7 +58,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     }
     for (int i = W.sub; i < I.nj; i += W.G) {
         const int jid = I.jorder(i);
-        const int ia = m.joint_a[jid], ib = m.joint_b[jid];
+        const int ia = m.joint[jid].a, ib = m.joint[jid].b;
         Rot qA, qB;
         qA.c = bd.at(6, ia); qA.s = bd.at(7, ia);
         qB.c = bd.at(6, ib); qB.s = bd.at(7, ib);
@@ -190,7 +190,7 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
         last = group_max(W.grp(), last);
         for (int j = 0; j < W.J; ++j) {
             const int isl = I.joint_island(j);
-            if (isl >= 0 && (m.joint_a[j] == b || m.joint_b[j] == b)) last = max(last, isl);
+            if (isl >= 0 && (m.joint[j].a == b || m.joint[j].b == b)) last = max(last, isl);
         }
         if (last < 0) continue;
         W.awake(b) = !((isl_sleep >> last) & 1ull);
@@ -342,7 +342,7 @@ GOI_D void cs_position_row(const DModel& m, const World& W, const Rows& R, int i
     R.set2(i, CF_LN, mf.ln); R.set2(i, CF_LP, mf.lp);
     R.set2(i, CF_PL0, mf.pl0); R.set2(i, CF_PL1, mf.pl1);
     R.set2(i, CF_LCA, W.v2(GOI_B_LOCAL_CENTER, ia)); R.set2(i, CF_LCB, W.v2(GOI_B_LOCAL_CENTER, ib));
-    R.setf(i, CF_RADA, m.radius[fa]); R.setf(i, CF_RADB, m.radius[fb]);
+    R.setf(i, CF_RADA, m.fix[fa].radius); R.setf(i, CF_RADB, m.fix[fb].radius);
 }
 
 // The debug trace of event `ev` of a world (GoiDebug's toi_* arrays, when given): its slot, alpha and island size,

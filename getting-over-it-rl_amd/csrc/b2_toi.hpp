@@ -97,9 +97,9 @@ struct Proxy {
 GOI_D Proxy proxy_of(const DModel& m, int f) {
     Proxy p;
 #pragma unroll
-    for (int j = 0; j < kPoly; ++j) p.v[j] = m.verts[f * kPoly + j];
-    p.count = m.count[f];
-    p.radius = m.radius[f];
+    for (int j = 0; j < kPoly; ++j) p.v[j] = m.poly[16 * f + j];
+    p.count = m.fix[f].count;
+    p.radius = m.fix[f].radius;
     return p;
 }
 // b2DistanceProxy::GetSupport: first index of the largest dot

@@ -13,49 +13,60 @@ namespace goi {
 // Device copy of the Model plus the static-terrain acceleration structures built by goi_model_create.
 constexpr int kWideDepth = 8;  // levels of the static tree below its root, at most
 
+// The Model's per-fixture, per-joint and per-row data are records, so that the kernel keeps a few base pointers in
+// scalar registers (one per record table) rather than one per field.
+struct MFixture {       // 64 bytes
+    int body, type;
+    float radius;
+    int count;
+    int slot;           // the fixture's State row, -1 for a static fixture
+    float friction, restitution;  // a static fixture's (a row's live in the State)
+    int edge_flags;     // edge ghost flags; 0 when absent
+    float4 fat;         // a static fixture's fat AABB
+    V2 centroid;        // polygon centroid (edge-polygon contacts); zeros when the Model has no edges
+    int pad_[2];
+};
+struct MJoint {         // 48 bytes
+    int type, a, b;
+    float reference_angle;
+    V2 anchor_a, anchor_b, axis_a, yaxis_a;
+};
+struct MRow {           // a non-static fixture row
+    int fixture, body, dynamic, pad_;
+};
+// Static 8-wide tree node: child j has the box box[j] and the reference ref[j], either a child node (>= 0) or a leaf,
+// ~(first << 4 | count), of count (1..8) consecutive entries of DModel::leaf from first; an unused child slot holds an
+// empty box (lx > ux), which overlaps nothing.
+struct MNode {          // 160 bytes
+    float4 box[8];
+    int ref[8];
+};
+struct MLeaf {          // a static fixture in the tree: its fat AABB and its body | (body is dynamic) << 16
+    float4 fat;
+    int info, pad_[3];
+};
+
+static_assert(sizeof(MFixture) == 64 && sizeof(MJoint) == 48 && sizeof(MNode) == 160 && sizeof(MLeaf) == 32,
+              "the Model's records are packed without holes");
+
 struct DModel {
     int F, J, P, B, R;  // R = non-static fixture rows (compact layout)
-    const int* fixture_body;
-    const int* shape_type;
-    const float* radius;
-    const int* count;
-    const V2* verts;    // [F * 8]
-    const V2* normals;  // [F * 8]
-    const int* joint_type;
-    const int* joint_a;
-    const int* joint_b;
-    const V2* local_anchor_a;
-    const V2* local_anchor_b;
-    const V2* local_axis_a;
-    const V2* local_yaxis_a;
-    const float* reference_angle;
-    const int* pair_a;
-    const int* pair_b;
-    const int* fixture_slot;    // [F] State row or -1 (static)
-    const int* slot_fixture;    // [R]
-    const float4* static_fat;   // [F] (rows of static fixtures)
-    const float* static_friction;
-    const float* static_restitution;
-    const int* body_type;       // [B]
-    const V2* centroid;         // [F] polygon centroids (edge-polygon contacts); zeros when the Model has no edges
-    const int* edge_flags;      // [F] edge ghost flags; zeros when absent
-    int any_toi_body;           // Model.toi_bodies has a set entry (or is absent)
-    int rev_only;               // every joint is revolute
-    int no_edges;               // no edge fixture
-    // Static 8-wide tree over the static fixtures' fat AABBs (node 0 = the root): child j of node k has the box
-    // wbox[8k + j] and the reference wref[8k + j], either a child node (>= 0) or a leaf, ~(first << 4 | count), of
-    // count (1..8) consecutive entries of the leaf_* arrays from first; an unused child slot holds an empty box
-    // (lx > ux), which overlaps nothing. Nodes lie at most kWideDepth levels below the root.
-    int n_wnodes;               // 0 without static fixtures
-    const float4* wbox;         // [8 n_wnodes] lx ly ux uy
-    const int* wref;            // [8 n_wnodes]
-    const float4* leaf_fat;     // [n_leaf] fat AABB of each leaf entry (a static fixture)
-    const int* leaf_info;       // [n_leaf] the entry's body | (body is dynamic) << 16
-    const int* leaf_cand;       // [n_leaf * R]: candidate index of (leaf entry i, row r), -1 if none
-    const int* row_dynamic;     // [R] the row's body is dynamic
-    const int* row_body;        // [R] the row's body
-    int n_dd;                   // candidates whose fixtures are both non-static
-    const int4* dd_info;        // [n_dd] ascending: candidate, row_a | row_b << 8, body_a | body_b << 8, 0
+    const MFixture* fix;  // [F]
+    const V2* poly;       // [F * 16]: fixture f's vertices at 16 f + i, its edge normals at 16 f + 8 + i
+    const MJoint* joint;  // [J]
+    const int2* pair;     // [P] the candidate pairs' fixtures
+    const MRow* row;      // [R]
+    const int* body_type; // [B]
+    int any_toi_body;     // Model.toi_bodies has a set entry (or is absent)
+    int rev_only;         // every joint is revolute
+    int no_edges;         // no edge fixture
+    // the static fixtures' 8-wide tree (node 0 = the root); nodes lie at most kWideDepth levels below the root
+    int n_wnodes;         // 0 without static fixtures
+    const MNode* wnode;   // [n_wnodes]
+    const MLeaf* leaf;    // [n_leaf]
+    const int* leaf_cand; // [n_leaf * R]: candidate index of (leaf entry i, row r), -1 if none
+    int n_dd;             // candidates whose fixtures are both non-static
+    const int4* dd_info;  // [n_dd] ascending: candidate, row_a | row_b << 8, body_a | body_b << 8, 0
 };
 
 // Float body leaves mirrored in the workspace for the whole step: the leaf's per-body element count and the
@@ -466,8 +477,8 @@ GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
             for (int u = 0; u < kCopyU; ++u) {
                 const int c = c0 + u * bc.stride, cc = min(c, bc.C - 1);
                 live[u] = c < bc.C && bc.wi(k.o_pair + cc) >= 0;
-                ba[u] = m.fixture_body[live[u] ? bc.wi(k.o_fa + cc) : 0];
-                bb[u] = m.fixture_body[live[u] ? bc.wi(k.o_fb + cc) : 0];
+                ba[u] = m.fix[live[u] ? bc.wi(k.o_fa + cc) : 0].body;
+                bb[u] = m.fix[live[u] ? bc.wi(k.o_fb + cc) : 0].body;
             }
 #pragma unroll
             for (int u = 0; u < kCopyU; ++u)
@@ -563,18 +574,18 @@ GOI_D void store_toi_block(const BlockCopy& bc) {
 
 // Fat AABB of a fixture in the compact layout: the world's own row, or the Model's shared static box.
 GOI_D float4 fat_of(const DModel& m, const World& W, int fixture) {
-    int r = m.fixture_slot[fixture];
-    if (r < 0) return m.static_fat[fixture];
+    const int r = m.fix[fixture].slot;
+    if (r < 0) return m.fix[fixture].fat;
     return make_float4(W.f(GOI_F_FAT, 4 * r), W.f(GOI_F_FAT, 4 * r + 1), W.f(GOI_F_FAT, 4 * r + 2),
                        W.f(GOI_F_FAT, 4 * r + 3));
 }
 GOI_D float friction_of(const DModel& m, const World& W, int fixture) {
-    int r = m.fixture_slot[fixture];
-    return r < 0 ? m.static_friction[fixture] : W.f(GOI_F_FRICTION, r);
+    const int r = m.fix[fixture].slot;
+    return r < 0 ? m.fix[fixture].friction : W.f(GOI_F_FRICTION, r);
 }
 GOI_D float restitution_of(const DModel& m, const World& W, int fixture) {
-    int r = m.fixture_slot[fixture];
-    return r < 0 ? m.static_restitution[fixture] : W.f(GOI_F_RESTITUTION, r);
+    const int r = m.fix[fixture].slot;
+    return r < 0 ? m.fix[fixture].restitution : W.f(GOI_F_RESTITUTION, r);
 }
 
 // b2TestOverlap

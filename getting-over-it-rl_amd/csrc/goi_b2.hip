@@ -82,13 +82,13 @@ __global__ void k_world_manifold(DModel m, Launch L, float* normal, float* point
     const int cnt = at_i(GOI_C_PAIR, c) >= 0 ? at_i(GOI_C_COUNT, c) : 0;
     if (cnt > 0) {
         const int fa = at_i(GOI_C_FA, c), fb = at_i(GOI_C_FB, c);
-        const int ba = m.fixture_body[fa], bb = m.fixture_body[fb];
+        const int ba = m.fix[fa].body, bb = m.fix[fb].body;
         Xf xa, xb;
         xa.p = mk(at_f(GOI_B_XF_P, 2 * ba), at_f(GOI_B_XF_P, 2 * ba + 1));
         xa.q.c = at_f(GOI_B_XF_Q, 2 * ba); xa.q.s = at_f(GOI_B_XF_Q, 2 * ba + 1);
         xb.p = mk(at_f(GOI_B_XF_P, 2 * bb), at_f(GOI_B_XF_P, 2 * bb + 1));
         xb.q.c = at_f(GOI_B_XF_Q, 2 * bb); xb.q.s = at_f(GOI_B_XF_Q, 2 * bb + 1);
-        const float ra = m.radius[fa], rb = m.radius[fb];
+        const float ra = m.fix[fa].radius, rb = m.fix[fb].radius;
         const int mtype = at_i(GOI_C_MTYPE, c);
         const V2 ln = mk(at_f(GOI_C_LOCAL_NORMAL, 2 * c), at_f(GOI_C_LOCAL_NORMAL, 2 * c + 1));
         const V2 lp = mk(at_f(GOI_C_LOCAL_POINT, 2 * c), at_f(GOI_C_LOCAL_POINT, 2 * c + 1));
@@ -222,7 +222,7 @@ int upload(GoiModel* M, const T* host, size_t n, const T*& dev, hipStream_t st) 
     return GOI_OK;
 }
 
-// The static fixtures' 8-wide tree (DModel::wbox / wref): a node splits its entries by three rounds of median
+// The static fixtures' 8-wide tree (DModel::wnode): a node splits its entries by three rounds of median
 // splits on the longer axis of their centroid bounds (a range of at most 8 entries is not split further) into up to
 // 8 children; a child of at most 8 entries is a leaf, a larger one an inner node. Entries end in leaf order.
 struct WideBuild {
@@ -314,6 +314,9 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
             return fail(GOI_E_UNSUPPORTED, "goi_model_create: unknown joint type");
     }
     bool any_edge = false;
+    for (int f = 0; f < F; ++f)
+        if (desc->fixture_slot[f] < 0 && (!desc->static_friction || !desc->static_restitution))
+            return fail(GOI_E_ARG, "goi_model_create: static fixtures need their friction and restitution");
     for (int f = 0; f < F; ++f) {
         const int t = desc->shape_type[f], c = desc->count[f];
         if ((t != GOI_CIRCLE && t != GOI_POLYGON && t != GOI_EDGE) || c < 1 || c > GOI_MAX_POLY)
@@ -377,22 +380,29 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
         return fail(GOI_E_UNSUPPORTED, "goi_model_create: static tree deeper than its traversal allows");
     }
     d.n_wnodes = (int)(tree.box.size() / 8);
-    // per leaf entry: fat box, body, candidate row; per row: dynamic body
+    // per leaf entry: fat box, body, candidate row
     const size_t n_leaf = tree.leaf.size();
-    std::vector<float4> leaf_fat(std::max<size_t>(n_leaf, 1), make_float4(0.f, 0.f, 0.f, 0.f));
-    std::vector<int> leaf_info(std::max<size_t>(n_leaf, 1), 0), leaf_cand(std::max<size_t>(n_leaf * R, 1), -1),
-        row_dyn(std::max(R, 1), 0);
+    std::vector<MLeaf> leaf(std::max<size_t>(n_leaf, 1), MLeaf{});
+    std::vector<int> leaf_cand(std::max<size_t>(n_leaf * R, 1), -1);
     for (size_t i = 0; i < n_leaf; ++i) {
         const int f = tree.leaf[i], b = desc->fixture_body[f];
-        leaf_fat[i] = make_float4(desc->static_fat[4 * f], desc->static_fat[4 * f + 1], desc->static_fat[4 * f + 2],
+        leaf[i].fat = make_float4(desc->static_fat[4 * f], desc->static_fat[4 * f + 1], desc->static_fat[4 * f + 2],
                                   desc->static_fat[4 * f + 3]);
-        leaf_info[i] = b | ((desc->body_type[b] == GOI_DYNAMIC ? 1 : 0) << 16);
+        leaf[i].info = b | ((desc->body_type[b] == GOI_DYNAMIC ? 1 : 0) << 16);
         for (int r = 0; r < R; ++r) leaf_cand[i * R + r] = cand[(size_t)f * R + r];
     }
-    std::vector<int> row_body(std::max(R, 1), 0);
+    std::vector<MNode> wnode(std::max<size_t>(d.n_wnodes, 1), MNode{});
+    for (int k = 0; k < d.n_wnodes; ++k)
+        for (int j = 0; j < 8; ++j) {
+            wnode[k].box[j] = tree.box[8 * k + j];
+            wnode[k].ref[j] = tree.ref[8 * k + j];
+        }
+    // per row: its fixture, body and whether the body is dynamic
+    std::vector<MRow> row(std::max(R, 1), MRow{});
     for (int r = 0; r < R; ++r) {
-        row_body[r] = desc->fixture_body[slot_fixture[r]];
-        row_dyn[r] = desc->body_type[row_body[r]] == GOI_DYNAMIC;
+        row[r].fixture = slot_fixture[r];
+        row[r].body = desc->fixture_body[slot_fixture[r]];
+        row[r].dynamic = desc->body_type[row[r].body] == GOI_DYNAMIC;
     }
     d.n_dd = (int)dd.size();
     int any = desc->toi_bodies ? 0 : 1;
@@ -402,53 +412,63 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     d.rev_only = 1;
     for (int j = 0; j < J; ++j) d.rev_only &= desc->joint_type[j] == GOI_REVOLUTE ? 1 : 0;
     d.no_edges = any_edge ? 0 : 1;
-    int rc = GOI_OK;
-#define UP(field, host, n) \
-    if (rc == GOI_OK) rc = upload(M, host, (size_t)(n), d.field, st)
-    UP(fixture_body, desc->fixture_body, F);
-    UP(shape_type, desc->shape_type, F);
-    UP(radius, desc->radius, F);
-    UP(count, desc->count, F);
-    UP(verts, reinterpret_cast<const V2*>(desc->verts), (size_t)F * kPoly);
-    UP(normals, reinterpret_cast<const V2*>(desc->normals), (size_t)F * kPoly);
-    UP(joint_type, desc->joint_type, J);
-    UP(joint_a, desc->joint_a, J);
-    UP(joint_b, desc->joint_b, J);
-    UP(local_anchor_a, reinterpret_cast<const V2*>(desc->local_anchor_a), J);
-    UP(local_anchor_b, reinterpret_cast<const V2*>(desc->local_anchor_b), J);
-    UP(local_axis_a, reinterpret_cast<const V2*>(desc->local_axis_a), J);
-    UP(local_yaxis_a, reinterpret_cast<const V2*>(desc->local_yaxis_a), J);
-    UP(reference_angle, desc->reference_angle, J);
-    UP(pair_a, desc->pair_a, P);
-    UP(pair_b, desc->pair_b, P);
-    UP(fixture_slot, desc->fixture_slot, F);
-    UP(slot_fixture, slot_fixture.data(), R);
-    UP(static_fat, reinterpret_cast<const float4*>(desc->static_fat), F);
-    UP(static_friction, desc->static_friction, F);
-    UP(static_restitution, desc->static_restitution, F);
-    UP(body_type, desc->body_type, B);
-    // host copies live until the stream synchronises below
-    std::vector<V2> cen(std::max(F, 1), V2{0.0f, 0.0f});
-    std::vector<int> eflags(std::max(F, 1), 0);
+    // per fixture: its scalars, its static fat box and its vertex and normal slots
+    std::vector<MFixture> fix(std::max(F, 1), MFixture{});
+    std::vector<V2> poly((size_t)std::max(F, 1) * 16, V2{0.0f, 0.0f});
     for (int f = 0; f < F; ++f) {
-        if (desc->centroid) cen[f] = V2{desc->centroid[2 * f], desc->centroid[2 * f + 1]};
-        if (desc->edge_flags) eflags[f] = desc->edge_flags[f];
+        MFixture& x = fix[f];
+        x.body = desc->fixture_body[f];
+        x.type = desc->shape_type[f];
+        x.radius = desc->radius[f];
+        x.count = desc->count[f];
+        x.slot = desc->fixture_slot[f];
+        if (x.slot < 0) {  // checked above: present when a static fixture exists
+            x.friction = desc->static_friction[f];
+            x.restitution = desc->static_restitution[f];
+        }
+        x.edge_flags = desc->edge_flags ? desc->edge_flags[f] : 0;
+        x.fat = make_float4(desc->static_fat[4 * f], desc->static_fat[4 * f + 1], desc->static_fat[4 * f + 2],
+                            desc->static_fat[4 * f + 3]);
+        if (desc->centroid) x.centroid = V2{desc->centroid[2 * f], desc->centroid[2 * f + 1]};
+        for (int i = 0; i < kPoly; ++i) {
+            poly[16 * (size_t)f + i] = V2{desc->verts[2 * (kPoly * f + i)], desc->verts[2 * (kPoly * f + i) + 1]};
+            poly[16 * (size_t)f + 8 + i] =
+                V2{desc->normals[2 * (kPoly * f + i)], desc->normals[2 * (kPoly * f + i) + 1]};
+        }
     }
-    UP(centroid, cen.data(), F);
-    UP(edge_flags, eflags.data(), F);
-    UP(wbox, tree.box.data(), tree.box.size());
-    UP(wref, tree.ref.data(), tree.ref.size());
-    UP(leaf_fat, leaf_fat.data(), n_leaf);
-    UP(leaf_info, leaf_info.data(), n_leaf);
-    UP(leaf_cand, leaf_cand.data(), n_leaf * R);
-    UP(row_dynamic, row_dyn.data(), R);
-    UP(row_body, row_body.data(), R);
+    std::vector<MJoint> joint(std::max(J, 1), MJoint{});
+    for (int j = 0; j < J; ++j) {
+        MJoint& x = joint[j];
+        x.type = desc->joint_type[j];
+        x.a = desc->joint_a[j];
+        x.b = desc->joint_b[j];
+        x.reference_angle = desc->reference_angle[j];
+        x.anchor_a = V2{desc->local_anchor_a[2 * j], desc->local_anchor_a[2 * j + 1]};
+        x.anchor_b = V2{desc->local_anchor_b[2 * j], desc->local_anchor_b[2 * j + 1]};
+        x.axis_a = V2{desc->local_axis_a[2 * j], desc->local_axis_a[2 * j + 1]};
+        x.yaxis_a = V2{desc->local_yaxis_a[2 * j], desc->local_yaxis_a[2 * j + 1]};
+    }
+    std::vector<int2> pair(std::max(P, 1), int2{});
+    for (int p = 0; p < P; ++p) pair[p] = make_int2(desc->pair_a[p], desc->pair_b[p]);
     std::vector<int4> dd_info(std::max<size_t>(dd.size(), 1));
     for (size_t i = 0; i < dd.size(); ++i) {
         const int p = dd[i], a = desc->pair_a[p], b = desc->pair_b[p];
         dd_info[i] = make_int4(p, desc->fixture_slot[a] | (desc->fixture_slot[b] << 8),
                                desc->fixture_body[a] | (desc->fixture_body[b] << 8), 0);
     }
+    int rc = GOI_OK;
+    // the host tables above live until the stream synchronises below
+#define UP(field, host, n) \
+    if (rc == GOI_OK) rc = upload(M, host, (size_t)(n), d.field, st)
+    UP(fix, fix.data(), F);
+    UP(poly, poly.data(), (size_t)F * 16);
+    UP(joint, joint.data(), J);
+    UP(pair, pair.data(), P);
+    UP(row, row.data(), R);
+    UP(body_type, desc->body_type, B);
+    UP(wnode, wnode.data(), d.n_wnodes);
+    UP(leaf, leaf.data(), n_leaf);
+    UP(leaf_cand, leaf_cand.data(), n_leaf * R);
     UP(dd_info, dd_info.data(), dd.size());
 #undef UP
     if (rc == GOI_OK) {
@@ -654,13 +674,17 @@ static int launch_step(const GoiModel* M, const GoiStateView* state, const GoiSe
     if (debug) L.dbg = *debug;
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
     const size_t lds = block_lds_bytes(L);
+    // the fixed instances write no debug arrays (it frees the scalar registers their pointers would hold)
+    const GoiDebug& D = L.dbg;
+    const bool dbg = D.body_island || D.contact_island || D.contact_order || D.n_islands || D.toi_event_slot ||
+                     D.toi_event_alpha || D.toi_event_island || D.toi_island_rows;
     const bool rig = L.B == kRigB && L.C == kRigC && L.J == kRigJ && L.R == kRigR && L.wpw == kRigS &&
-                     M->d.B == kRigB && M->d.J == kRigJ && M->d.R == kRigR && L.packed;
+                     M->d.B == kRigB && M->d.J == kRigJ && M->d.R == kRigR && L.packed && !dbg;
     const dim3 g(grid), b(kBlock);
     const bool plain = M->d.rev_only && M->d.no_edges && settings->revolute_v24;
     const bool island = L.B == kIslandB && L.C == kIslandC && L.J == kIslandJ && L.R == kIslandR &&
                         L.wpw == kIslandS && M->d.B == kIslandB && M->d.J == kIslandJ && M->d.R == kIslandR &&
-                        L.packed && plain;
+                        L.packed && plain && !dbg;
     if (rig) {
         const hipError_t e = launch_rig_step(M->d, L, n_steps != 1, plain, g, lds, st);
         if (e != hipSuccess) return fail(GOI_E_HIP, std::string("launch_rig_step: ") + hipGetErrorString(e));

@@ -9,6 +9,7 @@ Covers the general step (one buffer per leaf), the fixed-dimension rig and islan
 goi_step_n_noalloc, the TOI and edge scenes and the island-heavy configuration. The host build runs one world per
 one-lane block, so the lane-group exchanges it checks are those of groups of one lane; the device's wider groups
 are covered by the GPU parity tests."""
+import fcntl
 import importlib
 import os
 import shutil
@@ -39,7 +40,11 @@ DESC_DTYPES = dict(fixture_body=I32, shape_type=I32, radius=F32, count=I32, vert
 def host_step():
     if shutil.which("g++") is None or shutil.which("make") is None:
         pytest.skip("g++ and make are needed for the host build")
-    r = subprocess.run(["make", "-C", str(HOST), "-j4"], capture_output=True, text=True)
+    # one make at a time (parallel test workers share the build folder)
+    EXE.parent.mkdir(parents=True, exist_ok=True)
+    with open(EXE.parent / ".lock", "w") as lock:
+        fcntl.flock(lock, fcntl.LOCK_EX)
+        r = subprocess.run(["make", "-C", str(HOST), "-j4"], capture_output=True, text=True)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
     return EXE
 
