@@ -108,55 +108,115 @@ __device__ __forceinline__ Coop block_coop(const Launch& L, const World& W, int*
     return co;
 }
 
-// The whole b2World::Step (step.py:28-47) of each world of the block on its lane group: FindNewContacts where
-// new_fixture, Collide, Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to share the block's
-// manifold and TOI work.
+// A lane's views of its block: its world's State and workspace, the block's cooperative queues, the solver's body
+// arrays and constraint rows, and the block's State copy.
+struct LaneViews {
+    LaneMap lm;
+    World W;  // used if lm.valid
+    Coop co;
+    Bodies bd;
+    Rows CR;
+    BlockCopy bc;
+};
+__device__ __forceinline__ LaneViews lane_views(const DModel& m, const Launch& L, int* lds, int w0, int lane) {
+    LaneViews v;
+    v.lm = lane_map(L, w0, lane);
+    const bool valid = v.lm.valid;
+    v.W = make_world(m, L, valid ? w0 + v.lm.wl : w0, lds, valid ? v.lm.wl : 0, v.lm.sub, v.lm.G);
+    v.co = block_coop(L, v.W, lds, w0);
+    v.bd.s = reinterpret_cast<float*>(lds) + v.W.k.o_body * v.W.S + (valid ? v.lm.wl : 0);
+    v.bd.B = L.B;
+    v.bd.st = v.W.S;
+    v.CR = contact_rows(L, w0, valid ? v.lm.wl : 0);
+    v.bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
+    return v;
+}
+
+// One b2World::Step (step.py:28-47) of each world of the block on its lane group, on the workspace mirror:
+// FindNewContacts where new_fixture, Collide, Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to
+// share the block's manifold and TOI work.
+__device__ __forceinline__ void step_worlds(const DModel& m, const Launch& L, int w0, const LaneViews& v) {
+    const LaneMap& lm = v.lm;
+    const bool valid = lm.valid;
+    const World& W = v.W;
+    build_order_block(v.bc);
+    if (valid) {
+        if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
+        W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
+    }
+    collide_block(m, v.co, W, valid, lm.leader, L.s);
+    if (valid) {
+        solve_world(m, W, v.bd, v.CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
+        clear_toi_trace(W, L.dbg);
+    }
+    if (L.s.continuous_physics) solve_toi_world(m, W, v.bd, v.CR, L.s, L.dt, valid, lm.leader, v.co, v.bc, L.dbg);
+    if (valid) {
+        const float dt = L.dt;
+        if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
+        if (L.s.auto_clear_forces)
+            for (int b = 0; b < W.B; ++b) {
+                W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
+                W.f(GOI_B_TORQUE, b) = 0.0f;
+            }
+    }
+}
+
+// The block's worlds: the State into the workspace mirror, one step (kMulti false) or L.n_steps steps, the mirror
+// back. Across the steps of a multi-step launch the mirror stays in LDS (it is the State's current value; every access
+// to a mirrored leaf inside a step goes through the workspace), so the worlds need neither a store nor a reload between
+// steps, and the block never waits for other blocks' steps. Each of those steps sets up its lane's views from a lane
+// index the compiler cannot see through, so no per-lane State or row address of one step is kept live (spilled to
+// scratch) into the next.
 // At most 256 registers (two waves per SIMD): the second wave hides the latency chains of the first.
 template <bool kMulti>
 __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     GOI_DYNAMIC_LDS(lds);
     sincos_table_load();
-    const int lane = threadIdx.x;
     const int w0 = xcd_group() * L.wpw;
-    const LaneMap lm = lane_map(L, w0, lane);
-    const bool valid = lm.valid;
-    const World W = make_world(m, L, valid ? w0 + lm.wl : w0, lds, valid ? lm.wl : 0, lm.sub, lm.G);  // used if valid
-    const Coop co = block_coop(L, W, lds, w0);
-    Bodies bd;
-    bd.s = reinterpret_cast<float*>(lds) + W.k.o_body * W.S + (valid ? lm.wl : 0);
-    bd.B = L.B;
-    bd.st = W.S;
-    const Rows CR = contact_rows(L, w0, valid ? lm.wl : 0);
-    const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
-    load_mirror_block(m, bc);
-    // n_steps consecutive steps: the workspace mirror stays in LDS from one to the next (it is the State's current
-    // value; every access to a mirrored leaf inside a step goes through the workspace), so the block's worlds need
-    // neither a store nor a reload between steps, and the block never waits for other blocks' steps.
-    const int n_steps = kMulti ? L.n_steps : 1;  // the single-step instances carry no loop state
-    for (int step = 0; step < n_steps; ++step) {
-        if (step > 0) __syncthreads();  // the worlds' workspace writes of the previous step
-        build_order_block(bc);
-        if (valid) {
-            if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
-            W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
+    if constexpr (!kMulti) {
+        const int lane = threadIdx.x;
+        const LaneMap lm = lane_map(L, w0, lane);
+        const bool valid = lm.valid;
+        const World W = make_world(m, L, valid ? w0 + lm.wl : w0, lds, valid ? lm.wl : 0, lm.sub, lm.G);  // if valid
+        const Coop co = block_coop(L, W, lds, w0);
+        Bodies bd;
+        bd.s = reinterpret_cast<float*>(lds) + W.k.o_body * W.S + (valid ? lm.wl : 0);
+        bd.B = L.B;
+        bd.st = W.S;
+        const Rows CR = contact_rows(L, w0, valid ? lm.wl : 0);
+        const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
+        load_mirror_block(m, bc);
+        for (int step = 0; step < 1; ++step) {  // one trip: without the loop the code generated differs, 2% slower
+            build_order_block(bc);
+            if (valid) {
+                if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
+                W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
+            }
+            collide_block(m, co, W, valid, lm.leader, L.s);
+            if (valid) {
+                solve_world(m, W, bd, CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
+                clear_toi_trace(W, L.dbg);
+            }
+            if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, lm.leader, co, bc, L.dbg);
+            if (valid) {
+                const float dt = L.dt;
+                if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
+                if (L.s.auto_clear_forces)
+                    for (int b = 0; b < W.B; ++b) {
+                        W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
+                        W.f(GOI_B_TORQUE, b) = 0.0f;
+                    }
+            }
         }
-        collide_block(m, co, W, valid, lm.leader, L.s);
-        if (valid) {
-            solve_world(m, W, bd, CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
-            clear_toi_trace(W, L.dbg);
+        store_mirror_block(bc);
+    } else {
+        load_mirror_block(m, lane_views(m, L, lds, w0, threadIdx.x).bc);
+        for (int step = 0; step < L.n_steps; ++step) {
+            if (step > 0) __syncthreads();  // the worlds' workspace writes of the previous step
+            step_worlds(m, L, w0, lane_views(m, L, lds, w0, opaque((int)threadIdx.x)));
         }
-        if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, lm.leader, co, bc, L.dbg);
-        if (valid) {
-            const float dt = L.dt;
-            if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
-            if (L.s.auto_clear_forces)
-                for (int b = 0; b < W.B; ++b) {
-                    W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
-                    W.f(GOI_B_TORQUE, b) = 0.0f;
-                }
-        }
+        store_mirror_block(lane_views(m, L, lds, w0, threadIdx.x).bc);
     }
-    store_mirror_block(bc);
 }
 
 // The 4-body rig's dimensions (5 bodies, 40 contact slots, 3 joints, 4 fixture rows, 8 worlds per wave) and its

@@ -88,6 +88,15 @@ inline
 #endif
 __shared__ __align__(16) double g_sincos_lds[128];
 
+// v itself, as a value the compiler cannot see through: what is computed from it after this point is computed there,
+// not earlier (a multi-step loop then holds no per-lane address of one step across the next).
+GOI_D int opaque(int v) {
+#ifndef GOI_HOST_BUILD
+    asm volatile("" : "+v"(v));
+#endif
+    return v;
+}
+
 // Copies the table into the block's LDS; called by every lane of the block before its first rot_of.
 GOI_D void sincos_table_load() {
 #ifdef GOI_HOST_BUILD
