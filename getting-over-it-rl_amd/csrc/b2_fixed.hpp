@@ -26,7 +26,7 @@ __global__ void __launch_bounds__(kBlock, 2) k_step_fixed(DModel m, Launch L) {
         m.no_edges = 1;
         L.s.revolute_v24 = 1;
     }
-    step_block<kMulti>(m, L);
+    step_block<kMulti, (kC > 64)>(m, L);  // the island instance (128 slots) re-derives its SolveTOI views
 }
 
 }  // namespace

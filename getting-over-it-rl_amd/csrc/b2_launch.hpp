@@ -135,6 +135,7 @@ __device__ __forceinline__ LaneViews lane_views(const DModel& m, const Launch& L
 // One b2World::Step (step.py:28-47) of each world of the block on its lane group, on the workspace mirror:
 // FindNewContacts where new_fixture, Collide, Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to
 // share the block's manifold and TOI work.
+template <bool kOpaqueToi>
 __device__ __forceinline__ void step_worlds(const DModel& m, const Launch& L, int w0, const LaneViews& v) {
     const LaneMap& lm = v.lm;
     const bool valid = lm.valid;
@@ -149,7 +150,8 @@ __device__ __forceinline__ void step_worlds(const DModel& m, const Launch& L, in
         solve_world(m, W, v.bd, v.CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
         clear_toi_trace(W, L.dbg);
     }
-    if (L.s.continuous_physics) solve_toi_world(m, W, v.bd, v.CR, L.s, L.dt, valid, lm.leader, v.co, v.bc, L.dbg);
+    if (L.s.continuous_physics)
+        solve_toi_world<kOpaqueToi>(m, W, v.bd, v.CR, L.s, L.dt, valid, lm.leader, v.co, v.bc, L.dbg);
     if (valid) {
         const float dt = L.dt;
         if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
@@ -168,7 +170,7 @@ __device__ __forceinline__ void step_worlds(const DModel& m, const Launch& L, in
 // index the compiler cannot see through, so no per-lane State or row address of one step is kept live (spilled to
 // scratch) into the next.
 // At most 256 registers (two waves per SIMD): the second wave hides the latency chains of the first.
-template <bool kMulti>
+template <bool kMulti, bool kOpaqueToi = false>  // kOpaqueToi: solve_toi_world's kOpaqueViews
 __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     GOI_DYNAMIC_LDS(lds);
     sincos_table_load();
@@ -197,7 +199,8 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
                 solve_world(m, W, bd, CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
                 clear_toi_trace(W, L.dbg);
             }
-            if (L.s.continuous_physics) solve_toi_world(m, W, bd, CR, L.s, L.dt, valid, lm.leader, co, bc, L.dbg);
+            if (L.s.continuous_physics)
+                solve_toi_world<kOpaqueToi>(m, W, bd, CR, L.s, L.dt, valid, lm.leader, co, bc, L.dbg);
             if (valid) {
                 const float dt = L.dt;
                 if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
@@ -213,7 +216,7 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
         load_mirror_block(m, lane_views(m, L, lds, w0, threadIdx.x).bc);
         for (int step = 0; step < L.n_steps; ++step) {
             if (step > 0) __syncthreads();  // the worlds' workspace writes of the previous step
-            step_worlds(m, L, w0, lane_views(m, L, lds, w0, opaque((int)threadIdx.x)));
+            step_worlds<kOpaqueToi>(m, L, w0, lane_views(m, L, lds, w0, opaque((int)threadIdx.x)));
         }
         store_mirror_block(lane_views(m, L, lds, w0, threadIdx.x).bc);
     }

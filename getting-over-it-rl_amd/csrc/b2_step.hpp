@@ -582,6 +582,11 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
 
 // b2World::SolveTOI (toi.py:827-865). Called by every lane of the block (the reset, the TOI searches and the final
 // copy are cooperative); `valid` marks the lanes that run a world, `leader` the first lane of each world's group.
+// kOpaqueViews: each iteration of the event loop re-derives the world's views through an offset the compiler cannot
+// see through, so that no per-lane address is held (spilled) from one iteration to the next. The island instance's
+// spilled registers go (816 to 16 B of scratch per lane, 3.5% faster); the rig instance, with few spills, measured
+// slower with it.
+template <bool kOpaqueViews = false>
 GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
                            float dt, bool valid, bool leader, const Coop& co, const BlockCopy& bc,
                            const GoiDebug& dbg) {
@@ -600,13 +605,31 @@ GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, co
         // the block iterates while any world has an event to process; the others take part in the searches only
         while (__any(found && events < max_events)) {
             const bool act = found && events < max_events;
-            if (act) {
-                toi_event(m, W, bd, CR, s, dt, slot, alpha, events, dbg);
-                ++events;
+            if constexpr (kOpaqueViews) {
+                const int z = opaque(0);
+                World Wi = W;
+                Wi.w = W.w + z;
+                Wi.ws = W.ws + z;
+                Bodies bdi = bd;
+                bdi.s = bd.s + z;
+                Rows CRi = CR;
+                CRi.base = CR.base + z;
+                if (act) {
+                    toi_event(m, Wi, bdi, CRi, s, dt, slot, alpha, events, dbg);
+                    ++events;
+                }
+                const int nt = act ? toi_search_prepare(m, Wi, CRi, s) : 0;
+                coop_run(co, leader ? nt : 0, toi);
+                found = act && toi_search_pick(Wi, s, slot, alpha);
+            } else {
+                if (act) {
+                    toi_event(m, W, bd, CR, s, dt, slot, alpha, events, dbg);
+                    ++events;
+                }
+                const int nt = act ? toi_search_prepare(m, W, CR, s) : 0;
+                coop_run(co, leader ? nt : 0, toi);
+                found = act && toi_search_pick(W, s, slot, alpha);
             }
-            const int nt = act ? toi_search_prepare(m, W, CR, s) : 0;
-            coop_run(co, leader ? nt : 0, toi);
-            found = act && toi_search_pick(W, s, slot, alpha);
         }
     }
     if (valid) W.i32(GOI_T_EVENTS, 0) = events;
