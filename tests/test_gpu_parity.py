@@ -375,15 +375,20 @@ def test_new_fixture_forces_full_search(oracle):
     assert (np.asarray(ref.contacts.pair) >= 0).sum() > live.sum() - drop.sum()  # the search re-created contacts
 
 
-@pytest.mark.parametrize("case,wpw,k", [("config4", None, 4), ("rig", "8", 3), ("pile", None, 5)])
+@pytest.mark.parametrize("case,wpw,k", [("config4", None, 4), ("rig", "8", 3), ("pile", None, 5), ("island", "4", 3)])
 def test_step_n_equals_repeated_steps(oracle, monkeypatch, case, wpw, k):
     """step_n_(k) (k steps in one launch, the workspaces kept in LDS between them) leaves the State k calls of
-    step_ leave, and the oracle's after k steps, bit for bit; three launches in a row."""
+    step_ leave, and the oracle's after k steps, bit for bit; three launches in a row. "rig" and "island" run the
+    multi-step instances for the rig's and the island workload's dimensions."""
     if wpw is not None:
         monkeypatch.setenv("GOI_WORLDS_PER_WAVE", wpw)
     if case == "pile":
         s, m, st = scene_defs.build_test_scene("pile", iterations=(8, 3))
         st, dt = perturbed(st, 64, seed=7), 1.0 / 60.0
+    elif case == "island":
+        s, m, st, cfg = b2.scenes.make_config(5, 256, edges="quad")
+        assert wd.dims(st) == (17, 16, 3, 128)
+        dt = cfg.dt
     else:
         s, m, st, cfg = b2.scenes.make_config(4, 512 if case == "config4" else 1024)
         dt = cfg.dt
