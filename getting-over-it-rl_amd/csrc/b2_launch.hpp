@@ -176,6 +176,8 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     sincos_table_load();
     const int w0 = xcd_group() * L.wpw;
     if constexpr (!kMulti) {
+        // step_worlds' sequence written out around the mirror's load and store: the code generated for this form (the
+        // views set up once, the step in a one-trip loop) measured 2% faster than a call of step_worlds
         const int lane = threadIdx.x;
         const LaneMap lm = lane_map(L, w0, lane);
         const bool valid = lm.valid;
@@ -188,7 +190,7 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
         const Rows CR = contact_rows(L, w0, valid ? lm.wl : 0);
         const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
         load_mirror_block(m, bc);
-        for (int step = 0; step < 1; ++step) {  // one trip: without the loop the code generated differs, 2% slower
+        for (int step = 0; step < 1; ++step) {
             build_order_block(bc);
             if (valid) {
                 if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
