@@ -584,8 +584,8 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
 // copy are cooperative); `valid` marks the lanes that run a world, `leader` the first lane of each world's group.
 // kOpaqueViews: each iteration of the event loop re-derives the world's views through an offset the compiler cannot
 // see through, so that no per-lane address is held (spilled) from one iteration to the next. The island instance's
-// spilled registers go (816 to 16 B of scratch per lane, 3.5% faster); the rig instance, with few spills, measured
-// slower with it.
+// spilled registers go (816 to 16 B of scratch per lane, 3.5% faster), and most of the generic kernel's (960 to 160 B,
+// 8% faster on the rig at 4 worlds per wave); the rig instance, with few spills, measured slower with it.
 template <bool kOpaqueViews = false>
 GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
                            float dt, bool valid, bool leader, const Coop& co, const BlockCopy& bc,

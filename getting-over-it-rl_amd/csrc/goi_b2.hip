@@ -64,7 +64,9 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
 }
 
 template <bool kMulti>
-__global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) { step_block<kMulti>(m, L); }
+__global__ void __launch_bounds__(kBlock, 2) k_step(DModel m, Launch L) {
+    step_block<kMulti, true>(m, L);  // SolveTOI's views re-derived in each event iteration
+}
 
 // b2WorldManifold::Initialize (Box2D 2.3.1; the solver's prepare computes the same, contact_solver.py:60-104) of
 // every slot of every world from the bodies' transforms, one thread per (slot, world): normal [C, 2], points
