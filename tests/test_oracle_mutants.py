@@ -155,6 +155,29 @@ MUTANTS = [
     ("revolute_v23_limit_never_releases",
      "int redo = (st == AT_LOWER && new_z < 0.0f) || (st == AT_UPPER && new_z > 0.0f);", "int redo = 0;",
      lambda o: P.test_revolute_velocity_rows(o, *_vel("leaving_lower_v23"))),
+    # SynchronizeFixtures, the TOI position passes, warm start, the rotation clamp, the per-island exit
+    ("sync_multiplier_one", "float ddx = 2.0f * d.x, ddy = 2.0f * d.y;", "float ddx = 1.0f * d.x, ddy = 1.0f * d.y;",
+     lambda o: P.test_synchronize_fixtures_refattens_a_moved_box(o, *P._SYNC_MOVES[0])),
+    ("sync_always_refattens", "if (fat[0] <= lx && fat[1] <= ly && ux <= fat[2] && uy <= fat[3]) continue;",
+     "if (0) continue;", lambda o: P.test_synchronize_fixtures_keeps_a_fat_box_that_still_holds(o, (3.0, 1.0))),
+    ("sync_extension_0_2", "float e = 0.1f; /* b2_aabbExtension */", "float e = 0.2f;",
+     lambda o: P.test_synchronize_fixtures_refattens_a_moved_box(o, *P._SYNC_MOVES[0])),
+    ("toi_position_stops_at_3_slop", "if (min_sep >= -1.5f * s->linear_slop) break;",
+     "if (min_sep >= -3.0f * s->linear_slop) break;", lambda o: P.test_toi_position_passes_closed_form(o)),
+    ("toi_position_uses_baumgarte", "float ms = cs_solve_position(x, c, k, s->toi_baumgarte, mA, mB, iA, iB);",
+     "float ms = cs_solve_position(x, c, k, s->baumgarte, mA, mB, iA, iB);",
+     lambda o: P.test_toi_position_passes_closed_form(o)),
+    ("warm_start_without_dt_ratio", "c->ni[j] = warm ? dt_ratio * w->c_ni[2 * slot + j] : 0.0f;",
+     "c->ni[j] = warm ? w->c_ni[2 * slot + j] : 0.0f;", lambda o: P.test_warm_start_scales_impulses_by_dt_ratio(o)),
+    ("rotation_clamp_removed",
+     "if (rot * rot > max_r * max_r) {\n            float ratio = max_r / babs(rot);\n            ww = ww * ratio;\n"
+     "        }\n        k->cx[b]",
+     "if (0) {\n            float ratio = max_r / babs(rot);\n            ww = ww * ratio;\n        }\n        k->cx[b]",
+     lambda o: P.test_rotation_clamp(o, 200.0)),
+    ("position_exit_at_1_5_slop", "k->min_sep[i] >= -3.0f * s->linear_slop && k->jok[i]",
+     "k->min_sep[i] >= -1.5f * s->linear_slop && k->jok[i]", lambda o: P.test_position_iterations_exit_per_island(o)),
+    ("position_exit_all_islands_together", "if (k->done[isl]) continue;\n            float ms",
+     "if (!more) continue;\n            float ms", lambda o: P.test_position_iterations_exit_per_island(o)),
 ]
 
 

@@ -1283,3 +1283,216 @@ def test_revolute_velocity_rows(oracle, name, v24, where, w0, motor, want):
     st = wd.batch(state, 1)
     oracle.step_(model, st, s, h)
     assert abs(float(st.bodies.w[0, 1]) - want(float(h))) < 2e-5
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# SynchronizeFixtures' re-fatten rule   (pairs.py:181-207, shapes.py:136-146; b2DynamicTree::MoveProxy)
+#
+# A body that moved has its fixture's swept AABB (the union of the AABBs at the sweep start (c0, a0) and at the
+# new transform) checked against its fat AABB. If the fat box still holds it, nothing changes. Otherwise the new fat
+# box is the swept box extended by b2_aabbExtension = 0.1 on every side, and then by b2_aabbMultiplier = 2 times the
+# transform's displacement on the side the body moved to. A circle centred on its body has the AABB p +- r, so with
+# no gravity and no contacts every number is fixed by the step's integration (semi-implicit Euler, pinned above).
+
+def _moved_circle(oracle, p, v, r=0.5, dt=F32(1 / 60)):
+    s = S.stock(gravity=(0.0, 0.0))
+    d = wd.WorldDef(s)
+    b = d.add_body(wd.DYNAMIC, p, velocity=v, mass=1.0, inertia=1.0)
+    d.add_circle(b, r)
+    model, state = d.build(4)
+    cm = wd.compact_model(model, state)
+    st = wd.batch(wd.compact_state(cm, state), 1)
+    fat0 = st.fixtures.fat[0, 0].copy()
+    oracle.step_(cm, st, s, dt)
+    return fat0, st.bodies.xf_p[0, 0].copy(), st.bodies.c0[0, 0].copy(), st.fixtures.fat[0, 0].copy()
+
+
+_SYNC_MOVES = [((0.25, 5.0), (12.0, -7.0)), ((-3.0, 1.0), (-15.0, 9.5)), ((7.5, -2.0), (0.5, 30.0)),
+               ((0.0, 0.0), (-8.0, -0.25))]
+
+
+@pytest.mark.parametrize("p,v", _SYNC_MOVES)
+def test_synchronize_fixtures_refattens_a_moved_box(oracle, p, v):
+    r = F32(0.5)
+    fat0, p1, p0, fat = _moved_circle(oracle, p, v, r)
+    assert np.array_equal(p0, np.array(p, F32))  # the sweep start is the step's start
+    lo = np.minimum(p0 - r, p1 - r)
+    hi = np.maximum(p0 + r, p1 + r)
+    assert not (np.all(fat0[:2] <= lo) and np.all(hi <= fat0[2:]))  # the move leaves the old fat box
+    e, d = F32(0.1), (p1 - p0).astype(F32)
+    lo, hi = (lo - e).astype(F32), (hi + e).astype(F32)
+    for i in range(2):
+        dd = F32(F32(2.0) * d[i])
+        if dd < 0:
+            lo[i] = F32(lo[i] + dd)
+        else:
+            hi[i] = F32(hi[i] + dd)
+    assert np.array_equal(fat, np.concatenate([lo, hi])), (fat, lo, hi)
+
+
+@pytest.mark.parametrize("v", [(3.0, 1.0), (-5.5, 0.0), (0.0, -5.9)])
+def test_synchronize_fixtures_keeps_a_fat_box_that_still_holds(oracle, v):
+    """A move of under 0.1 m keeps the swept AABB inside the fat box from b2BroadPhase::CreateProxy (the AABB
+    +- 0.1): the fat box stays the same to the bit."""
+    fat0, p1, p0, fat = _moved_circle(oracle, (0.25, 5.0), v)
+    assert 0 < np.abs(p1 - p0).max() < 0.1
+    assert np.array_equal(fat, fat0)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the TOI island's position passes   (toi.py:719-760; b2Island::SolveTOI)
+#
+# A circle (radius 0.5, no gravity) flies head-on into a static slab's face and would pass through it in one step.
+# b2TimeOfImpact stops it where the core shapes are target = r_total - 3 slop apart, so the contact's separation is
+# -3 slop (-0.015) at the event. Only the TOI pair has mass; the contact point lies on the line through the circle's
+# centre along the normal, so the effective mass is the circle's inverse mass and each pass moves the circle by
+# exactly -clamp(b (sep + slop), -max_linear_correction, 0) along the normal, b = toi_baumgarte, sep measured before
+# the pass. A pass that measured sep >= -1.5 slop is the last one (its correction still applies). The TOI velocity
+# pass then stops the circle (restitution 0), so it ends the step at the solved pose.
+#
+# With the stock b = 0.75 the second pass measures -0.0075 = -1.5 slop (the scheme is built to land there), so its
+# outcome turns on the last bit of the TOI root; b = 0.6 keeps every decision 1e-3 away from its threshold.
+
+def test_toi_position_passes_closed_form(oracle):
+    s = S.stock(gravity=(0.0, 0.0), continuous_physics=True, toi_baumgarte=0.6)
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (3.0, 0.0))
+    d.add_box(g, (0.5, 2.0))  # face at x = 2.5, skin 0.01
+    x0, vx, r = F32(1.2), F32(110.0), 0.5
+    b = d.add_body(wd.DYNAMIC, (x0, 0.0), velocity=(vx, 0.0), mass=1.0, inertia=1.0)
+    d.add_circle(b, r)
+    model, state = d.build(4)
+    cm = wd.compact_model(model, state)
+    st = wd.batch(wd.compact_state(cm, state), 1)
+    dbg = toi_trace(1, wd.dims(st))
+    h = F32(1 / 60)
+    oracle.step_(cm, st, s, h, debug=dbg)
+    assert int(st.toi.events[0]) == 1
+    alpha = dbg["toi_event_alpha"][0, 0].view(np.float32)
+    x1 = F32(x0 + F32(h * vx))  # Solve's integration
+    x = float(F32(x0 + F32(alpha * F32(x1 - x0))))  # b2Sweep::Advance to the event
+    slop, b_toi = float(s.linear_slop), float(s.toi_baumgarte)
+    seps = []
+    for _ in range(20):
+        sep = (2.5 - x) - (r + float(s.polygon_radius))
+        seps.append(sep)
+        x += max(b_toi * (sep + slop), -float(s.max_linear_correction))
+        if sep >= -1.5 * slop:
+            break
+    assert abs(seps[0] + 3 * slop) < 2e-4  # the TOI target
+    assert len(seps) == 3 and min(abs(q + 1.5 * slop) for q in seps) > 5e-4
+    assert abs(float(st.bodies.c[0, 1, 0]) - x) < 2e-6, (st.bodies.c[0, 1, 0], x)
+    assert st.bodies.c[0, 1, 1] == 0 and st.bodies.a[0, 1] == 0
+    assert np.array_equal(st.bodies.c0[0, 1], st.bodies.c[0, 1])  # the leap of faith
+    assert np.all(st.bodies.v[0, 1] == 0) and st.bodies.w[0, 1] == 0
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# warm start's dtRatio   (contact_solver.py:165-184, step.py:34)
+#
+# b2ContactSolver scales the stored impulses by dtRatio = dt * inv_dt0 before warm-starting; with no velocity
+# iteration StoreImpulses writes those scaled values back. At dt = 1/64 (inv_dt0 = 64 exactly) followed by a step of
+# 1/128, dtRatio is exactly 1/2, so every stored impulse halves to the bit.
+
+def test_warm_start_scales_impulses_by_dt_ratio(oracle):
+    import dataclasses
+    s = dataclasses.replace(S.stock(), allow_sleep=False)
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (0.0, -0.5))
+    d.add_box(g, (10.0, 0.5))
+    b = d.add_body(wd.DYNAMIC, (0.0, 0.5), mass=2.0, inertia=F32(2) / F32(6))
+    d.add_box(b, (0.5, 0.5))
+    model, state = d.build(4)
+    cm = wd.compact_model(model, state)
+    st = wd.batch(wd.compact_state(cm, state), 1)
+    for _ in range(20):
+        oracle.step_(cm, st, s, F32(1 / 64))
+    assert float(st.inv_dt0[0]) == 64.0
+    ct = st.contacts
+    k = int(np.nonzero((ct.pair[0] >= 0) & ct.touching[0])[0][0])
+    ni, ti, ids = ct.normal_impulse[0, k].copy(), ct.tangent_impulse[0, k].copy(), ct.point_id[0, k].copy()
+    assert int(ct.count[0, k]) == 2 and np.all(ni > 0.1)
+    oracle.step_(cm, st, dataclasses.replace(s, velocity_iterations=0), F32(1 / 128))
+    assert np.array_equal(ct.point_id[0, k], ids)  # the same features: the impulses carry over
+    assert np.array_equal(ct.normal_impulse[0, k], ni * F32(0.5))
+    assert np.array_equal(ct.tangent_impulse[0, k], ti * F32(0.5))
+    assert float(st.inv_dt0[0]) == 128.0
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Solve's rotation clamp   (step.py:117-135)
+#
+# A free body whose step would turn it by more than max_rotation (stock pi/2) has its angular velocity scaled by
+# max_rotation / |h w|: it turns by exactly max_rotation (to float rounding) and keeps the scaled spin.
+
+@pytest.mark.parametrize("w0", [200.0, -150.0, 95.0])
+def test_rotation_clamp(oracle, w0):
+    s = S.stock(gravity=(0.0, 0.0))
+    d = wd.WorldDef(s)
+    b = d.add_body(wd.DYNAMIC, (0.0, 0.0), 0.3, angular_velocity=w0, mass=1.0, inertia=1.0)
+    d.add_box(b, (0.5, 0.5))
+    model, state = d.build(4)
+    cm = wd.compact_model(model, state)
+    st = wd.batch(wd.compact_state(cm, state), 1)
+    h = F32(1 / 60)
+    oracle.step_(cm, st, s, h)
+    turn, max_r = float(st.bodies.a[0, 0]) - float(F32(0.3)), float(s.max_rotation)
+    assert abs(float(h) * w0) > max_r
+    assert abs(turn - np.sign(w0) * max_r) < 1e-6
+    assert float(st.bodies.w[0, 0]) == pytest.approx(np.sign(w0) * max_r / float(h), rel=1e-6)
+    assert np.all(st.bodies.v[0, 0] == 0)
+
+
+def test_rotation_below_the_clamp_is_untouched(oracle):
+    s = S.stock(gravity=(0.0, 0.0))
+    d = wd.WorldDef(s)
+    b = d.add_body(wd.DYNAMIC, (0.0, 0.0), 0.3, angular_velocity=90.0, mass=1.0, inertia=1.0)
+    d.add_box(b, (0.5, 0.5))
+    model, state = d.build(4)
+    cm = wd.compact_model(model, state)
+    st = wd.batch(wd.compact_state(cm, state), 1)
+    h = F32(1 / 60)
+    oracle.step_(cm, st, s, h)
+    assert st.bodies.w[0, 0] == F32(90.0) and st.bodies.a[0, 0] == F32(F32(0.3) + F32(h * F32(90.0)))
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the position iterations' per-island exit   (step.py:197-251)
+#
+# Each island stops after the first position pass whose smallest separation is at least -3 slop and whose joints
+# are within tolerance (that pass's corrections apply). Two boxes rest on one static slab, so they form two islands:
+# box A overlaps the slab by 0.0125 (separation -0.0125, within -3 slop at the first pass), box B by 0.05. With no
+# gravity and no velocity neither moves before the position passes. Box A must end the step exactly as with one
+# position iteration, whatever the iteration count; box B keeps correcting.
+
+def _two_islands(oracle, iterations):
+    import dataclasses
+    s = dataclasses.replace(S.stock(gravity=(0.0, 0.0)), position_iterations=iterations, allow_sleep=False)
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (0.0, -0.5))
+    d.add_box(g, (10.0, 0.5))
+    a = d.add_body(wd.DYNAMIC, (-3.0, 0.5 + 0.0075), mass=1.0, inertia=0.2)  # separation 0.0075 - 2 skins
+    d.add_box(a, (0.5, 0.5))
+    bb = d.add_body(wd.DYNAMIC, (3.0, 0.5 - 0.03), mass=1.0, inertia=0.2)
+    d.add_box(bb, (0.5, 0.5))
+    model, state = d.build(4)
+    cm = wd.compact_model(model, state)
+    st = wd.batch(wd.compact_state(cm, state), 1)
+    dbg = {k: np.full(shape, -7, np.int32) for k, shape in b2.debug_shapes(1, wd.dims(st)).items()}
+    oracle.step_(cm, st, s, F32(1 / 60), debug=dbg)
+    return st, dbg
+
+
+def test_position_iterations_exit_per_island(oracle):
+    runs = {n: _two_islands(oracle, n) for n in (1, 2, 3, 8)}
+    st1, dbg1 = runs[1]
+    isl = dbg1["body_island"][:, 0]
+    assert isl[0] == -1 and isl[1] >= 0 and isl[2] >= 0 and isl[1] != isl[2]
+    pose = lambda st, b: (st.bodies.c[0, b].tobytes(), st.bodies.a[0, b].tobytes(),  # noqa: E731
+                          st.bodies.xf_p[0, b].tobytes(), st.bodies.xf_q[0, b].tobytes())
+    assert float(st1.bodies.c[0, 1, 1]) > 0.5 + 0.0075  # the first pass moved box A
+    for n in (2, 3, 8):
+        st, _ = runs[n]
+        assert pose(st, 1) == pose(st1, 1), n
+    ys = [float(runs[n][0].bodies.c[0, 2, 1]) for n in (1, 2, 3, 8)]
+    assert all(y1 < y2 for y1, y2 in zip(ys, ys[1:]))  # box B rises with every pass
