@@ -14,13 +14,15 @@ import numpy as np
 
 from . import debug, io, layout, record, scenes, shapes, world
 from .settings import Settings
-from .step import collide_, debug_shapes, make_debug, prepare, sincos, step, step_, step_n_, world_manifolds
+from .step import (collide_, debug_shapes, last_launch, make_debug, prepare, sincos, step, step_, step_n_,
+                   world_manifolds)
 from .world import (DYNAMIC, KINEMATIC, PRISMATIC, REVOLUTE, STATIC, WELD, Model, State, WorldDef, compact_model,
                     compact_state, expand_state)
 
 GAME_DT = np.float32(0.008333334)  # Time.fixedDeltaTime (float32 nearest 1/120)
 
-__all__ = ["Settings", "step", "step_", "step_n_", "collide_", "debug_shapes", "make_debug", "prepare", "sincos", "world_manifolds",
+__all__ = ["Settings", "step", "step_", "step_n_", "collide_", "debug_shapes", "last_launch", "make_debug", "prepare",
+           "sincos", "world_manifolds",
            "Model", "State",
            "WorldDef", "GAME_DT", "STATIC", "KINEMATIC", "DYNAMIC", "REVOLUTE", "PRISMATIC", "WELD", "compact_model",
            "compact_state", "expand_state", "debug", "io", "layout", "record", "scenes", "shapes", "world"]

@@ -12,7 +12,7 @@ import numpy as np
 PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = PKG / "lib" / "libgoi_b2.so"
 NUM_LEAVES = 71
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 GOI_OK, GOI_E_ARG, GOI_E_SHAPE, GOI_E_HIP, GOI_E_UNSUPPORTED = 0, -1, -2, -3, -4
 
@@ -64,9 +64,16 @@ class GoiDebug(ctypes.Structure):
                 ("toi_event_slot", _P), ("toi_event_alpha", _P), ("toi_event_island", _P), ("toi_island_rows", _P)]
 
 
+class GoiLaunchInfo(ctypes.Structure):
+    _fields_ = [("worlds_per_wave", ctypes.c_int32), ("blocks", ctypes.c_int32), ("lds_bytes", ctypes.c_int32),
+                ("kernel", ctypes.c_int32)]
+
+
+KERNEL_GENERIC, KERNEL_RIG, KERNEL_ISLAND, KERNEL_COLLIDE = 1, 2, 3, 4  # GOI_KERNEL_*
+
 EXPORTS = ("goi_abi_version", "goi_model_create", "goi_model_destroy", "goi_step", "goi_step_n", "goi_step_n_noalloc",
            "goi_collide", "goi_world_manifold", "goi_apply_motor_actions", "goi_sincos", "goi_packed_layout",
-           "goi_last_error")
+           "goi_model_release_rows", "goi_last_launch", "goi_last_error")
 
 _LIB = None
 
@@ -106,6 +113,10 @@ def lib(path=None):
     L.goi_packed_layout.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                     ctypes.POINTER(ctypes.c_int32)]
     L.goi_packed_layout.restype = ctypes.c_int32
+    L.goi_model_release_rows.argtypes = [_P]
+    L.goi_model_release_rows.restype = ctypes.c_int32
+    L.goi_last_launch.argtypes = [ctypes.POINTER(GoiLaunchInfo)]
+    L.goi_last_launch.restype = ctypes.c_int32
     if L.goi_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{p}: ABI version {L.goi_abi_version()} != {ABI_VERSION}")
     if path is None:

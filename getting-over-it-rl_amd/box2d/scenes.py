@@ -299,9 +299,13 @@ def _native_actions(speed, torque, a):
     return True
 
 
-def make_config(k, n=None, edges="quad"):
-    """(settings, compact Model, batched compact numpy State, Config) of benchmark configuration k (1-5)."""
+def make_config(k, n=None, edges="quad", capacity=None):
+    """(settings, compact Model, batched compact numpy State, Config) of benchmark configuration k (1-5); `capacity`
+    replaces the configuration's contact slots per world (a small table makes FindNewContacts drop pairs)."""
     cfg = CONFIGS[k]
+    if capacity is not None:
+        from dataclasses import replace
+        cfg = replace(cfg, capacity=int(capacity))
     settings = settings_for(cfg)
     model, state, pts = build_world(cfg, settings, edges)
     st = place_worlds(cfg, model, state, pts, n)

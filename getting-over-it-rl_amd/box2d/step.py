@@ -46,16 +46,47 @@ class DeviceModel:
             self.handle = None
 
 
+def _compact_from_device_state(model, state):
+    """compact_model (world.py:437-472) of a full-layout Model from a device State's fixture rows: the body types and
+    the static fixtures' fat AABBs, friction and restitution must be the same in every world (checked on the device;
+    a step never changes them), and world 0's become the Model's shared tables."""
+    types = state.bodies.type
+    if bool((types != types[:1]).any()):
+        raise ValueError("compact_model: the worlds' body types differ, so static fixtures cannot be shared")
+    types0 = types[:1].cpu().numpy()
+    on_static = types0[0][np.asarray(model.fixture_body)] == wd.STATIC
+    fx = state.fixtures
+    if fx.fat.shape[1] != on_static.size:
+        raise ValueError("a full-layout Model needs a full-layout State (a row per fixture)")
+    idx = torch.as_tensor(np.flatnonzero(on_static), device=fx.fat.device, dtype=torch.long)
+    for name, leaf in (("fat", fx.fat), ("friction", fx.friction), ("restitution", fx.restitution)):
+        rows = leaf.index_select(1, idx)
+        if bool((rows != rows[:1]).any()):
+            raise ValueError(f"compact_model: a static fixture's {name} differs between worlds")
+    host = wd.State(bodies=wd.Bodies(*[types0 if f == "type" else None for f in wd.Bodies._fields]),
+                    fixtures=wd.Fixtures(friction=fx.friction[:1].cpu().numpy(),
+                                         restitution=fx.restitution[:1].cpu().numpy(), fat=fx.fat[:1].cpu().numpy()),
+                    joints=None, contacts=None, gravity=None, inv_dt0=None, next_key=None, new_fixture=None,
+                    overflow=None)
+    return wd.compact_model(model, host)
+
+
 def device_model(model, contact_capacity, device=None, state=None):
     """Cached DeviceModel for (model object, capacity, device). A compact Model built without body types (the
     reference's compact_model keeps them in the State only, world.py:437-472) takes them from `state`, whose worlds
-    must agree."""
+    must agree. A full-layout Model (WorldDef.build's) is compacted first from `state`'s static fixture rows, as the
+    reference's GPU path does (gpu/pairs.py:286-303 read a compact Model's shared tables): its States may stay in the
+    full layout, whose static rows the step leaves untouched."""
     key = (id(model), int(contact_capacity), str(device))
     hit = _MODELS.get(key)
     if hit is not None and hit[0] is model:
         return hit[1]
     desc_model = model
-    if model.body_type is None and state is not None:
+    if model.fixture_slot is None:
+        if state is None:
+            raise ValueError("a full-layout Model needs the State its static fixture rows come from")
+        desc_model = _compact_from_device_state(model, state)
+    elif model.body_type is None and state is not None:
         bt = np.asarray(state.bodies.type.to("cpu") if torch.is_tensor(state.bodies.type) else state.bodies.type)
         bt = bt.reshape(-1, bt.shape[-1])
         if not (bt == bt[0]).all():
@@ -132,6 +163,18 @@ def world_manifolds(model, state, stream=None):
     _abi.check(dm.L.goi_world_manifold(dm.handle, ctypes.byref(view), *[ctypes.c_void_p(b.data_ptr()) for b in bufs],
                                        ctypes.c_void_p(st)), dm.L)
     return tuple(b[..., :n].movedim(-1, 0) for b in bufs)
+
+
+def last_launch():
+    """The calling thread's last step or collide launch (goi_last_launch): dict(worlds_per_wave, blocks, lds_bytes,
+    kernel), kernel one of "generic", "rig", "island", "collide"."""
+    L = _abi.lib()
+    info = _abi.GoiLaunchInfo()
+    _abi.check(L.goi_last_launch(ctypes.byref(info)), L)
+    names = {_abi.KERNEL_GENERIC: "generic", _abi.KERNEL_RIG: "rig", _abi.KERNEL_ISLAND: "island",
+             _abi.KERNEL_COLLIDE: "collide"}
+    return dict(worlds_per_wave=info.worlds_per_wave, blocks=info.blocks, lds_bytes=info.lds_bytes,
+                kernel=names.get(info.kernel))
 
 
 def sincos(x):

@@ -19,6 +19,7 @@ namespace {
 template <int kB, int kC, int kJ, int kR, int kS, bool kMulti, bool kPlain>
 __global__ void __launch_bounds__(kBlock, 2) k_step_fixed(DModel m, Launch L) {
     L.B = kB; L.C = kC; L.J = kJ; L.R = kR; L.wpw = kS;
+    L.full_rows = 0;  // the launch takes these instances for compact packed States only
     L.dbg = GoiDebug{};
     m.B = kB; m.J = kJ; m.R = kR;
     if (kPlain) {

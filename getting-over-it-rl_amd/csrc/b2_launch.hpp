@@ -21,6 +21,7 @@ static_assert(kBlock == kCoopLanes, "the cooperative passes span the block");
 struct Launch {
     void* leaf[GOI_NUM_LEAVES];
     int packed;  // the leaves are the consecutive parts of leaf[0]'s buffer (goi_packed_layout)
+    int full_rows;  // the fixture leaves have a row per fixture (the full layout); R counts the non-static ones
     int n, pitch, B, C, R, J;
     int wpw;  // worlds per wavefront: lanes >= wpw idle, so small batches still spread over every SIMD
     uint32_t* scratch;  // contact rows then joint rows
@@ -47,6 +48,7 @@ __device__ __forceinline__ World make_world(const DModel& m, const Launch& L, in
     W.S = L.wpw;
     W.sub = sub;
     W.G = G;
+    W.frow_map = L.full_rows ? m.row : nullptr;
     W.init_masks(m);
     return W;
 }

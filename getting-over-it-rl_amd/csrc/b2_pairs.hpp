@@ -308,8 +308,9 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
     unsigned long long rows = 0ull;
     float4 U = make_float4(kMaxFloat, kMaxFloat, -kMaxFloat, -kMaxFloat);
     for (int r = 0; r < m.R; ++r) {
-        const float4 q = make_float4(W.f(GOI_F_FAT, 4 * r), W.f(GOI_F_FAT, 4 * r + 1), W.f(GOI_F_FAT, 4 * r + 2),
-                                     W.f(GOI_F_FAT, 4 * r + 3));
+        const int fr = 4 * W.frow(r);
+        const float4 q = make_float4(W.f(GOI_F_FAT, fr), W.f(GOI_F_FAT, fr + 1), W.f(GOI_F_FAT, fr + 2),
+                                     W.f(GOI_F_FAT, fr + 3));
         W.set_qbox(r, q);
         if (!((query_rows >> r) & 1ull) || !W.active(m.row[r].body)) continue;
         rows |= 1ull << r;
@@ -470,18 +471,19 @@ GOI_D unsigned long long sync_body_fixtures(const DModel& m, const World& W, int
         shape_aabb2(m, f, x1, x2, a1, a2);
         float lx = bmin(a1.x, a2.x), ly = bmin(a1.y, a2.y);
         float ux = bmax(a1.z, a2.z), uy = bmax(a1.w, a2.w);
-        const float fx0 = W.f(GOI_F_FAT, 4 * r), fy0 = W.f(GOI_F_FAT, 4 * r + 1);
-        const float fx1 = W.f(GOI_F_FAT, 4 * r + 2), fy1 = W.f(GOI_F_FAT, 4 * r + 3);
+        const int fr = 4 * W.frow(r);
+        const float fx0 = W.f(GOI_F_FAT, fr), fy0 = W.f(GOI_F_FAT, fr + 1);
+        const float fx1 = W.f(GOI_F_FAT, fr + 2), fy1 = W.f(GOI_F_FAT, fr + 3);
         if (fx0 <= lx && fy0 <= ly && ux <= fx1 && uy <= fy1) continue;
         const V2 d = x2.p - x1.p;
         lx = lx - 0.1f; ly = ly - 0.1f; ux = ux + 0.1f; uy = uy + 0.1f;  // b2_aabbExtension
         const float ddx = 2.0f * d.x, ddy = 2.0f * d.y;                  // b2_aabbMultiplier
         if (ddx < 0.0f) lx = lx + ddx; else ux = ux + ddx;
         if (ddy < 0.0f) ly = ly + ddy; else uy = uy + ddy;
-        W.f(GOI_F_FAT, 4 * r) = lx;
-        W.f(GOI_F_FAT, 4 * r + 1) = ly;
-        W.f(GOI_F_FAT, 4 * r + 2) = ux;
-        W.f(GOI_F_FAT, 4 * r + 3) = uy;
+        W.f(GOI_F_FAT, fr) = lx;
+        W.f(GOI_F_FAT, fr + 1) = ly;
+        W.f(GOI_F_FAT, fr + 2) = ux;
+        W.f(GOI_F_FAT, fr + 3) = uy;
         moved |= 1ull << r;
     }
     return moved;

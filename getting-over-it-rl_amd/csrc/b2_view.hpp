@@ -226,6 +226,18 @@ struct World {
     Workspace k;
     unsigned long long smask, dmask;  // static and dynamic bodies (Model.body_type, the same in every world)
     int sub, G;       // the lane's place in the world's lane group, and the group's size
+    const MRow* frow_map;  // non-null for a State in the full fixture layout (DModel::row)
+
+    // The State row of non-static fixture row r: r itself in the compact fixture layout, the fixture's own index in
+    // the full layout, where every fixture has a row (world.py:98-101, 400-403; the static rows are never read: their
+    // fat AABB, friction and restitution are the Model's).
+    GOI_D int frow(int r) const {
+#if GOI_PACKED_STATE
+        return r;
+#else
+        return frow_map ? frow_map[r].fixture : r;
+#endif
+    }
 
     GOI_D Group grp() const { return Group{sub, G}; }
 
@@ -576,16 +588,16 @@ GOI_D void store_toi_block(const BlockCopy& bc) {
 GOI_D float4 fat_of(const DModel& m, const World& W, int fixture) {
     const int r = m.fix[fixture].slot;
     if (r < 0) return m.fix[fixture].fat;
-    return make_float4(W.f(GOI_F_FAT, 4 * r), W.f(GOI_F_FAT, 4 * r + 1), W.f(GOI_F_FAT, 4 * r + 2),
-                       W.f(GOI_F_FAT, 4 * r + 3));
+    const int i = 4 * W.frow(r);
+    return make_float4(W.f(GOI_F_FAT, i), W.f(GOI_F_FAT, i + 1), W.f(GOI_F_FAT, i + 2), W.f(GOI_F_FAT, i + 3));
 }
 GOI_D float friction_of(const DModel& m, const World& W, int fixture) {
     const int r = m.fix[fixture].slot;
-    return r < 0 ? m.fix[fixture].friction : W.f(GOI_F_FRICTION, r);
+    return r < 0 ? m.fix[fixture].friction : W.f(GOI_F_FRICTION, W.frow(r));
 }
 GOI_D float restitution_of(const DModel& m, const World& W, int fixture) {
     const int r = m.fix[fixture].slot;
-    return r < 0 ? m.fix[fixture].restitution : W.f(GOI_F_RESTITUTION, r);
+    return r < 0 ? m.fix[fixture].restitution : W.f(GOI_F_RESTITUTION, W.frow(r));
 }
 
 // b2TestOverlap

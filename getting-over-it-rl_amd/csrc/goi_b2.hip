@@ -13,6 +13,7 @@
 // per-block HBM scratch tile ([row][field][world]); the static terrain is a BVH over the static fixtures' fat AABBs,
 // shared by every world and read through L2.
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -28,6 +29,7 @@ using namespace goi;
 namespace {
 
 thread_local std::string g_error;
+thread_local GoiLaunchInfo g_last_launch{};  // goi_last_launch
 
 int fail(int code, const std::string& msg) {
     g_error = msg;
@@ -500,11 +502,29 @@ int32_t goi_model_destroy(GoiModel* M) {
     return GOI_OK;
 }
 
+int32_t goi_model_release_rows(GoiModel* M) {
+    if (!M) return fail(GOI_E_ARG, "goi_model_release_rows: null argument");
+    std::lock_guard<std::mutex> hold(M->mu);
+    if (M->scratch.empty()) return GOI_OK;
+    // every launch that reads a buffer has finished before it is freed (the streams themselves may be gone)
+    int cur = 0;
+    const bool switch_dev = hipGetDevice(&cur) == hipSuccess && cur != M->device;
+    if (switch_dev) (void)hipSetDevice(M->device);
+    hipError_t e = hipDeviceSynchronize();
+    for (StreamScratch& s : M->scratch)
+        if (e == hipSuccess) e = hipFree(s.rows);
+    if (switch_dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess) return fail(GOI_E_HIP, std::string("goi_model_release_rows: ") + hipGetErrorString(e));
+    M->scratch.clear();
+    return GOI_OK;
+}
+
 static int check_view(const GoiModel* M, const GoiStateView* v, const char* who) {
     if (!M || !v) return fail(GOI_E_ARG, std::string(who) + ": null argument");
     if (v->n_worlds < 0 || v->pitch < v->n_worlds) return fail(GOI_E_ARG, std::string(who) + ": bad n_worlds/pitch");
-    if (v->B != M->d.B || v->R != M->d.R || v->J != M->d.J || v->C != M->C)
-        return fail(GOI_E_SHAPE, std::string(who) + ": state capacities differ from the model's (B, R, J, C)");
+    // R: the model's non-static fixture rows (the compact fixture layout) or all its fixtures (the full layout)
+    if (v->B != M->d.B || (v->R != M->d.R && v->R != M->d.F) || v->J != M->d.J || v->C != M->C)
+        return fail(GOI_E_SHAPE, std::string(who) + ": state capacities differ from the model's (B, R or F, J, C)");
     for (int i = 0; i < GOI_NUM_LEAVES; ++i) {
         // leaves over an empty axis (no joints, no non-static fixtures, no slots) may be null
         const bool by_j = i >= GOI_J_ENABLE_MOTOR && i <= GOI_J_UPPER_IMPULSE;
@@ -523,16 +543,16 @@ static int check_view(const GoiModel* M, const GoiStateView* v, const char* who)
     return GOI_OK;
 }
 
-// Compute units of the current device (cached per process; one device per process is the common case).
+// Compute units of the current device, looked up once per device (256, the MI355X's count, if the query fails).
 static int cu_count() {
-    static int n = 0;
+    static std::atomic<int> cached[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int n = cached[dev].load(std::memory_order_relaxed);
     if (n <= 0) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) ==
-                                                    hipSuccess && v > 0)
-            n = v;
-        else
-            n = 256;
+        int v = 0;
+        n = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0 ? v : 256;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
     return n;
 }
@@ -601,6 +621,9 @@ static size_t block_lds_bytes(const Launch& L) {
     return ((size_t)words * L.wpw + kBlock) * sizeof(int);
 }
 
+// A State in the full fixture layout (a row per fixture: v->R is the model's F, not its R non-static rows) runs with
+// full_rows set: the kernels then address non-static row r at the fixture's own row and never touch the static rows
+// (a static fixture's fat AABB, friction and restitution are the Model's; a step never changes them).
 static void fill_launch(Launch& L, const GoiModel* M, const GoiStateView* v, const GoiSettings* s, float dt) {
     std::memcpy(L.leaf, v->leaf, sizeof(L.leaf));
     L.n_steps = 1;
@@ -608,14 +631,15 @@ static void fill_launch(Launch& L, const GoiModel* M, const GoiStateView* v, con
     L.pitch = v->pitch;
     L.B = v->B;
     L.C = v->C;
-    L.R = v->R;
+    L.R = M->d.R;
     L.J = v->J;
+    L.full_rows = v->R != M->d.R;
     L.s = *s;
     L.dt = dt;
     std::memset(&L.dbg, 0, sizeof(L.dbg));
     L.scratch = nullptr;
-    L.wpw = worlds_per_wave(v->n_worlds, workspace_bytes(v->B, v->C, v->J, v->R));
-    L.packed = packed_state(v) != nullptr;
+    L.wpw = worlds_per_wave(v->n_worlds, workspace_bytes(L.B, L.C, L.J, L.R));
+    L.packed = !L.full_rows && packed_state(v) != nullptr;
 }
 
 // Words of constraint and task rows a launch over `state` uses: per world C contact rows and J joint rows, in tiles of
@@ -687,6 +711,8 @@ static int launch_step(const GoiModel* M, const GoiStateView* state, const GoiSe
     const bool island = L.B == kIslandB && L.C == kIslandC && L.J == kIslandJ && L.R == kIslandR &&
                         L.wpw == kIslandS && M->d.B == kIslandB && M->d.J == kIslandJ && M->d.R == kIslandR &&
                         L.packed && plain && !dbg;
+    g_last_launch = GoiLaunchInfo{L.wpw, grid, (int32_t)lds,
+                                  rig ? GOI_KERNEL_RIG : island ? GOI_KERNEL_ISLAND : GOI_KERNEL_GENERIC};
     if (rig) {
         const hipError_t e = launch_rig_step(M->d, L, n_steps != 1, plain, g, lds, st);
         if (e != hipSuccess) return fail(GOI_E_HIP, std::string("launch_rig_step: ") + hipGetErrorString(e));
@@ -746,6 +772,7 @@ int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiS
     rc = stream_rows(M, state, st, &L.scratch);
     if (rc != GOI_OK) return rc;
     const size_t lds = block_lds_bytes(L);
+    g_last_launch = GoiLaunchInfo{L.wpw, grid, (int32_t)lds, GOI_KERNEL_COLLIDE};
     hipLaunchKernelGGL(k_collide, dim3(grid), dim3(kBlock), lds, st, M->d, L, 0);
     HIP_TRY(hipGetLastError());
     return GOI_OK;
@@ -784,6 +811,12 @@ int32_t goi_apply_motor_actions(const float* actions, float* motor_speed, float*
 int32_t goi_packed_layout(int32_t B, int32_t C, int32_t J, int32_t R, int32_t* words) {
     if (B < 0 || C < 0 || J < 0 || R < 0 || !words) return fail(GOI_E_ARG, "goi_packed_layout: bad arguments");
     for (int l = 0; l <= GOI_NUM_LEAVES; ++l) words[l] = packed_word(l, B, C, J, R);
+    return GOI_OK;
+}
+
+int32_t goi_last_launch(GoiLaunchInfo* out) {
+    if (!out) return fail(GOI_E_ARG, "goi_last_launch: null argument");
+    *out = g_last_launch;
     return GOI_OK;
 }
 

@@ -25,7 +25,8 @@
  * read-only after creation; its one mutable part is the scratch memory of goi_step, goi_step_n and goi_collide (the
  * constraint and task rows), which it keeps per stream: one device buffer per stream handle, allocated on that
  * stream's first call and replaced by a larger one when a larger batch arrives on that stream (the old buffer is
- * freed after that stream's earlier work has finished). Calls on different streams therefore never share rows, and
+ * freed after that stream's earlier work has finished). The buffers stay until goi_model_release_rows or
+ * goi_model_destroy, so each stream a handle was used on holds one. Calls on different streams therefore never share rows, and
  * calls on one stream are ordered by it. A mutex in the handle covers the table from lookup through launch. A state
  * must not be stepped by two calls at once. goi_model_destroy waits for the device to finish (hipDeviceSynchronize)
  * before freeing, and must not overlap other calls on the same handle.
@@ -39,7 +40,7 @@
 extern "C" {
 #endif
 
-#define GOI_ABI_VERSION 4
+#define GOI_ABI_VERSION 5
 
 #define GOI_OK 0
 #define GOI_E_ARG (-1)
@@ -217,7 +218,12 @@ typedef struct GoiModelDesc {
     const int32_t* edge_flags;     /* [F] or NULL (no ghost vertices) */
 } GoiModelDesc;
 
-/* A batch of States on the device: GOI_NUM_LEAVES device pointers, worlds-minor with the given pitch (>= n). */
+/* A batch of States on the device: GOI_NUM_LEAVES device pointers, worlds-minor with the given pitch (>= n). R is the
+ * fixture rows of the fixture leaves: the model's non-static fixtures (the compact layout) or all F of its fixtures
+ * (the full layout that WorldDef.build returns, world.py:98-101; a reader tells the two apart by the row count, as
+ * world.py:400-403 does). In the full layout the step reads and writes only the non-static fixtures' rows: the
+ * static rows stay as they are, their values taken from the model, which must have been made from them
+ * (compact_model checks that they agree in every world). */
 typedef struct GoiStateView {
     int32_t n_worlds;
     int32_t pitch;
@@ -254,6 +260,14 @@ int32_t goi_abi_version(void);
 int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, void* hip_stream, GoiModel** out);
 int32_t goi_model_destroy(GoiModel* model);
 
+/* Frees the handle's per-stream constraint and task rows (goi_step, goi_step_n and goi_collide keep one buffer per
+ * stream handle they were called on, (C * 54 + J * 57) * (pitch + 64) 4-byte words each: about 153 MB for 16,384
+ * worlds of the 4-body rig, until goi_model_destroy). A caller that steps on many short-lived or pooled streams calls
+ * it to return that memory; the next call on a stream allocates its buffer again. Waits for the model's device to
+ * finish first (hipDeviceSynchronize). Must not overlap other calls on the same handle. No counterpart in the
+ * reference. */
+int32_t goi_model_release_rows(GoiModel* model);
+
 /* One b2World::Step (step.py:28-47) of every world in place. dt in seconds. debug may be NULL. */
 int32_t goi_step(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
                  void* hip_stream, const GoiDebug* debug);
@@ -272,7 +286,8 @@ int32_t goi_step_n(const GoiModel* model, const GoiStateView* state, const GoiSe
  * the handle's per-stream buffers. No counterpart in the reference: it is for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It calls no hipMalloc,
  * hipFree or allocating library routine. A batch needing more than the maximum, (C * 54 + J * 57) * (pitch + 64)
- * words (about 17,600 worlds of the 4-body rig with 32 slots), returns GOI_E_UNSUPPORTED. Every call on a device
+ * words (about 14,300 worlds of the 4-body rig with its 40 slots, so the 16,384-world benchmark batch is refused),
+ * returns GOI_E_UNSUPPORTED before anything is launched. Every call on a device
  * shares that device's array: calls that overlap on one device (on different streams, or from different threads)
  * race and must not be made. */
 int32_t goi_step_n_noalloc(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
@@ -312,6 +327,23 @@ int32_t goi_sincos(const float* x, float* s, float* c, int32_t n, void* hip_stre
  * State is a pytree of separate arrays): it describes this library's fast layout, for callers that allocate States.
  * Returns GOI_E_ARG for a negative capacity or a null `words`. */
 int32_t goi_packed_layout(int32_t B, int32_t C, int32_t J, int32_t R, int32_t* words);
+
+/* The shape of the calling thread's last launch of goi_step, goi_step_n, goi_step_n_noalloc or goi_collide: the
+ * worlds each 64-lane wavefront stepped (GOI_WORLDS_PER_WAVE may ask for another count; the library lowers a request
+ * whose workspaces do not fit a block's LDS), the blocks launched, the dynamic LDS of a block in bytes and the kernel
+ * instance that ran. No counterpart in the reference: it is for tests and profiling. Returns GOI_E_ARG for a null
+ * `out`; all zero before the thread's first launch. */
+#define GOI_KERNEL_GENERIC 1 /* the step for any dimensions */
+#define GOI_KERNEL_RIG 2     /* the step compiled for the 4-body rig (5 bodies, 40 slots, 3 joints, 4 rows) */
+#define GOI_KERNEL_ISLAND 3  /* the step compiled for the rig with 12 boxes (17 bodies, 128 slots, 3 joints, 16 rows) */
+#define GOI_KERNEL_COLLIDE 4 /* goi_collide's kernel */
+typedef struct GoiLaunchInfo {
+    int32_t worlds_per_wave;
+    int32_t blocks;
+    int32_t lds_bytes;
+    int32_t kernel;
+} GoiLaunchInfo;
+int32_t goi_last_launch(GoiLaunchInfo* out);
 
 /* Thread-local message of the last failed call ("" if none). */
 const char* goi_last_error(void);

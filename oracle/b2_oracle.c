@@ -158,6 +158,8 @@ typedef struct {
     const GoiModelDesc* m;
     const GoiSettings* s;
     float dt;
+    int compact; /* the State holds only the non-static fixture rows (world.py:400-403: a compact Model and fewer rows
+                    than fixtures); otherwise every fixture has its row, whatever the Model's layout */
 } Ctx;
 
 /* body transform, sweep pieces */
@@ -176,7 +178,7 @@ static inline void wake(W* w, int b) {
 /* fixture accessors in either layout (world.py:413-434) */
 static inline const float* fat_of(const Ctx* x, const W* w, int f) {
     const GoiModelDesc* m = x->m;
-    if (m->fixture_slot) {
+    if (x->compact) {
         int r = m->fixture_slot[f];
         return r >= 0 ? w->f_fat + 4 * r : m->static_fat + 4 * f;
     }
@@ -184,7 +186,7 @@ static inline const float* fat_of(const Ctx* x, const W* w, int f) {
 }
 static inline float friction_of(const Ctx* x, const W* w, int f) {
     const GoiModelDesc* m = x->m;
-    if (m->fixture_slot) {
+    if (x->compact) {
         int r = m->fixture_slot[f];
         return r >= 0 ? w->f_friction[r] : m->static_friction[f];
     }
@@ -192,7 +194,7 @@ static inline float friction_of(const Ctx* x, const W* w, int f) {
 }
 static inline float restitution_of(const Ctx* x, const W* w, int f) {
     const GoiModelDesc* m = x->m;
-    if (m->fixture_slot) {
+    if (x->compact) {
         int r = m->fixture_slot[f];
         return r >= 0 ? w->f_restitution[r] : m->static_restitution[f];
     }
@@ -792,7 +794,7 @@ static void synchronize_fixtures(const Ctx* x, W* w, const uint8_t* moved) {
     for (int f = 0; f < m->F; ++f) {
         int b = m->fixture_body[f];
         if (!moved[b]) continue;
-        int row = m->fixture_slot ? m->fixture_slot[f] : f;
+        int row = x->compact ? m->fixture_slot[f] : f;
         if (row < 0) continue;
         Xf x1;
         x1.q = rot_of(w->b_a0[b]);
@@ -2508,7 +2510,7 @@ static void bind_world(W* w, void* const* lv, int B, int C, int R, int J, size_t
  * are worlds-minor with pitch n. Returns 0. */
 int oracle_step(const GoiModelDesc* m, void* const* leaves, int32_t n, int32_t B, int32_t C, int32_t R, int32_t J,
                 const GoiSettings* s, float dt, int32_t n_threads, GoiDebug* dbg) {
-    Ctx x = {m, s, dt};
+    Ctx x = {m, s, dt, m->fixture_slot != NULL && R != m->F};
 #ifdef _OPENMP
     int nt = n_threads > 0 ? n_threads : omp_get_max_threads();
 #pragma omp parallel num_threads(nt)
@@ -2533,7 +2535,7 @@ int oracle_step(const GoiModelDesc* m, void* const* leaves, int32_t n, int32_t B
 /* Broadphase + narrowphase only (config 2): start-of-step FindNewContacts where new_fixture, then Collide. */
 int oracle_collide(const GoiModelDesc* m, void* const* leaves, int32_t n, int32_t B, int32_t C, int32_t R, int32_t J,
                    const GoiSettings* s, int32_t n_threads) {
-    Ctx x = {m, s, 0.0f};
+    Ctx x = {m, s, 0.0f, m->fixture_slot != NULL && R != m->F};
 #ifdef _OPENMP
     int nt = n_threads > 0 ? n_threads : omp_get_max_threads();
 #pragma omp parallel num_threads(nt)

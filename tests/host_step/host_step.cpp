@@ -245,6 +245,15 @@ int main(int argc, char** argv) {
         std::fflush(stdout);
     }
     goi_model_destroy(model);
+    // the regime the run reached: contacts dropped by full tables (overflow) and TOI events of the last step
+    long overflow = 0, events = 0;
+    const int32_t* ovf = (const int32_t*)leaves[leaf_index("overflow")].ref;
+    const int32_t* ev = (const int32_t*)leaves[leaf_index("toi.events")].ref;
+    for (int w = 0; w < n; ++w) {
+        overflow += ovf[w];
+        events += ev[w];
+    }
+    std::printf("overflow %ld events %ld\n", overflow, events);
     std::printf("PASS %d worlds, %d steps, %ld elements compared (%s, %s State)\n", n, n_steps, compared, mode.c_str(),
                 packed ? "packed" : "one buffer per leaf");
     return 0;

@@ -40,3 +40,19 @@ def test_model_shared_by_two_streams(oracle):
     for ref, dev in ((ref_a, dev_a), (ref_b0, dev_b0), (ref_b1, dev_b1)):
         bad = leaf_mismatches(ref, b2.layout.to_host(dev))
         assert bad == [], bad[:4]
+
+
+def test_release_rows_between_steps(oracle):
+    """goi_model_release_rows frees the handle's per-stream rows; the next step allocates them again and the
+    results stay bit-exact."""
+    step_mod = __import__("importlib").import_module("getting-over-it-rl_amd.box2d.step")
+    s, m, st, cfg = b2.scenes.make_config(4, 512)
+    dev = b2.layout.to_device(st, "cuda")
+    ref = oracle.copy(st)
+    dm = step_mod.device_model(m, dev.contacts.pair.shape[-1], dev.contacts.pair.device, dev)
+    for k in range(6):
+        b2.step_(m, dev, s, cfg.dt)
+        oracle.step_(m, ref, s, cfg.dt)
+        if k % 2 == 0:
+            b2._abi.check(dm.L.goi_model_release_rows(dm.handle), dm.L)
+    assert leaf_mismatches(ref, b2.layout.to_host(dev)) == []

@@ -322,6 +322,10 @@ def test_bad_arguments_fail_before_the_device():
     assert L.goi_sincos(None, None, None, -1, None) == A.GOI_E_ARG
     assert L.goi_sincos(None, None, None, 0, None) == A.GOI_OK
     assert L.goi_model_destroy(None) == A.GOI_OK
+    assert L.goi_model_release_rows(None) == A.GOI_E_ARG
+    assert L.goi_last_launch(None) == A.GOI_E_ARG
+    info = A.GoiLaunchInfo()
+    assert L.goi_last_launch(ctypes.byref(info)) == A.GOI_OK and info.kernel == 0  # nothing launched here
 
 
 def test_host_state_is_rejected():

@@ -118,6 +118,20 @@ def test_config4_sanitized(host_step, tmp_path, packed, edges):
     assert all(("k_step_fixed" in ln) == packed for ln in launches), launches[:2]
 
 
+@pytest.mark.parametrize("capacity", [6, 10])
+def test_contact_table_overflow_sanitized(host_step, tmp_path, capacity):
+    """Config 4 with 6 or 10 contact slots a world: FindNewContacts drops pairs (overflow > 0 in many worlds) and
+    those worlds keep full candidate searches; the general kernel (the fixed rig instance needs 40 slots)."""
+    s, m, st, cfg = b2.scenes.make_config(4, 64, capacity=capacity)
+    rng = np.random.default_rng(31)
+    acts = np.stack([b2.scenes.actions(rng, 64) for _ in range(40)])
+    p = tmp_path / "scn.bin"
+    write_scenario(p, m, st, s, cfg.dt, 40, True, acts)
+    r = run(host_step, p, "step")
+    check(r)
+    assert "overflow" in r.stdout and "overflow 0 " not in r.stdout, r.stdout[-500:]
+
+
 @pytest.mark.parametrize("mode", ["step_n:4", "noalloc:5"])
 def test_multi_step_launches_sanitized(host_step, tmp_path, mode):
     """goi_step_n and goi_step_n_noalloc on the rig's packed State (no actions between the steps of a launch)."""
@@ -157,3 +171,26 @@ def test_planted_mismatch_is_reported(host_step, tmp_path):
     write_scenario(p, m, st, s, dt, 3, True, acts)
     r = run(host_step, p, "step", plant=True)
     assert r.returncode == 1 and "MISMATCH after step 1" in r.stdout, r.stdout + r.stderr[-3000:]
+
+
+@pytest.mark.parametrize("case", ["config4", "joints", "circles"])
+def test_full_layout_state_sanitized(host_step, tmp_path, case):
+    """States in the full fixture layout (a row per fixture, as WorldDef.build returns them) with the compact Model:
+    the step addresses the non-static rows at their fixtures' rows and leaves the static rows alone. config4's
+    non-static fixtures are the last rows; in "joints" and "circles" static fixtures sit between them."""
+    if case == "config4":
+        s, m, st, cfg = b2.scenes.make_config(4, 32)
+        st, dt, steps = wd.expand_state(m, st), cfg.dt, 40
+        rng = np.random.default_rng(5)
+        acts = np.stack([b2.scenes.actions(rng, 32) for _ in range(steps)])
+    else:
+        s, m, st = scene_defs.build_test_scene(case, iterations=(8, 3))
+        st, dt, steps, acts = wd.expand_state(m, perturbed(st, 16)), 1.0 / 60.0, 60, None
+    B, R, J, C = wd.dims(st)
+    assert R == m.fixture_body.shape[0] > int((np.asarray(m.fixture_slot) >= 0).sum())
+    p = tmp_path / "scn.bin"
+    write_scenario(p, m, st, s, dt, steps, True, acts)
+    r = run(host_step, p, "step")
+    check(r)
+    launches = [ln for ln in r.stderr.splitlines() if ln.startswith("launch ") and "k_step" in ln]
+    assert launches and not any("k_step_fixed" in ln for ln in launches)

@@ -31,7 +31,12 @@ def _call(fn, m, dev, s, dt, n_steps):
                              ctypes.c_int32(n_steps), ctypes.c_void_p(stream), None)
 
 
-def test_noalloc_equals_step_n_twice():
+@pytest.mark.parametrize("wpw,kernel", [(None, "generic"), ("8", "rig")])
+def test_noalloc_equals_step_n_twice(monkeypatch, wpw, kernel):
+    """The default wave size (1 world a wave at these batch sizes: the generic kernel) and 8 worlds a wave (the
+    packed rig State then runs the instance compiled for the rig, the headline workload's kernel)."""
+    if wpw is not None:
+        monkeypatch.setenv("GOI_WORLDS_PER_WAVE", wpw)
     s, m, st, cfg = b2.scenes.make_config(4, 1536)
     A = b2._abi
     for n, n_steps in ((1536, 3), (384, 2)):
@@ -40,6 +45,8 @@ def test_noalloc_equals_step_n_twice():
         got = b2.layout.to_device(part, "cuda")
         A.check(_call("goi_step_n", m, want, s, cfg.dt, n_steps))
         A.check(_call("goi_step_n_noalloc", m, got, s, cfg.dt, n_steps))
+        info = b2.last_launch()
+        assert info["kernel"] == kernel and (wpw is None or info["worlds_per_wave"] == int(wpw)), info
         torch.cuda.synchronize()
         bad = leaf_mismatches(b2.layout.to_host(want), b2.layout.to_host(got))
         assert bad == [], (n, bad[:4])
@@ -47,7 +54,9 @@ def test_noalloc_equals_step_n_twice():
 
 
 def test_noalloc_refuses_a_batch_above_its_maximum():
-    s, m, st, cfg = b2.scenes.make_config(4, 18000)
+    """The headline batch (16,384 rig worlds with 40 slots) needs (40 * 54 + 3 * 57) * (16,384 + 64) words of rows,
+    more than the static array's 2^25: refused before anything runs."""
+    s, m, st, cfg = b2.scenes.make_config(4, 16384)
     dev = b2.layout.to_device(st, "cuda")
     torch.cuda.synchronize()
     before = b2.layout.to_host(dev)
