@@ -697,6 +697,9 @@ static int launch_step(const GoiModel* M, const GoiStateView* state, const GoiSe
     fill_launch(L, M, state, settings, dt);
     L.scratch = rows;
     L.n_steps = n_steps;
+#ifdef GOI_HOST_BUILD
+    goi_host_poison(rows, scratch_words(state) * sizeof(uint32_t));  // no launch may read rows an earlier one wrote
+#endif
     if (debug) L.dbg = *debug;
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
     const size_t lds = block_lds_bytes(L);
@@ -771,6 +774,9 @@ int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiS
     const int grid = (state->n_worlds + L.wpw - 1) / L.wpw;
     rc = stream_rows(M, state, st, &L.scratch);
     if (rc != GOI_OK) return rc;
+#ifdef GOI_HOST_BUILD
+    goi_host_poison(L.scratch, scratch_words(state) * sizeof(uint32_t));
+#endif
     const size_t lds = block_lds_bytes(L);
     g_last_launch = GoiLaunchInfo{L.wpw, grid, (int32_t)lds, GOI_KERNEL_COLLIDE};
     hipLaunchKernelGGL(k_collide, dim3(grid), dim3(kBlock), lds, st, M->d, L, 0);

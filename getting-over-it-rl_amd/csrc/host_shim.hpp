@@ -93,8 +93,26 @@ inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) { *v 
 #define HIP_SYMBOL(x) (x)
 template <typename T> inline hipError_t hipGetSymbolAddress(void** p, T& sym) { *p = (void*)&sym; return hipSuccess; }
 
+// The word the host build fills scratch memory with before each launch (every block's dynamic LDS, and the constraint
+// and task rows through goi_host_poison), so that a read of a word the launch has not written yields it instead of a
+// leftover of an earlier launch: GOI_HOST_POISON = "nan" (a quiet NaN with payload 0xdead), an integer (say 8), or
+// unset (zeros). A result that depends on such a read then differs from the oracle's.
+inline bool goi_host_poison_word(int* word) {
+    const char* e = std::getenv("GOI_HOST_POISON");
+    if (!e || !*e) return false;
+    *word = std::strcmp(e, "nan") == 0 ? 0x7fc0dead : std::atoi(e);
+    return true;
+}
+inline void goi_host_poison(void* p, size_t bytes) {
+    int word = 0;
+    if (!p || !goi_host_poison_word(&word)) return;
+    int* q = static_cast<int*>(p);
+    for (size_t i = 0; i < bytes / sizeof(int); ++i) q[i] = word;
+}
+
 // a launch: the blocks one after another, the threads of a block one after another, each block with its own
-// exactly-sized dynamic LDS; with GOI_HOST_LAUNCH_LOG set, each launch prints the kernel's name to stderr
+// exactly-sized dynamic LDS (poisoned, see above); with GOI_HOST_LAUNCH_LOG set, each launch prints the kernel's name
+// to stderr
 template <typename K, typename... A>
 inline void goi_host_launch(const char* name, K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t, A... args) {
     if (std::getenv("GOI_HOST_LAUNCH_LOG")) std::fprintf(stderr, "launch %s grid %u\n", name, grid.x);
@@ -102,7 +120,9 @@ inline void goi_host_launch(const char* name, K kernel, dim3 grid, dim3 block, s
     blockDim = GoiHostIdx{block.x, block.y, block.z};
     for (unsigned by = 0; by < grid.y; ++by)
         for (unsigned bx = 0; bx < grid.x; ++bx) {
-            std::vector<int> mem((lds + sizeof(int) - 1) / sizeof(int));
+            int fill = 0;
+            goi_host_poison_word(&fill);
+            std::vector<int> mem((lds + sizeof(int) - 1) / sizeof(int), fill);
             goi_host_lds = mem.empty() ? nullptr : mem.data();
             blockIdx = GoiHostIdx{bx, by, 0};
             for (unsigned t = 0; t < block.x; ++t) {

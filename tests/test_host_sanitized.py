@@ -83,9 +83,12 @@ def write_scenario(path, model, state, settings, dt, steps, packed, actions=None
             f.write(np.ascontiguousarray(actions, dtype=F32).tobytes())
 
 
-def run(exe, scenario, mode, plant=False):
+def run(exe, scenario, mode, plant=False, poison="nan"):
+    """host_step on a scenario file. Every launch first fills each block's LDS and the constraint and task rows with
+    `poison` (host_shim.hpp): a quiet NaN by default, so that a read of a word the launch did not write shows as a
+    mismatch instead of passing on a value an earlier launch left."""
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:halt_on_error=1",
-               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1", GOI_HOST_LAUNCH_LOG="1")
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1", GOI_HOST_LAUNCH_LOG="1", GOI_HOST_POISON=poison)
     cmd = [str(exe), str(scenario), mode] + (["plant"] if plant else [])
     return subprocess.run(cmd, capture_output=True, text=True, env=env, timeout=600)
 
@@ -116,6 +119,18 @@ def test_config4_sanitized(host_step, tmp_path, packed, edges):
     launches = [ln for ln in r.stderr.splitlines() if ln.startswith("launch ") and "k_step" in ln]
     assert len(launches) == 60
     assert all(("k_step_fixed" in ln) == packed for ln in launches), launches[:2]
+
+
+@pytest.mark.parametrize("poison", ["8", "-1", "0"])
+def test_poisoned_scratch_sanitized(host_step, tmp_path, poison):
+    """The benchmark rig (packed: the fixed instance) and the general kernel with the LDS workspaces and rows filled
+    with small integers instead of NaN before every launch (8 as a body or slot index, -1 as an empty slot, 0): the
+    same results, so no pass reads a word its launch has not written."""
+    m, st, s, dt, acts = config_case(4, 64, 30)
+    for packed in (True, False):
+        p = tmp_path / f"scn{int(packed)}.bin"
+        write_scenario(p, m, st, s, dt, 30, packed, acts)
+        check(run(host_step, p, "step", poison=poison))
 
 
 @pytest.mark.parametrize("capacity", [6, 10])
