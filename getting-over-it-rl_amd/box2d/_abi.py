@@ -61,7 +61,12 @@ DEBUG_TOI_EVENTS, DEBUG_TOI_ROWS = 8, 32  # GOI_DEBUG_TOI_EVENTS, GOI_DEBUG_TOI_
 
 class GoiDebug(ctypes.Structure):
     _fields_ = [("body_island", _P), ("contact_island", _P), ("contact_order", _P), ("n_islands", _P),
-                ("toi_event_slot", _P), ("toi_event_alpha", _P), ("toi_event_island", _P), ("toi_island_rows", _P)]
+                ("toi_event_slot", _P), ("toi_event_alpha", _P), ("toi_event_island", _P), ("toi_island_rows", _P),
+                ("status", _P)]
+
+
+# GoiDebug.status bits (GOI_STATUS_*)
+STATUS_OVERFLOW, STATUS_NONFINITE, STATUS_TOI_CAPPED, STATUS_TOI_SKIPPED = 1, 2, 4, 8
 
 
 class GoiLaunchInfo(ctypes.Structure):

@@ -386,6 +386,12 @@ def to_world(geometry, snap, settings=None, contact_capacity=None):
     geo_list = geometry.bodies  # list order
     order = list(range(len(geo_list)))[::-1]  # creation order
     snap_of_rb = {b.rb: b for b in snap.bodies if b.rb >= 0}
+    # every moving body of the snapshot must have its geometry (a body created after the maps were built, such as
+    # the gift at the list's head, NativeRecord.cs:98, has none and would otherwise vanish from the world)
+    geo_rbs = {g.rb for g in geo_list if g.rb >= 0}
+    for nb in snap.bodies:
+        if nb.type != wd.STATIC and (nb.rb < 0 or nb.rb not in geo_rbs):
+            raise RecordError(f"non-static snapshot body (rigidbody {nb.rb}) has no entry in the geometry")
     d = wd.WorldDef(settings)
     body_of_pos, body_of_rb, ground, fixture_of = {}, {}, [], {}
     for pos in order:

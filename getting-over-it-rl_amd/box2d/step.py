@@ -194,7 +194,8 @@ def debug_shapes(n, dims):
     B, _, _, C = dims
     E, Rw = _abi.DEBUG_TOI_EVENTS, _abi.DEBUG_TOI_ROWS
     return dict(body_island=(B, n), contact_island=(C, n), contact_order=(C, n), n_islands=(n,),
-                toi_event_slot=(E, n), toi_event_alpha=(E, n), toi_event_island=(E, n), toi_island_rows=(E * Rw, n))
+                toi_event_slot=(E, n), toi_event_alpha=(E, n), toi_event_island=(E, n), toi_island_rows=(E * Rw, n),
+                status=(n,))
 
 
 def make_debug(n, dims, device="cuda", pitch=None):

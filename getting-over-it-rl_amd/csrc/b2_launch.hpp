@@ -142,6 +142,7 @@ __device__ __forceinline__ void step_worlds(const DModel& m, const Launch& L, in
     const LaneMap& lm = v.lm;
     const bool valid = lm.valid;
     const World& W = v.W;
+    const int overflow0 = valid && L.dbg.status ? W.i32(GOI_S_OVERFLOW, 0) : 0;
     build_order_block(v.bc);
     if (valid) {
         if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
@@ -152,8 +153,9 @@ __device__ __forceinline__ void step_worlds(const DModel& m, const Launch& L, in
         solve_world(m, W, v.bd, v.CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
         clear_toi_trace(W, L.dbg);
     }
+    bool capped = false;
     if (L.s.continuous_physics)
-        solve_toi_world<kOpaqueToi>(m, W, v.bd, v.CR, L.s, L.dt, valid, lm.leader, v.co, v.bc, L.dbg);
+        capped = solve_toi_world<kOpaqueToi>(m, W, v.bd, v.CR, L.s, L.dt, valid, lm.leader, v.co, v.bc, L.dbg);
     if (valid) {
         const float dt = L.dt;
         if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
@@ -162,6 +164,7 @@ __device__ __forceinline__ void step_worlds(const DModel& m, const Launch& L, in
                 W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
                 W.f(GOI_B_TORQUE, b) = 0.0f;
             }
+        if (L.dbg.status) L.dbg.status[W.w] = step_status(W, overflow0, capped, dt, L.s);
     }
 }
 
@@ -192,6 +195,7 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
         const Rows CR = contact_rows(L, w0, valid ? lm.wl : 0);
         const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
         load_mirror_block(m, bc);
+        const int overflow0 = valid && L.dbg.status ? W.i32(GOI_S_OVERFLOW, 0) : 0;
         for (int step = 0; step < 1; ++step) {
             build_order_block(bc);
             if (valid) {
@@ -203,8 +207,9 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
                 solve_world(m, W, bd, CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
                 clear_toi_trace(W, L.dbg);
             }
+            bool capped = false;
             if (L.s.continuous_physics)
-                solve_toi_world<kOpaqueToi>(m, W, bd, CR, L.s, L.dt, valid, lm.leader, co, bc, L.dbg);
+                capped = solve_toi_world<kOpaqueToi>(m, W, bd, CR, L.s, L.dt, valid, lm.leader, co, bc, L.dbg);
             if (valid) {
                 const float dt = L.dt;
                 if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
@@ -213,6 +218,7 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
                         W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
                         W.f(GOI_B_TORQUE, b) = 0.0f;
                     }
+                if (L.dbg.status) L.dbg.status[W.w] = step_status(W, overflow0, capped, dt, L.s);
             }
         }
         store_mirror_block(bc);

@@ -22,6 +22,7 @@ namespace goi {
 
 constexpr float kEps = 1.1920928955078125e-7f;       // b2_epsilon
 constexpr float kMaxFloat = 3.40282346638528859812e+38f;  // b2_maxFloat
+constexpr float kNaN = __builtin_nanf("");
 constexpr float kPi = 3.14159265359f;                // b2_pi
 constexpr int kMaxSubSteps = 8;
 constexpr int kMaxToiContacts = 32;

@@ -307,6 +307,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
     // the fat boxes of all rows into the workspace; the queried rows on active bodies and their union box
     unsigned long long rows = 0ull;
     float4 U = make_float4(kMaxFloat, kMaxFloat, -kMaxFloat, -kMaxFloat);
+    bool nan_query = false;
     for (int r = 0; r < m.R; ++r) {
         const int fr = 4 * W.frow(r);
         const float4 q = make_float4(W.f(GOI_F_FAT, fr), W.f(GOI_F_FAT, fr + 1), W.f(GOI_F_FAT, fr + 2),
@@ -315,9 +316,15 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         if (!((query_rows >> r) & 1ull) || !W.active(m.row[r].body)) continue;
         rows |= 1ull << r;
         U.x = fminf(U.x, q.x); U.y = fminf(U.y, q.y); U.z = fmaxf(U.z, q.z); U.w = fmaxf(U.w, q.w);
+        nan_query |= q.x != q.x || q.y != q.y || q.z != q.z || q.w != q.w;
     }
+    // b2TestOverlap finds a box with a NaN coordinate overlapping every box, so such a row meets every static leaf:
+    // a NaN union box then passes every node and leaf test below (and the row's own tests decide)
+    if (nan_query) U = make_float4(kNaN, kNaN, kNaN, kNaN);
     // the static tree, depth first: the lane group tests a node's 8 child boxes together against the union box; per
-    // level, the node and the mask of its overlapping children not yet visited (registers, selected by level)
+    // level, the node and the mask of its overlapping children not yet visited (registers, selected by level). An
+    // unused child slot holds an empty box (lower > upper), which a NaN union box would pass: the hit needs a
+    // non-empty box too (the Model's static boxes are finite, checked at goi_model_create).
     if (rows && m.n_wnodes > 0) {
         int path[kWideDepth];
         unsigned masks[kWideDepth];
@@ -325,8 +332,10 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         for (int l = 0; l < kWideDepth; ++l) { path[l] = 0; masks[l] = 0u; }
         const auto children = [&](int nd) {
             unsigned hit = 0u;
-            for (int j = W.sub; j < 8; j += W.G)
-                if (overlap(U, m.wnode[nd].box[j])) hit |= 1u << j;
+            for (int j = W.sub; j < 8; j += W.G) {
+                const float4 b = m.wnode[nd].box[j];
+                if (overlap(U, b) && b.x <= b.z) hit |= 1u << j;
+            }
             return group_or(W.grp(), hit);
         };
         masks[0] = children(0);

@@ -586,14 +586,16 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
 // see through, so that no per-lane address is held (spilled) from one iteration to the next. The island instance's
 // spilled registers go (816 to 16 B of scratch per lane, 3.5% faster), and most of the generic kernel's (960 to 160 B,
 // 8% faster on the rig at 4 worlds per wave); the rig instance, with few spills, measured slower with it.
+// Returns true when the world stopped at max_events with another event pending.
 template <bool kOpaqueViews = false>
-GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
+GOI_D bool solve_toi_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
                            float dt, bool valid, bool leader, const Coop& co, const BlockCopy& bc,
                            const GoiDebug& dbg) {
-    if (W.C == 0 || m.P == 0) return;
-    if (s.unity_toi && !m.any_toi_body) return;
+    if (W.C == 0 || m.P == 0) return false;
+    if (s.unity_toi && !m.any_toi_body) return false;
     reset_toi_block(bc);
     int events = 0;
+    bool capped = false;
     if (dt > 0.0f) {
         const int max_events = s.max_events >= 0 ? s.max_events : W.C * (kMaxSubSteps + 1) + 8;
         int slot = -1;
@@ -631,9 +633,28 @@ GOI_D void solve_toi_world(const DModel& m, const World& W, const Bodies& bd, co
                 found = act && toi_search_pick(W, s, slot, alpha);
             }
         }
+        capped = found && events >= max_events;
     }
     if (valid) W.i32(GOI_T_EVENTS, 0) = events;
     store_toi_block(bc);
+    return capped;
+}
+
+// GoiDebug::status of a world after its step: overflow0 is State.overflow before the step, capped what
+// solve_toi_world returned.
+GOI_D int step_status(const World& W, int overflow0, bool capped, float dt, const GoiSettings& s) {
+    int st = W.i32(GOI_S_OVERFLOW, 0) != overflow0 ? GOI_STATUS_OVERFLOW : 0;
+    bool finite = true;
+    for (int b = 0; b < W.B; ++b) {
+        const V2 c = W.v2(GOI_B_C, b), v = W.v2(GOI_B_V, b);
+        const float a = W.f(GOI_B_A, b), w = W.f(GOI_B_W, b);
+        finite = finite && isfinite(c.x) && isfinite(c.y) && isfinite(a) && isfinite(v.x) && isfinite(v.y) &&
+                 isfinite(w);
+    }
+    if (!finite) st |= GOI_STATUS_NONFINITE;
+    if (capped) st |= GOI_STATUS_TOI_CAPPED;
+    if (s.continuous_physics && !(dt > 0.0f)) st |= GOI_STATUS_TOI_SKIPPED;
+    return st;
 }
 
 }  // namespace goi

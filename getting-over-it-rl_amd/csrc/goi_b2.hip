@@ -14,6 +14,7 @@
 // shared by every world and read through L2.
 #include <algorithm>
 #include <atomic>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -318,9 +319,16 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
             return fail(GOI_E_UNSUPPORTED, "goi_model_create: unknown joint type");
     }
     bool any_edge = false;
-    for (int f = 0; f < F; ++f)
-        if (desc->fixture_slot[f] < 0 && (!desc->static_friction || !desc->static_restitution))
+    for (int f = 0; f < F; ++f) {
+        if (desc->fixture_slot[f] >= 0) continue;
+        if (!desc->static_friction || !desc->static_restitution)
             return fail(GOI_E_ARG, "goi_model_create: static fixtures need their friction and restitution");
+        const float* b = desc->static_fat + 4 * f;
+        // the static tree's bounds and its empty child slots (lower > upper) need finite, ordered boxes
+        if (!(std::isfinite(b[0]) && std::isfinite(b[1]) && std::isfinite(b[2]) && std::isfinite(b[3]) &&
+              b[0] <= b[2] && b[1] <= b[3]))
+            return fail(GOI_E_ARG, "goi_model_create: a static fixture's fat AABB is not finite and ordered");
+    }
     for (int f = 0; f < F; ++f) {
         const int t = desc->shape_type[f], c = desc->count[f];
         if ((t != GOI_CIRCLE && t != GOI_POLYGON && t != GOI_EDGE) || c < 1 || c > GOI_MAX_POLY)

@@ -45,6 +45,7 @@ inline int __float_as_int(float f) { int u; std::memcpy(&u, &f, 4); return u; }
 inline float __int_as_float(int u) { float f; std::memcpy(&f, &u, 4); return f; }
 inline int __popcll(unsigned long long x) { return __builtin_popcountll(x); }
 using std::fabs;
+using std::isfinite;
 using std::fma;
 using std::rint;
 using std::sqrt;

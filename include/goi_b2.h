@@ -247,7 +247,15 @@ typedef struct GoiDebug {
     int32_t* toi_event_alpha;  /* [E] the bits of its float minAlpha */
     int32_t* toi_event_island; /* [E] island contacts | island bodies << 16; 0 when the contact stopped touching */
     int32_t* toi_island_rows;  /* [E, 32] the island's contact slots in walk order (the event's contact first), -1 padded */
+    int32_t* status;           /* [] the world's GOI_STATUS_* bits for the step (below) */
 } GoiDebug;
+
+/* GoiDebug::status bits, the failure counters of a step as one word per world (the reference keeps them as State
+ * counters and bench checks: world.py:154, 173; toi.py:838-842; bench_gpu.py:135-136). */
+#define GOI_STATUS_OVERFLOW 1    /* FindNewContacts dropped a pair on a full contact table (State.overflow grew) */
+#define GOI_STATUS_NONFINITE 2   /* a body's position, angle or velocity is not finite after the step */
+#define GOI_STATUS_TOI_CAPPED 4  /* SolveTOI stopped at max_events with another event pending (toi.py:838-842) */
+#define GOI_STATUS_TOI_SKIPPED 8 /* continuous physics on but dt <= 0, so SolveTOI did not run (toi.py:841) */
 
 typedef struct GoiModel GoiModel;
 

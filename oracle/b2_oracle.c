@@ -2414,14 +2414,15 @@ static void toi_event(const Ctx* x, W* w, Work* k, int min_slot, float min_alpha
     }
 }
 
-static void solve_toi(const Ctx* x, W* w, Work* k, float dt, GoiDebug* dbg, int wi, int pitch) {
+/* Returns 1 when the world stopped at max_events with another event pending (toi.py:838-842). */
+static int solve_toi(const Ctx* x, W* w, Work* k, float dt, GoiDebug* dbg, int wi, int pitch) {
     const GoiModelDesc* m = x->m;
     int B = w->B, C = w->C;
-    if (C == 0 || m->P == 0) return;
+    if (C == 0 || m->P == 0) return 0;
     if (x->s->unity_toi && m->toi_bodies) {
         int any = 0;
         for (int b = 0; b < B; ++b) any |= m->toi_bodies[b];
-        if (!any) return;
+        if (!any) return 0;
     }
     for (int b = 0; b < B; ++b) w->t_alpha0[b] = 0.0f;
     for (int c = 0; c < C; ++c) {
@@ -2429,7 +2430,7 @@ static void solve_toi(const Ctx* x, W* w, Work* k, float dt, GoiDebug* dbg, int 
         w->t_ni[2 * c] = 0.0f; w->t_ni[2 * c + 1] = 0.0f; w->t_ti[2 * c] = 0.0f; w->t_ti[2 * c + 1] = 0.0f;
     }
     *w->t_events = 0;
-    if (!(dt > 0.0f)) return;
+    if (!(dt > 0.0f)) return 0;
     int max_events = x->s->max_events >= 0 ? x->s->max_events : C * (MAX_SUB_STEPS + 1) + 8;
     int slot;
     float alpha;
@@ -2439,12 +2440,14 @@ static void solve_toi(const Ctx* x, W* w, Work* k, float dt, GoiDebug* dbg, int 
         *w->t_events += 1;
         found = toi_search(x, w, k, &slot, &alpha);
     }
+    return found;
 }
 
 /* ------------------------------------------------------------------------------------------------ step (step.py:28-47) */
 
 static void step_world(const Ctx* x, W* w, Work* k, GoiDebug* dbg, int wi, int pitch) {
     float dt = x->dt;
+    int overflow0 = *w->overflow, capped = 0;
     if (*w->new_fixture) find_new_contacts(x, w);
     *w->new_fixture = 0;
     float inv_dt = dt > 0.0f ? 1.0f / dt : 0.0f;
@@ -2453,10 +2456,20 @@ static void step_world(const Ctx* x, W* w, Work* k, GoiDebug* dbg, int wi, int p
     solve(x, w, k, dt, dt_ratio, dbg, wi, pitch);
     if (dbg && dbg->toi_event_slot) /* the blank trace; SolveTOI's events overwrite their entries */
         for (int e = 0; e < GOI_DEBUG_TOI_EVENTS; ++e) record_toi_event(dbg, wi, pitch, e, -1, 0.0f, k->corder, 0, 0);
-    if (x->s->continuous_physics) solve_toi(x, w, k, dt, dbg, wi, pitch);
+    if (x->s->continuous_physics) capped = solve_toi(x, w, k, dt, dbg, wi, pitch);
     if (dt > 0.0f) *w->inv_dt0 = inv_dt;
     if (x->s->auto_clear_forces) {
         for (int b = 0; b < w->B; ++b) { w->b_force[2 * b] = 0.0f; w->b_force[2 * b + 1] = 0.0f; w->b_torque[b] = 0.0f; }
+    }
+    if (dbg && dbg->status) { /* the step's failure counters as one word (GOI_STATUS_*) */
+        int st = *w->overflow != overflow0 ? GOI_STATUS_OVERFLOW : 0, finite = 1;
+        for (int b = 0; b < w->B; ++b)
+            finite = finite && isfinite(w->b_c[2 * b]) && isfinite(w->b_c[2 * b + 1]) && isfinite(w->b_a[b]) &&
+                     isfinite(w->b_v[2 * b]) && isfinite(w->b_v[2 * b + 1]) && isfinite(w->b_w[b]);
+        if (!finite) st |= GOI_STATUS_NONFINITE;
+        if (capped) st |= GOI_STATUS_TOI_CAPPED;
+        if (x->s->continuous_physics && !(dt > 0.0f)) st |= GOI_STATUS_TOI_SKIPPED;
+        dbg->status[wi] = st;
     }
 }
 

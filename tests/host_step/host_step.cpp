@@ -8,10 +8,10 @@
 // launch) or "noalloc:K" (goi_step_n_noalloc); "plant" moves the last world's first body by one ulp in the oracle's
 // copy only, so that run must end in a mismatch. The scenario file (written by tests/test_host_sanitized.py,
 // little-endian):
-//   "GOISCN01", int32 F J P B, then the 24 GoiModelDesc arrays in declaration order, each an int64 byte count
+//   "GOISCN02", int32 F J P B, then the 24 GoiModelDesc arrays in declaration order, each an int64 byte count
 //   (-1 = NULL) and the bytes; int32 sizeof(GoiSettings) and the struct; float dt; int32 n_steps, n, B R J C,
 //   contact_capacity, packed, n_leaves; per leaf: int32 name length, name, int32 element size, int64 elements per
-//   world, n * that many elements batch-major; int32 motor joint (-1: no actions), float speed gain, torque gain,
+//   world, int32 kind (1 float, 0 integer or bool), n * that many elements batch-major; int32 motor joint (-1: no actions), float speed gain, torque gain,
 //   then n_steps * n * 2 float actions.
 #include <algorithm>
 #include <cmath>
@@ -66,6 +66,7 @@ struct Leaf {
     std::string name;
     int esize;
     int64_t per_world;
+    bool is_float;
     uint8_t* ref;  // the oracle's copy, batch-major [n][per_world]
     uint8_t* dev;  // the library's copy, worlds-minor [per_world][pitch]
 };
@@ -94,7 +95,7 @@ int main(int argc, char** argv) {
     if (!r.f) die(std::string("cannot open ") + argv[1]);
     char magic[8];
     r.raw(magic, 8);
-    if (std::memcmp(magic, "GOISCN01", 8) != 0) die("not a scenario file");
+    if (std::memcmp(magic, "GOISCN02", 8) != 0) die("not a scenario file");
 
     GoiModelDesc d{};
     d.F = r.get<int32_t>();
@@ -153,6 +154,7 @@ int main(int argc, char** argv) {
         r.raw(&L.name[0], L.name.size());
         L.esize = r.get<int32_t>();
         L.per_world = r.get<int64_t>();
+        L.is_float = r.get<int32_t>() == 1;
         const size_t bytes = (size_t)n * L.per_world * L.esize;
         L.ref = block(bytes);
         r.raw(L.ref, bytes);
@@ -232,9 +234,20 @@ int main(int argc, char** argv) {
                 for (int64_t i = 0; i < L.per_world; ++i) {
                     const uint8_t* a = L.ref + ((size_t)w * L.per_world + i) * L.esize;
                     const uint8_t* b = L.dev + ((size_t)i * pitch + w) * L.esize;
-                    if (std::memcmp(a, b, L.esize) != 0) {
-                        std::printf("MISMATCH after step %d: leaf %s world %d element %lld\n", k1, L.name.c_str(), w,
-                                    (long long)i);
+                    // float elements compare bit for bit, except that any two NaNs are equal: a NaN's sign and
+                    // payload follow the operand order of the operations that made it, which neither IEEE 754 nor
+                    // the reference fixes
+                    float fa = 0.0f, fb = 0.0f;
+                    if (L.is_float) {
+                        std::memcpy(&fa, a, 4);
+                        std::memcpy(&fb, b, 4);
+                    }
+                    if (std::memcmp(a, b, L.esize) != 0 && !(L.is_float && std::isnan(fa) && std::isnan(fb))) {
+                        uint32_t ua = 0, ub = 0;
+                        std::memcpy(&ua, a, L.esize);
+                        std::memcpy(&ub, b, L.esize);
+                        std::printf("MISMATCH after step %d: leaf %s world %d element %lld (oracle 0x%08x, step 0x%08x)\n",
+                                    k1, L.name.c_str(), w, (long long)i, ua, ub);
                         std::fflush(stdout);
                         goi_model_destroy(model);
                         return 1;

@@ -97,3 +97,43 @@ def test_motor_actions_native_equals_host():
     assert np.asarray(got.joints.max_motor).tobytes() == torque.tobytes()
     others = [j for j in range(speed.shape[1]) if j != B2.scenes.MOTOR_JOINT]
     assert np.array_equal(np.asarray(got.joints.motor_speed)[:, others], np.asarray(before.joints.motor_speed)[:, others])
+
+
+def test_decoded_records_step_on_the_device(oracle):
+    """Worlds decoded from step records (box2d/record.py; the test-side encoder writes NAT1 snapshots and the geometry
+    blob in the plugin's layout, plugin/NativeRecord.cs:92-152) step on the device as in the oracle, bit for bit: 32
+    config-4 worlds stepped 14 times by the oracle with actions, each encoded and decoded (full fixture layout, the
+    game's settings from the record), then 20 steps with actions on both, TOI events on the way."""
+    import importlib
+    import test_record as TR
+    R = importlib.import_module("getting-over-it-rl_amd.box2d.record")
+    cfg = b2.scenes.CONFIGS[4]
+    s = b2.scenes.settings_for(cfg)
+    model, state, pts = b2.scenes.build_world(cfg, s)
+    n = 32
+    st = b2.scenes.place_worlds(cfg, model, state, pts, n)
+    rng = np.random.default_rng(19)
+    for _ in range(14):
+        b2.scenes.apply_actions(st.joints.motor_speed, st.joints.max_motor, b2.scenes.actions(rng, n))
+        oracle.step_(model, st, s, cfg.dt)
+    geo = R.read_geometry(TR.encode_geometry(model, TR._world(st, 0)))
+    dec = []
+    for w in range(n):
+        one = TR._world(st, w)
+        m2, s2, set2, _ = R.to_world(geo, R.decode_native(TR.encode_native(model, one, s)), s,
+                                     contact_capacity=one.contacts.pair.shape[0])
+        dec.append(s2._replace(fixtures=s2.fixtures._replace(fat=one.fixtures.fat.copy())))  # not in a record
+    full = wd.from_leaves([np.stack(v) for v in zip(*[wd.leaves(x) for x in dec])])
+    assert m2.fixture_slot is None and wd.dims(full)[1] == m2.fixture_body.shape[0]
+    dev = b2.layout.to_device(full, "cuda")
+    ref = oracle.copy(full)
+    events = 0
+    for k in range(20):
+        a = b2.scenes.actions(rng, n)
+        b2.scenes.apply_actions(ref.joints.motor_speed, ref.joints.max_motor, a)
+        b2.scenes.apply_actions(dev.joints.motor_speed, dev.joints.max_motor, torch.from_numpy(a).cuda())
+        b2.step_(m2, dev, set2, cfg.dt)
+        oracle.step_(m2, ref, set2, cfg.dt)
+        events += int(np.asarray(ref.toi.events).sum())
+        assert leaf_mismatches(ref, b2.layout.to_host(dev)) == [], k + 1
+    assert events > 0

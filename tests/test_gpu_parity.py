@@ -16,9 +16,10 @@ torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 
-def _run(model, state, settings, dt, steps, oracle, actions=None, every=1, on_step=None):
+def _run(model, state, settings, dt, steps, oracle, actions=None, every=1, on_step=None, nan_equal=False):
     """Steps the device and the oracle side by side from the same State (and actions), comparing every leaf bit for
-    bit after every `every`-th step and after the last. on_step(k, ref, dev) runs after each step."""
+    bit after every `every`-th step and after the last (nan_equal: any two NaNs equal). on_step(k, ref, dev) runs
+    after each step."""
     dev = b2.layout.to_device(state, "cuda")
     ref = oracle.copy(state)
     for k in range(steps):
@@ -32,7 +33,7 @@ def _run(model, state, settings, dt, steps, oracle, actions=None, every=1, on_st
             on_step(k, ref, dev)
         if (k + 1) % every == 0 or k + 1 == steps:
             got = b2.layout.to_host(dev)
-            bad = leaf_mismatches(ref, got)
+            bad = leaf_mismatches(ref, got, nan_equal)
             assert bad == [], f"step {k + 1}: {bad[:4]}"
     return ref
 
@@ -527,3 +528,77 @@ def test_full_layout_parity(oracle, case):
     cm = wd.compact_model(model, st)
     out = b2.step(cm, b2.layout.to_device(st, "cuda"), s, dt)
     assert leaf_mismatches(oracle.step(model, st, s, dt), b2.layout.to_host(out)) == []
+
+
+@pytest.mark.parametrize("wpw", [None, "8"])
+def test_nonfinite_worlds_parity(oracle, monkeypatch, wpw):
+    """NaN and infinite values written into a few worlds of config 4 (a NaN velocity, an infinite spin, a NaN
+    position, 1e30 m/s, a NaN force; the failure inputs of the reference's bench, bench_gpu.py:135-136): the other
+    worlds stay bit-exact and the poisoned ones follow the oracle, NaN for NaN (a box with a NaN coordinate overlaps
+    every box under b2TestOverlap, so their tables fill and overflow). 64 worlds, 30 steps, the general kernel and the
+    rig instance (8 worlds per wave). The same scenario runs first under the sanitizers on the CPU
+    (test_host_sanitized.py::test_nonfinite_worlds_sanitized)."""
+    from test_host_sanitized import nonfinite_case
+    if wpw is not None:
+        monkeypatch.setenv("GOI_WORLDS_PER_WAVE", wpw)
+    m, st, s, dt, acts = nonfinite_case()
+    bad = [3, 5, 7, 11]  # world 9's 1e30 m/s is scaled to rest by the max-translation clamp (h v squared is inf)
+    ref = _run(m, st, s, dt, 30, oracle, list(acts), nan_equal=True)
+    c = np.asarray(ref.bodies.c)
+    finite = np.isfinite(c).reshape(c.shape[0], -1).all(1)
+    assert not finite[bad].any() and finite[np.setdiff1d(np.arange(64), bad)].all()
+    assert (np.asarray(ref.overflow)[bad] > 0).any()
+
+
+@pytest.mark.parametrize("dt", [0.0, -0.02])
+def test_non_positive_dt_parity(oracle, dt):
+    """dt <= 0 (step.py:35-40, toi.py:841): Solve runs, SolveTOI is skipped, inv_dt0 is left as it was."""
+    s, m, st, cfg = b2.scenes.make_config(4, 256)
+    rng = np.random.default_rng(41)
+    ref = _run(m, st, s, np.float32(dt), 6, oracle, [b2.scenes.actions(rng, 256) for _ in range(6)])
+    assert int(np.asarray(ref.toi.events).sum()) == 0
+
+
+@pytest.mark.parametrize("max_events", [1, 2, 3])
+def test_max_events_parity(oracle, monkeypatch, max_events):
+    """SolveTOI stops after max_events events a step (toi.py:838-842): config 4, 1,024 worlds, 20 steps, on the rig
+    instance; some worlds reach the cap."""
+    from dataclasses import replace
+    monkeypatch.setenv("GOI_WORLDS_PER_WAVE", "8")
+    s, m, st, cfg = b2.scenes.make_config(4, 1024)
+    s = replace(s, max_events=max_events)
+    rng = np.random.default_rng(43)
+    capped = []
+    ref = _run(m, st, s, cfg.dt, 20, oracle, [b2.scenes.actions(rng, 1024) for _ in range(20)],
+               on_step=lambda k, r, d: capped.append(int((np.asarray(r.toi.events) == max_events).sum())))
+    assert sum(capped) > 0 and int(np.asarray(ref.toi.events).max()) <= max_events
+
+
+def test_status_word_parity(oracle):
+    """GoiDebug.status (the step's failure counters as one word per world) on the device equals the oracle's at every
+    step, with every bit raised somewhere: non-finite worlds (which also overflow their tables), max_events 2
+    (SolveTOI capped) and one step of dt 0 (SolveTOI skipped). Config 4, 64 worlds, 12 steps, the general kernel (a
+    launch with debug arrays takes it); the other debug arrays and every leaf are compared too, NaN for NaN."""
+    from dataclasses import replace
+    from test_host_sanitized import nonfinite_case
+    A = b2._abi
+    m, st, s, dt, acts = nonfinite_case(steps=12)
+    s = replace(s, max_events=2)
+    n, dims = 64, wd.dims(st)
+    dev = b2.layout.to_device(st, "cuda")
+    ref = oracle.copy(st)
+    seen = 0
+    for k in range(12):
+        b2.scenes.apply_actions(ref.joints.motor_speed, ref.joints.max_motor, acts[k])
+        b2.scenes.apply_actions(dev.joints.motor_speed, dev.joints.max_motor, torch.from_numpy(acts[k]).cuda())
+        dtk = np.float32(0.0) if k == 5 else dt
+        dbg, t = b2.make_debug(n, dims, pitch=b2.layout.pitch_of(dev))
+        b2.step_(m, dev, s, dtk, debug=dbg)
+        d = {key: np.full(v.shape[:-1] + (n,), -9, np.int32) for key, v in t.items()}
+        oracle.step_(m, ref, s, dtk, debug=d)
+        torch.cuda.synchronize()
+        for key in d:
+            assert np.array_equal(d[key], t[key][..., :n].cpu().numpy()), (k + 1, key)
+        assert leaf_mismatches(ref, b2.layout.to_host(dev), nan_equal=True) == [], k + 1
+        seen |= int(np.bitwise_or.reduce(d["status"]))
+    assert seen == A.STATUS_OVERFLOW | A.STATUS_NONFINITE | A.STATUS_TOI_CAPPED | A.STATUS_TOI_SKIPPED

@@ -54,7 +54,7 @@ def write_scenario(path, model, state, settings, dt, steps, packed, actions=None
     B, R, J, C = wd.dims(state)
     n = np.asarray(state.bodies.type).shape[0]
     with open(path, "wb") as f:
-        f.write(b"GOISCN01")
+        f.write(b"GOISCN02")
         f.write(struct.pack("<4i", model.fixture_body.shape[0], model.joint_type.shape[0], model.pair_a.shape[0],
                             0 if model.body_type is None else model.body_type.shape[0]))
         names = [name for name, _ in _abi.GoiModelDesc._fields_[4:]]
@@ -70,11 +70,12 @@ def write_scenario(path, model, state, settings, dt, steps, packed, actions=None
         f.write(struct.pack("<i", len(cs)) + cs)
         f.write(np.float32(dt).tobytes())
         f.write(struct.pack("<9i", steps, n, B, R, J, C, C, int(packed), len(wd.LEAVES)))
-        for (group, name, _, _), leaf in zip(wd.LEAVES, wd.leaves(state)):
+        for (group, name, dt, _), leaf in zip(wd.LEAVES, wd.leaves(state)):
             a = np.ascontiguousarray(np.asarray(leaf))
             full = (f"{group}.{name}" if group else name).encode()
             per_world = int(np.prod(a.shape[1:], dtype=np.int64))
-            f.write(struct.pack("<i", len(full)) + full + struct.pack("<iq", a.itemsize, per_world) + a.tobytes())
+            kind = 1 if np.dtype(dt) == np.float32 else 0
+            f.write(struct.pack("<i", len(full)) + full + struct.pack("<iqi", a.itemsize, per_world, kind) + a.tobytes())
         if actions is None:
             f.write(struct.pack("<i", -1) + np.float32(0).tobytes() * 2)
         else:
@@ -131,6 +132,53 @@ def test_poisoned_scratch_sanitized(host_step, tmp_path, poison):
         p = tmp_path / f"scn{int(packed)}.bin"
         write_scenario(p, m, st, s, dt, 30, packed, acts)
         check(run(host_step, p, "step", poison=poison))
+
+
+def nonfinite_case(n=64, steps=30, seed=7):
+    """Config 4 with non-finite values written into a few worlds (the failure inputs of the reference's bench,
+    bench_gpu.py:135-136): a NaN linear velocity (world 3), an infinite angular velocity (5), a NaN position (7), a
+    velocity of 1e30 m/s (9: the max-translation clamp scales it by 2 / inf = 0) and a NaN force (11); the other
+    worlds are untouched."""
+    m, st, s, dt, acts = config_case(4, n, steps, seed=seed)
+    bd = st.bodies
+    bd.v[3, 1, 0] = np.nan
+    bd.w[5, 4] = np.inf
+    bd.c[7, 2, 1] = np.nan
+    bd.v[9, 3] = (1e30, -1e30)
+    bd.force[11, 1, 1] = np.nan
+    return m, st, s, dt, acts
+
+
+def test_nonfinite_worlds_sanitized(host_step, tmp_path):
+    """NaN and infinite body values step without an out-of-bounds access or undefined operation in either the
+    library's step or the oracle, to the same bits (both run here on the same float hardware), on the rig instance
+    and the general kernel."""
+    m, st, s, dt, acts = nonfinite_case()
+    for packed in (True, False):
+        p = tmp_path / f"scn{int(packed)}.bin"
+        write_scenario(p, m, st, s, dt, 30, packed, acts)
+        check(run(host_step, p, "step"))
+
+
+@pytest.mark.parametrize("dt", [0.0, -0.02])
+def test_non_positive_dt_sanitized(host_step, tmp_path, dt):
+    """dt <= 0: Solve still runs (step.py:35-40) and SolveTOI is skipped (toi.py:841); inv_dt0 keeps its value."""
+    m, st, s, _, acts = config_case(4, 64, 6)
+    p = tmp_path / "scn.bin"
+    write_scenario(p, m, st, s, dt, 6, True, acts)
+    r = run(host_step, p, "step")
+    check(r)
+    assert "events 0" in r.stdout
+
+
+@pytest.mark.parametrize("max_events", [1, 2, 3])
+def test_max_events_sanitized(host_step, tmp_path, max_events):
+    """SolveTOI stopped after max_events events per step (toi.py:838-842), on the rig instance."""
+    from dataclasses import replace
+    m, st, s, dt, acts = config_case(4, 64, 30)
+    p = tmp_path / "scn.bin"
+    write_scenario(p, m, st, replace(s, max_events=max_events), dt, 30, True, acts)
+    check(run(host_step, p, "step"))
 
 
 @pytest.mark.parametrize("capacity", [6, 10])

@@ -153,3 +153,45 @@ def test_resting_box_world_manifold(oracle):
     assert np.allclose(r["worldNormal"], (0, 1), atol=1e-6)
     assert np.allclose(sorted(r["worldPoints"][:, 0]), (-0.5, 0.5), atol=2e-3)
     assert np.allclose(r["separations"], -0.005, atol=1.5e-3)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the per-world status word (GoiDebug.status): the step's failure counters, each forced from the host
+
+def _status_run(oracle, st, m, s, dt, steps, acts=None):
+    """OR of the oracle's status words over `steps` steps, per world."""
+    n = st.bodies.type.shape[0]
+    seen = np.zeros(n, np.int32)
+    for k in range(steps):
+        if acts is not None:
+            b2.scenes.apply_actions(st.joints.motor_speed, st.joints.max_motor, acts[k])
+        d = {key: np.full(shape, -7, np.int32) for key, shape in b2.debug_shapes(n, wd.dims(st)).items()}
+        before = np.asarray(st.overflow).copy()
+        oracle.step_(m, st, s, dt, debug=d)
+        assert np.array_equal((d["status"] & b2._abi.STATUS_OVERFLOW) != 0, np.asarray(st.overflow) != before)
+        seen |= d["status"]
+    return seen
+
+
+def test_status_word(oracle):
+    """Each bit from the condition that sets it: a small contact table (overflow), non-finite bodies, max_events 1
+    (SolveTOI capped with an event pending), dt 0 with continuous physics (SolveTOI skipped); none on a healthy run."""
+    from dataclasses import replace
+    from test_host_sanitized import nonfinite_case
+    A = b2._abi
+    rng = np.random.default_rng(3)
+    s, m, st, cfg = b2.scenes.make_config(4, 64)
+    acts = [b2.scenes.actions(rng, 64) for _ in range(10)]
+    healthy = _status_run(oracle, oracle.copy(st), m, s, cfg.dt, 10, acts)
+    assert (healthy == 0).all()
+    s6, m6, st6, _ = b2.scenes.make_config(4, 64, capacity=6)
+    assert (_status_run(oracle, st6, m6, s6, cfg.dt, 10, acts) & A.STATUS_OVERFLOW).any()
+    mn, stn, sn, dtn, actsn = nonfinite_case()
+    bad = _status_run(oracle, stn, mn, sn, dtn, 3, list(actsn))
+    # world 9's 1e30 m/s stays finite: h v squared overflows, so the max-translation clamp scales v by 2 / inf = 0
+    assert np.array_equal(np.nonzero(bad & A.STATUS_NONFINITE)[0], [3, 5, 7, 11])
+    assert np.isfinite(stn.bodies.c[9]).all() and np.isfinite(stn.bodies.v[9]).all()
+    capped = _status_run(oracle, oracle.copy(st), m, replace(s, max_events=1), cfg.dt, 10, acts)
+    assert (capped & A.STATUS_TOI_CAPPED).any() and not (healthy & A.STATUS_TOI_CAPPED).any()
+    skipped = _status_run(oracle, oracle.copy(st), m, s, np.float32(0.0), 1, acts)
+    assert (skipped == A.STATUS_TOI_SKIPPED).all()

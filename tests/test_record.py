@@ -307,3 +307,10 @@ def test_unmapped_objects_are_refused(stepped):
     snap = R.decode_native(encode_native(model, one, s))
     with pytest.raises(R.RecordError, match="exceed"):
         R.to_world(geo, snap, s, contact_capacity=1)
+    # a moving body at the head of the snapshot's list with no geometry (created after the maps: the gift,
+    # NativeRecord.cs:98), unmapped (-1) or with a Rigidbody2D index the geometry does not know
+    for rb in (-1, 77):
+        snap = R.decode_native(encode_native(model, one, s))
+        snap.bodies.insert(0, R.NativeBody(rb, snap.bodies[0].raw))
+        with pytest.raises(R.RecordError, match="no entry in the geometry"):
+            R.to_world(geo, snap, s, contact_capacity=one.contacts.pair.shape[0])

@@ -7,8 +7,10 @@ b2 = importlib.import_module("getting-over-it-rl_amd.box2d")
 wd = b2.world
 
 
-def leaf_mismatches(ref, got):
-    """[(leaf name, worlds that differ)] comparing two batched numpy States bit for bit."""
+def leaf_mismatches(ref, got, nan_equal=False):
+    """[(leaf name, worlds that differ)] comparing two batched numpy States bit for bit. nan_equal: two float NaNs
+    count as equal whatever their sign and payload bits (which follow the operand order of the operations that made
+    them; neither IEEE 754 nor the reference fixes them)."""
     out = []
     for (g, name, _, _), a, b in zip(wd.LEAVES, wd.leaves(ref), wd.leaves(got)):
         a, b = np.asarray(a), np.asarray(b)
@@ -16,8 +18,15 @@ def leaf_mismatches(ref, got):
             out.append((f"{g}.{name}", "shape"))
             continue
         if a.tobytes() != b.tobytes():
-            diff = (a != b).reshape(a.shape[0], -1).any(1) if a.ndim > 1 else (a != b)
-            out.append((f"{g}.{name}", np.nonzero(diff)[0][:8].tolist()))
+            if a.dtype.kind == "f":
+                ne = (a.view(np.uint32) != b.view(np.uint32))
+                if nan_equal:
+                    ne &= ~(np.isnan(a) & np.isnan(b))
+            else:
+                ne = a != b
+            diff = ne.reshape(a.shape[0], -1).any(1) if a.ndim > 1 else ne
+            if diff.any():
+                out.append((f"{g}.{name}", np.nonzero(diff)[0][:8].tolist()))
     return out
 
 
