@@ -602,3 +602,68 @@ def test_status_word_parity(oracle):
         assert leaf_mismatches(ref, b2.layout.to_host(dev), nan_equal=True) == [], k + 1
         seen |= int(np.bitwise_or.reduce(d["status"]))
     assert seen == A.STATUS_OVERFLOW | A.STATUS_NONFINITE | A.STATUS_TOI_CAPPED | A.STATUS_TOI_SKIPPED
+
+
+@pytest.mark.parametrize("variant", ["no_warm_start", "clamps_per_second", "no_position_iterations", "damping",
+                                     "tangent_speed"])
+def test_settings_variants_parity(oracle, variant):
+    """The Settings switches and State inputs the benchmark configurations leave at their defaults: warm starting
+    off, per-second clamps, no position iteration (islands never position-solved, so never asleep), angular and
+    linear damping with a gravity scale, and a conveyor tangent speed on every live contact. Config 4, 256 worlds, 25
+    steps with actions (the tangent speed on the pile scene, 32 worlds), bit for bit."""
+    from dataclasses import replace
+    s, m, st, cfg = b2.scenes.make_config(4, 256)
+    dt, n, steps = cfg.dt, 256, 25
+    if variant == "no_warm_start":
+        s = replace(s, warm_starting=False)
+    elif variant == "clamps_per_second":
+        s = replace(s, clamps_per_second=True, max_translation=np.float32(60.0), max_rotation=np.float32(40.0))
+    elif variant == "no_position_iterations":
+        s = replace(s, position_iterations=0)
+    elif variant == "damping":
+        st.bodies.linear_damping[...] = np.float32(0.3)
+        st.bodies.angular_damping[...] = np.float32(0.7)
+        st.bodies.gravity_scale[:, 2] = np.float32(0.5)
+    else:
+        s, m, st = scene_defs.build_test_scene("pile", iterations=(8, 3))
+        st, dt, n, steps = perturbed(st, 32, seed=5), np.float32(1 / 60), 32, 40
+        ref = oracle.copy(st)
+        for _ in range(10):
+            oracle.step_(m, ref, s, dt)
+        live = np.asarray(ref.contacts.pair) >= 0
+        ref.contacts.tangent_speed[...] = np.where(live, np.random.default_rng(2).uniform(-2, 2, live.shape), 0)
+        st = ref
+    rng = np.random.default_rng(29)
+    acts = [b2.scenes.actions(rng, n) for _ in range(steps)] if variant != "tangent_speed" else None
+    _run(m, st, s, dt, steps, oracle, acts)
+
+
+@pytest.mark.parametrize("case", ["cage", "walk_restore"])
+def test_toi_bookkeeping_parity(oracle, case):
+    """The TOI scenes of the oracle pins on the device, 64 worlds with varied speeds: a ball between two walls (up to
+    18 events a step, each wall's contact capped at 9 sub-steps, the moved ball's contacts searched again after each
+    event) and a bullet passing a box it shares a contact with but never touches (the island walk advances and
+    restores it)."""
+    from test_oracle_pins import _ball_between_walls
+    rng = np.random.default_rng(37)
+    if case == "cage":
+        s, m, st = _ball_between_walls(700.0)
+        st = wd.batch(wd.from_leaves([np.asarray(x)[0] for x in wd.leaves(st)]), 64)
+        st.bodies.v[:, 1, 0] = rng.uniform(150.0, 900.0, 64).astype(np.float32) * rng.choice([-1, 1], 64)
+    else:
+        s = b2.Settings.stock(gravity=(0.0, 0.0), continuous_physics=True, max_translation=100.0)
+        d = wd.WorldDef(s)
+        g = d.add_body(wd.STATIC, (0.0, 0.0))
+        d.add_box(g, (0.05, 2.0), center=(4.0, 0.0))
+        ball = d.add_body(wd.DYNAMIC, (0.0, 0.0), velocity=(300.0, 0.0), mass=1.0, inertia=1.0, bullet=True)
+        d.add_circle(ball, 0.1)
+        box = d.add_body(wd.DYNAMIC, (2.0, 0.25), velocity=(0.0, 1.0), mass=1.0, inertia=1.0)
+        d.add_box(box, (0.5, 0.1))
+        model, state = d.build(8)
+        m = wd.compact_model(model, state)
+        st = wd.batch(wd.compact_state(m, state), 64)
+        st.bodies.v[:, 1, 0] = rng.uniform(200.0, 400.0, 64).astype(np.float32)
+        st.bodies.v[:, 2, 1] = rng.uniform(-2.0, 2.0, 64).astype(np.float32)
+    events = []
+    _run(m, st, s, np.float32(1 / 60), 4, oracle, on_step=lambda k, r, d: events.append(int(r.toi.events.sum())))
+    assert events[0] > 64

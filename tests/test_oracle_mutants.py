@@ -178,6 +178,58 @@ MUTANTS = [
      "k->min_sep[i] >= -1.5f * s->linear_slop && k->jok[i]", lambda o: P.test_position_iterations_exit_per_island(o)),
     ("position_exit_all_islands_together", "if (k->done[isl]) continue;\n            float ms",
      "if (!more) continue;\n            float ms", lambda o: P.test_position_iterations_exit_per_island(o)),
+    # settings paths and per-step bookkeeping
+    ("sleep_without_position_solve", "k->isl_sleep[i] = k->min_st[i] >= s->time_to_sleep && k->done[i];",
+     "k->isl_sleep[i] = k->min_st[i] >= s->time_to_sleep;", lambda o: P.test_sleep_needs_the_position_solve(o)),
+    ("restitution_without_threshold", "c->bias[j] = vrel < -x->s->velocity_threshold ? -restitution * vrel : 0.0f;",
+     "c->bias[j] = vrel < 0.0f ? -restitution * vrel : 0.0f;", lambda o: P.test_restitution_velocity_threshold(o)),
+    ("angular_damping_uses_linear", "float ad = 1.0f / (1.0f + h * w->b_ad[b]);",
+     "float ad = 1.0f / (1.0f + h * w->b_ld[b]);", lambda o: P.test_angular_damping_closed_form(o)),
+    ("tangent_speed_sign", "float vt = dot(dv, t) - c->tangent_speed;", "float vt = dot(dv, t) + c->tangent_speed;",
+     lambda o: P.test_tangent_speed_drives_the_contact(o)),
+    ("inv_dt0_on_any_dt", "if (dt > 0.0f) *w->inv_dt0 = inv_dt;", "*w->inv_dt0 = inv_dt;",
+     lambda o: P.test_inv_dt0_kept_for_non_positive_dt(o)),
+    ("clamps_per_second_ignored",
+     "float max_t = s->clamps_per_second ? s->max_translation * h : s->max_translation;",
+     "float max_t = s->max_translation;", lambda o: P.test_clamps_per_second(o)),
+    ("sleep_time_kept_when_moving", "if (moving) { w->b_sleep_time[b] = 0.0f; k->min_st[isl] = 0.0f; }",
+     "if (moving) { k->min_st[isl] = 0.0f; }", lambda o: P.test_sleep_time_resets_when_moving(o)),
+    ("warm_starting_flag_ignored", "c->ni[j] = warm ? dt_ratio * w->c_ni[2 * slot + j] : 0.0f;",
+     "c->ni[j] = dt_ratio * w->c_ni[2 * slot + j];", lambda o: P.test_warm_starting_off(o)),
+    ("joint_warm_without_dt_ratio", "    r->imp[0] = warm ? ix * dt_ratio : 0.0f;", "    r->imp[0] = warm ? ix : 0.0f;",
+     lambda o: P.test_joint_warm_start_scales_by_dt_ratio(o, True)),
+    ("motor_warm_without_dt_ratio", "    r->mimp = warm ? mimp * dt_ratio : 0.0f;", "    r->mimp = warm ? mimp : 0.0f;",
+     lambda o: P.test_joint_warm_start_scales_by_dt_ratio(o, True)),
+    ("limit_warm_without_dt_ratio", "    r->imp[3] = warm ? lo * dt_ratio : 0.0f;", "    r->imp[3] = warm ? lo : 0.0f;",
+     lambda o: P.test_joint_warm_start_scales_by_dt_ratio(o, True)),
+    ("static_awake_from_first_island", "        if (isl > k->last[ba]) k->last[ba] = isl;",
+     "        if (k->last[ba] < 0) k->last[ba] = isl;", lambda o: P.test_static_body_takes_the_last_islands_awake_flag(o)),
+    ("revolute_exit_ignores_limit_error", "    return pos_err <= s->linear_slop && ang_err <= s->angular_slop;",
+     "    return pos_err <= s->linear_slop;", lambda o: P.test_joint_error_keeps_position_iterations_going(o, "revolute_v24")),
+    ("prismatic_exit_ignores_angle", "        ok = lin_err <= s->linear_slop && ang_err <= s->angular_slop;",
+     "        ok = lin_err <= s->linear_slop;", lambda o: P.test_joint_error_keeps_position_iterations_going(o, "prismatic")),
+    ("weld_exit_ignores_angle", "        ok = pos_err <= s->linear_slop && ang_err <= s->angular_slop;",
+     "        ok = pos_err <= s->linear_slop;", lambda o: P.test_joint_error_keeps_position_iterations_going(o, "weld")),
+    # SolveTOI's bookkeeping
+    ("toi_sub_step_cap_at_8", "w->t_count[c] > MAX_SUB_STEPS", "w->t_count[c] >= MAX_SUB_STEPS",
+     lambda o: P.test_toi_sub_step_cap_and_re_search(o)),
+    ("toi_re_search_body_a_only", "if (k->moved[ca] || k->moved[cb]) w->t_flag[c] = 0;",
+     "if (k->moved[ca]) w->t_flag[c] = 0;", lambda o: P.test_toi_sub_step_cap_and_re_search(o)),
+    ("toi_walk_keeps_advanced_neighbour", "if (!w->c_touching[c]) { restore_sweep(w, k, other); continue; }",
+     "if (!w->c_touching[c]) { continue; }", lambda o: P.test_toi_walk_restores_a_body_it_does_not_keep(o)),
+    ("angular_sleep_tolerance_not_squared",
+     "float ang_tol = s->angular_sleep_tolerance * s->angular_sleep_tolerance;",
+     "float ang_tol = s->angular_sleep_tolerance;", lambda o: P.test_angular_sleep_tolerance_is_squared(o)),
+    ("gravity_scale_ignored_x", "w->b_gs[b] * w->gravity[0]", "w->gravity[0]",
+     lambda o: P.test_gravity_scale_and_lateral_gravity(o)),
+    ("soft_weld_gamma_without_h", "        float gamma = h * (dd + h * kk);", "        float gamma = dd + h * kk;",
+     lambda o: P.test_soft_weld_velocity_row(o, 0.5)),
+    ("soft_weld_bias_sign", "        float bias = C * h * kk * gamma;", "        float bias = -C * h * kk * gamma;",
+     lambda o: P.test_soft_weld_velocity_row(o, 0.0)),
+    ("toi_integration_clamp_over_h",
+     "    float max_t = s->clamps_per_second ? s->max_translation * x->dt : s->max_translation;",
+     "    float max_t = s->clamps_per_second ? s->max_translation * h : s->max_translation;",
+     lambda o: P.test_toi_integration_clamp_is_per_step(o)),
 ]
 
 

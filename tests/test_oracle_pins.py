@@ -1496,3 +1496,413 @@ def test_position_iterations_exit_per_island(oracle):
         assert pose(st, 1) == pose(st1, 1), n
     ys = [float(runs[n][0].bodies.c[0, 2, 1]) for n in (1, 2, 3, 8)]
     assert all(y1 < y2 for y1, y2 in zip(ys, ys[1:]))  # box B rises with every pass
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# settings paths and per-step bookkeeping   (step.py:28-47, 73-194; contact_solver.py:32-147, 194-290)
+
+def _single(d, capacity=4):
+    model, state = d.build(capacity)
+    cm = wd.compact_model(model, state)
+    return cm, wd.batch(wd.compact_state(cm, state), 1)
+
+
+def test_angular_damping_closed_form(oracle):
+    """b2Island::Solve's angular damping, w <- w / (1 + h c_ang), apart from the linear one: a free spinning body
+    with angular damping 0.3 and linear damping 0.05 follows the float32 recurrence to the bit."""
+    import dataclasses
+    s = dataclasses.replace(S.stock(gravity=(0.0, 0.0)), allow_sleep=False)
+    d = wd.WorldDef(s)
+    b = d.add_body(wd.DYNAMIC, (0.0, 0.0), 0.0, (2.0, 0.0), 7.0, mass=1.0, inertia=1.0, linear_damping=0.05,
+                   angular_damping=0.3)
+    d.add_circle(b, 0.5)
+    m, st = _single(d)
+    h = F32(1 / 60)
+    w, v = F32(7.0), F32(2.0)
+    wd_, vd_ = F32(1) / (F32(1) + h * F32(0.3)), F32(1) / (F32(1) + h * F32(0.05))
+    for _ in range(50):
+        oracle.step_(m, st, s, h)
+        w, v = w * wd_, v * vd_
+        assert st.bodies.w[0, 0] == w and st.bodies.v[0, 0, 0] == v
+
+
+def test_clamps_per_second(oracle):
+    """Settings.clamps_per_second: max_translation and max_rotation are per second, so a step may move at most
+    max_translation * h and turn at most max_rotation * h (step.py:120-135)."""
+    import dataclasses
+    s = dataclasses.replace(S.stock(gravity=(0.0, 0.0), max_translation=120.0, max_rotation=30.0),
+                            clamps_per_second=True, allow_sleep=False)
+    d = wd.WorldDef(s)
+    b = d.add_body(wd.DYNAMIC, (0.0, 0.0), 0.0, (300.0, 400.0), 50.0, mass=1.0, inertia=1.0)
+    d.add_box(b, (0.5, 0.5))
+    m, st = _single(d)
+    h = F32(1 / 60)
+    oracle.step_(m, st, s, h)
+    assert float(np.hypot(*st.bodies.c[0, 0])) == pytest.approx(120.0 / 60.0, rel=2e-6)
+    assert float(np.hypot(*st.bodies.v[0, 0])) == pytest.approx(120.0, rel=2e-6)
+    assert float(st.bodies.a[0, 0]) == pytest.approx(30.0 / 60.0, rel=2e-6)
+    assert float(st.bodies.w[0, 0]) == pytest.approx(30.0, rel=2e-6)
+    # the same settings without clamps_per_second: 120 m and 30 rad per step bind nothing here
+    m2, st2 = _single(d)
+    oracle.step_(m2, st2, dataclasses.replace(s, clamps_per_second=False), h)
+    assert float(np.hypot(*st2.bodies.v[0, 0])) == pytest.approx(500.0, rel=1e-6)
+
+
+def test_restitution_velocity_threshold(oracle):
+    """b2VelocityConstraintPoint::velocityBias = -e vRel only when vRel < -velocity_threshold: a ball with
+    restitution 1 meeting the ground at 0.5 m/s (below the stock 1 m/s threshold) stops, one at 3 m/s bounces
+    back at 3 m/s."""
+    for speed, bounce in ((0.5, False), (3.0, True)):
+        s = S.stock(gravity=(0.0, 0.0))
+        d = wd.WorldDef(s)
+        g = d.add_body(wd.STATIC, (0.0, -0.5))
+        d.add_box(g, (10.0, 0.5), restitution=1.0)
+        b = d.add_body(wd.DYNAMIC, (0.0, 0.5 + 0.005), 0.0, (0.0, -speed), mass=1.0, inertia=1.0)
+        d.add_circle(b, 0.5, restitution=1.0)
+        m, st = _single(d)
+        oracle.step_(m, st, s, F32(1 / 60))
+        vy = float(st.bodies.v[0, 1, 1])
+        assert (vy == pytest.approx(speed, rel=1e-5)) if bounce else abs(vy) < 1e-6, (speed, vy)
+
+
+def test_warm_starting_off(oracle):
+    """Settings.warm_starting false: every contact starts the step with zero impulses, so with no velocity iteration
+    the stored impulses are zero (contact_solver.py:160-164), while warm starting keeps them (dtRatio 1)."""
+    import dataclasses
+    s = dataclasses.replace(S.stock(), allow_sleep=False)
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (0.0, -0.5))
+    d.add_box(g, (10.0, 0.5))
+    b = d.add_body(wd.DYNAMIC, (0.0, 0.5), mass=2.0, inertia=F32(2) / F32(6))
+    d.add_box(b, (0.5, 0.5))
+    m, st = _single(d)
+    for _ in range(10):
+        oracle.step_(m, st, s, F32(1 / 64))
+    k = int(np.nonzero(st.contacts.touching[0])[0][0])
+    ni = st.contacts.normal_impulse[0, k].copy()
+    assert np.all(ni > 0.1)
+    on, off = oracle.copy(st), oracle.copy(st)
+    oracle.step_(m, on, dataclasses.replace(s, velocity_iterations=0), F32(1 / 64))
+    oracle.step_(m, off, dataclasses.replace(s, velocity_iterations=0, warm_starting=False), F32(1 / 64))
+    assert np.array_equal(on.contacts.normal_impulse[0, k], ni)
+    assert np.all(off.contacts.normal_impulse[0, k] == 0) and np.all(off.contacts.tangent_impulse[0, k] == 0)
+
+
+def test_inv_dt0_kept_for_non_positive_dt(oracle):
+    """inv_dt0 becomes 1 / dt after a step with dt > 0 and is left alone by a step with dt <= 0 (step.py:41-44),
+    so the next positive step's dtRatio still refers to the last real step."""
+    d, box = resting_box()
+    m, st = _single(d, 8)
+    oracle.step_(m, st, d.settings, F32(1 / 64))
+    assert float(st.inv_dt0[0]) == 64.0
+    for dt in (0.0, -0.02):
+        oracle.step_(m, st, d.settings, F32(dt))
+        assert float(st.inv_dt0[0]) == 64.0
+
+
+def test_sleep_needs_the_position_solve(oracle):
+    """An island sleeps only when its bodies have been slow for time_to_sleep and its position iterations reached
+    tolerance in the step (b2Island::Solve's positionSolved; step.py:153-168). With no position iteration an island
+    is never position-solved: a box at rest in zero gravity then never sleeps; with one iteration it sleeps once its
+    sleep time reaches 0.5 s (31 steps of 1/60: the sleep time is the float sum of the steps)."""
+    import dataclasses
+    for iters, sleeps in ((0, False), (1, True)):
+        s = dataclasses.replace(S.stock(gravity=(0.0, 0.0)), position_iterations=iters)
+        d = wd.WorldDef(s)
+        b = d.add_body(wd.DYNAMIC, (0.0, 0.0), mass=1.0, inertia=1.0)
+        d.add_box(b, (0.5, 0.5))
+        m, st = _single(d)
+        t = F32(0)
+        asleep_at = None
+        for k in range(40):
+            oracle.step_(m, st, s, F32(1 / 60))
+            t = t + F32(1 / 60)
+            if asleep_at is None and not st.bodies.awake[0, 0]:
+                asleep_at = k
+        assert (asleep_at is not None) == sleeps, (iters, asleep_at)
+        if sleeps:
+            n = 0
+            acc = F32(0)
+            while acc < F32(0.5):
+                acc = acc + F32(1 / 60)
+                n += 1
+            assert asleep_at == n - 1
+
+
+def test_sleep_time_resets_when_moving(oracle):
+    """A body slower than the sleep tolerances accumulates sleep time; one moving faster has it reset to 0 in the
+    step (step.py:153-168)."""
+    s = S.stock(gravity=(0.0, 0.0))
+    d = wd.WorldDef(s)
+    b = d.add_body(wd.DYNAMIC, (0.0, 0.0), mass=1.0, inertia=1.0)
+    d.add_box(b, (0.5, 0.5))
+    m, st = _single(d)
+    for _ in range(10):
+        oracle.step_(m, st, s, F32(1 / 60))
+    assert float(st.bodies.sleep_time[0, 0]) > 0.15
+    st.bodies.v[0, 0] = (0.5, 0.0)
+    oracle.step_(m, st, s, F32(1 / 60))
+    assert st.bodies.sleep_time[0, 0] == 0 and st.bodies.awake[0, 0]
+
+
+@pytest.mark.parametrize("v24", [True, False])
+def test_joint_warm_start_scales_by_dt_ratio(oracle, v24):
+    """b2RevoluteJoint::InitVelocityConstraints scales every stored impulse (point, motor, limit) by dtRatio before
+    warm-starting (joints.py:151-160). A bar hanging from a static pivot against its lower limit with a weak motor
+    holding it: after steps of 1/64 s (inv_dt0 = 64 exactly), one step of 1/128 s with no velocity iteration stores
+    exactly half of each impulse."""
+    import dataclasses
+    s = dataclasses.replace(S.stock(gravity=(0.0, -10.0)), revolute_v24=v24, allow_sleep=False)
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (0.0, 0.0))
+    b = d.add_body(wd.DYNAMIC, (1.0, 0.0), mass=2.0, inertia=0.5)
+    d.add_box(b, (1.0, 0.1))
+    d.add_revolute(g, b, (0.0, 0.0), (-1.0, 0.0), limits=(-0.1, 0.1), motor_speed=0.0, max_motor_torque=3.0,
+                   enable_motor=True)
+    m, st = _single(d)
+    for _ in range(40):
+        oracle.step_(m, st, s, F32(1 / 64))
+    jt = st.joints
+    imp, mot = jt.impulse[0, 0].copy(), jt.motor_impulse[0, 0].copy()
+    low = jt.lower_impulse[0, 0].copy()
+    assert abs(float(imp[1])) > 0.1 and abs(float(mot)) > 1e-3
+    assert (float(low) > 1e-3) if v24 else (abs(float(imp[2])) > 1e-3)  # resting on the lower limit
+    oracle.step_(m, st, dataclasses.replace(s, velocity_iterations=0), F32(1 / 128))
+    half = F32(0.5)
+    assert np.array_equal(jt.impulse[0, 0, :2], imp[:2] * half)
+    assert jt.motor_impulse[0, 0] == mot * half
+    if v24:
+        assert jt.lower_impulse[0, 0] == low * half
+    else:
+        assert jt.impulse[0, 0, 2] == imp[2] * half
+
+
+def test_tangent_speed_drives_the_contact(oracle):
+    """contacts.tangent_speed (b2Contact::m_tangentSpeed, a conveyor belt): the friction rows solve for a relative
+    tangential velocity dot(vB - vA, t) equal to it, t = cross(n, 1) (contact_solver.py:252-262). A box resting on a
+    high-friction slab with tangent speed 1 set on its contact moves at +1 m/s along the slab after one step (either
+    fixture order gives the same sign), and at -1 m/s for tangent speed -1; the box's inertia is so large that it
+    does not turn, so the first friction row reaches the target and the second finds it reached."""
+    import dataclasses
+    s = dataclasses.replace(S.stock(gravity=(0.0, -10.0)), allow_sleep=False)
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (0.0, -0.5))
+    d.add_box(g, (10.0, 0.5), friction=100.0)
+    b = d.add_body(wd.DYNAMIC, (0.0, 0.5), mass=1.0, inertia=1e6)  # (nearly) no rotation: the rows decouple
+    d.add_box(b, (0.5, 0.5), friction=100.0)
+    m, st = _single(d)
+    for _ in range(20):
+        oracle.step_(m, st, s, F32(1 / 60))
+    k = int(np.nonzero(st.contacts.touching[0])[0][0])
+    for speed in (1.0, -1.0):
+        x = oracle.copy(st)
+        x.contacts.tangent_speed[0, k] = speed
+        oracle.step_(m, x, s, F32(1 / 60))
+        assert float(x.bodies.v[0, 1, 0]) == pytest.approx(speed, abs=1e-3)
+        assert abs(float(x.bodies.w[0, 1])) < 1e-3
+
+
+def test_static_body_takes_the_last_islands_awake_flag(oracle):
+    """A static body shared by several islands ends the step with the awake flag of the highest-numbered island that
+    included it (step.py:173-194). Islands are numbered in seed order, newest body first (island.py:8-9). Two boxes
+    on one frictionless slab: body 1 drops onto it and then slides (its contact is the newer), body 2 rests on it
+    from the start and falls asleep after time_to_sleep. Body 1 is seeded last, so in the step where body 2's island
+    falls asleep the slab follows body 1's island and stays awake, whatever the contacts' slot order."""
+    s = S.stock(gravity=(0.0, -10.0))
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (0.0, -0.5))
+    d.add_box(g, (50.0, 0.5), friction=0.0)
+    slide = d.add_body(wd.DYNAMIC, (0.0, 1.0), velocity=(2.0, 0.0), mass=1.0, inertia=F32(1) / F32(6))
+    d.add_box(slide, (0.5, 0.5), friction=0.0)
+    rest = d.add_body(wd.DYNAMIC, (-20.0, 0.5), mass=1.0, inertia=F32(1) / F32(6))
+    d.add_box(rest, (0.5, 0.5), friction=0.0)
+    m, st = _single(d)
+    for _ in range(45):
+        oracle.step_(m, st, s, F32(1 / 60))
+        if not st.bodies.awake[0, rest]:
+            break
+    live = np.nonzero(st.contacts.touching[0])[0]
+    by_body = {int(m.fixture_body[st.contacts.fb[0, k]]): int(k) for k in live}
+    assert by_body[rest] < by_body[slide]  # the resting box's contact holds the lower slot
+    assert not st.bodies.awake[0, rest] and st.bodies.awake[0, slide]
+    assert st.bodies.awake[0, g]
+
+
+@pytest.mark.parametrize("kind", ["revolute_v24", "revolute_v23", "prismatic", "weld"])
+def test_joint_error_keeps_position_iterations_going(oracle, kind):
+    """An island stops its position iterations only once its joints report both their linear error within
+    linear_slop and their angular error within angular_slop (step.py:197-251, joints.py:462-606). A bar joined to a
+    static body, with no linear error and an angular error far beyond angular_slop: a revolute pivoted at the bar's
+    centre 0.8 rad past its upper limit (each pass turns it back by at most max_angular_correction and moves no
+    anchor, so three passes leave less error than one, and eight less than three); a prismatic or weld joint at the
+    bar's end turned 0.9 rad from its reference angle (one pass
+    removes the angular error but, the anchor being off the bar's centre, leaves a linear one that the second pass
+    corrects: one pass and three end in different poses)."""
+    import dataclasses
+    s = dataclasses.replace(S.stock(gravity=(0.0, 0.0)), revolute_v24=(kind != "revolute_v23"), allow_sleep=False)
+
+    def run(iters):
+        d = wd.WorldDef(dataclasses.replace(s, position_iterations=iters))
+        g = d.add_body(wd.STATIC, (0.0, 0.0))
+        ang = 0.9
+        c, sn = np.cos(ang), np.sin(ang)
+        b = d.add_body(wd.DYNAMIC, (c, sn), ang, mass=1.0, inertia=0.3)
+        d.add_box(b, (1.0, 0.1))
+        if kind.startswith("revolute"):  # pivot at the bar's centre: correcting the angle moves no anchor
+            d.add_revolute(g, b, (c, sn), (0.0, 0.0), limits=(-0.1, 0.1))
+        elif kind == "prismatic":
+            d.add_prismatic(g, b, (0.0, 0.0), (-1.0, 0.0), axis=(c, sn))
+        else:
+            d.add_weld(g, b, (0.0, 0.0), (-1.0, 0.0))
+        m, st = _single(d)
+        oracle.step_(m, st, d.settings, F32(1 / 60))
+        return np.concatenate([st.bodies.c[0, 1], st.bodies.a[0, 1:2]]).astype(np.float64)
+    poses = [run(n) for n in (1, 3, 8)]
+    if kind.startswith("revolute"):
+        errs = [abs(p[2] - 0.1) for p in poses]
+        assert errs[0] > errs[1] > errs[2], errs
+    else:
+        assert np.abs(poses[0] - poses[1]).max() > 1e-4, poses
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# SolveTOI's bookkeeping: the sub-step cap, re-search after a move, the island walk's restore   (toi.py:462-716)
+
+def _ball_between_walls(speed):
+    s = S.stock(gravity=(0.0, 0.0), continuous_physics=True, max_translation=100.0)
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (0.0, 0.0))
+    d.add_box(g, (0.1, 2.0), center=(-0.45, 0.0), restitution=1.0)
+    d.add_box(g, (0.1, 2.0), center=(0.45, 0.0), restitution=1.0)
+    b = d.add_body(wd.DYNAMIC, (0.0, 0.0), velocity=(speed, 0.0), mass=1.0, inertia=1.0)
+    d.add_circle(b, 0.1, restitution=1.0)
+    m, st = _single(d)
+    return s, m, st
+
+
+def test_toi_sub_step_cap_and_re_search(oracle):
+    """A ball (radius 0.1, restitution 1) at 700 m/s between two walls 0.7 apart: every TOI event reflects its
+    velocity exactly, and after each event the moved ball's contacts get their TOIs searched again (the wall it now
+    heads to included). A contact takes events while its count is at most b2_maxSubSteps = 8, so each wall takes 9
+    events: 18 in the step, then both contacts are skipped and the ball leaves through a wall at full speed."""
+    s, m, st = _ball_between_walls(700.0)
+    oracle.step_(m, st, s, F32(1 / 60))
+    assert int(st.toi.events[0]) == 18
+    live = st.contacts.pair[0] >= 0
+    assert sorted(st.toi.count[0][live].tolist()) == [9, 9]
+    assert abs(float(st.bodies.c[0, 1, 0])) > 0.55 and abs(float(st.bodies.v[0, 1, 0])) == 700.0
+    # slower, the same cage never reaches the cap: fewer events, all of them reflections
+    s, m, st = _ball_between_walls(200.0)
+    oracle.step_(m, st, s, F32(1 / 60))
+    assert 2 <= int(st.toi.events[0]) < 18 and abs(float(st.bodies.c[0, 1, 0])) < 0.25
+
+
+def test_toi_walk_restores_a_body_it_does_not_keep(oracle):
+    """The TOI island walk advances each candidate neighbour to the event's alpha to update their contact, and puts
+    it back where it was when the contact does not touch (toi.py:640-680). A bullet ball flies into a wall past a
+    slowly rising box whose fat box its swept box overlaps (so they share a contact) but which it never touches: after
+    the event the box stands exactly where Solve put it, c + h v."""
+    s = S.stock(gravity=(0.0, 0.0), continuous_physics=True, max_translation=100.0)
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (0.0, 0.0))
+    d.add_box(g, (0.05, 2.0), center=(4.0, 0.0))
+    ball = d.add_body(wd.DYNAMIC, (0.0, 0.0), velocity=(300.0, 0.0), mass=1.0, inertia=1.0, bullet=True)
+    d.add_circle(ball, 0.1)
+    box = d.add_body(wd.DYNAMIC, (2.0, 0.25), velocity=(0.0, 1.0), mass=1.0, inertia=1.0)
+    d.add_box(box, (0.5, 0.1))
+    m, st = _single(d, 8)
+    h = F32(1 / 60)
+    c0 = st.bodies.c[0, box].copy()
+    dbg = toi_trace(1, wd.dims(st))
+    oracle.step_(m, st, s, h, debug=dbg)
+    assert int(st.toi.events[0]) >= 1
+    slot = int(dbg["toi_event_slot"][0, 0])
+    assert {int(m.fixture_body[st.contacts.fa[0, slot]]), int(m.fixture_body[st.contacts.fb[0, slot]])} == {0, ball}
+    shared = [k for k in range(st.contacts.pair.shape[1]) if st.contacts.pair[0, k] >= 0 and
+              {int(m.fixture_body[st.contacts.fa[0, k]]), int(m.fixture_body[st.contacts.fb[0, k]])} == {ball, box}]
+    assert shared and not st.contacts.touching[0, shared[0]]
+    want = np.array([c0[0] + h * F32(0.0), c0[1] + h * F32(1.0)], F32)  # semi-implicit Euler, no force
+    assert np.array_equal(st.bodies.c[0, box], want)
+    assert float(st.bodies.c[0, ball, 0]) < 3.95
+
+
+def test_angular_sleep_tolerance_is_squared(oracle):
+    """A body is slow enough to sleep when w^2 <= angular_sleep_tolerance^2 (2 degrees a second) and
+    |v|^2 <= linear_sleep_tolerance^2 (step.py:153-168): spinning at 0.1 rad/s it never sleeps, at 0.02 rad/s it
+    falls asleep after time_to_sleep."""
+    s = S.stock(gravity=(0.0, 0.0))
+    for w0, sleeps in ((0.1, False), (0.02, True)):
+        d = wd.WorldDef(s)
+        b = d.add_body(wd.DYNAMIC, (0.0, 0.0), 0.0, angular_velocity=w0, mass=1.0, inertia=1.0)
+        d.add_box(b, (0.5, 0.5))
+        m, st = _single(d)
+        for _ in range(45):
+            oracle.step_(m, st, s, F32(1 / 60))
+        assert bool(st.bodies.awake[0, 0]) != sleeps, w0
+
+
+def test_gravity_scale_and_lateral_gravity(oracle):
+    """Integration uses gravity_scale x gravity on both axes (step.py:86-93): with gravity (3, -10) and a gravity
+    scale of 0.5 a free body's velocity after one step is exactly h (0.5 g) in float32."""
+    s = S.stock(gravity=(3.0, -10.0))
+    d = wd.WorldDef(s)
+    b = d.add_body(wd.DYNAMIC, (0.0, 0.0), mass=1.0, inertia=1.0, gravity_scale=0.5)
+    d.add_box(b, (0.5, 0.5))
+    m, st = _single(d)
+    h = F32(1 / 60)
+    oracle.step_(m, st, s, h)
+    one = F32(1)
+    want = [F32(F32(0) + h * (F32(0.5) * F32(3.0) + one * F32(0))),
+            F32(F32(0) + h * (F32(0.5) * F32(-10.0) + one * F32(0)))]
+    assert st.bodies.v[0, 0].tolist() == want
+
+
+@pytest.mark.parametrize("damping", [0.0, 0.5])
+def test_soft_weld_velocity_row(oracle, damping):
+    """b2WeldJoint with frequency > 0 is a spring on the angle (joints.py:125-144, 375-400): with m = 1 / (iA + iB),
+    omega = 2 pi f, d = 2 m zeta omega, k = m omega^2, gamma = 1 / (h (d + h k)) and bias = C h k gamma, one velocity
+    pass from rest gives the angular impulse -(bias) / (invM + gamma). A box welded at its centre to a static body
+    and turned 0.3 rad from the reference angle, no warm start, one velocity and no position iteration: its spin after
+    the step is iB times that impulse (float64 closed form, to 1e-5)."""
+    import dataclasses
+    s = dataclasses.replace(S.stock(gravity=(0.0, 0.0)), velocity_iterations=1, position_iterations=0,
+                            warm_starting=False, allow_sleep=False)
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (0.0, 0.0))
+    C, inertia, f = 0.3, 0.5, 2.0
+    b = d.add_body(wd.DYNAMIC, (0.0, 0.0), C, mass=1.0, inertia=inertia)
+    d.add_box(b, (0.5, 0.5))
+    d.add_weld(g, b, (0.0, 0.0), (0.0, 0.0), frequency=f, damping=damping)
+    m, st = _single(d)
+    h = 1.0 / 60.0
+    oracle.step_(m, st, s, F32(h))
+    iB = 1.0 / float(F32(inertia))
+    mass = 1.0 / iB
+    omega = 2.0 * np.pi * f
+    dd, kk = 2.0 * mass * damping * omega, mass * omega * omega
+    gamma = 1.0 / (h * (dd + h * kk))
+    bias = float(F32(C)) * h * kk * gamma
+    want = iB * (-bias / (iB + gamma))
+    assert float(st.bodies.w[0, 1]) == pytest.approx(want, rel=1e-5)
+
+
+def test_toi_integration_clamp_is_per_step(oracle):
+    """With clamps_per_second, the TOI island's integration over the rest of the step (h = (1 - alpha) dt) clamps
+    the translation at max_translation x dt, the step's, not x h (toi.py:780-790). A ball at 50 m/s (max_translation
+    50 m/s) meets a wall of restitution 3 and leaves at 150 m/s; over h the translation 150 h exceeds 50 dt, so its
+    speed is scaled to exactly 50 dt / h = 50 / (1 - alpha)."""
+    import dataclasses
+    s = dataclasses.replace(S.stock(gravity=(0.0, 0.0), continuous_physics=True, max_translation=50.0),
+                            clamps_per_second=True, allow_sleep=False)
+    d = wd.WorldDef(s)
+    g = d.add_body(wd.STATIC, (0.0, 0.0))
+    d.add_box(g, (0.05, 2.0), center=(0.5, 0.0), restitution=3.0)
+    ball = d.add_body(wd.DYNAMIC, (0.0, 0.0), velocity=(50.0, 0.0), mass=1.0, inertia=1.0)
+    d.add_circle(ball, 0.1, restitution=3.0)
+    m, st = _single(d)
+    dbg = toi_trace(1, wd.dims(st))
+    oracle.step_(m, st, s, F32(1 / 60), debug=dbg)
+    assert int(st.toi.events[0]) >= 1
+    alpha = float(dbg["toi_event_alpha"][0, 0].view(np.float32))
+    assert alpha < 0.6
+    assert float(st.bodies.v[0, 1, 0]) == pytest.approx(-50.0 / (1.0 - alpha), rel=1e-5)
