@@ -666,4 +666,4 @@ def test_toi_bookkeeping_parity(oracle, case):
         st.bodies.v[:, 2, 1] = rng.uniform(-2.0, 2.0, 64).astype(np.float32)
     events = []
     _run(m, st, s, np.float32(1 / 60), 4, oracle, on_step=lambda k, r, d: events.append(int(r.toi.events.sum())))
-    assert events[0] > 64
+    assert events[0] > (64 if case == "cage" else 32)
