@@ -316,6 +316,19 @@ def scene_toi_plank(s, ball_bullet=False, plank_bullet=False):
     return d
 
 
+def scene_kinematic_wall(s):
+    """A thin kinematic wall on x = 0 rising at 0.5 m/s (at x = -0 with tests/util.negative_zero_kinematic) and two
+    boxes flying into it at 300 and 250 m/s, one from each side: TOI events whose side without mass is kinematic."""
+    d = wd.WorldDef(s)
+    k = d.add_body(wd.KINEMATIC, (0.0, 0.0), 0.0, (0.0, 0.5), 0.0)
+    d.add_box(k, (0.05, 3.0))
+    a = d.add_body(wd.DYNAMIC, (-3.0, 0.5), 0.2, (300.0, 10.0), 2.0, mass=1.0, inertia=0.02, continuous=True)
+    d.add_box(a, (0.15, 0.1))
+    b = d.add_body(wd.DYNAMIC, (3.0, -0.5), -0.3, (-250.0, -5.0), -3.0, mass=0.8, inertia=0.02, continuous=True)
+    d.add_box(b, (0.1, 0.12))
+    return d
+
+
 def scene_edges(s):
     """Native edge shapes: an open chain with convex and concave corners and a collinear run, a closed loop, an
     isolated two-sided segment and a segment with ghost vertices but no neighbours; boxes slide across the chain's
@@ -369,6 +382,7 @@ TEST_SCENES = {
     "stock_bullets": (scene_stock_bullets, lambda: _toi(unity=False), 16),
     "island_walk": (scene_island_walk, _toi, 32),
     "edges": (scene_edges, _toi, 32),
+    "kinematic_wall": (scene_kinematic_wall, lambda: _toi(unity=False, gravity=(0.0, 0.0)), 8),
     "toi_tie": (scene_toi_tie, lambda: Settings.stock(gravity=(0.0, 0.0), continuous_physics=True), 8),
     "toi_tie_oldest": (scene_toi_tie, lambda: Settings.stock(gravity=(0.0, 0.0), continuous_physics=True,
                                                              toi_tie_oldest=True), 8),

@@ -20,7 +20,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from util import b2, perturbed, wd
+from util import b2, negative_zero_kinematic, perturbed, wd
 import scene_defs
 
 _abi = importlib.import_module("getting-over-it-rl_amd.box2d._abi")
@@ -218,12 +218,25 @@ def test_config5_sanitized(host_step, tmp_path, packed):
 
 
 @pytest.mark.parametrize("name", ["pile", "joints", "joints_v23", "misc", "hammer_chain", "multi_event",
-                                  "island_walk", "toi_tie", "edges", "poly_angles"])
+                                  "island_walk", "toi_tie", "edges", "poly_angles", "ball_wall", "stock_bullets",
+                                  "toi_plank_bullet"])
 def test_scenes_sanitized(host_step, tmp_path, name):
     """The test scenes, a few perturbed copies each: every shape pair, joint type, TOI path and edge case."""
     s, m, st = scene_defs.build_test_scene(name, iterations=(8, 3))
     p = tmp_path / "scn.bin"
     write_scenario(p, m, perturbed(st, 16), s, 1.0 / 60.0, 90, False)
+    check(run(host_step, p, "step"))
+
+
+def test_negative_zero_kinematic_sanitized(host_step, tmp_path):
+    """TOI events against a kinematic wall that starts at x = -0 (a side without mass in the TOI position passes).
+    b2Sweep::Advance turns a resting -0 coordinate into +0 (c0 + beta * (c - c0) with c - c0 = +0) before the passes
+    see it; the -0 until then, and the +0 after, follow the oracle."""
+    s, m, st = scene_defs.build_test_scene("kinematic_wall", iterations=(8, 3))
+    st = negative_zero_kinematic(perturbed(st, 16))
+    assert np.signbit(st.bodies.c[:, 0, 0]).all()
+    p = tmp_path / "scn.bin"
+    write_scenario(p, m, st, s, 1.0 / 60.0, 40, False)
     check(run(host_step, p, "step"))
 
 

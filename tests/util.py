@@ -40,3 +40,19 @@ def perturbed(state, n, seed=1, sigma=0.2):
     dv[0] = 0.0
     st.bodies.v[...] = st.bodies.v + dv
     return st
+
+
+
+def negative_zero_kinematic(state):
+    """The State with the zero x coordinate, x velocity, angle and angular velocity of its kinematic bodies made -0
+    (c, c0, xf.p, v, a, a0, w, xf.q's sine): such a body keeps the -0 through its integration (-0 + h * -0), and as
+    the side without mass of a TOI position row its update c - 0 * P is not an identity (-0 - -0 is +0)."""
+    bd = state.bodies
+    kin = (np.asarray(bd.type) == wd.KINEMATIC)
+    nz = np.float32(-0.0)
+    for leaf in (bd.c, bd.c0, bd.xf_p, bd.v):
+        leaf[..., 0] = np.where(kin & (leaf[..., 0] == 0.0), nz, leaf[..., 0])
+    for leaf in (bd.a, bd.a0, bd.w):
+        leaf[...] = np.where(kin & (leaf == 0.0), nz, leaf)
+    bd.xf_q[..., 0] = np.where(kin & (bd.xf_q[..., 0] == 0.0), nz, bd.xf_q[..., 0])
+    return state
