@@ -58,6 +58,10 @@ __device__ __forceinline__ World make_world(const DModel& m, const Launch& L, in
 __device__ __forceinline__ Rows contact_rows(const Launch& L, int w0, int wl) {
     return rows_of(L.scratch, L.C, CF_N, L.wpw, w0 / L.wpw, wl);
 }
+// The contact rows' tile read world-major, for SolveTOI (Solve's rows are dead by then).
+__device__ __forceinline__ Rows toi_rows(const Launch& L, int w0, int wl) {
+    return rows_world_major(L.scratch, L.C, CF_N, L.wpw, w0 / L.wpw, wl);
+}
 __device__ __forceinline__ Rows joint_rows(const Launch& L, int w0, int wl) {
     uint32_t* region = L.scratch + (size_t)L.C * CF_N * ((size_t)gridDim.x * L.wpw);
     return rows_of(region, L.J, JF_N, L.wpw, w0 / L.wpw, wl);
@@ -118,6 +122,7 @@ struct LaneViews {
     Coop co;
     Bodies bd;
     Rows CR;
+    Rows TR;  // CR's tile world-major (toi_rows)
     BlockCopy bc;
 };
 __device__ __forceinline__ LaneViews lane_views(const DModel& m, const Launch& L, int* lds, int w0, int lane) {
@@ -130,6 +135,7 @@ __device__ __forceinline__ LaneViews lane_views(const DModel& m, const Launch& L
     v.bd.B = L.B;
     v.bd.st = v.W.S;
     v.CR = contact_rows(L, w0, valid ? v.lm.wl : 0);
+    v.TR = toi_rows(L, w0, valid ? v.lm.wl : 0);
     v.bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
     return v;
 }
@@ -155,7 +161,7 @@ __device__ __forceinline__ void step_worlds(const DModel& m, const Launch& L, in
     }
     bool capped = false;
     if (L.s.continuous_physics)
-        capped = solve_toi_world<kOpaqueToi>(m, W, v.bd, v.CR, L.s, L.dt, valid, lm.leader, v.co, v.bc, L.dbg);
+        capped = solve_toi_world<kOpaqueToi>(m, W, v.bd, v.TR, L.s, L.dt, valid, lm.leader, v.co, v.bc, L.dbg);
     if (valid) {
         const float dt = L.dt;
         if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
@@ -209,7 +215,8 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
             }
             bool capped = false;
             if (L.s.continuous_physics)
-                capped = solve_toi_world<kOpaqueToi>(m, W, bd, CR, L.s, L.dt, valid, lm.leader, co, bc, L.dbg);
+                capped = solve_toi_world<kOpaqueToi>(m, W, bd, toi_rows(L, w0, valid ? lm.wl : 0), L.s, L.dt, valid,
+                                                     lm.leader, co, bc, L.dbg);
             if (valid) {
                 const float dt = L.dt;
                 if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;

@@ -90,6 +90,8 @@ struct Coop {
         return W;
     }
     GOI_D Rows task_rows(int o) const { return rows_of(rows, base.C, CF_N, base.S, w0 / base.S, o); }
+    // world o's rows in SolveTOI (rows_world_major over the same tile)
+    GOI_D Rows toi_rows(int o) const { return rows_world_major(rows, base.C, CF_N, base.S, w0 / base.S, o); }
 };
 
 // Called by all lanes of the block together; `my` = this lane's task count: the world's count on the first lane of

@@ -286,7 +286,7 @@ GOI_D int toi_search_prepare(const DModel& m, const World& W, const Rows& CR, co
 
 // pass 2: the TOI of task i of the block's world o
 GOI_D void toi_task(const DModel& m, const Coop& co, int o, int i, float linear_slop) {
-    const Rows R = co.task_rows(o);
+    const Rows R = co.toi_rows(o);
     Sweep sa, sb;
     sa.lc = R.get2(i, TT_SA); sa.c0 = R.get2(i, TT_SA + 2); sa.c = R.get2(i, TT_SA + 4);
     sa.a0 = R.getf(i, TT_SA + 6); sa.a = R.getf(i, TT_SA + 7);

@@ -632,6 +632,16 @@ GOI_D Rows rows_of(uint32_t* region, int nrows, int nf, int S, int tile, int lan
     R.S = S;
     return R;
 }
+// The same tile read world-major: world `lane` owns words [lane * nrows * nf, (lane + 1) * nrows * nf) of it, a row's
+// fields contiguous. For rows that one world writes while the block's other worlds write none (SolveTOI's task
+// snapshots and event islands): its stores then fill whole lines instead of one 4-byte word in each 32 bytes.
+GOI_D Rows rows_world_major(uint32_t* region, int nrows, int nf, int S, int tile, int lane) {
+    Rows R;
+    R.base = region + (size_t)tile * ((size_t)nrows * nf * S) + (size_t)lane * ((size_t)nrows * nf);
+    R.nf = nf;
+    R.S = 1;
+    return R;
+}
 
 // contact constraint row fields
 enum {
