@@ -235,21 +235,46 @@ GOI_D bool pair_rule(const DModel& m, const World& W, const GoiSettings& s, int 
 // Box2D's search walks the contact list once: for each contact without a cached TOI it aligns the two sweeps
 // (b2Sweep::Advance of the body with the smaller alpha0) and computes the TOI, then keeps the minimum. Alignments
 // depend only on alpha0 values, never on TOI results, so the walk splits into three passes with the same results:
-//   1. toi_search_prepare (each world, list order): the alignments, with each TOI's inputs (fixtures, both sweeps
-//      as aligned at that contact, alpha0) snapshotted into the world's contact row `task`;
+//   1. toi_search_prepare (each world, list order): the alignments, and the list of the contacts that need a TOI
+//      (the world's newp array);
 //   2. toi_task under coop_run (the whole wavefront): the TOIs of all worlds of the block, over all 64 lanes;
 //   3. toi_search_pick (each world, list order): the minimum with the reference's tie rule.
+// A TOI's inputs are the two sweeps as aligned at its contact. They stay the bodies' sweeps in the workspace until
+// one of the two bodies is advanced again later in the walk: only then (rarely: a body met by bodies of two larger
+// alpha0 values) are the task's sweeps and alpha0 copied into its row of the world's TOI rows (the task is frozen,
+// kFrozenTask in its newp entry), before the advance. Pass 2 reads the sweeps of the other tasks from the workspace.
 
-// task snapshot fields in a contact row
-enum { TT_FA = 0, TT_FB, TT_ALPHA0, TT_SA, TT_SB = TT_SA + 8, TT_N = TT_SB + 8 };
+// task snapshot fields in a TOI row
+enum { TT_ALPHA0 = 0, TT_SA, TT_SB = TT_SA + 8, TT_N = TT_SB + 8 };
 static_assert(TT_N <= CF_N, "TOI task snapshot must fit a contact row");
+constexpr int kFrozenTask = 1 << 30;  // newp flag of a task whose inputs are in its row
 
 GOI_D void put_sweep(const Rows& R, int row, int f, const Sweep& sw) {
     R.set2(row, f, sw.lc); R.set2(row, f + 2, sw.c0); R.set2(row, f + 4, sw.c);
     R.setf(row, f + 6, sw.a0); R.setf(row, f + 7, sw.a);
 }
+GOI_D Sweep get_sweep(const Rows& R, int row, int f) {
+    Sweep sw;
+    sw.lc = R.get2(row, f); sw.c0 = R.get2(row, f + 2); sw.c = R.get2(row, f + 4);
+    sw.a0 = R.getf(row, f + 6); sw.a = R.getf(row, f + 7);
+    return sw;
+}
 
-// pass 1; returns the number of TOI tasks, whose slots are W.newp(0 .. n-1)
+// freezes tasks 0 .. nt-1 that involve body b and are not frozen yet (b is about to be advanced)
+GOI_D void freeze_tasks(const World& W, const Rows& CR, int nt, int b) {
+    for (int t = 0; t < nt; ++t) {
+        const int k = W.newp(t);
+        if (k & kFrozenTask) continue;
+        const int A = W.ba(k), Bb = W.bb(k);
+        if (A != b && Bb != b) continue;
+        CR.setf(t, TT_ALPHA0, W.f(GOI_T_ALPHA0, A));  // both bodies' alpha0 since the task's alignment
+        put_sweep(CR, t, TT_SA, body_sweep(W, A));
+        put_sweep(CR, t, TT_SB, body_sweep(W, Bb));
+        W.newp(t) = k | kFrozenTask;
+    }
+}
+
+// pass 1; returns the number of TOI tasks, whose slots are W.newp(0 .. n-1) (with kFrozenTask on frozen ones)
 GOI_D int toi_search_prepare(const DModel& m, const World& W, const Rows& CR, const GoiSettings& s) {
     const int n = list_order(W);
     int nt = 0;
@@ -265,17 +290,15 @@ GOI_D int toi_search_prepare(const DModel& m, const World& W, const Rows& CR, co
         });
         for (unsigned long long left = need; left; left &= left - 1) {
             const int c = W.order(q0 + __builtin_ctzll(left));
-            const int fa = W.fa(c), fb = W.fb(c);
             const int A = W.ba(c), Bb = W.bb(c);
             const float alA = W.f(GOI_T_ALPHA0, A), alB = W.f(GOI_T_ALPHA0, Bb);
-            float alpha0 = alA;
-            if (alA < alB) { alpha0 = alB; sweep_advance(W, A, alpha0); }
-            else if (alB < alA) { alpha0 = alA; sweep_advance(W, Bb, alpha0); }
-            CR.seti(nt, TT_FA, fa);
-            CR.seti(nt, TT_FB, fb);
-            CR.setf(nt, TT_ALPHA0, alpha0);
-            put_sweep(CR, nt, TT_SA, body_sweep(W, A));
-            put_sweep(CR, nt, TT_SB, body_sweep(W, Bb));
+            if (alA < alB) {
+                freeze_tasks(W, CR, nt, A);
+                sweep_advance(W, A, alB);
+            } else if (alB < alA) {
+                freeze_tasks(W, CR, nt, Bb);
+                sweep_advance(W, Bb, alA);
+            }
             W.newp(nt++) = c;
             W.set_tflag(c, 1);  // the toi itself arrives in pass 2
         }
@@ -286,18 +309,25 @@ GOI_D int toi_search_prepare(const DModel& m, const World& W, const Rows& CR, co
 
 // pass 2: the TOI of task i of the block's world o
 GOI_D void toi_task(const DModel& m, const Coop& co, int o, int i, float linear_slop) {
-    const Rows R = co.toi_rows(o);
-    Sweep sa, sb;
-    sa.lc = R.get2(i, TT_SA); sa.c0 = R.get2(i, TT_SA + 2); sa.c = R.get2(i, TT_SA + 4);
-    sa.a0 = R.getf(i, TT_SA + 6); sa.a = R.getf(i, TT_SA + 7);
-    sb.lc = R.get2(i, TT_SB); sb.c0 = R.get2(i, TT_SB + 2); sb.c = R.get2(i, TT_SB + 4);
-    sb.a0 = R.getf(i, TT_SB + 6); sb.a = R.getf(i, TT_SB + 7);
-    const float alpha0 = R.getf(i, TT_ALPHA0);
-    float beta;
-    const int st = time_of_impact(proxy_of(m, R.geti(i, TT_FA)), sa, proxy_of(m, R.geti(i, TT_FB)), sb, linear_slop,
-                                  beta);
     const World W = co.world(o);
-    W.ttoi(W.newp(i)) = st == kToiTouching ? bmin(alpha0 + (1.0f - alpha0) * beta, 1.0f) : 1.0f;
+    const int k = W.newp(i);
+    const int c = k & ~kFrozenTask;
+    const int A = W.ba(c), Bb = W.bb(c);
+    Sweep sa, sb;
+    float alpha0;
+    if (k & kFrozenTask) {
+        const Rows R = co.toi_rows(o);
+        alpha0 = R.getf(i, TT_ALPHA0);
+        sa = get_sweep(R, i, TT_SA);
+        sb = get_sweep(R, i, TT_SB);
+    } else {
+        alpha0 = W.f(GOI_T_ALPHA0, A);
+        sa = body_sweep(W, A);
+        sb = body_sweep(W, Bb);
+    }
+    float beta;
+    const int st = time_of_impact(proxy_of(m, W.fa(c)), sa, proxy_of(m, W.fb(c)), sb, linear_slop, beta);
+    W.ttoi(c) = st == kToiTouching ? bmin(alpha0 + (1.0f - alpha0) * beta, 1.0f) : 1.0f;
 }
 
 // pass 3; returns whether an event was found
