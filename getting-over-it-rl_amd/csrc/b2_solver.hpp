@@ -423,4 +423,126 @@ GOI_D float solve_prow(const Bodies& bd, const PRow& r, float baumgarte, float m
     return min_sep;
 }
 
+// ---- TOI position passes with one moving body
+//
+// In b2Island::SolveTOI's position passes (toi.py:738-760) only the TOI pair has mass. When exactly one of the pair
+// has mass (M; the other is static or kinematic, as in every event of a dynamic body against the terrain), every row
+// has M on one side and a side without mass (mass and inertia 0) on the other. That side's updates c - 0 * P and
+// a - 0 * cross(r, P), and its term 0 * rn * rn of K, are identities when its c and a are finite, below 2^60 and not
+// -0, and p and the impulse stay below 2^60 (which bounds r, rn and P). The passes then need only M's pose, kept in
+// registers, and per row the fixed side's transform and the normal, plane point or clip points it alone determines,
+// evaluated once per event: solve_prow's floats for M with a third of its instructions (a wave running one world's
+// TOI events alone issues one instruction every few clocks, so the count is the time). K is m + i * rn * rn of M,
+// M's update c + ms * P and a + is * cross(r, P) with ms, is = +-m, +-i (x - y is x + -y), and the face-B normal
+// flip a multiply by -1. The bounds are checked by one running sum over the passes (an infinity or NaN stays in it);
+// when it fails, or a row does not have this form, solve_prow's passes run from the same poses.
+struct TRow {
+    V2 lc;      // M's local center
+    V2 u0, u1;  // M's local vectors: kind 1 the local normal and point, kind 2 the two local points
+    V2 k0, k1;  // the fixed side's: kind 1 the two clip points, kind 2 the normal (before the face-B flip) and the
+                // plane point
+    float radA, radB, ms, is;
+    int bits;   // point count | 4 when M holds the reference face (kind 1; else kind 2, M holds the incident
+                // points) | 8 for face B (the normal's sign)
+};
+
+// a TOI row in a row's velocity-solver fields (the event sets those up, impulses included, after the passes)
+enum { TF_BITS = CF_RA0, TF_LC, TF_U0 = TF_LC + 2, TF_U1 = TF_U0 + 2, TF_K0 = TF_U1 + 2, TF_K1 = TF_K0 + 2,
+       TF_RADA = TF_K1 + 2, TF_RADB, TF_MS, TF_IS, TF_END };
+static_assert(TF_END <= CF_LN, "a TOI row must fit the velocity-solver fields");
+
+GOI_D void store_trow(const Rows& R, int i, const TRow& t) {
+    R.seti(i, TF_BITS, t.bits); R.set2(i, TF_LC, t.lc); R.set2(i, TF_U0, t.u0); R.set2(i, TF_U1, t.u1);
+    R.set2(i, TF_K0, t.k0); R.set2(i, TF_K1, t.k1);
+    R.setf(i, TF_RADA, t.radA); R.setf(i, TF_RADB, t.radB); R.setf(i, TF_MS, t.ms); R.setf(i, TF_IS, t.is);
+}
+GOI_D TRow load_trow(const Rows& R, int i) {
+    TRow t;
+    t.bits = R.geti(i, TF_BITS); t.lc = R.get2(i, TF_LC); t.u0 = R.get2(i, TF_U0); t.u1 = R.get2(i, TF_U1);
+    t.k0 = R.get2(i, TF_K0); t.k1 = R.get2(i, TF_K1);
+    t.radA = R.getf(i, TF_RADA); t.radB = R.getf(i, TF_RADB); t.ms = R.getf(i, TF_MS); t.is = R.getf(i, TF_IS);
+    return t;
+}
+
+// Row r as a TRow for the moving body M (mass m, inertia i); false when the row is not of the form above or the fixed
+// side fails the guard.
+GOI_D bool make_trow(const Bodies& bd, const PRow& r, int M, float m, float i, TRow& t) {
+    const bool mvB = r.ib == M;
+    if (mvB == (r.ia == M) || r.mtype == kCircles) return false;
+    const int f = mvB ? r.ia : r.ib;
+    const V2 cF = bd.c(f);
+    const float aF = bd.a(f);
+    const bool ok = fabsf(cF.x) < 0x1p60f && fabsf(cF.y) < 0x1p60f && fabsf(aF) < 0x1p60f &&
+                    __float_as_uint(cF.x) != 0x80000000u && __float_as_uint(cF.y) != 0x80000000u &&
+                    __float_as_uint(aF) != 0x80000000u && fabsf(r.ln.x) < 4.0f && fabsf(r.ln.y) < 4.0f &&
+                    !(__float_as_uint(m) >> 31) && !(__float_as_uint(i) >> 31);
+    Xf xf;
+    xf.q = rot_of(aF);
+    xf.p = cF - mul(xf.q, mvB ? r.lcA : r.lcB);
+    const bool fa = r.mtype == kFaceA;
+    const bool mref = fa != mvB;
+    if (mref) {
+        t.u0 = r.ln;
+        t.u1 = r.lp;
+        t.k0 = mul(xf, r.pl0);
+        t.k1 = mul(xf, r.pl1);
+    } else {
+        t.u0 = r.pl0;
+        t.u1 = r.pl1;
+        t.k0 = mul(xf.q, r.ln);
+        t.k1 = mul(xf, r.lp);
+    }
+    t.lc = mvB ? r.lcB : r.lcA;
+    t.radA = r.radA;
+    t.radB = r.radB;
+    t.ms = mvB ? m : -m;
+    t.is = mvB ? i : -i;
+    t.bits = r.cnt | (mref ? 4 : 0) | (fa ? 0 : 8);
+    return ok;
+}
+
+// One pass over a TRow of kind kKind on M's pose; acc gathers the guard's magnitudes.
+template <int kKind>
+GOI_D float trow_pass(const TRow& t, float baumgarte, float linear_slop, float max_linear_correction, V2& cM,
+                      float& aM, float& acc) {
+    const float sg = (t.bits & 8) ? -1.0f : 1.0f;
+    const V2 n2 = sg * t.k0;  // kind 2's normal
+    float min_sep = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        if (j >= (t.bits & 3)) break;
+        Xf xf;
+        xf.q = rot_of_small(aM);
+        xf.p = cM - mul(xf.q, t.lc);
+        V2 cp, n;
+        float sep;
+        if constexpr (kKind == 1) {
+            const V2 n1 = mul(xf.q, t.u0);
+            cp = j == 0 ? t.k0 : t.k1;
+            sep = (dot(cp - mul(xf, t.u1), n1) - t.radA) - t.radB;
+            n = sg * n1;
+        } else {
+            cp = mul(xf, j == 0 ? t.u0 : t.u1);
+            sep = (dot(cp - t.k1, t.k0) - t.radA) - t.radB;
+            n = n2;
+        }
+        const V2 r = cp - cM;
+        min_sep = bmin(min_sep, sep);
+        const float C = bclamp(baumgarte * (sep + linear_slop), -max_linear_correction, 0.0f);
+        const float rn = cross(r, n);
+        const float K = fabsf(t.ms) + fabsf(t.is) * rn * rn;
+        const float imp = K > 0.0f ? -C / K : 0.0f;
+        const V2 P = imp * n;
+        cM = cM + t.ms * P;
+        aM = aM + t.is * cross(r, P);
+        acc = acc + ((fabsf(cp.x) + fabsf(cp.y)) + (fabsf(imp) + fabsf(aM) * 0x1p40f));
+    }
+    return min_sep;
+}
+GOI_D float trow_pass(const TRow& t, float baumgarte, float linear_slop, float max_linear_correction, V2& cM,
+                      float& aM, float& acc) {
+    return (t.bits & 4) ? trow_pass<1>(t, baumgarte, linear_slop, max_linear_correction, cM, aM, acc)
+                        : trow_pass<2>(t, baumgarte, linear_slop, max_linear_correction, cM, aM, acc);
+}
+
 }  // namespace goi

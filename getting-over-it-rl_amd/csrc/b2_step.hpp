@@ -402,6 +402,76 @@ GOI_D void clear_toi_trace(const World& W, const GoiDebug& dbg) {
     for (int i = W.sub; i < GOI_DEBUG_TOI_EVENTS * GOI_DEBUG_TOI_ROWS; i += W.G) dbg.toi_island_rows[i * P + W.w] = -1;
 }
 
+// b2Island::SolveTOI's position passes (toi.py:738-760) on the island's nc rows, the poses in bd: at most 20 passes,
+// each over the rows in order, until the smallest separation is at least -1.5 linear slop. Only the TOI pair (A, Bb)
+// has mass. The rows do not change across the passes: the first two (most islands have one or two) stay in
+// registers, loaded once, each with its own rotation memos (a static side's rotation is then computed once per
+// event); rows past them are read from the row tile in each pass and share a pair of memos.
+GOI_D void toi_positions(const Bodies& bd, const Rows& CR, int nc, int A, int Bb, float mA_, float iA_, float mB_,
+                         float iB_, const GoiSettings& s) {
+    const PRow r0 = load_prow(CR, 0);
+    const PRow r1 = nc > 1 ? load_prow(CR, 1) : r0;
+    const auto masses = [&](const PRow& r, float& mA, float& mB, float& iA, float& iB) {
+        const bool ta = r.ia == A || r.ia == Bb, tb = r.ib == A || r.ib == Bb;
+        mA = ta ? (r.ia == A ? mA_ : mB_) : 0.0f;
+        iA = ta ? (r.ia == A ? iA_ : iB_) : 0.0f;
+        mB = tb ? (r.ib == A ? mA_ : mB_) : 0.0f;
+        iB = tb ? (r.ib == A ? iA_ : iB_) : 0.0f;
+    };
+    float m0A, m0B, i0A, i0B, m1A, m1B, i1A, i1B;
+    masses(r0, m0A, m0B, i0A, i0B);
+    masses(r1, m1A, m1B, i1A, i1B);
+    RotMemo qa0, qb0, qa1, qb1, qa, qb;
+    for (int it = 0; it < 20; ++it) {
+        float min_sep = solve_prow(bd, r0, s.toi_baumgarte, m0A, m0B, i0A, i0B, s.linear_slop, s.max_linear_correction,
+                                   qa0, qb0);
+        if (nc > 1)
+            min_sep = bmin(min_sep, solve_prow(bd, r1, s.toi_baumgarte, m1A, m1B, i1A, i1B, s.linear_slop,
+                                               s.max_linear_correction, qa1, qb1));
+        for (int i = 2; i < nc; ++i) {
+            const PRow cur = load_prow(CR, i);
+            float mA, mB, iA, iB;
+            masses(cur, mA, mB, iA, iB);
+            min_sep = bmin(min_sep, solve_prow(bd, cur, s.toi_baumgarte, mA, mB, iA, iB, s.linear_slop,
+                                               s.max_linear_correction, qa, qb));
+        }
+        if (min_sep >= -1.5f * s.linear_slop) break;
+    }
+}
+
+// The same passes when exactly one of the TOI pair has mass (TRow): its pose in registers, rows 0 and 1 as TRows in
+// registers, the others as TRows in the row tile. Returns false, with bd untouched, when the event is not of that
+// form or the guard fails; toi_positions then runs the passes.
+GOI_D bool toi_positions_one_body(const Bodies& bd, const Rows& CR, int nc, int A, int Bb, float mA_, float iA_,
+                                  float mB_, float iB_, const GoiSettings& s) {
+    const bool movA = mA_ != 0.0f || iA_ != 0.0f, movB = mB_ != 0.0f || iB_ != 0.0f;
+    if (movA == movB) return false;
+    const int M = movA ? A : Bb;
+    const float mM = movA ? mA_ : mB_, iM = movA ? iA_ : iB_;
+    TRow t0, t1;
+    bool ok = make_trow(bd, load_prow(CR, 0), M, mM, iM, t0);
+    if (nc > 1) ok = make_trow(bd, load_prow(CR, 1), M, mM, iM, t1) && ok;
+    for (int i = 2; i < nc; ++i) {
+        TRow t;
+        ok = make_trow(bd, load_prow(CR, i), M, mM, iM, t) && ok;
+        store_trow(CR, i, t);  // each lane of the group stores and reads back its own copy of the same words
+    }
+    if (!ok) return false;
+    V2 cM = bd.c(M);
+    float aM = bd.a(M);
+    float acc = fabsf(aM) * 0x1p40f;
+    const float b = s.toi_baumgarte, slop = s.linear_slop, maxc = s.max_linear_correction;
+    for (int it = 0; it < 20; ++it) {
+        float min_sep = trow_pass(t0, b, slop, maxc, cM, aM, acc);
+        if (nc > 1) min_sep = bmin(min_sep, trow_pass(t1, b, slop, maxc, cM, aM, acc));
+        for (int i = 2; i < nc; ++i) min_sep = bmin(min_sep, trow_pass(load_trow(CR, i), b, slop, maxc, cM, aM, acc));
+        if (min_sep >= -1.5f * slop) break;
+    }
+    if (!(acc < 0x1p60f)) return false;
+    bd.set_c(M, cM, aM);
+    return true;
+}
+
 // one TOI event (toi.py:604-716) on min_slot at min_alpha, the step's event number `ev`: the event island's contacts
 // are marked with a stamp distinct for each event of the step (-2 - ev) in the workspace's cisl array, whose island
 // ids Solve no longer needs
@@ -486,38 +556,8 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     }
     const float mA_ = W.f(GOI_B_INV_MASS, A), iA_ = W.f(GOI_B_INV_INERTIA, A);
     const float mB_ = W.f(GOI_B_INV_MASS, Bb), iB_ = W.f(GOI_B_INV_INERTIA, Bb);
-    // The rows do not change across the passes: the island's first two (most islands have one or two; a world whose
-    // passes run to the cap of 20 spends most of its events here) stay in registers, loaded once, each with its own
-    // rotation memos (a static side's rotation is then computed once per event); rows past them are read from the row
-    // tile in each pass and share a pair of memos.
-    const PRow r0 = load_prow(CR, 0);
-    const PRow r1 = nc > 1 ? load_prow(CR, 1) : r0;
-    const auto masses = [&](const PRow& r, float& mA, float& mB, float& iA, float& iB) {
-        const bool ta = r.ia == A || r.ia == Bb, tb = r.ib == A || r.ib == Bb;
-        mA = ta ? (r.ia == A ? mA_ : mB_) : 0.0f;
-        iA = ta ? (r.ia == A ? iA_ : iB_) : 0.0f;
-        mB = tb ? (r.ib == A ? mA_ : mB_) : 0.0f;
-        iB = tb ? (r.ib == A ? iA_ : iB_) : 0.0f;
-    };
-    float m0A, m0B, i0A, i0B, m1A, m1B, i1A, i1B;
-    masses(r0, m0A, m0B, i0A, i0B);
-    masses(r1, m1A, m1B, i1A, i1B);
-    RotMemo qa0, qb0, qa1, qb1, qa, qb;
-    for (int it = 0; it < 20; ++it) {
-        float min_sep = solve_prow(bd, r0, s.toi_baumgarte, m0A, m0B, i0A, i0B, s.linear_slop, s.max_linear_correction,
-                                   qa0, qb0);
-        if (nc > 1)
-            min_sep = bmin(min_sep, solve_prow(bd, r1, s.toi_baumgarte, m1A, m1B, i1A, i1B, s.linear_slop,
-                                               s.max_linear_correction, qa1, qb1));
-        for (int i = 2; i < nc; ++i) {
-            const PRow cur = load_prow(CR, i);
-            float mA, mB, iA, iB;
-            masses(cur, mA, mB, iA, iB);
-            min_sep = bmin(min_sep, solve_prow(bd, cur, s.toi_baumgarte, mA, mB, iA, iB, s.linear_slop,
-                                               s.max_linear_correction, qa, qb));
-        }
-        if (min_sep >= -1.5f * s.linear_slop) break;
-    }
+    if (!toi_positions_one_body(bd, CR, nc, A, Bb, mA_, iA_, mB_, iB_, s))
+        toi_positions(bd, CR, nc, A, Bb, mA_, iA_, mB_, iB_, s);
     // leap of faith: the TOI pair's sweep start is the solved pose
     W.set2(GOI_B_C0, A, bd.c(A)); W.f(GOI_B_A0, A) = bd.a(A);
     W.set2(GOI_B_C0, Bb, bd.c(Bb)); W.f(GOI_B_A0, Bb) = bd.a(Bb);
