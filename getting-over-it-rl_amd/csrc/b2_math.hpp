@@ -120,9 +120,11 @@ GOI_D void sincos_table_load() {
 // 2 x 1.23e9 of them, checked by tests/sincos_check.c, which restates these operations on the CPU; the factored form
 // St cos r + Ct sin r misses one). sin(-0) = -0 is kept by returning a zero angle itself. Angles of magnitude 2^20
 // and above, infinities and NaN call the library's double sin/cos.
-// sin x and cos x in double by the table method above, for |x| < 2^20.
+// sin x and cos x in double by the table method above, for |x| < 2^20. The table row, k mod 64, is the low bits of
+// k + 1.5 * 2^52 (exact for |k| < 2^51); for any other x, infinities and NaN included, it is some row in 0 .. 63.
 GOI_D void sincos_table(double x, double& s, double& c) {
     const double k = rint(x * GOI_SC_32_OVER_PI);
+    const int row = (int)(__double_as_longlong(k + 6755399441055744.0) & 63);
     double r = fma(-k, GOI_SC_P1, x);
     r = fma(-k, GOI_SC_P2, r);
     r = fma(-k, GOI_SC_P3, r);
@@ -136,7 +138,7 @@ GOI_D void sincos_table(double x, double& s, double& c) {
     pc = fma(pc, r2, GOI_SC_C4);
     pc = fma(pc, r2, GOI_SC_C2);
     const double sr = fma(r * r2, ps, r), cm1 = r2 * pc;
-    const double2 t = reinterpret_cast<const double2*>(g_sincos_lds)[(int)k & 63];  // St, Ct
+    const double2 t = reinterpret_cast<const double2*>(g_sincos_lds)[row];  // St, Ct
     s = t.x + fma(t.x, cm1, t.y * sr);
     c = t.y + fma(t.y, cm1, -(t.x * sr));
 }
@@ -157,12 +159,11 @@ GOI_D Rot rot_of(float a) {
     return q;
 }
 
-// rot_of for an angle its caller checks to be below 2^20 in magnitude, without the branch to the library: a larger
-// angle, an infinity or NaN gives the rotation of angle 0 here (the caller discards what it computed with it).
+// rot_of for an angle its caller checks to be below 2^20 in magnitude, without the branch to the library (a larger
+// angle, an infinity or NaN gives some rotation, which the caller discards).
 GOI_D Rot rot_of_small(float a) {
-    const double x = fabs((double)a) < 1048576.0 ? (double)a : 0.0;
     double s, c;
-    sincos_table(x, s, c);
+    sincos_table((double)a, s, c);
     Rot q;
     q.s = a == 0.0f ? a : (float)s;
     q.c = (float)c;

@@ -337,6 +337,149 @@ GOI_D void solve_vrow(const Bodies& bd, VRow& r) {
     bd.set_v(r.ib, vB, wB);
 }
 
+// ---- TOI velocity passes with one moving body
+//
+// b2Island::SolveTOI's velocity passes (toi.py:762-772) give every island body its mass. When one body M of the
+// island has mass and every row pairs it with a body without mass (static or kinematic: mass and inertia 0), that
+// side's updates v - 0 * P and w - 0 * cross(r, P) are identities when its v and w are finite and not -0 and P and
+// cross(r, P) are finite; its velocity terms in the relative velocity are then constants of the row: for M on side
+// B, ((vM + cross(wM, rM)) - vF) - cross(wF, rF), for M on side A, ((vF + cross(wF, rF)) - vM) - cross(wM, rM), with
+// cross(wF, rF) and vF + cross(wF, rF) evaluated once. M's velocity stays in registers, its updates are
+// v + ms * P and w + is * cross(r, P) (ms, is = +-m, +-i): solve_vrow's floats for M with fewer instructions. The
+// guard (the fixed velocity and arms finite, not -0 and below 2^60 when the rows are built; every applied impulse
+// below 2^60, as one running sum) fails over to solve_vrow's passes from the same velocities.
+struct TVRow {
+    V2 n, r0, r1;  // the normal and M's arms
+    V2 f0, f1;     // the fixed side's term at each point (see above)
+    V2 vF;         // M on side B: the fixed side's velocity
+    float tm0, tm1, nm0, nm1, b0, b1, K0, K1, K2, K3, N0, N1, N2, N3, friction, tspeed, ms, is;
+    float ni0, ni1, ti0, ti1;
+    int cnt;
+    bool mvB;
+};
+
+// Velocity row r as a TVRow for the moving body M; false when the row is not of the form above or fails the guard.
+GOI_D bool make_tvrow(const Bodies& bd, const VRow& r, int M, TVRow& t) {
+    const bool mvB = r.ib == M;
+    if (mvB == (r.ia == M)) return false;
+    const int f = mvB ? r.ia : r.ib;
+    const V2 vF = bd.v(f);
+    const float wF = bd.w(f);
+    const V2 rF0 = mvB ? r.rA0 : r.rB0, rF1 = mvB ? r.rA1 : r.rB1;
+    const float mF = mvB ? r.mA : r.mB, iF = mvB ? r.iA : r.iB;
+    const auto sane = [](float x) { return fabsf(x) < 0x1p60f && __float_as_uint(x) != 0x80000000u; };
+    const bool ok = mF == 0.0f && iF == 0.0f && sane(vF.x) && sane(vF.y) && sane(wF) && fabsf(rF0.x) < 0x1p60f &&
+                    fabsf(rF0.y) < 0x1p60f && fabsf(rF1.x) < 0x1p60f && fabsf(rF1.y) < 0x1p60f &&
+                    fabsf(r.n.x) < 4.0f && fabsf(r.n.y) < 4.0f;
+    t.n = r.n;
+    t.r0 = mvB ? r.rB0 : r.rA0;
+    t.r1 = mvB ? r.rB1 : r.rA1;
+    if (mvB) {
+        t.vF = vF;
+        t.f0 = cross(wF, rF0);
+        t.f1 = cross(wF, rF1);
+    } else {
+        t.vF = mk(0.0f, 0.0f);
+        t.f0 = vF + cross(wF, rF0);
+        t.f1 = vF + cross(wF, rF1);
+    }
+    t.ms = mvB ? r.mB : -r.mA;
+    t.is = mvB ? r.iB : -r.iA;
+    t.tm0 = r.tm0; t.tm1 = r.tm1; t.nm0 = r.nm0; t.nm1 = r.nm1; t.b0 = r.b0; t.b1 = r.b1;
+    t.K0 = r.K0; t.K1 = r.K1; t.K2 = r.K2; t.K3 = r.K3; t.N0 = r.N0; t.N1 = r.N1; t.N2 = r.N2; t.N3 = r.N3;
+    t.friction = r.friction; t.tspeed = r.tspeed;
+    t.ni0 = r.ni0; t.ni1 = r.ni1; t.ti0 = r.ti0; t.ti1 = r.ti1;
+    t.cnt = r.cnt;
+    t.mvB = mvB;
+    return ok;
+}
+
+// solve_vrow on a TVRow, M's velocity (vM, wM) in registers; acc gathers the applied impulses' magnitudes.
+template <bool kMvB>
+GOI_D void solve_tvrow(TVRow& r, V2& vM, float& wM, float& acc) {
+    const V2 n = r.n, t = cross(n, 1.0f);
+    const auto dv = [&](V2 rM, V2 f) {
+        if constexpr (kMvB) return ((vM + cross(wM, rM)) - r.vF) - f;
+        else return (f - vM) - cross(wM, rM);
+    };
+    float ni0 = r.ni0, ni1 = r.ni1, ti0 = r.ti0, ti1 = r.ti1;
+    if (r.cnt > 0) {
+        const float vt = dot(dv(r.r0, r.f0), t) - r.tspeed;
+        float lam = r.tm0 * (-vt);
+        const float maxf = r.friction * ni0;
+        const float nw = bclamp(ti0 + lam, -maxf, maxf);
+        lam = nw - ti0;
+        ti0 = nw;
+        const V2 P = lam * t;
+        vM = vM + r.ms * P;
+        wM = wM + r.is * cross(r.r0, P);
+        acc = acc + fabsf(lam);
+    }
+    if (r.cnt > 1) {
+        const float vt = dot(dv(r.r1, r.f1), t) - r.tspeed;
+        float lam = r.tm1 * (-vt);
+        const float maxf = r.friction * ni1;
+        const float nw = bclamp(ti1 + lam, -maxf, maxf);
+        lam = nw - ti1;
+        ti1 = nw;
+        const V2 P = lam * t;
+        vM = vM + r.ms * P;
+        wM = wM + r.is * cross(r.r1, P);
+        acc = acc + fabsf(lam);
+    }
+    if (r.cnt == 1) {
+        const float vn = dot(dv(r.r0, r.f0), n);
+        float lam = -r.nm0 * (vn - r.b0);
+        const float nw = bmax(ni0 + lam, 0.0f);
+        lam = nw - ni0;
+        ni0 = nw;
+        const V2 P = lam * n;
+        vM = vM + r.ms * P;
+        wM = wM + r.is * cross(r.r0, P);
+        acc = acc + fabsf(lam);
+    } else if (r.cnt == 2) {
+        const float K0 = r.K0, K1 = r.K1, K2 = r.K2, K3 = r.K3;
+        const float ax = ni0, ay = ni1;
+        const float vn1 = dot(dv(r.r0, r.f0), n);
+        const float vn2 = dot(dv(r.r1, r.f1), n);
+        float bx = vn1 - r.b0, by = vn2 - r.b1;
+        bx = bx - (K0 * ax + K2 * ay);
+        by = by - (K1 * ax + K3 * ay);
+        float xx = -(r.N0 * bx + r.N2 * by);
+        float xy = -(r.N1 * bx + r.N3 * by);
+        bool ok = xx >= 0.0f && xy >= 0.0f;
+        if (!ok) {
+            xx = -r.nm0 * bx;
+            xy = 0.0f;
+            ok = xx >= 0.0f && K1 * xx + by >= 0.0f;
+        }
+        if (!ok) {
+            xx = 0.0f;
+            xy = -r.nm1 * by;
+            ok = xy >= 0.0f && K2 * xy + bx >= 0.0f;
+        }
+        if (!ok) {
+            xx = 0.0f;
+            xy = 0.0f;
+            ok = bx >= 0.0f && by >= 0.0f;
+        }
+        if (ok) {
+            const float dx = xx - ax, dy = xy - ay;
+            const V2 P1 = dx * n, P2 = dy * n;
+            vM = vM + r.ms * (P1 + P2);
+            wM = wM + r.is * (cross(r.r0, P1) + cross(r.r1, P2));
+            ni0 = xx;
+            ni1 = xy;
+            acc = acc + (fabsf(dx) + fabsf(dy));
+        }
+    }
+    r.ni0 = ni0; r.ni1 = ni1; r.ti0 = ti0; r.ti1 = ti1;
+}
+GOI_D void solve_tvrow(TVRow& r, V2& vM, float& wM, float& acc) {
+    if (r.mvB) solve_tvrow<true>(r, vM, wM, acc);
+    else solve_tvrow<false>(r, vM, wM, acc);
+}
+
 GOI_D void store_vimpulses(const Rows& R, int i, const VRow& r) {
     R.setf(i, CF_NI0, r.ni0); R.setf(i, CF_NI1, r.ni1); R.setf(i, CF_TI0, r.ti0); R.setf(i, CF_TI1, r.ti1);
 }
@@ -428,22 +571,27 @@ GOI_D float solve_prow(const Bodies& bd, const PRow& r, float baumgarte, float m
 // In b2Island::SolveTOI's position passes (toi.py:738-760) only the TOI pair has mass. When exactly one of the pair
 // has mass (M; the other is static or kinematic, as in every event of a dynamic body against the terrain), every row
 // has M on one side and a side without mass (mass and inertia 0) on the other. That side's updates c - 0 * P and
-// a - 0 * cross(r, P), and its term 0 * rn * rn of K, are identities when its c and a are finite, below 2^60 and not
-// -0, and p and the impulse stay below 2^60 (which bounds r, rn and P). The passes then need only M's pose, kept in
-// registers, and per row the fixed side's transform and the normal, plane point or clip points it alone determines,
-// evaluated once per event: solve_prow's floats for M with a third of its instructions (a wave running one world's
-// TOI events alone issues one instruction every few clocks, so the count is the time). K is m + i * rn * rn of M,
-// M's update c + ms * P and a + is * cross(r, P) with ms, is = +-m, +-i (x - y is x + -y), and the face-B normal
-// flip a multiply by -1. The bounds are checked by one running sum over the passes (an infinity or NaN stays in it);
-// when it fails, or a row does not have this form, solve_prow's passes run from the same poses.
+// a - 0 * cross(r, P), and its term 0 * rn * rn of K, are identities when its c and a are finite and not -0 and r,
+// rn and P are finite. The passes then need only M's pose, kept in registers, and per row the fixed side's transform
+// and the normal, plane point or clip points it alone determines, evaluated once per event: solve_prow's floats for M
+// with half its instructions (a wave running one world's TOI events alone issues one instruction every few clocks,
+// so the count is the time). K is m + i * rn * rn of M, M's update c + ms * P and a + is * cross(r, P) with
+// ms, is = +-m, +-i (x - y is x + -y), and the face-B flip of the normal n folded into ms and is: with n = -n1,
+// rn * rn, P = -(imp * n1) and cross(r, P) = -cross(r, imp * n1) are the same floats negated or not.
+// The guard. When the rows are built: the fixed pose finite, below 2^40 and not -0; M's pose below 2^40 and its angle
+// below 2^20; the local vectors and fixed points below 2^40 and the local normal below 4; M's mass in [2^-40, 2^40),
+// its inertia in [0, 2^40); the max linear correction in [0, 2^10]. Then K >= m > 0 (solve_prow's K > 0 always
+// holds), |C| <= max correction, so M moves by at most 2^13 a point and at most 2^24 over the passes (20 passes of at
+// most 64 points), every point, r, rn and P stay finite. In the passes: each angle that sin/cos is taken of below 2^20
+// (one running sum of |a| * 2^40, which an infinity or NaN also fails). When it fails, or a row does not have this
+// form, solve_prow's passes run from the same poses.
 struct TRow {
     V2 lc;      // M's local center
     V2 u0, u1;  // M's local vectors: kind 1 the local normal and point, kind 2 the two local points
     V2 k0, k1;  // the fixed side's: kind 1 the two clip points, kind 2 the normal (before the face-B flip) and the
                 // plane point
     float radA, radB, ms, is;
-    int bits;   // point count | 4 when M holds the reference face (kind 1; else kind 2, M holds the incident
-                // points) | 8 for face B (the normal's sign)
+    int bits;   // point count | 4 when M holds the reference face (kind 1; else kind 2, M holds the incident points)
 };
 
 // a TOI row in a row's velocity-solver fields (the event sets those up, impulses included, after the passes)
@@ -464,18 +612,16 @@ GOI_D TRow load_trow(const Rows& R, int i) {
     return t;
 }
 
-// Row r as a TRow for the moving body M (mass m, inertia i); false when the row is not of the form above or the fixed
-// side fails the guard.
+GOI_D bool below40(V2 v) { return fabsf(v.x) < 0x1p40f && fabsf(v.y) < 0x1p40f; }
+
+// Row r as a TRow for the moving body M (mass m, inertia i; checked by the caller); false when the row is not of the
+// form above or fails the guard.
 GOI_D bool make_trow(const Bodies& bd, const PRow& r, int M, float m, float i, TRow& t) {
     const bool mvB = r.ib == M;
     if (mvB == (r.ia == M) || r.mtype == kCircles) return false;
     const int f = mvB ? r.ia : r.ib;
     const V2 cF = bd.c(f);
     const float aF = bd.a(f);
-    const bool ok = fabsf(cF.x) < 0x1p60f && fabsf(cF.y) < 0x1p60f && fabsf(aF) < 0x1p60f &&
-                    __float_as_uint(cF.x) != 0x80000000u && __float_as_uint(cF.y) != 0x80000000u &&
-                    __float_as_uint(aF) != 0x80000000u && fabsf(r.ln.x) < 4.0f && fabsf(r.ln.y) < 4.0f &&
-                    !(__float_as_uint(m) >> 31) && !(__float_as_uint(i) >> 31);
     Xf xf;
     xf.q = rot_of(aF);
     xf.p = cF - mul(xf.q, mvB ? r.lcA : r.lcB);
@@ -495,18 +641,20 @@ GOI_D bool make_trow(const Bodies& bd, const PRow& r, int M, float m, float i, T
     t.lc = mvB ? r.lcB : r.lcA;
     t.radA = r.radA;
     t.radB = r.radB;
-    t.ms = mvB ? m : -m;
-    t.is = mvB ? i : -i;
-    t.bits = r.cnt | (mref ? 4 : 0) | (fa ? 0 : 8);
-    return ok;
+    const float sg = fa ? 1.0f : -1.0f;
+    t.ms = sg * (mvB ? m : -m);
+    t.is = sg * (mvB ? i : -i);
+    t.bits = r.cnt | (mref ? 4 : 0);
+    return below40(cF) && fabsf(aF) < 0x1p40f && __float_as_uint(cF.x) != 0x80000000u &&
+           __float_as_uint(cF.y) != 0x80000000u && __float_as_uint(aF) != 0x80000000u && fabsf(r.ln.x) < 4.0f &&
+           fabsf(r.ln.y) < 4.0f && below40(t.lc) && below40(t.u0) && below40(t.u1) && below40(t.k0) &&
+           below40(t.k1);
 }
 
-// One pass over a TRow of kind kKind on M's pose; acc gathers the guard's magnitudes.
+// One pass over a TRow of kind kKind on M's pose; acc gathers the guard's angles.
 template <int kKind>
 GOI_D float trow_pass(const TRow& t, float baumgarte, float linear_slop, float max_linear_correction, V2& cM,
                       float& aM, float& acc) {
-    const float sg = (t.bits & 8) ? -1.0f : 1.0f;
-    const V2 n2 = sg * t.k0;  // kind 2's normal
     float min_sep = 0.0f;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -514,28 +662,26 @@ GOI_D float trow_pass(const TRow& t, float baumgarte, float linear_slop, float m
         Xf xf;
         xf.q = rot_of_small(aM);
         xf.p = cM - mul(xf.q, t.lc);
-        V2 cp, n;
+        V2 cp, n1;
         float sep;
         if constexpr (kKind == 1) {
-            const V2 n1 = mul(xf.q, t.u0);
+            n1 = mul(xf.q, t.u0);
             cp = j == 0 ? t.k0 : t.k1;
             sep = (dot(cp - mul(xf, t.u1), n1) - t.radA) - t.radB;
-            n = sg * n1;
         } else {
+            n1 = t.k0;
             cp = mul(xf, j == 0 ? t.u0 : t.u1);
-            sep = (dot(cp - t.k1, t.k0) - t.radA) - t.radB;
-            n = n2;
+            sep = (dot(cp - t.k1, n1) - t.radA) - t.radB;
         }
         const V2 r = cp - cM;
         min_sep = bmin(min_sep, sep);
         const float C = bclamp(baumgarte * (sep + linear_slop), -max_linear_correction, 0.0f);
-        const float rn = cross(r, n);
-        const float K = fabsf(t.ms) + fabsf(t.is) * rn * rn;
-        const float imp = K > 0.0f ? -C / K : 0.0f;
-        const V2 P = imp * n;
+        const float rn = cross(r, n1);
+        const float imp = -C / (fabsf(t.ms) + fabsf(t.is) * rn * rn);
+        const V2 P = imp * n1;
         cM = cM + t.ms * P;
         aM = aM + t.is * cross(r, P);
-        acc = acc + ((fabsf(cp.x) + fabsf(cp.y)) + (fabsf(imp) + fabsf(aM) * 0x1p40f));
+        acc = fmaf(fabsf(aM), 0x1p40f, acc);
     }
     return min_sep;
 }

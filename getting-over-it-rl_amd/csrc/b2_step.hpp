@@ -448,6 +448,12 @@ GOI_D bool toi_positions_one_body(const Bodies& bd, const Rows& CR, int nc, int 
     if (movA == movB) return false;
     const int M = movA ? A : Bb;
     const float mM = movA ? mA_ : mB_, iM = movA ? iA_ : iB_;
+    const float maxc = s.max_linear_correction;
+    if (!(mM >= 0x1p-40f && mM < 0x1p40f && iM >= 0.0f && iM < 0x1p40f && maxc >= 0.0f && maxc <= 1024.0f))
+        return false;
+    V2 cM = bd.c(M);
+    float aM = bd.a(M);
+    if (!below40(cM)) return false;
     TRow t0, t1;
     bool ok = make_trow(bd, load_prow(CR, 0), M, mM, iM, t0);
     if (nc > 1) ok = make_trow(bd, load_prow(CR, 1), M, mM, iM, t1) && ok;
@@ -457,10 +463,8 @@ GOI_D bool toi_positions_one_body(const Bodies& bd, const Rows& CR, int nc, int 
         store_trow(CR, i, t);  // each lane of the group stores and reads back its own copy of the same words
     }
     if (!ok) return false;
-    V2 cM = bd.c(M);
-    float aM = bd.a(M);
     float acc = fabsf(aM) * 0x1p40f;
-    const float b = s.toi_baumgarte, slop = s.linear_slop, maxc = s.max_linear_correction;
+    const float b = s.toi_baumgarte, slop = s.linear_slop;
     for (int it = 0; it < 20; ++it) {
         float min_sep = trow_pass(t0, b, slop, maxc, cM, aM, acc);
         if (nc > 1) min_sep = bmin(min_sep, trow_pass(t1, b, slop, maxc, cM, aM, acc));
@@ -469,6 +473,33 @@ GOI_D bool toi_positions_one_body(const Bodies& bd, const Rows& CR, int nc, int 
     }
     if (!(acc < 0x1p60f)) return false;
     bd.set_c(M, cM, aM);
+    return true;
+}
+
+// b2Island::SolveTOI's velocity passes (toi.py:762-772) for an island of at most two rows whose only body with mass
+// is one of the TOI pair (TVRow): its velocity in registers. Returns false, with bd and the rows untouched, when the
+// island is not of that form or the guard fails; the event then runs solve_vrow's passes.
+GOI_D bool toi_velocities_one_body(const Bodies& bd, const Rows& CR, int nc, int A, int Bb, float mA_, float iA_,
+                                   float mB_, float iB_, int iterations) {
+    const bool movA = mA_ != 0.0f || iA_ != 0.0f, movB = mB_ != 0.0f || iB_ != 0.0f;
+    if (nc > 2 || movA == movB) return false;
+    const int M = movA ? A : Bb;
+    TVRow t0, t1;
+    bool ok = make_tvrow(bd, load_vrow(CR, 0), M, t0);
+    if (nc > 1) ok = make_tvrow(bd, load_vrow(CR, 1), M, t1) && ok;
+    if (!ok) return false;
+    V2 vM = bd.v(M);
+    float wM = bd.w(M), acc = 0.0f;
+    for (int it = 0; it < iterations; ++it) {
+        solve_tvrow(t0, vM, wM, acc);
+        if (nc > 1) solve_tvrow(t1, vM, wM, acc);
+    }
+    if (!(acc < 0x1p60f)) return false;
+    CR.setf(0, CF_NI0, t0.ni0); CR.setf(0, CF_NI1, t0.ni1); CR.setf(0, CF_TI0, t0.ti0); CR.setf(0, CF_TI1, t0.ti1);
+    if (nc > 1) {
+        CR.setf(1, CF_NI0, t1.ni0); CR.setf(1, CF_NI1, t1.ni1); CR.setf(1, CF_TI0, t1.ti0); CR.setf(1, CF_TI1, t1.ti1);
+    }
+    bd.set_v(M, vM, wM);
     return true;
 }
 
@@ -567,7 +598,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
         cs_prepare(m, W, bd, CR, i, slot, false, 1.0f, rot_of(bd.a(ia)), rot_of(bd.a(ib)), s.velocity_threshold);
     }
     group_sync();
-    {
+    if (!toi_velocities_one_body(bd, CR, nc, A, Bb, mA_, iA_, mB_, iB_, s.velocity_iterations)) {
         // rows 0 (the TOI contact, which every island has) and 1 stay in registers through the passes; rows past them
         // are read from the row tile in each pass
         VRow r0 = load_vrow(CR, 0);
