@@ -29,13 +29,26 @@ GOI_D unsigned long long list_mask(const World& W, int q0, int n, F&& pred) {
     return group_or(W.grp(), mk);
 }
 
+// A slot's old manifold points (their feature keys and impulses, State leaves), loaded by the caller before it
+// evaluates the new manifold so that the loads are in flight meanwhile.
+struct OldPoints {
+    int o0, o1;
+    float n0, n1, t0, t1;
+};
+GOI_D OldPoints old_points(const World& W, int k) {
+    OldPoints p;
+    p.o0 = W.i32(GOI_C_POINT_ID, 2 * k); p.o1 = W.i32(GOI_C_POINT_ID, 2 * k + 1);
+    p.n0 = W.f(GOI_C_NORMAL_IMPULSE, 2 * k); p.n1 = W.f(GOI_C_NORMAL_IMPULSE, 2 * k + 1);
+    p.t0 = W.f(GOI_C_TANGENT_IMPULSE, 2 * k); p.t1 = W.f(GOI_C_TANGENT_IMPULSE, 2 * k + 1);
+    return p;
+}
+
 // b2Contact::Update's manifold part: new manifold, impulses carried over from the first old point with the same
 // feature key, touching flag (pairs.py:56-83). Returns whether touching flipped.
-GOI_D bool contact_update(const World& W, int k, const Manifold& mf) {
+GOI_D bool contact_update(const World& W, int k, const Manifold& mf, const OldPoints& old) {
     const int oldn = W.ccount(k);
-    const int o0 = W.i32(GOI_C_POINT_ID, 2 * k), o1 = W.i32(GOI_C_POINT_ID, 2 * k + 1);
-    const float n0 = W.f(GOI_C_NORMAL_IMPULSE, 2 * k), n1 = W.f(GOI_C_NORMAL_IMPULSE, 2 * k + 1);
-    const float t0 = W.f(GOI_C_TANGENT_IMPULSE, 2 * k), t1 = W.f(GOI_C_TANGENT_IMPULSE, 2 * k + 1);
+    const int o0 = old.o0, o1 = old.o1;
+    const float n0 = old.n0, n1 = old.n1, t0 = old.t0, t1 = old.t1;
     const int n = mf.count;
     float ni0 = 0.0f, ti0 = 0.0f, ni1 = 0.0f, ti1 = 0.0f;
     if (n > 0) {
@@ -64,6 +77,9 @@ GOI_D bool contact_update(const World& W, int k, const Manifold& mf) {
     if (__float_as_uint(ti0) != __float_as_uint(t0)) W.f(GOI_C_TANGENT_IMPULSE, 2 * k) = ti0;
     if (__float_as_uint(ti1) != __float_as_uint(t1)) W.f(GOI_C_TANGENT_IMPULSE, 2 * k + 1) = ti1;
     return flip;
+}
+GOI_D bool contact_update(const World& W, int k, const Manifold& mf) {
+    return contact_update(W, k, mf, old_points(W, k));
 }
 
 // ---------------------------------------------------------------- block-cooperative task runs

@@ -222,11 +222,11 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
 
 GOI_D bool pair_rule(const DModel& m, const World& W, const GoiSettings& s, int a, int b) {
     const bool dyn_a = W.is_dynamic(a), dyn_b = W.is_dynamic(b);
-    const bool bul_a = W.u8(GOI_B_BULLET, a) != 0, bul_b = W.u8(GOI_B_BULLET, b) != 0;
+    const bool bul_a = W.bullet(a), bul_b = W.bullet(b);
     const bool stock = bul_a || !dyn_a || bul_b || !dyn_b;
     if (!s.unity_toi) return stock;
     const bool rule = bul_a || bul_b ||
-                      (!dyn_b ? W.u8(GOI_B_CONTINUOUS, a) != 0 : (!dyn_a ? W.u8(GOI_B_CONTINUOUS, b) != 0 : false));
+                      (!dyn_b ? W.continuous(a) : (!dyn_a ? W.continuous(b) : false));
     return stock && rule;
 }
 
@@ -514,9 +514,10 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     const SweepBackup bkA = backup(W, A), bkB = backup(W, Bb);
     body_advance(W, A, min_alpha);
     body_advance(W, Bb, min_alpha);
+    const OldPoints old0 = old_points(W, min_slot);  // in flight during the narrowphase
     Manifold mf0;
     evaluate(m, fa, fb, W.xf(A), W.xf(Bb), s, mf0, W.grp());
-    if (contact_update(W, min_slot, mf0)) { W.wake(A); W.wake(Bb); }
+    if (contact_update(W, min_slot, mf0, old0)) { W.wake(A); W.wake(Bb); }
     W.set_tflag(min_slot, 0);
     W.set_tcount(min_slot, W.tcount(min_slot) + 1);
     if (!W.touching(min_slot)) {
@@ -555,13 +556,14 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
                 }
                 if (W.cisl(c) == stamp) continue;
                 const int other = ca == body ? cb : ca;
-                if (W.is_dynamic(other) && !W.u8(GOI_B_BULLET, body) && !W.u8(GOI_B_BULLET, other)) continue;
+                if (W.is_dynamic(other) && !W.bullet(body) && !W.bullet(other)) continue;
                 if (s.unity_toi && !pair_rule(m, W, s, body, other)) continue;
                 const SweepBackup bk = backup(W, other);
                 if (!((bflag >> other) & 1ull)) body_advance(W, other, min_alpha);
+                const OldPoints old = old_points(W, c);  // in flight during the narrowphase
                 Manifold mf;
                 evaluate(m, W.fa(c), W.fb(c), W.xf(ca), W.xf(cb), s, mf, W.grp());
-                if (contact_update(W, c, mf)) { W.wake(ca); W.wake(cb); }
+                if (contact_update(W, c, mf, old)) { W.wake(ca); W.wake(cb); }
                 W.set_ten(c, 1);
                 if (!W.touching(c)) {
                     restore(W, other, bk);

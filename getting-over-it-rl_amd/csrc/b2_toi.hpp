@@ -45,7 +45,14 @@ GOI_D void sweep_advance(const World& W, int b, float alpha) {
 
 // b2Body::SynchronizeTransform
 GOI_D void sync_transform(const World& W, int b) {
-    const Rot q = rot_of(W.f(GOI_B_A, b));
+    const float a = W.f(GOI_B_A, b);
+    Rot q;
+    if (a == 0.0f) {  // a static body's usual angle: rot_of's result, sin = the angle itself (+-0), cos = 1
+        q.s = a;
+        q.c = 1.0f;
+    } else {
+        q = rot_of(a);
+    }
     W.set2(GOI_B_XF_P, b, W.v2(GOI_B_C, b) - mul(q, W.v2(GOI_B_LOCAL_CENTER, b)));
     W.f(GOI_B_XF_Q, 2 * b) = q.c;
     W.f(GOI_B_XF_Q, 2 * b + 1) = q.s;

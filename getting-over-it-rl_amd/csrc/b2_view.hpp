@@ -276,7 +276,10 @@ struct World {
         if (odd || ((was >> kMetaCount) & 3) != n) i32(GOI_C_COUNT, c) = n;
     }
     GOI_D int& awake(int b) const { return wi(k.o_awake, b); }    // bodies.awake
-    GOI_D int& active(int b) const { return wi(k.o_active, b); }  // bodies.active (read-only in a step)
+    // bodies.active, .bullet and .continuous (read-only in a step), one word per body: bits 0, 1 and 2
+    GOI_D bool active(int b) const { return wi(k.o_active, b) & 1; }
+    GOI_D bool bullet(int b) const { return (wi(k.o_active, b) >> 1) & 1; }
+    GOI_D bool continuous(int b) const { return (wi(k.o_active, b) >> 2) & 1; }
     // toi.flag, toi.enabled and toi.count of a slot
     GOI_D int tflag(int c) const { return (meta(c) >> kMetaTFlag) & 1; }
     GOI_D int ten(int c) const { return (meta(c) >> kMetaTEn) & 1; }
@@ -447,7 +450,7 @@ GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
         // the float body leaves: rows i < width * B of each, at word coef * B + i
         for (int i0 = bc.r0; i0 < 2 * bc.B; i0 += 2 * bc.stride) {
             float v[13][2];
-            uint8_t aw[2], ac[2];
+            uint8_t aw[2], ac[2], bu[2], co[2];
 #pragma unroll
             for (int l = 0; l < 13; ++l) {
                 const int rows = kBodyMirrorWidth[l] * bc.B;
@@ -459,6 +462,8 @@ GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
                 const int b = min(i0 + u * bc.stride, bc.B - 1);
                 aw[u] = bc.ld<uint8_t>(GOI_B_AWAKE, b);
                 ac[u] = bc.ld<uint8_t>(GOI_B_ACTIVE, b);
+                bu[u] = bc.ld<uint8_t>(GOI_B_BULLET, b);
+                co[u] = bc.ld<uint8_t>(GOI_B_CONTINUOUS, b);
             }
 #pragma unroll
             for (int l = 0; l < 13; ++l) {
@@ -474,7 +479,7 @@ GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
                 const int b = i0 + u * bc.stride;
                 if (b < bc.B) {
                     bc.wi(k.o_awake + b) = aw[u];
-                    bc.wi(k.o_active + b) = ac[u];
+                    bc.wi(k.o_active + b) = (ac[u] != 0 ? 1 : 0) | (bu[u] != 0 ? 2 : 0) | (co[u] != 0 ? 4 : 0);
                 }
             }
         }
