@@ -140,102 +140,114 @@ __device__ __forceinline__ LaneViews lane_views(const DModel& m, const Launch& L
     return v;
 }
 
+// The lane's views set up afresh from lane_now(), where block-cooperative code follows code that some lanes skipped
+// (a world's own phases, which lanes without a world and the lanes of other worlds do not run). A per-lane value
+// carried across such code was seen to be lost, in some builds, for the lanes that skipped it: lanes without a world
+// (in a block's last, partly filled group of worlds, or at wave sizes that leave lanes idle) then ran cooperative
+// tasks and block copies with a broken view and wrote over their block's worlds.
+__device__ __forceinline__ LaneViews fresh_views(const DModel& m, const Launch& L, int* lds, int w0) {
+    return lane_views(m, L, lds, w0, lane_now());
+}
+
+// inv_dt0, ClearForces and the debug status word of the lane's world after its step (step.py:41-47)
+__device__ __forceinline__ void finish_step(const Launch& L, const LaneViews& v, int overflow0, bool capped) {
+    if (!v.lm.valid) return;
+    const World& W = v.W;
+    const float dt = L.dt;
+    if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
+    if (L.s.auto_clear_forces)
+        for (int b = 0; b < W.B; ++b) {
+            W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
+            W.f(GOI_B_TORQUE, b) = 0.0f;
+        }
+    if (L.dbg.status) L.dbg.status[W.w] = step_status(W, overflow0, capped, dt, L.s);
+}
+
 // One b2World::Step (step.py:28-47) of each world of the block on its lane group, on the workspace mirror:
 // FindNewContacts where new_fixture, Collide, Solve, SolveTOI, inv_dt0, ClearForces. Lanes without a world stay to
-// share the block's manifold and TOI work.
+// share the block's manifold and TOI work. Each block-cooperative phase sets up the lane's views afresh (fresh_views).
 template <bool kOpaqueToi>
-__device__ __forceinline__ void step_worlds(const DModel& m, const Launch& L, int w0, const LaneViews& v) {
-    const LaneMap& lm = v.lm;
-    const bool valid = lm.valid;
-    const World& W = v.W;
-    const int overflow0 = valid && L.dbg.status ? W.i32(GOI_S_OVERFLOW, 0) : 0;
+__device__ __forceinline__ void step_worlds(const DModel& m, const Launch& L, int* lds, int w0) {
+    const LaneViews v = fresh_views(m, L, lds, w0);
+    const int overflow0 = v.lm.valid && L.dbg.status ? v.W.i32(GOI_S_OVERFLOW, 0) : 0;
     build_order_block(v.bc);
-    if (valid) {
-        if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
-        W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
+    if (v.lm.valid) {
+        if (v.W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, v.W);
+        v.W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     }
-    collide_block(m, v.co, W, valid, lm.leader, L.s);
-    if (valid) {
-        solve_world(m, W, v.bd, v.CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
-        clear_toi_trace(W, L.dbg);
+    const LaneViews c = fresh_views(m, L, lds, w0);
+    collide_block(m, c.co, c.W, c.lm.valid, c.lm.leader, L.s);
+    if (c.lm.valid) {
+        solve_world(m, c.W, c.bd, c.CR, joint_rows(L, w0, c.lm.wl), L.s, L.dt, L.dbg);
+        clear_toi_trace(c.W, L.dbg);
     }
     bool capped = false;
-    if (L.s.continuous_physics)
-        capped = solve_toi_world<kOpaqueToi>(m, W, v.bd, v.TR, L.s, L.dt, valid, lm.leader, v.co, v.bc, L.dbg);
-    if (valid) {
-        const float dt = L.dt;
-        if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
-        if (L.s.auto_clear_forces)
-            for (int b = 0; b < W.B; ++b) {
-                W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
-                W.f(GOI_B_TORQUE, b) = 0.0f;
-            }
-        if (L.dbg.status) L.dbg.status[W.w] = step_status(W, overflow0, capped, dt, L.s);
+    if (L.s.continuous_physics) {
+        const LaneViews t = fresh_views(m, L, lds, w0);
+        capped = solve_toi_world<kOpaqueToi>(m, t.W, t.bd, t.TR, L.s, L.dt, t.lm.valid,
+                                             [&] { return fresh_views(m, L, lds, w0); }, L.dbg);
     }
+    finish_step(L, fresh_views(m, L, lds, w0), overflow0, capped);
 }
 
 // The block's worlds: the State into the workspace mirror, one step (kMulti false) or L.n_steps steps, the mirror
 // back. Across the steps of a multi-step launch the mirror stays in LDS (it is the State's current value; every access
 // to a mirrored leaf inside a step goes through the workspace), so the worlds need neither a store nor a reload between
-// steps, and the block never waits for other blocks' steps. Each of those steps sets up its lane's views from a lane
-// index the compiler cannot see through, so no per-lane State or row address of one step is kept live (spilled to
-// scratch) into the next.
+// steps, and the block never waits for other blocks' steps. The lane's views are set up afresh (fresh_views) for each
+// block-cooperative phase and for the mirror's load and store.
 // At most 256 registers (two waves per SIMD): the second wave hides the latency chains of the first.
 template <bool kMulti, bool kOpaqueToi = false>  // kOpaqueToi: solve_toi_world's kOpaqueViews
 __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     GOI_DYNAMIC_LDS(lds);
     sincos_table_load();
     const int w0 = xcd_group() * L.wpw;
+    const auto fresh_bc = [&] {
+        return block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane_now(), kBlock);
+    };
     if constexpr (!kMulti) {
-        // step_worlds' sequence written out around the mirror's load and store: the code generated for this form (the
-        // views set up once, the step in a one-trip loop) measured 2% faster than a call of step_worlds
-        const int lane = threadIdx.x;
+        // step_worlds' sequence written out, a world's own views set up once (2% faster than a call of step_worlds);
+        // the cooperative phases take theirs afresh
+        const int lane = lane_now();
         const LaneMap lm = lane_map(L, w0, lane);
         const bool valid = lm.valid;
         const World W = make_world(m, L, valid ? w0 + lm.wl : w0, lds, valid ? lm.wl : 0, lm.sub, lm.G);  // if valid
-        const Coop co = block_coop(L, W, lds, w0);
         Bodies bd;
         bd.s = reinterpret_cast<float*>(lds) + W.k.o_body * W.S + (valid ? lm.wl : 0);
         bd.B = L.B;
         bd.st = W.S;
         const Rows CR = contact_rows(L, w0, valid ? lm.wl : 0);
-        const BlockCopy bc = block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane, kBlock);
-        load_mirror_block(m, bc);
+        load_mirror_block(m, fresh_bc());
         const int overflow0 = valid && L.dbg.status ? W.i32(GOI_S_OVERFLOW, 0) : 0;
         for (int step = 0; step < 1; ++step) {
-            build_order_block(bc);
+            build_order_block(fresh_bc());
             if (valid) {
                 if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
                 W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
             }
-            collide_block(m, co, W, valid, lm.leader, L.s);
+            {
+                const LaneViews c = fresh_views(m, L, lds, w0);
+                collide_block(m, c.co, c.W, c.lm.valid, c.lm.leader, L.s);
+            }
             if (valid) {
                 solve_world(m, W, bd, CR, joint_rows(L, w0, lm.wl), L.s, L.dt, L.dbg);
                 clear_toi_trace(W, L.dbg);
             }
             bool capped = false;
-            if (L.s.continuous_physics)
-                capped = solve_toi_world<kOpaqueToi>(m, W, bd, toi_rows(L, w0, valid ? lm.wl : 0), L.s, L.dt, valid,
-                                                     lm.leader, co, bc, L.dbg);
-            if (valid) {
-                const float dt = L.dt;
-                if (dt > 0.0f) W.f(GOI_S_INV_DT0, 0) = 1.0f / dt;
-                if (L.s.auto_clear_forces)
-                    for (int b = 0; b < W.B; ++b) {
-                        W.set2(GOI_B_FORCE, b, mk(0.0f, 0.0f));
-                        W.f(GOI_B_TORQUE, b) = 0.0f;
-                    }
-                if (L.dbg.status) L.dbg.status[W.w] = step_status(W, overflow0, capped, dt, L.s);
+            if (L.s.continuous_physics) {
+                const LaneViews t = fresh_views(m, L, lds, w0);
+                capped = solve_toi_world<kOpaqueToi>(m, t.W, t.bd, t.TR, L.s, L.dt, t.lm.valid,
+                                                     [&] { return fresh_views(m, L, lds, w0); }, L.dbg);
             }
+            finish_step(L, fresh_views(m, L, lds, w0), overflow0, capped);
         }
-        store_mirror_block(bc);
+        store_mirror_block(fresh_bc());
     } else {
-        load_mirror_block(m, lane_views(m, L, lds, w0, threadIdx.x).bc);
+        load_mirror_block(m, fresh_bc());
         for (int step = 0; step < L.n_steps; ++step) {
             if (step > 0) __syncthreads();  // the worlds' workspace writes of the previous step
-            step_worlds<kOpaqueToi>(m, L, w0, lane_views(m, L, lds, w0, opaque((int)threadIdx.x)));
+            step_worlds<kOpaqueToi>(m, L, lds, w0);
         }
-        store_mirror_block(lane_views(m, L, lds, w0, threadIdx.x).bc);
+        store_mirror_block(fresh_bc());
     }
 }
 

@@ -89,6 +89,19 @@ inline
 #endif
 __shared__ __align__(16) double g_sincos_lds[128];
 
+// This lane's index in its wavefront (a block is one wavefront), read from the hardware at the call: a fresh value,
+// not one carried from earlier code (the mask goes through an empty asm statement, so the compiler recomputes the
+// count at every call instead of reusing an earlier one).
+GOI_D int lane_now() {
+#ifdef GOI_HOST_BUILD
+    return (int)threadIdx.x;
+#else
+    unsigned mask = ~0u;
+    asm volatile("" : "+s"(mask));
+    return (int)__builtin_amdgcn_mbcnt_hi(mask, __builtin_amdgcn_mbcnt_lo(mask, 0u));
+#endif
+}
+
 // v itself, as a value the compiler cannot see through: what is computed from it after this point is computed there,
 // not earlier (a multi-step loop then holds no per-lane address of one step across the next).
 GOI_D int opaque(int v) {

@@ -684,28 +684,32 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
 }
 
 // b2World::SolveTOI (toi.py:827-865). Called by every lane of the block (the reset, the TOI searches and the final
-// copy are cooperative); `valid` marks the lanes that run a world, `leader` the first lane of each world's group.
+// copy are cooperative); `valid` marks the lanes that run a world. fresh() returns the lane's views set up afresh
+// (W, the cooperative view co, the block copy bc, the lane map lm with the group's leader) for every cooperative
+// phase: each search, which follows events that the lanes of other worlds and lanes without a world skipped, and the
+// stores after the event loop.
 // kOpaqueViews: each iteration of the event loop re-derives the world's views through an offset the compiler cannot
 // see through, so that no per-lane address is held (spilled) from one iteration to the next. The island instance's
 // spilled registers go (816 to 16 B of scratch per lane, 3.5% faster), and most of the generic kernel's (960 to 160 B,
 // 8% faster on the rig at 4 worlds per wave); the rig instance, with few spills, measured slower with it.
 // Returns true when the world stopped at max_events with another event pending.
-template <bool kOpaqueViews = false>
+template <bool kOpaqueViews = false, class Fresh>
 GOI_D bool solve_toi_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const GoiSettings& s,
-                           float dt, bool valid, bool leader, const Coop& co, const BlockCopy& bc,
-                           const GoiDebug& dbg) {
+                           float dt, bool valid, const Fresh& fresh, const GoiDebug& dbg) {
     if (W.C == 0 || m.P == 0) return false;
     if (s.unity_toi && !m.any_toi_body) return false;
-    reset_toi_block(bc);
+    reset_toi_block(fresh().bc);
     int events = 0;
     bool capped = false;
     if (dt > 0.0f) {
         const int max_events = s.max_events >= 0 ? s.max_events : W.C * (kMaxSubSteps + 1) + 8;
         int slot = -1;
         float alpha = 1.0f;
-        const auto toi = [&](int o, int i) { toi_task(m, co, o, i, s.linear_slop); };
-        const int nt0 = valid ? toi_search_prepare(m, W, CR, s) : 0;
-        coop_run(co, leader ? nt0 : 0, toi);
+        const auto search = [&](int nt) {
+            const auto v = fresh();
+            coop_run(v.co, v.lm.leader ? nt : 0, [&](int o, int i) { toi_task(m, v.co, o, i, s.linear_slop); });
+        };
+        search(valid ? toi_search_prepare(m, W, CR, s) : 0);
         bool found = valid && toi_search_pick(W, s, slot, alpha);
         // the block iterates while any world has an event to process; the others take part in the searches only
         while (__any(found && events < max_events)) {
@@ -723,23 +727,22 @@ GOI_D bool solve_toi_world(const DModel& m, const World& W, const Bodies& bd, co
                     toi_event(m, Wi, bdi, CRi, s, dt, slot, alpha, events, dbg);
                     ++events;
                 }
-                const int nt = act ? toi_search_prepare(m, Wi, CRi, s) : 0;
-                coop_run(co, leader ? nt : 0, toi);
+                search(act ? toi_search_prepare(m, Wi, CRi, s) : 0);
                 found = act && toi_search_pick(Wi, s, slot, alpha);
             } else {
                 if (act) {
                     toi_event(m, W, bd, CR, s, dt, slot, alpha, events, dbg);
                     ++events;
                 }
-                const int nt = act ? toi_search_prepare(m, W, CR, s) : 0;
-                coop_run(co, leader ? nt : 0, toi);
+                search(act ? toi_search_prepare(m, W, CR, s) : 0);
                 found = act && toi_search_pick(W, s, slot, alpha);
             }
         }
         capped = found && events >= max_events;
     }
-    if (valid) W.i32(GOI_T_EVENTS, 0) = events;
-    store_toi_block(bc);
+    const auto v = fresh();
+    if (v.lm.valid) v.W.i32(GOI_T_EVENTS, 0) = events;
+    store_toi_block(v.bc);
     return capped;
 }
 

@@ -300,32 +300,35 @@ GOI_D SepFn sep_init(const SimplexCache& cache, const Proxy& pA, const Sweep& sA
     return f;
 }
 
-GOI_D float sep_eval(const SepFn& f, const Proxy& pA, const Sweep& sA, const Proxy& pB, const Sweep& sB, int iA,
-                     int iB, float t, RotMemo& ma, RotMemo& mb) {
+// b2SeparationFunction::Evaluate at the support vertices lA = pA.at(iA), lB = pB.at(iB) that FindMinSeparation chose
+// (those of a face's own proxy unused), looked up once by the caller for all the root finder's steps
+GOI_D float sep_eval(const SepFn& f, const Sweep& sA, const Sweep& sB, V2 lA, V2 lB, float t, RotMemo& ma,
+                     RotMemo& mb) {
     const Xf xA = sweep_xf(sA, t, ma), xB = sweep_xf(sB, t, mb);
-    if (f.type == kSepPoints) return dot(mul(xB, pB.at(iB)) - mul(xA, pA.at(iA)), f.axis);
-    if (f.type == kSepFaceA) return dot(mul(xB, pB.at(iB)) - mul(xA, f.lp), mul(xA.q, f.axis));
-    return dot(mul(xA, pA.at(iA)) - mul(xB, f.lp), mul(xB.q, f.axis));
+    if (f.type == kSepPoints) return dot(mul(xB, lB) - mul(xA, lA), f.axis);
+    if (f.type == kSepFaceA) return dot(mul(xB, lB) - mul(xA, f.lp), mul(xA.q, f.axis));
+    return dot(mul(xA, lA) - mul(xB, f.lp), mul(xB.q, f.axis));
 }
 
-GOI_D float sep_find_min(const SepFn& f, const Proxy& pA, const Sweep& sA, const Proxy& pB, const Sweep& sB, int& iA,
-                         int& iB, float t, RotMemo& ma, RotMemo& mb) {
+// b2SeparationFunction::FindMinSeparation; lA, lB its support vertices (lA = (0, 0) for face A, lB for face B)
+GOI_D float sep_find_min(const SepFn& f, const Proxy& pA, const Sweep& sA, const Proxy& pB, const Sweep& sB, V2& lA,
+                         V2& lB, float t, RotMemo& ma, RotMemo& mb) {
     const Xf xA = sweep_xf(sA, t, ma), xB = sweep_xf(sB, t, mb);
     if (f.type == kSepPoints) {
-        iA = support(pA, mulT(xA.q, f.axis));
-        iB = support(pB, mulT(xB.q, -f.axis));
-        return dot(mul(xB, pB.at(iB)) - mul(xA, pA.at(iA)), f.axis);
+        lA = pA.at(support(pA, mulT(xA.q, f.axis)));
+        lB = pB.at(support(pB, mulT(xB.q, -f.axis)));
+        return dot(mul(xB, lB) - mul(xA, lA), f.axis);
     }
     if (f.type == kSepFaceA) {
         const V2 n = mul(xA.q, f.axis);
-        iA = -1;
-        iB = support(pB, mulT(xB.q, -n));
-        return dot(mul(xB, pB.at(iB)) - mul(xA, f.lp), n);
+        lA = mk(0.0f, 0.0f);
+        lB = pB.at(support(pB, mulT(xB.q, -n)));
+        return dot(mul(xB, lB) - mul(xA, f.lp), n);
     }
     const V2 n = mul(xB.q, f.axis);
-    iB = -1;
-    iA = support(pA, mulT(xA.q, -n));
-    return dot(mul(xA, pA.at(iA)) - mul(xB, f.lp), n);
+    lB = mk(0.0f, 0.0f);
+    lA = pA.at(support(pA, mulT(xA.q, -n)));
+    return dot(mul(xA, lA) - mul(xB, f.lp), n);
 }
 
 enum { kToiUnknown = 0, kToiFailed = 1, kToiOverlapped = 2, kToiTouching = 3, kToiSeparated = 4 };
@@ -360,18 +363,18 @@ GOI_D int time_of_impact(const Proxy& pA, Sweep sA, const Proxy& pB, Sweep sB, f
         bool done = false;
         float t2 = 1.0f;
         for (int push = 0;;) {
-            int iA, iB;
-            float s2 = sep_find_min(f, pA, sA, pB, sB, iA, iB, t2, ma, mb);
+            V2 lA, lB;
+            float s2 = sep_find_min(f, pA, sA, pB, sB, lA, lB, t2, ma, mb);
             if (s2 > target + tol) { state = kToiSeparated; t_out = 1.0f; done = true; break; }
             if (s2 > target - tol) { t1 = t2; break; }
-            float s1 = sep_eval(f, pA, sA, pB, sB, iA, iB, t1, ma, mb);
+            float s1 = sep_eval(f, sA, sB, lA, lB, t1, ma, mb);
             if (s1 < target - tol) { state = kToiFailed; t_out = t1; done = true; break; }
             if (s1 <= target + tol) { state = kToiTouching; t_out = t1; done = true; break; }
             float a1 = t1, a2 = t2;
             for (int rc = 0;;) {
                 const float t = (rc & 1) ? a1 + (target - s1) * (a2 - a1) / (s2 - s1) : 0.5f * (a1 + a2);
                 ++rc;
-                const float s = sep_eval(f, pA, sA, pB, sB, iA, iB, t, ma, mb);
+                const float s = sep_eval(f, sA, sB, lA, lB, t, ma, mb);
                 if (babs(s - target) < tol) { t2 = t; break; }
                 if (s > target) { a1 = t; s1 = s; }
                 else { a2 = t; s2 = s; }

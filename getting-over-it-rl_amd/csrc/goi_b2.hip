@@ -62,8 +62,11 @@ __global__ void __launch_bounds__(kBlock) k_collide(DModel m, Launch L, int star
         if (W.u8(GOI_S_NEW_FIXTURE, 0)) find_new_contacts(m, W);
         W.u8(GOI_S_NEW_FIXTURE, 0) = 0;
     }
-    if (!start_only) collide_block(m, block_coop(L, W, lds, w0), W, lm.valid, lm.leader, L.s);
-    store_mirror_block(bc);
+    if (!start_only) {
+        const LaneViews v = fresh_views(m, L, lds, w0);  // the search above is a world's own phase
+        collide_block(m, v.co, v.W, v.lm.valid, v.lm.leader, L.s);
+    }
+    store_mirror_block(fresh_views(m, L, lds, w0).bc);
 }
 
 template <bool kMulti>

@@ -16,11 +16,11 @@ torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 
-def _run(model, state, settings, dt, steps, oracle, actions=None, every=1, on_step=None, nan_equal=False):
+def _run(model, state, settings, dt, steps, oracle, actions=None, every=1, on_step=None, nan_equal=False, pitch=None):
     """Steps the device and the oracle side by side from the same State (and actions), comparing every leaf bit for
     bit after every `every`-th step and after the last (nan_equal: any two NaNs equal). on_step(k, ref, dev) runs
-    after each step."""
-    dev = b2.layout.to_device(state, "cuda")
+    after each step; pitch: the device State's pitch (the world count by default)."""
+    dev = b2.layout.to_device(state, "cuda", pitch)
     ref = oracle.copy(state)
     for k in range(steps):
         if actions is not None:
@@ -446,6 +446,29 @@ def test_worlds_per_wave_variants(oracle, monkeypatch, wpw, capacity):
         assert info["worlds_per_wave"] == wpw and info["blocks"] == -(-256 // wpw), info
         assert info["kernel"] == ("rig" if (wpw, capacity) == (8, 40) else "generic"), info
     _run(m, st, s, cfg.dt, 10, oracle, [b2.scenes.actions(rng, 256) for _ in range(10)], on_step=used)
+
+
+@pytest.mark.parametrize("wpw,n,pitch,max_events", [(8, 250, 256, -1), (8, 250, 256, 0), (8, 250, None, -1),
+                                                    (4, 250, None, -1), (16, 250, None, 0), (20, 256, None, -1),
+                                                    (20, 256, None, 0), (13, 256, None, 0)])
+def test_lanes_without_a_world(oracle, monkeypatch, wpw, n, pitch, max_events):
+    """Blocks with lanes that run no world take part in every cooperative phase (manifolds, TOI searches, the block
+    copies) after phases that only the lanes with a world run: a world count that leaves the last block partly filled
+    (250 worlds at 8, 4 or 16 a block; the rig instance at 8 on a packed State of pitch 256, the generic kernel on one
+    of pitch 250), or one that leaves lanes idle in every block (20 and 13 worlds per wave). max_events 0 stops every
+    world's TOI walk before its first event, so the block's searches follow the solver directly. Config 4, 4 steps
+    with actions, bit for bit."""
+    from dataclasses import replace
+    monkeypatch.setenv("GOI_WORLDS_PER_WAVE", str(wpw))
+    s, m, st, cfg = b2.scenes.make_config(4, n, capacity=40)
+    s = replace(s, max_events=max_events)
+    rng = np.random.default_rng(21)
+
+    def used(k, ref, dev):
+        info = b2.last_launch()
+        assert info["worlds_per_wave"] == wpw and info["blocks"] == -(-n // wpw), info
+        assert info["kernel"] == ("rig" if pitch == 256 else "generic"), info
+    _run(m, st, s, cfg.dt, 4, oracle, [b2.scenes.actions(rng, n) for _ in range(4)], on_step=used, pitch=pitch)
 
 
 @pytest.mark.parametrize("auto_clear", [True, False])
