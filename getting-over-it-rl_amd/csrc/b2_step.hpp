@@ -542,11 +542,21 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     for (int pi = 0; pi < 2; ++pi) {
         const int body = pi == 0 ? A : Bb;
         if (!W.is_dynamic(body)) continue;
+        const bool bullet = W.bullet(body);
         bool full = false;
-        // the contacts of `body` in list order, a chunk of the list at a time (found by the lane group together)
+        // the contacts of `body` in list order that the walk does not skip, a chunk of the list at a time (found by
+        // the lane group together). The skips test flags that the walk does not change, and stamps: a contact in the
+        // chunk is stamped only when the walk visits it. A skipped contact does nothing, so leaving it out of the walk
+        // changes nothing either, the island-full stop included (it stops at the next contact not skipped instead).
         for (int q0 = 0; q0 < n && !full; q0 += 64) {
-            const unsigned long long hits =
-                list_mask(W, q0, n, [&](int c) { return W.ba(c) == body || W.bb(c) == body; });
+            const unsigned long long hits = list_mask(W, q0, n, [&](int c) {
+                const int ca = W.ba(c), cb = W.bb(c);
+                if (ca != body && cb != body) return false;
+                if (W.cisl(c) == stamp) return false;
+                const int other = ca == body ? cb : ca;
+                if (W.is_dynamic(other) && !bullet && !W.bullet(other)) return false;
+                return !s.unity_toi || pair_rule(m, W, s, body, other);
+            });
             for (unsigned long long left = hits; left; left &= left - 1) {
                 const int c = W.order(q0 + __builtin_ctzll(left));
                 const int ca = W.ba(c), cb = W.bb(c);
@@ -554,10 +564,7 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
                     full = true;
                     break;
                 }
-                if (W.cisl(c) == stamp) continue;
                 const int other = ca == body ? cb : ca;
-                if (W.is_dynamic(other) && !W.bullet(body) && !W.bullet(other)) continue;
-                if (s.unity_toi && !pair_rule(m, W, s, body, other)) continue;
                 const SweepBackup bk = backup(W, other);
                 if (!((bflag >> other) & 1ull)) body_advance(W, other, min_alpha);
                 const OldPoints old = old_points(W, c);  // in flight during the narrowphase
