@@ -102,6 +102,14 @@ GOI_D int lane_now() {
 #endif
 }
 
+// The wave's instruction-issue priority among the waves of its SIMD (0 to 3); nothing else depends on it.
+template <int kPrio>
+GOI_D void wave_priority() {
+#ifndef GOI_HOST_BUILD
+    __builtin_amdgcn_s_setprio(kPrio);
+#endif
+}
+
 // v itself, as a value the compiler cannot see through: what is computed from it after this point is computed there,
 // not earlier (a multi-step loop then holds no per-lane address of one step across the next).
 GOI_D int opaque(int v) {
