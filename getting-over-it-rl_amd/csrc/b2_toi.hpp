@@ -109,19 +109,27 @@ GOI_D Proxy proxy_of(const DModel& m, int f) {
     p.radius = m.fix[f].radius;
     return p;
 }
-// b2DistanceProxy::GetSupport: first index of the largest dot
-GOI_D int support(const Proxy& p, V2 d) {
-    int best = 0;
+// b2DistanceProxy::GetSupport and GetVertex together: the first index of the largest dot and its vertex, selected in
+// the same pass over the slots (no select chain over the slots by index after it)
+struct Support {
+    V2 v;
+    int i;
+};
+GOI_D Support support(const Proxy& p, V2 d) {
+    Support s;
+    s.i = 0;
+    s.v = p.v[0];
     float bv = dot(p.v[0], d);
 #pragma unroll
     for (int i = 1; i < kPoly; ++i) {
         const float v = dot(p.v[i], d);
         if (i < p.count && v > bv) {
-            best = i;
+            s.i = i;
+            s.v = p.v[i];
             bv = v;
         }
     }
-    return best;
+    return s;
 }
 
 struct SVert {
@@ -141,12 +149,15 @@ GOI_D float metric(const SVert* v, int count) {
     return 0.0f;
 }
 
-GOI_D void set_vertex(SVert& v, const Proxy& pA, const Xf& xA, int iA, const Proxy& pB, const Xf& xB, int iB) {
+GOI_D void set_vertex(SVert& v, const Xf& xA, int iA, V2 lA, const Xf& xB, int iB, V2 lB) {
     v.iA = iA;
     v.iB = iB;
-    v.wA = mul(xA, pA.at(iA));
-    v.wB = mul(xB, pB.at(iB));
+    v.wA = mul(xA, lA);
+    v.wB = mul(xB, lB);
     v.w = v.wB - v.wA;
+}
+GOI_D void set_vertex(SVert& v, const Proxy& pA, const Xf& xA, int iA, const Proxy& pB, const Xf& xB, int iB) {
+    set_vertex(v, xA, iA, pA.at(iA), xB, iB, pB.at(iB));
 }
 
 GOI_D void simplex_solve2(SVert* v, int& count) {
@@ -232,7 +243,8 @@ GOI_D float gjk_distance(SimplexCache& cache, const Proxy& pA, const Xf& xA, con
         if (dot(d, d) < kEps * kEps) break;
         // the new vertex takes slot `count` (1 or 2); its barycentric coordinate is left as it was
         SVert nv;
-        set_vertex(nv, pA, xA, support(pA, mulT(xA.q, -d)), pB, xB, support(pB, mulT(xB.q, d)));
+        const Support sa = support(pA, mulT(xA.q, -d)), sb = support(pB, mulT(xB.q, d));
+        set_vertex(nv, xA, sa.i, sa.v, xB, sb.i, sb.v);
         nv.a = count == 1 ? v[1].a : v[2].a;
         if (count == 1) v[1] = nv;
         else v[2] = nv;
@@ -315,19 +327,19 @@ GOI_D float sep_find_min(const SepFn& f, const Proxy& pA, const Sweep& sA, const
                          V2& lB, float t, RotMemo& ma, RotMemo& mb) {
     const Xf xA = sweep_xf(sA, t, ma), xB = sweep_xf(sB, t, mb);
     if (f.type == kSepPoints) {
-        lA = pA.at(support(pA, mulT(xA.q, f.axis)));
-        lB = pB.at(support(pB, mulT(xB.q, -f.axis)));
+        lA = support(pA, mulT(xA.q, f.axis)).v;
+        lB = support(pB, mulT(xB.q, -f.axis)).v;
         return dot(mul(xB, lB) - mul(xA, lA), f.axis);
     }
     if (f.type == kSepFaceA) {
         const V2 n = mul(xA.q, f.axis);
         lA = mk(0.0f, 0.0f);
-        lB = pB.at(support(pB, mulT(xB.q, -n)));
+        lB = support(pB, mulT(xB.q, -n)).v;
         return dot(mul(xB, lB) - mul(xA, f.lp), n);
     }
     const V2 n = mul(xB.q, f.axis);
     lB = mk(0.0f, 0.0f);
-    lA = pA.at(support(pA, mulT(xA.q, -n)));
+    lA = support(pA, mulT(xA.q, -n)).v;
     return dot(mul(xA, lA) - mul(xB, f.lp), n);
 }
 
