@@ -27,8 +27,22 @@ GOI_D int feature_key(int ia, int ib, int ta, int tb) { return ia | (ib << 8) | 
 GOI_D V2 mvert(const DModel& m, int f, int i) { return m.poly[16 * f + i]; }
 GOI_D V2 mnorm(const DModel& m, int f, int i) { return m.poly[16 * f + 8 + i]; }
 
+// the smallest separation of poly2's first c2 vertices (of kN slots) from the plane through v1 with normal n
+template <int kN>
+GOI_D float face_min_separation(V2 n, V2 v1, const V2* v2s, int c2) {
+    float si = kMaxFloat;
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+        if (j < c2) {
+            const float sij = dot(n, v2s[j] - v1);
+            if (sij < si) si = sij;
+        }
+    }
+    return si;
+}
+
 // b2FindMaxSeparation: (edge of poly1, separation) over poly1's normals against poly2's vertices; poly1's normals
-// split over the lane group
+// split over the lane group. Most shapes are quads: their vertex loop runs over 4 slots, not 8.
 template <class Grp>
 GOI_D float max_separation(const DModel& m, int f1, const Xf& xf1, int f2, const Xf& xf2, int& edge, const Grp& g) {
     const int c1 = m.fix[f1].count, c2 = m.fix[f2].count;
@@ -46,14 +60,9 @@ GOI_D float max_separation(const DModel& m, int f1, const Xf& xf1, int f2, const
         if (i >= c1) break;
         const V2 n = mul(xf.q, ni);
         const V2 v1 = mul(xf, vi);
-        float si = kMaxFloat;
-#pragma unroll
-        for (int j = 0; j < kPoly; ++j) {
-            if (j < c2) {
-                const float sij = dot(n, v2s[j] - v1);
-                if (sij < si) si = sij;
-            }
-        }
+        float si;
+        if (c2 <= 4) si = face_min_separation<4>(n, v1, v2s, c2);
+        else si = face_min_separation<kPoly>(n, v1, v2s, c2);
         if (si > maxsep) {
             maxsep = si;
             best = i;

@@ -454,7 +454,21 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
     W.i32(GOI_S_OVERFLOW, 0) += np.total - np.kept;
 }
 
-// b2Fixture::ComputeAABB for fixture f at transform t
+// the bounds of vertices 1 .. n-1 (of kN slots) under transforms t1 and t2, joined to (lo1, hi1) and (lo2, hi2)
+template <int kN>
+GOI_D void aabb2_over(const V2* vs, int n, const Xf& t1, const Xf& t2, V2& lo1, V2& hi1, V2& lo2, V2& hi2) {
+#pragma unroll
+    for (int i = 1; i < kN; ++i) {
+        if (i < n) {
+            const V2 v1 = mul(t1, vs[i]), v2 = mul(t2, vs[i]);
+            lo1.x = bmin(lo1.x, v1.x); lo1.y = bmin(lo1.y, v1.y);
+            hi1.x = bmax(hi1.x, v1.x); hi1.y = bmax(hi1.y, v1.y);
+            lo2.x = bmin(lo2.x, v2.x); lo2.y = bmin(lo2.y, v2.y);
+            hi2.x = bmax(hi2.x, v2.x); hi2.y = bmax(hi2.y, v2.y);
+        }
+    }
+}
+
 // b2Shape::ComputeAABB of fixture f under transforms t1 and t2 (a1, a2). The fixture's vertex slots (all kPoly of
 // them: the Model pads every shape) load in one batch with its type, count and radius.
 GOI_D void shape_aabb2(const DModel& m, int f, const Xf& t1, const Xf& t2, float4& a1, float4& a2) {
@@ -470,16 +484,8 @@ GOI_D void shape_aabb2(const DModel& m, int f, const Xf& t1, const Xf& t2, float
         return;
     }
     V2 lo1 = mul(t1, vs[0]), hi1 = lo1, lo2 = mul(t2, vs[0]), hi2 = lo2;
-#pragma unroll
-    for (int i = 1; i < kPoly; ++i) {
-        if (i < n) {
-            const V2 v1 = mul(t1, vs[i]), v2 = mul(t2, vs[i]);
-            lo1.x = bmin(lo1.x, v1.x); lo1.y = bmin(lo1.y, v1.y);
-            hi1.x = bmax(hi1.x, v1.x); hi1.y = bmax(hi1.y, v1.y);
-            lo2.x = bmin(lo2.x, v2.x); lo2.y = bmin(lo2.y, v2.y);
-            hi2.x = bmax(hi2.x, v2.x); hi2.y = bmax(hi2.y, v2.y);
-        }
-    }
+    if (n <= 4) aabb2_over<4>(vs, n, t1, t2, lo1, hi1, lo2, hi2);  // a quad's loop covers 4 slots
+    else aabb2_over<kPoly>(vs, n, t1, t2, lo1, hi1, lo2, hi2);
     a1 = make_float4(lo1.x - r, lo1.y - r, hi1.x + r, hi1.y + r);
     a2 = make_float4(lo2.x - r, lo2.y - r, hi2.x + r, hi2.y + r);
 }

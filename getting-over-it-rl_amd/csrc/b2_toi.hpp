@@ -110,18 +110,19 @@ GOI_D Proxy proxy_of(const DModel& m, int f) {
     return p;
 }
 // b2DistanceProxy::GetSupport and GetVertex together: the first index of the largest dot and its vertex, selected in
-// the same pass over the slots (no select chain over the slots by index after it)
+// the same pass over the slots (no select chain over the slots by index after it); a quad's pass covers 4 slots
 struct Support {
     V2 v;
     int i;
 };
-GOI_D Support support(const Proxy& p, V2 d) {
+template <int kN>
+GOI_D Support support_over(const Proxy& p, V2 d) {
     Support s;
     s.i = 0;
     s.v = p.v[0];
     float bv = dot(p.v[0], d);
 #pragma unroll
-    for (int i = 1; i < kPoly; ++i) {
+    for (int i = 1; i < kN; ++i) {
         const float v = dot(p.v[i], d);
         if (i < p.count && v > bv) {
             s.i = i;
@@ -130,6 +131,10 @@ GOI_D Support support(const Proxy& p, V2 d) {
         }
     }
     return s;
+}
+GOI_D Support support(const Proxy& p, V2 d) {
+    if (p.count <= 4) return support_over<4>(p, d);
+    return support_over<kPoly>(p, d);
 }
 
 struct SVert {
