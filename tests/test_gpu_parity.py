@@ -406,6 +406,29 @@ def test_step_n_equals_repeated_steps(oracle, monkeypatch, case, wpw, k):
         assert leaf_mismatches(ref, got_f) == [], f"launch {launch}"
 
 
+@pytest.mark.parametrize("wpw,n,pitch", [(8, 250, 256), (20, 256, None), (13, 250, None)])
+def test_step_n_lanes_without_a_world(oracle, monkeypatch, wpw, n, pitch):
+    """step_n_ (3 steps a launch, two launches) on blocks with lanes that run no world: the multi-step path sets up
+    each step's cooperative views afresh as the single step does. The rig's multi-step instance on a packed State of
+    pitch 256 with 250 worlds, the generic kernel at 20 and 13 worlds per wave. Config 4 with actions, bit for bit."""
+    monkeypatch.setenv("GOI_WORLDS_PER_WAVE", str(wpw))
+    s, m, st, cfg = b2.scenes.make_config(4, n, capacity=40)
+    rng = np.random.default_rng(29)
+    dev = b2.layout.to_device(st, "cuda", pitch)
+    ref = oracle.copy(st)
+    for launch in range(2):
+        a = b2.scenes.actions(rng, n)
+        b2.scenes.apply_actions(ref.joints.motor_speed, ref.joints.max_motor, a)
+        b2.scenes.apply_actions(dev.joints.motor_speed, dev.joints.max_motor, torch.from_numpy(a).cuda())
+        b2.step_n_(m, dev, s, cfg.dt, 3)
+        info = b2.last_launch()
+        assert info["worlds_per_wave"] == wpw and info["blocks"] == -(-n // wpw), info
+        assert info["kernel"] == ("rig" if pitch == 256 else "generic"), info
+        for _ in range(3):
+            oracle.step_(m, ref, s, cfg.dt)
+        assert leaf_mismatches(ref, b2.layout.to_host(dev)) == [], f"launch {launch}"
+
+
 @pytest.mark.parametrize("edges", ["quad", "native"])
 def test_rig_kernel_parity(oracle, monkeypatch, edges):
     """The step instance compiled for the rig's dimensions (5 bodies, 40 slots, 3 joints, 4 rows, 8 worlds per
