@@ -288,6 +288,27 @@ GOI_D int toi_search_prepare(const DModel& m, const World& W, const Rows& CR, co
             const bool act_b = W.awake(Bb) && !W.is_static(Bb);
             return (act_a || act_b) && pair_rule(m, W, s, A, Bb);
         });
+        // No alignment happens when no needed contact's bodies differ in alpha0 (the first search of a step, where
+        // every body starts at 0): the chunk's tasks are then its needed contacts in list order, which the lane group
+        // sets up together, each lane at its own positions.
+        const int e = min(q0 + 64, n);
+        bool align = false;
+        for (int i = q0 + W.sub; i < e; i += W.G) {
+            if (!((need >> (i - q0)) & 1ull)) continue;
+            const int c = W.order(i);
+            align |= W.f(GOI_T_ALPHA0, W.ba(c)) != W.f(GOI_T_ALPHA0, W.bb(c));
+        }
+        if (!group_any(W.grp(), align)) {
+            for (int i = q0 + W.sub; i < e; i += W.G) {
+                if (!((need >> (i - q0)) & 1ull)) continue;
+                const int c = W.order(i);
+                W.newp(nt + __popcll(need & ((1ull << (i - q0)) - 1ull))) = c;
+                W.set_tflag(c, 1);  // the toi itself arrives in pass 2
+            }
+            nt += __popcll(need);
+            group_sync();
+            continue;
+        }
         for (unsigned long long left = need; left; left &= left - 1) {
             const int c = W.order(q0 + __builtin_ctzll(left));
             const int A = W.ba(c), Bb = W.bb(c);
