@@ -406,6 +406,28 @@ def test_step_n_equals_repeated_steps(oracle, monkeypatch, case, wpw, k):
         assert leaf_mismatches(ref, got_f) == [], f"launch {launch}"
 
 
+@pytest.mark.parametrize("case", ["island", "native_edges"])
+def test_other_kernels_with_lanes_without_a_world(oracle, monkeypatch, case):
+    """A partly filled last block on the island instance (config 5, 250 worlds at 4 a wave on a packed State of pitch
+    256: its SolveTOI re-derives its views in each event iteration) and on the generic kernel with native edge shapes
+    (config 4 with a b2ChainShape terrain, 250 worlds at 8 a wave). 8 steps with actions, bit for bit."""
+    if case == "island":
+        monkeypatch.setenv("GOI_WORLDS_PER_WAVE", "4")
+        s, m, st, cfg = b2.scenes.make_config(5, 250, edges="quad")
+        pitch, wpw, kernel = 256, 4, "island"
+    else:
+        monkeypatch.setenv("GOI_WORLDS_PER_WAVE", "8")
+        s, m, st, cfg = b2.scenes.make_config(4, 250, edges="native")
+        pitch, wpw, kernel = None, 8, "generic"
+    rng = np.random.default_rng(31)
+
+    def used(k, ref, dev):
+        info = b2.last_launch()
+        assert info["worlds_per_wave"] == wpw and info["blocks"] == -(-250 // wpw), info
+        assert info["kernel"] == kernel, info
+    _run(m, st, s, cfg.dt, 8, oracle, [b2.scenes.actions(rng, 250) for _ in range(8)], on_step=used, pitch=pitch)
+
+
 @pytest.mark.parametrize("wpw,n,pitch", [(8, 250, 256), (20, 256, None), (13, 250, None)])
 def test_step_n_lanes_without_a_world(oracle, monkeypatch, wpw, n, pitch):
     """step_n_ (3 steps a launch, two launches) on blocks with lanes that run no world: the multi-step path sets up
