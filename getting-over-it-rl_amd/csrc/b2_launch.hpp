@@ -29,6 +29,7 @@ struct Launch {
     float dt;
     int n_steps;  // consecutive steps of every world in this launch (>= 1)
     GoiDebug dbg;
+    const int* order;  // block b steps world group order[b] (k_group_order), or null: the XCD mapping (xcd_group)
 };
 
 
@@ -100,6 +101,9 @@ __device__ __forceinline__ int xcd_group() {
     const int nb = gridDim.x, b = blockIdx.x, x = b & 7, q = nb >> 3, r = nb & 7;
     return x * q + min(x, r) + (b >> 3);
 }
+
+// The world group of this block of launch L.
+__device__ __forceinline__ int block_group(const Launch& L) { return L.order ? L.order[blockIdx.x] : xcd_group(); }
 
 // The block's cooperative view (Coop) for lanes whose world is W (or lane 0's, for lanes without one).
 __device__ __forceinline__ Coop block_coop(const Launch& L, const World& W, int* lds, int w0) {
@@ -213,7 +217,7 @@ template <bool kMulti, bool kOpaqueToi = false>  // kOpaqueToi: solve_toi_world'
 __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     GOI_DYNAMIC_LDS(lds);
     sincos_table_load();
-    const int w0 = xcd_group() * L.wpw;
+    const int w0 = block_group(L) * L.wpw;
     const auto fresh_bc = [&] {
         return block_copy(L.leaf, L.pitch, L.n, L.B, L.C, L.J, L.R, L.wpw, lds, w0, lane_now(), kBlock);
     };

@@ -139,6 +139,44 @@ __global__ void k_world_manifold(DModel m, Launch L, float* normal, float* point
     }
 }
 
+// The block order of a launch that runs its blocks in more than one round: the world groups whose worlds had the most
+// TOI events in the previous step (the State's toi.events) first, so that the longest blocks start in the first
+// round and the others fill the rounds after them. A group's class is its largest count (8 or more, 3 or more, the
+// rest); the groups of a class keep their order. One wavefront: lane i takes a run of consecutive groups, and the
+// lanes' class counts are scanned across the wavefront. The step's results do not depend on the order.
+__global__ void __launch_bounds__(kBlock) k_group_order(const int* events, int n, int wpw, int groups, int* order) {
+    const int lane = threadIdx.x, lanes = blockDim.x;
+    const int per = (groups + lanes - 1) / lanes;
+    const int g0 = min(lane * per, groups), g1 = min(g0 + per, groups);
+    const auto cls = [&](int g) {
+        int mx = 0;
+        for (int w = g * wpw; w < min(n, (g + 1) * wpw); ++w) mx = max(mx, events[w]);
+        return mx >= 8 ? 0 : mx >= 3 ? 1 : 2;
+    };
+    int c0 = 0, c1 = 0, c2 = 0;
+    for (int g = g0; g < g1; ++g) {
+        const int c = cls(g);
+        c0 += c == 0;
+        c1 += c == 1;
+        c2 += c == 2;
+    }
+    int i0 = c0, i1 = c1, i2 = c2;  // inclusive prefix sums over the lanes
+    for (int d = 1; d < lanes; d <<= 1) {
+        const int v0 = __shfl_up(i0, d, 64), v1 = __shfl_up(i1, d, 64), v2 = __shfl_up(i2, d, 64);
+        if (lane >= d) {
+            i0 += v0;
+            i1 += v1;
+            i2 += v2;
+        }
+    }
+    const int t0 = __shfl(i0, lanes - 1, 64), t1 = __shfl(i1, lanes - 1, 64);
+    int p0 = i0 - c0, p1 = t0 + i1 - c1, p2 = t0 + t1 + i2 - c2;
+    for (int g = g0; g < g1; ++g) {
+        const int c = cls(g);
+        order[c == 0 ? p0++ : c == 1 ? p1++ : p2++] = g;
+    }
+}
+
 // The action-driven motor of joint `joint` in every world: motor_speed = gs * a_x, max_motor = gt * |a| (float32,
 // one rounding per operation, |a| by IEEE square root), into the State's worlds-minor joint leaves.
 __global__ void k_motor_actions(const float* a, float* speed, float* torque, int n, int pitch, int joint, float gs,
@@ -649,6 +687,7 @@ static void fill_launch(Launch& L, const GoiModel* M, const GoiStateView* v, con
     L.dt = dt;
     std::memset(&L.dbg, 0, sizeof(L.dbg));
     L.scratch = nullptr;
+    L.order = nullptr;
     L.wpw = worlds_per_wave(v->n_worlds, workspace_bytes(L.B, L.C, L.J, L.R));
     L.packed = !L.full_rows && packed_state(v) != nullptr;
 }
@@ -661,9 +700,10 @@ static size_t scratch_words(const GoiStateView* state) {
 
 // The rows of stream st's launches with model M (M->mu held): the stream's buffer, allocated on its first call and
 // replaced by a larger one when this batch needs more. The old buffer is freed only after the stream's earlier work,
-// the only work that reads it, has finished.
+// the only work that reads it, has finished. Past the rows, pitch + 64 words hold a launch's block order
+// (k_group_order).
 static int stream_rows(GoiModel* M, const GoiStateView* state, hipStream_t st, uint32_t** rows) {
-    const size_t words = std::max<size_t>(scratch_words(state), 1);
+    const size_t words = scratch_words(state) + (size_t)state->pitch + 64;
     StreamScratch* e = nullptr;
     for (StreamScratch& s : M->scratch)
         if (s.stream == st) e = &s;
@@ -702,8 +742,10 @@ static int check_step_args(const GoiModel* model, const GoiStateView* state, con
 }
 
 // Launches n_steps steps of every world of `state` with the constraint rows at `rows` (scratch_words(state) words).
+// order_buf: room for the block order (pitch + 64 words), or null (the blocks then run in the XCD order). A launch
+// whose blocks do not all fit on the GPU at once, with TOI on, first orders its blocks (k_group_order).
 static int launch_step(const GoiModel* M, const GoiStateView* state, const GoiSettings* settings, float dt,
-                       int32_t n_steps, hipStream_t st, const GoiDebug* debug, uint32_t* rows) {
+                       int32_t n_steps, hipStream_t st, const GoiDebug* debug, uint32_t* rows, int* order_buf) {
     Launch L;
     fill_launch(L, M, state, settings, dt);
     L.scratch = rows;
@@ -727,6 +769,14 @@ static int launch_step(const GoiModel* M, const GoiStateView* state, const GoiSe
                         L.packed && plain && !dbg;
     g_last_launch = GoiLaunchInfo{L.wpw, grid, (int32_t)lds,
                                   rig ? GOI_KERNEL_RIG : island ? GOI_KERNEL_ISLAND : GOI_KERNEL_GENERIC};
+    const long resident = (long)cu_count() * std::min<long>(kBlocksPerCu, (long)(kCuLdsBytes / (lds + kStaticLdsBytes)));
+    if (order_buf && settings->continuous_physics && grid > resident) {
+        hipLaunchKernelGGL(k_group_order, dim3(1), dim3(kBlock), 0, st,
+                           static_cast<const int*>(state->leaf[GOI_T_EVENTS]), state->n_worlds, L.wpw, grid,
+                           order_buf);
+        HIP_TRY(hipGetLastError());
+        L.order = order_buf;
+    }
     if (rig) {
         const hipError_t e = launch_rig_step(M->d, L, n_steps != 1, plain, g, lds, st);
         if (e != hipSuccess) return fail(GOI_E_HIP, std::string("launch_rig_step: ") + hipGetErrorString(e));
@@ -754,7 +804,8 @@ int32_t goi_step_n(const GoiModel* model, const GoiStateView* state, const GoiSe
     uint32_t* rows = nullptr;
     rc = stream_rows(M, state, st, &rows);
     if (rc != GOI_OK) return rc;
-    return launch_step(M, state, settings, dt, n_steps, st, debug, rows);
+    return launch_step(M, state, settings, dt, n_steps, st, debug, rows,
+                       reinterpret_cast<int*>(rows + scratch_words(state)));
 }
 
 int32_t goi_step_n_noalloc(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, float dt,
@@ -769,7 +820,8 @@ int32_t goi_step_n_noalloc(const GoiModel* model, const GoiStateView* state, con
                                            " ((C * 54 + J * 57) * (pitch + 64) words); use goi_step_n");
     uint32_t* rows = static_rows(model->device);
     if (!rows) return fail(GOI_E_ARG, "goi_step_n_noalloc: the model's device has no static rows set up");
-    return launch_step(model, state, settings, dt, n_steps, static_cast<hipStream_t>(hip_stream), debug, rows);
+    return launch_step(model, state, settings, dt, n_steps, static_cast<hipStream_t>(hip_stream), debug, rows,
+                       nullptr);
 }
 
 int32_t goi_collide(const GoiModel* model, const GoiStateView* state, const GoiSettings* settings, void* hip_stream) {

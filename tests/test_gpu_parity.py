@@ -406,6 +406,29 @@ def test_step_n_equals_repeated_steps(oracle, monkeypatch, case, wpw, k):
         assert leaf_mismatches(ref, got_f) == [], f"launch {launch}"
 
 
+@pytest.mark.parametrize("case", ["island", "rig4"])
+def test_multi_round_launches(oracle, monkeypatch, case):
+    """Launches with more blocks than the GPU holds at once run their blocks in the order k_group_order gives (the
+    world groups with the most TOI events of the previous step first): config 5 at 8,192 worlds (2,048 blocks of the
+    island instance, 5 a CU) and config 4 at 16,384 worlds with 4 worlds a wave (4,096 blocks of the generic kernel,
+    8 a CU). 6 steps with actions, bit for bit."""
+    if case == "island":
+        monkeypatch.setenv("GOI_WORLDS_PER_WAVE", "4")
+        s, m, st, cfg = b2.scenes.make_config(5, 8192, edges="quad")
+        n, kernel = 8192, "island"
+    else:
+        monkeypatch.setenv("GOI_WORLDS_PER_WAVE", "4")
+        s, m, st, cfg = b2.scenes.make_config(4, 16384)
+        n, kernel = 16384, "generic"
+    rng = np.random.default_rng(37)
+
+    def used(k, ref, dev):
+        info = b2.last_launch()
+        assert info["worlds_per_wave"] == 4 and info["blocks"] == n // 4 and info["kernel"] == kernel, info
+    ref = _run(m, st, s, cfg.dt, 6, oracle, [b2.scenes.actions(rng, n) for _ in range(6)], on_step=used, every=3)
+    assert int(np.asarray(ref.toi.events).sum()) > 0
+
+
 @pytest.mark.parametrize("case", ["island", "native_edges"])
 def test_other_kernels_with_lanes_without_a_world(oracle, monkeypatch, case):
     """A partly filled last block on the island instance (config 5, 250 worlds at 4 a wave on a packed State of pitch
