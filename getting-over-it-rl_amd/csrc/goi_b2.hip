@@ -141,39 +141,50 @@ __global__ void k_world_manifold(DModel m, Launch L, float* normal, float* point
 
 // The block order of a launch that runs its blocks in more than one round: the world groups whose worlds had the most
 // TOI events in the previous step (the State's toi.events) first, so that the longest blocks start in the first
-// round and the others fill the rounds after them. A group's class is its largest count (8 or more, 3 or more, the
-// rest); the groups of a class keep their order. One wavefront: lane i takes a run of consecutive groups, and the
-// lanes' class counts are scanned across the wavefront. The step's results do not depend on the order.
+// round and the others fill the rounds after them. Each XCD keeps the contiguous range of groups xcd_group gives it
+// (block b runs on XCD b % 8): within the range, chunks of groups that share the State's 128-byte lines (32 worlds)
+// are ordered by class, the largest count of their worlds (8 or more, 3 or more, the rest), each class in chunk
+// order, so that a line's worlds stay in one XCD's L2. One wavefront: per XCD, lane i takes a run of consecutive
+// chunks, and the lanes' class sizes are scanned across the wavefront. The step's results do not depend on the order.
 __global__ void __launch_bounds__(kBlock) k_group_order(const int* events, int n, int wpw, int groups, int* order) {
     const int lane = threadIdx.x, lanes = blockDim.x;
-    const int per = (groups + lanes - 1) / lanes;
-    const int g0 = min(lane * per, groups), g1 = min(g0 + per, groups);
-    const auto cls = [&](int g) {
-        int mx = 0;
-        for (int w = g * wpw; w < min(n, (g + 1) * wpw); ++w) mx = max(mx, events[w]);
-        return mx >= 8 ? 0 : mx >= 3 ? 1 : 2;
-    };
-    int c0 = 0, c1 = 0, c2 = 0;
-    for (int g = g0; g < g1; ++g) {
-        const int c = cls(g);
-        c0 += c == 0;
-        c1 += c == 1;
-        c2 += c == 2;
-    }
-    int i0 = c0, i1 = c1, i2 = c2;  // inclusive prefix sums over the lanes
-    for (int d = 1; d < lanes; d <<= 1) {
-        const int v0 = __shfl_up(i0, d, 64), v1 = __shfl_up(i1, d, 64), v2 = __shfl_up(i2, d, 64);
-        if (lane >= d) {
-            i0 += v0;
-            i1 += v1;
-            i2 += v2;
+    const int cg = wpw < 32 ? 32 / wpw : 1;  // groups per chunk
+    const int q = groups >> 3, r = groups & 7;
+    for (int x = 0; x < 8; ++x) {
+        const int base = x * q + min(x, r), size = q + (x < r ? 1 : 0);  // XCD x's groups
+        const int chunks = (size + cg - 1) / cg;
+        const int per = (chunks + lanes - 1) / lanes;
+        const int k0 = min(lane * per, chunks), k1 = min(k0 + per, chunks);
+        const auto span = [&](int k) { return min(cg, size - k * cg); };  // groups in chunk k
+        const auto cls = [&](int k) {
+            int mx = 0;
+            const int w1 = min(n, (base + k * cg + span(k)) * wpw);
+            for (int w = (base + k * cg) * wpw; w < w1; ++w) mx = max(mx, events[w]);
+            return mx >= 8 ? 0 : mx >= 3 ? 1 : 2;
+        };
+        int c0 = 0, c1 = 0, c2 = 0;  // this lane's groups per class
+        for (int k = k0; k < k1; ++k) {
+            const int c = cls(k), g = span(k);
+            c0 += c == 0 ? g : 0;
+            c1 += c == 1 ? g : 0;
+            c2 += c == 2 ? g : 0;
         }
-    }
-    const int t0 = __shfl(i0, lanes - 1, 64), t1 = __shfl(i1, lanes - 1, 64);
-    int p0 = i0 - c0, p1 = t0 + i1 - c1, p2 = t0 + t1 + i2 - c2;
-    for (int g = g0; g < g1; ++g) {
-        const int c = cls(g);
-        order[c == 0 ? p0++ : c == 1 ? p1++ : p2++] = g;
+        int i0 = c0, i1 = c1, i2 = c2;  // inclusive prefix sums over the lanes
+        for (int d = 1; d < lanes; d <<= 1) {
+            const int v0 = __shfl_up(i0, d, 64), v1 = __shfl_up(i1, d, 64), v2 = __shfl_up(i2, d, 64);
+            if (lane >= d) {
+                i0 += v0;
+                i1 += v1;
+                i2 += v2;
+            }
+        }
+        const int t0 = __shfl(i0, lanes - 1, 64), t1 = __shfl(i1, lanes - 1, 64);
+        int p0 = i0 - c0, p1 = t0 + i1 - c1, p2 = t0 + t1 + i2 - c2;  // this lane's first position in each class
+        for (int k = k0; k < k1; ++k) {
+            const int c = cls(k), g = span(k);
+            int& p = c == 0 ? p0 : c == 1 ? p1 : p2;
+            for (int i = 0; i < g; ++i, ++p) order[8 * p + x] = base + k * cg + i;  // XCD x's p-th block
+        }
     }
 }
 
