@@ -30,6 +30,7 @@ struct Launch {
     int n_steps;  // consecutive steps of every world in this launch (>= 1)
     GoiDebug dbg;
     const int* order;  // block b steps world group order[b] (k_group_order), or null: the XCD mapping (xcd_group)
+    int* cost;         // with order: each group's block time in this launch (clock ticks), for the next launch's order
 };
 
 
@@ -216,6 +217,7 @@ __device__ __forceinline__ void step_worlds(const DModel& m, const Launch& L, in
 template <bool kMulti, bool kOpaqueToi = false>  // kOpaqueToi: solve_toi_world's kOpaqueViews
 __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
     GOI_DYNAMIC_LDS(lds);
+    const uint64_t t_start = block_clock();
     sincos_table_load();
     const int w0 = block_group(L) * L.wpw;
     const auto fresh_bc = [&] {
@@ -266,6 +268,10 @@ __device__ __forceinline__ void step_block(const DModel& m, const Launch& L) {
             step_worlds<kOpaqueToi>(m, L, lds, w0);
         }
         store_mirror_block(fresh_bc());
+    }
+    if (L.cost && lane_now() == 0) {
+        const uint64_t dt = block_clock() - t_start;
+        L.cost[block_group(L)] = dt < 0x7fffffffull ? (int)dt : 0x7fffffff;
     }
 }
 

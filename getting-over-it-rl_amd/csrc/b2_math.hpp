@@ -102,6 +102,16 @@ GOI_D int lane_now() {
 #endif
 }
 
+// A clock for timing a block's work (the GPU's constant-rate real-time counter; 0 in the host build); nothing the step
+// computes depends on it.
+GOI_D uint64_t block_clock() {
+#ifdef GOI_HOST_BUILD
+    return 0;
+#else
+    return __builtin_amdgcn_s_memrealtime();
+#endif
+}
+
 // The wave's instruction-issue priority among the waves of its SIMD (0 to 3); nothing else depends on it.
 template <int kPrio>
 GOI_D void wave_priority() {

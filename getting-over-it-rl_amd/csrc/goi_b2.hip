@@ -139,15 +139,22 @@ __global__ void k_world_manifold(DModel m, Launch L, float* normal, float* point
     }
 }
 
-// The block order of a launch that runs its blocks in more than one round: the world groups whose worlds had the most
-// TOI events in the previous step (the State's toi.events) first, so that the longest blocks start in the first
-// round and the others fill the rounds after them. Each XCD keeps the contiguous range of groups xcd_group gives it
-// (block b runs on XCD b % 8): within the range, chunks of groups that share the State's 128-byte lines (32 worlds)
-// are ordered by class, the largest count of their worlds (8 or more, 3 or more, the rest), each class in chunk
-// order, so that a line's worlds stay in one XCD's L2. One wavefront: per XCD, lane i takes a run of consecutive
-// chunks, and the lanes' class sizes are scanned across the wavefront. The step's results do not depend on the order.
-__global__ void __launch_bounds__(kBlock) k_group_order(const int* events, int n, int wpw, int groups, int* order) {
+// The block order of a launch that runs its blocks in more than one round: the longest blocks first, so that they
+// start in the first round and the shorter ones fill the rounds after them. A world group's expected time is its
+// block's time in the previous launch on this stream (`cost`, clock ticks, 0 where unknown), in classes a factor of
+// sqrt(2) apart below the longest; without any such time, its worlds' largest TOI event count of the previous step
+// (the State's toi.events: 8 or more, 3 or more, the rest). Each XCD keeps the contiguous range of groups xcd_group
+// gives it (block b runs on XCD b % 8): within the range, chunks of groups that share the State's 128-byte lines
+// (32 worlds) are ordered by class, each class in chunk order, so that a line's worlds stay in one XCD's L2. One
+// wavefront: per XCD, lane i takes a run of consecutive chunks, and the lanes' class sizes are scanned across the
+// wavefront. The step's results do not depend on the order.
+__global__ void __launch_bounds__(kBlock) k_group_order(const int* events, const int* cost, int n, int wpw, int groups,
+                                                        int* order) {
+    constexpr int kClasses = 8;
     const int lane = threadIdx.x, lanes = blockDim.x;
+    int top = 0;  // the longest block time of the previous launch
+    for (int g = lane; g < groups; g += lanes) top = max(top, cost[g]);
+    for (int d = 1; d < lanes; d <<= 1) top = max(top, __shfl_xor(top, d, 64));
     const int cg = wpw < 32 ? 32 / wpw : 1;  // groups per chunk
     const int q = groups >> 3, r = groups & 7;
     for (int x = 0; x < 8; ++x) {
@@ -157,33 +164,44 @@ __global__ void __launch_bounds__(kBlock) k_group_order(const int* events, int n
         const int k0 = min(lane * per, chunks), k1 = min(k0 + per, chunks);
         const auto span = [&](int k) { return min(cg, size - k * cg); };  // groups in chunk k
         const auto cls = [&](int k) {
+            const int g0 = base + k * cg, g1 = g0 + span(k);
+            if (top > 0) {
+                int t = 0;
+                for (int g = g0; g < g1; ++g) t = max(t, cost[g]);
+                return t > 0 ? min(kClasses - 1, (int)(2.0f * log2f((float)top / (float)t))) : kClasses - 1;
+            }
             int mx = 0;
-            const int w1 = min(n, (base + k * cg + span(k)) * wpw);
-            for (int w = (base + k * cg) * wpw; w < w1; ++w) mx = max(mx, events[w]);
+            for (int w = g0 * wpw; w < min(n, g1 * wpw); ++w) mx = max(mx, events[w]);
             return mx >= 8 ? 0 : mx >= 3 ? 1 : 2;
         };
-        int c0 = 0, c1 = 0, c2 = 0;  // this lane's groups per class
+        int cnt[kClasses];  // this lane's groups per class
+#pragma unroll
+        for (int c = 0; c < kClasses; ++c) cnt[c] = 0;
         for (int k = k0; k < k1; ++k) {
             const int c = cls(k), g = span(k);
-            c0 += c == 0 ? g : 0;
-            c1 += c == 1 ? g : 0;
-            c2 += c == 2 ? g : 0;
+#pragma unroll
+            for (int e = 0; e < kClasses; ++e) cnt[e] += e == c ? g : 0;
         }
-        int i0 = c0, i1 = c1, i2 = c2;  // inclusive prefix sums over the lanes
-        for (int d = 1; d < lanes; d <<= 1) {
-            const int v0 = __shfl_up(i0, d, 64), v1 = __shfl_up(i1, d, 64), v2 = __shfl_up(i2, d, 64);
-            if (lane >= d) {
-                i0 += v0;
-                i1 += v1;
-                i2 += v2;
+        int pos[kClasses];  // this lane's first position in each class
+        int before = 0;     // the groups of the classes before
+#pragma unroll
+        for (int c = 0; c < kClasses; ++c) {
+            int incl = cnt[c];
+            for (int d = 1; d < lanes; d <<= 1) {
+                const int v = __shfl_up(incl, d, 64);
+                if (lane >= d) incl += v;
             }
+            pos[c] = before + incl - cnt[c];
+            before += __shfl(incl, lanes - 1, 64);
         }
-        const int t0 = __shfl(i0, lanes - 1, 64), t1 = __shfl(i1, lanes - 1, 64);
-        int p0 = i0 - c0, p1 = t0 + i1 - c1, p2 = t0 + t1 + i2 - c2;  // this lane's first position in each class
         for (int k = k0; k < k1; ++k) {
             const int c = cls(k), g = span(k);
-            int& p = c == 0 ? p0 : c == 1 ? p1 : p2;
-            for (int i = 0; i < g; ++i, ++p) order[8 * p + x] = base + k * cg + i;  // XCD x's p-th block
+            int p = 0;
+#pragma unroll
+            for (int e = 0; e < kClasses; ++e) p = e == c ? pos[e] : p;
+            for (int i = 0; i < g; ++i) order[8 * (p + i) + x] = base + k * cg + i;  // XCD x's (p + i)-th block
+#pragma unroll
+            for (int e = 0; e < kClasses; ++e) pos[e] += e == c ? g : 0;
         }
     }
 }
@@ -699,6 +717,7 @@ static void fill_launch(Launch& L, const GoiModel* M, const GoiStateView* v, con
     std::memset(&L.dbg, 0, sizeof(L.dbg));
     L.scratch = nullptr;
     L.order = nullptr;
+    L.cost = nullptr;
     L.wpw = worlds_per_wave(v->n_worlds, workspace_bytes(L.B, L.C, L.J, L.R));
     L.packed = !L.full_rows && packed_state(v) != nullptr;
 }
@@ -711,10 +730,10 @@ static size_t scratch_words(const GoiStateView* state) {
 
 // The rows of stream st's launches with model M (M->mu held): the stream's buffer, allocated on its first call and
 // replaced by a larger one when this batch needs more. The old buffer is freed only after the stream's earlier work,
-// the only work that reads it, has finished. Past the rows, pitch + 64 words hold a launch's block order
-// (k_group_order).
+// the only work that reads it, has finished. Past the rows, pitch + 64 words hold a launch's block order and as many
+// its blocks' times (k_group_order), zero in a new buffer.
 static int stream_rows(GoiModel* M, const GoiStateView* state, hipStream_t st, uint32_t** rows) {
-    const size_t words = scratch_words(state) + (size_t)state->pitch + 64;
+    const size_t words = scratch_words(state) + 2 * ((size_t)state->pitch + 64);
     StreamScratch* e = nullptr;
     for (StreamScratch& s : M->scratch)
         if (s.stream == st) e = &s;
@@ -731,6 +750,8 @@ static int stream_rows(GoiModel* M, const GoiStateView* state, hipStream_t st, u
         }
         HIP_TRY(hipMalloc(&e->rows, words * sizeof(uint32_t)));
         e->words = words;
+        const size_t times = scratch_words(state) + (size_t)state->pitch + 64;  // the blocks' times: none yet
+        HIP_TRY(hipMemsetAsync(e->rows + times, 0, (words - times) * sizeof(uint32_t), st));
     }
     *rows = e->rows;
     return GOI_OK;
@@ -782,11 +803,13 @@ static int launch_step(const GoiModel* M, const GoiStateView* state, const GoiSe
                                   rig ? GOI_KERNEL_RIG : island ? GOI_KERNEL_ISLAND : GOI_KERNEL_GENERIC};
     const long resident = (long)cu_count() * std::min<long>(kBlocksPerCu, (long)(kCuLdsBytes / (lds + kStaticLdsBytes)));
     if (order_buf && settings->continuous_physics && grid > resident) {
+        int* cost = order_buf + state->pitch + 64;
         hipLaunchKernelGGL(k_group_order, dim3(1), dim3(kBlock), 0, st,
-                           static_cast<const int*>(state->leaf[GOI_T_EVENTS]), state->n_worlds, L.wpw, grid,
+                           static_cast<const int*>(state->leaf[GOI_T_EVENTS]), cost, state->n_worlds, L.wpw, grid,
                            order_buf);
         HIP_TRY(hipGetLastError());
         L.order = order_buf;
+        L.cost = cost;
     }
     if (rig) {
         const hipError_t e = launch_rig_step(M->d, L, n_steps != 1, plain, g, lds, st);

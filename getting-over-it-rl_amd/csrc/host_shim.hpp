@@ -87,6 +87,10 @@ inline hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind
     if (n) std::memcpy(d, s, n);
     return hipSuccess;
 }
+inline hipError_t hipMemsetAsync(void* d, int v, size_t n, hipStream_t) {
+    if (n) std::memset(d, v, n);
+    return hipSuccess;
+}
 inline hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
 inline hipError_t hipDeviceSynchronize() { return hipSuccess; }
 inline hipError_t hipGetDevice(int* d) { *d = 0; return hipSuccess; }
