@@ -269,8 +269,9 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
 int32_t goi_model_destroy(GoiModel* model);
 
 /* Frees the handle's per-stream constraint and task rows (goi_step, goi_step_n and goi_collide keep one buffer per
- * stream handle they were called on, (C * 54 + J * 57 + 1) * (pitch + 64) 4-byte words each, the last pitch + 64 of
- * them a launch's block order: about 153 MB for 16,384 worlds of the 4-body rig, until goi_model_destroy). A caller that steps on many short-lived or pooled streams calls
+ * stream handle they were called on, (C * 54 + J * 57 + 2) * (pitch + 64) 4-byte words each, the last 2 * (pitch +
+ * 64) of them a launch's block order and its blocks' times: about 153 MB for 16,384 worlds of the 4-body rig, until
+ * goi_model_destroy). A caller that steps on many short-lived or pooled streams calls
  * it to return that memory; the next call on a stream allocates its buffer again. Waits for the model's device to
  * finish first (hipDeviceSynchronize). Must not overlap other calls on the same handle. No counterpart in the
  * reference. */
