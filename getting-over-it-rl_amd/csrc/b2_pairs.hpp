@@ -322,6 +322,22 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
     for (int k = W.sub; k < W.C; k += W.G) n_free += W.pair(k) < 0;
     n_free = group_sum(W.grp(), n_free);
     NewPairs np{W, 0, 0, n_free};
+    // the pairs of this lane's slots (sub, sub + G, ...) in registers for the membership tests below, when they fit
+    constexpr int kHeld = 8;
+    const bool held_all = W.C <= kHeld * W.G;
+    int held[kHeld];
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+        const int k = W.sub + j * W.G;
+        held[j] = held_all && k < W.C ? W.pair(k) : -1;
+    }
+    const auto has_pair = [&](int p) {
+        if (!held_all) return slot_has_pair(W, p);
+        bool has = false;
+#pragma unroll
+        for (int j = 0; j < kHeld; ++j) has |= held[j] == p;
+        return group_any(W.grp(), has);
+    };
     // the fat boxes of all rows into the workspace; the queried rows on active bodies and their union box
     unsigned long long rows = 0ull;
     float4 U = make_float4(kMaxFloat, kMaxFloat, -kMaxFloat, -kMaxFloat);
@@ -398,7 +414,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
                     if (!overlap(fj, W.get_qbox(r))) continue;
                     if (!(m.row[r].dynamic || (ij >> 16))) continue;
                     const int p = m.leaf_cand[(size_t)(first + j) * m.R + r];
-                    if (p < 0 || slot_has_pair(W, p)) continue;
+                    if (p < 0 || has_pair(p)) continue;
                     np.add(p);
                 }
             }
@@ -412,7 +428,7 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         if (!overlap(W.get_qbox(ra), W.get_qbox(rb))) continue;
         if (!(W.is_dynamic(ba) || W.is_dynamic(bb))) continue;
         if (!(W.active(ba) && W.active(bb))) continue;
-        if (slot_has_pair(W, p)) continue;
+        if (has_pair(p)) continue;
         np.add(p);
     }
     if (np.total == 0) return;
