@@ -506,36 +506,28 @@ GOI_D void shape_aabb2(const DModel& m, int f, const Xf& t1, const Xf& t2, float
     a2 = make_float4(lo2.x - r, lo2.y - r, hi2.x + r, hi2.y + r);
 }
 
-// b2Body::SynchronizeFixtures for body b (pairs.py:181-207): swept AABB over the sweep start and the current
-// transform; b2DynamicTree::MoveProxy re-fattens only if the fat box no longer contains it. Returns the rows it
-// re-fattened.
-GOI_D unsigned long long sync_body_fixtures(const DModel& m, const World& W, int b, const Xf& x1) {
-    unsigned long long moved = 0ull;
-    const Xf x2 = W.xf(b);
-    for (int r = 0; r < m.R; ++r) {
-        const MRow row = m.row[r];
-        if (row.body != b) continue;
-        const int f = row.fixture;
-        float4 a1, a2;
-        shape_aabb2(m, f, x1, x2, a1, a2);
-        float lx = bmin(a1.x, a2.x), ly = bmin(a1.y, a2.y);
-        float ux = bmax(a1.z, a2.z), uy = bmax(a1.w, a2.w);
-        const int fr = 4 * W.frow(r);
-        const float fx0 = W.f(GOI_F_FAT, fr), fy0 = W.f(GOI_F_FAT, fr + 1);
-        const float fx1 = W.f(GOI_F_FAT, fr + 2), fy1 = W.f(GOI_F_FAT, fr + 3);
-        if (fx0 <= lx && fy0 <= ly && ux <= fx1 && uy <= fy1) continue;
-        const V2 d = x2.p - x1.p;
-        lx = lx - 0.1f; ly = ly - 0.1f; ux = ux + 0.1f; uy = uy + 0.1f;  // b2_aabbExtension
-        const float ddx = 2.0f * d.x, ddy = 2.0f * d.y;                  // b2_aabbMultiplier
-        if (ddx < 0.0f) lx = lx + ddx; else ux = ux + ddx;
-        if (ddy < 0.0f) ly = ly + ddy; else uy = uy + ddy;
-        W.f(GOI_F_FAT, fr) = lx;
-        W.f(GOI_F_FAT, fr + 1) = ly;
-        W.f(GOI_F_FAT, fr + 2) = ux;
-        W.f(GOI_F_FAT, fr + 3) = uy;
-        moved |= 1ull << r;
-    }
-    return moved;
+// b2Body::SynchronizeFixtures (pairs.py:181-207) for one non-static row r (fixture f) of a body moved from transform
+// x1 (its sweep start) to x2: the swept AABB over both; b2DynamicTree::MoveProxy re-fattens only if the fat box no
+// longer contains it. Returns whether it re-fattened. A body's rows are independent, so callers take one a lane.
+GOI_D bool sync_row(const DModel& m, const World& W, int r, int f, const Xf& x1, const Xf& x2) {
+    float4 a1, a2;
+    shape_aabb2(m, f, x1, x2, a1, a2);
+    float lx = bmin(a1.x, a2.x), ly = bmin(a1.y, a2.y);
+    float ux = bmax(a1.z, a2.z), uy = bmax(a1.w, a2.w);
+    const int fr = 4 * W.frow(r);
+    const float fx0 = W.f(GOI_F_FAT, fr), fy0 = W.f(GOI_F_FAT, fr + 1);
+    const float fx1 = W.f(GOI_F_FAT, fr + 2), fy1 = W.f(GOI_F_FAT, fr + 3);
+    if (fx0 <= lx && fy0 <= ly && ux <= fx1 && uy <= fy1) return false;
+    const V2 d = x2.p - x1.p;
+    lx = lx - 0.1f; ly = ly - 0.1f; ux = ux + 0.1f; uy = uy + 0.1f;  // b2_aabbExtension
+    const float ddx = 2.0f * d.x, ddy = 2.0f * d.y;                  // b2_aabbMultiplier
+    if (ddx < 0.0f) lx = lx + ddx; else ux = ux + ddx;
+    if (ddy < 0.0f) ly = ly + ddy; else uy = uy + ddy;
+    W.f(GOI_F_FAT, fr) = lx;
+    W.f(GOI_F_FAT, fr + 1) = ly;
+    W.f(GOI_F_FAT, fr + 2) = ux;
+    W.f(GOI_F_FAT, fr + 3) = uy;
+    return true;
 }
 
 // the sweep-start transform of body b: q(a0), c0 - q * localCenter

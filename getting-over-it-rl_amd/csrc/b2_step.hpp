@@ -209,9 +209,11 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     // (Collide destroys only contacts whose fat AABBs separated), so the result is the full scan's; a world that ever
     // dropped a candidate (overflow) keeps scanning all rows, since its dropped pairs may now find a slot.
     unsigned long long refat = 0ull;
-    for (int b = W.sub; b < W.B; b += W.G) {
+    for (int r = W.sub; r < m.R; r += W.G) {  // the rows are independent: one per lane of the group
+        const MRow row = m.row[r];
+        const int b = row.body;
         if (I.body_island(b) < 0 || W.is_static(b)) continue;
-        refat |= sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
+        if (sync_row(m, W, r, row.fixture, sweep_start_xf(W, b), W.xf(b))) refat |= 1ull << r;
     }
     refat = group_or(W.grp(), refat);
     group_sync();
@@ -678,13 +680,16 @@ GOI_D void toi_event(const DModel& m, const World& W, const Bodies& bd, const Ro
     group_sync();
     // fixture sync of the island's dynamic bodies and TOI invalidation of their contacts
     unsigned long long moved = 0ull, refat = 0ull;
-    for (int i = W.sub; i < nb; i += W.G) {  // one body per lane of the group, the sets combined after
+    for (int i = W.sub; i < nb; i += W.G) {  // the island's dynamic bodies, combined over the group
         const int b = W.ibuf(i);
-        if (!W.is_dynamic(b)) continue;
-        moved |= 1ull << b;
-        refat |= sync_body_fixtures(m, W, b, sweep_start_xf(W, b));
+        if (W.is_dynamic(b)) moved |= 1ull << b;
     }
     moved = group_or(W.grp(), moved);
+    for (int r = W.sub; r < m.R; r += W.G) {  // their rows, one per lane of the group
+        const MRow row = m.row[r];
+        const int b = row.body;
+        if (((moved >> b) & 1ull) && sync_row(m, W, r, row.fixture, sweep_start_xf(W, b), W.xf(b))) refat |= 1ull << r;
+    }
     refat = group_or(W.grp(), refat);
     // the slot loops below split over the lane group (slots are independent)
     // FindNewContacts; a slot that received a new contact starts with fresh TOI state. Before it, the workspace's
