@@ -619,8 +619,11 @@ GOI_D bool overlap(float4 a, float4 b) {
 struct Rows {
     uint32_t* base;  // the tile's word 0 of this world
     int nf, S;
+    // the row's word 0 first, then the field in it: a constant field becomes a constant offset from one row address
+    // (one address computation per row, not one per field)
     GOI_D uint32_t& u(int row, int field) const {
-        return base[((uint32_t)row * (uint32_t)nf + (uint32_t)field) * (uint32_t)S];
+        uint32_t* const r = base + (uint32_t)row * (uint32_t)(nf * S);
+        return r[(uint32_t)field * (uint32_t)S];
     }
     GOI_D float getf(int row, int field) const { return __uint_as_float(u(row, field)); }
     GOI_D void setf(int row, int field, float v) const { u(row, field) = __float_as_uint(v); }
