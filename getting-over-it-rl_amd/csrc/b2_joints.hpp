@@ -395,13 +395,15 @@ GOI_D void store_rev_impulses(const Rows& R, int i, const RevVRow& r) {
 // joint rows 0..n-1 of a revolute-only model under the v2.4.1 solver, once each, in order
 GOI_D void rev_velocity_sweep(const Bodies& bd, const Rows& R, int n) {
     if (n <= 0) return;
-    RevVRow r = load_rev_vrow(R, 0);
-    for (int i = 0; i < n; ++i) {
-        RevVRow next;
-        if (i + 1 < n) next = load_rev_vrow(R, i + 1);  // in flight while joint i is solved
-        solve_rev_vrow(bd, r);
-        store_rev_impulses(R, i, r);
-        r = next;
+    RevVRow a = load_rev_vrow(R, 0), b;
+    for (int i = 0; i < n; i += 2) {  // as cs_solve_velocity_sweep: joint i + 1 in flight while joint i is solved
+        if (i + 1 < n) b = load_rev_vrow(R, i + 1);
+        solve_rev_vrow(bd, a);
+        store_rev_impulses(R, i, a);
+        if (i + 1 >= n) break;
+        if (i + 2 < n) a = load_rev_vrow(R, i + 2);
+        solve_rev_vrow(bd, b);
+        store_rev_impulses(R, i + 1, b);
     }
 }
 

@@ -484,16 +484,19 @@ GOI_D void store_vimpulses(const Rows& R, int i, const VRow& r) {
     R.setf(i, CF_NI0, r.ni0); R.setf(i, CF_NI1, r.ni1); R.setf(i, CF_TI0, r.ti0); R.setf(i, CF_TI1, r.ti1);
 }
 
-// rows 0..n-1 once each, in order, each loaded in one batch
+// rows 0..n-1 once each, in order, each loaded in one batch while the row before it is solved; two rows a loop
+// iteration, so the two row buffers alternate without copies between them
 GOI_D void cs_solve_velocity_sweep(const Bodies& bd, const Rows& R, int n) {
     if (n <= 0) return;
-    VRow r = load_vrow(R, 0);
-    for (int i = 0; i < n; ++i) {
-        VRow next;
-        if (i + 1 < n) next = load_vrow(R, i + 1);  // in flight while row i is solved
-        solve_vrow(bd, r);
-        store_vimpulses(R, i, r);
-        r = next;
+    VRow a = load_vrow(R, 0), b;
+    for (int i = 0; i < n; i += 2) {
+        if (i + 1 < n) b = load_vrow(R, i + 1);
+        solve_vrow(bd, a);
+        store_vimpulses(R, i, a);
+        if (i + 1 >= n) break;
+        if (i + 2 < n) a = load_vrow(R, i + 2);
+        solve_vrow(bd, b);
+        store_vimpulses(R, i + 1, b);
     }
 }
 
