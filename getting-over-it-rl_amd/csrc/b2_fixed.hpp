@@ -14,11 +14,13 @@ namespace {
 // Every workspace offset, loop bound and leaf offset folds into the instructions, which frees the scalar registers
 // the runtime dimensions and the 71 leaf pointers would hold (spilled scalars come back through v_readlane on every
 // use). kPlain: revolute joints only (the v2.4.1 solver) and no edge shapes, so the other joint and collider code
-// drops out. Launches with debug arrays take k_step, so the debug writes drop out too. The results are those of
-// k_step.
-template <int kB, int kC, int kJ, int kR, int kS, bool kMulti, bool kPlain>
+// drops out. Launches with debug arrays take k_step, so the debug writes drop out too. kIslands: worlds of several
+// islands solve them on separate lanes of the group (DModel::island_lanes); without it that path drops out, for
+// models whose bodies are joined into one island (the rig). The results are those of k_step.
+template <int kB, int kC, int kJ, int kR, int kS, bool kMulti, bool kPlain, bool kIslands>
 __global__ void __launch_bounds__(kBlock, 2) k_step_fixed(DModel m, Launch L) {
     L.B = kB; L.C = kC; L.J = kJ; L.R = kR; L.wpw = kS;
+    if (!kIslands) m.island_lanes = 0;
     L.full_rows = 0;  // the launch takes these instances for compact packed States only
     L.dbg = GoiDebug{};
     m.B = kB; m.J = kJ; m.R = kR;

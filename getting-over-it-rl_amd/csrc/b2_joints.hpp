@@ -142,7 +142,8 @@ GOI_D void jn_prepare(const DModel& m, const World& W, const Bodies& bd, const R
 }
 
 // the velocity part of InitVelocityConstraints (joints.py:202-248)
-GOI_D void jn_warm_start(const Bodies& bd, const Rows& R, int i, bool v24, bool rev_only) {
+template <class BD>
+GOI_D void jn_warm_start(const BD& bd, const Rows& R, int i, bool v24, bool rev_only) {
     const int type = rev_only ? (int)GOI_REVOLUTE : R.geti(i, JF_TYPE), ia = R.geti(i, JF_IA), ib = R.geti(i, JF_IB);
     const float mA = R.getf(i, JF_MA), mB = R.getf(i, JF_MB), iA = R.getf(i, JF_IIA), iB = R.getf(i, JF_IIB);
     const float ix = R.getf(i, JF_IMP0), iy = R.getf(i, JF_IMP1), iz = R.getf(i, JF_IMP2), mi = R.getf(i, JF_MIMP);
@@ -177,7 +178,8 @@ GOI_D void jn_warm_start(const Bodies& bd, const Rows& R, int i, bool v24, bool 
 }
 
 // SolveVelocityConstraints for joint row i (joints.py:257-437, revolute24.patch:166-240)
-GOI_D void jn_solve_velocity(const Bodies& bd, const Rows& R, int i, bool v24, bool rev_only) {
+template <class BD>
+GOI_D void jn_solve_velocity(const BD& bd, const Rows& R, int i, bool v24, bool rev_only) {
     const int type = rev_only ? (int)GOI_REVOLUTE : R.geti(i, JF_TYPE), ia = R.geti(i, JF_IA), ib = R.geti(i, JF_IB);
     const float mA = R.getf(i, JF_MA), mB = R.getf(i, JF_MB), iA = R.getf(i, JF_IIA), iB = R.getf(i, JF_IIB);
     const bool emotor = R.geti(i, JF_EMOTOR) != 0, elimit = R.geti(i, JF_ELIMIT) != 0;
@@ -350,7 +352,8 @@ GOI_D RevVRow load_rev_vrow(const Rows& R, int i) {
     r.lower = R.getf(i, JF_LOWER); r.upper = R.getf(i, JF_UPPER);
     return r;
 }
-GOI_D void solve_rev_vrow(const Bodies& bd, RevVRow& r) {
+template <class BD>
+GOI_D void solve_rev_vrow(const BD& bd, RevVRow& r) {
     V2 vA = bd.v(r.ia), vB = bd.v(r.ib);
     float wA = bd.w(r.ia), wB = bd.w(r.ib);
     const float mA = r.mA, mB = r.mB, iA = r.iA, iB = r.iB;
@@ -392,11 +395,12 @@ GOI_D void store_rev_impulses(const Rows& R, int i, const RevVRow& r) {
     R.setf(i, JF_IMP0, r.i0); R.setf(i, JF_IMP1, r.i1);
     R.setf(i, JF_IMP3, r.i3); R.setf(i, JF_IMP4, r.i4); R.setf(i, JF_MIMP, r.mi);
 }
-// joint rows 0..n-1 of a revolute-only model under the v2.4.1 solver, once each, in order
-GOI_D void rev_velocity_sweep(const Bodies& bd, const Rows& R, int n) {
-    if (n <= 0) return;
-    RevVRow a = load_rev_vrow(R, 0), b;
-    for (int i = 0; i < n; i += 2) {  // as cs_solve_velocity_sweep: joint i + 1 in flight while joint i is solved
+// joint rows i0..n-1 of a revolute-only model under the v2.4.1 solver, once each, in order
+template <class BD>
+GOI_D void rev_velocity_sweep(const BD& bd, const Rows& R, int i0, int n) {
+    if (n <= i0) return;
+    RevVRow a = load_rev_vrow(R, i0), b;
+    for (int i = i0; i < n; i += 2) {  // as cs_solve_velocity_sweep: joint i + 1 in flight while joint i is solved
         if (i + 1 < n) b = load_rev_vrow(R, i + 1);
         solve_rev_vrow(bd, a);
         store_rev_impulses(R, i, a);
@@ -423,7 +427,8 @@ GOI_D bool rev_point(float mA, float mB, float iA, float iB, V2 la, V2 lb, V2& c
 }
 
 // SolvePositionConstraints for joint row i (joints.py:462-606); returns the joint's ok flag
-GOI_D bool jn_solve_position(const Bodies& bd, const Rows& R, int i, const GoiSettings& s, bool rev_only) {
+template <class BD>
+GOI_D bool jn_solve_position(const BD& bd, const Rows& R, int i, const GoiSettings& s, bool rev_only) {
     const int type = rev_only ? (int)GOI_REVOLUTE : R.geti(i, JF_TYPE), ia = R.geti(i, JF_IA), ib = R.geti(i, JF_IB);
     const float mA = R.getf(i, JF_MA), mB = R.getf(i, JF_MB), iA = R.getf(i, JF_IIA), iB = R.getf(i, JF_IIB);
     const bool elimit = R.geti(i, JF_ELIMIT) != 0;

@@ -33,6 +33,31 @@ struct Bodies {
     GOI_D void set_c(int b, V2 x, float aa) const { cx(b) = x.x; cy(b) = x.y; a(b) = aa; }
 };
 
+// One lane's view of the bodies while the lanes of a world's group solve its islands side by side, each lane its own
+// island (island.py:3-7: islands share no body but static ones). The island's bodies (`own`) are read and written;
+// another body that a row touches, a static one, is only read: Box2D's update of it (x - 0 * P) leaves it unchanged
+// unless an impulse is not finite or the value is -0, and a write that would change it raises the world's flag
+// (`changed`) instead, after which the world solves its islands again one after another. Without such a write, every
+// row saw the values it sees in Box2D's order, so the results are the same floats.
+struct IslandBodies {
+    Bodies bd;
+    unsigned long long own;
+    int* changed;
+    GOI_D V2 v(int b) const { return bd.v(b); }
+    GOI_D float w(int b) const { return bd.w(b); }
+    GOI_D V2 c(int b) const { return bd.c(b); }
+    GOI_D float a(int b) const { return bd.a(b); }
+    GOI_D static bool differ(float x, float y) { return __float_as_uint(x) != __float_as_uint(y); }
+    GOI_D void set_v(int b, V2 x, float ww) const {
+        if ((own >> b) & 1ull) bd.set_v(b, x, ww);
+        else if (differ(x.x, bd.vx(b)) || differ(x.y, bd.vy(b)) || differ(ww, bd.w(b))) *changed = 1;
+    }
+    GOI_D void set_c(int b, V2 x, float aa) const {
+        if ((own >> b) & 1ull) bd.set_c(b, x, aa);
+        else if (differ(x.x, bd.cx(b)) || differ(x.y, bd.cy(b)) || differ(aa, bd.a(b))) *changed = 1;
+    }
+};
+
 GOI_D V2 rel_vel(V2 vB, float wB, V2 rB, V2 vA, float wA, V2 rA) {
     return ((vB + cross(wB, rB)) - vA) - cross(wA, rA);
 }
@@ -48,6 +73,19 @@ struct Islands {
     GOI_D int& body_island(int b) const { return W.bisl(b); }
     GOI_D int& contact_island(int c) const { return W.cisl(c); }
     GOI_D int& joint_island(int j) const { return W.jisl(j); }
+    // island k's contact rows [c0, c1) and joint rows [j0, j1) of the solve order (find_islands notes where each
+    // island's rows start)
+    GOI_D void rows_of(int k, int& c0, int& c1, int& j0, int& j1) const {
+        const int s0 = W.ibuf(k), s1 = k + 1 < n ? W.ibuf(k + 1) : (nc | (nj << 16));
+        c0 = s0 & 0xffff; j0 = s0 >> 16;
+        c1 = s1 & 0xffff; j1 = s1 >> 16;
+    }
+    GOI_D unsigned long long bodies_of(int k) const {
+        unsigned long long own = 0ull;
+        for (int b = 0; b < W.B; ++b)
+            if (body_island(b) == k) own |= 1ull << b;
+        return own;
+    }
 };
 
 // b2World::Solve's depth-first search: seeds newest body first; popping b wakes it, walks b's touching contacts
@@ -65,6 +103,7 @@ GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
         if ((bflag >> seed) & 1ull) continue;
         if (!W.awake(seed) || !W.active(seed) || W.is_static(seed)) continue;
         const int isl = nisl++;
+        if (m.island_lanes) W.ibuf(isl) = nc | (nj << 16);  // the island's first rows (nc <= 256, nj <= 64)
         int sp = 0;
         W.stack(sp++) = seed;
         bflag |= 1ull << seed;
@@ -212,7 +251,8 @@ GOI_D void cs_prepare(const DModel& m, const World& W, const Bodies& bd, const R
     R.setf(i, CF_NM0, N0); R.setf(i, CF_NM1, N1); R.setf(i, CF_NM2, N2); R.setf(i, CF_NM3, N3);
 }
 
-GOI_D void cs_warm_start(const Bodies& bd, const Rows& R, int i) {
+template <class BD>
+GOI_D void cs_warm_start(const BD& bd, const Rows& R, int i) {
     const int ia = R.geti(i, CF_IA), ib = R.geti(i, CF_IB), cnt = R.geti(i, CF_COUNT);
     const float mA = R.getf(i, CF_MA), mB = R.getf(i, CF_MB), iA = R.getf(i, CF_IIA), iB = R.getf(i, CF_IIB);
     const V2 n = R.get2(i, CF_NX), t = cross(n, 1.0f);
@@ -256,7 +296,8 @@ GOI_D VRow load_vrow(const Rows& R, int i) {
 
 // b2ContactSolver::SolveVelocityConstraints for one row (contact_solver.py:194-290): tangent rows first, then the
 // normal row or the 2-point block solver's four cases. Updates the row's impulses in r and the bodies in LDS.
-GOI_D void solve_vrow(const Bodies& bd, VRow& r) {
+template <class BD>
+GOI_D void solve_vrow(const BD& bd, VRow& r) {
     const V2 n = r.n, t = cross(n, 1.0f);
     const float mA = r.mA, mB = r.mB, iA = r.iA, iB = r.iB;
     const V2 rA0 = r.rA0, rA1 = r.rA1, rB0 = r.rB0, rB1 = r.rB1;
@@ -484,12 +525,13 @@ GOI_D void store_vimpulses(const Rows& R, int i, const VRow& r) {
     R.setf(i, CF_NI0, r.ni0); R.setf(i, CF_NI1, r.ni1); R.setf(i, CF_TI0, r.ti0); R.setf(i, CF_TI1, r.ti1);
 }
 
-// rows 0..n-1 once each, in order, each loaded in one batch while the row before it is solved; two rows a loop
+// rows i0..n-1 once each, in order, each loaded in one batch while the row before it is solved; two rows a loop
 // iteration, so the two row buffers alternate without copies between them
-GOI_D void cs_solve_velocity_sweep(const Bodies& bd, const Rows& R, int n) {
-    if (n <= 0) return;
-    VRow a = load_vrow(R, 0), b;
-    for (int i = 0; i < n; i += 2) {
+template <class BD>
+GOI_D void cs_solve_velocity_sweep(const BD& bd, const Rows& R, int i0, int n) {
+    if (n <= i0) return;
+    VRow a = load_vrow(R, i0), b;
+    for (int i = i0; i < n; i += 2) {
         if (i + 1 < n) b = load_vrow(R, i + 1);
         solve_vrow(bd, a);
         store_vimpulses(R, i, a);
@@ -520,7 +562,8 @@ GOI_D PRow load_prow(const Rows& R, int i) {
 // b2ContactSolver::SolvePositionConstraints for one row (contact_solver.py:307-354); masses given (the TOI solve
 // passes zero for bodies other than the TOI pair). Returns the row's min separation, starting at 0. The callers keep
 // one rotation memo per side across rows and passes.
-GOI_D float solve_prow(const Bodies& bd, const PRow& r, float baumgarte, float mA, float mB, float iA, float iB,
+template <class BD>
+GOI_D float solve_prow(const BD& bd, const PRow& r, float baumgarte, float mA, float mB, float iA, float iB,
                        float linear_slop, float max_linear_correction, RotMemo& qa, RotMemo& qb) {
     const V2 lcA = r.lcA, lcB = r.lcB, ln = r.ln, lp = r.lp;
     const float radA = r.radA, radB = r.radB;

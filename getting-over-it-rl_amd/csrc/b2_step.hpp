@@ -8,6 +8,44 @@ namespace goi {
 
 // ---------------------------------------------------------------- b2World::Solve for one world
 
+// b2Island::Solve's warm start and velocity iterations (step.py:96-117) for island k alone, on its rows
+GOI_D void island_velocities(const IslandBodies& ib, const Islands& I, const Rows& CR, const Rows& JRw, int k,
+                             bool warm, bool v24, bool rev_only, int iterations) {
+    int c0, c1, j0, j1;
+    I.rows_of(k, c0, c1, j0, j1);
+    if (warm)
+        for (int i = c0; i < c1; ++i) cs_warm_start(ib, CR, i);
+    for (int i = j0; i < j1; ++i) jn_warm_start(ib, JRw, i, v24, rev_only);
+    for (int it = 0; it < iterations; ++it) {
+        if (rev_only && v24)
+            rev_velocity_sweep(ib, JRw, j0, j1);
+        else
+            for (int i = j0; i < j1; ++i) jn_solve_velocity(ib, JRw, i, v24, rev_only);
+        cs_solve_velocity_sweep(ib, CR, c0, c1);
+    }
+}
+
+// b2Island::Solve's position iterations (step.py:197-251) for island k alone; returns its positionSolved
+GOI_D bool island_positions(const IslandBodies& ib, const Islands& I, const Rows& CR, const Rows& JRw, int k,
+                            const GoiSettings& s, bool rev_only) {
+    int c0, c1, j0, j1;
+    I.rows_of(k, c0, c1, j0, j1);
+    RotMemo qa, qb;
+    for (int it = 0; it < s.position_iterations; ++it) {
+        float min_sep = 0.0f;
+        for (int i = c0; i < c1; ++i) {
+            const PRow r = load_prow(CR, i);
+            min_sep = bmin(min_sep, solve_prow(ib, r, s.baumgarte, r.mA, r.mB, r.iA, r.iB, s.linear_slop,
+                                               s.max_linear_correction, qa, qb));
+        }
+        bool jok = true;
+        for (int i = j0; i < j1; ++i)
+            if (!jn_solve_position(ib, JRw, i, s, rev_only)) jok = false;
+        if (min_sep >= -3.0f * s.linear_slop && jok) return true;
+    }
+    return false;
+}
+
 GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const Rows& CR, const Rows& JRw,
                             const GoiSettings& s, float dt, const GoiDebug& dbg) {
     const float dt_ratio = W.f(GOI_S_INV_DT0, 0) * dt;
@@ -15,65 +53,85 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     find_islands(m, W, I);
     const float h = dt;
     const float gx = W.f(GOI_S_GRAVITY, 0), gy = W.f(GOI_S_GRAVITY, 1);
-    // integrate velocities of dynamic island bodies; the sweep starts at the current pose (bodies are independent
-    // here and in the other per-body loops below: one body per lane of the group)
-    for (int b = W.sub; b < W.B; b += W.G) {
-        V2 v = W.v2(GOI_B_V, b);
-        float w = W.f(GOI_B_W, b);
-        const V2 c = W.v2(GOI_B_C, b);
-        const float a = W.f(GOI_B_A, b);
-        if (I.body_island(b) >= 0) {
-            if (W.is_dynamic(b)) {
-                const float gs = W.f(GOI_B_GRAVITY_SCALE, b), im = W.f(GOI_B_INV_MASS, b);
-                const float ax = gs * gx + im * W.f(GOI_B_FORCE, 2 * b);
-                const float ay = gs * gy + im * W.f(GOI_B_FORCE, 2 * b + 1);
-                const float vx = v.x + h * ax, vy = v.y + h * ay;
-                const float ww = w + h * W.f(GOI_B_INV_INERTIA, b) * W.f(GOI_B_TORQUE, b);
-                const float ld = 1.0f / (1.0f + h * W.f(GOI_B_LINEAR_DAMPING, b));
-                const float ad = 1.0f / (1.0f + h * W.f(GOI_B_ANGULAR_DAMPING, b));
-                v = mk(vx * ld, vy * ld);
-                w = ww * ad;
-            }
-            W.set2(GOI_B_C0, b, c);
-            W.f(GOI_B_A0, b) = a;
-        }
-        bd.set_v(b, v, w);
-        bd.set_c(b, c, a);
-        const Rot q = rot_of(a);
-        bd.at(6, b) = q.c;
-        bd.at(7, b) = q.s;
-    }
-    group_sync();
     const bool warm = s.warm_starting != 0;
     const bool v24 = s.revolute_v24 != 0;
-    // the constraint rows are independent of each other: the world's lane group prepares them together (one row
-    // per lane), then every lane warm-starts them in order
-    for (int i = W.sub; i < I.nc; i += W.G) {
-        const int slot = I.corder(i);
-        const int ia = W.ba(slot), ib = W.bb(slot);
-        Rot qA, qB;
-        qA.c = bd.at(6, ia); qA.s = bd.at(7, ia);
-        qB.c = bd.at(6, ib); qB.s = bd.at(7, ib);
-        cs_prepare(m, W, bd, CR, i, slot, warm, dt_ratio, qA, qB, s.velocity_threshold);
-    }
-    for (int i = W.sub; i < I.nj; i += W.G) {
-        const int jid = I.jorder(i);
-        const int ia = m.joint[jid].a, ib = m.joint[jid].b;
-        Rot qA, qB;
-        qA.c = bd.at(6, ia); qA.s = bd.at(7, ia);
-        qB.c = bd.at(6, ib); qB.s = bd.at(7, ib);
-        jn_prepare(m, W, bd, JRw, i, jid, s, dt, dt_ratio, warm, qA, qB);
-    }
-    group_sync();  // rows written by one lane of the group are read by all
-    if (warm)
-        for (int i = 0; i < I.nc; ++i) cs_warm_start(bd, CR, i);
-    for (int i = 0; i < I.nj; ++i) jn_warm_start(bd, JRw, i, v24, m.rev_only);
-    for (int it = 0; it < s.velocity_iterations; ++it) {
-        if (m.rev_only && v24)
-            rev_velocity_sweep(bd, JRw, I.nj);
-        else
-            for (int i = 0; i < I.nj; ++i) jn_solve_velocity(bd, JRw, i, v24, m.rev_only);
-        cs_solve_velocity_sweep(bd, CR, I.nc);
+    // A world of several islands has its group's lanes solve them side by side (lane sub takes islands sub, sub + G,
+    // ...; IslandBodies). If a row would change a static body, the world's velocity phase runs again from the
+    // integration below with the islands one after another, as is its position phase from the integrated poses.
+    bool par = m.island_lanes && I.n > 1;
+    int* const changed = &W.stack(0);  // the flag (the search's stack is free after find_islands)
+    for (;;) {
+        // integrate velocities of dynamic island bodies; the sweep starts at the current pose (bodies are independent
+        // here and in the other per-body loops below: one body per lane of the group)
+        for (int b = W.sub; b < W.B; b += W.G) {
+            V2 v = W.v2(GOI_B_V, b);
+            float w = W.f(GOI_B_W, b);
+            const V2 c = W.v2(GOI_B_C, b);
+            const float a = W.f(GOI_B_A, b);
+            if (I.body_island(b) >= 0) {
+                if (W.is_dynamic(b)) {
+                    const float gs = W.f(GOI_B_GRAVITY_SCALE, b), im = W.f(GOI_B_INV_MASS, b);
+                    const float ax = gs * gx + im * W.f(GOI_B_FORCE, 2 * b);
+                    const float ay = gs * gy + im * W.f(GOI_B_FORCE, 2 * b + 1);
+                    const float vx = v.x + h * ax, vy = v.y + h * ay;
+                    const float ww = w + h * W.f(GOI_B_INV_INERTIA, b) * W.f(GOI_B_TORQUE, b);
+                    const float ld = 1.0f / (1.0f + h * W.f(GOI_B_LINEAR_DAMPING, b));
+                    const float ad = 1.0f / (1.0f + h * W.f(GOI_B_ANGULAR_DAMPING, b));
+                    v = mk(vx * ld, vy * ld);
+                    w = ww * ad;
+                }
+                W.set2(GOI_B_C0, b, c);
+                W.f(GOI_B_A0, b) = a;
+            }
+            bd.set_v(b, v, w);
+            bd.set_c(b, c, a);
+            const Rot q = rot_of(a);
+            bd.at(6, b) = q.c;
+            bd.at(7, b) = q.s;
+        }
+        group_sync();
+        // the constraint rows are independent of each other: the world's lane group prepares them together (one row
+        // per lane), then every lane warm-starts them in order
+        for (int i = W.sub; i < I.nc; i += W.G) {
+            const int slot = I.corder(i);
+            const int ia = W.ba(slot), ib = W.bb(slot);
+            Rot qA, qB;
+            qA.c = bd.at(6, ia); qA.s = bd.at(7, ia);
+            qB.c = bd.at(6, ib); qB.s = bd.at(7, ib);
+            cs_prepare(m, W, bd, CR, i, slot, warm, dt_ratio, qA, qB, s.velocity_threshold);
+        }
+        for (int i = W.sub; i < I.nj; i += W.G) {
+            const int jid = I.jorder(i);
+            const int ia = m.joint[jid].a, ib = m.joint[jid].b;
+            Rot qA, qB;
+            qA.c = bd.at(6, ia); qA.s = bd.at(7, ia);
+            qB.c = bd.at(6, ib); qB.s = bd.at(7, ib);
+            jn_prepare(m, W, bd, JRw, i, jid, s, dt, dt_ratio, warm, qA, qB);
+        }
+        group_sync();  // rows written by one lane of the group are read by all
+        if (par) {
+            *changed = 0;
+            group_sync();
+            for (int k = W.sub; k < I.n; k += W.G)
+                island_velocities(IslandBodies{bd, I.bodies_of(k), changed}, I, CR, JRw, k, warm, v24, m.rev_only,
+                                  s.velocity_iterations);
+            group_sync();
+            if (*changed == 0) break;
+            par = false;
+            group_sync();
+            continue;
+        }
+        if (warm)
+            for (int i = 0; i < I.nc; ++i) cs_warm_start(bd, CR, i);
+        for (int i = 0; i < I.nj; ++i) jn_warm_start(bd, JRw, i, v24, m.rev_only);
+        for (int it = 0; it < s.velocity_iterations; ++it) {
+            if (m.rev_only && v24)
+                rev_velocity_sweep(bd, JRw, 0, I.nj);
+            else
+                for (int i = 0; i < I.nj; ++i) jn_solve_velocity(bd, JRw, i, v24, m.rev_only);
+            cs_solve_velocity_sweep(bd, CR, 0, I.nc);
+        }
+        break;
     }
     // StoreImpulses (contact_solver.py:293-304), rows split over the lane group
     for (int i = W.sub; i < I.nc; i += W.G) {
@@ -109,8 +167,24 @@ GOI_D void solve_world(const DModel& m, const World& W, const Bodies& bd, const 
     group_sync();
     // position iterations with per-island early exit (step.py:197-251)
     unsigned long long done = 0ull, all = I.n >= 64 ? ~0ull : ((1ull << I.n) - 1ull);
+    if (par) {
+        *changed = 0;
+        group_sync();
+        for (int k = W.sub; k < I.n; k += W.G)
+            if (island_positions(IslandBodies{bd, I.bodies_of(k), changed}, I, CR, JRw, k, s, m.rev_only))
+                done |= 1ull << k;
+        done = group_or(W.grp(), done);
+        group_sync();
+        if (*changed != 0) {  // from the integrated poses again, the islands one after another
+            for (int b = W.sub; b < W.B; b += W.G)
+                if (I.body_island(b) >= 0) bd.set_c(b, W.v2(GOI_B_C, b) + h * bd.v(b), W.f(GOI_B_A, b) + h * bd.w(b));
+            group_sync();
+            done = 0ull;
+            par = false;
+        }
+    }
     RotMemo qa, qb;
-    for (int it = 0; it < s.position_iterations && done != all; ++it) {
+    for (int it = 0; !par && it < s.position_iterations && done != all; ++it) {
         unsigned long long jbad = 0ull;
         for (int i = 0; i < I.n; ++i) W.fwork(i) = 0.0f;  // min separation per island
         for (int i = 0; i < I.nc; ++i) {

@@ -60,6 +60,8 @@ struct DModel {
     int any_toi_body;     // Model.toi_bodies has a set entry (or is absent)
     int rev_only;         // every joint is revolute
     int no_edges;         // no edge fixture
+    int island_lanes;     // the non-static bodies are not all joined by joints: a world may hold several islands,
+                          // which its lane group then solves side by side
     // the static fixtures' 8-wide tree (node 0 = the root); nodes lie at most kWideDepth levels below the root
     int n_wnodes;         // 0 without static fixtures
     const MNode* wnode;   // [n_wnodes]

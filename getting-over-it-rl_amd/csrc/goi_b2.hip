@@ -494,6 +494,20 @@ int32_t goi_model_create(const GoiModelDesc* desc, int32_t contact_capacity, voi
     d.rev_only = 1;
     for (int j = 0; j < J; ++j) d.rev_only &= desc->joint_type[j] == GOI_REVOLUTE ? 1 : 0;
     d.no_edges = any_edge ? 0 : 1;
+    // joint components of the non-static bodies (union-find): more than one, and a world can hold several islands
+    std::vector<int> root(B);
+    for (int b = 0; b < B; ++b) root[b] = b;
+    const auto find = [&](int b) {
+        while (root[b] != b) b = root[b] = root[root[b]];
+        return b;
+    };
+    for (int j = 0; j < J; ++j) {
+        const int a = desc->joint_a[j], b = desc->joint_b[j];
+        if (desc->body_type[a] != GOI_STATIC && desc->body_type[b] != GOI_STATIC) root[find(a)] = find(b);
+    }
+    int components = 0;
+    for (int b = 0; b < B; ++b) components += desc->body_type[b] != GOI_STATIC && find(b) == b ? 1 : 0;
+    d.island_lanes = components > 1 ? 1 : 0;
     // per fixture: its scalars, its static fat box and its vertex and normal slots
     std::vector<MFixture> fix(std::max(F, 1), MFixture{});
     std::vector<V2> poly((size_t)std::max(F, 1) * 16, V2{0.0f, 0.0f});

@@ -9,10 +9,10 @@ namespace goi {
 hipError_t launch_island_step(const DModel& d, const Launch& L, bool multi, dim3 grid, size_t lds, hipStream_t st) {
     const dim3 b(kBlock);
     if (!multi)
-        hipLaunchKernelGGL((k_step_fixed<kIslandB, kIslandC, kIslandJ, kIslandR, kIslandS, false, true>), grid, b, lds,
+        hipLaunchKernelGGL((k_step_fixed<kIslandB, kIslandC, kIslandJ, kIslandR, kIslandS, false, true, true>), grid, b, lds,
                            st, d, L);
     else
-        hipLaunchKernelGGL((k_step_fixed<kIslandB, kIslandC, kIslandJ, kIslandR, kIslandS, true, true>), grid, b, lds,
+        hipLaunchKernelGGL((k_step_fixed<kIslandB, kIslandC, kIslandJ, kIslandR, kIslandS, true, true, true>), grid, b, lds,
                            st, d, L);
     return hipGetLastError();
 }

@@ -9,13 +9,13 @@ hipError_t launch_rig_step(const DModel& d, const Launch& L, bool multi, bool pl
                            hipStream_t st) {
     const dim3 b(kBlock);
     if (!multi && plain)
-        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, false, true>), grid, b, lds, st, d, L);
+        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, false, true, false>), grid, b, lds, st, d, L);
     else if (!multi)
-        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, false, false>), grid, b, lds, st, d, L);
+        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, false, false, false>), grid, b, lds, st, d, L);
     else if (plain)
-        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, true, true>), grid, b, lds, st, d, L);
+        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, true, true, false>), grid, b, lds, st, d, L);
     else
-        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, true, false>), grid, b, lds, st, d, L);
+        hipLaunchKernelGGL((k_step_fixed<kRigB, kRigC, kRigJ, kRigR, kRigS, true, false, false>), grid, b, lds, st, d, L);
     return hipGetLastError();
 }
 

@@ -498,6 +498,22 @@ def test_island_kernel_parity(oracle, monkeypatch):
     assert int(np.asarray(ref.overflow).sum()) == 0
 
 
+@pytest.mark.parametrize("wpw", ["4", "8"])
+def test_nonfinite_islands_parity(oracle, monkeypatch, wpw):
+    """Worlds of several islands, whose lanes solve the islands side by side, with a NaN or infinite value in one
+    island (test_host_sanitized.nonfinite_islands_case, 64 worlds): Box2D's order carries it through the terrain into
+    the other islands, which the device must follow by solving those worlds' islands one after another. 20 steps,
+    NaN for NaN, on the island instance (4 worlds per wave) and the general kernel (8)."""
+    from test_host_sanitized import nonfinite_islands_case
+    monkeypatch.setenv("GOI_WORLDS_PER_WAVE", wpw)
+    m, st, s, dt = nonfinite_islands_case(oracle, n=64)
+
+    def used(k, ref, dev):
+        assert b2.last_launch()["kernel"] == ("island" if wpw == "4" else "generic")
+    ref = _run(m, st, s, dt, 20, oracle, on_step=used, nan_equal=True)
+    assert np.isnan(ref.bodies.v[1]).any() and not np.isnan(ref.bodies.v[0]).any()
+
+
 @pytest.mark.parametrize("wpw,capacity", [(1, 40), (2, 40), (4, 40), (8, 40), (16, 40), (27, 40), (32, 6), (64, 6)])
 def test_worlds_per_wave_variants(oracle, monkeypatch, wpw, capacity):
     """The block-cooperative passes (manifolds, TOIs) for other world counts per wavefront than the default (the

@@ -160,6 +160,32 @@ def test_nonfinite_worlds_sanitized(host_step, tmp_path):
         check(run(host_step, p, "step"))
 
 
+def nonfinite_islands_case(oracle, n=8, clean=50):
+    """Config 5 after `clean` steps on the oracle (its worlds then hold 1 to 11 awake islands), with non-finite values
+    written into one island of a few worlds: a NaN linear velocity of a box (world 1), an infinite angular velocity
+    (world 3) and a NaN force (world 5). In Box2D's order a non-finite impulse reaches the terrain's velocity
+    (v - 0 * P) and from there the world's other islands; the library, whose lanes solve a world's islands side by
+    side, must then solve that world's islands one after another to give the same bits."""
+    s, m, st, cfg = b2.scenes.make_config(5, n)
+    for _ in range(clean):
+        oracle.step_(m, st, s, cfg.dt)
+    bd = st.bodies
+    bd.v[1, 10, 0] = np.nan
+    bd.w[3, 12] = np.inf
+    bd.force[5, 8, 1] = np.nan
+    return m, st, s, cfg.dt
+
+
+def test_nonfinite_islands_sanitized(host_step, tmp_path, oracle):
+    """Worlds of several islands with non-finite values in one of them step to the oracle's bits, on the island
+    instance and the general kernel."""
+    m, st, s, dt = nonfinite_islands_case(oracle)
+    for packed in (True, False):
+        p = tmp_path / f"scn{int(packed)}.bin"
+        write_scenario(p, m, st, s, dt, 20, packed)
+        check(run(host_step, p, "step"))
+
+
 @pytest.mark.parametrize("dt", [0.0, -0.02])
 def test_non_positive_dt_sanitized(host_step, tmp_path, dt):
     """dt <= 0: Solve still runs (step.py:35-40) and SolveTOI is skipped (toi.py:841); inv_dt0 keeps its value."""
