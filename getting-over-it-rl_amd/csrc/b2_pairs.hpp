@@ -338,19 +338,33 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         for (int j = 0; j < kHeld; ++j) has |= held[j] == p;
         return group_any(W.grp(), has);
     };
-    // the fat boxes of all rows into the workspace; the queried rows on active bodies and their union box
+    // the fat boxes of all rows into the workspace; the queried rows on active bodies and a box around them
     unsigned long long rows = 0ull;
     float4 U = make_float4(kMaxFloat, kMaxFloat, -kMaxFloat, -kMaxFloat);
     bool nan_query = false;
-    for (int r = 0; r < m.R; ++r) {
+    const auto row_box = [&](int r) {
         const int fr = 4 * W.frow(r);
         const float4 q = make_float4(W.f(GOI_F_FAT, fr), W.f(GOI_F_FAT, fr + 1), W.f(GOI_F_FAT, fr + 2),
                                      W.f(GOI_F_FAT, fr + 3));
         W.set_qbox(r, q);
-        if (!((query_rows >> r) & 1ull) || !W.active(m.row[r].body)) continue;
+        if (!((query_rows >> r) & 1ull) || !W.active(m.row[r].body)) return;
         rows |= 1ull << r;
         U.x = fminf(U.x, q.x); U.y = fminf(U.y, q.y); U.z = fmaxf(U.z, q.z); U.w = fmaxf(U.w, q.w);
         nan_query |= q.x != q.x || q.y != q.y || q.z != q.z || q.w != q.w;
+    };
+    if (m.R > 8) {
+        // many rows: one a lane of the group, the results combined over it (the union box in any order: it only
+        // filters the tree walk, and each of its hits is tested against the rows' own boxes)
+        for (int r = W.sub; r < m.R; r += W.G) row_box(r);
+        rows = group_or(W.grp(), rows);
+        nan_query = group_or(W.grp(), nan_query ? 1ull : 0ull) != 0ull;
+        for (int d = 1; d < W.G; d <<= 1) {
+            U.x = fminf(U.x, lane_partner(U.x, d)); U.y = fminf(U.y, lane_partner(U.y, d));
+            U.z = fmaxf(U.z, lane_partner(U.z, d)); U.w = fmaxf(U.w, lane_partner(U.w, d));
+        }
+        group_sync();  // the boxes one lane wrote are read by all
+    } else {
+        for (int r = 0; r < m.R; ++r) row_box(r);
     }
     // b2TestOverlap finds a box with a NaN coordinate overlapping every box, so such a row meets every static leaf:
     // a NaN union box then passes every node and leaf test below (and the row's own tests decide)
@@ -421,15 +435,28 @@ GOI_D void find_new_contacts(const DModel& m, const World& W, unsigned long long
         }
     }
     // non-static x non-static candidates
-    for (int i = 0; i < m.n_dd; ++i) {
-        const int4 d = m.dd_info[i];  // candidate, rows, bodies
-        const int p = d.x, ra = d.y & 0xff, rb = d.y >> 8, ba = d.z & 0xff, bb = d.z >> 8;
-        if (!(((query_rows >> ra) | (query_rows >> rb)) & 1ull)) continue;
-        if (!overlap(W.get_qbox(ra), W.get_qbox(rb))) continue;
-        if (!(W.is_dynamic(ba) || W.is_dynamic(bb))) continue;
-        if (!(W.active(ba) && W.active(bb))) continue;
-        if (has_pair(p)) continue;
-        np.add(p);
+    const auto dd_passes = [&](int i) {  // the tests that depend on candidate i alone
+        const int4 d = m.dd_info[i];     // candidate, rows, bodies
+        const int ra = d.y & 0xff, rb = d.y >> 8, ba = d.z & 0xff, bb = d.z >> 8;
+        return (((query_rows >> ra) | (query_rows >> rb)) & 1ull) && overlap(W.get_qbox(ra), W.get_qbox(rb)) &&
+               (W.is_dynamic(ba) || W.is_dynamic(bb)) && W.active(ba) && W.active(bb);
+    };
+    if (m.R > 8) {
+        // many rows, so many candidates: those tests split over the group, 64 candidates at a time; the ones that
+        // pass then take the membership test and join the new pairs in order
+        for (int q0 = 0; q0 < m.n_dd; q0 += 64) {
+            const int e = min(q0 + 64, m.n_dd);
+            unsigned long long mk = 0ull;
+            for (int i = q0 + W.sub; i < e; i += W.G)
+                if (dd_passes(i)) mk |= 1ull << (i - q0);
+            for (unsigned long long left = group_or(W.grp(), mk); left; left &= left - 1) {
+                const int p = m.dd_info[q0 + __builtin_ctzll(left)].x;
+                if (!has_pair(p)) np.add(p);
+            }
+        }
+    } else {
+        for (int i = 0; i < m.n_dd; ++i)
+            if (dd_passes(i) && !has_pair(m.dd_info[i].x)) np.add(m.dd_info[i].x);
     }
     if (np.total == 0) return;
     const int base_key = W.i32(GOI_S_NEXT_KEY, 0);
