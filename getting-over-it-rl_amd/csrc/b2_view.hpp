@@ -510,15 +510,30 @@ GOI_D void load_mirror_block(const DModel& m, const BlockCopy& bc) {
 // Box2D's contact list of the block's worlds (newest first = descending key, pairs.py:12-13) into each workspace's
 // order(0 .. nlive-1): each live slot's position is the number of live slots with a larger key (keys of live slots
 // are distinct). Every lane ranks its rows of its world. Called by every lane after load_mirror_block.
+// The ranks read each world's keys from a contiguous copy in its newp rows (free until FindNewContacts), a free
+// slot's key replaced by INT32_MIN, which no key is below: one comparison per slot, four slots per load.
 GOI_D void build_order_block(const BlockCopy& bc) {
     const Workspace& k = bc.k;
+    int* const keys = bc.lds + k.o_newp * bc.S + bc.j * bc.C;
+    if (bc.on)
+        for (int c = bc.r0; c < bc.C; c += bc.stride)
+            keys[c] = bc.wi(k.o_pair + c) >= 0 ? bc.wi(k.o_key + c) : INT32_MIN;
+    __syncthreads();
     if (bc.on) {
+        const bool by4 = bc.C % 4 == 0 && (k.o_newp * bc.S) % 4 == 0;  // every world's copy 16-byte aligned
         for (int c = bc.r0; c < bc.C; c += bc.stride) {
             if (bc.wi(k.o_pair + c) < 0) continue;
-            const int key = bc.wi(k.o_key + c);
+            const int key = keys[c];
             int rank = 0;
-#pragma unroll 8
-            for (int i = 0; i < bc.C; ++i) rank += (bc.wi(k.o_pair + i) >= 0 && bc.wi(k.o_key + i) > key) ? 1 : 0;
+            if (by4) {
+                const int4* const k4 = reinterpret_cast<const int4*>(keys);
+                for (int q = 0; q < bc.C / 4; ++q) {
+                    const int4 t = k4[q];
+                    rank += (t.x > key ? 1 : 0) + (t.y > key ? 1 : 0) + (t.z > key ? 1 : 0) + (t.w > key ? 1 : 0);
+                }
+            } else {
+                for (int i = 0; i < bc.C; ++i) rank += keys[i] > key ? 1 : 0;
+            }
             bc.wi(k.o_order + rank) = c;
         }
         if (bc.r0 == 0) {
