@@ -94,9 +94,9 @@ struct Islands {
 GOI_D void find_islands(const DModel& m, const World& W, Islands& I) {
     const int n = list_order(W);
     unsigned long long bflag = 0ull, jflag = 0ull;
-    for (int b = 0; b < W.B; ++b) I.body_island(b) = -1;
-    for (int c = 0; c < W.C; ++c) I.contact_island(c) = -1;  // also the "in an island" flag of each contact
-    for (int j = 0; j < W.J; ++j) I.joint_island(j) = -1;
+    for (int b = W.sub; b < W.B; b += W.G) I.body_island(b) = -1;  // split over the lane group
+    for (int c = W.sub; c < W.C; c += W.G) I.contact_island(c) = -1;  // also the "in an island" flag of each contact
+    for (int j = W.sub; j < W.J; j += W.G) I.joint_island(j) = -1;
     group_sync();
     int nisl = 0, nc = 0, nj = 0;
     for (int seed = W.B - 1; seed >= 0; --seed) {
