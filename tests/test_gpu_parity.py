@@ -45,6 +45,19 @@ def test_scene_parity(name, oracle):
     _run(m, perturbed(st, 64), s, 1.0 / 60.0, 90, oracle)
 
 
+@pytest.mark.parametrize("name,wpw", [("pile", 2), ("pile", 8), ("joints", 16), ("polygons", 16), ("misc", 8)])
+def test_islands_side_by_side_parity(name, wpw, oracle, monkeypatch):
+    """Scenes of several islands (pile up to 12, polygons 9, joints 8 with every joint type, misc 6) at wave shapes
+    whose lane groups hold fewer lanes than the world has islands (2 to 32 lanes), so lanes take several islands
+    each: 64 perturbed copies, 60 steps."""
+    monkeypatch.setenv("GOI_WORLDS_PER_WAVE", str(wpw))
+    s, m, st = scene_defs.build_test_scene(name, iterations=(8, 3))
+
+    def used(k, ref, dev):
+        assert b2.last_launch()["worlds_per_wave"] == wpw
+    _run(m, perturbed(st, 64), s, 1.0 / 60.0, 60, oracle, on_step=used)
+
+
 @pytest.mark.parametrize("name", ["pile", "hammer_chain", "island_walk", "joints"])
 def test_scene_parity_game_iterations(name, oracle):
     """The game's 300 / 30 iterations on the heavier scenes."""
