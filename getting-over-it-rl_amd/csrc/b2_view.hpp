@@ -406,7 +406,7 @@ GOI_HD BlockCopy block_copy(void* const* lv, int pitch, int n, int B, int C, int
     return bc;
 }
 
-constexpr int kCopyU = 4;  // rows per lane and leaf in one batch
+constexpr int kCopyU = 8;  // rows per lane and leaf in one batch
 
 // The mirrored leaves of the block's worlds into their workspaces (contact metadata, awake and active flags, the
 // mirrored float body leaves, the bodies of every live slot). Called by every lane of the block.
